@@ -1,0 +1,164 @@
+/*
+ * quanta_hip.h — C-ABI of the MI355X (gfx950) quantized matmul path.
+ *
+ * Drop-in boundary under the reference's L1 kernels (engine/src/ops.h) and its shortlist head
+ * (engine/src/model.cpp:240-334). Plain pointers and sizes only. Every function returns a status
+ * (QH_OK = 0); on failure qh_last_error() gives a message for the calling thread.
+ *
+ * Memory: every tensor, activation and output pointer below is a DEVICE pointer unless the
+ * parameter name ends in _host. `stream` is a hipStream_t (NULL = the null stream). Calls only
+ * enqueue work; nothing synchronises unless the function says so. Functions are reentrant and may
+ * be called from any host thread; the only shared state is the per-device init record.
+ *
+ * Block layouts are the .qnt layouts, unchanged (reference engine/src/model_file.h:16-38,
+ * scripts/export.py:10-13):
+ *   Q8_0 [rows][cols]: int8 quants [rows*cols], then fp16 scales [rows*cols/32]
+ *   Q4_0 [rows][cols]: packed nibbles [rows*cols/2] (per 32-block, byte j = (q[j]+8) | (q[j+16]+8)<<4),
+ *                      then fp16 scales [rows*cols/32]
+ *   quantized activation (QuantVec, ops.h:47-51): int8 q[cols], f32 d[cols/32]
+ * Results are bit-identical to the reference's scalar kernels (ops_ref.cpp) on the same inputs.
+ */
+#ifndef QUANTA_HIP_H
+#define QUANTA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+enum {
+    QH_OK = 0,
+    QH_ERR_ARG = 1,         /* null pointer, bad count or range */
+    QH_ERR_DTYPE = 2,       /* dtype not allowed for this call */
+    QH_ERR_SHAPE = 3,       /* cols % 32 != 0, mismatched tensors, size limits */
+    QH_ERR_ALIGN = 4,       /* device pointer not 16-byte aligned */
+    QH_ERR_HIP = 5,         /* a HIP runtime call failed */
+    QH_ERR_NOMEM = 6,       /* workspace too small / allocation failed */
+    QH_ERR_UNSUPPORTED = 7  /* e.g. top_k beyond the supported maximum */
+};
+
+/* Tensor dtypes, numbered as the .qnt file stores them (reference model_file.h:16, DType). */
+enum { QH_F32 = 0, QH_F16 = 1, QH_Q8_0 = 2, QH_Q4_0 = 3 };
+
+/* Quantization block size (reference model_file.h:17, QK). */
+#define QH_QK 32
+
+/* Device view of a .qnt tensor (reference model_file.h:27-38, Tensor): `data` is the device
+ * address of the quant section; for Q8_0 / Q4_0 the fp16 scales follow at data + quant bytes. */
+typedef struct qh_tensor {
+    int32_t dtype;
+    int32_t rows;
+    int32_t cols;
+    const void* data;
+} qh_tensor;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* qh_last_error(void);
+
+/* Library version string. */
+const char* qh_version(void);
+
+/* Selects `device` for the calling thread and records its properties (idempotent).
+ * Replaces: nothing (the reference has no device); called once before the others. */
+int qh_init(int device);
+
+/* Size in bytes of the quant section (reference model_file.cpp:29-38, Tensor::quant_bytes). */
+size_t qh_quant_bytes(int dtype, int rows, int cols);
+
+/* Quant section plus scale section. */
+size_t qh_tensor_bytes(int dtype, int rows, int cols);
+
+/* Checks a tensor view: dtype, shape, cols % 32 and 16-byte alignment of `data`. */
+int qh_validate_tensor(const qh_tensor* W);
+
+/* Thin device-memory helpers so C/C++ callers need no HIP headers. */
+int qh_malloc(void** ptr, size_t bytes);
+int qh_free(void* ptr);
+int qh_memcpy_h2d(void* dst, const void* src_host, size_t bytes, void* stream); /* async */
+int qh_memcpy_d2h(void* dst_host, const void* src, size_t bytes, void* stream); /* synchronous */
+int qh_memset(void* dst, int value, size_t bytes, void* stream);
+int qh_stream_sync(void* stream);
+
+/* Per-32-block int8 quantization of n_tok activation rows of length n (x is [n_tok][n] f32):
+ * q [n_tok][n] int8, d [n_tok][n/32] f32.
+ * Replaces: void quantize_q8(const float* x, int n, QuantVec& out)   (reference ops.h:52,
+ *           implementation ops_ref.cpp:69-83), once per token row. */
+int qh_quantize_q8(const float* x, int n_tok, int n, int8_t* q, float* d, void* stream);
+
+/* Decode GEMV: out[r] = W[r,:] . x for r in [r0, r1) (out indexed by absolute row), W Q8_0 or Q4_0,
+ * x = (xq [cols] int8, xd [cols/32] f32). Per row: int32 block dots, then the serial chain
+ * acc = fma(float(s_b) * dw_b, dx_b, acc) in block order.
+ * Replaces: void matvec_q(float* out, const Tensor& W, const QuantVec& x, int r0, int r1)
+ *           (reference ops.h:61, MatvecQFn ops.h:57; implementation ops_ref.cpp:85-120). */
+int qh_matvec_q(float* out, const qh_tensor* W, const int8_t* xq, const float* xd, int r0, int r1,
+                void* stream);
+
+/* Prefill matmul for n tokens: out[t*ldo + r] for t in [0, n), r in [r0, r1); xq is [n][cols]
+ * int8, xd is [n][cols/32] f32 (the n QuantVecs back to back). Every (row, token) value is
+ * bit-identical to qh_matvec_q on that token (int8 MFMA, K = 32 per instruction = one block).
+ * Replaces: void matmul_q(float* out, int ldo, const Tensor& W, const QuantVec* x, int n, int r0,
+ *           int r1) (reference ops.h:69, MatmulQFn ops.h:68; implementation ops_ref.cpp:122-160). */
+int qh_matmul_q(float* out, int ldo, const qh_tensor* W, const int8_t* xq, const float* xd, int n, int r0,
+                int r1, void* stream);
+
+/* First index of the maximum of logits[0, n) written to *index (device int32).
+ * Replaces: the greedy branch of Sampler::sample, std::max_element (reference sampler.cpp:35-37). */
+int qh_argmax(const float* logits, int n, int32_t* index, void* stream);
+
+/* ------------------------------------------------------------------ Exact Shortlist Head */
+
+/* Which logits the caller needs (reference model.h:24-29, HeadQuery). `must` is a DEVICE array of
+ * n_must ids. top_k must be in [1, QH_HEAD_MAX_TOPK]. */
+typedef struct qh_head_query {
+    int32_t top_k;
+    int32_t n_valid; /* ids >= n_valid are ignored; 0 = whole vocab */
+    const int32_t* must;
+    int32_t n_must;
+} qh_head_query;
+
+#define QH_HEAD_MAX_TOPK 56 /* seeds = top_k + 8 <= 64 */
+
+/* Device-side summary of one shortlist call. */
+typedef struct qh_head_stats {
+    int32_t top1;       /* first argmax of logits over [0, n_valid) (greedy token) */
+    int32_t n_rows;     /* 8-bit rows rescored (reference Model::last_head_rows) */
+    int32_t n_seeds;    /* seeds rescored first */
+    int32_t n_cand;     /* candidates: upper bound >= tau */
+    int32_t n_must;     /* must ids rescored */
+    int32_t seed_tie;   /* 1 if the last seed's coarse score ties an unselected eligible row */
+    float tau;          /* k-th best exact seed logit (-inf if fewer than k seeds) */
+    float top1_logit;   /* logits[top1] */
+} qh_head_stats;
+
+/* Outputs of qh_shortlist_head, all device buffers owned by the caller. */
+typedef struct qh_head_out {
+    float* logits;        /* [V]: exact logit for rescored rows, -inf elsewhere */
+    float* coarse;        /* [V]: 4-bit score (reference Model::head_coarse) */
+    float* upper;         /* [V]: coarse + error bound (reference Model::head_upper) */
+    int32_t* rows;        /* [V + n_must]: rescored rows: seeds (best coarse first), then candidates
+                             (unordered), then must ids */
+    qh_head_stats* stats; /* one record */
+} qh_head_out;
+
+/* Workspace bytes qh_shortlist_head needs for a V x D head and top_k. */
+size_t qh_shortlist_workspace_bytes(int V, int D, int top_k);
+
+/* Exact Shortlist Head on one quantized hidden state (xq [D] int8, xd [D/32] f32):
+ * 4-bit screen of all V rows with bound = fma(sum_b fma(err_b, xnorm_b), 1.001, 1e-5); seeds = the
+ * top_k+8 best eligible coarse scores (lower row first on ties), rescored exactly; tau = k-th best
+ * exact seed; candidates {r < n_valid, not seed or must, upper[r] >= tau} and must ids rescored
+ * exactly; then the greedy argmax. head8 Q8_0 [V][D], head4 Q4_0 [V][D], err F16 [V][D/32].
+ * Replaces: void Model::shortlist_head(const HeadQuery&) (reference model.cpp:240-334) followed by
+ *           the greedy sample (sampler.cpp:35-37). */
+int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_tensor* err, const int8_t* xq,
+                      const float* xd, const qh_head_query* query, const qh_head_out* out, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QUANTA_HIP_H */

@@ -1,0 +1,167 @@
+"""ctypes bindings of the parity checkers.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's CPU-baseline
+leg, as the checker. The product (quanta.cpp_amd) never imports this package.
+
+* `liboracle.so`: the plain-C restatement in quanta_oracle.c (always built by `make -C oracle`).
+* `_ref/libquanta_ref.so`: the reference engine's own kernels compiled from its sources plus
+  ref_harness.cpp (`make -C oracle ref`, only where the reference tree is mounted). `ref` is None
+  when it is absent.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+QK = 32
+Q8_0, Q4_0 = 2, 3
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_int, _f = C.c_int, C.c_float
+
+
+def build(ref: bool | None = None) -> None:
+    """Compile liboracle.so, and the reference build too when the reference tree is present."""
+    subprocess.run(["make", "-s", "-C", HERE, "oracle"], check=True)
+    if ref is None:
+        ref = os.path.isdir(os.environ.get("REF", "/root/reference") + "/engine/src")
+    if ref:
+        subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+
+
+def _load(path):
+    return C.CDLL(path) if os.path.exists(path) else None
+
+
+class _Oracle:
+    def __init__(self, lib):
+        self.lib = lib
+        L = lib
+        L.qo_fp16_to_f32.argtypes, L.qo_fp16_to_f32.restype = [C.c_uint16], _f
+        L.qo_quantize_q8.argtypes = [_f32p, _int, _i8p, _f32p]
+        L.qo_matvec_q.argtypes = [_f32p, _int, _int, _int, _u8p, _i8p, _f32p, _int, _int]
+        L.qo_matmul_q.argtypes = [_f32p, _int, _int, _int, _int, _u8p, _i8p, _f32p, _int, _int, _int]
+        L.qo_matvec_q_mt.argtypes = [_f32p, _int, _int, _int, _u8p, _i8p, _f32p, _int]
+        L.qo_matmul_q_mt.argtypes = [_f32p, _int, _int, _int, _int, _u8p, _i8p, _f32p, _int, _int]
+        L.qo_argmax.argtypes, L.qo_argmax.restype = [_f32p, _int], _int
+        L.qo_shortlist_head.argtypes = [_u8p, _u8p, _u16p, _int, _int, _i8p, _f32p, _int, _int, C.c_void_p, _int,
+                                        _f32p, _f32p, _f32p, _i32p, C.POINTER(_int), C.POINTER(_f), C.POINTER(_int)]
+        L.qo_shortlist_head.restype = _int
+
+    def fp16_to_f32(self, h: int) -> float:
+        return self.lib.qo_fp16_to_f32(h)
+
+    def quantize_q8(self, x: np.ndarray):
+        x = np.ascontiguousarray(x, np.float32)
+        n = x.shape[-1]
+        flat = x.reshape(-1, n)
+        q = np.empty(flat.shape, np.int8)
+        d = np.empty((flat.shape[0], n // QK), np.float32)
+        for i in range(flat.shape[0]):
+            qi, di = q[i], d[i]
+            self.lib.qo_quantize_q8(flat[i], n, qi, di)
+        return q.reshape(x.shape), d.reshape(x.shape[:-1] + (n // QK,))
+
+    def matvec_q(self, dtype, rows, cols, buf, xq, xd, r0=0, r1=None, threads=1):
+        out = np.zeros(rows, np.float32)
+        xq = np.ascontiguousarray(xq, np.int8)
+        xd = np.ascontiguousarray(xd, np.float32)
+        if threads > 1 and r0 == 0 and r1 is None:
+            self.lib.qo_matvec_q_mt(out, dtype, rows, cols, buf, xq, xd, threads)
+        else:
+            self.lib.qo_matvec_q(out, dtype, rows, cols, buf, xq, xd, r0, rows if r1 is None else r1)
+        return out
+
+    def matmul_q(self, dtype, rows, cols, buf, xq, xd, r0=0, r1=None, threads=1):
+        xq = np.ascontiguousarray(xq, np.int8)
+        xd = np.ascontiguousarray(xd, np.float32)
+        n = xq.shape[0]
+        out = np.zeros((n, rows), np.float32)
+        if threads > 1 and r0 == 0 and r1 is None:
+            self.lib.qo_matmul_q_mt(out, rows, dtype, rows, cols, buf, xq, xd, n, threads)
+        else:
+            self.lib.qo_matmul_q(out, rows, dtype, rows, cols, buf, xq, xd, n, r0, rows if r1 is None else r1)
+        return out
+
+    def argmax(self, logits: np.ndarray, n: int | None = None) -> int:
+        logits = np.ascontiguousarray(logits, np.float32)
+        return self.lib.qo_argmax(logits, logits.size if n is None else n)
+
+    def shortlist_head(self, head8, head4, err, V, D, xq, xd, top_k=1, n_valid=0, must=None):
+        must_arr = np.ascontiguousarray(must if must is not None else [], np.int32)
+        logits = np.empty(V, np.float32)
+        coarse = np.empty(V, np.float32)
+        upper = np.empty(V, np.float32)
+        rows = np.empty(V + must_arr.size, np.int32)
+        ns, tau, tie = _int(0), _f(0), _int(0)
+        n = self.lib.qo_shortlist_head(head8, head4, np.ascontiguousarray(err).view(np.uint16).reshape(-1), V, D,
+                                       np.ascontiguousarray(xq, np.int8), np.ascontiguousarray(xd, np.float32),
+                                       top_k, n_valid, must_arr.ctypes.data if must_arr.size else None,
+                                       must_arr.size, logits, coarse, upper, rows, C.byref(ns), C.byref(tau),
+                                       C.byref(tie))
+        return dict(logits=logits, coarse=coarse, upper=upper, rows=rows[:n].copy(), n_rows=n,
+                    n_seeds=ns.value, tau=tau.value, seed_tie=bool(tie.value))
+
+
+class _Ref:
+    """The reference engine's own kernels (compiled from its sources)."""
+
+    def __init__(self, lib):
+        self.lib = L = lib
+        L.ref_fp16_to_f32.argtypes, L.ref_fp16_to_f32.restype = [C.c_uint16], _f
+        L.ref_quantize_q8.argtypes = [_f32p, _int, _i8p, _f32p]
+        L.ref_matvec_q.argtypes = [_f32p, _int, _int, _int, _u8p, _i8p, _f32p, _int]
+        L.ref_matmul_q.argtypes = [_f32p, _int, _int, _int, _u8p, _i8p, _f32p, _int, _int]
+        L.ref_shortlist_head.argtypes = [_u8p, _u8p, _u16p, _int, _int, _i8p, _f32p, _int, _int, C.c_void_p, _int,
+                                         _int, _f32p, _f32p, _f32p, _i32p]
+        L.ref_shortlist_head.restype = _int
+
+    def fp16_to_f32(self, h: int) -> float:
+        return self.lib.ref_fp16_to_f32(h)
+
+    def quantize_q8(self, x: np.ndarray):
+        x = np.ascontiguousarray(x, np.float32)
+        n = x.shape[-1]
+        q = np.empty(n, np.int8)
+        d = np.empty(n // QK, np.float32)
+        self.lib.ref_quantize_q8(x, n, q, d)
+        return q, d
+
+    def matvec_q(self, dtype, rows, cols, buf, xq, xd, threads=1):
+        out = np.zeros(rows, np.float32)
+        self.lib.ref_matvec_q(out, dtype, rows, cols, buf, np.ascontiguousarray(xq, np.int8),
+                              np.ascontiguousarray(xd, np.float32), threads)
+        return out
+
+    def matmul_q(self, dtype, rows, cols, buf, xq, xd, threads=1):
+        xq = np.ascontiguousarray(xq, np.int8)
+        n = xq.shape[0]
+        out = np.zeros((n, rows), np.float32)
+        self.lib.ref_matmul_q(out, dtype, rows, cols, buf, xq, np.ascontiguousarray(xd, np.float32), n, threads)
+        return out
+
+    def shortlist_head(self, head8, head4, err, V, D, xq, xd, top_k=1, n_valid=0, must=None, threads=1):
+        must_arr = np.ascontiguousarray(must if must is not None else [], np.int32)
+        logits = np.empty(V, np.float32)
+        coarse = np.empty(V, np.float32)
+        upper = np.empty(V, np.float32)
+        rows = np.empty(V + must_arr.size, np.int32)
+        n = self.lib.ref_shortlist_head(head8, head4, np.ascontiguousarray(err).view(np.uint16).reshape(-1), V, D,
+                                        np.ascontiguousarray(xq, np.int8), np.ascontiguousarray(xd, np.float32),
+                                        top_k, n_valid, must_arr.ctypes.data if must_arr.size else None,
+                                        must_arr.size, threads, logits, coarse, upper, rows)
+        return dict(logits=logits, coarse=coarse, upper=upper, rows=rows[:n].copy(), n_rows=n)
+
+
+_olib = _load(os.path.join(HERE, "liboracle.so"))
+oracle = _Oracle(_olib) if _olib is not None else None
+_rlib = _load(os.path.join(HERE, "_ref", "libquanta_ref.so"))
+ref = _Ref(_rlib) if _rlib is not None else None

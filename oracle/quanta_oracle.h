@@ -1,0 +1,81 @@
+/*
+ * Oracle: a plain-C restatement of the reference's quantized matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This code is the checker, never the product: only tests/,
+ * __graft_entry__.smoke() and bench.py's CPU-baseline leg may link or call it. The HIP
+ * library never falls back to it.
+ *
+ * Every function follows one reference function (cited as file:line, relative to the
+ * reference repository). Float association is kept explicit (fmaf where the reference
+ * build contracts a multiply-add), and the file is compiled with -ffp-contract=off so the
+ * compiler cannot fuse anything else.
+ *
+ * Layouts (reference engine/src/model_file.h:16-38, scripts/export.py:10-13):
+ *   Q8_0 tensor [rows][cols]: int8 quants [rows*cols], then fp16 scales [rows*cols/32]
+ *   Q4_0 tensor [rows][cols]: packed nibbles [rows*cols/2], then fp16 scales [rows*cols/32];
+ *        per 32-block, byte j = (q[j]+8) | (q[j+16]+8) << 4, value = nibble - 8.
+ *   Quantized activation ("QuantVec", ops.h:47-51): int8 q[n], f32 d[n/32].
+ */
+#ifndef QUANTA_ORACLE_H
+#define QUANTA_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { QO_F32 = 0, QO_F16 = 1, QO_Q8_0 = 2, QO_Q4_0 = 3 };
+enum { QO_QK = 32 };
+
+/* IEEE binary16 -> binary32, exact (ops.h:15-40). */
+float qo_fp16_to_f32(uint16_t h);
+
+/* Bytes of the quant section of a tensor (model_file.cpp:29-38). */
+uint64_t qo_quant_bytes(int dtype, int rows, int cols);
+
+/* Per-32-block int8 quantization of an activation vector (ops_ref.cpp:69-83). */
+void qo_quantize_q8(const float* x, int n, int8_t* q, float* d);
+
+/* Integer-dot matvec over rows [r0, r1) (ops_ref.cpp:85-120). data points at the quants;
+ * the fp16 scales follow at data + qo_quant_bytes(). out is indexed by absolute row. */
+void qo_matvec_q(float* out, int dtype, int rows, int cols, const uint8_t* data, const int8_t* xq,
+                 const float* xd, int r0, int r1);
+
+/* Multi-token matmul (ops_ref.cpp:122-160, contract ops.h:65-70): out[t*ldo + r] for tokens
+ * t in [0, n) and rows r in [r0, r1). xq is [n][cols] int8, xd is [n][cols/32]. Every
+ * (row, token) value is bit-identical to qo_matvec_q on that token. */
+void qo_matmul_q(float* out, int ldo, int dtype, int rows, int cols, const uint8_t* data,
+                 const int8_t* xq, const float* xd, int n, int r0, int r1);
+
+/* Exact Shortlist Head (model.cpp:240-334) for one quantized hidden state.
+ *   head8: Q8_0 [V][D] (the exact head), head4: Q4_0 [V][D], err: f16 [V][D/32].
+ *   top_k > 0, n_valid (0 = all rows), must[n_must] ids that must come back exact.
+ * Outputs (caller-allocated):
+ *   logits[V]: exact value for every row that was rescored, -inf elsewhere;
+ *   coarse[V], upper[V]: 4-bit score and its upper bound for every row;
+ *   rows[V]: rescored rows, seeds first (by coarse score descending, lower row first on ties),
+ *            then candidates in ascending row order, then must ids in query order.
+ * Returns the number of rescored rows (the reference's last_head_rows). *n_seeds receives the
+ * seed count, *tau the cut-off, *seed_tie 1 when the n_seed-th and next-best eligible coarse
+ * scores are equal (the reference's per-thread heaps may then pick a different seed). */
+int qo_shortlist_head(const uint8_t* head8, const uint8_t* head4, const uint16_t* err, int V, int D,
+                      const int8_t* xq, const float* xd, int top_k, int n_valid, const int* must, int n_must,
+                      float* logits, float* coarse, float* upper, int* rows, int* n_seeds, float* tau,
+                      int* seed_tie);
+
+/* Greedy token: first index of the maximum over logits[0, n) (sampler.cpp:35-37). */
+int qo_argmax(const float* logits, int n);
+
+/* Row-parallel drivers for the CPU baseline: rows split in chunks that are multiples of 16 over
+ * n_threads pthreads, as ThreadPool::parallel_for(rows, 16, ...) does (threadpool.h:28-40). */
+void qo_matvec_q_mt(float* out, int dtype, int rows, int cols, const uint8_t* data, const int8_t* xq,
+                    const float* xd, int n_threads);
+void qo_matmul_q_mt(float* out, int ldo, int dtype, int rows, int cols, const uint8_t* data,
+                    const int8_t* xq, const float* xd, int n, int n_threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

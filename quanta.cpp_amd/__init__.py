@@ -1,0 +1,218 @@
+"""Python binding of libquanta_hip.so (C-ABI in include/quanta_hip.h) for tests and benchmarks.
+
+The directory name is not an importable identifier, so callers load this file by path under the module
+name ``quanta_cpp_amd`` (see ``load_package``). Device memory and streams come from torch; every call
+goes through the C-ABI into the gfx950 kernels. There is no CPU fallback: if the library is missing or
+a call fails, a ``QHError`` is raised.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libquanta_hip.so")
+QK = 32
+F32, F16, Q8_0, Q4_0 = 0, 1, 2, 3
+HEAD_MAX_TOPK = 56
+
+
+class QHError(RuntimeError):
+    pass
+
+
+class qh_tensor(C.Structure):
+    _fields_ = [("dtype", C.c_int32), ("rows", C.c_int32), ("cols", C.c_int32), ("data", C.c_void_p)]
+
+
+class qh_head_query(C.Structure):
+    _fields_ = [("top_k", C.c_int32), ("n_valid", C.c_int32), ("must", C.c_void_p), ("n_must", C.c_int32)]
+
+
+class qh_head_stats(C.Structure):
+    _fields_ = [("top1", C.c_int32), ("n_rows", C.c_int32), ("n_seeds", C.c_int32), ("n_cand", C.c_int32),
+                ("n_must", C.c_int32), ("seed_tie", C.c_int32), ("tau", C.c_float), ("top1_logit", C.c_float)]
+
+
+class qh_head_out(C.Structure):
+    _fields_ = [("logits", C.c_void_p), ("coarse", C.c_void_p), ("upper", C.c_void_p), ("rows", C.c_void_p),
+                ("stats", C.c_void_p)]
+
+
+# Every symbol include/quanta_hip.h declares, in header order.
+EXPORTS = ("qh_last_error", "qh_version", "qh_init", "qh_quant_bytes", "qh_tensor_bytes", "qh_validate_tensor",
+           "qh_malloc", "qh_free", "qh_memcpy_h2d", "qh_memcpy_d2h", "qh_memset", "qh_stream_sync",
+           "qh_quantize_q8", "qh_matvec_q", "qh_matmul_q", "qh_argmax", "qh_shortlist_workspace_bytes",
+           "qh_shortlist_head")
+
+
+def build() -> None:
+    """Compile libquanta_hip.so for gfx950 (always recompiles what changed)."""
+    subprocess.run(["make", "-s", "-C", HERE, "-j8", "lib"], check=True)
+
+
+def _bind(lib):
+    vp, i32, sz = C.c_void_p, C.c_int, C.c_size_t
+    sig = {
+        "qh_last_error": ([], C.c_char_p), "qh_version": ([], C.c_char_p), "qh_init": ([i32], i32),
+        "qh_quant_bytes": ([i32, i32, i32], sz), "qh_tensor_bytes": ([i32, i32, i32], sz),
+        "qh_validate_tensor": ([C.POINTER(qh_tensor)], i32), "qh_malloc": ([C.POINTER(vp), sz], i32),
+        "qh_free": ([vp], i32), "qh_memcpy_h2d": ([vp, vp, sz, vp], i32), "qh_memcpy_d2h": ([vp, vp, sz, vp], i32),
+        "qh_memset": ([vp, i32, sz, vp], i32), "qh_stream_sync": ([vp], i32),
+        "qh_quantize_q8": ([vp, i32, i32, vp, vp, vp], i32),
+        "qh_matvec_q": ([vp, C.POINTER(qh_tensor), vp, vp, i32, i32, vp], i32),
+        "qh_matmul_q": ([vp, i32, C.POINTER(qh_tensor), vp, vp, i32, i32, i32, vp], i32),
+        "qh_argmax": ([vp, i32, vp, vp], i32),
+        "qh_shortlist_workspace_bytes": ([i32, i32, i32], sz),
+        "qh_shortlist_head": ([C.POINTER(qh_tensor)] * 3 + [vp, vp, C.POINTER(qh_head_query), C.POINTER(qh_head_out),
+                               vp, sz, vp], i32),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes, fn.restype = args, res
+    return lib
+
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises QHError when it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise QHError(f"{LIB_PATH} is missing: build it with `make -C {HERE}` (no CPU fallback exists)")
+        _lib = _bind(C.CDLL(LIB_PATH))
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise QHError(f"status {rc}: {lib().qh_last_error().decode()}")
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _stream():
+    return C.c_void_p(_torch().cuda.current_stream().cuda_stream)
+
+
+def _ptr(t) -> C.c_void_p:
+    return C.c_void_p(t.data_ptr())
+
+
+def init(device: int = 0) -> None:
+    _check(lib().qh_init(device))
+
+
+def tensor_bytes(dtype: int, rows: int, cols: int) -> int:
+    return lib().qh_tensor_bytes(dtype, rows, cols)
+
+
+class DeviceTensor:
+    """A .qnt tensor resident in device memory (quants then scales, one allocation)."""
+
+    def __init__(self, buf, dtype: int, rows: int, cols: int):
+        self.buf, self.dtype, self.rows, self.cols = buf, dtype, rows, cols
+        self.view = qh_tensor(dtype, rows, cols, buf.data_ptr())
+
+    @staticmethod
+    def upload(host: np.ndarray, dtype: int, rows: int, cols: int, device="cuda") -> "DeviceTensor":
+        torch = _torch()
+        host = np.ascontiguousarray(host).view(np.uint8).reshape(-1)
+        buf = torch.from_numpy(host.copy()).to(device)
+        return DeviceTensor(buf, dtype, rows, cols)
+
+    def validate(self) -> None:
+        _check(lib().qh_validate_tensor(C.byref(self.view)))
+
+
+def quantize_q8(x, q=None, d=None):
+    """x: f32 [n_tok][n] (or [n]) device tensor -> (q int8, d f32) device tensors."""
+    torch = _torch()
+    x2 = x.reshape(-1, x.shape[-1])
+    n_tok, n = x2.shape
+    if q is None:
+        q = torch.empty((n_tok, n), dtype=torch.int8, device=x.device)
+    if d is None:
+        d = torch.empty((n_tok, n // QK), dtype=torch.float32, device=x.device)
+    _check(lib().qh_quantize_q8(_ptr(x2), n_tok, n, _ptr(q), _ptr(d), _stream()))
+    shape = x.shape[:-1]
+    return q.reshape(*shape, n), d.reshape(*shape, n // QK)
+
+
+def matvec_q(W: DeviceTensor, xq, xd, out=None, r0: int = 0, r1: int | None = None):
+    torch = _torch()
+    if out is None:
+        out = torch.zeros(W.rows, dtype=torch.float32, device=xq.device)
+    r1 = W.rows if r1 is None else r1
+    _check(lib().qh_matvec_q(_ptr(out), C.byref(W.view), _ptr(xq), _ptr(xd), r0, r1, _stream()))
+    return out
+
+
+def matmul_q(W: DeviceTensor, xq, xd, out=None, r0: int = 0, r1: int | None = None, ldo: int | None = None):
+    """xq [n][cols], xd [n][cols/32] -> out [n][ldo] with rows [r0, r1) written."""
+    torch = _torch()
+    n = xq.shape[0]
+    ldo = W.rows if ldo is None else ldo
+    if out is None:
+        out = torch.zeros((n, ldo), dtype=torch.float32, device=xq.device)
+    r1 = W.rows if r1 is None else r1
+    _check(lib().qh_matmul_q(_ptr(out), ldo, C.byref(W.view), _ptr(xq), _ptr(xd), n, r0, r1, _stream()))
+    return out
+
+
+def argmax(logits, n: int | None = None):
+    torch = _torch()
+    idx = torch.empty(1, dtype=torch.int32, device=logits.device)
+    _check(lib().qh_argmax(_ptr(logits), logits.numel() if n is None else n, _ptr(idx), _stream()))
+    return idx
+
+
+class ShortlistHead:
+    """Device-resident Exact Shortlist Head: Q8_0 head, its Q4_0 copy and f16 block error bounds."""
+
+    def __init__(self, head8: DeviceTensor, head4: DeviceTensor, err: DeviceTensor, top_k: int = 1):
+        torch = _torch()
+        self.head8, self.head4, self.err = head8, head4, err
+        self.V, self.D = head8.rows, head8.cols
+        self.top_k = top_k
+        nbytes = lib().qh_shortlist_workspace_bytes(self.V, self.D, top_k)
+        if nbytes == 0:
+            raise QHError(f"unsupported shortlist shape/top_k: {self.V} x {self.D}, k={top_k}")
+        dev = head8.buf.device
+        self.ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        self.logits = torch.empty(self.V, dtype=torch.float32, device=dev)
+        self.coarse = torch.empty(self.V, dtype=torch.float32, device=dev)
+        self.upper = torch.empty(self.V, dtype=torch.float32, device=dev)
+        self.stats_dev = torch.zeros(8, dtype=torch.int32, device=dev)
+        self._rows_cap = 0
+        self.rows = None
+
+    def __call__(self, xq, xd, n_valid: int = 0, must=None, top_k: int | None = None):
+        """Enqueues one head call; results stay on the device (see `stats()`)."""
+        torch = _torch()
+        k = self.top_k if top_k is None else top_k
+        if k != self.top_k:
+            raise QHError("top_k differs from the one the workspace was sized for")
+        n_must = 0 if must is None else int(must.numel())
+        if self._rows_cap < self.V + n_must:
+            self._rows_cap = self.V + n_must
+            self.rows = torch.empty(self._rows_cap, dtype=torch.int32, device=self.logits.device)
+        q = qh_head_query(k, n_valid, must.data_ptr() if n_must else None, n_must)
+        o = qh_head_out(self.logits.data_ptr(), self.coarse.data_ptr(), self.upper.data_ptr(), self.rows.data_ptr(),
+                        self.stats_dev.data_ptr())
+        _check(lib().qh_shortlist_head(C.byref(self.head8.view), C.byref(self.head4.view), C.byref(self.err.view),
+                                       _ptr(xq), _ptr(xd), C.byref(q), C.byref(o), _ptr(self.ws),
+                                       self.ws.numel(), _stream()))
+
+    def stats(self) -> dict:
+        raw = self.stats_dev.cpu().numpy()
+        s = qh_head_stats.from_buffer_copy(raw.tobytes())
+        return {f: getattr(s, f) for f, _ in qh_head_stats._fields_}

@@ -1,0 +1,214 @@
+// C-ABI layer: argument validation, error reporting and dispatch to the kernel launchers.
+// Every entry point returns a status and records a message for the calling thread on failure.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "qh_internal.h"
+
+namespace qh {
+
+namespace {
+thread_local char g_error[512] = "";
+std::mutex g_init_mu;
+bool g_inited[64] = {};
+}  // namespace
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof g_error, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return QH_OK;
+    return fail(QH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int validate_quant(const qh_tensor* W, const char* what) {
+    if (!W) return fail(QH_ERR_ARG, "%s: null tensor", what);
+    if (W->dtype != QH_Q8_0 && W->dtype != QH_Q4_0)
+        return fail(QH_ERR_DTYPE, "%s: dtype %d is not q8_0 (2) or q4_0 (3)", what, W->dtype);
+    if (W->rows <= 0 || W->cols <= 0) return fail(QH_ERR_SHAPE, "%s: bad shape %d x %d", what, W->rows, W->cols);
+    if (W->cols % QH_QK != 0) return fail(QH_ERR_SHAPE, "%s: cols %d is not a multiple of 32", what, W->cols);
+    if (W->cols > kMaxCols) return fail(QH_ERR_SHAPE, "%s: cols %d above the supported %d", what, W->cols, kMaxCols);
+    if (!W->data) return fail(QH_ERR_ARG, "%s: null data", what);
+    if (!aligned16(W->data)) return fail(QH_ERR_ALIGN, "%s: data is not 16-byte aligned", what);
+    return QH_OK;
+}
+
+int validate_range(int rows, int r0, int r1, const char* what) {
+    if (r0 < 0 || r1 > rows || r0 > r1)
+        return fail(QH_ERR_ARG, "%s: row range [%d, %d) outside [0, %d)", what, r0, r1, rows);
+    return QH_OK;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+}  // namespace qh
+
+using namespace qh;
+
+extern "C" {
+
+const char* qh_last_error(void) { return g_error; }
+
+const char* qh_version(void) { return "quanta-hip 0.1 gfx950"; }
+
+int qh_init(int device) {
+    int n = 0;
+    if (int rc = check_hip(hipGetDeviceCount(&n), "hipGetDeviceCount")) return rc;
+    if (device < 0 || device >= n || device >= 64) return fail(QH_ERR_ARG, "qh_init: device %d of %d", device, n);
+    if (int rc = check_hip(hipSetDevice(device), "hipSetDevice")) return rc;
+    std::lock_guard<std::mutex> lk(g_init_mu);
+    if (!g_inited[device]) {
+        hipDeviceProp_t prop;
+        if (int rc = check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties")) return rc;
+        if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            return fail(QH_ERR_UNSUPPORTED, "qh_init: device %d is %s, this build targets gfx950", device,
+                        prop.gcnArchName);
+        g_inited[device] = true;
+    }
+    return QH_OK;
+}
+
+size_t qh_quant_bytes(int dtype, int rows, int cols) {
+    const size_t n = (size_t)rows * (size_t)cols;
+    switch (dtype) {
+        case QH_F32: return n * 4;
+        case QH_F16: return n * 2;
+        case QH_Q8_0: return n;
+        case QH_Q4_0: return n / 2;
+        default: return 0;
+    }
+}
+
+size_t qh_tensor_bytes(int dtype, int rows, int cols) {
+    size_t b = qh_quant_bytes(dtype, rows, cols);
+    if (dtype == QH_Q8_0 || dtype == QH_Q4_0) b += (size_t)rows * cols / QH_QK * 2;
+    return b;
+}
+
+int qh_validate_tensor(const qh_tensor* W) {
+    if (!W) return fail(QH_ERR_ARG, "qh_validate_tensor: null tensor");
+    if (W->dtype == QH_F32 || W->dtype == QH_F16) {
+        if (W->rows <= 0 || W->cols <= 0) return fail(QH_ERR_SHAPE, "bad shape %d x %d", W->rows, W->cols);
+        if (!W->data) return fail(QH_ERR_ARG, "null data");
+        if (!aligned16(W->data)) return fail(QH_ERR_ALIGN, "data is not 16-byte aligned");
+        return QH_OK;
+    }
+    return validate_quant(W, "qh_validate_tensor");
+}
+
+int qh_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(QH_ERR_ARG, "qh_malloc: null out pointer");
+    *ptr = nullptr;
+    if (bytes == 0) return QH_OK;
+    hipError_t e = hipMalloc(ptr, bytes);
+    if (e == hipErrorOutOfMemory) return fail(QH_ERR_NOMEM, "qh_malloc: out of memory (%zu bytes)", bytes);
+    return check_hip(e, "hipMalloc");
+}
+
+int qh_free(void* ptr) { return ptr ? check_hip(hipFree(ptr), "hipFree") : QH_OK; }
+
+int qh_memcpy_h2d(void* dst, const void* src_host, size_t bytes, void* stream) {
+    if (bytes == 0) return QH_OK;
+    if (!dst || !src_host) return fail(QH_ERR_ARG, "qh_memcpy_h2d: null pointer");
+    return check_hip(hipMemcpyAsync(dst, src_host, bytes, hipMemcpyHostToDevice, as_stream(stream)), "hipMemcpyAsync");
+}
+
+int qh_memcpy_d2h(void* dst_host, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return QH_OK;
+    if (!dst_host || !src) return fail(QH_ERR_ARG, "qh_memcpy_d2h: null pointer");
+    if (int rc = check_hip(hipMemcpyAsync(dst_host, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)),
+                           "hipMemcpyAsync"))
+        return rc;
+    return check_hip(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+}
+
+int qh_memset(void* dst, int value, size_t bytes, void* stream) {
+    if (bytes == 0) return QH_OK;
+    if (!dst) return fail(QH_ERR_ARG, "qh_memset: null pointer");
+    return check_hip(hipMemsetAsync(dst, value, bytes, as_stream(stream)), "hipMemsetAsync");
+}
+
+int qh_stream_sync(void* stream) { return check_hip(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize"); }
+
+int qh_quantize_q8(const float* x, int n_tok, int n, int8_t* q, float* d, void* stream) {
+    if (!x || !q || !d) return fail(QH_ERR_ARG, "qh_quantize_q8: null pointer");
+    if (n_tok < 0 || n <= 0 || n % QH_QK != 0) return fail(QH_ERR_SHAPE, "qh_quantize_q8: n_tok %d, n %d", n_tok, n);
+    if (n_tok == 0) return QH_OK;
+    return check_hip(launch_quantize_q8(x, n_tok, n, q, d, as_stream(stream)), "qh_quantize_q8 launch");
+}
+
+int qh_matvec_q(float* out, const qh_tensor* W, const int8_t* xq, const float* xd, int r0, int r1, void* stream) {
+    if (int rc = validate_quant(W, "qh_matvec_q")) return rc;
+    if (int rc = validate_range(W->rows, r0, r1, "qh_matvec_q")) return rc;
+    if (!out || !xq || !xd) return fail(QH_ERR_ARG, "qh_matvec_q: null pointer");
+    if (!aligned16(xq)) return fail(QH_ERR_ALIGN, "qh_matvec_q: xq is not 16-byte aligned");
+    if (r0 == r1) return QH_OK;
+    const GemvPlan plan = gemv_plan(W->dtype, W->cols, r1 - r0);
+    return check_hip(launch_gemv(out, *W, xq, xd, r0, r1, plan, as_stream(stream)), "qh_matvec_q launch");
+}
+
+int qh_matmul_q(float* out, int ldo, const qh_tensor* W, const int8_t* xq, const float* xd, int n, int r0, int r1,
+                void* stream) {
+    if (int rc = validate_quant(W, "qh_matmul_q")) return rc;
+    if (int rc = validate_range(W->rows, r0, r1, "qh_matmul_q")) return rc;
+    if (!out || !xq || !xd) return fail(QH_ERR_ARG, "qh_matmul_q: null pointer");
+    if (n < 0) return fail(QH_ERR_ARG, "qh_matmul_q: n = %d", n);
+    if (ldo < r1) return fail(QH_ERR_ARG, "qh_matmul_q: ldo %d < r1 %d", ldo, r1);
+    if (!aligned16(xq)) return fail(QH_ERR_ALIGN, "qh_matmul_q: xq is not 16-byte aligned");
+    if (n == 0 || r0 == r1) return QH_OK;
+    if ((long)n * ldo > 0x7fffffffL) return fail(QH_ERR_SHAPE, "qh_matmul_q: n * ldo too large");
+    return check_hip(launch_matmul(out, ldo, *W, xq, xd, n, r0, r1, as_stream(stream)), "qh_matmul_q launch");
+}
+
+int qh_argmax(const float* logits, int n, int32_t* index, void* stream) {
+    if (!logits || !index) return fail(QH_ERR_ARG, "qh_argmax: null pointer");
+    if (n <= 0) return fail(QH_ERR_ARG, "qh_argmax: n = %d", n);
+    return check_hip(launch_argmax(logits, n, index, as_stream(stream)), "qh_argmax launch");
+}
+
+size_t qh_shortlist_workspace_bytes(int V, int D, int top_k) {
+    if (V <= 0 || D <= 0 || top_k <= 0 || top_k > QH_HEAD_MAX_TOPK) return 0;
+    return head_workspace_bytes(V, D, top_k);
+}
+
+int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_tensor* err, const int8_t* xq,
+                      const float* xd, const qh_head_query* query, const qh_head_out* out, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+    if (!head8 || !head4 || !err || !query || !out) return fail(QH_ERR_ARG, "qh_shortlist_head: null argument");
+    if (int rc = validate_quant(head8, "qh_shortlist_head head8")) return rc;
+    if (int rc = validate_quant(head4, "qh_shortlist_head head4")) return rc;
+    if (head8->dtype != QH_Q8_0 || head4->dtype != QH_Q4_0 || err->dtype != QH_F16)
+        return fail(QH_ERR_DTYPE, "qh_shortlist_head: needs q8_0 head, q4_0 copy and f16 bounds");
+    const int V = head8->rows, D = head8->cols;
+    if (head4->rows != V || head4->cols != D || err->rows != V || err->cols != D / QH_QK)
+        return fail(QH_ERR_SHAPE, "qh_shortlist_head: bad shortlist tensors");  // as model.cpp:49-58
+    if (!err->data || !aligned16(err->data)) return fail(QH_ERR_ALIGN, "qh_shortlist_head: err not 16-byte aligned");
+    if (!xq || !xd || !aligned16(xq)) return fail(QH_ERR_ARG, "qh_shortlist_head: bad activation pointers");
+    if (query->top_k < 1 || query->top_k > QH_HEAD_MAX_TOPK)
+        return fail(QH_ERR_UNSUPPORTED, "qh_shortlist_head: top_k %d outside [1, %d]", query->top_k, QH_HEAD_MAX_TOPK);
+    if (query->n_must < 0 || (query->n_must > 0 && !query->must))
+        return fail(QH_ERR_ARG, "qh_shortlist_head: bad must list");
+    if (!out->logits || !out->coarse || !out->upper || !out->rows || !out->stats)
+        return fail(QH_ERR_ARG, "qh_shortlist_head: null output buffer");
+    const size_t need = head_workspace_bytes(V, D, query->top_k);
+    if (!workspace || workspace_bytes < need)
+        return fail(QH_ERR_NOMEM, "qh_shortlist_head: workspace %zu bytes, needs %zu", workspace_bytes, need);
+    if (!aligned16(workspace)) return fail(QH_ERR_ALIGN, "qh_shortlist_head: workspace not 16-byte aligned");
+    return check_hip(launch_shortlist_head(*head8, *head4, *err, xq, xd, *query, *out, workspace, as_stream(stream)),
+                     "qh_shortlist_head launch");
+}
+
+}  // extern "C"

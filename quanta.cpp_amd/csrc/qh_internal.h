@@ -1,0 +1,41 @@
+// Host-side declarations shared between the C-ABI layer (qh_api.hip) and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "quanta_hip.h"
+
+namespace qh {
+
+// Records a formatted message as this thread's last error and returns `code`.
+int fail(int code, const char* fmt, ...);
+
+// Maps a HIP status to QH_ERR_HIP with context, QH_OK otherwise.
+int check_hip(hipError_t e, const char* what);
+
+// Launch configuration of the decode GEMV for one (dtype, cols) pair.
+struct GemvPlan {
+    int unroll;     // 16-byte chunks each thread loads per pass (template instance)
+    int tile_rows;  // rows per workgroup
+};
+GemvPlan gemv_plan(int dtype, int cols, int rows);
+
+// Largest supported cols for the decode GEMV and the prefill matmul.
+constexpr int kMaxCols = 32768;
+
+hipError_t launch_quantize_q8(const float* x, int n_tok, int n, int8_t* q, float* d, hipStream_t s);
+hipError_t launch_gemv(float* out, const qh_tensor& W, const int8_t* xq, const float* xd, int r0, int r1,
+                       const GemvPlan& plan, hipStream_t s);
+hipError_t launch_matmul(float* out, int ldo, const qh_tensor& W, const int8_t* xq, const float* xd, int n,
+                         int r0, int r1, hipStream_t s);
+hipError_t launch_argmax(const float* logits, int n, int32_t* index, hipStream_t s);
+
+// Shortlist head. Workspace layout is private to qh_head.hip.
+size_t head_workspace_bytes(int V, int D, int top_k);
+hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4, const qh_tensor& err,
+                                 const int8_t* xq, const float* xd, const qh_head_query& q, const qh_head_out& out,
+                                 void* ws, hipStream_t s);
+
+}  // namespace qh

@@ -1,0 +1,103 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol the header declares, and its host-only
+entry points (sizes, validation) behave; no kernel is launched."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "quanta_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\**\s+\**(qh_[a-z0-9_]+)\s*\(", text, flags=re.M)
+
+
+def test_header_declarations_are_exported(qh):
+    names = declared_functions()
+    assert len(names) >= 15
+    assert tuple(names) == qh.EXPORTS
+    out = subprocess.run(["nm", "-D", "--defined-only", qh.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r" T (qh_[a-z0-9_]+)$", out, flags=re.M))
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    lib = qh.lib()
+    for n in names:
+        assert hasattr(lib, n)
+
+
+def test_sizes_follow_qnt_layout(qh):
+    L = qh.lib()
+    assert L.qh_quant_bytes(qh.Q8_0, 4864, 896) == 4864 * 896
+    assert L.qh_quant_bytes(qh.Q4_0, 4864, 896) == 4864 * 896 // 2
+    assert L.qh_quant_bytes(qh.F16, 3, 5) == 30 and L.qh_quant_bytes(qh.F32, 3, 5) == 60
+    assert L.qh_tensor_bytes(qh.Q8_0, 4864, 896) == 4630528  # 1.0625 B per weight
+    assert L.qh_tensor_bytes(qh.Q4_0, 4864, 896) == 2451456  # 0.5625 B per weight
+    assert L.qh_tensor_bytes(qh.F16, 151936, 28) == 151936 * 28 * 2
+    assert L.qh_shortlist_workspace_bytes(151936, 896, 1) > 151936
+    assert L.qh_shortlist_workspace_bytes(151936, 896, 57) == 0  # above the top_k limit
+    assert L.qh_shortlist_workspace_bytes(151936, 896, 0) == 0
+
+
+@pytest.mark.parametrize("dtype,rows,cols,ptr,code", [
+    (0, 4, 32, 256, 2),       # f32 is not a quantized dtype for matvec
+    (2, 4, 48, 256, 3),       # cols % 32
+    (2, 0, 32, 256, 3),       # empty
+    (3, 4, 64, 260, 4),       # misaligned data
+    (2, 4, 64, 0, 1),         # null data
+])
+def test_validation_codes(qh, dtype, rows, cols, ptr, code):
+    L = qh.lib()
+    W = qh.qh_tensor(dtype, rows, cols, ptr or None)
+    assert L.qh_matvec_q(C.c_void_p(16), C.byref(W), C.c_void_p(16), C.c_void_p(16), 0, max(rows, 0), None) == code
+    assert L.qh_last_error()
+
+
+def test_range_and_pointer_checks(qh):
+    L = qh.lib()
+    W = qh.qh_tensor(qh.Q8_0, 64, 64, 4096)
+    assert L.qh_matvec_q(C.c_void_p(16), C.byref(W), C.c_void_p(16), C.c_void_p(16), 10, 65, None) == 1
+    assert L.qh_matvec_q(C.c_void_p(16), C.byref(W), C.c_void_p(16), C.c_void_p(16), 5, 4, None) == 1
+    assert L.qh_matvec_q(None, C.byref(W), C.c_void_p(16), C.c_void_p(16), 0, 64, None) == 1
+    assert L.qh_matvec_q(C.c_void_p(16), C.byref(W), C.c_void_p(24), C.c_void_p(16), 0, 64, None) == 4
+    # empty ranges and empty batches are no-ops
+    assert L.qh_matvec_q(C.c_void_p(16), C.byref(W), C.c_void_p(16), C.c_void_p(16), 3, 3, None) == 0
+    assert L.qh_matmul_q(C.c_void_p(16), 64, C.byref(W), C.c_void_p(16), C.c_void_p(16), 0, 0, 64, None) == 0
+    assert L.qh_matmul_q(C.c_void_p(16), 32, C.byref(W), C.c_void_p(16), C.c_void_p(16), 4, 0, 64, None) == 1
+    assert L.qh_quantize_q8(C.c_void_p(16), 1, 40, C.c_void_p(16), C.c_void_p(16), None) == 3
+    assert L.qh_argmax(C.c_void_p(16), 0, C.c_void_p(16), None) == 1
+
+
+def test_shortlist_argument_checks(qh):
+    L = qh.lib()
+    V, D = 1000, 64
+    h8 = qh.qh_tensor(qh.Q8_0, V, D, 4096)
+    h4 = qh.qh_tensor(qh.Q4_0, V, D, 8192)
+    he = qh.qh_tensor(qh.F16, V, D // 32, 16384)
+    bad = qh.qh_tensor(qh.F16, V, D // 32 + 1, 16384)
+    out = qh.qh_head_out(16, 16, 16, 16, 16)
+    q = qh.qh_head_query(1, 0, None, 0)
+    ws = L.qh_shortlist_workspace_bytes(V, D, 1)
+    call = lambda e, qq, w: L.qh_shortlist_head(C.byref(h8), C.byref(h4), C.byref(e), C.c_void_p(16),
+                                                C.c_void_p(16), C.byref(qq), C.byref(out), C.c_void_p(4096), w, None)
+    assert call(bad, q, ws) == 3                     # bound tensor shape (model.cpp:49-58)
+    assert call(he, q, ws - 1) == 6                  # workspace too small
+    assert call(he, qh.qh_head_query(0, 0, None, 0), ws) == 7
+    assert call(he, qh.qh_head_query(57, 0, None, 0), ws) == 7
+    assert call(he, qh.qh_head_query(1, 0, None, 3), ws) == 1  # must count without a list
+    swapped = lambda: L.qh_shortlist_head(C.byref(h4), C.byref(h8), C.byref(he), C.c_void_p(16), C.c_void_p(16),
+                                          C.byref(q), C.byref(out), C.c_void_p(4096), ws, None)
+    assert swapped() == 2
+
+
+def test_package_fails_loudly_without_library(qh, monkeypatch, tmp_path):
+    monkeypatch.setattr(qh, "LIB_PATH", str(tmp_path / "missing.so"))
+    monkeypatch.setattr(qh, "_lib", None)
+    with pytest.raises(qh.QHError, match="no CPU fallback"):
+        qh.lib()

@@ -1,0 +1,129 @@
+"""GPU parity of the prefill matmul and the Exact Shortlist Head against the oracle.
+
+Prefill: every (row, token) output must be bit-identical to the oracle, and to the GPU decode GEMV of
+that token (the reference's own invariant, engine/src/checks.cpp:114-143).
+Shortlist head: candidate set, rescored logits, coarse scores, upper bounds, tau and the greedy token
+must be identical to the oracle (engine/src/model.cpp:240-334, sampler.cpp:35-37).
+"""
+import numpy as np
+import pytest
+
+from conftest import bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, gpu):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+
+
+PREFILL = [(2, 896, 896), (2, 128, 896), (3, 4864, 896), (3, 896, 4864)]
+
+
+@pytest.mark.parametrize("dtype,N,K", PREFILL)
+@pytest.mark.parametrize("M", [1, 7, 32, 33])
+def test_matmul_matches_oracle(qh, oracle, synth, gpu, dtype, N, K, M):
+    buf = synth.q8_tensor(11 + N, N, K) if dtype == 2 else synth.q4_tensor(13 + N, N, K)
+    x = synth.activations(17 + M, M, K)
+    W = qh.DeviceTensor.upload(buf, dtype, N, K)
+    xq, xd = qh.quantize_q8(_dev(x, gpu))
+    got = qh.matmul_q(W, xq, xd).cpu().numpy()
+    want = oracle.matmul_q(dtype, N, K, buf, xq.cpu().numpy(), xd.cpu().numpy(), threads=8)
+    assert (bits(got) == bits(want)).all(), f"max diff {np.abs(got - want).max()}"
+
+
+@pytest.mark.parametrize("dtype,N,K", PREFILL)
+@pytest.mark.parametrize("M", [128, 512])
+def test_matmul_rows_equal_gemv(qh, oracle, synth, gpu, dtype, N, K, M):
+    """Large M: every token row equals the decode GEMV of that token; a slice of rows against the oracle."""
+    import torch
+    buf = synth.q8_tensor(21 + N, N, K) if dtype == 2 else synth.q4_tensor(23 + N, N, K)
+    x = synth.activations(29 + M, M, K)
+    W = qh.DeviceTensor.upload(buf, dtype, N, K)
+    xq, xd = qh.quantize_q8(_dev(x, gpu))
+    got = qh.matmul_q(W, xq, xd)
+    per_tok = torch.stack([qh.matvec_q(W, xq[t], xd[t]) for t in range(M)])
+    assert torch.equal(got.view(torch.int32), per_tok.view(torch.int32))
+    r0, r1 = 64, 96
+    want = oracle.matmul_q(dtype, N, K, buf, xq.cpu().numpy(), xd.cpu().numpy(), r0=r0, r1=r1)
+    assert (bits(got.cpu().numpy()[:, r0:r1]) == bits(want[:, r0:r1])).all()
+
+
+def test_matmul_row_range_and_ldo(qh, oracle, synth, gpu):
+    import torch
+    N, K, M = 200, 896, 19
+    buf = synth.q4_tensor(31, N, K)
+    W = qh.DeviceTensor.upload(buf, 3, N, K)
+    xq, xd = qh.quantize_q8(_dev(synth.activations(37, M, K), gpu))
+    want = oracle.matmul_q(3, N, K, buf, xq.cpu().numpy(), xd.cpu().numpy())
+    ldo = 300
+    out = torch.full((M, ldo), 5.0, device=gpu)
+    qh.matmul_q(W, xq, xd, out=out, r0=7, r1=150, ldo=ldo)
+    o = out.cpu().numpy()
+    assert (bits(o[:, 7:150]) == bits(want[:, 7:150])).all()
+    assert (o[:, :7] == 5.0).all() and (o[:, 150:] == 5.0).all()
+
+
+# ----------------------------------------------------------------------------------------- shortlist head
+
+def _head(qh, synth, gpu, V, D, seed):
+    head8, head4, err = synth.shortlist_head(seed, V, D)
+    dev = (qh.DeviceTensor.upload(head8, 2, V, D), qh.DeviceTensor.upload(head4, 3, V, D),
+           qh.DeviceTensor.upload(err.view(np.uint8), 1, V, D // 32))
+    return (head8, head4, err), dev
+
+
+def _check_head(qh, oracle, head_np, sl, xq, xd, V, D, top_k, n_valid=0, must=None):
+    import torch
+    head8, head4, err = head_np
+    must_t = None if must is None else torch.tensor(must, dtype=torch.int32, device=xq.device)
+    sl(xq, xd, n_valid=n_valid, must=must_t)
+    st = sl.stats()
+    o = oracle.shortlist_head(head8, head4, err, V, D, xq.cpu().numpy(), xd.cpu().numpy(), top_k=top_k,
+                              n_valid=n_valid, must=must)
+    assert not st["seed_tie"] and not o["seed_tie"]
+    assert (bits(sl.coarse.cpu().numpy()) == bits(o["coarse"])).all(), "coarse"
+    assert (bits(sl.upper.cpu().numpy()) == bits(o["upper"])).all(), "upper"
+    assert st["n_rows"] == o["n_rows"] and st["n_seeds"] == o["n_seeds"]
+    rows = sl.rows.cpu().numpy()[: st["n_rows"]]
+    assert sorted(rows.tolist()) == sorted(o["rows"].tolist())
+    assert rows[: st["n_seeds"]].tolist() == o["rows"][: o["n_seeds"]].tolist(), "seed order"
+    assert (bits(sl.logits.cpu().numpy()) == bits(o["logits"])).all(), "logits"
+    assert np.float32(st["tau"]).tobytes() == np.float32(o["tau"]).tobytes()
+    nv = n_valid if 0 < n_valid < V else V
+    assert st["top1"] == oracle.argmax(o["logits"], nv)
+    return st, o
+
+
+@pytest.mark.parametrize("top_k", [1, 20])
+def test_shortlist_small_vocab(qh, oracle, synth, gpu, top_k):
+    V, D = 6007, 896
+    head_np, (h8, h4, he) = _head(qh, synth, gpu, V, D, 41)
+    sl = qh.ShortlistHead(h8, h4, he, top_k=top_k)
+    x = synth.activations(43, 6, D, scale=0.5)
+    xq, xd = qh.quantize_q8(_dev(x, gpu))
+    for t in range(4):
+        _check_head(qh, oracle, head_np, sl, xq[t], xd[t], V, D, top_k)
+    # n_valid below V and must ids (duplicates, out-of-range and >= n_valid ones are ignored)
+    must = [5, 17, 5, 6000, -3, 4000, 123, 17]
+    _check_head(qh, oracle, head_np, sl, xq[4], xd[4], V, D, top_k, n_valid=5000, must=must)
+    _check_head(qh, oracle, head_np, sl, xq[5], xd[5], V, D, top_k, n_valid=5000, must=must)
+
+
+def test_shortlist_full_vocab(qh, oracle, synth, gpu):
+    """The benchmark head: vocab 151936 x 896, k = 1, a few hidden states N(0,1)*0.5."""
+    V, D = 151936, 896
+    head_np, (h8, h4, he) = _head(qh, synth, gpu, V, D, 47)
+    sl = qh.ShortlistHead(h8, h4, he, top_k=1)
+    x = synth.activations(53, 4, D, scale=0.5)
+    xq, xd = qh.quantize_q8(_dev(x, gpu))
+    full = qh.matvec_q(h8, xq[0], xd[0])
+    for t in range(4):
+        st, o = _check_head(qh, oracle, head_np, sl, xq[t], xd[t], V, D, 1)
+        assert 0 < st["n_rows"] < V // 10
+    # the top-1 of the shortlist is the top-1 of the full 8-bit head, and its logit is bit-identical
+    sl(xq[0], xd[0])
+    st = sl.stats()
+    assert st["top1"] == int(qh.argmax(full).item())
+    assert np.float32(st["top1_logit"]).tobytes() == full[st["top1"]].cpu().numpy().tobytes()
