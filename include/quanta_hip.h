@@ -81,6 +81,8 @@ int qh_memcpy_h2d(void* dst, const void* src_host, size_t bytes, void* stream); 
 int qh_memcpy_d2h(void* dst_host, const void* src, size_t bytes, void* stream); /* synchronous */
 int qh_memset(void* dst, int value, size_t bytes, void* stream);
 int qh_stream_sync(void* stream);
+int qh_stream_create(void** stream); /* non-blocking stream at the default priority */
+int qh_stream_destroy(void* stream);
 
 /* Per-32-block int8 quantization of n_tok activation rows of length n (x is [n_tok][n] f32):
  * q [n_tok][n] int8, d [n_tok][n/32] f32.
@@ -143,7 +145,8 @@ typedef struct qh_head_out {
     qh_head_stats* stats; /* one record */
 } qh_head_out;
 
-/* Workspace bytes qh_shortlist_head needs for a V x D head and top_k. */
+/* Workspace bytes qh_shortlist_head needs for a V x D head and top_k. The workspace needs no
+ * initialisation (each call resets what it uses); calls that overlap must not share one. */
 size_t qh_shortlist_workspace_bytes(int V, int D, int top_k);
 
 /* Exact Shortlist Head on one quantized hidden state (xq [D] int8, xd [D/32] f32):

@@ -123,6 +123,8 @@ class _Ref:
         L.ref_shortlist_head.argtypes = [_u8p, _u8p, _u16p, _int, _int, _i8p, _f32p, _int, _int, C.c_void_p, _int,
                                          _int, _f32p, _f32p, _f32p, _i32p]
         L.ref_shortlist_head.restype = _int
+        L.ref_time_matvec_q.argtypes = [_f32p, _int, _int, _int, _u8p, _i8p, _f32p, _int, _int]
+        L.ref_time_matvec_q.restype = C.c_double
 
     def fp16_to_f32(self, h: int) -> float:
         return self.lib.ref_fp16_to_f32(h)
@@ -140,6 +142,12 @@ class _Ref:
         self.lib.ref_matvec_q(out, dtype, rows, cols, buf, np.ascontiguousarray(xq, np.int8),
                               np.ascontiguousarray(xd, np.float32), threads)
         return out
+
+    def time_matvec_q(self, dtype, rows, cols, buf, xq, xd, threads, reps):
+        """Seconds for `reps` row-parallel matvec calls on one reference thread pool."""
+        out = np.zeros(rows, np.float32)
+        return self.lib.ref_time_matvec_q(out, dtype, rows, cols, buf, np.ascontiguousarray(xq, np.int8),
+                                          np.ascontiguousarray(xd, np.float32), threads, reps)
 
     def matmul_q(self, dtype, rows, cols, buf, xq, xd, threads=1):
         xq = np.ascontiguousarray(xq, np.int8)

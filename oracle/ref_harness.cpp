@@ -10,6 +10,7 @@
 // headers it pulls in are included first so the widening reaches only the reference's own classes.
 #include <algorithm>
 #include <array>
+#include <chrono>
 #include <atomic>
 #include <cmath>
 #include <condition_variable>
@@ -72,6 +73,19 @@ void ref_matvec_q(float* out, int dtype, int rows, int cols, const uint8_t* data
     const QuantVec x = make_qv(xq, xd, cols);
     quanta::ThreadPool pool(n_threads);
     pool.parallel_for(rows, 16, [&](int r0, int r1) { quanta::matvec_q(out, W, x, r0, r1); });
+}
+
+// Seconds for `reps` calls of Model::linear on one pool (the CPU baseline's timed loop).
+double ref_time_matvec_q(float* out, int dtype, int rows, int cols, const uint8_t* data, const int8_t* xq,
+                         const float* xd, int n_threads, int reps) {
+    const Tensor W = make_tensor(dtype, rows, cols, data);
+    const QuantVec x = make_qv(xq, xd, cols);
+    quanta::ThreadPool pool(n_threads);
+    pool.parallel_for(rows, 16, [&](int r0, int r1) { quanta::matvec_q(out, W, x, r0, r1); });  // warm-up
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < reps; ++i)
+        pool.parallel_for(rows, 16, [&](int r0, int r1) { quanta::matvec_q(out, W, x, r0, r1); });
+    return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
 }
 
 // Model::linear_batch for a quantized W (model.cpp:336-347): out is [n][rows].

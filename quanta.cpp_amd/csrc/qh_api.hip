@@ -143,6 +143,18 @@ int qh_memset(void* dst, int value, size_t bytes, void* stream) {
 
 int qh_stream_sync(void* stream) { return check_hip(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize"); }
 
+int qh_stream_create(void** stream) {
+    if (!stream) return fail(QH_ERR_ARG, "qh_stream_create: null out pointer");
+    hipStream_t s = nullptr;
+    if (int rc = check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags")) return rc;
+    *stream = s;
+    return QH_OK;
+}
+
+int qh_stream_destroy(void* stream) {
+    return stream ? check_hip(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy") : QH_OK;
+}
+
 int qh_quantize_q8(const float* x, int n_tok, int n, int8_t* q, float* d, void* stream) {
     if (!x || !q || !d) return fail(QH_ERR_ARG, "qh_quantize_q8: null pointer");
     if (n_tok < 0 || n <= 0 || n % QH_QK != 0) return fail(QH_ERR_SHAPE, "qh_quantize_q8: n_tok %d, n %d", n_tok, n);

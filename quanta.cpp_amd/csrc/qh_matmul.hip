@@ -52,7 +52,6 @@ __global__ __launch_bounds__(256) void matmul_kernel(float* __restrict__ out, in
     }
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
     for (int b = 0; b < nb; ++b) {
         long a;
         if (DT == kQ8) {
