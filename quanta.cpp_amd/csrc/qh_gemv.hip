@@ -8,9 +8,12 @@
 // is turned into p = float(s) * f16(scale) (one rounded multiply, order-free) and parked in LDS at
 // [row][block]. After one barrier, thread r runs row r's serial chain acc = fma(p_b, dx_b, acc) over
 // the blocks in order, which is the reference's float association, so the result is bit-identical.
-// The activation (at most a few KB) is read straight from global memory and stays in L1/L2.
+// Every load of a pass (weights, scales, the activation bytes each chunk pairs with, the activation scales)
+// is issued before the first wait, so a single-pass tile costs one memory round trip and one barrier;
+// longer tiles prefetch the next pass while computing the current one.
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include "qh_device.h"
 #include "qh_internal.h"
@@ -43,55 +46,117 @@ hipError_t launch_quantize_q8(const float* x, int n_tok, int n, int8_t* q, float
     return hipGetLastError();
 }
 
-template <int DT, int U>
+// Serial chain acc = fma(p[b], dx[b], acc) for b = 0 .. nb-1 over LDS operands (the reference's order).
+__device__ __forceinline__ float chain_lds(const float* p, const float* dx, int nb) {
+    float acc = 0.0f;
+    for (int b = 0; b < nb; ++b) acc = __builtin_fmaf(p[b], dx[b], acc);
+    return acc;
+}
+
+// One pass of a workgroup: U chunks of 16 bytes per thread, the block scale of each chunk and, unless the
+// activation is staged in LDS (XL), the activation bytes the chunk pairs with. The chunk index is clamped
+// into the tile, so every load is unconditional and all of them go out back to back.
+template <int DT, int U, bool XL>
+struct GemvPass {
+    uint4 w[U];
+    uint4 xa[XL ? 1 : U];
+    uint4 xb[(XL || DT == kQ8) ? 1 : U];
+    uint16_t sc[U];
+    uint32_t rt[U], b[U];
+
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ base, const uint16_t* __restrict__ sbase,
+                                         const int8_t* __restrict__ xq, int c0, int last, int nb, uint32_t nb_magic) {
+        constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int c = min(c0 + j * 256 + (int)threadIdx.x, last);
+            const uint32_t g = (uint32_t)c / kChunksPerBlock;  // block index within the tile
+            rt[j] = nb == 1 ? g : div_magic(g, nb_magic);      // tile row
+            b[j] = g - rt[j] * (uint32_t)nb;                    // block within the row
+            w[j] = load16(base + (size_t)c * 16);
+            sc[j] = sbase[g];
+            if constexpr (!XL) {
+                if constexpr (DT == kQ8) {
+                    xa[j] = load16(xq + b[j] * QK + (c & 1) * 16);
+                } else {
+                    xa[j] = load16(xq + b[j] * QK);
+                    xb[j] = load16(xq + b[j] * QK + 16);
+                }
+            }
+        }
+    }
+
+    // Block products of the pass into LDS (only chunks below nchunks are stored). xs: LDS activation (XL).
+    __device__ __forceinline__ void products(float* prod, int pstride, int c0, int nchunks, const int8_t* xs) const {
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int c = c0 + j * 256 + (int)threadIdx.x;
+            if constexpr (DT == kQ8) {
+                const uint4 xv = XL ? *reinterpret_cast<const uint4*>(xs + b[j] * QK + (c & 1) * 16) : xa[XL ? 0 : j];
+                int s = dot16_i8(w[j], xv);
+                s += swap_pair(s);
+                if (c < nchunks && !(c & 1)) prod[rt[j] * pstride + b[j]] = (float)s * f16_to_f32(sc[j]);
+            } else {
+                const uint4 xlo = XL ? *reinterpret_cast<const uint4*>(xs + b[j] * QK) : xa[XL ? 0 : j];
+                const uint4 xhi = XL ? *reinterpret_cast<const uint4*>(xs + b[j] * QK + 16) : xb[XL ? 0 : j];
+                const int s = dot_q4_block(w[j], xlo, xhi);
+                if (c < nchunks) prod[rt[j] * pstride + b[j]] = (float)s * f16_to_f32(sc[j]);
+            }
+        }
+    }
+};
+
+// XL = false: activation read with the weights (best for small, latency-bound matrices).
+// XL = true: activation staged once in LDS (best for large matrices, where per-chunk activation loads
+// would compete with the weight stream).
+template <int DT, int U, bool XL>
 __global__ __launch_bounds__(256) void gemv_kernel(float* __restrict__ out, const uint8_t* __restrict__ wq,
                                                    const uint16_t* __restrict__ wscale,
                                                    const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                    int nb, int r0, int r1, int tile_rows, uint32_t nb_magic) {
-    extern __shared__ float prod[];  // [tile_rows][nb + 1]
+    extern __shared__ float smem[];
     constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
     constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
+    const int cols = nb * QK;
+    float* xds = smem;                                          // [nb] activation scales
+    float* prod = smem + nb;                                    // [tile_rows][nb + 1] block products
+    // [cols] codes (XL), 16-byte aligned after the products
+    int8_t* xs = reinterpret_cast<int8_t*>(smem) + ((((size_t)nb + (size_t)tile_rows * (nb + 1)) * 4 + 15) & ~size_t(15));
     const int pstride = nb + 1;
+    const int tid = (int)threadIdx.x;
     const int ra = r0 + (int)blockIdx.x * tile_rows;
     const int nrows = min(tile_rows, r1 - ra);
     const int nchunks = nrows * nb * kChunksPerBlock;
     const uint8_t* base = wq + (size_t)ra * nb * kBlockBytes;
     const uint16_t* sbase = wscale + (size_t)ra * nb;
 
+    GemvPass<DT, U, XL> cur;
+    cur.load(base, sbase, xq, 0, nchunks - 1, nb, nb_magic);
+    {
+        // Issued behind the first pass, so it arrives in the same round trip.
+        const int xch = cols / 16;
+        uint4 xv = make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (XL) xv = load16(xq + min(tid, xch - 1) * 16);
+        const float dv = xd[min(tid, nb - 1)];
+        if (XL && tid < xch) reinterpret_cast<uint4*>(xs)[tid] = xv;
+        if (tid < nb) xds[tid] = dv;
+        if constexpr (XL)
+            for (int i = tid + 256; i < xch; i += 256) reinterpret_cast<uint4*>(xs)[i] = load16(xq + i * 16);
+        for (int i = tid + 256; i < nb; i += 256) xds[i] = xd[i];
+    }
+    if constexpr (XL) __syncthreads();
     for (int c0 = 0; c0 < nchunks; c0 += 256 * U) {
-        uint4 w[U];
-#pragma unroll
-        for (int j = 0; j < U; ++j) {
-            const int c = c0 + j * 256 + (int)threadIdx.x;
-            w[j] = c < nchunks ? load16(base + (size_t)c * 16) : make_uint4(0u, 0u, 0u, 0u);
-        }
-#pragma unroll
-        for (int j = 0; j < U; ++j) {
-            const int c = c0 + j * 256 + (int)threadIdx.x;
-            const uint32_t g = (uint32_t)c / kChunksPerBlock;  // block index within the tile
-            const uint32_t rt = nb == 1 ? g : div_magic(g, nb_magic);  // tile row
-            const uint32_t b = g - rt * (uint32_t)nb;           // block within the row, always < nb
-            if (DT == kQ8) {
-                const uint4 xv = load16(xq + b * QK + (c & 1) * 16);
-                int s = dot16_i8(w[j], xv);
-                s += swap_pair(s);
-                if (c < nchunks && !(c & 1)) prod[rt * pstride + b] = (float)s * f16_to_f32(sbase[g]);
-            } else {
-                const uint4 xlo = load16(xq + b * QK);
-                const uint4 xhi = load16(xq + b * QK + 16);
-                const int s = dot_q4_block(w[j], xlo, xhi);
-                if (c < nchunks) prod[rt * pstride + b] = (float)s * f16_to_f32(sbase[g]);
-            }
+        if (c0 + 256 * U < nchunks) {  // uniform: prefetch the next pass, then compute this one
+            GemvPass<DT, U, XL> nxt;
+            nxt.load(base, sbase, xq, c0 + 256 * U, nchunks - 1, nb, nb_magic);
+            cur.products(prod, pstride, c0, nchunks, xs);
+            cur = nxt;
+        } else {
+            cur.products(prod, pstride, c0, nchunks, xs);
         }
     }
     __syncthreads();
-    const int t = (int)threadIdx.x;
-    if (t < nrows) {
-        const float* p = prod + t * pstride;
-        float acc = 0.0f;
-        for (int b = 0; b < nb; ++b) acc = __builtin_fmaf(p[b], xd[b], acc);
-        out[ra + t] = acc;
-    }
+    if (tid < nrows) out[ra + tid] = chain_lds(prod + tid * pstride, xds, nb);
 }
 
 namespace {
@@ -99,28 +164,43 @@ namespace {
 int round_unroll(int need) { return need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8; }
 
 bool env_plan(GemvPlan* p) {
-    // QH_GEMV_PLAN="unroll:tile_rows" overrides the heuristic (tuning sweeps); read once.
-    static const char* env = getenv("QH_GEMV_PLAN");
+    // QH_GEMV_PLAN="unroll:tile_rows" overrides the heuristic (tuning sweeps).
+    const char* env = getenv("QH_GEMV_PLAN");
     if (!env) return false;
     int u = 0, t = 0;
     if (sscanf(env, "%d:%d", &u, &t) != 2) return false;
     p->unroll = round_unroll(u);
     p->tile_rows = t;
+    p->act_lds = strstr(env, ":lds") != nullptr;
     return true;
 }
 
 }  // namespace
 
+size_t gemv_lds_bytes(int cols, int tile_rows, bool xl) {
+    const int nb = cols / QK;
+    const size_t f = ((size_t)nb + (size_t)tile_rows * (nb + 1)) * 4;
+    return xl ? ((f + 15) & ~size_t(15)) + (size_t)cols : f;
+}
+
 GemvPlan gemv_plan(int dtype, int cols, int rows) {
     const int nb = cols / QK;
-    const int chunks_per_row = dtype == kQ8 ? 2 * nb : nb;
-    const int lds_rows = 16384 / (nb + 1);  // prod tile <= 64 KB
+    const int cpr = dtype == kQ8 ? 2 * nb : nb;  // 16-byte chunks per row
+    const int lds_rows = (65536 - 16 - cols - nb * 4) / ((nb + 1) * 4);  // LDS <= 64 KB
     GemvPlan p;
     if (!env_plan(&p)) {
-        // Aim for about two workgroups per CU on the 256-CU part; short rows get several per tile.
-        int t = (rows + 511) / 512;
+        // Measured on MI355X (cold HBM, graph-replayed): small matrices are latency-bound and do best with
+        // about one 16-byte load per thread per workgroup (4 Q8 / 8 Q4 rows of 896, 2 rows of 4864);
+        // vocabulary-sized matrices prefer about two loads per thread.
+        // Q4_0 pairs each 16-byte chunk with 32 activation bytes, so large Q4 matrices stage the activation
+        // in LDS; everything else reads it alongside the weights.
+        const bool large = rows >= 16384;
+        int t = (large ? (dtype == kQ4 ? 1024 : 512) : 256) / cpr;
+        if (t < 1) t = 1;
+        if (!large && t == 1 && cpr < 512) t = 2;
         p.tile_rows = t;
-        p.unroll = round_unroll((t * chunks_per_row + 255) / 256);
+        p.unroll = round_unroll((t * cpr + 255) / 256);
+        p.act_lds = large && dtype == kQ4;
     }
     p.tile_rows = p.tile_rows < 1 ? 1 : p.tile_rows;
     p.tile_rows = p.tile_rows > 256 ? 256 : p.tile_rows;
@@ -128,7 +208,7 @@ GemvPlan gemv_plan(int dtype, int cols, int rows) {
     return p;
 }
 
-template <int DT, int U>
+template <int DT, int U, bool XL>
 static void launch_gemv_t(float* out, const qh_tensor& W, const int8_t* xq, const float* xd, int r0, int r1,
                           int tile_rows, hipStream_t s) {
     const int nb = W.cols / QK;
@@ -136,17 +216,20 @@ static void launch_gemv_t(float* out, const qh_tensor& W, const int8_t* xq, cons
     const uint16_t* ws = reinterpret_cast<const uint16_t*>(wq + qh_quant_bytes(W.dtype, W.rows, W.cols));
     const uint32_t magic = nb == 1 ? 0u : (uint32_t)((0x100000000ull + (uint64_t)nb - 1) / (uint64_t)nb);
     const unsigned grid = (unsigned)((r1 - r0 + tile_rows - 1) / tile_rows);
-    const size_t lds = (size_t)tile_rows * (nb + 1) * sizeof(float);
-    hipLaunchKernelGGL((gemv_kernel<DT, U>), dim3(grid), dim3(256), lds, s, out, wq, ws, xq, xd, nb, r0, r1,
+    const size_t lds = gemv_lds_bytes(W.cols, tile_rows, XL);
+    hipLaunchKernelGGL((gemv_kernel<DT, U, XL>), dim3(grid), dim3(256), lds, s, out, wq, ws, xq, xd, nb, r0, r1,
                        tile_rows, magic);
 }
 
 hipError_t launch_gemv(float* out, const qh_tensor& W, const int8_t* xq, const float* xd, int r0, int r1,
                        const GemvPlan& plan, hipStream_t s) {
-#define QH_GEMV_CASE(DT, U)                                                       \
-    if (W.dtype == DT && plan.unroll == U) {                                      \
-        launch_gemv_t<DT, U>(out, W, xq, xd, r0, r1, plan.tile_rows, s);          \
-        return hipGetLastError();                                                 \
+#define QH_GEMV_CASE(DT, U)                                                               \
+    if (W.dtype == DT && plan.unroll == U) {                                              \
+        if (plan.act_lds)                                                                 \
+            launch_gemv_t<DT, U, true>(out, W, xq, xd, r0, r1, plan.tile_rows, s);        \
+        else                                                                              \
+            launch_gemv_t<DT, U, false>(out, W, xq, xd, r0, r1, plan.tile_rows, s);       \
+        return hipGetLastError();                                                         \
     }
     QH_GEMV_CASE(kQ8, 1) QH_GEMV_CASE(kQ8, 2) QH_GEMV_CASE(kQ8, 4) QH_GEMV_CASE(kQ8, 8)
     QH_GEMV_CASE(kQ4, 1) QH_GEMV_CASE(kQ4, 2) QH_GEMV_CASE(kQ4, 4) QH_GEMV_CASE(kQ4, 8)

@@ -19,8 +19,10 @@ int check_hip(hipError_t e, const char* what);
 struct GemvPlan {
     int unroll;     // 16-byte chunks each thread loads per pass (template instance)
     int tile_rows;  // rows per workgroup
+    bool act_lds;   // stage the activation in LDS (large matrices) instead of loading it with the weights
 };
 GemvPlan gemv_plan(int dtype, int cols, int rows);
+size_t gemv_lds_bytes(int cols, int tile_rows, bool act_lds);
 
 // Largest supported cols for the decode GEMV and the prefill matmul.
 constexpr int kMaxCols = 32768;
