@@ -106,9 +106,13 @@ int qh_matvec_q(float* out, const qh_tensor* W, const int8_t* xq, const float* x
 int qh_matmul_q(float* out, int ldo, const qh_tensor* W, const int8_t* xq, const float* xd, int n, int r0,
                 int r1, void* stream);
 
-/* First index of the maximum of logits[0, n) written to *index (device int32).
+/* Workspace bytes qh_argmax needs for n logits (0 if n <= 0); no initialisation needed. */
+size_t qh_argmax_workspace_bytes(int n);
+
+/* First index of the maximum of logits[0, n) written to *index (device int32). Calls that overlap must not
+ * share a workspace.
  * Replaces: the greedy branch of Sampler::sample, std::max_element (reference sampler.cpp:35-37). */
-int qh_argmax(const float* logits, int n, int32_t* index, void* stream);
+int qh_argmax(const float* logits, int n, int32_t* index, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ Exact Shortlist Head */
 
@@ -121,7 +125,7 @@ typedef struct qh_head_query {
     int32_t n_must;
 } qh_head_query;
 
-#define QH_HEAD_MAX_TOPK 56 /* seeds = top_k + 8 <= 64 */
+#define QH_HEAD_MAX_TOPK 55 /* seeds = top_k + 8, kept with one more key in a 64-lane wave */
 
 /* Device-side summary of one shortlist call. */
 typedef struct qh_head_stats {
@@ -145,8 +149,9 @@ typedef struct qh_head_out {
     qh_head_stats* stats; /* one record */
 } qh_head_out;
 
-/* Workspace bytes qh_shortlist_head needs for a V x D head and top_k. The workspace needs no
- * initialisation (each call resets what it uses); calls that overlap must not share one. */
+/* Workspace bytes qh_shortlist_head needs for a V x D head and top_k (0 if unsupported: D must be a multiple
+ * of 64 and at most 4096). The workspace needs no initialisation (each call resets what it uses); calls that
+ * overlap must not share one. */
 size_t qh_shortlist_workspace_bytes(int V, int D, int top_k);
 
 /* Exact Shortlist Head on one quantized hidden state (xq [D] int8, xd [D/32] f32):

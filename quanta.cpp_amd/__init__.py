@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libquanta_hip.so")
 QK = 32
 F32, F16, Q8_0, Q4_0 = 0, 1, 2, 3
-HEAD_MAX_TOPK = 56
+HEAD_MAX_TOPK = 55
 
 
 class QHError(RuntimeError):
@@ -46,7 +46,8 @@ class qh_head_out(C.Structure):
 EXPORTS = ("qh_last_error", "qh_version", "qh_init", "qh_quant_bytes", "qh_tensor_bytes", "qh_validate_tensor",
            "qh_malloc", "qh_free", "qh_memcpy_h2d", "qh_memcpy_d2h", "qh_memset", "qh_stream_sync",
            "qh_stream_create", "qh_stream_destroy",
-           "qh_quantize_q8", "qh_matvec_q", "qh_matmul_q", "qh_argmax", "qh_shortlist_workspace_bytes",
+           "qh_quantize_q8", "qh_matvec_q", "qh_matmul_q", "qh_argmax_workspace_bytes", "qh_argmax",
+           "qh_shortlist_workspace_bytes",
            "qh_shortlist_head")
 
 
@@ -67,7 +68,8 @@ def _bind(lib):
         "qh_quantize_q8": ([vp, i32, i32, vp, vp, vp], i32),
         "qh_matvec_q": ([vp, C.POINTER(qh_tensor), vp, vp, i32, i32, vp], i32),
         "qh_matmul_q": ([vp, i32, C.POINTER(qh_tensor), vp, vp, i32, i32, i32, vp], i32),
-        "qh_argmax": ([vp, i32, vp, vp], i32),
+        "qh_argmax_workspace_bytes": ([i32], sz),
+        "qh_argmax": ([vp, i32, vp, vp, sz, vp], i32),
         "qh_shortlist_workspace_bytes": ([i32, i32, i32], sz),
         "qh_shortlist_head": ([C.POINTER(qh_tensor)] * 3 + [vp, vp, C.POINTER(qh_head_query), C.POINTER(qh_head_out),
                                vp, sz, vp], i32),
@@ -170,11 +172,25 @@ def matmul_q(W: DeviceTensor, xq, xd, out=None, r0: int = 0, r1: int | None = No
     return out
 
 
+class Argmax:
+    """Greedy token of a logits vector of up to `n` entries, with its own workspace."""
+
+    def __init__(self, n: int, device="cuda"):
+        torch = _torch()
+        self.n = n
+        self.ws = torch.empty(lib().qh_argmax_workspace_bytes(n), dtype=torch.uint8, device=device)
+        self.index = torch.empty(1, dtype=torch.int32, device=device)
+
+    def __call__(self, logits, n: int | None = None):
+        n = logits.numel() if n is None else n
+        if n > self.n:
+            raise QHError(f"argmax over {n} entries, workspace sized for {self.n}")
+        _check(lib().qh_argmax(_ptr(logits), n, _ptr(self.index), _ptr(self.ws), self.ws.numel(), _stream()))
+        return self.index
+
+
 def argmax(logits, n: int | None = None):
-    torch = _torch()
-    idx = torch.empty(1, dtype=torch.int32, device=logits.device)
-    _check(lib().qh_argmax(_ptr(logits), logits.numel() if n is None else n, _ptr(idx), _stream()))
-    return idx
+    return Argmax(logits.numel(), device=logits.device)(logits, n)
 
 
 class ShortlistHead:

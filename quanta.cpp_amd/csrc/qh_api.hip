@@ -185,14 +185,20 @@ int qh_matmul_q(float* out, int ldo, const qh_tensor* W, const int8_t* xq, const
     return check_hip(launch_matmul(out, ldo, *W, xq, xd, n, r0, r1, as_stream(stream)), "qh_matmul_q launch");
 }
 
-int qh_argmax(const float* logits, int n, int32_t* index, void* stream) {
+size_t qh_argmax_workspace_bytes(int n) { return n > 0 ? argmax_workspace_bytes(n) : 0; }
+
+int qh_argmax(const float* logits, int n, int32_t* index, void* workspace, size_t workspace_bytes, void* stream) {
     if (!logits || !index) return fail(QH_ERR_ARG, "qh_argmax: null pointer");
     if (n <= 0) return fail(QH_ERR_ARG, "qh_argmax: n = %d", n);
-    return check_hip(launch_argmax(logits, n, index, as_stream(stream)), "qh_argmax launch");
+    const size_t need = argmax_workspace_bytes(n);
+    if (!workspace || workspace_bytes < need)
+        return fail(QH_ERR_NOMEM, "qh_argmax: workspace %zu bytes, needs %zu", workspace_bytes, need);
+    if (!aligned16(workspace)) return fail(QH_ERR_ALIGN, "qh_argmax: workspace not 16-byte aligned");
+    return check_hip(launch_argmax(logits, n, index, workspace, as_stream(stream)), "qh_argmax launch");
 }
 
 size_t qh_shortlist_workspace_bytes(int V, int D, int top_k) {
-    if (V <= 0 || D <= 0 || top_k <= 0 || top_k > QH_HEAD_MAX_TOPK) return 0;
+    if (V <= 0 || D <= 0 || top_k <= 0 || top_k > QH_HEAD_MAX_TOPK || !head_shape_supported(D)) return 0;
     return head_workspace_bytes(V, D, top_k);
 }
 
@@ -207,6 +213,9 @@ int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_t
     const int V = head8->rows, D = head8->cols;
     if (head4->rows != V || head4->cols != D || err->rows != V || err->cols != D / QH_QK)
         return fail(QH_ERR_SHAPE, "qh_shortlist_head: bad shortlist tensors");  // as model.cpp:49-58
+    if (!head_shape_supported(D))
+        return fail(QH_ERR_SHAPE, "qh_shortlist_head: hidden size %d must be a multiple of 64 and at most %d", D,
+                    kMaxHeadCols);
     if (!err->data || !aligned16(err->data)) return fail(QH_ERR_ALIGN, "qh_shortlist_head: err not 16-byte aligned");
     if (!xq || !xd || !aligned16(xq)) return fail(QH_ERR_ARG, "qh_shortlist_head: bad activation pointers");
     if (query->top_k < 1 || query->top_k > QH_HEAD_MAX_TOPK)

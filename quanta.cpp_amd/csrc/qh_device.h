@@ -97,4 +97,29 @@ __device__ __forceinline__ int dot_q4_block(const uint4 w, const uint4 xlo, cons
 
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// The same chain over 16-byte aligned operands, read four blocks per LDS access.
+__device__ __forceinline__ float chain_lds4(const float* p, const float* dx, int nb) {
+    float acc = 0.0f;
+    int b = 0;
+#pragma unroll 4
+    for (; b + 4 <= nb; b += 4) {
+        const float4 pv = *reinterpret_cast<const float4*>(p + b);
+        const float4 xv = *reinterpret_cast<const float4*>(dx + b);
+        acc = __builtin_fmaf(pv.x, xv.x, acc);
+        acc = __builtin_fmaf(pv.y, xv.y, acc);
+        acc = __builtin_fmaf(pv.z, xv.z, acc);
+        acc = __builtin_fmaf(pv.w, xv.w, acc);
+    }
+    for (; b < nb; ++b) acc = __builtin_fmaf(p[b], dx[b], acc);
+    return acc;
+}
+
+// Row stride (floats) of an LDS product tile read by chain_lds4: a multiple of 4, and not a multiple of 32, so
+// the 16-byte reads of neighbouring rows fall in different banks.
+__host__ __device__ __forceinline__ int prod_stride4(int nb) {
+    const int p = (nb + 3) & ~3;
+    return (p & 31) == 0 ? p + 4 : p;
+}
+
+
 }  // namespace qh

@@ -159,16 +159,136 @@ __global__ __launch_bounds__(256) void gemv_kernel(float* __restrict__ out, cons
     if (tid < nrows) out[ra + tid] = chain_lds(prod + tid * pstride, xds, nb);
 }
 
+// Streaming GEMV for large matrices (vocabulary-sized heads). The grid is persistent: workgroup g walks the
+// contiguous run of row tiles [g*nt/G, (g+1)*nt/G), so each workgroup streams one long byte range. Two register
+// sets alternate: the 16-byte chunks (and block scales) of tile t+1 are in flight while tile t's block products
+// and row chains are computed. The activation codes and scales are staged in LDS once per launch. Products go to
+// one of two LDS buffers, so one barrier per tile suffices: the chain of tile t-1 (same buffer as t+1) finishes
+// before any thread passes the barrier of tile t.
+template <int DT, int U>
+struct StreamRegs {
+    uint4 w[U];
+    uint16_t sc[U];
+
+    // Loads the chunks of the tile starting at `base` (nchunks valid, later slots clamped onto the last one).
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ base, const uint16_t* __restrict__ sbase,
+                                         int nchunks) {
+        constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int c = min(j * 256 + (int)threadIdx.x, nchunks - 1);
+            w[j] = load16(base + (size_t)c * 16);
+            sc[j] = sbase[c / kChunksPerBlock];
+        }
+    }
+
+    __device__ __forceinline__ void products(float* prod, int pstride, int nchunks, int nb, uint32_t nb_magic,
+                                             const int8_t* xs) const {
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int c = j * 256 + (int)threadIdx.x;
+            const int cc = min(c, nchunks - 1);
+            if constexpr (DT == kQ8) {
+                const uint32_t g = (uint32_t)cc >> 1;
+                const uint32_t rt = nb == 1 ? g : div_magic(g, nb_magic);
+                const uint32_t b = g - rt * (uint32_t)nb;
+                const uint4 xv = *reinterpret_cast<const uint4*>(xs + b * QK + (cc & 1) * 16);
+                int s = dot16_i8(w[j], xv);
+                s += swap_pair(s);
+                if (c < nchunks && !(c & 1)) prod[rt * pstride + b] = (float)s * f16_to_f32(sc[j]);
+            } else {
+                const uint32_t g = (uint32_t)cc;
+                const uint32_t rt = nb == 1 ? g : div_magic(g, nb_magic);
+                const uint32_t b = g - rt * (uint32_t)nb;
+                const uint4 xlo = *reinterpret_cast<const uint4*>(xs + b * QK);
+                const uint4 xhi = *reinterpret_cast<const uint4*>(xs + b * QK + 16);
+                const int s = dot_q4_block(w[j], xlo, xhi);
+                if (c < nchunks) prod[rt * pstride + b] = (float)s * f16_to_f32(sc[j]);
+            }
+        }
+    }
+};
+
+template <int DT, int U>
+__global__ __launch_bounds__(256) void gemv_stream_kernel(float* __restrict__ out, const uint8_t* __restrict__ wq,
+                                                          const uint16_t* __restrict__ wscale,
+                                                          const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                          int nb, int r0, int r1, int tile_rows, uint32_t nb_magic) {
+    extern __shared__ float smem[];
+    constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
+    constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
+    const int cols = nb * QK;
+    const int pstride = prod_stride4(nb);
+    float* xds = smem;                                          // [nb], padded to 4
+    float* prod0 = smem + ((nb + 3) & ~3);                      // [tile_rows][pstride]
+    float* prod1 = prod0 + (size_t)tile_rows * pstride;
+    int8_t* xs = reinterpret_cast<int8_t*>(prod1 + (size_t)tile_rows * pstride);  // [cols]
+    const int tid = (int)threadIdx.x;
+    // Rows [ra, rb) of this workgroup: an even split, so no workgroup carries more than one extra partial tile.
+    const int n = r1 - r0;
+    const int ra = r0 + (int)((long)blockIdx.x * n / gridDim.x);
+    const int rb = r0 + (int)((long)(blockIdx.x + 1) * n / gridDim.x);
+    if (ra >= rb) return;  // uniform per workgroup; nothing below synchronises across workgroups
+
+    const size_t row_bytes = (size_t)nb * kBlockBytes;
+    auto chunks_of = [&](int r) { return min(tile_rows, rb - r) * nb * kChunksPerBlock; };
+
+    StreamRegs<DT, U> A, B;
+    A.load(wq + (size_t)ra * row_bytes, wscale + (size_t)ra * nb, chunks_of(ra));
+    for (int i = tid; i < cols / 16; i += 256) reinterpret_cast<uint4*>(xs)[i] = load16(xq + i * 16);
+    for (int i = tid; i < nb; i += 256) xds[i] = xd[i];
+    __syncthreads();
+
+    // One tile: block products into `prod`, then one barrier, then one chain thread per row.
+    auto tile_body = [&](const StreamRegs<DT, U>& regs, int r, float* prod) {
+        const int nrows = min(tile_rows, rb - r);
+        regs.products(prod, pstride, nrows * nb * kChunksPerBlock, nb, nb_magic, xs);
+        __syncthreads();
+        if (tid < nrows) out[r + tid] = chain_lds4(prod + tid * pstride, xds, nb);
+    };
+    // Loads in the steady-state loop are unconditional (a conditional load makes the compiler's wait counting
+    // assume the worst at the join); the last one or two tiles are peeled.
+    const int n_tiles = (rb - ra + tile_rows - 1) / tile_rows;
+    int t = 0;
+    while (t + 2 < n_tiles) {
+        const int r = ra + t * tile_rows;
+        B.load(wq + (size_t)(r + tile_rows) * row_bytes, wscale + (size_t)(r + tile_rows) * nb, chunks_of(r + tile_rows));
+        tile_body(A, r, prod0);
+        A.load(wq + (size_t)(r + 2 * tile_rows) * row_bytes, wscale + (size_t)(r + 2 * tile_rows) * nb,
+               chunks_of(r + 2 * tile_rows));
+        tile_body(B, r + tile_rows, prod1);
+        t += 2;
+    }
+    const int r = ra + t * tile_rows;
+    if (t + 1 < n_tiles) {
+        B.load(wq + (size_t)(r + tile_rows) * row_bytes, wscale + (size_t)(r + tile_rows) * nb, chunks_of(r + tile_rows));
+        tile_body(A, r, prod0);
+        tile_body(B, r + tile_rows, prod1);
+    } else {
+        tile_body(A, r, prod0);
+    }
+}
+
 namespace {
 
 int round_unroll(int need) { return need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8; }
 
 bool env_plan(GemvPlan* p) {
-    // QH_GEMV_PLAN="unroll:tile_rows" overrides the heuristic (tuning sweeps).
+    // Tuning sweeps override the heuristic with QH_GEMV_PLAN:
+    //   "unroll:tile_rows[:lds]"      one-pass tile kernel
+    //   "s:unroll:wg_per_cu"          streaming kernel (tile_rows derived from unroll)
     const char* env = getenv("QH_GEMV_PLAN");
     if (!env) return false;
     int u = 0, t = 0;
+    if (sscanf(env, "s:%d:%d", &u, &t) == 2) {
+        p->stream = true;
+        p->unroll = round_unroll(u);
+        p->grid = t * device_cus();
+        p->act_lds = true;
+        return true;
+    }
     if (sscanf(env, "%d:%d", &u, &t) != 2) return false;
+    p->stream = false;
     p->unroll = round_unroll(u);
     p->tile_rows = t;
     p->act_lds = strstr(env, ":lds") != nullptr;
@@ -177,10 +297,26 @@ bool env_plan(GemvPlan* p) {
 
 }  // namespace
 
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return cus[dev];
+}
+
 size_t gemv_lds_bytes(int cols, int tile_rows, bool xl) {
     const int nb = cols / QK;
     const size_t f = ((size_t)nb + (size_t)tile_rows * (nb + 1)) * 4;
     return xl ? ((f + 15) & ~size_t(15)) + (size_t)cols : f;
+}
+
+static size_t gemv_stream_lds_bytes(int cols, int tile_rows) {
+    const int nb = cols / QK;
+    return ((size_t)((nb + 3) & ~3) + 2 * (size_t)tile_rows * prod_stride4(nb)) * 4 + (size_t)cols;
 }
 
 GemvPlan gemv_plan(int dtype, int cols, int rows) {
@@ -188,19 +324,41 @@ GemvPlan gemv_plan(int dtype, int cols, int rows) {
     const int cpr = dtype == kQ8 ? 2 * nb : nb;  // 16-byte chunks per row
     const int lds_rows = (65536 - 16 - cols - nb * 4) / ((nb + 1) * 4);  // LDS <= 64 KB
     GemvPlan p;
+    p.stream = false;
+    p.grid = 0;
     if (!env_plan(&p)) {
         // Measured on MI355X (cold HBM, graph-replayed): small matrices are latency-bound and do best with
-        // about one 16-byte load per thread per workgroup (4 Q8 / 8 Q4 rows of 896, 2 rows of 4864);
-        // vocabulary-sized matrices prefer about two loads per thread.
-        // Q4_0 pairs each 16-byte chunk with 32 activation bytes, so large Q4 matrices stage the activation
-        // in LDS; everything else reads it alongside the weights.
-        const bool large = rows >= 16384;
-        int t = (large ? (dtype == kQ4 ? 1024 : 512) : 256) / cpr;
-        if (t < 1) t = 1;
-        if (!large && t == 1 && cpr < 512) t = 2;
+        // about one 16-byte load per thread per workgroup (4 Q8 / 8 Q4 rows of 896, 2 rows of 4864).
+        // Matrices of several MB and up go to the streaming kernel, which keeps two tiles per workgroup in
+        // flight with a persistent grid of two workgroups per CU.
+        const long chunks = (long)rows * cpr;
+        if (chunks >= 512L * 1024) {
+            p.stream = true;
+            p.unroll = 8;
+            p.grid = 2 * device_cus();
+            p.act_lds = true;
+        } else {
+            int t = 256 / cpr;
+            if (t < 1) t = 1;
+            if (t == 1 && cpr < 512) t = 2;
+            p.tile_rows = t;
+            p.unroll = round_unroll((t * cpr + 255) / 256);
+            p.act_lds = false;
+        }
+    }
+    if (p.stream) {
+        // Rows per tile: as many whole rows as unroll * 256 chunk slots hold, within 64 KB of LDS.
+        int t = p.unroll * 256 / cpr;
+        const int lds_stream_rows = (65536 - cols - (nb + 4) * 4) / (2 * prod_stride4(nb) * 4);
+        t = t < 1 ? 1 : t;
+        t = t > 256 ? 256 : t;  // one chain thread per row
+        t = t > lds_stream_rows ? lds_stream_rows : t;
         p.tile_rows = t;
-        p.unroll = round_unroll((t * cpr + 255) / 256);
-        p.act_lds = large && dtype == kQ4;
+        if (p.tile_rows * cpr > p.unroll * 256) p.stream = false;  // row longer than the register tile
+        else return p;
+        p.unroll = round_unroll((cpr + 255) / 256);
+        p.tile_rows = 1;
+        p.act_lds = true;
     }
     p.tile_rows = p.tile_rows < 1 ? 1 : p.tile_rows;
     p.tile_rows = p.tile_rows > 256 ? 256 : p.tile_rows;
@@ -221,10 +379,33 @@ static void launch_gemv_t(float* out, const qh_tensor& W, const int8_t* xq, cons
                        tile_rows, magic);
 }
 
+template <int DT, int U>
+static void launch_gemv_stream_t(float* out, const qh_tensor& W, const int8_t* xq, const float* xd, int r0, int r1,
+                                 int tile_rows, int grid, hipStream_t s) {
+    const int nb = W.cols / QK;
+    const uint8_t* wq = static_cast<const uint8_t*>(W.data);
+    const uint16_t* ws = reinterpret_cast<const uint16_t*>(wq + qh_quant_bytes(W.dtype, W.rows, W.cols));
+    const uint32_t magic = nb == 1 ? 0u : (uint32_t)((0x100000000ull + (uint64_t)nb - 1) / (uint64_t)nb);
+    const int n = r1 - r0;
+    const int n_tiles = (n + tile_rows - 1) / tile_rows;
+    const int g = grid < n_tiles ? grid : n_tiles;
+    // Even tiles within a workgroup's share: the fewest tiles of at most tile_rows rows, all the same size.
+    const int per = (n + g - 1) / g;
+    const int k = (per + tile_rows - 1) / tile_rows;
+    tile_rows = (per + k - 1) / k;
+    const size_t lds = gemv_stream_lds_bytes(W.cols, tile_rows);
+    hipLaunchKernelGGL((gemv_stream_kernel<DT, U>), dim3((unsigned)g), dim3(256), lds, s, out, wq, ws, xq, xd, nb, r0,
+                       r1, tile_rows, magic);
+}
+
 hipError_t launch_gemv(float* out, const qh_tensor& W, const int8_t* xq, const float* xd, int r0, int r1,
                        const GemvPlan& plan, hipStream_t s) {
 #define QH_GEMV_CASE(DT, U)                                                               \
     if (W.dtype == DT && plan.unroll == U) {                                              \
+        if (plan.stream) {                                                                \
+            launch_gemv_stream_t<DT, U>(out, W, xq, xd, r0, r1, plan.tile_rows, plan.grid, s); \
+            return hipGetLastError();                                                     \
+        }                                                                                 \
         if (plan.act_lds)                                                                 \
             launch_gemv_t<DT, U, true>(out, W, xq, xd, r0, r1, plan.tile_rows, s);        \
         else                                                                              \
@@ -237,27 +418,71 @@ hipError_t launch_gemv(float* out, const qh_tensor& W, const int8_t* xq, const f
     return hipErrorInvalidValue;
 }
 
-// Greedy token: first index of the maximum (reference sampler.cpp:35-37). One 1024-thread workgroup.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
-                                                      int32_t* __restrict__ index) {
-    __shared__ uint64_t part[16];
+// Greedy token: first index of the maximum (reference sampler.cpp:35-37), in two launches. Each workgroup folds
+// a contiguous slice into one 64-bit key (ordered score bits, then the complement of the index, so equal scores
+// prefer the lower index); one workgroup then folds the partial keys and writes the index.
+constexpr int kArgmaxThreads = 256;
+constexpr int kArgmaxPerThread = 8;
+constexpr int kArgmaxMaxParts = 1024;
+
+int argmax_parts(int n) {
+    const int p = (n + kArgmaxThreads * kArgmaxPerThread - 1) / (kArgmaxThreads * kArgmaxPerThread);
+    return p < kArgmaxMaxParts ? p : kArgmaxMaxParts;
+}
+
+size_t argmax_workspace_bytes(int n) { return ((size_t)argmax_parts(n) * 8 + 255) & ~size_t(255); }
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_part_kernel(const float* __restrict__ logits, int n,
+                                                                     uint64_t* __restrict__ part) {
+    __shared__ uint64_t wbest[kArgmaxThreads / 64];
+    const int a = (int)((long)blockIdx.x * n / gridDim.x), b = (int)((long)(blockIdx.x + 1) * n / gridDim.x);
     uint64_t best = 0;
-    for (int i = (int)threadIdx.x; i < n; i += 1024) {
-        const uint64_t k = score_key(logits[i], i);
-        best = k > best ? k : best;
+    for (int i0 = a; i0 < b; i0 += kArgmaxThreads * kArgmaxPerThread) {
+        float v[kArgmaxPerThread];
+#pragma unroll
+        for (int j = 0; j < kArgmaxPerThread; ++j) {
+            const int i = i0 + j * kArgmaxThreads + (int)threadIdx.x;
+            v[j] = logits[min(i, b - 1)];
+        }
+#pragma unroll
+        for (int j = 0; j < kArgmaxPerThread; ++j) {
+            const int i = i0 + j * kArgmaxThreads + (int)threadIdx.x;
+            const uint64_t k = i < b ? score_key(v[j], i) : 0ull;
+            best = k > best ? k : best;
+        }
     }
     best = wave_max_u64(best);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = best;
+    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint64_t m = part[0];
-        for (int w = 1; w < 16; ++w) m = part[w] > m ? part[w] : m;
+        uint64_t m = wbest[0];
+        for (int w = 1; w < kArgmaxThreads / 64; ++w) m = wbest[w] > m ? wbest[w] : m;
+        part[blockIdx.x] = m;
+    }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(const uint64_t* __restrict__ part, int n_parts,
+                                                                      int32_t* __restrict__ index) {
+    __shared__ uint64_t wbest[kArgmaxThreads / 64];
+    uint64_t best = 0;
+    for (int i = (int)threadIdx.x; i < n_parts; i += kArgmaxThreads) best = part[i] > best ? part[i] : best;
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t m = wbest[0];
+        for (int w = 1; w < kArgmaxThreads / 64; ++w) m = wbest[w] > m ? wbest[w] : m;
         *index = key_row(m);
     }
 }
 
-hipError_t launch_argmax(const float* logits, int n, int32_t* index, hipStream_t s) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, logits, n, index);
+hipError_t launch_argmax(const float* logits, int n, int32_t* index, void* ws, hipStream_t s) {
+    const int parts = argmax_parts(n);
+    uint64_t* part = static_cast<uint64_t*>(ws);
+    hipLaunchKernelGGL(argmax_part_kernel, dim3((unsigned)parts), dim3(kArgmaxThreads), 0, s, logits, n, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, part, parts, index);
     return hipGetLastError();
 }
 

@@ -1,21 +1,22 @@
 // Exact Shortlist Head (reference engine/src/model.cpp:240-334) on gfx950, three launches:
 //
-//  1. screen    one workgroup per tile of vocab rows: the 4-bit GEMV over the Q4_0 copy (same streaming
-//               scheme as the decode GEMV), the per-row bound chain over the f16 block errors and the
-//               activation's block norms (bound = fma(sum_b fma(err_b, xnorm_b), 1.001f, 1e-5f)), upper =
-//               coarse + bound, logits = -inf; then the tile's best top_k+9 eligible coarse scores
-//               (key = score, lower row first on ties) by repeated workgroup max.
-//  2. seeds     one workgroup: merges the tile lists into the global top_k+8 seeds (plus one more key to
-//               detect a tie at the cut), dedupes the must ids (first occurrence), rescoring seeds and must
-//               rows exactly with the Q8_0 row dot, tau = k-th best exact seed.
-//  3. cand      one workgroup per 256 rows: candidates {r < n_valid, unmarked, upper[r] >= tau} compacted
-//               with a ballot scan, appended to the row list, rescored exactly in the same workgroup, and the
-//               greedy argmax key folded in with a 64-bit atomic max; the last workgroup to finish writes the
-//               stats record.
+//  1. screen    persistent streaming grid over the vocabulary rows (even row split per workgroup, tiles of up to 64
+//               rows, the next tile's Q4_0 chunks and f16 block errors in flight while the current tile is reduced).
+//               Per row: the 4-bit score chain (same block products and association as the decode GEMV), the bound
+//               chain over the f16 block errors and the activation's block norms
+//               (bound = fma(sum_b fma(err_b, xnorm_b), 1.001f, 1e-5f)), upper = coarse + bound, logits = -inf.
+//               Wave 0 owns one row per lane and keeps the workgroup's best top_k+9 eligible keys (score, then
+//               lower row first) sorted across its lanes, inserting only keys above the current cut.
+//  2. seeds     one workgroup: merges the per-workgroup lists (held in registers) into the global top_k+8 seeds
+//               plus one more key to detect a tie at the cut, dedupes the must ids (first occurrence), rescoring
+//               seeds and must rows exactly with the Q8_0 row dot, tau = k-th best exact seed.
+//  3. cand      one workgroup per 256 rows: candidates {r < n_valid, unmarked, upper[r] >= tau} compacted with a
+//               ballot scan, appended to the row list, rescored exactly in the same workgroup, and the greedy argmax
+//               key folded in with a 64-bit atomic max; the last workgroup to finish writes the stats record.
 //
 // Exact rows use the same block products and serial chain as the decode GEMV, so each rescored logit is
-// bit-identical to the full Q8_0 head. The mark array (1 byte per row) lives in the workspace: screen clears
-// its rows, seeds sets 2 (seed) and 3 (must), cand skips every marked row.
+// bit-identical to the full Q8_0 head. The mark array (1 byte per row) lives in the workspace: screen clears its
+// rows, seeds sets 2 (seed) and 3 (must), cand skips every marked row.
 #include "qh_device.h"
 #include "qh_internal.h"
 
@@ -35,17 +36,40 @@ struct HeadCtrl {
 
 constexpr int kMaxMust = 1024;
 constexpr int kScreenThreads = 256;
-constexpr int kSeedThreads = 512;
+constexpr int kScreenU = 8;         // 16-byte weight chunks per thread per tile
+constexpr int kScreenMaxRows = 64;  // rows per tile: one per lane of wave 0
+constexpr int kScreenErrU = 4;      // 4-byte error words per thread per tile
+constexpr int kScreenMaxShare = 1024;  // rows per screen workgroup: their keys sit in LDS until the final selection
+constexpr int kSeedThreads = 1024;
+constexpr int kSeedMaxPool = 2048;     // keys that survive the seed threshold, held in LDS
+constexpr int kSeedKeysPerThread = 32; // fallback when more survive: every partial key in registers
 constexpr int kCandThreads = 256;
+constexpr int kCandRowsPerThread = 4;
 
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
+// Rows per screen tile: even, at most one per wave-0 lane, and at most kScreenU * 256 Q4_0 chunks.
 int screen_tile_rows(int nb) {
-    // prod tile (f32, nb+1 per row) + error tile (f16, nb per row) within 48 KB; even row count.
-    int t = (48 * 1024) / ((nb + 1) * 4 + nb * 2);
-    t = t > 256 ? 256 : t;
+    int t = kScreenU * kScreenThreads / nb;
+    t = t > kScreenMaxRows ? kScreenMaxRows : t;
     t &= ~1;
     return t < 2 ? 2 : t;
+}
+
+int screen_grid(int V, int tile) {
+    int g = 4 * device_cus();
+    const int min_g = (V + kScreenMaxShare - 3) / (kScreenMaxShare - 2);  // shares are rounded to even rows
+    g = g > min_g ? g : min_g;
+    const int tiles = (V + tile - 1) / tile;
+    return g < tiles ? g : tiles;
+}
+
+int cand_grid(int nv) {
+    int g = device_cus();
+    const int min_g = (nv + kCandRowsPerThread * kCandThreads - 1) / (kCandRowsPerThread * kCandThreads);
+    g = g > min_g ? g : min_g;
+    const int chunks = (nv + kCandThreads - 1) / kCandThreads;
+    return g < chunks ? g : chunks;
 }
 
 struct WsLayout {
@@ -54,8 +78,7 @@ struct WsLayout {
 
 WsLayout ws_layout(int V, int D, int top_k) {
     const int nb = D / QK;
-    const int tile = screen_tile_rows(nb);
-    const int parts = (V + tile - 1) / tile;
+    const int parts = screen_grid(V, screen_tile_rows(nb));
     const int keep = top_k + 9;
     WsLayout l;
     l.mark = 0;
@@ -90,145 +113,333 @@ __device__ float chain(const float* p, const float* __restrict__ xd, int nb) {
     return acc;
 }
 
+// Register set of one screen tile: the Q4_0 chunks with their block scales, and the f16 error words.
+struct ScreenRegs {
+    uint4 w[kScreenU];
+    uint16_t sc[kScreenU];
+    uint32_t e[kScreenErrU];
+
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ w4, const uint16_t* __restrict__ s4,
+                                         const uint32_t* __restrict__ e32, int r, int nrows, int nb) {
+        const int tid = (int)threadIdx.x;
+        const int nch = nrows * nb;
+        const uint8_t* base = w4 + (size_t)r * nb * (QK / 2);
+        const uint16_t* sbase = s4 + (size_t)r * nb;
+#pragma unroll
+        for (int j = 0; j < kScreenU; ++j) {
+            const int c = min(j * kScreenThreads + tid, nch - 1);
+            w[j] = load16(base + (size_t)c * 16);
+            sc[j] = sbase[c];
+        }
+        // nb is even, so a tile's errors are nrows * nb / 2 whole 4-byte words starting 4-byte aligned.
+        const int n32 = nrows * nb / 2;
+        const uint32_t* ebase = e32 + (size_t)r * nb / 2;
+#pragma unroll
+        for (int j = 0; j < kScreenErrU; ++j) e[j] = ebase[min(j * kScreenThreads + tid, n32 - 1)];
+    }
+
+    // Block products and block errors (as f32) into LDS tiles [row][pstride].
+    __device__ __forceinline__ void stage(float* prod, float* errf, int pstride, int nrows, int nb, uint32_t nb_magic,
+                                          const int8_t* xs) const {
+        const int tid = (int)threadIdx.x;
+        const int nch = nrows * nb;
+#pragma unroll
+        for (int j = 0; j < kScreenU; ++j) {
+            const int c = j * kScreenThreads + tid;
+            const uint32_t g = (uint32_t)min(c, nch - 1);
+            const uint32_t rt = nb == 1 ? g : div_magic(g, nb_magic);
+            const uint32_t b = g - rt * (uint32_t)nb;
+            const uint4 xlo = *reinterpret_cast<const uint4*>(xs + b * QK);
+            const uint4 xhi = *reinterpret_cast<const uint4*>(xs + b * QK + 16);
+            const int s = dot_q4_block(w[j], xlo, xhi);
+            if (c < nch) prod[rt * pstride + b] = (float)s * f16_to_f32(sc[j]);
+        }
+        const int n32 = nrows * nb / 2;
+#pragma unroll
+        for (int j = 0; j < kScreenErrU; ++j) {
+            const int i = j * kScreenThreads + tid;
+            const uint32_t g = 2u * (uint32_t)min(i, n32 - 1);  // first of the word's two blocks (same row)
+            const uint32_t rt = div_magic(g, nb_magic);
+            const uint32_t b = g - rt * (uint32_t)nb;
+            if (i < n32) {
+                errf[rt * pstride + b] = f16_to_f32((uint16_t)(e[j] & 0xffffu));
+                errf[rt * pstride + b + 1] = f16_to_f32((uint16_t)(e[j] >> 16));
+            }
+        }
+    }
+};
+
+// Ranks within a wave: a[s] holds key number s*64 + lane of n keys (n <= 64*NS, missing keys are 0); rank[s]
+// receives how many of the n keys are larger than a[s]. Keys are broadcast lane by lane through scalar registers
+// (v_readlane), so every lane reads different LDS words beforehand and nothing serialises on one address.
+// Every lane of the wave must call it with the same n.
+template <int NS>
+__device__ __forceinline__ void wave_rank(const uint64_t (&a)[NS], int n, int (&rank)[NS]) {
+#pragma unroll
+    for (int t = 0; t < NS; ++t) rank[t] = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        if (s * 64 >= n) break;
+        const int lo = (int)(uint32_t)a[s], hi = (int)(uint32_t)(a[s] >> 32);
+#pragma unroll 16
+        for (int j = 0; j < 64; ++j) {
+            const uint64_t kj = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi, j) << 32) |
+                                (uint64_t)(uint32_t)__builtin_amdgcn_readlane(lo, j);
+#pragma unroll
+            for (int t = 0; t < NS; ++t) rank[t] += kj > a[t] ? 1 : 0;
+        }
+    }
+}
+
 }  // namespace
 
-template <int U>
 __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
-    const uint8_t* __restrict__ w4, const uint16_t* __restrict__ s4, const uint16_t* __restrict__ err,
+    const uint8_t* __restrict__ w4, const uint16_t* __restrict__ s4, const uint32_t* __restrict__ e32,
     const int8_t* __restrict__ xq, const float* __restrict__ xd, int V, int nb, int nv, const int32_t* __restrict__ must,
     int n_must, int tile, uint32_t nb_magic, float* __restrict__ coarse, float* __restrict__ upper,
-    float* __restrict__ logits, uint8_t* __restrict__ mark, uint64_t* __restrict__ seedpart, int n_keep,
-    HeadCtrl* __restrict__ ctrl) {
+    float* __restrict__ logits, uint8_t* __restrict__ mark, uint64_t* __restrict__ seedpart, int n_keep) {
     extern __shared__ float smem[];
-    float* prod = smem;                                                    // [tile][nb + 1]
-    float* xnorm = prod + (size_t)tile * (nb + 1);                         // [nb]
-    uint16_t* errs = reinterpret_cast<uint16_t*>(xnorm + nb);              // [tile][nb]
-    uint8_t* mflag = reinterpret_cast<uint8_t*>(errs + (size_t)tile * nb);  // [tile]
-    __shared__ uint64_t wbest[2][kScreenThreads / 64];
+    const int ps = prod_stride4(nb);
+    const int nb4 = (nb + 3) & ~3;
+    float* xds = smem;                                   // [nb4]
+    float* xnorm = xds + nb4;                            // [nb4]
+    float* prod0 = xnorm + nb4;                          // [tile][ps] block products, two buffers
+    float* prod1 = prod0 + (size_t)tile * ps;
+    float* errf0 = prod1 + (size_t)tile * ps;            // [tile][ps] block errors, two buffers
+    float* errf1 = errf0 + (size_t)tile * ps;
+    uint64_t* wkeys = reinterpret_cast<uint64_t*>(errf1 + (size_t)tile * ps);  // [kScreenMaxShare + 2]
+    uint8_t* mflag = reinterpret_cast<uint8_t*>(wkeys + kScreenMaxShare + 2);  // [2][tile]
+    int8_t* xs = reinterpret_cast<int8_t*>(mflag + ((2 * (size_t)tile + 15) & ~size_t(15)));  // [nb * 32]
+    __shared__ int n_elig;
+    __shared__ uint64_t lvl2[4 * 64];
 
     const int tid = (int)threadIdx.x;
-    const int ra = (int)blockIdx.x * tile;
-    const int nrows = min(tile, V - ra);
-    const int pstride = nb + 1;
-    if (blockIdx.x == 0 && tid == 0) {
-        ctrl->argmax_key = 0ull;
-        ctrl->n_cand = 0u;
-        ctrl->done = 0u;
+    lvl2[tid] = 0ull;  // ordered before its writes by the barriers of the tile loop
+    const int ra = (int)((long)blockIdx.x * V / gridDim.x) & ~1;  // even, so error words stay 4-byte aligned
+    const int rb = blockIdx.x + 1 == gridDim.x ? V : (int)((long)(blockIdx.x + 1) * V / gridDim.x) & ~1;
+    if (ra >= rb) {  // uniform per workgroup: an empty share still publishes an empty list
+        if (tid < n_keep) seedpart[(size_t)blockIdx.x * n_keep + tid] = 0ull;
+        return;
     }
-    for (int i = tid; i < nrows; i += kScreenThreads) {
-        mflag[i] = 0;
-        mark[ra + i] = 0;
-    }
+
+    ScreenRegs A, B;
+    A.load(w4, s4, e32, ra, min(tile, rb - ra), nb);
+    const int cols = nb * QK;
+    for (int i = tid; i < cols / 16; i += kScreenThreads) reinterpret_cast<uint4*>(xs)[i] = load16(xq + i * 16);
+    for (int i = tid; i < nb; i += kScreenThreads) xds[i] = xd[i];
+    __syncthreads();
     // xnorm_b = d_b * sqrt(sum q^2) (model.cpp:247-251); the sum is an exact integer in f32.
     for (int b = tid; b < nb; b += kScreenThreads) {
         float ss = 0.0f;
         for (int i = 0; i < QK; ++i) {
-            const float v = (float)xq[b * QK + i];
+            const float v = (float)xs[b * QK + i];
             ss = __builtin_fmaf(v, v, ss);
         }
-        xnorm[b] = xd[b] * __builtin_sqrtf(ss);
-    }
-    // Error tile -> LDS (4-byte loads; ra is even so the tile starts 4-byte aligned).
-    {
-        const int n16 = nrows * nb;
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(err + (size_t)ra * nb);
-        uint32_t* dst = reinterpret_cast<uint32_t*>(errs);
-        for (int i = tid; i < n16 / 2; i += kScreenThreads) dst[i] = src[i];
-        if ((n16 & 1) && tid == 0) errs[n16 - 1] = err[(size_t)ra * nb + n16 - 1];
-    }
-    __syncthreads();
-    for (int i = tid; i < n_must; i += kScreenThreads) {
-        const int id = must[i];
-        if (id >= ra && id < ra + nrows && id < nv) mflag[id - ra] = 1;
+        xnorm[b] = xds[b] * __builtin_sqrtf(ss);
     }
 
-    // 4-bit block products of the tile.
-    const int nchunks = nrows * nb;
-    const uint8_t* base = w4 + (size_t)ra * nb * (QK / 2);
-    const uint16_t* sbase = s4 + (size_t)ra * nb;
-    for (int c0 = 0; c0 < nchunks; c0 += kScreenThreads * U) {
-        uint4 w[U];
-#pragma unroll
-        for (int j = 0; j < U; ++j) {
-            const int c = c0 + j * kScreenThreads + tid;
-            w[j] = c < nchunks ? load16(base + (size_t)c * 16) : make_uint4(0u, 0u, 0u, 0u);
+    int elig = 0;  // wave 0: eligible keys so far
+    // One tile whose chunks sit in `regs`: stage into LDS, then wave 0 (one row per lane) runs both chains.
+    auto tile_body = [&](const ScreenRegs& regs, int r, float* prod, float* errf, uint8_t* mf) {
+        const int nrows = min(tile, rb - r);
+        regs.stage(prod, errf, ps, nrows, nb, nb_magic, xs);
+        for (int i = tid; i < nrows; i += kScreenThreads) {
+            mf[i] = 0;
+            mark[r + i] = 0;
         }
-#pragma unroll
-        for (int j = 0; j < U; ++j) {
-            const int c = c0 + j * kScreenThreads + tid;
-            const uint32_t g = (uint32_t)c;
-            const uint32_t rt = nb == 1 ? g : div_magic(g, nb_magic);
-            const uint32_t b = g - rt * (uint32_t)nb;
-            const uint4 xlo = load16(xq + b * QK);
-            const uint4 xhi = load16(xq + b * QK + 16);
-            const int s = dot_q4_block(w[j], xlo, xhi);
-            if (c < nchunks) prod[rt * pstride + b] = (float)s * f16_to_f32(sbase[g]);
-        }
-    }
-    __syncthreads();
-
-    uint64_t key = 0;
-    if (tid < nrows) {
-        const int r = ra + tid;
-        const float c = chain(prod + tid * pstride, xd, nb);
-        const uint16_t* e = errs + tid * nb;
-        float bound = 0.0f;
-        for (int b = 0; b < nb; ++b) bound = __builtin_fmaf(f16_to_f32(e[b]), xnorm[b], bound);
-        bound = __builtin_fmaf(bound, 1.001f, 1e-5f);  // model.cpp:271
-        coarse[r] = c;
-        upper[r] = c + bound;
-        logits[r] = -__builtin_inff();
-        if (r < nv && !mflag[tid]) key = score_key(c, r);
-    }
-    // Best n_keep keys of the tile, best first.
-    const int lane = tid & 63, wave = tid >> 6;
-    uint64_t* out = seedpart + (size_t)blockIdx.x * n_keep;
-    for (int i = 0; i < n_keep; ++i) {
-        const uint64_t m = wave_max_u64(key);
-        if (lane == 0) wbest[i & 1][wave] = m;
         __syncthreads();
-        uint64_t best = wbest[i & 1][0];
+        if (n_must > 0) {
+            for (int i = tid; i < n_must; i += kScreenThreads) {
+                const int id = must[i];
+                if (id >= r && id < r + nrows && id < nv) mf[id - r] = 1;
+            }
+            __syncthreads();
+        }
+        if (tid < 64) {
+            uint64_t key = 0;
+            if (tid < nrows) {
+                const int row = r + tid;
+                const float c = chain_lds4(prod + tid * ps, xds, nb);
+                float bound = chain_lds4(errf + tid * ps, xnorm, nb);
+                bound = __builtin_fmaf(bound, 1.001f, 1e-5f);  // model.cpp:271
+                coarse[row] = c;
+                upper[row] = c + bound;
+                logits[row] = -__builtin_inff();
+                if (row < nv && !mf[tid]) key = score_key(c, row);
+                wkeys[row - ra] = key;
+            }
+            elig += __popcll(__ballot(key != 0));
+        }
+    };
+    // Two register sets in straight-line halves, so the wait before staging one set leaves the other's loads in
+    // flight. Loads in the steady-state loop are unconditional (a conditional load makes the compiler's wait
+    // counting assume the worst at the join); the last one or two tiles are peeled.
+    const int n_tiles = (rb - ra + tile - 1) / tile;
+    int t = 0;
+    while (t + 2 < n_tiles) {
+        B.load(w4, s4, e32, ra + (t + 1) * tile, min(tile, rb - ra - (t + 1) * tile), nb);
+        tile_body(A, ra + t * tile, prod0, errf0, mflag);
+        A.load(w4, s4, e32, ra + (t + 2) * tile, min(tile, rb - ra - (t + 2) * tile), nb);
+        tile_body(B, ra + (t + 1) * tile, prod1, errf1, mflag + tile);
+        t += 2;
+    }
+    if (t + 1 < n_tiles) {
+        B.load(w4, s4, e32, ra + (t + 1) * tile, min(tile, rb - ra - (t + 1) * tile), nb);
+        tile_body(A, ra + t * tile, prod0, errf0, mflag);
+        tile_body(B, ra + (t + 1) * tile, prod1, errf1, mflag + tile);
+    } else {
+        tile_body(A, ra + t * tile, prod0, errf0, mflag);
+    }
+    const int R = rb - ra;
+    if (tid == 0) n_elig = elig;
+    __syncthreads();
+    // The share's best n_keep keys (keys are unique). Level 1: each wave ranks its quarter of the share (at most
+    // 256 keys) and keeps its best n_keep; level 2: wave 0 ranks the 4 * n_keep survivors.
+    const int lane = tid & 63, wave = tid >> 6;
+    const int Q = (R + 3) / 4;
+    const int q0 = min(R, wave * Q), q1 = min(R, q0 + Q);
+    {
+        uint64_t a[4];
+        int rk[4];
 #pragma unroll
-        for (int w = 1; w < kScreenThreads / 64; ++w) best = wbest[i & 1][w] > best ? wbest[i & 1][w] : best;
-        if (key == best) key = 0;
-        if (tid == 0) out[i] = best;
+        for (int s2 = 0; s2 < 4; ++s2) {
+            const int i = q0 + s2 * 64 + lane;
+            a[s2] = i < q1 ? wkeys[i] : 0ull;
+        }
+        if (Q <= 128) {  // uniform
+            uint64_t a2[2] = {a[0], a[1]};
+            int rk2[2];
+            wave_rank<2>(a2, q1 - q0, rk2);
+            rk[0] = rk2[0];
+            rk[1] = rk2[1];
+            rk[2] = rk[3] = n_keep;
+        } else {
+            wave_rank<4>(a, q1 - q0, rk);
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+            if (a[s2] != 0 && rk[s2] < n_keep) lvl2[wave * n_keep + rk[s2]] = a[s2];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        uint64_t* part = seedpart + (size_t)blockIdx.x * n_keep;
+        uint64_t a[4];
+        int rk[4];
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+            const int i = s2 * 64 + lane;
+            a[s2] = i < 4 * n_keep ? lvl2[i] : 0ull;
+        }
+        if (4 * n_keep <= 64) {  // uniform
+            uint64_t a1[1] = {a[0]};
+            int rk1[1];
+            wave_rank<1>(a1, 4 * n_keep, rk1);
+            rk[0] = rk1[0];
+            rk[1] = rk[2] = rk[3] = n_keep;
+        } else {
+            wave_rank<4>(a, 4 * n_keep, rk);
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+            if (a[s2] != 0 && rk[s2] < n_keep) part[rk[s2]] = a[s2];
+        if (lane < n_keep && lane >= n_elig) part[lane] = 0ull;
     }
 }
 
 __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
     const uint8_t* __restrict__ w8, const uint16_t* __restrict__ s8, const int8_t* __restrict__ xq,
-    const float* __restrict__ xd, int nb, int nv, int k, int n_keep, int n_parts, uint64_t* __restrict__ seedpart,
-    const int32_t* __restrict__ must, int n_must, uint8_t* __restrict__ mark, int32_t* __restrict__ rows,
-    float* __restrict__ logits, HeadCtrl* __restrict__ ctrl) {
+    const float* __restrict__ xd, int nb, int nv, int k, int n_keep, int n_parts,
+    const uint64_t* __restrict__ seedpart, const int32_t* __restrict__ must, int n_must, uint8_t* __restrict__ mark,
+    int32_t* __restrict__ rows, float* __restrict__ logits, HeadCtrl* __restrict__ ctrl) {
     extern __shared__ float wprod[];  // [waves][nb]
+    constexpr int kWaves = kSeedThreads / 64;
     __shared__ uint64_t best[QH_HEAD_MAX_TOPK + 9];
-    __shared__ uint64_t wb[2][kSeedThreads / 64];
+    __shared__ uint64_t wb[2][kWaves];
+    __shared__ uint64_t pool[kSeedMaxPool];
     __shared__ int rowl[QH_HEAD_MAX_TOPK + 8 + kMaxMust];
     __shared__ float exact[QH_HEAD_MAX_TOPK + 8 + kMaxMust];
     __shared__ int counts[2];
+    __shared__ int n_pool;
 
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    constexpr int kWaves = kSeedThreads / 64;
     const int n_seed = n_keep - 1;
+    // Each share's list holds its best n_keep keys, best first. Any n_keep distinct keys bound the global n_keep-th
+    // key from below; here each wave takes a slice of the list heads and offers its n_keep-th best head, and L is
+    // the largest offer (0 if no slice has n_keep heads). Only keys >= L can be selected.
+    __shared__ unsigned long long L_sh;
+    // Every partial key in registers, loaded together with the list heads below (one round trip).
     const int total = n_parts * n_keep;
-    for (int i = 0; i < n_keep; ++i) {
-        uint64_t m = 0;
-        int mi = -1;
-        for (int j = tid; j < total; j += kSeedThreads) {
-            const uint64_t v = seedpart[j];
-            if (v > m) {
-                m = v;
-                mi = j;
-            }
-        }
-        const uint64_t g = wave_max_u64(m);
-        if (lane == 0) wb[i & 1][wave] = g;
-        __syncthreads();
-        uint64_t gb = wb[i & 1][0];
+    uint64_t kv[kSeedKeysPerThread];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) gb = wb[i & 1][w] > gb ? wb[i & 1][w] : gb;
-        if (gb != 0 && m == gb) seedpart[mi] = 0;  // keys are unique (one per row)
-        if (tid == 0) best[i] = gb;
+    for (int j = 0; j < kSeedKeysPerThread; ++j) {
+        const int i = j * kSeedThreads + tid;
+        kv[j] = i < total ? seedpart[i] : 0ull;
+    }
+    if (tid < QH_HEAD_MAX_TOPK + 9) best[tid] = 0ull;
+    if (tid == 0) {
+        n_pool = 0;
+        L_sh = 0ull;
+    }
+    __syncthreads();
+    {
+        const int H = (n_parts + kWaves - 1) / kWaves;  // <= 128 (n_parts <= 2048)
+        const int h0 = min(n_parts, wave * H), h1 = min(n_parts, h0 + H);
+        uint64_t a[2];
+        int rk[2];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const int t = h0 + s2 * 64 + lane;
+            a[s2] = t < h1 ? seedpart[(size_t)t * n_keep] : 0ull;
+        }
+        wave_rank<2>(a, h1 - h0, rk);
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+            if (a[s2] != 0 && rk[s2] == n_keep - 1) atomicMax(&L_sh, (unsigned long long)a[s2]);
+    }
+    __syncthreads();
+    const uint64_t L = L_sh;
+#pragma unroll
+    for (int j = 0; j < kSeedKeysPerThread; ++j) {
+        const uint64_t v = kv[j];
+        if (v != 0 && v >= L) {
+            const int at = atomicAdd(&n_pool, 1);
+            if (at < kSeedMaxPool) pool[at] = v;
+        }
+    }
+    __syncthreads();
+    const int np = n_pool;
+    if (np <= 256) {
+        if (wave == 0) {  // rank selection within the pool (keys are unique)
+            uint64_t a[4];
+            int rk[4];
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const int i = s2 * 64 + lane;
+                a[s2] = i < np ? pool[i] : 0ull;
+            }
+            wave_rank<4>(a, np, rk);
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2)
+                if (a[s2] != 0 && rk[s2] < n_keep) best[rk[s2]] = a[s2];
+        }
+    } else {
+        // Many survivors (e.g. many equal scores): n_keep rounds of a block-wide maximum over every partial key.
+        for (int i = 0; i < n_keep; ++i) {
+            uint64_t m = 0;
+#pragma unroll
+            for (int j = 0; j < kSeedKeysPerThread; ++j) m = kv[j] > m ? kv[j] : m;
+            const uint64_t g = wave_max_u64(m);
+            if (lane == 0) wb[i & 1][wave] = g;
+            __syncthreads();
+            uint64_t gb = wb[i & 1][0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) gb = wb[i & 1][w] > gb ? wb[i & 1][w] : gb;
+            if (gb != 0 && m == gb) {
+#pragma unroll
+                for (int j = 0; j < kSeedKeysPerThread; ++j) kv[j] = kv[j] == gb ? 0ull : kv[j];
+            }
+            if (tid == 0) best[i] = gb;
+        }
     }
     __syncthreads();
     if (tid == 0) {
@@ -294,6 +505,8 @@ __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
             kmax = kk > kmax ? kk : kmax;
         }
         ctrl->argmax_key = kmax;
+        ctrl->n_cand = 0u;
+        ctrl->done = 0u;
     }
 }
 
@@ -303,31 +516,51 @@ __global__ __launch_bounds__(kCandThreads) void head_cand_kernel(
     int32_t* __restrict__ rows, float* __restrict__ logits, HeadCtrl* __restrict__ ctrl,
     qh_head_stats* __restrict__ stats) {
     extern __shared__ float wprod[];  // [waves][nb]
-    __shared__ int candl[kCandThreads];
-    __shared__ int wcount[kCandThreads / 64];
-    __shared__ int base_sh;
-    __shared__ uint64_t wkey[kCandThreads / 64];
     constexpr int kWaves = kCandThreads / 64;
+    __shared__ int candl[kCandRowsPerThread * kCandThreads];
+    __shared__ int wcount[kCandRowsPerThread][kWaves];
+    __shared__ int base_sh;
+    __shared__ uint64_t wkey[kWaves];
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = (int)blockIdx.x * kCandThreads + tid;
+    // Rows [ca, cb) of this workgroup (at most kCandRowsPerThread per thread): every row's bound and mark are
+    // loaded up front, candidates are compacted with ballots and rescored, one row per wave at a time.
+    const int ca = (int)((long)blockIdx.x * nv / gridDim.x), cb = (int)((long)(blockIdx.x + 1) * nv / gridDim.x);
     const float tau = ctrl->tau;
-    const bool cand = r < nv && mark[r] == 0 && upper[r] >= tau;
-    const uint64_t ball = __ballot(cand);
-    const int pos = __popcll(ball & ((1ull << lane) - 1ull));
-    if (lane == 0) wcount[wave] = __popcll(ball);
-    __syncthreads();
-    int off = 0, count = 0;
-    for (int w = 0; w < kWaves; ++w) {
-        off += w < wave ? wcount[w] : 0;
-        count += wcount[w];
+    const int row_base = ctrl->n_seeds + ctrl->n_must;
+    float up[kCandRowsPerThread];
+    uint8_t mk[kCandRowsPerThread];
+#pragma unroll
+    for (int j = 0; j < kCandRowsPerThread; ++j) {
+        const int r = min(ca + j * kCandThreads + tid, cb - 1);
+        up[j] = upper[r];
+        mk[j] = mark[r];
     }
-    if (cand) candl[off + pos] = r;
-    if (tid == 0 && count > 0) base_sh = (int)atomicAdd(&ctrl->n_cand, (unsigned)count);
+    bool cand[kCandRowsPerThread];
+    int pos[kCandRowsPerThread];
+#pragma unroll
+    for (int j = 0; j < kCandRowsPerThread; ++j) {
+        const int r = ca + j * kCandThreads + tid;
+        cand[j] = r < cb && mk[j] == 0 && up[j] >= tau;
+        const uint64_t ball = __ballot(cand[j]);
+        pos[j] = __popcll(ball & ((1ull << lane) - 1ull));
+        if (lane == 0) wcount[j][wave] = __popcll(ball);
+    }
     __syncthreads();
+    int count = 0;
+#pragma unroll
+    for (int j = 0; j < kCandRowsPerThread; ++j) {
+        int off = count;
+        for (int w = 0; w < kWaves; ++w) {
+            off += w < wave ? wcount[j][w] : 0;
+            count += wcount[j][w];
+        }
+        if (cand[j]) candl[off + pos[j]] = ca + j * kCandThreads + tid;
+    }
     uint64_t kbest = 0;
     if (count > 0) {
-        const int row_off = ctrl->n_seeds + ctrl->n_must + base_sh;
-        for (int i = tid; i < count; i += kCandThreads) rows[row_off + i] = candl[i];
+        if (tid == 0) base_sh = (int)atomicAdd(&ctrl->n_cand, (unsigned)count);
+        __syncthreads();
+        for (int i = tid; i < count; i += kCandThreads) rows[row_base + base_sh + i] = candl[i];
         float* p = wprod + wave * nb;
         for (int j0 = 0; j0 < count; j0 += kWaves) {
             const int j = j0 + wave;
@@ -370,11 +603,13 @@ __global__ __launch_bounds__(kCandThreads) void head_cand_kernel(
 
 size_t head_workspace_bytes(int V, int D, int top_k) { return ws_layout(V, D, top_k).total; }
 
+bool head_shape_supported(int D) { return D % 64 == 0 && D <= kMaxHeadCols; }
+
 hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4, const qh_tensor& err,
                                  const int8_t* xq, const float* xd, const qh_head_query& q, const qh_head_out& out,
                                  void* ws, hipStream_t s) {
     const int V = head8.rows, D = head8.cols, nb = D / QK;
-    if (q.n_must > kMaxMust) return hipErrorInvalidValue;
+    if (q.n_must > kMaxMust || !head_shape_supported(D)) return hipErrorInvalidValue;
     const int nv = (q.n_valid > 0 && q.n_valid < V) ? q.n_valid : V;
     const WsLayout l = ws_layout(V, D, q.top_k);
     uint8_t* wsb = static_cast<uint8_t*>(ws);
@@ -385,26 +620,26 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
     const uint16_t* s8 = reinterpret_cast<const uint16_t*>(w8 + qh_quant_bytes(QH_Q8_0, V, D));
     const uint8_t* w4 = static_cast<const uint8_t*>(head4.data);
     const uint16_t* s4 = reinterpret_cast<const uint16_t*>(w4 + qh_quant_bytes(QH_Q4_0, V, D));
-    const uint16_t* e16 = static_cast<const uint16_t*>(err.data);
+    const uint32_t* e32 = static_cast<const uint32_t*>(err.data);
 
     const int tile = screen_tile_rows(nb);
-    const int parts = (V + tile - 1) / tile;
+    const int grid = screen_grid(V, tile);
     const int n_keep = q.top_k + 9;
+    if (grid * n_keep > kSeedThreads * kSeedKeysPerThread || grid > kSeedMaxPool) return hipErrorInvalidValue;
     const uint32_t magic = nb == 1 ? 0u : (uint32_t)((0x100000000ull + (uint64_t)nb - 1) / (uint64_t)nb);
-    const size_t lds1 = (size_t)tile * (nb + 1) * 4 + (size_t)nb * 4 + (size_t)tile * nb * 2 + (size_t)tile;
-    hipLaunchKernelGGL((head_screen_kernel<4>), dim3(parts), dim3(kScreenThreads), lds1, s, w4, s4, e16, xq, xd, V, nb,
-                       nv, q.must, q.n_must, tile, magic, out.coarse, out.upper, out.logits, mark, seedpart, n_keep,
-                       ctrl);
+    const size_t lds1 = ((size_t)2 * ((nb + 3) & ~3) + 4 * (size_t)tile * prod_stride4(nb)) * 4 +
+                        ((size_t)kScreenMaxShare + 2) * 8 + ((2 * (size_t)tile + 15) & ~size_t(15)) + (size_t)D;
+    hipLaunchKernelGGL(head_screen_kernel, dim3(grid), dim3(kScreenThreads), lds1, s, w4, s4, e32, xq, xd, V, nb, nv,
+                       q.must, q.n_must, tile, magic, out.coarse, out.upper, out.logits, mark, seedpart, n_keep);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const size_t lds2 = (size_t)(kSeedThreads / 64) * nb * 4;
     hipLaunchKernelGGL(head_seed_kernel, dim3(1), dim3(kSeedThreads), lds2, s, w8, s8, xq, xd, nb, nv, q.top_k, n_keep,
-                       parts, seedpart, q.must, q.n_must, mark, out.rows, out.logits, ctrl);
+                       grid, seedpart, q.must, q.n_must, mark, out.rows, out.logits, ctrl);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     const size_t lds3 = (size_t)(kCandThreads / 64) * nb * 4;
-    hipLaunchKernelGGL(head_cand_kernel, dim3((unsigned)((nv + kCandThreads - 1) / kCandThreads)), dim3(kCandThreads),
-                       lds3, s, w8, s8, xq, xd, nb, nv, out.upper, mark, out.rows, out.logits, ctrl, out.stats);
+    hipLaunchKernelGGL(head_cand_kernel, dim3((unsigned)cand_grid(nv)), dim3(kCandThreads), lds3, s, w8, s8, xq, xd, nb, nv, out.upper, mark, out.rows, out.logits, ctrl, out.stats);
     return hipGetLastError();
 }
 

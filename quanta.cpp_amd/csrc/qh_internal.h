@@ -18,11 +18,16 @@ int check_hip(hipError_t e, const char* what);
 // Launch configuration of the decode GEMV for one (dtype, cols) pair.
 struct GemvPlan {
     int unroll;     // 16-byte chunks each thread loads per pass (template instance)
-    int tile_rows;  // rows per workgroup
+    int tile_rows;  // rows per workgroup (per tile for the streaming kernel)
     bool act_lds;   // stage the activation in LDS (large matrices) instead of loading it with the weights
+    bool stream;    // persistent streaming kernel (large matrices): `grid` workgroups walk the tiles
+    int grid;       // workgroups of the streaming kernel
 };
 GemvPlan gemv_plan(int dtype, int cols, int rows);
 size_t gemv_lds_bytes(int cols, int tile_rows, bool act_lds);
+
+// Compute units of the current device (cached per device).
+int device_cus();
 
 // Largest supported cols for the decode GEMV and the prefill matmul.
 constexpr int kMaxCols = 32768;
@@ -32,9 +37,13 @@ hipError_t launch_gemv(float* out, const qh_tensor& W, const int8_t* xq, const f
                        const GemvPlan& plan, hipStream_t s);
 hipError_t launch_matmul(float* out, int ldo, const qh_tensor& W, const int8_t* xq, const float* xd, int n,
                          int r0, int r1, hipStream_t s);
-hipError_t launch_argmax(const float* logits, int n, int32_t* index, hipStream_t s);
+size_t argmax_workspace_bytes(int n);
+hipError_t launch_argmax(const float* logits, int n, int32_t* index, void* ws, hipStream_t s);
 
-// Shortlist head. Workspace layout is private to qh_head.hip.
+// Shortlist head. Workspace layout is private to qh_head.hip. Supported hidden sizes: D % 64 == 0 (whole 4-byte
+// words of f16 block errors per row) and D <= kMaxHeadCols (a 64-row tile's errors fit one register pass).
+constexpr int kMaxHeadCols = 4096;
+bool head_shape_supported(int D);
 size_t head_workspace_bytes(int V, int D, int top_k);
 hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4, const qh_tensor& err,
                                  const int8_t* xq, const float* xd, const qh_head_query& q, const qh_head_out& out,

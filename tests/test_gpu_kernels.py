@@ -108,6 +108,26 @@ def test_matvec_row_range_and_full_int8_range(qh, oracle, gpu, dtype):
         assert (got[:r0] == 7.0).all() and (got[r1:] == 7.0).all(), "wrote outside [r0, r1)"
 
 
+@pytest.mark.parametrize("dtype", [2, 3])
+def test_matvec_vocab_sized_stream(qh, oracle, synth, gpu, dtype):
+    """Vocabulary-sized matrices take the streaming kernel: whole range and ragged sub-ranges."""
+    import torch
+    N, K = 151936, 896
+    buf = synth.q8_tensor(5000, N, K) if dtype == 2 else synth.q4_tensor(5001, N, K)
+    xq, xd = oracle.quantize_q8(synth.activations(5002, 1, K)[0])
+    W = qh.DeviceTensor.upload(buf, dtype, N, K)
+    dq, dd = _dev(xq, gpu), _dev(xd, gpu)
+    want = oracle.matvec_q(dtype, N, K, buf, xq, xd, threads=8)
+    got = qh.matvec_q(W, dq, dd).cpu().numpy()
+    assert (bits(got) == bits(want)).all()
+    for r0, r1 in [(1, N - 3), (70001, 140003)]:
+        out = torch.full((N,), 7.0, dtype=torch.float32, device=gpu)
+        qh.matvec_q(W, dq, dd, out=out, r0=r0, r1=r1)
+        o = out.cpu().numpy()
+        assert (bits(o[r0:r1]) == bits(want[r0:r1])).all(), (r0, r1)
+        assert (o[:r0] == 7.0).all() and (o[r1:] == 7.0).all()
+
+
 @pytest.mark.parametrize("cols", [32, 64, 96, 4096])
 def test_matvec_other_widths(qh, oracle, gpu, cols):
     rng = np.random.default_rng(cols)
@@ -134,6 +154,15 @@ def test_argmax_first_max(qh, gpu):
     assert int(qh.argmax(x, n=1000).item()) == 0
     y = torch.randn(151936, device=gpu)
     assert int(qh.argmax(y).item()) == int(torch.argmax(y).item())
+    # ragged sizes and equal maxima on both sides of a workgroup slice boundary: the lower index wins
+    for n in (1, 2, 255, 2049, 4097, 1 << 22):
+        z = torch.zeros(n, device=gpu)
+        z[n // 2:] = 1.0
+        assert int(qh.argmax(z).item()) == n // 2
+    z = torch.full((1 << 22,), -1.0, device=gpu)
+    z[3_000_001] = 5.0
+    z[3_999_999] = 5.0
+    assert int(qh.argmax(z).item()) == 3_000_001
 
 
 def test_abi_rejects_bad_arguments(qh, gpu):
