@@ -1,16 +1,26 @@
 // Prefill matmul for n tokens (reference ops_ref.cpp:122-160, contract ops.h:65-70) on gfx950 int8 MFMA.
 //
-// v_mfma_i32_16x16x32_i8 takes K = 32 per instruction, exactly one Q8_0 / Q4_0 block, so every block's
-// exact int32 dot s(row, token, b) arrives in registers on its own and the per-(row, token) chain
-// acc = fma(float(s) * dw_b, dx_b, acc) runs in block order in the lane that holds the element: each
-// output equals the decode GEMV bit for bit. (The K = 64 forms would merge two scale blocks.)
+// v_mfma_i32_16x16x32_i8 takes K = 32 per instruction, exactly one Q8_0 / Q4_0 block, so every block's exact
+// int32 dot s(row, token, b) comes out on its own. The per-(row, token) f32 chain acc = fma(float(s) * dw_b, dx_b,
+// acc) then runs in block order in one thread, so each output equals the decode GEMV bit for bit. (The K = 64
+// forms would merge two scale blocks.)
 //
-// Tiling: a wave computes a 16-row x 16-token tile over the whole K; a workgroup of four waves covers
-// 64 consecutive rows and shares the 16 token rows through L1. Operand layout for one block b: lane l
-// supplies row (l % 16) and k-group (l / 16) as 8 int8 values; the activation operand uses the same
-// k-group split, so the integer sum pairs the same elements. Q4_0 nibbles are unpacked in registers to
-// signed bytes (k-groups 0,1 take the low nibbles of bytes 0-7 / 8-15, k-groups 2,3 the high ones).
-// The result register i of lane l is row 4*(l/16)+i, token l%16.
+// Workgroup: 16 consecutive rows x 16*TT tokens, all of K, in chunks of KC blocks.
+//  * MFMA phase: wave w takes blocks [w*KC/4, (w+1)*KC/4) of the chunk for all TT token tiles (the weight
+//    operand is loaded once and reused across the tiles) and parks the int32 sums in LDS as s[block][row][token];
+//    the chunk's row scales (f16 -> f32) and token scales go to LDS beside them.
+//  * chain phase: each thread owns TT (row, token) pairs (one token, TT rows) and advances their chains over the
+//    chunk's blocks. The chains live in registers across chunks, so LDS only ever holds one chunk.
+//  * two register sets alternate in straight-line halves: the operands of chunk c+1 are loaded before chunk c is
+//    reduced, and the loads of the steady-state loop are unconditional (the tail is peeled).
+// Operand layout of one MFMA (block b): lane l supplies row (l % 16) / token (l % 16) and k-group (l / 16) as 8 int8
+// values; Q4_0 nibbles are unpacked in registers (k-groups 0, 1 take the low nibbles of bytes 0-7 / 8-15, k-groups
+// 2, 3 the high ones). Result register i of lane l is row 4*(l/16)+i, token l%16.
+// Workgroups that share a row tile (different token groups) are numbered so that they land on the same XCD
+// (workgroups are dealt to the 8 XCDs round-robin), where the weights they all read stay in that XCD's L2.
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "qh_device.h"
 #include "qh_internal.h"
 
@@ -18,30 +28,59 @@ namespace qh {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+namespace {
+
+constexpr int kMmThreads = 256;  // 4 waves
+constexpr int kXcds = 8;
+
 // Nibbles (0..15 per byte) -> signed bytes (nibble - 8), no borrow between bytes.
 __device__ __forceinline__ uint32_t nibbles_to_i8(uint32_t v) { return ((v | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
 
-template <int DT>
-__global__ __launch_bounds__(256) void matmul_kernel(float* __restrict__ out, int ldo, const uint8_t* __restrict__ wq,
-                                                     const uint16_t* __restrict__ wscale,
-                                                     const int8_t* __restrict__ xq, const float* __restrict__ xd,
-                                                     int cols, int n, int r0, int r1) {
+template <int TT, int KC>
+struct MmShape {
+    static constexpr int kTok = 16 * TT;           // tokens per workgroup
+    static constexpr int kTokPad = kTok + 4;       // LDS row stride: the 4 row groups of one MFMA store hit different banks
+    static constexpr int kBpw = KC / 4;            // blocks per wave per chunk
+    static constexpr int kDxPer = kTok * KC / kMmThreads;  // token scales each thread stages per chunk
+    static_assert(KC % 4 == 0 && (kTok * KC) % kMmThreads == 0 && 16 * KC <= kMmThreads, "chunk shape");
+};
+
+template <int DT, int TT, int KC>
+struct MmRegs {
+    using S = MmShape<TT, KC>;
+    long a[S::kBpw];          // weight bytes of the wave's blocks (Q4_0: packed, unpacked at use)
+    long x[S::kBpw][TT];      // activation operand per block and token tile
+    float dx[S::kDxPer];      // staged token scales
+    uint16_t dw;              // staged row scale (threads < 16 * KC)
+};
+
+}  // namespace
+
+template <int DT, int TT, int KC>
+__global__ __launch_bounds__(kMmThreads) void matmul_lds_kernel(float* __restrict__ out, int ldo,
+                                                            const uint8_t* __restrict__ wq,
+                                                            const uint16_t* __restrict__ wscale,
+                                                            const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                            int cols, int n, int r0, int r1, int n_tg) {
+    using S = MmShape<TT, KC>;
+    constexpr int kTok = S::kTok, kTokPad = S::kTokPad, kBpw = S::kBpw;
+    __shared__ int sl[KC][16][kTokPad];     // int32 block sums
+    __shared__ float dxs[kTok][KC + 1];     // token scales of the chunk
+    __shared__ float dws[16][KC + 1];       // row scales of the chunk (f32)
     const int nb = cols / QK;
-    const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
-    const int rbase = r0 + (int)blockIdx.x * 64 + wave * 16;
-    const int tbase = (int)blockIdx.y * 16;
-    if (rbase >= r1) return;  // whole wave past the last row (uniform per wave)
 
-    // Operand rows; rows / tokens past the end are clamped for loading and never stored.
+    // XCD-aware numbering: physical workgroup p runs on XCD p % 8; logical tiles [start(x), start(x+1)) go to XCD x.
+    const int G = (int)gridDim.x, p = (int)blockIdx.x;
+    const int xcd = p % kXcds, per = G / kXcds, rem = G % kXcds;
+    const int logical = xcd * per + min(xcd, rem) + p / kXcds;
+    const int rt = logical / n_tg, tg = logical % n_tg;
+    const int rbase = r0 + rt * 16, tbase = tg * kTok;
+
+    // MFMA operands: row (rbase + li) for the weights, tokens (tbase + tt*16 + li) for the activations; rows and
+    // tokens past the end are clamped for loading and never stored.
     const int arow = min(rbase + li, r1 - 1);
-    const int btok = min(tbase + li, n - 1);
-    const int8_t* xrow = xq + (size_t)btok * cols + lq * 8;
-    const float* dxrow = xd + (size_t)btok * nb;
-    const uint16_t* srow[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) srow[i] = wscale + (size_t)min(rbase + 4 * lq + i, r1 - 1) * nb;
-
     const uint8_t* wrow;
     int shift = 0;
     if (DT == kQ8) {
@@ -50,45 +89,357 @@ __global__ __launch_bounds__(256) void matmul_kernel(float* __restrict__ out, in
         wrow = wq + (size_t)arow * (cols / 2) + (lq & 1) * 8;
         shift = (lq >> 1) * 4;
     }
-
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int b = 0; b < nb; ++b) {
-        long a;
-        if (DT == kQ8) {
-            a = *reinterpret_cast<const long*>(wrow + (size_t)b * QK);
-        } else {
-            const uint2 v = *reinterpret_cast<const uint2*>(wrow + (size_t)b * (QK / 2));
-            const uint32_t lo = nibbles_to_i8((v.x >> shift) & 0x0F0F0F0Fu);
-            const uint32_t hi = nibbles_to_i8((v.y >> shift) & 0x0F0F0F0Fu);
-            a = (long)(((uint64_t)hi << 32) | lo);
-        }
-        const long x = *reinterpret_cast<const long*>(xrow + (size_t)b * QK);
-        v4i c = {0, 0, 0, 0};
-        c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, x, c, 0, 0, 0);
-        const float dx = dxrow[b];
+    const int8_t* xrow[TT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf((float)c[i] * f16_to_f32(srow[i][b]), dx, acc[i]);
+    for (int tt = 0; tt < TT; ++tt) xrow[tt] = xq + (size_t)min(tbase + tt * 16 + li, n - 1) * cols + lq * 8;
+    // Staging of the chunk scales: token scale e = j*256 + tid is (token e / KC, block e % KC); row scale tid is
+    // (row tid / KC, block tid % KC) for tid < 16 * KC.
+    const int dw_row = min(rbase + (tid / KC) % 16, r1 - 1);
+
+    auto load = [&](MmRegs<DT, TT, KC>& R, int c0) {
+#pragma unroll
+        for (int i = 0; i < kBpw; ++i) {
+            const int b = min(c0 + wave * kBpw + i, nb - 1);
+            R.a[i] = *reinterpret_cast<const long*>(wrow + (size_t)b * (DT == kQ8 ? QK : QK / 2));
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) R.x[i][tt] = *reinterpret_cast<const long*>(xrow[tt] + (size_t)b * QK);
+        }
+#pragma unroll
+        for (int j = 0; j < S::kDxPer; ++j) {
+            const int e = j * kMmThreads + tid;
+            const int t = min(tbase + e / KC, n - 1), b = min(c0 + e % KC, nb - 1);
+            R.dx[j] = xd[(size_t)t * nb + b];
+        }
+        R.dw = wscale[(size_t)dw_row * nb + min(c0 + tid % KC, nb - 1)];
+    };
+
+    // Chain pairs of this thread: token ctok, rows crow(j) = j * (256 / kTok) + tid / kTok.
+    const int ctok = tid % kTok;
+    float acc[TT];
+#pragma unroll
+    for (int j = 0; j < TT; ++j) acc[j] = 0.0f;
+
+    auto reduce = [&](const MmRegs<DT, TT, KC>& R, int c0) {
+#pragma unroll
+        for (int i = 0; i < kBpw; ++i) {
+            const int bl = wave * kBpw + i;
+            long a = R.a[i];
+            if (DT == kQ4) {
+                const uint64_t v = (uint64_t)a;
+                const uint32_t lo = nibbles_to_i8(((uint32_t)v >> shift) & 0x0F0F0F0Fu);
+                const uint32_t hi = nibbles_to_i8(((uint32_t)(v >> 32) >> shift) & 0x0F0F0F0Fu);
+                a = (long)(((uint64_t)hi << 32) | lo);
+            }
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) {
+                v4i c = {0, 0, 0, 0};
+                c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, R.x[i][tt], c, 0, 0, 0);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) sl[bl][4 * lq + k][tt * 16 + li] = c[k];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < S::kDxPer; ++j) {
+            const int e = j * kMmThreads + tid;
+            dxs[e / KC][e % KC] = R.dx[j];
+        }
+        if (tid < 16 * KC) dws[tid / KC][tid % KC] = f16_to_f32(R.dw);
+        __syncthreads();
+        // The chunk's operands are read first (the loop is unrolled, so the LDS reads overlap), then the chains
+        // advance block by block; blocks past the end of the row leave them unchanged.
+        const int nblk = min(KC, nb - c0);
+        float dxv[KC], pv[KC][TT];
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+            dxv[k] = dxs[ctok][k];
+#pragma unroll
+            for (int j = 0; j < TT; ++j) {
+                const int row = j * (kMmThreads / kTok) + tid / kTok;
+                pv[k][j] = (float)sl[k][row][ctok] * dws[row][k];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+#pragma unroll
+            for (int j = 0; j < TT; ++j) {
+                const float nx = __builtin_fmaf(pv[k][j], dxv[k], acc[j]);
+                acc[j] = k < nblk ? nx : acc[j];
+            }
+        }
+        __syncthreads();
+    };
+
+    const int n_chunks = (nb + KC - 1) / KC;
+    MmRegs<DT, TT, KC> A, B;
+    load(A, 0);
+    int c = 0;
+    while (c + 2 < n_chunks) {
+        load(B, (c + 1) * KC);
+        reduce(A, c * KC);
+        load(A, (c + 2) * KC);
+        reduce(B, (c + 1) * KC);
+        c += 2;
     }
-    const int tok = tbase + li;
+    if (c + 1 < n_chunks) {
+        load(B, (c + 1) * KC);
+        reduce(A, c * KC);
+        reduce(B, (c + 1) * KC);
+    } else {
+        reduce(A, c * KC);
+    }
+
+    const int tok = tbase + ctok;
     if (tok < n) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = rbase + 4 * lq + i;
-            if (r < r1) out[(size_t)tok * ldo + r] = acc[i];
+        for (int j = 0; j < TT; ++j) {
+            const int r = rbase + j * (kMmThreads / kTok) + tid / kTok;
+            if (r < r1) out[(size_t)tok * ldo + r] = acc[j];
         }
     }
 }
+
+// Register-chain variant: a wave owns 16 rows x 16*TT tokens over all of K and runs the chains of its own MFMA
+// outputs in registers (lane l: rows 4*(l/16)+i, token l%16 of each tile), so no block sum goes through LDS. The NW
+// waves of a workgroup share the 16 rows (their weight loads hit L1) and take consecutive token tiles. Blocks go in
+// chunks of 4: two register sets alternate in straight-line halves, the operands of chunk c+1 in flight while chunk c
+// is reduced. VEC (nb % 4 == 0 and 16-byte aligned token scales): the 4 row scales and the token scales of a chunk
+// are single 8- and 16-byte loads.
+template <int DT, int TT, bool VEC>
+struct RegChunk {
+    long a[4];          // weight bytes per block (Q4_0 packed, unpacked at use)
+    long x[4][TT];      // activation operand per block and token tile
+    uint2 dw[4];        // row 4*(l/16)+i: fp16 scales of the chunk's 4 blocks (VEC)
+    float4 dx[TT];      // token of tile tt: f32 scales of the chunk's 4 blocks (VEC)
+    uint16_t dws[VEC ? 1 : 4][VEC ? 1 : 4];  // scalar path: [row i][block]
+    float dxs[VEC ? 1 : TT][VEC ? 1 : 4];    // scalar path: [tile][block]
+};
+
+template <int DT, int TT, int NW, bool VEC>
+__global__ __launch_bounds__(64 * NW) void matmul_reg_kernel(float* __restrict__ out, int ldo,
+                                                            const uint8_t* __restrict__ wq,
+                                                            const uint16_t* __restrict__ wscale,
+                                                            const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                            int cols, int n, int r0, int r1, int n_tg) {
+    const int nb = cols / QK;
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lq = lane >> 4;
+    const int G = (int)gridDim.x, p = (int)blockIdx.x;
+    const int xcd = p % kXcds, per = G / kXcds, rem = G % kXcds;
+    const int logical = xcd * per + min(xcd, rem) + p / kXcds;
+    const int rt = logical / n_tg, tg = logical % n_tg;
+    const int rbase = r0 + rt * 16;
+    const int tbase = (tg * NW + wave) * TT * 16;
+    if (tbase >= n) return;  // uniform per wave; nothing below synchronises across waves
+
+    const int arow = min(rbase + li, r1 - 1);
+    const uint8_t* wrow;
+    int shift = 0;
+    if (DT == kQ8) {
+        wrow = wq + (size_t)arow * cols + lq * 8;
+    } else {
+        wrow = wq + (size_t)arow * (cols / 2) + (lq & 1) * 8;
+        shift = (lq >> 1) * 4;
+    }
+    const int8_t* xrow[TT];
+    const float* dxrow[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+        const int t = min(tbase + tt * 16 + li, n - 1);
+        xrow[tt] = xq + (size_t)t * cols + lq * 8;
+        dxrow[tt] = xd + (size_t)t * nb;
+    }
+    const uint16_t* dwrow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dwrow[i] = wscale + (size_t)min(rbase + 4 * lq + i, r1 - 1) * nb;
+
+    auto load = [&](RegChunk<DT, TT, VEC>& R, int c0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int b = min(c0 + k, nb - 1);
+            R.a[k] = *reinterpret_cast<const long*>(wrow + (size_t)b * (DT == kQ8 ? QK : QK / 2));
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) R.x[k][tt] = *reinterpret_cast<const long*>(xrow[tt] + (size_t)b * QK);
+        }
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) R.dw[i] = *reinterpret_cast<const uint2*>(dwrow[i] + c0);
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) R.dx[tt] = *reinterpret_cast<const float4*>(dxrow[tt] + c0);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int b = min(c0 + k, nb - 1);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) R.dws[i][k] = dwrow[i][b];
+#pragma unroll
+                for (int tt = 0; tt < TT; ++tt) R.dxs[tt][k] = dxrow[tt][b];
+            }
+        }
+    };
+
+    float acc[TT][4];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[tt][i] = 0.0f;
+
+    auto reduce = [&](const RegChunk<DT, TT, VEC>& R, int c0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            long a = R.a[k];
+            if (DT == kQ4) {
+                const uint64_t v = (uint64_t)a;
+                const uint32_t lo = nibbles_to_i8(((uint32_t)v >> shift) & 0x0F0F0F0Fu);
+                const uint32_t hi = nibbles_to_i8(((uint32_t)(v >> 32) >> shift) & 0x0F0F0F0Fu);
+                a = (long)(((uint64_t)hi << 32) | lo);
+            }
+            float dw[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint16_t h;
+                if constexpr (VEC) {
+                    const uint32_t w2 = k < 2 ? R.dw[i].x : R.dw[i].y;
+                    h = (uint16_t)((k & 1) ? (w2 >> 16) : (w2 & 0xffffu));
+                } else {
+                    h = R.dws[i][k];
+                }
+                dw[i] = f16_to_f32(h);
+            }
+            const bool live = c0 + k < nb;
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) {
+                v4i c = {0, 0, 0, 0};
+                c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, R.x[k][tt], c, 0, 0, 0);
+                float dx;
+                if constexpr (VEC) {
+                    dx = k == 0 ? R.dx[tt].x : k == 1 ? R.dx[tt].y : k == 2 ? R.dx[tt].z : R.dx[tt].w;
+                } else {
+                    dx = R.dxs[tt][k];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float nx = __builtin_fmaf((float)c[i] * dw[i], dx, acc[tt][i]);
+                    acc[tt][i] = live ? nx : acc[tt][i];
+                }
+            }
+        }
+    };
+
+    const int n_chunks = (nb + 3) / 4;
+    RegChunk<DT, TT, VEC> A, B;
+    load(A, 0);
+    int c = 0;
+    while (c + 2 < n_chunks) {
+        load(B, (c + 1) * 4);
+        reduce(A, c * 4);
+        load(A, (c + 2) * 4);
+        reduce(B, (c + 1) * 4);
+        c += 2;
+    }
+    if (c + 1 < n_chunks) {
+        load(B, (c + 1) * 4);
+        reduce(A, c * 4);
+        reduce(B, (c + 1) * 4);
+    } else {
+        reduce(A, c * 4);
+    }
+
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+        const int tok = tbase + tt * 16 + li;
+        if (tok < n) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = rbase + 4 * lq + i;
+                if (r < r1) out[(size_t)tok * ldo + r] = acc[tt][i];
+            }
+        }
+    }
+}
+
+namespace {
+
+// Launch plan: kernel family, token tiles (per workgroup for the LDS kernel, per wave for the register kernel) and
+// waves per workgroup. QH_MM="lds:TT" or "reg:TT:NW" overrides the heuristic (tuning sweeps).
+struct MmPlan {
+    bool reg;
+    int tt, nw;
+};
+
+MmPlan matmul_plan(int rows, int cols, int n) {
+    MmPlan pl{true, 1, 1};
+    const char* env = getenv("QH_MM");
+    if (env) {
+        int a = 0, b = 0;
+        if (sscanf(env, "lds:%d", &a) == 1 && (a == 1 || a == 2 || a == 4)) return MmPlan{false, a, 4};
+        if (sscanf(env, "reg:%d:%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && (b == 1 || b == 2 || b == 4))
+            return MmPlan{true, a, b};
+    }
+    (void)cols;
+    // From a sweep on MI355X (cold weights) at the Qwen2.5-0.5B shapes, M = 32 / 128 / 512: with few (row tile,
+    // token tile) pairs the LDS-staged kernel wins (its 4 waves split each chunk's blocks, so more of the chip works
+    // on few tiles); with 1024 or more the register-chain kernel wins (no LDS round trip for the block sums). Few row
+    // tiles take 4 token tiles per wave, others 2, with 2 waves per workgroup once a row tile has 8 waves or more.
+    const int row_tiles = (rows + 15) / 16;
+    const int tiles = (n + 15) / 16;
+    if ((long)row_tiles * tiles < 1024) return MmPlan{false, 1, 4};
+    pl.tt = row_tiles < 128 ? 4 : 2;
+    pl.nw = (pl.tt == 2 && tiles / pl.tt >= 8) ? 2 : 1;
+    return pl;
+}
+
+template <int DT, int TT, int KC>
+void launch_mm_lds(float* out, int ldo, const uint8_t* wq, const uint16_t* ws, const int8_t* xq, const float* xd,
+                   int cols, int n, int r0, int r1, hipStream_t s) {
+    const int row_tiles = (r1 - r0 + 15) / 16;
+    const int n_tg = (n + 16 * TT - 1) / (16 * TT);
+    hipLaunchKernelGGL((matmul_lds_kernel<DT, TT, KC>), dim3((unsigned)(row_tiles * n_tg)), dim3(kMmThreads), 0, s,
+                       out, ldo, wq, ws, xq, xd, cols, n, r0, r1, n_tg);
+}
+
+template <int DT, int TT, int NW, bool VEC>
+void launch_mm_reg(float* out, int ldo, const uint8_t* wq, const uint16_t* ws, const int8_t* xq, const float* xd,
+                   int cols, int n, int r0, int r1, hipStream_t s) {
+    const int row_tiles = (r1 - r0 + 15) / 16;
+    const int waves = (n + 16 * TT - 1) / (16 * TT);
+    const int n_tg = (waves + NW - 1) / NW;
+    hipLaunchKernelGGL((matmul_reg_kernel<DT, TT, NW, VEC>), dim3((unsigned)(row_tiles * n_tg)), dim3(64 * NW), 0, s,
+                       out, ldo, wq, ws, xq, xd, cols, n, r0, r1, n_tg);
+}
+
+}  // namespace
 
 hipError_t launch_matmul(float* out, int ldo, const qh_tensor& W, const int8_t* xq, const float* xd, int n, int r0,
                          int r1, hipStream_t s) {
     const uint8_t* wq = static_cast<const uint8_t*>(W.data);
     const uint16_t* ws = reinterpret_cast<const uint16_t*>(wq + qh_quant_bytes(W.dtype, W.rows, W.cols));
-    const dim3 grid((unsigned)((r1 - r0 + 63) / 64), (unsigned)((n + 15) / 16));
-    if (W.dtype == kQ8)
-        hipLaunchKernelGGL(matmul_kernel<kQ8>, grid, dim3(256), 0, s, out, ldo, wq, ws, xq, xd, W.cols, n, r0, r1);
-    else
-        hipLaunchKernelGGL(matmul_kernel<kQ4>, grid, dim3(256), 0, s, out, ldo, wq, ws, xq, xd, W.cols, n, r0, r1);
-    return hipGetLastError();
+    const MmPlan pl = matmul_plan(r1 - r0, W.cols, n);
+    const bool vec = (W.cols / QK) % 4 == 0 && (reinterpret_cast<uintptr_t>(xd) & 15u) == 0;
+    if (!pl.reg) {
+#define QH_MM_LDS(DT, TT, KC)                                                          \
+        if (W.dtype == DT && pl.tt == TT) {                                            \
+            launch_mm_lds<DT, TT, KC>(out, ldo, wq, ws, xq, xd, W.cols, n, r0, r1, s); \
+            return hipGetLastError();                                                  \
+        }
+        QH_MM_LDS(kQ8, 1, 16) QH_MM_LDS(kQ8, 2, 16) QH_MM_LDS(kQ8, 4, 8)
+        QH_MM_LDS(kQ4, 1, 16) QH_MM_LDS(kQ4, 2, 16) QH_MM_LDS(kQ4, 4, 8)
+#undef QH_MM_LDS
+        return hipErrorInvalidValue;
+    }
+#define QH_MM_REG(DT, TT, NW)                                                                          \
+    if (W.dtype == DT && pl.tt == TT && pl.nw == NW) {                                                 \
+        if (vec)                                                                                       \
+            launch_mm_reg<DT, TT, NW, true>(out, ldo, wq, ws, xq, xd, W.cols, n, r0, r1, s);           \
+        else                                                                                           \
+            launch_mm_reg<DT, TT, NW, false>(out, ldo, wq, ws, xq, xd, W.cols, n, r0, r1, s);          \
+        return hipGetLastError();                                                                      \
+    }
+    QH_MM_REG(kQ8, 1, 1) QH_MM_REG(kQ8, 1, 2) QH_MM_REG(kQ8, 1, 4) QH_MM_REG(kQ8, 2, 1) QH_MM_REG(kQ8, 2, 2)
+    QH_MM_REG(kQ8, 2, 4) QH_MM_REG(kQ8, 4, 1) QH_MM_REG(kQ8, 4, 2) QH_MM_REG(kQ8, 4, 4)
+    QH_MM_REG(kQ4, 1, 1) QH_MM_REG(kQ4, 1, 2) QH_MM_REG(kQ4, 1, 4) QH_MM_REG(kQ4, 2, 1) QH_MM_REG(kQ4, 2, 2)
+    QH_MM_REG(kQ4, 2, 4) QH_MM_REG(kQ4, 4, 1) QH_MM_REG(kQ4, 4, 2) QH_MM_REG(kQ4, 4, 4)
+#undef QH_MM_REG
+    return hipErrorInvalidValue;
 }
 
 }  // namespace qh

@@ -127,3 +127,18 @@ def test_shortlist_full_vocab(qh, oracle, synth, gpu):
     st = sl.stats()
     assert st["top1"] == int(qh.argmax(full).item())
     assert np.float32(st["top1_logit"]).tobytes() == full[st["top1"]].cpu().numpy().tobytes()
+
+
+@pytest.mark.parametrize("tt", ["lds:1", "lds:2", "lds:4", "reg:1:1", "reg:1:4", "reg:2:2", "reg:4:1", "reg:4:4"])
+@pytest.mark.parametrize("dtype,N,K", [(2, 200, 896), (3, 200, 896), (2, 40, 4864), (3, 40, 4864)])
+def test_matmul_every_token_tiling(qh, oracle, synth, gpu, monkeypatch, tt, dtype, N, K):
+    """Both prefill kernels at every token tiling (LDS-staged block sums, register chains) on ragged shapes: rows not a
+    multiple of 16, a last K chunk shorter than the others, token counts around the tile widths."""
+    monkeypatch.setenv("QH_MM", tt)
+    buf = synth.q8_tensor(61 + N, N, K) if dtype == 2 else synth.q4_tensor(67 + N, N, K)
+    W = qh.DeviceTensor.upload(buf, dtype, N, K)
+    for M in (1, 15, 17, 40, 65):
+        xq, xd = qh.quantize_q8(_dev(synth.activations(71 + M, M, K), gpu))
+        got = qh.matmul_q(W, xq, xd).cpu().numpy()
+        want = oracle.matmul_q(dtype, N, K, buf, xq.cpu().numpy(), xd.cpu().numpy(), threads=8)
+        assert (bits(got) == bits(want)).all(), (tt, M)
