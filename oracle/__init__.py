@@ -56,8 +56,30 @@ class _Oracle:
                                         _f32p, _f32p, _f32p, _i32p, C.POINTER(_int), C.POINTER(_f), C.POINTER(_int)]
         L.qo_shortlist_head.restype = _int
 
+        L.qo_f32_to_f16.argtypes, L.qo_f32_to_f16.restype = [_f], C.c_uint16
+        L.qo_decoder_create.argtypes = [_i32p, np.ctypeslib.ndpointer(np.float32), C.c_void_p, _i32p]
+        L.qo_decoder_create.restype = C.c_void_p
+        L.qo_decoder_free.argtypes = [C.c_void_p]
+        L.qo_decoder_forward.argtypes = [C.c_void_p, _int, _int, _int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.qo_decoder_forward_batch.argtypes = [C.c_void_p, _i32p, _int, _int, _int, C.c_void_p, C.c_void_p, C.c_void_p,
+                                               C.c_void_p]
+        L.qo_rope_table.argtypes = [_f32p, _int, _int, _f]
+
     def fp16_to_f32(self, h: int) -> float:
         return self.lib.qo_fp16_to_f32(h)
+
+    def f32_to_f16(self, f: float) -> int:
+        return self.lib.qo_f32_to_f16(f)
+
+    def rope_table(self, n_pos: int, head_dim: int, theta: float) -> np.ndarray:
+        cs = np.empty((n_pos, head_dim // 2, 2), np.float32)
+        self.lib.qo_rope_table(cs, n_pos, head_dim, theta)
+        return cs
+
+    def decoder(self, hp: dict, arrays: list, dtypes: list) -> "Decoder":
+        """hp: vocab, dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, ctx_len, qkv_bias, rope_theta, norm_eps;
+        arrays / dtypes in the order of qo_decoder_create (None for absent tensors)."""
+        return Decoder(self.lib, hp, arrays, dtypes)
 
     def quantize_q8(self, x: np.ndarray):
         x = np.ascontiguousarray(x, np.float32)
@@ -109,6 +131,45 @@ class _Oracle:
                                        C.byref(tie))
         return dict(logits=logits, coarse=coarse, upper=upper, rows=rows[:n].copy(), n_rows=n,
                     n_seeds=ns.value, tau=tau.value, seed_tie=bool(tie.value))
+
+
+class Decoder:
+    """The oracle's decoder (qo_decoder_*): the reference's Model::forward / forward_batch restated in C."""
+
+    def __init__(self, lib, hp, arrays, dtypes):
+        self.lib = lib
+        self.V, self.D = hp["vocab"], hp["dim"]
+        self._keep = [None if a is None else np.ascontiguousarray(a) for a in arrays]
+        self._ptrs = (C.c_void_p * len(arrays))(*[None if a is None else a.ctypes.data for a in self._keep])
+        ints = np.array([hp[k] for k in ("vocab", "dim", "n_layers", "n_heads", "n_kv_heads", "head_dim", "ffn_dim",
+                                         "ctx_len", "qkv_bias")], np.int32)
+        floats = np.array([hp["rope_theta"], hp["norm_eps"]], np.float32)
+        self._dt = np.array(dtypes, np.int32)
+        self.h = lib.qo_decoder_create(ints, floats, C.cast(self._ptrs, C.c_void_p), self._dt)
+        if not self.h:
+            raise ValueError("qo_decoder_create rejected the model")
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.lib.qo_decoder_free(self.h)
+            self.h = None
+
+    def _outs(self):
+        return (np.empty(self.V, np.float32), np.empty(self.D, np.float32), np.empty(self.D, np.int8),
+                np.empty(self.D // QK, np.float32))
+
+    def forward(self, token, pos, top_k=1):
+        lg, h, q, d = self._outs()
+        rows = self.lib.qo_decoder_forward(self.h, token, pos, top_k, lg.ctypes.data, h.ctypes.data, q.ctypes.data,
+                                           d.ctypes.data)
+        return dict(logits=lg, hidden=h, hq=q, hd=d, rows=rows)
+
+    def forward_batch(self, tokens, pos0, top_k=1):
+        lg, h, q, d = self._outs()
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        rows = self.lib.qo_decoder_forward_batch(self.h, tokens, tokens.size, pos0, top_k, lg.ctypes.data,
+                                                 h.ctypes.data, q.ctypes.data, d.ctypes.data)
+        return dict(logits=lg, hidden=h, hq=q, hd=d, rows=rows)
 
 
 class _Ref:

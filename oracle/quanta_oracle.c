@@ -304,3 +304,234 @@ void qo_matmul_q_mt(float* out, int ldo, int dtype, int rows, int cols, const ui
     job_t j = {1, out, ldo, dtype, rows, cols, n, data, xq, xd, 0, rows};
     run_parallel(j, n_threads);
 }
+
+/* ---------------------------------------------------------------- decoder (model.cpp:10-228, 349-433) */
+
+uint16_t qo_f32_to_f16(float f) {
+    /* round to nearest even: normals drop 13 mantissa bits, binary16 subnormals are round(|f| * 2^24) */
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, a = x & 0x7fffffffu;
+    if (a >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (a > 0x7f800000u ? 0x200u | ((a >> 13) & 0x3ffu) : 0u));
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 rounds to infinity */
+    if (a < 0x38800000u) {                                   /* below 2^-14: binary16 subnormal */
+        const uint32_t e = a >> 23;
+        if (e < 102u) return (uint16_t)sign; /* below 2^-25 */
+        const uint32_t shift = 126u - e, m = (a & 0x7fffffu) | 0x800000u;
+        uint32_t q = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) ++q;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t h = (a - 0x38000000u) >> 13;
+    const uint32_t rem = a & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+}
+
+void qo_rope_table(float* cs, int n_pos, int head_dim, float theta) {
+    /* ops_ref.cpp:203-206: freq = powf(theta, -2.0f * i / head_dim), angle = pos * freq */
+    const int half = head_dim / 2;
+    for (int p = 0; p < n_pos; ++p)
+        for (int i = 0; i < half; ++i) {
+            const float freq = powf(theta, -2.0f * (float)i / (float)head_dim);
+            const float angle = (float)p * freq;
+            cs[((size_t)p * half + i) * 2] = cosf(angle);
+            cs[((size_t)p * half + i) * 2 + 1] = sinf(angle);
+        }
+}
+
+enum { L_ATTN_NORM, L_WQ, L_WK, L_WV, L_WO, L_BQ, L_BK, L_BV, L_FFN_NORM, L_WG, L_WU, L_WD, L_COUNT };
+
+struct qo_decoder {
+    int V, D, nl, nh, nkv, hdim, F, ctx, bias;
+    float theta, eps;
+    const void* const* t;
+    const int* dt;
+    uint16_t *kc, *vc; /* [layer][ctx][kv_dim] f16 bits */
+    float *x, *xb, *xb2, *q, *k, *v, *att, *hb, *hb2, *logits, *coarse, *upper, *cs;
+    int8_t *xq, *hq;
+    float *xd, *hd;
+    int* rows;
+};
+
+static const void* lt(const qo_decoder* d, int l, int which) { return d->t[2 + l * L_COUNT + which]; }
+static int ldt(const qo_decoder* d, int l, int which) { return d->dt[2 + l * L_COUNT + which]; }
+
+qo_decoder* qo_decoder_create(const int* hp, const float* hpf, const void* const* tensors, const int* dtypes) {
+    qo_decoder* d = (qo_decoder*)calloc(1, sizeof(qo_decoder));
+    d->V = hp[0]; d->D = hp[1]; d->nl = hp[2]; d->nh = hp[3]; d->nkv = hp[4]; d->hdim = hp[5]; d->F = hp[6];
+    d->ctx = hp[7]; d->bias = hp[8];
+    d->theta = hpf[0]; d->eps = hpf[1];
+    if (d->nh * d->hdim != d->D || d->nh % d->nkv != 0 || d->D % QO_QK || d->F % QO_QK) { free(d); return NULL; }
+    d->t = tensors;
+    d->dt = dtypes;
+    const size_t kvd = (size_t)d->nkv * d->hdim;
+    d->kc = (uint16_t*)calloc((size_t)d->nl * d->ctx * kvd, 2);
+    d->vc = (uint16_t*)calloc((size_t)d->nl * d->ctx * kvd, 2);
+    d->x = (float*)calloc(d->D, 4); d->xb = (float*)calloc(d->D, 4); d->xb2 = (float*)calloc(d->D, 4);
+    d->q = (float*)calloc(d->D, 4); d->k = (float*)calloc(kvd, 4); d->v = (float*)calloc(kvd, 4);
+    d->att = (float*)calloc((size_t)d->ctx, 4);
+    d->hb = (float*)calloc(d->F, 4); d->hb2 = (float*)calloc(d->F, 4);
+    d->logits = (float*)calloc(d->V, 4); d->coarse = (float*)calloc(d->V, 4); d->upper = (float*)calloc(d->V, 4);
+    d->rows = (int*)calloc(d->V, 4);
+    d->xq = (int8_t*)calloc(d->D > d->F ? d->D : d->F, 1); d->hq = (int8_t*)calloc(d->F, 1);
+    d->xd = (float*)calloc(d->D / QO_QK, 4); d->hd = (float*)calloc(d->F / QO_QK, 4);
+    d->cs = (float*)malloc(sizeof(float) * (size_t)d->ctx * d->hdim);
+    qo_rope_table(d->cs, d->ctx, d->hdim, d->theta);
+    return d;
+}
+
+void qo_decoder_free(qo_decoder* d) {
+    if (!d) return;
+    free(d->kc); free(d->vc); free(d->x); free(d->xb); free(d->xb2); free(d->q); free(d->k); free(d->v);
+    free(d->att); free(d->hb); free(d->hb2); free(d->logits); free(d->coarse); free(d->upper); free(d->rows);
+    free(d->xq); free(d->hq); free(d->xd); free(d->hd); free(d->cs); free(d);
+}
+
+/* ops_ref.cpp:194-199 */
+static void rmsnorm(float* out, const float* x, const float* w, int n, float eps) {
+    float ss = 0.f;
+    for (int i = 0; i < n; ++i) ss = fmaf(x[i], x[i], ss);
+    const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = 0; i < n; ++i) out[i] = x[i] * scale * w[i];
+}
+
+/* ops_ref.cpp:201-214 with the angle table: a*c - b*s and b*c + a*s, each contracted into one multiply-add */
+static void rope(float* v, int n_heads, int hd, const float* cs) {
+    const int half = hd / 2;
+    for (int i = 0; i < half; ++i) {
+        const float c = cs[2 * i], s = cs[2 * i + 1];
+        for (int h = 0; h < n_heads; ++h) {
+            float* p = v + h * hd;
+            const float a = p[i], b = p[i + half];
+            p[i] = fmaf(a, c, -(b * s));
+            p[i + half] = fmaf(b, c, a * s);
+        }
+    }
+}
+
+/* ops_ref.cpp:216-226 */
+static void softmax(float* x, int n) {
+    float mx = x[0];
+    for (int i = 1; i < n; ++i) mx = x[i] > mx ? x[i] : mx;
+    float sum = 0.f;
+    for (int i = 0; i < n; ++i) {
+        x[i] = expf(x[i] - mx);
+        sum += x[i];
+    }
+    const float inv = 1.0f / sum;
+    for (int i = 0; i < n; ++i) x[i] *= inv;
+}
+
+static void linear(const qo_decoder* d, float* out, int l, int which, int rows, int cols, const int8_t* xq,
+                   const float* xd) {
+    qo_matvec_q(out, ldt(d, l, which), rows, cols, (const uint8_t*)lt(d, l, which), xq, xd, 0, rows);
+}
+
+/* One token through every layer (model.cpp:174-222); leaves the residual stream in d->x. */
+static void layers(qo_decoder* d, int token, int pos) {
+    const int D = d->D, hd = d->hdim, kvd = d->nkv * hd, group = d->nh / d->nkv, F = d->F;
+    const float scale = 1.0f / sqrtf((float)hd);
+    /* get_row on the Q8_0 embedding (ops_ref.cpp:176-181) */
+    const int8_t* eq = (const int8_t*)d->t[0] + (size_t)token * D;
+    const uint16_t* es = (const uint16_t*)((const uint8_t*)d->t[0] + (size_t)d->V * D) + (size_t)token * (D / QO_QK);
+    for (int i = 0; i < D; ++i) d->x[i] = (float)eq[i] * qo_fp16_to_f32(es[i / QO_QK]);
+    const float* cs = d->cs + (size_t)pos * hd;
+    for (int l = 0; l < d->nl; ++l) {
+        rmsnorm(d->xb, d->x, (const float*)lt(d, l, L_ATTN_NORM), D, d->eps);
+        qo_quantize_q8(d->xb, D, d->xq, d->xd);
+        linear(d, d->q, l, L_WQ, D, D, d->xq, d->xd);
+        linear(d, d->k, l, L_WK, kvd, D, d->xq, d->xd);
+        linear(d, d->v, l, L_WV, kvd, D, d->xq, d->xd);
+        if (d->bias) {
+            const float *bq = (const float*)lt(d, l, L_BQ), *bk = (const float*)lt(d, l, L_BK),
+                        *bv = (const float*)lt(d, l, L_BV);
+            for (int i = 0; i < D; ++i) d->q[i] += bq[i];
+            for (int i = 0; i < kvd; ++i) d->k[i] += bk[i];
+            for (int i = 0; i < kvd; ++i) d->v[i] += bv[i];
+        }
+        rope(d->q, d->nh, hd, cs);
+        rope(d->k, d->nkv, hd, cs);
+        uint16_t* kc = d->kc + (size_t)l * d->ctx * kvd;
+        uint16_t* vc = d->vc + (size_t)l * d->ctx * kvd;
+        for (int i = 0; i < kvd; ++i) {
+            kc[(size_t)pos * kvd + i] = qo_f32_to_f16(d->k[i]);
+            vc[(size_t)pos * kvd + i] = qo_f32_to_f16(d->v[i]);
+        }
+        /* attend (model.cpp:115-137), head by head */
+        for (int h = 0; h < d->nh; ++h) {
+            const float* qh = d->q + h * hd;
+            const int kvh = h / group;
+            for (int t = 0; t <= pos; ++t) {
+                const uint16_t* kt = kc + (size_t)t * kvd + kvh * hd;
+                float s = 0.f;
+                for (int i = 0; i < hd; ++i) s = fmaf(qh[i], qo_fp16_to_f32(kt[i]), s);
+                d->att[t] = s * scale;
+            }
+            softmax(d->att, pos + 1);
+            float* out = d->xb + h * hd;
+            for (int i = 0; i < hd; ++i) out[i] = 0.f;
+            for (int t = 0; t <= pos; ++t) {
+                const uint16_t* vt = vc + (size_t)t * kvd + kvh * hd;
+                const float a = d->att[t];
+                for (int i = 0; i < hd; ++i) out[i] = fmaf(a, qo_fp16_to_f32(vt[i]), out[i]);
+            }
+        }
+        qo_quantize_q8(d->xb, D, d->xq, d->xd);
+        linear(d, d->xb2, l, L_WO, D, D, d->xq, d->xd);
+        for (int i = 0; i < D; ++i) d->x[i] += d->xb2[i];
+        rmsnorm(d->xb, d->x, (const float*)lt(d, l, L_FFN_NORM), D, d->eps);
+        qo_quantize_q8(d->xb, D, d->xq, d->xd);
+        linear(d, d->hb, l, L_WG, F, D, d->xq, d->xd);
+        linear(d, d->hb2, l, L_WU, F, D, d->xq, d->xd);
+        for (int i = 0; i < F; ++i) { /* swiglu, ops_ref.cpp:243-248 */
+            const float g = d->hb[i];
+            d->hb[i] = g / (1.0f + expf(-g)) * d->hb2[i];
+        }
+        qo_quantize_q8(d->hb, F, d->hq, d->hd);
+        linear(d, d->xb2, l, L_WD, D, F, d->hq, d->hd);
+        for (int i = 0; i < D; ++i) d->x[i] += d->xb2[i];
+    }
+}
+
+/* final norm, quantization and head (model.cpp:225-238) */
+static int head(qo_decoder* d, int top_k, float* logits, float* hidden, int8_t* hq, float* hd) {
+    const int D = d->D, V = d->V;
+    rmsnorm(d->x, d->x, (const float*)d->t[1], D, d->eps);
+    qo_quantize_q8(d->x, D, d->xq, d->xd);
+    int rows;
+    const void* h4 = d->t[2 + d->nl * L_COUNT];
+    const void* he = d->t[3 + d->nl * L_COUNT];
+    if (top_k > 0 && h4 && he) {
+        int ns, tie;
+        float tau;
+        rows = qo_shortlist_head((const uint8_t*)d->t[0], (const uint8_t*)h4, (const uint16_t*)he, V, D, d->xq, d->xd,
+                                 top_k, V, NULL, 0, d->logits, d->coarse, d->upper, d->rows, &ns, &tau, &tie);
+    } else {
+        qo_matvec_q(d->logits, QO_Q8_0, V, D, (const uint8_t*)d->t[0], d->xq, d->xd, 0, V);
+        rows = V;
+    }
+    if (logits) memcpy(logits, d->logits, sizeof(float) * (size_t)V);
+    if (hidden) memcpy(hidden, d->x, sizeof(float) * (size_t)D);
+    if (hq) memcpy(hq, d->xq, (size_t)D);
+    if (hd) memcpy(hd, d->xd, sizeof(float) * (size_t)(D / QO_QK));
+    return rows;
+}
+
+int qo_decoder_forward(qo_decoder* d, int token, int pos, int top_k, float* logits, float* hidden, int8_t* hq,
+                       float* hd) {
+    if (pos < 0 || pos >= d->ctx || token < 0 || token >= d->V) return -1;
+    layers(d, token, pos);
+    return head(d, top_k, logits, hidden, hq, hd);
+}
+
+int qo_decoder_forward_batch(qo_decoder* d, const int* tokens, int n, int pos0, int top_k, float* logits,
+                             float* hidden, int8_t* hq, float* hd) {
+    if (n <= 0 || pos0 < 0 || pos0 + n > d->ctx) return -1;
+    for (int t = 0; t < n; ++t) {
+        if (tokens[t] < 0 || tokens[t] >= d->V) return -1;
+        layers(d, tokens[t], pos0 + t);
+    }
+    return head(d, top_k, logits, hidden, hq, hd);
+}

@@ -74,6 +74,39 @@ void qo_matvec_q_mt(float* out, int dtype, int rows, int cols, const uint8_t* da
 void qo_matmul_q_mt(float* out, int ldo, int dtype, int rows, int cols, const uint8_t* data,
                     const int8_t* xq, const float* xd, int n, int n_threads);
 
+/* ------------------------------------------------------------------ decoder (model.cpp:10-228, 349-433) */
+
+/* IEEE binary32 -> binary16, round to nearest even (the _Float16 conversion of the reference's KV store,
+ * model.cpp:140-143), as bits. */
+uint16_t qo_f32_to_f16(float f);
+
+/* glibc-identical expf is the host's own: the oracle calls expf() from libm, as the reference does. */
+
+typedef struct qo_decoder qo_decoder;
+
+/* hp: vocab, dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, ctx_len, qkv_bias (9 ints);
+ * hpf: rope_theta, norm_eps. tensors / dtypes: embed (Q8_0 [V][D], tied head), final norm (F32 [D]); per layer
+ * attn_norm, wq, wk, wv, wo, bq, bk, bv, ffn_norm, w_gate, w_up, w_down (12 each; biases NULL without qkv_bias,
+ * weights Q8_0 or Q4_0); then the shortlist copy head_q4 (Q4_0 [V][D]) and head_err (F16 [V][D/32]), or NULL.
+ * The KV cache is f16, as the reference's default. Returns NULL on a bad argument. */
+qo_decoder* qo_decoder_create(const int* hp, const float* hpf, const void* const* tensors, const int* dtypes);
+void qo_decoder_free(qo_decoder* d);
+
+/* Model::forward (model.cpp:165-228): one token at position pos; top_k > 0 runs the shortlist head with
+ * n_valid = vocab, else the full head. logits [V], hidden [D] (the final normed state), hq / hd its quantization
+ * (each may be NULL). Returns the 8-bit head rows read. */
+int qo_decoder_forward(qo_decoder* d, int token, int pos, int top_k, float* logits, float* hidden, int8_t* hq,
+                       float* hd);
+
+/* Model::forward_batch (model.cpp:349-361) for n tokens from pos0: every token's layers (token t attends over
+ * positions <= pos0 + t, which is what the 32-token chunks compute), then the head for the last token. */
+int qo_decoder_forward_batch(qo_decoder* d, const int* tokens, int n, int pos0, int top_k, float* logits,
+                             float* hidden, int8_t* hq, float* hd);
+
+/* RoPE table of the reference (ops_ref.cpp:201-214) for positions [0, n_pos): cs[pos][i] = (cosf, sinf) of
+ * pos * powf(theta, -2 i / head_dim), i < head_dim / 2, as [n_pos][head_dim / 2][2] floats. */
+void qo_rope_table(float* cs, int n_pos, int head_dim, float theta);
+
 #ifdef __cplusplus
 }
 #endif

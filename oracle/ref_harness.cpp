@@ -1,7 +1,8 @@
 // C entry points around the reference engine's own kernels, for parity checks only.
 //
 // TEST INFRASTRUCTURE ONLY. oracle/Makefile compiles this file together with the reference sources
-// (engine/src/ops_ref.cpp, ops_dispatch.cpp, model_file.cpp, model.cpp, threadpool.cpp) into
+// (engine/src/ops_ref.cpp, ops_dispatch.cpp, model_file.cpp, model.cpp, threadpool.cpp, tokenizer.cpp, sampler.cpp,
+// session.cpp) into
 // oracle/_ref/libquanta_ref.so. Nothing of the reference is copied here: the functions below build
 // the reference's own Tensor / QuantVec / Model objects over caller buffers and call into it.
 //
@@ -29,6 +30,9 @@
 #define private public
 #include "model.h"
 #undef private
+#include "sampler.h"
+#include "session.h"
+#include "tokenizer.h"
 
 using quanta::DType;
 using quanta::QuantVec;
@@ -135,6 +139,88 @@ int ref_shortlist_head(const uint8_t* head8, const uint8_t* head4, const uint16_
     // The Model never owned these tensors; detach before it is destroyed.
     m->lm_head_ = m->head_q4_ = m->head_err_ = nullptr;
     return m->last_head_rows_;
+}
+
+// ---- whole-model entry points (model.cpp:10-228, 349-433; session.cpp:13-52; tools/cli/main.cpp:216-251)
+
+// Loads a .qnt through Model::load with an f16 KV cache (the CLI default). Returns an opaque handle or null.
+void* ref_model_load(const char* path, int ctx_len, int n_threads) {
+    auto m = std::make_unique<quanta::Model>();
+    std::string err;
+    if (!m->load(path, ctx_len, &err, n_threads, true)) return nullptr;
+    return m.release();
+}
+
+void ref_model_free(void* m) { delete static_cast<quanta::Model*>(m); }
+
+// Copies the state a forward leaves behind: logits [V] (exact where the head computed them, -inf elsewhere with the
+// shortlist), the final normed hidden state [dim] and its quantization; returns last_head_rows().
+static int ref_dump(quanta::Model* m, float* logits, float* hidden, int8_t* hq, float* hd) {
+    const auto& hp = m->hparams();
+    if (logits) std::memcpy(logits, m->logits_.data(), sizeof(float) * size_t(hp.vocab_size));
+    if (hidden) std::memcpy(hidden, m->x_.data(), sizeof(float) * size_t(hp.dim));
+    if (hq) std::memcpy(hq, m->xq_.q.data(), size_t(hp.dim));
+    if (hd) std::memcpy(hd, m->xq_.d.data(), sizeof(float) * size_t(hp.dim / quanta::QK));
+    return m->last_head_rows_;
+}
+
+// Model::forward for one token. top_k > 0 uses the shortlist head with n_valid = vocab, else the full head.
+int ref_model_forward(void* mp, int token, int pos, int top_k, float* logits, float* hidden, int8_t* hq, float* hd) {
+    auto* m = static_cast<quanta::Model*>(mp);
+    quanta::HeadQuery q;
+    q.top_k = top_k;
+    q.n_valid = m->hparams().vocab_size;
+    m->forward(token, pos, top_k > 0 ? &q : nullptr);
+    return ref_dump(m, logits, hidden, hq, hd);
+}
+
+// Model::forward_batch (32-token chunks) for n tokens from pos0.
+int ref_model_forward_batch(void* mp, const int* tokens, int n, int pos0, int top_k, float* logits, float* hidden,
+                            int8_t* hq, float* hd) {
+    auto* m = static_cast<quanta::Model*>(mp);
+    quanta::HeadQuery q;
+    q.top_k = top_k;
+    q.n_valid = m->hparams().vocab_size;
+    m->forward_batch(tokens, n, pos0, top_k > 0 ? &q : nullptr);
+    return ref_dump(m, logits, hidden, hq, hd);
+}
+
+// Copies the f16 KV cache of layer l, positions [0, n_pos): k and v as [n_pos][kv_dim] fp16 bits.
+void ref_model_kv(void* mp, int l, int n_pos, uint16_t* k, uint16_t* v) {
+    auto* m = static_cast<quanta::Model*>(mp);
+    const auto& hp = m->hparams();
+    const size_t kv_dim = size_t(hp.n_kv_heads) * hp.head_dim;
+    const size_t off = size_t(l) * m->ctx_len_ * kv_dim;
+    std::memcpy(k, m->k_cache16_.data() + off, 2 * kv_dim * n_pos);
+    std::memcpy(v, m->v_cache16_.data() + off, 2 * kv_dim * n_pos);
+}
+
+// `quanta gen --greedy --ids ... -n n_gen` (tools/cli/main.cpp:216-251): batched prefill of the prompt through a
+// Session with the greedy sampler parameters (so the shortlist head answers top_k = 1 queries), then n_gen greedy
+// tokens. Writes the generated ids, and per step (when non-null) the 8-bit head rows the forward before it read and the
+// logit of the chosen id (its exact value, the maximum); returns the count (or -1 if the prompt does not fit).
+int ref_gen(void* mp, const int* ids, int n_ids, int n_gen, int* out, int* head_rows, float* top_logit) {
+    auto* m = static_cast<quanta::Model*>(mp);
+    quanta::Tokenizer tok(m->file().tokenizer());
+    quanta::Session s(*m, tok);
+    s.set_batch_prefill(true);
+    quanta::SamplerParams sp;
+    sp.temperature = 0.f;
+    sp.repeat_penalty = 1.f;
+    s.set_sampler(&sp);
+    quanta::SamplerParams greedy;
+    greedy.temperature = 0.f;
+    greedy.repeat_penalty = 1.f;
+    quanta::Sampler sampler(greedy);
+    if (!s.feed(std::vector<int>(ids, ids + n_ids), nullptr)) return -1;
+    int n = 0;
+    s.generate(sampler, n_gen, {}, [&](int id) {
+        if (head_rows) head_rows[n] = m->last_head_rows_;
+        if (top_logit) top_logit[n] = m->logits_[size_t(id)];
+        out[n++] = id;
+        return true;
+    }, nullptr);
+    return n;
 }
 
 }  // extern "C"

@@ -1,0 +1,186 @@
+"""The .qnt model file: writer, reader, and the synthetic q4mix Qwen2.5-0.5B-shaped model.
+
+Layout (reference engine/src/model_file.cpp:104-218, scripts/export.py:3-13, 291-314), little-endian:
+  'QNT1', u32 version (2), hparams: u32 vocab, dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, max_seq,
+  f32 rope_theta, f32 norm_eps, u32 tied_embeddings, u32 qkv_bias, u32 flags;
+  tokenizer section (u32 length, then: u32 n_tokens + length-prefixed byte strings, u32 n_merges + 3 x u32 each,
+  u32 n_specials + (u32 id, string) each, three u32-counted lists of (u32, u32) code-point ranges);
+  tensor table: u32 count, then per tensor: string name, u32 dtype, u32 ndim, u32 dims, u64 absolute offset;
+  tensor data, each tensor 64-byte aligned. Quantized tensors hold their quants, then fp16 scales per 32 weights.
+
+The synthetic model follows the benchmark's end-to-end configuration: attention projections Q8_0 and MLP projections
+4-bit (Q4_0 with one scale per 128 columns written into its four 32-block slots), a tied Q8_0 embedding that is also
+the LM head, its shortlist copy (quanta.head_q4, quanta.head_err), norm weights 1.0 and small random q/k/v biases.
+Every tensor comes from its own seeded generator (numpy PCG64), so the file is the same on every machine.
+"""
+from __future__ import annotations
+
+import struct
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import synth
+
+MAGIC = b"QNT1"
+VERSION = 2
+ALIGN = 64
+F32, F16, Q8_0, Q4_0 = 0, 1, 2, 3
+
+
+@dataclass
+class HParams:
+    vocab_size: int = 151936
+    dim: int = 896
+    n_layers: int = 24
+    n_heads: int = 14
+    n_kv_heads: int = 2
+    head_dim: int = 64
+    ffn_dim: int = 4864
+    max_seq: int = 4096
+    rope_theta: float = 1e6
+    norm_eps: float = 1e-6
+    tied_embeddings: bool = True
+    qkv_bias: bool = True
+    flags: int = 0
+
+    def pack(self) -> bytes:
+        return struct.pack("<8I2f3I", self.vocab_size, self.dim, self.n_layers, self.n_heads, self.n_kv_heads,
+                           self.head_dim, self.ffn_dim, self.max_seq, self.rope_theta, self.norm_eps,
+                           int(self.tied_embeddings), int(self.qkv_bias), self.flags)
+
+
+@dataclass
+class TensorRec:
+    dtype: int
+    rows: int
+    cols: int
+    data: np.ndarray  # uint8 bytes as stored in the file
+    ndim: int = 2
+
+
+def _blob(b: bytes) -> bytes:
+    return struct.pack("<I", len(b)) + b
+
+
+def tokenizer_section(n_tokens: int) -> bytes:
+    """A byte-level vocabulary: ids 0-255 are the single bytes (the reference tokenizer needs all of them,
+    engine/src/tokenizer.cpp:57-61), the others distinct multi-byte strings; no merges, specials or ranges."""
+    out = [struct.pack("<I", n_tokens)]
+    out += [_blob(bytes([i])) for i in range(min(256, n_tokens))]
+    out += [_blob(b"<%d>" % i) for i in range(256, n_tokens)]
+    out.append(struct.pack("<I", 0))  # merges
+    out.append(struct.pack("<I", 0))  # specials
+    out += [struct.pack("<I", 0)] * 3  # letters, numbers, spaces
+    return b"".join(out)
+
+
+def write_qnt(path: str, hp: HParams, tensors: dict[str, TensorRec], n_tokens: int | None = None) -> None:
+    names = sorted(tensors)
+    tok = tokenizer_section(hp.vocab_size if n_tokens is None else n_tokens)
+    head = MAGIC + struct.pack("<I", VERSION) + hp.pack() + _blob(tok)
+
+    def table(offsets):
+        t = [struct.pack("<I", len(names))]
+        for n in names:
+            r = tensors[n]
+            dims = (r.cols,) if r.ndim == 1 else (r.rows, r.cols)
+            t.append(_blob(n.encode()) + struct.pack("<II", r.dtype, len(dims)) +
+                     b"".join(struct.pack("<I", d) for d in dims) + struct.pack("<Q", offsets.get(n, 0)))
+        return b"".join(t)
+
+    pos = len(head) + len(table({}))
+    offsets = {}
+    for n in names:
+        pos = (pos + ALIGN - 1) // ALIGN * ALIGN
+        offsets[n] = pos
+        pos += tensors[n].data.size
+    with open(path, "wb") as f:
+        f.write(head)
+        f.write(table(offsets))
+        for n in names:
+            f.write(b"\0" * (offsets[n] - f.tell()))
+            f.write(np.ascontiguousarray(tensors[n].data).tobytes())
+
+
+def read_qnt(path: str):
+    """(HParams, n_tokens, {name: TensorRec}) with tensor data as read-only views into a memory map."""
+    mm = np.memmap(path, dtype=np.uint8, mode="r")
+    buf = memoryview(mm)
+    p = 0
+
+    def take(n):
+        nonlocal p
+        if p + n > len(buf):
+            raise ValueError("model file truncated")
+        b = buf[p:p + n]
+        p += n
+        return b
+
+    if bytes(take(4)) != MAGIC:
+        raise ValueError("bad magic (not a .qnt file)")
+    version = struct.unpack("<I", take(4))[0]
+    if version not in (1, 2):
+        raise ValueError(f"unsupported version {version}")
+    v = struct.unpack("<8I2f2I", take(48))
+    flags = struct.unpack("<I", take(4))[0] if version >= 2 else 0
+    hp = HParams(*v[:8], float(v[8]), float(v[9]), bool(v[10]), bool(v[11]), flags)
+    tok_len = struct.unpack("<I", take(4))[0]
+    tok = take(tok_len)
+    n_tokens = struct.unpack("<I", tok[:4])[0]
+    n_tensors = struct.unpack("<I", take(4))[0]
+    tensors = {}
+    for _ in range(n_tensors):
+        nl = struct.unpack("<I", take(4))[0]
+        name = bytes(take(nl)).decode()
+        dtype, ndim = struct.unpack("<II", take(8))
+        if ndim == 1:
+            rows, cols = 1, struct.unpack("<I", take(4))[0]
+        elif ndim == 2:
+            rows, cols = struct.unpack("<II", take(8))
+        else:
+            raise ValueError(f"unsupported ndim for {name}")
+        off = struct.unpack("<Q", take(8))[0]
+        size = synth.tensor_bytes(dtype, rows, cols)
+        if off + size > len(mm):
+            raise ValueError(f"tensor out of bounds: {name}")
+        tensors[name] = TensorRec(dtype, rows, cols, mm[off:off + size], ndim)
+    return hp, n_tokens, tensors
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, np.float32).view(np.uint8).reshape(-1)
+
+
+def synthetic_q4mix(seed: int, hp: HParams | None = None, shortlist: bool = True) -> dict[str, TensorRec]:
+    """The random-init q4mix model (tensor name -> record). Sub-seeds: seed * 1000 + a fixed index per tensor."""
+    hp = hp or HParams()
+    D, F, V = hp.dim, hp.ffn_dim, hp.vocab_size
+    qd, kvd = hp.n_heads * hp.head_dim, hp.n_kv_heads * hp.head_dim
+    s = lambda i: seed * 1000 + i  # noqa: E731
+    t: dict[str, TensorRec] = {}
+    embed = synth.q8_tensor(s(0), V, D)
+    t["model.embed_tokens.weight"] = TensorRec(Q8_0, V, D, embed)
+    t["model.norm.weight"] = TensorRec(F32, 1, D, _f32(np.ones(D)), ndim=1)
+    for l in range(hp.n_layers):
+        p = f"model.layers.{l}."
+        b = 10 + 20 * l
+        t[p + "input_layernorm.weight"] = TensorRec(F32, 1, D, _f32(np.ones(D)), ndim=1)
+        t[p + "post_attention_layernorm.weight"] = TensorRec(F32, 1, D, _f32(np.ones(D)), ndim=1)
+        t[p + "self_attn.q_proj.weight"] = TensorRec(Q8_0, qd, D, synth.q8_tensor(s(b + 0), qd, D))
+        t[p + "self_attn.k_proj.weight"] = TensorRec(Q8_0, kvd, D, synth.q8_tensor(s(b + 1), kvd, D))
+        t[p + "self_attn.v_proj.weight"] = TensorRec(Q8_0, kvd, D, synth.q8_tensor(s(b + 2), kvd, D))
+        t[p + "self_attn.o_proj.weight"] = TensorRec(Q8_0, D, qd, synth.q8_tensor(s(b + 3), D, qd))
+        if hp.qkv_bias:
+            g = np.random.default_rng(s(b + 4))
+            t[p + "self_attn.q_proj.bias"] = TensorRec(F32, 1, qd, _f32(g.standard_normal(qd) * 0.02), ndim=1)
+            t[p + "self_attn.k_proj.bias"] = TensorRec(F32, 1, kvd, _f32(g.standard_normal(kvd) * 0.02), ndim=1)
+            t[p + "self_attn.v_proj.bias"] = TensorRec(F32, 1, kvd, _f32(g.standard_normal(kvd) * 0.02), ndim=1)
+        t[p + "mlp.gate_proj.weight"] = TensorRec(Q4_0, F, D, synth.q4_tensor(s(b + 5), F, D))
+        t[p + "mlp.up_proj.weight"] = TensorRec(Q4_0, F, D, synth.q4_tensor(s(b + 6), F, D))
+        t[p + "mlp.down_proj.weight"] = TensorRec(Q4_0, D, F, synth.q4_tensor(s(b + 7), D, F))
+    if shortlist:
+        head4, err = synth.shortlist_copy(embed, V, D)
+        t["quanta.head_q4"] = TensorRec(Q4_0, V, D, head4)
+        t["quanta.head_err"] = TensorRec(F16, V, D // 32, err.view(np.uint8).reshape(-1))
+    return t

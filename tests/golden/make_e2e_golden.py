@@ -1,0 +1,135 @@
+#!/usr/bin/env python3
+"""Writes the end-to-end golden vectors under tests/golden/ from the reference engine itself.
+
+The synthetic q4mix models are written by quanta.cpp_amd/qnt.py (seeded, the same on every machine) and loaded by the
+reference's own Model::load; the token streams come from the reference's `gen --greedy` flow (Session::feed with the
+batched 32-token prefill, then Session::generate with the greedy sampler, so the Exact Shortlist Head answers top-1
+queries), run through oracle/_ref/libquanta_ref.so (built from the reference sources by oracle/Makefile). Needs that
+build, so it runs only where the reference tree is mounted; the .npz files are data.
+
+  e2e_q4mix.npz   the benchmark model (24 layers, vocab 151936, Qwen2.5-0.5B shapes), seed 5: a 512-id prompt
+                  uniform over the vocabulary (seed 9), the 256 generated ids, per step the 8-bit head rows the
+                  forward read and the exact logit of the chosen id, and digests of a few tensors so a GPU host can
+                  show it rebuilt the same file. (A random-init model with a tied embedding soon repeats one token;
+                  the per-step head rows and logit bits still depend on every operation of every forward.)
+  e2e_small.npz   a 2-layer, vocab-4096 model of the same widths (seed 7): 40-id prompt, 24 generated ids, and after
+                  the prefill and every decode step the final normed hidden state and its int8 quantization.
+
+Usage: python tests/golden/make_e2e_golden.py [--small-only]
+"""
+import ctypes as C
+import hashlib
+import importlib.util
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+import oracle  # noqa: E402
+
+
+def load_pkg():
+    pkg = os.path.join(ROOT, "quanta.cpp_amd")
+    spec = importlib.util.spec_from_file_location("quanta_cpp_amd", os.path.join(pkg, "__init__.py"),
+                                                  submodule_search_locations=[pkg])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["quanta_cpp_amd"] = mod
+    spec.loader.exec_module(mod)
+    import quanta_cpp_amd.qnt as qnt
+    return qnt
+
+
+def bind(L):
+    L.ref_model_load.restype = C.c_void_p
+    L.ref_model_load.argtypes = [C.c_char_p, C.c_int, C.c_int]
+    L.ref_model_free.argtypes = [C.c_void_p]
+    L.ref_gen.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    L.ref_model_forward.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+                                    C.c_void_p]
+    L.ref_model_forward_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                          C.c_void_p, C.c_void_p]
+    return L
+
+
+def digest(a) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).view(np.uint8).tobytes()).hexdigest()
+
+
+def make_small(qnt, L):
+    hp = qnt.HParams(vocab_size=4096, n_layers=2)
+    path = "/tmp/quanta_e2e_small.qnt"
+    qnt.write_qnt(path, hp, qnt.synthetic_q4mix(7, hp))
+    m = L.ref_model_load(path.encode(), 4096, 8)
+    assert m, "reference failed to load the small model"
+    ids = np.random.default_rng(11).integers(0, hp.vocab_size, 40).astype(np.int32)
+    n_gen = 24
+    D = hp.dim
+    hidden = np.zeros((n_gen + 1, D), np.float32)
+    hq = np.zeros((n_gen + 1, D), np.int8)
+    hd = np.zeros((n_gen + 1, D // 32), np.float32)
+    logits = np.zeros(hp.vocab_size, np.float32)
+    out = np.zeros(n_gen, np.int32)
+    rows = np.zeros(n_gen + 1, np.int32)
+    # the gen flow by hand (Session::feed then greedy Session::generate), recording the state after every forward
+    rows[0] = L.ref_model_forward_batch(m, ids.ctypes.data, len(ids), 0, 1, logits.ctypes.data, hidden[0].ctypes.data,
+                                        hq[0].ctypes.data, hd[0].ctypes.data)
+    pos = len(ids)
+    for s in range(n_gen):
+        tok = int(np.argmax(logits))  # first maximum over the whole vocabulary (-inf outside the shortlist)
+        out[s] = tok
+        rows[s + 1] = L.ref_model_forward(m, tok, pos, 1, logits.ctypes.data, hidden[s + 1].ctypes.data,
+                                          hq[s + 1].ctypes.data, hd[s + 1].ctypes.data)
+        pos += 1
+    L.ref_model_free(m)
+    # the same stream through the reference's Session, as `quanta gen` runs it
+    m = L.ref_model_load(path.encode(), 4096, 8)
+    out2 = np.zeros(n_gen, np.int32)
+    assert L.ref_gen(m, ids.ctypes.data, len(ids), n_gen, out2.ctypes.data, None, None) == n_gen
+    L.ref_model_free(m)
+    assert (out == out2).all(), "hand-run gen flow differs from Session::generate"
+    np.savez_compressed(os.path.join(HERE, "e2e_small.npz"), seed=np.int32(7), vocab=np.int32(hp.vocab_size),
+                        n_layers=np.int32(hp.n_layers), prompt=ids, out=out, head_rows=rows, hidden=hidden, hq=hq, hd=hd)
+    os.remove(path)
+
+
+def make_full(qnt, L):
+    hp = qnt.HParams()
+    path = "/tmp/quanta_e2e_q4mix.qnt"
+    tens = qnt.synthetic_q4mix(5, hp)
+    qnt.write_qnt(path, hp, tens)
+    m = L.ref_model_load(path.encode(), 4096, 8)
+    assert m, "reference failed to load the q4mix model"
+    ids = np.random.default_rng(9).integers(0, hp.vocab_size, 512).astype(np.int32)
+    out = np.zeros(256, np.int32)
+    rows = np.zeros(256, np.int32)
+    top = np.zeros(256, np.float32)
+    n = L.ref_gen(m, ids.ctypes.data, len(ids), 256, out.ctypes.data, rows.ctypes.data, top.ctypes.data)
+    assert n == 256
+    L.ref_model_free(m)
+    names = ["model.embed_tokens.weight", "quanta.head_q4", "quanta.head_err", "model.layers.23.mlp.down_proj.weight",
+             "model.layers.0.self_attn.q_proj.bias"]
+    np.savez_compressed(os.path.join(HERE, "e2e_q4mix.npz"), seed=np.int32(5), prompt=ids, out=out, head_rows=rows,
+                        top_logit=top,
+                        digest_names=np.array(names), digests=np.array([digest(tens[k].data) for k in names]))
+    os.remove(path)
+
+
+def main():
+    if oracle.ref is None:
+        raise SystemExit("oracle/_ref/libquanta_ref.so is missing: run `make -C oracle ref`")
+    qnt = load_pkg()
+    L = bind(oracle.ref.lib)
+    make_small(qnt, L)
+    if "--small-only" not in sys.argv:
+        make_full(qnt, L)
+    for f in sorted(os.listdir(HERE)):
+        if f.startswith("e2e") and f.endswith(".npz"):
+            print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")
+
+
+if __name__ == "__main__":
+    main()
