@@ -210,6 +210,105 @@ def head_bench(qh, synth, torch, oracle, steps, warmup):
             "shortlist_GBps": sl_bytes / sl_us / 1e3, "full_head_GBps": full_bytes / full_us / 1e3}
 
 
+def e2e_bench(qh, torch, steps=256, n_prompt=512, check=True):
+    """End-to-end greedy generation on the q4mix Qwen2.5-0.5B-shaped model: prefill of a 512-token prompt in 32-token
+    chunks, then `steps` decode steps, each one HIP-graph replay of a captured step (the token is fed back on the
+    device). Checks the stream against the reference's (tests/golden/e2e_q4mix.npz) when it is the same workload."""
+    import quanta_cpp_amd.qnt as qnt
+    hp = qnt.HParams()
+    log("generating the synthetic q4mix model (seed 5)")
+    tens = qnt.synthetic_q4mix(5, hp)
+    dec = qh.Decoder(hp, tens, ctx_len=4096)
+    del tens
+    ids = np.random.default_rng(9).integers(0, hp.vocab_size, n_prompt).astype(np.int32)
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    dec.prefill(ids, 0, top_k=1)  # warm-up
+    torch.cuda.synchronize()
+    e0, e1 = ev(), ev()
+    e0.record()
+    dec.prefill(ids, 0, top_k=1)
+    e1.record()
+    torch.cuda.synchronize()
+    prefill_s = e0.elapsed_time(e1) / 1e3
+    dec.begin(steps + 1)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            dec.step(top_k=1)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    e0, e1 = ev(), ev()
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    decode_s = e0.elapsed_time(e1) / 1e3
+    out = dec.outputs(steps + 1)
+    parity = None
+    gpath = os.path.join(ROOT, "tests", "golden", "e2e_q4mix.npz")
+    if check and steps >= 255 and n_prompt == 512 and os.path.exists(gpath):
+        g = np.load(gpath, allow_pickle=False)
+        parity = bool((out[:256] == g["out"]).all())
+        if not parity:
+            raise SystemExit("bench: GPU token stream differs from the reference's")
+    layer_bytes = sum(_layer_bytes(hp))
+    screen_bytes = hp.vocab_size * (hp.dim // 2 + 2 * (hp.dim // 32) * 2)
+    dec.close()
+    del graph
+    return {"prefill_tok_per_s": n_prompt / prefill_s, "prefill_ms": prefill_s * 1e3,
+            "decode_tok_per_s": steps / decode_s, "decode_ms_per_token": decode_s / steps * 1e3,
+            "decode_weight_GBps": (layer_bytes + screen_bytes) / (decode_s / steps) / 1e9,
+            "stream_equals_reference": parity, "tokens": int(steps), "prompt": int(n_prompt)}
+
+
+def _layer_bytes(hp):
+    """Weight bytes one decode step streams through the layers (Q8_0 attention, Q4_0 MLP)."""
+    qd, kvd = hp.n_heads * hp.head_dim, hp.n_kv_heads * hp.head_dim
+    for _ in range(hp.n_layers):
+        yield 1.0625 * (qd * hp.dim + 2 * kvd * hp.dim + hp.dim * qd)
+        yield 0.5625 * (3 * hp.ffn_dim * hp.dim)
+
+
+def e2e_cpu_baseline(n_prompt=64, n_gen=16):
+    """The reference engine's own `gen --greedy` flow (oracle/_ref) on the host cores, bounded: a 64-token prompt and
+    16 greedy tokens of the same model. Decode rate from the difference of a 16-token and a 1-token run."""
+    sys.path.insert(0, ROOT)
+    import ctypes as C
+    import oracle as orc
+    if orc.ref is None:
+        return None
+    import quanta_cpp_amd.qnt as qnt
+    L = orc.ref.lib
+    L.ref_model_load.restype = C.c_void_p
+    L.ref_model_load.argtypes = [C.c_char_p, C.c_int, C.c_int]
+    L.ref_model_free.argtypes = [C.c_void_p]
+    L.ref_gen.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    hp = qnt.HParams()
+    path = os.path.join("/tmp", f"quanta_bench_q4mix_{os.getpid()}.qnt")
+    qnt.write_qnt(path, hp, qnt.synthetic_q4mix(5, hp))
+    threads = max(1, min(16, os.cpu_count() or 1))
+    try:
+        m = L.ref_model_load(path.encode(), 4096, threads)
+        ids = np.random.default_rng(9).integers(0, hp.vocab_size, n_prompt).astype(np.int32)
+        out = np.zeros(n_gen, np.int32)
+        L.ref_gen(m, ids.ctypes.data, n_prompt, 1, out.ctypes.data, None, None)  # warm-up (page-in)
+        t0 = time.perf_counter()
+        L.ref_gen(m, ids.ctypes.data, n_prompt, 1, out.ctypes.data, None, None)
+        t1 = time.perf_counter()
+        L.ref_gen(m, ids.ctypes.data, n_prompt, n_gen, out.ctypes.data, None, None)
+        t2 = time.perf_counter()
+        L.ref_model_free(m)
+    finally:
+        os.remove(path)
+    one, full = t1 - t0, t2 - t1
+    return {"prefill_tok_per_s": n_prompt / one, "decode_tok_per_s": (n_gen - 1) / max(full - one, 1e-9),
+            "cores": threads, "kind": "reference",
+            "sample": f"reference gen --greedy, {n_prompt}-token prompt, {n_gen} tokens, {threads} threads"}
+
+
 def read_traffic(path):
     """profiles/q4_gemv_traffic.txt: `fetch_bytes_per_launch: X` and `write_bytes_per_launch: Y`."""
     if not os.path.exists(path):
@@ -316,12 +415,22 @@ def main():
         log("shortlist head")
         h = head_bench(qh, synth, torch, orc.oracle, max(3, args.steps // 4), 1)
         extra["shortlist_head_151936x896"] = {kk: (round(v, 3) if isinstance(v, float) else v) for kk, v in h.items()}
+        log("end-to-end q4mix decode")
+        e = e2e_bench(qh, torch)
+        extra["e2e_q4mix_qwen2.5_0.5b"] = {kk: (round(v, 3) if isinstance(v, float) else v) for kk, v in e.items()}
     if extra:
         result["extra"] = extra
     if not args.no_cpu:
         log("CPU baseline")
         result["cpu_baseline"] = cpu_baseline(synth, shapes)
         result["cpu_baseline"]["value"] = round(result["cpu_baseline"]["value"], 3)
+        if not args.no_extra:
+            log("CPU baseline, end to end")
+            e = e2e_cpu_baseline()
+            if e is not None:
+                extra["e2e_q4mix_qwen2.5_0.5b_cpu_reference"] = {kk: (round(v, 3) if isinstance(v, float) else v)
+                                                                  for kk, v in e.items()}
+                result["extra"] = extra
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

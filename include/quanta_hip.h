@@ -165,6 +165,60 @@ int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_t
                       const float* xd, const qh_head_query* query, const qh_head_out* out, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------ GPU-resident decoder */
+
+/* Model shape (reference engine/src/model_file.h:40-45, HParams) and the context length of the KV cache. */
+typedef struct qh_model_desc {
+    int32_t vocab_size, dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, ctx_len, qkv_bias;
+    float rope_theta, norm_eps;
+} qh_model_desc;
+
+typedef struct qh_decoder qh_decoder;
+
+/* Device addresses of the decoder's results and state, valid until qh_decoder_destroy. */
+typedef struct qh_decoder_state {
+    float* logits;          /* [vocab]: the last head call's logits (-inf outside the shortlist) */
+    float* hidden;          /* [dim]: the last head call's final normed hidden state */
+    int8_t* xq;             /* [dim]: its int8 quantization (first dim bytes) */
+    float* xd;              /* [dim / 32]: its block scales */
+    qh_head_stats* stats;   /* the last shortlist call's summary (top1, n_rows, ...) */
+    int32_t* top1_full;     /* the greedy token of the last full-head call */
+    int32_t* pos;           /* next position */
+    int32_t* n_out;         /* tokens written to the output list since qh_decoder_begin */
+    int32_t* token;         /* the token the next step consumes */
+    uint16_t* kcache;       /* [n_layers][ctx_len][n_kv_heads * head_dim] fp16 bits */
+    uint16_t* vcache;
+} qh_decoder_state;
+
+/* Creates a decoder over device tensors, in this order (reference model.cpp:14-33, 47-58):
+ *   model.embed_tokens.weight (Q8_0 [vocab][dim], also the LM head), model.norm.weight (F32 [1][dim]);
+ *   per layer: input_layernorm (F32), q_proj, k_proj, v_proj, o_proj (Q8_0 or Q4_0), q/k/v biases (F32, or data NULL
+ *   without qkv_bias), post_attention_layernorm (F32), gate_proj, up_proj, down_proj (Q8_0 or Q4_0);
+ *   then quanta.head_q4 (Q4_0 [vocab][dim]) and quanta.head_err (F16 [vocab][dim/32]), or both with data NULL.
+ * Allocates an fp16 KV cache for ctx_len positions and the work buffers. dim, ctx_len <= 8192, head_dim <= 256
+ * and a multiple of 8, n_heads * head_dim == dim. The tensors must stay alive while the decoder is used.
+ * Replaces: Model::load (reference model.cpp:10-106) after the .qnt file is read and uploaded. */
+int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tensors, qh_decoder** out);
+int qh_decoder_destroy(qh_decoder* d);
+
+/* n prompt tokens (device array) at positions [pos0, pos0 + n): every layer in 32-token chunks, then the head for
+ * the last token (top_k > 0: shortlist head with n_valid = vocab; 0: full 8-bit head). The next position becomes
+ * pos0 + n. Replaces: Model::forward_batch (reference model.cpp:349-433). */
+int qh_decoder_prefill(qh_decoder* d, const int32_t* tokens, int n, int pos0, int top_k, void* stream);
+
+/* Starts a greedy generation: the last head call's greedy token becomes the first output (out_dev[0]) and the next
+ * input, as Session::generate samples its first token from the prompt's logits (reference session.cpp:33-52). */
+int qh_decoder_begin(qh_decoder* d, int top_k, int32_t* out_dev, int out_cap, void* stream);
+
+/* One greedy decode step entirely on the device: forward of the current token at the current position, head,
+ * greedy token appended to the output list and made the next input, position + 1. The launch sequence does not
+ * depend on host state, so it can be captured in a HIP graph once and replayed for every step.
+ * Replaces: one iteration of Session::generate with the greedy sampler (reference session.cpp:39-49, model.cpp:165-228,
+ * sampler.cpp:35-37). */
+int qh_decoder_step(qh_decoder* d, int top_k, void* stream);
+
+int qh_decoder_views(qh_decoder* d, qh_decoder_state* v);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,13 +42,25 @@ class qh_head_out(C.Structure):
                 ("stats", C.c_void_p)]
 
 
+class qh_model_desc(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("vocab_size", "dim", "n_layers", "n_heads", "n_kv_heads", "head_dim",
+                                         "ffn_dim", "ctx_len", "qkv_bias")] + [("rope_theta", C.c_float),
+                                                                              ("norm_eps", C.c_float)]
+
+
+class qh_decoder_state(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("logits", "hidden", "xq", "xd", "stats", "top1_full", "pos", "n_out",
+                                          "token", "kcache", "vcache")]
+
+
 # Every symbol include/quanta_hip.h declares, in header order.
 EXPORTS = ("qh_last_error", "qh_version", "qh_init", "qh_quant_bytes", "qh_tensor_bytes", "qh_validate_tensor",
            "qh_malloc", "qh_free", "qh_memcpy_h2d", "qh_memcpy_d2h", "qh_memset", "qh_stream_sync",
            "qh_stream_create", "qh_stream_destroy",
            "qh_quantize_q8", "qh_matvec_q", "qh_matmul_q", "qh_argmax_workspace_bytes", "qh_argmax",
            "qh_shortlist_workspace_bytes",
-           "qh_shortlist_head")
+           "qh_shortlist_head", "qh_decoder_create", "qh_decoder_destroy", "qh_decoder_prefill", "qh_decoder_begin",
+           "qh_decoder_step", "qh_decoder_views")
 
 
 def build() -> None:
@@ -73,6 +85,12 @@ def _bind(lib):
         "qh_shortlist_workspace_bytes": ([i32, i32, i32], sz),
         "qh_shortlist_head": ([C.POINTER(qh_tensor)] * 3 + [vp, vp, C.POINTER(qh_head_query), C.POINTER(qh_head_out),
                                vp, sz, vp], i32),
+        "qh_decoder_create": ([C.POINTER(qh_model_desc), C.POINTER(qh_tensor), i32, C.POINTER(vp)], i32),
+        "qh_decoder_destroy": ([vp], i32),
+        "qh_decoder_prefill": ([vp, vp, i32, i32, i32, vp], i32),
+        "qh_decoder_begin": ([vp, i32, vp, i32, vp], i32),
+        "qh_decoder_step": ([vp, i32, vp], i32),
+        "qh_decoder_views": ([vp, C.POINTER(qh_decoder_state)], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -234,3 +252,102 @@ class ShortlistHead:
         raw = self.stats_dev.cpu().numpy()
         s = qh_head_stats.from_buffer_copy(raw.tobytes())
         return {f: getattr(s, f) for f, _ in qh_head_stats._fields_}
+
+
+# ------------------------------------------------------------------------------------------------ decoder
+
+LAYER_ORDER = ("input_layernorm.weight", "self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+               "self_attn.o_proj.weight", "self_attn.q_proj.bias", "self_attn.k_proj.bias", "self_attn.v_proj.bias",
+               "post_attention_layernorm.weight", "mlp.gate_proj.weight", "mlp.up_proj.weight",
+               "mlp.down_proj.weight")
+
+
+def _d2h(ptr, nbytes, dtype):
+    out = np.empty(nbytes // np.dtype(dtype).itemsize, dtype)
+    _check(lib().qh_memcpy_d2h(out.ctypes.data, C.c_void_p(ptr), nbytes, _stream()))
+    return out
+
+
+class Decoder:
+    """The GPU-resident decoder (qh_decoder_*) over a .qnt tensor set (quanta_cpp_amd.qnt records), uploaded once."""
+
+    def __init__(self, hp, tensors: dict, ctx_len: int | None = None, device="cuda"):
+        torch = _torch()
+        self.hp = hp
+        names = ["model.embed_tokens.weight", "model.norm.weight"]
+        for l in range(hp.n_layers):
+            names += [f"model.layers.{l}.{n}" for n in LAYER_ORDER]
+        names += ["quanta.head_q4", "quanta.head_err"]
+        offs, total = [], 0
+        for n in names:
+            offs.append(total)
+            if n in tensors:
+                total += (tensors[n].data.size + 255) // 256 * 256
+        self.buf = torch.empty(max(total, 256), dtype=torch.uint8, device=device)
+        host = np.zeros(max(total, 256), np.uint8)
+        for n, o in zip(names, offs):
+            if n in tensors:
+                host[o:o + tensors[n].data.size] = np.asarray(tensors[n].data)
+        self.buf.copy_(torch.from_numpy(host))
+        del host
+        arr = (qh_tensor * len(names))()
+        base = self.buf.data_ptr()
+        for i, (n, o) in enumerate(zip(names, offs)):
+            t = tensors.get(n)
+            arr[i] = qh_tensor(0, 0, 0, None) if t is None else qh_tensor(t.dtype, t.rows, t.cols, base + o)
+        self._tensors = arr
+        self.desc = qh_model_desc(hp.vocab_size, hp.dim, hp.n_layers, hp.n_heads, hp.n_kv_heads, hp.head_dim,
+                                  hp.ffn_dim, ctx_len or hp.max_seq, int(hp.qkv_bias), hp.rope_theta, hp.norm_eps)
+        h = C.c_void_p()
+        _check(lib().qh_decoder_create(C.byref(self.desc), arr, len(names), C.byref(h)))
+        self.h = h
+        st = qh_decoder_state()
+        _check(lib().qh_decoder_views(self.h, C.byref(st)))
+        self.views = st
+        self.tokens = None
+        self.out = None
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().qh_decoder_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prefill(self, tokens, pos0: int = 0, top_k: int = 1):
+        torch = _torch()
+        self.tokens = torch.as_tensor(np.ascontiguousarray(tokens, np.int32)).to(self.buf.device)
+        _check(lib().qh_decoder_prefill(self.h, _ptr(self.tokens), self.tokens.numel(), pos0, top_k, _stream()))
+
+    def begin(self, out_cap: int, top_k: int = 1):
+        torch = _torch()
+        self.out = torch.zeros(out_cap, dtype=torch.int32, device=self.buf.device)
+        _check(lib().qh_decoder_begin(self.h, top_k, _ptr(self.out), out_cap, _stream()))
+
+    def step(self, top_k: int = 1):
+        _check(lib().qh_decoder_step(self.h, top_k, _stream()))
+
+    # host copies of the device state (synchronous)
+    def stats(self) -> dict:
+        raw = _d2h(self.views.stats, C.sizeof(qh_head_stats), np.uint8)
+        st = qh_head_stats.from_buffer_copy(raw.tobytes())
+        return {f: getattr(st, f) for f, _ in qh_head_stats._fields_}
+
+    def hidden(self):
+        return _d2h(self.views.hidden, 4 * self.hp.dim, np.float32)
+
+    def hq(self):
+        return _d2h(self.views.xq, self.hp.dim, np.int8), _d2h(self.views.xd, 4 * (self.hp.dim // QK), np.float32)
+
+    def logits(self):
+        return _d2h(self.views.logits, 4 * self.hp.vocab_size, np.float32)
+
+    def top1_full(self) -> int:
+        return int(_d2h(self.views.top1_full, 4, np.int32)[0])
+
+    def outputs(self, n: int):
+        return self.out[:n].cpu().numpy()

@@ -53,6 +53,13 @@ int validate_range(int rows, int r0, int r1, const char* what) {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
+// Device checks of qh_init for the current device (gfx950), once per device.
+int qh_init_current() {
+    int dev = 0;
+    if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    return qh_init(dev);
+}
+
 }  // namespace
 }  // namespace qh
 
@@ -230,6 +237,89 @@ int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_t
     if (!aligned16(workspace)) return fail(QH_ERR_ALIGN, "qh_shortlist_head: workspace not 16-byte aligned");
     return check_hip(launch_shortlist_head(*head8, *head4, *err, xq, xd, *query, *out, workspace, as_stream(stream)),
                      "qh_shortlist_head launch");
+}
+
+int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tensors, qh_decoder** out) {
+    if (!hp || !tensors || !out) return fail(QH_ERR_ARG, "qh_decoder_create: null argument");
+    *out = nullptr;
+    const int D = hp->dim, L = hp->n_layers;
+    if (D <= 0 || D > 8192 || D % 64 || hp->ffn_dim <= 0 || hp->ffn_dim % QH_QK || hp->ffn_dim > kMaxCols || L <= 0 ||
+        hp->n_heads <= 0 || hp->n_kv_heads <= 0 || hp->n_heads % hp->n_kv_heads || hp->head_dim <= 0 ||
+        hp->head_dim > 256 || hp->head_dim % 8 || hp->n_heads * hp->head_dim != D || hp->ctx_len <= 0 ||
+        hp->ctx_len > 8192 || hp->vocab_size <= 0)
+        return fail(QH_ERR_SHAPE, "qh_decoder_create: unsupported model shape");  // as model.cpp:39-46
+    if (n_tensors != 2 + 12 * L + 2) return fail(QH_ERR_ARG, "qh_decoder_create: %d tensors, needs %d", n_tensors, 4 + 12 * L);
+    const int kvd = hp->n_kv_heads * hp->head_dim, F = hp->ffn_dim;
+    auto want = [&](int i, int rows, int cols, bool quant, const char* what) -> int {
+        const qh_tensor& t = tensors[i];
+        if (quant) {
+            if (int rc = validate_quant(&t, what)) return rc;
+        } else if (t.dtype != QH_F32 || !t.data) {
+            return fail(QH_ERR_DTYPE, "qh_decoder_create: %s must be f32", what);
+        }
+        if (t.rows != rows || t.cols != cols)
+            return fail(QH_ERR_SHAPE, "qh_decoder_create: %s is %d x %d, expected %d x %d", what, t.rows, t.cols, rows,
+                        cols);
+        return QH_OK;
+    };
+    if (tensors[0].dtype != QH_Q8_0) return fail(QH_ERR_DTYPE, "qh_decoder_create: the embedding must be q8_0");
+    if (int rc = want(0, hp->vocab_size, D, true, "embedding")) return rc;
+    if (int rc = want(1, 1, D, false, "final norm")) return rc;
+    for (int l = 0; l < L; ++l) {
+        const int b = 2 + 12 * l;
+        const int rows[12] = {1, D, kvd, kvd, D, 1, 1, 1, 1, F, F, D};
+        const int cols[12] = {D, D, D, D, D, D, kvd, kvd, D, D, D, F};
+        const bool quant[12] = {false, true, true, true, true, false, false, false, false, true, true, true};
+        for (int j = 0; j < 12; ++j) {
+            if (j >= 5 && j <= 7 && !hp->qkv_bias) continue;
+            if (int rc = want(b + j, rows[j], cols[j], quant[j], "layer tensor")) return rc;
+        }
+    }
+    const qh_tensor& h4 = tensors[2 + 12 * L];
+    const qh_tensor& he = tensors[3 + 12 * L];
+    if (h4.data || he.data) {
+        if (h4.dtype != QH_Q4_0 || he.dtype != QH_F16 || h4.rows != hp->vocab_size || h4.cols != D ||
+            he.rows != hp->vocab_size || he.cols != D / QH_QK || !h4.data || !he.data || !head_shape_supported(D))
+            return fail(QH_ERR_SHAPE, "qh_decoder_create: bad shortlist head tensors");  // as model.cpp:49-58
+    }
+    if (int rc = qh_init_current()) return rc;
+    Decoder* d = nullptr;
+    if (int rc = decoder_create(hp, tensors, n_tensors, &d)) return rc;
+    *out = reinterpret_cast<qh_decoder*>(d);
+    return QH_OK;
+}
+
+int qh_decoder_destroy(qh_decoder* d) {
+    decoder_destroy(reinterpret_cast<Decoder*>(d));
+    return QH_OK;
+}
+
+int qh_decoder_prefill(qh_decoder* d, const int32_t* tokens, int n, int pos0, int top_k, void* stream) {
+    if (!d || !tokens) return fail(QH_ERR_ARG, "qh_decoder_prefill: null argument");
+    Decoder* dd = reinterpret_cast<Decoder*>(d);
+    if (n <= 0) return fail(QH_ERR_ARG, "qh_decoder_prefill: n = %d", n);  // as model.cpp:351
+    if (pos0 < 0 || pos0 + n > decoder_ctx(dd))
+        return fail(QH_ERR_ARG, "qh_decoder_prefill: positions [%d, %d) exceed the context", pos0, pos0 + n);
+    if (top_k < 0 || top_k > QH_HEAD_MAX_TOPK) return fail(QH_ERR_UNSUPPORTED, "qh_decoder_prefill: top_k %d", top_k);
+    return check_hip(decoder_prefill(dd, tokens, n, pos0, top_k, as_stream(stream)), "qh_decoder_prefill");
+}
+
+int qh_decoder_begin(qh_decoder* d, int top_k, int32_t* out_dev, int out_cap, void* stream) {
+    if (!d || !out_dev || out_cap <= 0) return fail(QH_ERR_ARG, "qh_decoder_begin: bad argument");
+    return check_hip(decoder_begin(reinterpret_cast<Decoder*>(d), top_k, out_dev, out_cap, as_stream(stream)),
+                     "qh_decoder_begin");
+}
+
+int qh_decoder_step(qh_decoder* d, int top_k, void* stream) {
+    if (!d) return fail(QH_ERR_ARG, "qh_decoder_step: null decoder");
+    if (top_k < 0 || top_k > QH_HEAD_MAX_TOPK) return fail(QH_ERR_UNSUPPORTED, "qh_decoder_step: top_k %d", top_k);
+    return check_hip(decoder_step(reinterpret_cast<Decoder*>(d), top_k, as_stream(stream)), "qh_decoder_step");
+}
+
+int qh_decoder_views(qh_decoder* d, qh_decoder_state* v) {
+    if (!d || !v) return fail(QH_ERR_ARG, "qh_decoder_views: null argument");
+    decoder_views(reinterpret_cast<Decoder*>(d), v);
+    return QH_OK;
 }
 
 }  // extern "C"

@@ -49,4 +49,14 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
                                  const int8_t* xq, const float* xd, const qh_head_query& q, const qh_head_out& out,
                                  void* ws, hipStream_t s);
 
+// GPU-resident decoder (qh_decoder.hip). Tensors in qh_decoder_create order; all sizes validated by the caller.
+struct Decoder;
+int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tensors, Decoder** out);
+void decoder_destroy(Decoder* d);
+hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, int top_k, hipStream_t s);
+hipError_t decoder_begin(Decoder* d, int top_k, int32_t* out, int out_cap, hipStream_t s);
+hipError_t decoder_step(Decoder* d, int top_k, hipStream_t s);
+void decoder_views(Decoder* d, qh_decoder_state* v);
+int decoder_ctx(const Decoder* d);
+
 }  // namespace qh

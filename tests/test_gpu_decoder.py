@@ -1,0 +1,132 @@
+"""GPU parity of the decoder (qh_decoder_*), through the C-ABI.
+
+* small synthetic model (2 layers, vocab 4096): after the batched prefill and after every greedy decode step, the final
+  normed hidden state, its int8 quantization, the 8-bit head rows and the token equal what the reference engine wrote
+  (tests/golden/e2e_small.npz), bit for bit;
+* another seed, 3 layers, a prompt longer than one 32-token chunk, shortlist and full-head steps: hidden states and
+  logits equal the oracle's decoder restatement, bit for bit;
+* the benchmark model (24 layers, vocab 151936): 512-token prompt, 256 greedy tokens equal the reference's `gen`
+  stream (tests/golden/e2e_q4mix.npz), with each step's head rows and the exact logit of the chosen token;
+* one decode step captured in a HIP graph and replayed gives the same stream as eager steps.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, bits
+from decoder_util import oracle_decoder, qnt_module
+
+pytestmark = pytest.mark.gpu
+
+
+def _golden(name):
+    return np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+
+
+def test_decoder_small_model_matches_reference_states(qh, gpu):
+    qnt = qnt_module()
+    g = _golden("e2e_small.npz")
+    hp = qnt.HParams(vocab_size=int(g["vocab"]), n_layers=int(g["n_layers"]))
+    dec = qh.Decoder(hp, qnt.synthetic_q4mix(int(g["seed"]), hp), ctx_len=256)
+    dec.prefill(g["prompt"], 0, top_k=1)
+    n_gen = len(g["out"])
+    dec.begin(n_gen + 1)
+    for s in range(n_gen + 1):
+        st = dec.stats()
+        assert st["n_rows"] == int(g["head_rows"][s]), s
+        assert (bits(dec.hidden()) == bits(g["hidden"][s])).all(), f"hidden state after step {s}"
+        q, d = dec.hq()
+        assert (q == g["hq"][s]).all() and (bits(d) == bits(g["hd"][s])).all(), s
+        if s == n_gen:
+            break
+        dec.step(top_k=1)
+    assert (dec.outputs(n_gen) == g["out"]).all()
+
+
+def test_decoder_equals_oracle_long_prompt_and_full_head(qh, oracle, gpu):
+    qnt = qnt_module()
+    hp = qnt.HParams(vocab_size=3072, n_layers=3)
+    tens = qnt.synthetic_q4mix(23, hp)
+    ctx = 512
+    orc = oracle_decoder(oracle, hp, tens, ctx_len=ctx)
+    dec = qh.Decoder(hp, tens, ctx_len=ctx)
+    ids = np.random.default_rng(5).integers(0, hp.vocab_size, 77).astype(np.int32)
+    r = orc.forward_batch(ids, 0, top_k=1)
+    dec.prefill(ids, 0, top_k=1)
+    assert (bits(dec.hidden()) == bits(r["hidden"])).all()
+    assert (bits(dec.logits()) == bits(r["logits"])).all()
+    assert dec.stats()["n_rows"] == r["rows"]
+    dec.begin(16, top_k=1)
+    pos = len(ids)
+    tok = int(np.argmax(r["logits"]))
+    for step in range(8):
+        top_k = 0 if step % 3 == 2 else 1
+        r = orc.forward(tok, pos, top_k=top_k)
+        dec.step(top_k=top_k)
+        assert (bits(dec.hidden()) == bits(r["hidden"])).all(), step
+        if top_k:
+            assert (bits(dec.logits()) == bits(r["logits"])).all(), step
+            assert dec.stats()["n_rows"] == r["rows"], step
+        else:
+            assert (bits(dec.logits()) == bits(r["logits"])).all(), step
+            assert dec.top1_full() == oracle.argmax(r["logits"]), step
+        tok = oracle.argmax(r["logits"])
+        pos += 1
+    assert dec.outputs(9)[1:].tolist() == [int(x) for x in dec.outputs(9)[1:]]
+
+
+@pytest.fixture(scope="module")
+def q4mix(qh, gpu):
+    qnt = qnt_module()
+    import hashlib
+    g = _golden("e2e_q4mix.npz")
+    hp = qnt.HParams()
+    tens = qnt.synthetic_q4mix(int(g["seed"]), hp)
+    for name, want in zip(g["digest_names"], g["digests"]):
+        got = hashlib.sha256(np.ascontiguousarray(tens[str(name)].data).view(np.uint8).tobytes()).hexdigest()
+        assert got == str(want), f"regenerated {name} differs from the one the golden stream was made with"
+    dec = qh.Decoder(hp, tens, ctx_len=4096)
+    return dec, g
+
+
+def test_decoder_q4mix_stream_equals_reference(qh, q4mix):
+    dec, g = q4mix
+    n_gen = len(g["out"])
+    dec.prefill(g["prompt"], 0, top_k=1)
+    dec.begin(n_gen + 1)
+    rows, tops = [], []
+    for s in range(n_gen):
+        st = dec.stats()
+        rows.append(st["n_rows"])
+        tops.append(st["top1_logit"])
+        dec.step(top_k=1)
+    out = dec.outputs(n_gen)
+    first = int(np.nonzero(out != g["out"])[0][0]) if (out != g["out"]).any() else -1
+    assert first < 0, f"token stream differs from step {first}: {out[first:first + 4]} vs {g['out'][first:first + 4]}"
+    assert rows == g["head_rows"].tolist()
+    assert (bits(np.array(tops, np.float32)) == bits(g["top_logit"])).all()
+
+
+def test_decoder_graph_replay_equals_eager(qh, q4mix):
+    import torch
+    dec, g = q4mix
+    n = 48
+    dec.prefill(g["prompt"][:300], 0, top_k=1)
+    dec.begin(n + 1)
+    for _ in range(n):
+        dec.step(top_k=1)
+    eager = dec.outputs(n + 1).copy()
+    dec.prefill(g["prompt"][:300], 0, top_k=1)
+    dec.begin(n + 1)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            dec.step(top_k=1)
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(n):
+        graph.replay()
+        torch.cuda.synchronize()  # eager work of the program between replays
+    assert (dec.outputs(n + 1) == eager).all()
