@@ -210,16 +210,18 @@ def head_bench(qh, synth, torch, oracle, steps, warmup):
             "shortlist_GBps": sl_bytes / sl_us / 1e3, "full_head_GBps": full_bytes / full_us / 1e3}
 
 
-def e2e_bench(qh, torch, steps=256, n_prompt=512, check=True):
-    """End-to-end greedy generation on the q4mix Qwen2.5-0.5B-shaped model: prefill of a 512-token prompt in 32-token
-    chunks, then `steps` decode steps, each one HIP-graph replay of a captured step (the token is fed back on the
-    device). Checks the stream against the reference's (tests/golden/e2e_q4mix.npz) when it is the same workload."""
+def e2e_model():
     import quanta_cpp_amd.qnt as qnt
     hp = qnt.HParams()
     log("generating the synthetic q4mix model (seed 5)")
-    tens = qnt.synthetic_q4mix(5, hp)
+    return hp, qnt.synthetic_q4mix(5, hp)
+
+
+def e2e_bench(qh, torch, hp, tens, steps=256, n_prompt=512, check=True):
+    """End-to-end greedy generation on the q4mix Qwen2.5-0.5B-shaped model: prefill of a 512-token prompt in 32-token
+    chunks, then `steps` decode steps, each one HIP-graph replay of a captured step (the token is fed back on the
+    device). Checks the stream against the reference's (tests/golden/e2e_q4mix.npz) when it is the same workload."""
     dec = qh.Decoder(hp, tens, ctx_len=4096)
-    del tens
     ids = np.random.default_rng(9).integers(0, hp.vocab_size, n_prompt).astype(np.int32)
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     dec.prefill(ids, 0, top_k=1)  # warm-up
@@ -272,7 +274,7 @@ def _layer_bytes(hp):
         yield 0.5625 * (3 * hp.ffn_dim * hp.dim)
 
 
-def e2e_cpu_baseline(n_prompt=64, n_gen=16):
+def e2e_cpu_baseline(hp, tens, n_prompt=64, n_gen=16):
     """The reference engine's own `gen --greedy` flow (oracle/_ref) on the host cores, bounded: a 64-token prompt and
     16 greedy tokens of the same model. Decode rate from the difference of a 16-token and a 1-token run."""
     sys.path.insert(0, ROOT)
@@ -286,9 +288,8 @@ def e2e_cpu_baseline(n_prompt=64, n_gen=16):
     L.ref_model_load.argtypes = [C.c_char_p, C.c_int, C.c_int]
     L.ref_model_free.argtypes = [C.c_void_p]
     L.ref_gen.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
-    hp = qnt.HParams()
     path = os.path.join("/tmp", f"quanta_bench_q4mix_{os.getpid()}.qnt")
-    qnt.write_qnt(path, hp, qnt.synthetic_q4mix(5, hp))
+    qnt.write_qnt(path, hp, tens)
     threads = max(1, min(16, os.cpu_count() or 1))
     try:
         m = L.ref_model_load(path.encode(), 4096, threads)
@@ -365,6 +366,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end prefill + decode measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path runs on a single "
@@ -377,6 +379,11 @@ def main():
     import oracle as orc
     qh.init(0)
     shapes = [(4864, 896), (896, 4864)]
+    if args.e2e_only:
+        hp, tens = e2e_model()
+        e = e2e_bench(qh, torch, hp, tens, steps=max(args.steps, 256))
+        print(json.dumps({kk: (round(v, 3) if isinstance(v, float) else v) for kk, v in e.items()}), flush=True)
+        return 0
     log("headline: Q4_0 GEMV rotation")
     head = gemv_rotation(qh, synth, torch, 3, shapes, args.steps, args.warmup, check=orc.oracle)
     result = {
@@ -416,7 +423,8 @@ def main():
         h = head_bench(qh, synth, torch, orc.oracle, max(3, args.steps // 4), 1)
         extra["shortlist_head_151936x896"] = {kk: (round(v, 3) if isinstance(v, float) else v) for kk, v in h.items()}
         log("end-to-end q4mix decode")
-        e = e2e_bench(qh, torch)
+        hp, tens = e2e_model()
+        e = e2e_bench(qh, torch, hp, tens)
         extra["e2e_q4mix_qwen2.5_0.5b"] = {kk: (round(v, 3) if isinstance(v, float) else v) for kk, v in e.items()}
     if extra:
         result["extra"] = extra
@@ -426,7 +434,7 @@ def main():
         result["cpu_baseline"]["value"] = round(result["cpu_baseline"]["value"], 3)
         if not args.no_extra:
             log("CPU baseline, end to end")
-            e = e2e_cpu_baseline()
+            e = e2e_cpu_baseline(hp, tens)
             if e is not None:
                 extra["e2e_q4mix_qwen2.5_0.5b_cpu_reference"] = {kk: (round(v, 3) if isinstance(v, float) else v)
                                                                   for kk, v in e.items()}

@@ -187,7 +187,11 @@ typedef struct qh_decoder_state {
     int32_t* n_out;         /* tokens written to the output list since qh_decoder_begin */
     int32_t* token;         /* the token the next step consumes */
     uint16_t* kcache;       /* [n_layers][ctx_len][n_kv_heads * head_dim] fp16 bits */
-    uint16_t* vcache;
+    uint16_t* vcache;       /* [n_layers][ceil(ctx_len / 8)][n_kv_heads * head_dim][8] fp16 bits: blocks of 8
+                               positions, each dimension's 8 values contiguous (position p, column c at
+                               ((p / 8) * kv_dim + c) * 8 + p % 8 within its layer) */
+    int32_t* status;        /* 0, or bit 0: a step ran at a position >= ctx_len (it wrote nothing to the cache);
+                               bit 1: a prompt token was outside [0, vocab). Cleared by qh_decoder_prefill. */
 } qh_decoder_state;
 
 /* Creates a decoder over device tensors, in this order (reference model.cpp:14-33, 47-58):
@@ -195,8 +199,8 @@ typedef struct qh_decoder_state {
  *   per layer: input_layernorm (F32), q_proj, k_proj, v_proj, o_proj (Q8_0 or Q4_0), q/k/v biases (F32, or data NULL
  *   without qkv_bias), post_attention_layernorm (F32), gate_proj, up_proj, down_proj (Q8_0 or Q4_0);
  *   then quanta.head_q4 (Q4_0 [vocab][dim]) and quanta.head_err (F16 [vocab][dim/32]), or both with data NULL.
- * Allocates an fp16 KV cache for ctx_len positions and the work buffers. dim, ctx_len <= 8192, head_dim <= 256
- * and a multiple of 8, n_heads * head_dim == dim. The tensors must stay alive while the decoder is used.
+ * Allocates an fp16 KV cache for ctx_len positions and the work buffers. dim, ctx_len <= 8192, head_dim 64 or
+ * 128, n_heads * head_dim == dim. The tensors must stay alive while the decoder is used.
  * Replaces: Model::load (reference model.cpp:10-106) after the .qnt file is read and uploaded. */
 int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tensors, qh_decoder** out);
 int qh_decoder_destroy(qh_decoder* d);

@@ -60,6 +60,7 @@ class _Oracle:
         L.qo_decoder_create.argtypes = [_i32p, np.ctypeslib.ndpointer(np.float32), C.c_void_p, _i32p]
         L.qo_decoder_create.restype = C.c_void_p
         L.qo_decoder_free.argtypes = [C.c_void_p]
+        L.qo_decoder_kv.argtypes = [C.c_void_p, _int, _int, C.c_void_p, C.c_void_p]
         L.qo_decoder_forward.argtypes = [C.c_void_p, _int, _int, _int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
         L.qo_decoder_forward_batch.argtypes = [C.c_void_p, _i32p, _int, _int, _int, C.c_void_p, C.c_void_p, C.c_void_p,
                                                C.c_void_p]
@@ -163,6 +164,13 @@ class Decoder:
         rows = self.lib.qo_decoder_forward(self.h, token, pos, top_k, lg.ctypes.data, h.ctypes.data, q.ctypes.data,
                                            d.ctypes.data)
         return dict(logits=lg, hidden=h, hq=q, hd=d, rows=rows)
+
+    def kv(self, layer, n_pos, kv_dim):
+        """The f16 KV cache bits of one layer, positions [0, n_pos): (k, v) as uint16 [n_pos][kv_dim]."""
+        k = np.empty((n_pos, kv_dim), np.uint16)
+        v = np.empty((n_pos, kv_dim), np.uint16)
+        self.lib.qo_decoder_kv(self.h, layer, n_pos, k.ctypes.data, v.ctypes.data)
+        return k, v
 
     def forward_batch(self, tokens, pos0, top_k=1):
         lg, h, q, d = self._outs()

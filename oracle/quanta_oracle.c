@@ -382,6 +382,12 @@ qo_decoder* qo_decoder_create(const int* hp, const float* hpf, const void* const
     return d;
 }
 
+void qo_decoder_kv(const qo_decoder* d, int l, int n_pos, uint16_t* k, uint16_t* v) {
+    const size_t kvd = (size_t)d->nkv * d->hdim, off = (size_t)l * d->ctx * kvd;
+    memcpy(k, d->kc + off, 2 * kvd * (size_t)n_pos);
+    memcpy(v, d->vc + off, 2 * kvd * (size_t)n_pos);
+}
+
 void qo_decoder_free(qo_decoder* d) {
     if (!d) return;
     free(d->kc); free(d->vc); free(d->x); free(d->xb); free(d->xb2); free(d->q); free(d->k); free(d->v);

@@ -103,6 +103,9 @@ int qo_decoder_forward(qo_decoder* d, int token, int pos, int top_k, float* logi
 int qo_decoder_forward_batch(qo_decoder* d, const int* tokens, int n, int pos0, int top_k, float* logits,
                              float* hidden, int8_t* hq, float* hd);
 
+/* Copies the f16 KV cache of layer l, positions [0, n_pos): k and v as [n_pos][n_kv_heads * head_dim] bits. */
+void qo_decoder_kv(const qo_decoder* d, int l, int n_pos, uint16_t* k, uint16_t* v);
+
 /* RoPE table of the reference (ops_ref.cpp:201-214) for positions [0, n_pos): cs[pos][i] = (cosf, sinf) of
  * pos * powf(theta, -2 i / head_dim), i < head_dim / 2, as [n_pos][head_dim / 2][2] floats. */
 void qo_rope_table(float* cs, int n_pos, int head_dim, float theta);

@@ -50,7 +50,7 @@ class qh_model_desc(C.Structure):
 
 class qh_decoder_state(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("logits", "hidden", "xq", "xd", "stats", "top1_full", "pos", "n_out",
-                                          "token", "kcache", "vcache")]
+                                          "token", "kcache", "vcache", "status")]
 
 
 # Every symbol include/quanta_hip.h declares, in header order.
@@ -348,6 +348,24 @@ class Decoder:
 
     def top1_full(self) -> int:
         return int(_d2h(self.views.top1_full, 4, np.int32)[0])
+
+    def status(self) -> int:
+        """0, or bit 0: a step ran past the context (nothing was written); bit 1: a prompt token was out of range."""
+        return int(_d2h(self.views.status, 4, np.int32)[0])
+
+    def kv(self, layer: int, n_pos: int):
+        """The f16 KV cache bits of one layer, positions [0, n_pos): (k, v) as uint16 [n_pos][n_kv_heads*head_dim]."""
+        kvd = self.hp.n_kv_heads * self.hp.head_dim
+        ctx = self.desc.ctx_len
+        k = _d2h(self.views.kcache + 2 * layer * ctx * kvd, 2 * n_pos * kvd, np.uint16).reshape(n_pos, kvd)
+        # V is stored in blocks of 8 positions, [pos / 8][kv_dim][8]
+        nblk = (n_pos + 7) // 8
+        raw = _d2h(self.views.vcache + 2 * layer * ((ctx + 7) // 8 * 8) * kvd, 2 * nblk * 8 * kvd, np.uint16)
+        v = raw.reshape(nblk, kvd, 8).transpose(0, 2, 1).reshape(nblk * 8, kvd)[:n_pos]
+        return k, np.ascontiguousarray(v)
+
+    def position(self) -> int:
+        return int(_d2h(self.views.pos, 4, np.int32)[0])
 
     def outputs(self, n: int):
         return self.out[:n].cpu().numpy()

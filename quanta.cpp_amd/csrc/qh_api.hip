@@ -244,8 +244,8 @@ int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_t
     *out = nullptr;
     const int D = hp->dim, L = hp->n_layers;
     if (D <= 0 || D > 8192 || D % 64 || hp->ffn_dim <= 0 || hp->ffn_dim % QH_QK || hp->ffn_dim > kMaxCols || L <= 0 ||
-        hp->n_heads <= 0 || hp->n_kv_heads <= 0 || hp->n_heads % hp->n_kv_heads || hp->head_dim <= 0 ||
-        hp->head_dim > 256 || hp->head_dim % 8 || hp->n_heads * hp->head_dim != D || hp->ctx_len <= 0 ||
+        hp->n_heads <= 0 || hp->n_kv_heads <= 0 || hp->n_heads % hp->n_kv_heads ||
+        (hp->head_dim != 64 && hp->head_dim != 128) || hp->n_heads * hp->head_dim != D || hp->ctx_len <= 0 ||
         hp->ctx_len > 8192 || hp->vocab_size <= 0)
         return fail(QH_ERR_SHAPE, "qh_decoder_create: unsupported model shape");  // as model.cpp:39-46
     if (n_tensors != 2 + 12 * L + 2) return fail(QH_ERR_ARG, "qh_decoder_create: %d tensors, needs %d", n_tensors, 4 + 12 * L);

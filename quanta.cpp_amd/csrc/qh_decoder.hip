@@ -2,29 +2,35 @@
 // (engine/src/model.cpp:165-228, 349-433) with the operation order of its CPU build, so every hidden state, logit and
 // greedy token is bit-identical to the reference.
 //
-// Per layer and token (decode: one token; prefill: a chunk of up to 32 tokens, all at once):
-//   add_rmsnorm_quant  residual add (previous down / o projection), rmsnorm (serial FMA sum of squares, one rounded
-//                      1/sqrt), int8 quantization per 32-block              (model.cpp:178-179, 211-213)
-//   q, k, v            decode GEMV or prefill int8-MFMA matmul            (model.cpp:180-182, 377-379)
-//   bias_rope_kv       biases, RoPE from a host table (glibc powf/cosf/sinf of the reference's formula), f16 K/V
-//                      store at the token's position                       (model.cpp:183-195, 385-395)
-//   attention          one workgroup per (head, token): scores (serial FMA dot over head_dim), max, glibc-identical
-//                      expf, serial sum in position order, normalise, serial weighted V sum in position order
-//                      (model.cpp:115-137, ops_ref.cpp:216-226)
-//   quantize, o        the attention output is quantized and projected    (model.cpp:207-208)
-//   gate, up, swiglu   g / (1 + expf(-g)) * u                              (ops_ref.cpp:243-248)
-//   quantize, down     then the next layer's add_rmsnorm_quant adds it to the residual stream
-// then the final add + rmsnorm + quantize and the head (Exact Shortlist Head for top-k queries, full 8-bit head
-// otherwise). Decoding keeps the position and the token on the device, so one decode step is a fixed sequence of
-// launches that a caller can capture in a HIP graph and replay: the step reads the token the previous step chose,
-// and its last kernel writes the new token, appends it to the output list and advances the position.
+// Decode (one token) runs five kernels per layer, each with its elementwise work fused in:
+//   qkv        one launch for the q, k and v GEMVs (three row segments, same activation)   (model.cpp:180-182)
+//   attention  per query head: biases, RoPE (host table of glibc powf/cosf/sinf of the reference's formula), this
+//              token's f16 K/V row into the cache, scores (serial FMA dot over head_dim), max, glibc-identical expf,
+//              serial sum in position order, normalise, serial weighted V sum in position order, and the int8
+//              quantization of the head's two 32-blocks of output        (model.cpp:115-137, 183-208, ops_ref.cpp:201-226)
+//   o          GEMV, residual add, then the workgroup that finishes last runs rmsnorm (serial FMA sum of squares, one
+//              rounded 1/sqrt) and quantizes the normed row for the MLP   (model.cpp:208-213, ops_ref.cpp:195-199)
+//   gate/up    one GEMV over the same rows of both matrices, g / (1 + expf(-g)) * u, quantization (ops_ref.cpp:243-248)
+//   down       GEMV, residual add, and the last workgroup normalises for the next layer (or the final norm)
+// then the head (Exact Shortlist Head for top-k queries, full 8-bit head + argmax otherwise). The position and the
+// token live on the device, so a decode step is a fixed launch sequence that can be captured in a HIP graph and
+// replayed: the step reads the token the previous step chose, and its last kernel writes the new token, appends it to
+// the output list and advances the position. A step at a position beyond the context writes nothing into the cache
+// and raises bit 0 of the status word; a prompt token outside the vocabulary raises bit 1.
+//
+// Prefill (chunks of up to 32 tokens) uses the int8-MFMA matmul for every projection and the same attention kernel
+// over a (head, token) grid: a token's keys and values for the chunk's positions come from the chunk's own
+// projections, so no kernel reads a cache row another workgroup of the same launch writes.
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
+#include <type_traits>
 #include <vector>
 
 #include "qh_device.h"
+#include "qh_gemv.h"
 #include "qh_internal.h"
 #include "qh_math.h"
 
@@ -32,150 +38,424 @@ namespace qh {
 
 namespace {
 
-constexpr int kChunk = 32;  // prefill chunk (reference Model::kBatch, model.h:52)
+constexpr int kChunk = 32;            // prefill chunk (reference Model::kBatch, model.h:52)
+constexpr int kMaxCtx = 8192;         // positions the attention kernel's score array holds
+constexpr int kVStageBytes = 96 * 1024;  // LDS for staged V rows (768 rows at head_dim 64)
+constexpr int kFuseLds = 65536;       // dynamic LDS limit of the fused GEMV kernels
+
+// Positions the V cache holds per layer: the context rounded up to its 8-position blocks.
+inline int v_ctx(int ctx) { return (ctx + 7) & ~7; }
+
+enum { kStatusCtx = 1, kStatusToken = 2 };
 
 // glibc-identical expf on the device (all 2^32 inputs checked against the host's expf in tests).
 __device__ __forceinline__ float dev_expf(float x) { return expf_variant<2>(x); }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return f16_to_f32(h); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// f32 -> f16 (round to nearest even) of an already rounded f32 value, as the reference stores its f32 K / V results
+// into the f16 cache. The empty asm makes the value opaque, so the compiler cannot fuse the FMA that produced it and
+// this conversion into one v_fma_mixlo_f16, which rounds only once (straight to f16) and differs on double-rounding
+// cases.
+__device__ __forceinline__ uint16_t f2h(float f) {
+    asm volatile("" : "+v"(f));
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// quantize_q8 of one 32-block held one value per lane of a half-wave (ops_ref.cpp:69-83): the block's absolute
+// maximum / 127, codes rounded half away from zero. Every lane of the half-wave must be active.
+__device__ __forceinline__ void quant_block32(float v, int8_t* __restrict__ q, float* __restrict__ d) {
+    float a = __builtin_fabsf(v);
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) a = __builtin_fmaxf(a, __shfl_xor(a, off, 64));
+    const float sc = a / 127.0f;
+    const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
+    const int i = (int)threadIdx.x & 31;
+    q[i] = (int8_t)(int)round_half_away(v * inv);
+    if (i == 0) *d = sc;
+}
+
+// acc = op(acc, p[i]) for i = 0 .. n-1 in order, by one thread, over floats in LDS (16-byte aligned, n >= 1). A wave
+// issues about one instruction per 4 cycles whatever its kind, so the loop is shaped for the fewest instructions
+// per element: batches of 32 values read as 8 b128 at immediate offsets from one base, two register sets that
+// alternate without copies (the next batch in flight while the current one is consumed), no clamping. It reads up
+// to kChainPad floats past n: callers size the array n + kChainPad.
+constexpr int kChainPad = 64;
+
+// An LDS address the compiler treats as per-lane: uniform LDS addresses otherwise get rematerialized into a VGPR for
+// every read, costing an instruction each (mbcnt_lo(0, 0) is 0 in every lane).
+template <typename T>
+__device__ __forceinline__ const T* lane_ptr(const T* p) {
+    return p + __builtin_amdgcn_mbcnt_lo(0u, 0u);
+}
+
+template <typename Op>
+__device__ __forceinline__ float lds_chain(const float* p, int n, Op op) {
+    float4 a[8], b[8];
+    auto ld = [](float4(&r)[8], const float* q) {
+        const float4* q4 = reinterpret_cast<const float4*>(q);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r[k] = q4[k];
+    };
+    float acc = 0.0f;
+    auto use = [&](const float4(&r)[8], int cnt) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (4 * k + 0 < cnt) acc = op(acc, r[k].x);
+            if (4 * k + 1 < cnt) acc = op(acc, r[k].y);
+            if (4 * k + 2 < cnt) acc = op(acc, r[k].z);
+            if (4 * k + 3 < cnt) acc = op(acc, r[k].w);
+        }
+    };
+    int j = 0;
+    p = lane_ptr(p);
+    ld(a, p);
+    // sched_barrier keeps each prefetch ahead of the values it overlaps (the scheduler would sink it)
+    for (; j + 64 <= n; j += 64) {
+        ld(b, p + j + 32);
+        __builtin_amdgcn_sched_barrier(0);
+        use(a, 32);
+        ld(a, p + j + 64);
+        __builtin_amdgcn_sched_barrier(0);
+        use(b, 32);
+    }
+    if (j + 32 <= n) {
+        ld(b, p + j + 32);
+        __builtin_amdgcn_sched_barrier(0);
+        use(a, 32);
+        use(b, n - j - 32);  // cnt is uniform
+    } else {
+        use(a, n - j);
+    }
+    return acc;
+}
+
+// Up to 8 float4 per thread of a row of n4 float4 (n4 <= 2048) with every load issued before the first use:
+// slot k holds element tid + 256 k (clamped onto the last element, so the loads are unconditional).
+struct Row4 {
+    float4 v[8];
+    __device__ __forceinline__ void load(const float* __restrict__ src, int n4) {
+        const float4* s4 = reinterpret_cast<const float4*>(src);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = s4[min((int)threadIdx.x + 256 * k, n4 - 1)];
+    }
+};
+
+// rmsnorm of the row xs[0..D) (LDS, 16-byte aligned, complete) with weight w (loaded into wr by the caller before
+// the row was complete, so its latency is hidden), then quantize_q8 of the normed row; also written to `normed`
+// when given (ops_ref.cpp:195-199: ss += x*x as one FMA per element in order, scale = 1/sqrt(ss/n + eps),
+// y = x * scale * w). Called by all 256 threads of a workgroup; D % 64 == 0, D <= 8192.
+__device__ void norm_quant_lds(float* xs, int D, const Row4& wr, float eps, int8_t* __restrict__ oq,
+                               float* __restrict__ od, float* __restrict__ normed) {
+    __shared__ float scale_sh;
+    const int tid = (int)threadIdx.x, n4 = D / 4;
+    if (tid == 0)
+        scale_sh = 1.0f / __builtin_sqrtf(lds_chain(xs, D, [](float acc, float v) { return __builtin_fmaf(v, v, acc); }) /
+                                              (float)D +
+                                          eps);
+    __syncthreads();
+    const float scale = scale_sh;
+    float4* x4 = reinterpret_cast<float4*>(xs);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int i4 = tid + 256 * k;
+        if (i4 < n4) {
+            float4 xv = x4[i4];
+            xv.x = xv.x * scale * wr.v[k].x;
+            xv.y = xv.y * scale * wr.v[k].y;
+            xv.z = xv.z * scale * wr.v[k].z;
+            xv.w = xv.w * scale * wr.v[k].w;
+            x4[i4] = xv;
+            if (normed) reinterpret_cast<float4*>(normed)[i4] = xv;
+        }
+    }
+    __syncthreads();
+    const int nb = D / QK;
+    for (int b = tid >> 5; b < nb; b += 8)  // a half-wave per 32-block (uniform within the half-wave)
+        quant_block32(xs[b * QK + (tid & 31)], oq + b * QK, od + b);
+}
+
+// Activation fill for a GEMV tile whose input is rmsnorm(x) * w quantized (the decode step's q/k/v and gate/up
+// inputs): every workgroup normalises the residual row itself, while its first pass of weight loads is in flight,
+// and quantizes it straight into the tile's LDS codes / scales, so no kernel of its own and no cross-workgroup
+// synchronisation is needed. With eq set, the row is instead the embedding of token *tok (the first layer), and
+// workgroup 0 also stores it as the residual stream x_out. tmp: LDS scratch of D + kChainPad floats (16-byte
+// aligned).
+struct NormAct {
+    const float* x;
+    const int8_t* eq;
+    const uint16_t* es;
+    const int32_t* tok;
+    int V;
+    float* x_out;
+    int* status;
+    const float* w;
+    float eps;
+    int D;
+    float* tmp;
+    template <bool XL>
+    __device__ __forceinline__ void fill(int8_t* xs, float* xds) const {
+        static_assert(XL, "the normed activation is produced in LDS");
+        __shared__ float scale_sh;
+        const int tid = (int)threadIdx.x, n4 = D / 4, nb = D / QK;
+        Row4 wr, xr;
+        wr.load(w, n4);
+        if (eq) {
+            int t = *tok;
+            const bool bad = t < 0 || t >= V;
+            if (bad && tid == 0 && blockIdx.x == 0) atomicOr(status, kStatusToken);
+            t = bad ? 0 : t;
+            const int8_t* er = eq + (size_t)t * D;
+            const uint16_t* sr = es + (size_t)t * nb;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int i4 = min(tid + 256 * k, n4 - 1);
+                const uint32_t c4 = *reinterpret_cast<const uint32_t*>(er + 4 * i4);
+                const float sc = h2f(sr[i4 / (QK / 4)]);
+                xr.v[k].x = bad ? 0.0f : (float)(int8_t)(c4 & 0xff) * sc;
+                xr.v[k].y = bad ? 0.0f : (float)(int8_t)((c4 >> 8) & 0xff) * sc;
+                xr.v[k].z = bad ? 0.0f : (float)(int8_t)((c4 >> 16) & 0xff) * sc;
+                xr.v[k].w = bad ? 0.0f : (float)(int8_t)(c4 >> 24) * sc;
+            }
+        } else {
+            xr.load(x, n4);
+        }
+        float4* t4 = reinterpret_cast<float4*>(tmp);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i4 = tid + 256 * k;
+            if (i4 < n4) {
+                t4[i4] = xr.v[k];
+                if (x_out && blockIdx.x == 0) reinterpret_cast<float4*>(x_out)[i4] = xr.v[k];
+            }
+        }
+        __syncthreads();
+        if (tid == 0)
+            scale_sh = 1.0f / __builtin_sqrtf(lds_chain(tmp, D, [](float acc, float v) { return __builtin_fmaf(v, v, acc); }) /
+                                                  (float)D +
+                                              eps);
+        __syncthreads();
+        const float scale = scale_sh;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i4 = tid + 256 * k;
+            if (i4 < n4) {
+                float4 y = xr.v[k];
+                y.x = y.x * scale * wr.v[k].x;
+                y.y = y.y * scale * wr.v[k].y;
+                y.z = y.z * scale * wr.v[k].z;
+                y.w = y.w * scale * wr.v[k].w;
+                t4[i4] = y;
+            }
+        }
+        __syncthreads();
+        for (int b = tid >> 5; b < nb; b += 8) quant_block32(tmp[b * QK + (tid & 31)], xs + b * QK, xds + b);
+    }
+};
 
 // ------------------------------------------------------------------------------------------------------ kernels
 
-// x[t] = embedding row of tokens[t] (Q8_0 get_row, ops_ref.cpp:176-181): code * f16 scale, exact in f32.
-__global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ tokens, const int8_t* __restrict__ eq,
-                                                    const uint16_t* __restrict__ es, int D, float* __restrict__ x) {
-    const int t = blockIdx.x;
-    const int tok = tokens[t];
-    for (int i = threadIdx.x; i < D; i += 256)
-        x[(size_t)t * D + i] = (float)eq[(size_t)tok * D + i] * h2f(es[(size_t)tok * (D / QK) + i / QK]);
+// x[t] = embedding row of tokens[t] (Q8_0 get_row, ops_ref.cpp:176-181: code * f16 scale, exact in f32), then the
+// first layer's rmsnorm and quantization. One workgroup per token.
+__global__ __launch_bounds__(256) void embed_norm_quant_kernel(const int32_t* __restrict__ tokens,
+                                                               const int8_t* __restrict__ eq,
+                                                               const uint16_t* __restrict__ es, int D, int V,
+                                                               float* __restrict__ x, const float* __restrict__ w,
+                                                               float eps, int8_t* __restrict__ oq,
+                                                               float* __restrict__ od, int* __restrict__ status) {
+    __shared__ __align__(16) float xs[8192 + kChainPad];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    Row4 wr;
+    wr.load(w, D / 4);
+    int tok = tokens[t];
+    const bool bad = tok < 0 || tok >= V;
+    if (bad) {
+        if (tid == 0) atomicOr(status, kStatusToken);
+        tok = 0;
+    }
+    const int8_t* er = eq + (size_t)tok * D;
+    const uint16_t* sr = es + (size_t)tok * (D / QK);
+    for (int i4 = tid; i4 < D / 4; i4 += 256) {  // 4 codes and their block's scale
+        const uint32_t c4 = *reinterpret_cast<const uint32_t*>(er + 4 * i4);
+        const float sc = h2f(sr[i4 / (QK / 4)]);
+        float4 v;
+        v.x = bad ? 0.0f : (float)(int8_t)(c4 & 0xff) * sc;
+        v.y = bad ? 0.0f : (float)(int8_t)((c4 >> 8) & 0xff) * sc;
+        v.z = bad ? 0.0f : (float)(int8_t)((c4 >> 16) & 0xff) * sc;
+        v.w = bad ? 0.0f : (float)(int8_t)(c4 >> 24) * sc;
+        reinterpret_cast<float4*>(x + (size_t)t * D)[i4] = v;
+        reinterpret_cast<float4*>(xs)[i4] = v;
+    }
+    __syncthreads();
+    norm_quant_lds(xs, D, wr, eps, oq + (size_t)t * D, od + (size_t)t * (D / QK), nullptr);
 }
 
-// One workgroup per token: optional residual add x += o, then rmsnorm with weight w and int8 quantization of the
-// normed row; the normed row is also written to `normed` when given. D <= 8192.
+// One workgroup per token: residual add x += o, then rmsnorm with weight w and int8 quantization of the normed row;
+// the normed row is also written to `normed` when given. D <= 8192.
 __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(float* __restrict__ x, const float* __restrict__ o,
                                                                 const float* __restrict__ w, int D, float eps,
                                                                 int8_t* __restrict__ xq, float* __restrict__ xd,
                                                                 float* __restrict__ normed) {
-    __shared__ float xs[8192];
-    __shared__ float scale_sh;
-    const int t = blockIdx.x, tid = threadIdx.x;
-    float* xr = x + (size_t)t * D;
-    for (int i = tid; i < D; i += 256) {
-        float v = xr[i];
-        if (o) {
-            v = v + o[(size_t)t * D + i];
-            xr[i] = v;
-        }
-        xs[i] = v;
-    }
-    __syncthreads();
-    if (tid == 0) {  // ops_ref.cpp:195-196: ss += x*x (one FMA per element, in order), then 1/sqrt(ss/n + eps)
-        float ss = 0.0f;
-        for (int i = 0; i < D; ++i) ss = __builtin_fmaf(xs[i], xs[i], ss);
-        scale_sh = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
-    }
-    __syncthreads();
-    const float scale = scale_sh;
-    for (int i = tid; i < D; i += 256) xs[i] = xs[i] * scale * w[i];
-    __syncthreads();
-    if (normed)
-        for (int i = tid; i < D; i += 256) normed[(size_t)t * D + i] = xs[i];
-    // quantize_q8 (ops_ref.cpp:69-83): a half-wave per 32-block
-    const int nb = D / QK;
-    for (int b0 = 0; b0 < nb; b0 += 8) {
-        const int b = b0 + (tid >> 5), i = tid & 31;
-        const bool ok = b < nb;
-        const float v = ok ? xs[b * QK + i] : 0.0f;
-        float a = __builtin_fabsf(v);
+    __shared__ __align__(16) float xs[8192 + kChainPad];
+    const int t = blockIdx.x, tid = threadIdx.x, n4 = D / 4;
+    Row4 wr, xr, orow;
+    wr.load(w, n4);
+    xr.load(x + (size_t)t * D, n4);
+    orow.load(o + (size_t)t * D, n4);
 #pragma unroll
-        for (int off = 16; off >= 1; off >>= 1) a = __builtin_fmaxf(a, __shfl_xor(a, off, 64));
-        const float d = a / 127.0f;
-        const float inv = d > 0.0f ? 1.0f / d : 0.0f;
-        if (ok) {
-            xq[(size_t)t * D + b * QK + i] = (int8_t)(int)round_half_away(v * inv);
-            if (i == 0) xd[(size_t)t * nb + b] = d;
+    for (int k = 0; k < 8; ++k) {
+        const int i4 = tid + 256 * k;
+        if (i4 < n4) {
+            float4 v = xr.v[k];
+            v.x = v.x + orow.v[k].x;
+            v.y = v.y + orow.v[k].y;
+            v.z = v.z + orow.v[k].z;
+            v.w = v.w + orow.v[k].w;
+            reinterpret_cast<float4*>(x + (size_t)t * D)[i4] = v;
+            reinterpret_cast<float4*>(xs)[i4] = v;
         }
     }
+    __syncthreads();
+    norm_quant_lds(xs, D, wr, eps, xq + (size_t)t * D, xd + (size_t)t * (D / QK), normed);
 }
 
-// Biases, RoPE and the K/V store for n tokens at positions pos0 + t. One workgroup per token.
-// rope (ops_ref.cpp:201-214): p[i] = a*c - b*s and p[i+half] = b*c + a*s with the reference build's contraction,
-// i.e. fma(a, c, -(b*s)) and fma(b, c, a*s).
-__global__ __launch_bounds__(256) void bias_rope_kv_kernel(float* __restrict__ q, float* __restrict__ k,
-                                                           float* __restrict__ v, const float* __restrict__ bq,
-                                                           const float* __restrict__ bk, const float* __restrict__ bv,
-                                                           const float* __restrict__ cs, const int* __restrict__ pos_dev,
-                                                           int n_heads, int n_kv, int hd, uint16_t* __restrict__ kc,
-                                                           uint16_t* __restrict__ vc) {
-    const int t = blockIdx.x, tid = threadIdx.x;
-    const int pos = *pos_dev + t;
-    const int qd = n_heads * hd, kvd = n_kv * hd, half = hd / 2;
-    float* qt = q + (size_t)t * qd;
-    float* kt = k + (size_t)t * kvd;
-    float* vt = v + (size_t)t * kvd;
-    const float* c = cs + (size_t)pos * hd;  // [half][2]
-    for (int e = tid; e < (n_heads + n_kv) * half; e += 256) {
-        const int h = e / half, i = e % half;
-        const bool isq = h < n_heads;
-        float* p = isq ? qt + h * hd : kt + (h - n_heads) * hd;
-        const float* bb = isq ? (bq ? bq + h * hd : nullptr) : (bk ? bk + (h - n_heads) * hd : nullptr);
-        float a = p[i], b = p[i + half];
-        if (bb) {
-            a = a + bb[i];
-            b = b + bb[i + half];
-        }
-        const float cc = c[2 * i], ss = c[2 * i + 1];
-        const float na = __builtin_fmaf(a, cc, -(b * ss));
-        const float nb = __builtin_fmaf(b, cc, a * ss);
-        if (isq) {
-            p[i] = na;
-            p[i + half] = nb;
-        } else {
-            const int kh = h - n_heads;
-            kc[(size_t)pos * kvd + kh * hd + i] = f2h(na);
-            kc[(size_t)pos * kvd + kh * hd + i + half] = f2h(nb);
-        }
-    }
-    for (int i = tid; i < kvd; i += 256) {
-        float val = vt[i];
-        if (bv) val = val + bv[i];
-        vc[(size_t)pos * kvd + i] = f2h(val);
-    }
-}
-
-// Attention of token t (position pos0 + t) and query head h over cached positions [0, pos]. One workgroup per
-// (head, token); scores live in LDS (ctx <= 8192).
-__global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
-                                                        const uint16_t* __restrict__ vc, const int* __restrict__ pos_dev,
-                                                        int n_heads, int n_kv, int hd, float* __restrict__ out) {
-    __shared__ float att[8192];
-    __shared__ float qs[256];
+// Attention of token t (position pos0 + t) and query head h over positions [0, pos0 + t], for a chunk of n <= 32
+// tokens whose raw projections are q [n][n_heads*HD], k / v [n][n_kv*HD]. One workgroup per (head, token).
+// Cache layouts (f16 bits, per layer): K row-major [pos][n_kv*HD]; V in blocks of 8 positions, [pos/8][n_kv*HD][8],
+// so one 16-byte read gives a lane 8 consecutive positions of its dimension. Rows below pos0 come from the cache; the
+// chunk's own rows are rebuilt from k / v (bias, RoPE, f16 rounding, exactly as stored), and workgroups of the first
+// query head of each KV group store their token's row. The output (HD values) is quantized straight into oq / od
+// ([n][n_heads*HD] codes, one scale per 32 values).
+// The LDS footprint allows one workgroup per CU (one wave per SIMD); saying so lets the compiler keep the V preload
+// in registers.
+template <int HD>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attention_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                        const float* __restrict__ v, const float* __restrict__ bq,
+                                                        const float* __restrict__ bk, const float* __restrict__ bv,
+                                                        const float* __restrict__ cs, const int* __restrict__ pos_dev,
+                                                        int ctx, int n_heads, int n_kv, uint16_t* __restrict__ kc,
+                                                        uint16_t* __restrict__ vc, int8_t* __restrict__ oq,
+                                                        float* __restrict__ od, int* __restrict__ status) {
+    constexpr int HALF = HD / 2, CPR = HD / 8;           // 16-byte chunks per f16 K row
+    constexpr int kVRows = kVStageBytes / (HD * 2);      // V rows one LDS stage holds (a multiple of 8)
+    constexpr int kVBlk = kVRows / 8;                    // 8-row blocks per stage
+    constexpr int kVRegs = kVBlk * HD / 256;             // 16-byte V chunks each thread preloads
+    __shared__ __align__(16) float att[kMaxCtx + kChainPad];
+    __shared__ __align__(16) uint4 vst[(kVBlk + 4) * HD];  // [block][dim] -> 8 rows; 4 blocks of read padding
+    __shared__ __align__(16) uint16_t kloc[kChunk * HD];
+    __shared__ __align__(16) uint16_t vloc[kChunk * HD];
+    __shared__ __align__(16) float qs[HD];
     __shared__ float red[4];
     __shared__ float inv_sh;
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int pos = *pos_dev + t;
-    const int kvd = n_kv * hd, group = n_heads / n_kv, kvh = h / group;
-    const float scale = 1.0f / __builtin_sqrtf((float)hd);
-    for (int i = tid; i < hd; i += 256) qs[i] = q[(size_t)t * n_heads * hd + h * hd + i];
-    __syncthreads();
-    // scores: s = sum_i q_i * k_i as one FMA per element in order, then * scale (model.cpp:122-125)
-    float mx = -__builtin_inff();
-    for (int j = tid; j <= pos; j += 256) {
-        const uint16_t* kr = kc + (size_t)j * kvd + kvh * hd;
-        float s = 0.0f;
-        for (int i = 0; i < hd; i += 8) {
-            const uint4 kv8 = *reinterpret_cast<const uint4*>(kr + i);
-            const uint32_t wv[4] = {kv8.x, kv8.y, kv8.z, kv8.w};
+    const int pos0 = *pos_dev, pos = pos0 + t, nrows = pos + 1;
+    if (pos >= ctx || pos0 < 0) {  // uniform: a step past the context touches no cache row
+        if (tid == 0 && h == 0) atomicOr(status, kStatusCtx);
+        return;
+    }
+    const int qd = n_heads * HD, kvd = n_kv * HD, group = n_heads / n_kv, kvh = h / group;
+    // V block b of this head: HD uint4 at vbase + b * kvd (in uint4 units, kvd / 8 per position... see vblock())
+    const uint4* vc4 = reinterpret_cast<const uint4*>(vc);
+    auto vchunk = [&](int blk, int d) { return (size_t)blk * kvd + kvh * HD + d; };  // uint4 index of (block, dim)
+
+    // V blocks [0, min(ceil(pos0 / 8), kVBlk)) of the cache: every load in flight before anything else.
+    const int ncb = min((pos0 + 7) / 8, kVBlk);
+    const int nch = ncb * HD;
+    const int clast = nch > 0 ? nch - 1 : 0;
+    uint4 vr[kVRegs];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                s = __builtin_fmaf(qs[i + 2 * e], h2f((uint16_t)(wv[e] & 0xffffu)), s);
-                s = __builtin_fmaf(qs[i + 2 * e + 1], h2f((uint16_t)(wv[e] >> 16)), s);
+    for (int i = 0; i < kVRegs; ++i) {
+        const int c = min(tid + i * 256, clast);
+        vr[i] = load16(vc4 + vchunk(c / HD, c % HD));
+    }
+
+    // q of this head with bias, rotated; keys and values of the chunk's tokens 0..t (model.cpp:183-195, rope
+    // ops_ref.cpp:201-214: a*c - b*s and b*c + a*s with the reference build's contraction fma(a, c, -(b*s)) and
+    // fma(b, c, a*s)).
+    if (tid < HALF) {
+        const float* qr = q + (size_t)t * qd + h * HD;
+        float a = qr[tid], b = qr[tid + HALF];
+        if (bq) {
+            a = a + bq[h * HD + tid];
+            b = b + bq[h * HD + tid + HALF];
+        }
+        const float* c = cs + (size_t)pos * HD;
+        const float cc = c[2 * tid], ss = c[2 * tid + 1];
+        qs[tid] = __builtin_fmaf(a, cc, -(b * ss));
+        qs[tid + HALF] = __builtin_fmaf(b, cc, a * ss);
+    }
+    for (int e = tid; e < (t + 1) * HALF; e += 256) {
+        const int r = e / HALF, i = e - r * HALF;
+        const float* kr = k + (size_t)r * kvd + kvh * HD;
+        float a = kr[i], b = kr[i + HALF];
+        if (bk) {
+            a = a + bk[kvh * HD + i];
+            b = b + bk[kvh * HD + i + HALF];
+        }
+        const float* c = cs + (size_t)(pos0 + r) * HD;
+        const float cc = c[2 * i], ss = c[2 * i + 1];
+        kloc[r * HD + i] = f2h(__builtin_fmaf(a, cc, -(b * ss)));
+        kloc[r * HD + i + HALF] = f2h(__builtin_fmaf(b, cc, a * ss));
+    }
+    for (int e = tid; e < (t + 1) * HD; e += 256) {
+        const int r = e / HD, i = e - r * HD;
+        float val = v[(size_t)r * kvd + kvh * HD + i];
+        if (bv) val = val + bv[kvh * HD + i];
+        vloc[r * HD + i] = f2h(val);
+    }
+    __syncthreads();
+    if (h % group == 0)
+        for (int i = tid; i < HD; i += 256) {
+            kc[(size_t)pos * kvd + kvh * HD + i] = kloc[t * HD + i];
+            vc[vchunk(pos / 8, i) * 8 + (pos & 7)] = vloc[t * HD + i];
+        }
+
+    // scores: s = sum_i q_i * k_i as one FMA per element in order, then * scale (model.cpp:122-125)
+    float qv[HD];
+#pragma unroll
+    for (int i = 0; i < HD; ++i) qv[i] = qs[i];
+    const float scale = 1.0f / __builtin_sqrtf((float)HD);
+    float mx = -__builtin_inff();
+    constexpr int RB = HD == 64 ? 2 : 1;  // rows per thread per batch, their loads issued together
+    const int grow = pos0 > 0 ? pos0 - 1 : 0;
+    for (int j0 = tid; j0 < nrows; j0 += 256 * RB) {
+        uint4 kk[RB][CPR];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            // both sources read unconditionally (clamped rows), the row's own chosen afterwards
+            const int j = min(j0 + 256 * r, nrows - 1);
+            const uint16_t* kg = kc + (size_t)min(j, grow) * kvd + kvh * HD;
+            const uint16_t* kl = kloc + min(max(j - pos0, 0), kChunk - 1) * HD;
+#pragma unroll
+            for (int i = 0; i < CPR; ++i) {
+                const uint4 g = load16(kg + i * 8);
+                const uint4 l = *reinterpret_cast<const uint4*>(kl + i * 8);
+                kk[r][i] = j < pos0 ? g : l;
             }
         }
-        const float a = s * scale;
-        att[j] = a;
-        mx = a > mx ? a : mx;
+        float sc[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) sc[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) {
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const uint32_t wv[4] = {kk[r][i].x, kk[r][i].y, kk[r][i].z, kk[r][i].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    sc[r] = __builtin_fmaf(qv[i * 8 + 2 * e], h2f((uint16_t)(wv[e] & 0xffffu)), sc[r]);
+                    sc[r] = __builtin_fmaf(qv[i * 8 + 2 * e + 1], h2f((uint16_t)(wv[e] >> 16)), sc[r]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int j = j0 + 256 * r;
+            if (j < nrows) {
+                const float a = sc[r] * scale;
+                att[j] = a;
+                mx = a > mx ? a : mx;
+            }
+        }
     }
     // the maximum does not depend on the order of comparison
 #pragma unroll
@@ -187,47 +467,211 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
     __syncthreads();
     mx = red[0];
     for (int w = 1; w < 4; ++w) mx = red[w] > mx ? red[w] : mx;
-    for (int j = tid; j <= pos; j += 256) att[j] = dev_expf(att[j] - mx);
-    __syncthreads();
-    if (tid == 0) {  // softmax sum in position order (ops_ref.cpp:220-224)
-        float sum = 0.0f;
-        for (int j = 0; j <= pos; ++j) sum = sum + att[j];
-        inv_sh = 1.0f / sum;
+    for (int j = tid; j < nrows; j += 256) att[j] = dev_expf(att[j] - mx);
+    // first V stage: the preloaded cache blocks (the block holding pos0 carries stale rows from pos0 on, replaced
+    // below), then the chunk's rows that fall inside the stage
+#pragma unroll
+    for (int i = 0; i < kVRegs; ++i) {  // unconditional stores (slots past nch go to this thread's padding slot)
+        const int c = tid + i * 256;
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(vst) + 8 * (c < nch ? c : kVBlk * HD + tid)) = vr[i];
     }
     __syncthreads();
-    const float inv = inv_sh;
-    for (int j = tid; j <= pos; j += 256) att[j] = att[j] * inv;
+    uint16_t* vst16 = reinterpret_cast<uint16_t*>(vst);
+    const int s1 = min(nrows, kVRows);
+    for (int e = tid; e < (s1 - pos0) * HD; e += 256) {  // empty when pos0 >= kVRows
+        const int r = pos0 + e / HD, d = e % HD;
+        vst16[((r >> 3) * HD + d) * 8 + (r & 7)] = vloc[(r - pos0) * HD + d];
+    }
     __syncthreads();
-    // out_i = sum_j a_j * v_ji, one FMA per position in order (model.cpp:131-135): thread i per dimension
-    if (tid < hd) {
-        const uint16_t* vr = vc + kvh * hd + tid;
-        float acc = 0.0f;
-        int j = 0;
-        for (; j + 4 <= pos + 1; j += 4) {
-            const uint16_t v0 = vr[(size_t)j * kvd], v1 = vr[(size_t)(j + 1) * kvd];
-            const uint16_t v2 = vr[(size_t)(j + 2) * kvd], v3 = vr[(size_t)(j + 3) * kvd];
-            acc = __builtin_fmaf(att[j], h2f(v0), acc);
-            acc = __builtin_fmaf(att[j + 1], h2f(v1), acc);
-            acc = __builtin_fmaf(att[j + 2], h2f(v2), acc);
-            acc = __builtin_fmaf(att[j + 3], h2f(v3), acc);
+    if (tid == 0)  // softmax sum in position order (ops_ref.cpp:220-224)
+        inv_sh = 1.0f / lds_chain(att, nrows, [](float acc, float a) { return acc + a; });
+    __syncthreads();
+    const float inv = inv_sh;
+    for (int j = tid; j < nrows; j += 256) att[j] = att[j] * inv;
+    __syncthreads();
+
+    // out_i = sum_j a_j * v_ji, one FMA per position in order (model.cpp:131-135): thread i per dimension, over
+    // the rows of each LDS stage. Batches of 32 rows (4 V reads, 8 broadcast reads of the weights) at immediate
+    // offsets, two register sets alternating; reads past the stage stay inside the padding.
+    float acc = 0.0f;
+    for (int s0 = 0;;) {
+        const int se = min(nrows, s0 + kVRows);
+        if (tid < HD) {
+            uint4 vA[4], vB[4];
+            float4 aA[8], aB[8];
+            auto ld = [&](uint4(&vv)[4], float4(&aa)[8], int jr) {  // rows s0 + jr .. + 31 (jr % 32 == 0)
+                const uint4* vp = vst + (jr >> 3) * HD + tid;
+                const float4* ap = reinterpret_cast<const float4*>(lane_ptr(att + s0) + jr);
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) vv[q4] = vp[q4 * HD];
+#pragma unroll
+                for (int q4 = 0; q4 < 8; ++q4) aa[q4] = ap[q4];
+            };
+            auto use = [&](const uint4(&vv)[4], const float4(&aa)[8], int cnt) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const uint32_t w[4] = {vv[q4].x, vv[q4].y, vv[q4].z, vv[q4].w};
+                    const float a8[8] = {aa[2 * q4].x, aa[2 * q4].y, aa[2 * q4].z, aa[2 * q4].w,
+                                         aa[2 * q4 + 1].x, aa[2 * q4 + 1].y, aa[2 * q4 + 1].z, aa[2 * q4 + 1].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (8 * q4 + e < cnt)
+                            acc = __builtin_fmaf(a8[e], h2f((uint16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xffffu)),
+                                                 acc);
+                }
+            };
+            const int n = se - s0;
+            int jr = 0;
+            ld(vA, aA, 0);
+            for (; jr + 64 <= n; jr += 64) {
+                ld(vB, aB, jr + 32);
+                __builtin_amdgcn_sched_barrier(0);
+                use(vA, aA, 32);
+                ld(vA, aA, jr + 64);
+                __builtin_amdgcn_sched_barrier(0);
+                use(vB, aB, 32);
+            }
+            if (jr + 32 <= n) {
+                ld(vB, aB, jr + 32);
+                __builtin_amdgcn_sched_barrier(0);
+                use(vA, aA, 32);
+                use(vB, aB, n - jr - 32);
+            } else {
+                use(vA, aA, n - jr);
+            }
         }
-        for (; j <= pos; ++j) acc = __builtin_fmaf(att[j], h2f(vr[(size_t)j * kvd]), acc);
-        out[(size_t)t * n_heads * hd + h * hd + tid] = acc;
+        s0 = se;
+        if (s0 >= nrows) break;
+        __syncthreads();  // the stage is consumed; load rows [s0, min(nrows, s0 + kVRows)) (s0 % 8 == 0)
+        const int sn = min(nrows, s0 + kVRows);
+        const int nb8 = (sn - s0 + 7) / 8;
+        for (int c = tid; c < nb8 * HD; c += 256) {  // whole cache blocks; the chunk's rows are written after
+            const int blk = s0 / 8 + c / HD, d = c % HD;
+            vst[c] = blk * 8 < pos0 ? vc4[vchunk(blk, d)] : make_uint4(0u, 0u, 0u, 0u);
+        }
+        __syncthreads();
+        for (int e = tid; e < (sn - max(s0, pos0)) * HD; e += 256) {
+            const int r = max(s0, pos0) + e / HD, d = e % HD;
+            vst16[(((r - s0) >> 3) * HD + d) * 8 + (r & 7)] = vloc[(r - pos0) * HD + d];
+        }
+        __syncthreads();
+    }
+    if (tid < HD) {  // quantize_q8 of the attention output, two 32-blocks per 64 dimensions
+        const int col = h * HD + (tid & ~31);
+        quant_block32(acc, oq + (size_t)t * qd + col, od + (size_t)t * (qd / QK) + col / QK);
     }
 }
 
-// h = g / (1 + expf(-g)) * u over n elements (ops_ref.cpp:243-248).
-__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, long n,
-                                                     float* __restrict__ h) {
-    const long i = (long)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) {
-        const float gv = g[i];
-        h[i] = gv / (1.0f + dev_expf(-gv)) * u[i];
+// h = g / (1 + expf(-g)) * u (ops_ref.cpp:243-248) over n_blocks 32-blocks, quantized per block.
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                           long n_blocks, int8_t* __restrict__ oq,
+                                                           float* __restrict__ od) {
+    const long blk = ((long)blockIdx.x * 256 + threadIdx.x) >> 5;
+    if (blk >= n_blocks) return;  // whole half-waves leave together
+    const long i = blk * QK + (threadIdx.x & 31);
+    const float gv = g[i];
+    quant_block32(gv / (1.0f + dev_expf(-gv)) * u[i], oq + blk * QK, od + blk);
+}
+
+// q, k and v GEMVs of one token in one launch: three row segments of one dtype and width over one activation,
+// the layer's normed input, which every workgroup builds itself (NormAct).
+struct QkvSegs {
+    const uint8_t *w0, *w1, *w2;
+    const uint16_t *s0, *s1, *s2;
+    float *o0, *o1, *o2;
+    int rows0, rows1, rows2;
+    int tiles0, tiles1;
+};
+
+template <int DT, int U>
+__global__ __launch_bounds__(256) void gemv_qkv_norm_kernel(QkvSegs a, NormAct act, int nb, int tile_rows,
+                                                            uint32_t nb_magic) {
+    extern __shared__ __align__(16) float smem[];
+    int blk = (int)blockIdx.x;
+    const uint8_t* w = a.w0;
+    const uint16_t* sc = a.s0;
+    float* out = a.o0;
+    int rows = a.rows0;
+    if (blk >= a.tiles0) {
+        blk -= a.tiles0;
+        if (blk >= a.tiles1) {
+            blk -= a.tiles1;
+            w = a.w2, sc = a.s2, out = a.o2, rows = a.rows2;
+        } else {
+            w = a.w1, sc = a.s1, out = a.o1, rows = a.rows1;
+        }
     }
+    const int ra = blk * tile_rows;
+    const int nrows = min(tile_rows, rows - ra);
+    act.tmp = smem + gemv_tile_lds_bytes(nb * QK, tile_rows, true) / 4;
+    const float val = gemv_tile<DT, U, true>(w, sc, nullptr, nullptr, nullptr, nullptr, nb, ra, nrows, tile_rows,
+                                             nb_magic, smem, act);
+    if ((int)threadIdx.x < nrows) out[ra + threadIdx.x] = val;
+}
+
+// One token's projection added into the residual stream: x[r] += (W . xq)[r] (model.cpp:208-210, 224-226).
+template <int DT, int U, bool XL>
+__global__ __launch_bounds__(256) void gemv_residual_kernel(const uint8_t* __restrict__ wq,
+                                                            const uint16_t* __restrict__ wscale,
+                                                            const int8_t* __restrict__ xq,
+                                                            const float* __restrict__ xd, int nb, int rows,
+                                                            int tile_rows, uint32_t nb_magic, float* __restrict__ x) {
+    extern __shared__ __align__(16) float smem[];
+    const int tid = (int)threadIdx.x;
+    const int ra = (int)blockIdx.x * tile_rows;
+    const int nrows = min(tile_rows, rows - ra);
+    const float val = gemv_tile<DT, U, XL>(wq, wscale, nullptr, nullptr, xq, xd, nb, ra, nrows, tile_rows, nb_magic,
+                                           smem);
+    if (tid < nrows) x[ra + tid] = x[ra + tid] + val;
+}
+
+// One token's gate and up GEMVs over the same 32 rows of both matrices, from the normed MLP input each workgroup
+// builds itself (NormAct), then h = g / (1 + expf(-g)) * u and the quantization of those 32 values (one block) for
+// the down projection.
+template <int DT, int U>
+__global__ __launch_bounds__(256) void gemv_swiglu_norm_kernel(const uint8_t* __restrict__ wg,
+                                                               const uint16_t* __restrict__ sg,
+                                                               const uint8_t* __restrict__ wu,
+                                                               const uint16_t* __restrict__ su, NormAct act, int nb,
+                                                               uint32_t nb_magic, int8_t* __restrict__ oq,
+                                                               float* __restrict__ od) {
+    extern __shared__ __align__(16) float smem[];
+    __shared__ float gu[2 * QK];
+    const int tid = (int)threadIdx.x, ra = (int)blockIdx.x * QK;
+    act.tmp = smem + gemv_tile_lds_bytes(nb * QK, 2 * QK, true) / 4;
+    const float val = gemv_tile<DT, U, true, true>(wg, sg, wu, su, nullptr, nullptr, nb, ra, QK, 2 * QK, nb_magic,
+                                                   smem, act);
+    if (tid < 2 * QK) gu[tid] = val;
+    __syncthreads();
+    if (tid < QK) {
+        const float g = gu[tid], u = gu[QK + tid];
+        quant_block32(g / (1.0f + dev_expf(-g)) * u, oq + ra, od + blockIdx.x);
+    }
+}
+
+__global__ __launch_bounds__(256) void residual_add_kernel(float* __restrict__ x, const float* __restrict__ o, int n) {
+    const int i = (int)(blockIdx.x * 256 + threadIdx.x);
+    if (i < n) x[i] = x[i] + o[i];
+}
+
+// rmsnorm + quantization of one row (the final norm before the head), normed row also to `normed`.
+__global__ __launch_bounds__(256) void norm_quant_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                         int D, float eps, int8_t* __restrict__ oq,
+                                                         float* __restrict__ od, float* __restrict__ normed) {
+    __shared__ __align__(16) float xs[8192 + kChainPad];
+    const int tid = threadIdx.x, n4 = D / 4;
+    Row4 wr, xr;
+    wr.load(w, n4);
+    xr.load(x, n4);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        if (tid + 256 * k < n4) reinterpret_cast<float4*>(xs)[tid + 256 * k] = xr.v[k];
+    __syncthreads();
+    norm_quant_lds(xs, D, wr, eps, oq, od, normed);
 }
 
 // Prefill / decode bookkeeping on the device.
-__global__ void set_pos_kernel(int* pos_dev, int value) { *pos_dev = value; }
+__global__ void set_int_kernel(int* p, int value) { *p = value; }
 
 // After a decode step: the chosen token becomes the next input, is appended to out[] and the position advances.
 __global__ void advance_kernel(const qh_head_stats* __restrict__ stats, const int32_t* __restrict__ top1_full,
@@ -263,13 +707,15 @@ struct Decoder {
     // device state
     uint16_t *kc = nullptr, *vc = nullptr;
     float* cs = nullptr;
-    float *x = nullptr, *o = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *g = nullptr,
-          *u = nullptr, *hbuf = nullptr, *hidden = nullptr;
-    int8_t* xq = nullptr;
-    float* xd = nullptr;
+    float *x = nullptr, *o = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *g = nullptr, *u = nullptr,
+          *hidden = nullptr;
+    // int8 activations: qa holds a layer's normed input (and the head's), qb the attention / MLP inner activation
+    int8_t *qa = nullptr, *qb = nullptr;
+    float *da = nullptr, *db = nullptr;
     int32_t* tokens = nullptr;  // [kChunk] prefill input / [0] decode input
     int* pos = nullptr;         // current position
     int* n_out = nullptr;
+    int* status = nullptr;
     int32_t* out = nullptr;
     int out_cap = 0;
     // head
@@ -281,6 +727,7 @@ struct Decoder {
     void* am_ws = nullptr;
     size_t am_ws_bytes = 0;
     int32_t* top1_full = nullptr;
+    bool fuse = true;  // fused decode kernels (QH_DECODER_FUSE=0 at creation selects one launch per operation)
     std::vector<void*> allocs;
 };
 
@@ -291,19 +738,21 @@ enum { L_ATTN_NORM, L_WQ, L_WK, L_WV, L_WO, L_BQ, L_BK, L_BV, L_FFN_NORM, L_WG, 
 
 const qh_tensor& lt(const Decoder* d, int l, int which) { return d->t[T_LAYER0 + l * L_COUNT + which]; }
 const float* lf(const Decoder* d, int l, int which) { return static_cast<const float*>(lt(d, l, which).data); }
+const float* bias(const Decoder* d, int l, int which) { return d->hp.qkv_bias ? lf(d, l, which) : nullptr; }
 const qh_tensor& head4(const Decoder* d) { return d->t[T_LAYER0 + d->hp.n_layers * L_COUNT]; }
 const qh_tensor& head_err(const Decoder* d) { return d->t[T_LAYER0 + d->hp.n_layers * L_COUNT + 1]; }
+const float* final_norm(const Decoder* d) { return static_cast<const float*>(d->t[T_NORM].data); }
+
+const uint8_t* quants(const qh_tensor& W) { return static_cast<const uint8_t*>(W.data); }
+const uint16_t* scales(const qh_tensor& W) {
+    return reinterpret_cast<const uint16_t*>(quants(W) + qh_quant_bytes(W.dtype, W.rows, W.cols));
+}
+uint32_t nb_magic(int nb) { return nb == 1 ? 0u : (uint32_t)((0x100000000ull + (uint64_t)nb - 1) / (uint64_t)nb); }
 
 hipError_t dalloc(Decoder* d, void** p, size_t bytes) {
     hipError_t e = hipMalloc(p, bytes < 256 ? 256 : bytes);
     if (e == hipSuccess) d->allocs.push_back(*p);
     return e;
-}
-
-// GEMV for one token, int8-MFMA matmul for several (identical per row).
-hipError_t linear(float* out, const qh_tensor& W, const int8_t* xq, const float* xd, int n, hipStream_t s) {
-    if (n == 1) return launch_gemv(out, W, xq, xd, 0, W.rows, gemv_plan(W.dtype, W.cols, W.rows), s);
-    return launch_matmul(out, W.rows, W, xq, xd, n, 0, W.rows, s);
 }
 
 #define QH_TRY(expr)                                 \
@@ -312,61 +761,229 @@ hipError_t linear(float* out, const qh_tensor& W, const int8_t* xq, const float*
         if (e_ != hipSuccess) return e_;             \
     } while (0)
 
-// All layers for n tokens whose embeddings are in d->x[0..n) and whose positions start at *d->pos. Leaves the last
-// layer's down projection in d->o (not yet added to the residual stream).
-hipError_t run_layers(Decoder* d, int n, hipStream_t s) {
+// Calls f(dt, u, xl) with std::integral_constant arguments for the plan's dtype, unroll and activation staging, so a
+// caller can launch KERNEL<dt, u, xl> for any plan gemv_plan makes.
+template <typename F>
+hipError_t plan_dispatch(int dtype, const GemvPlan& p, F&& f) {
+    using std::integral_constant;
+    auto go = [&](auto dt, auto u) {
+        if (p.act_lds)
+            f(dt, u, std::true_type{});
+        else
+            f(dt, u, std::false_type{});
+        return hipGetLastError();
+    };
+    auto by_unroll = [&](auto dt) {
+        switch (p.unroll) {
+            case 1: return go(dt, integral_constant<int, 1>{});
+            case 2: return go(dt, integral_constant<int, 2>{});
+            case 4: return go(dt, integral_constant<int, 4>{});
+            case 8: return go(dt, integral_constant<int, 8>{});
+            default: return hipErrorInvalidValue;
+        }
+    };
+    if (dtype == kQ8) return by_unroll(integral_constant<int, kQ8>{});
+    if (dtype == kQ4) return by_unroll(integral_constant<int, kQ4>{});
+    return hipErrorInvalidValue;
+}
+
+hipError_t embed(Decoder* d, const int32_t* tokens, int n, hipStream_t s) {
+    const qh_tensor& emb = d->t[T_EMBED];
+    hipLaunchKernelGGL(embed_norm_quant_kernel, dim3(n), dim3(256), 0, s, tokens,
+                       reinterpret_cast<const int8_t*>(quants(emb)),
+                       reinterpret_cast<const uint16_t*>(quants(emb) + (size_t)emb.rows * emb.cols), d->hp.dim,
+                       d->hp.vocab_size, d->x, lf(d, 0, L_ATTN_NORM), d->hp.norm_eps, d->qa, d->da, d->status);
+    return hipGetLastError();
+}
+
+// The normed-input fill of a decode kernel: layer input from the residual stream x, or (first layer) from the
+// embedding of the current token, which workgroup 0 also stores as x.
+NormAct make_norm(Decoder* d, bool embedding, const float* w) {
+    NormAct a{};
+    if (embedding) {
+        const qh_tensor& emb = d->t[T_EMBED];
+        a.eq = reinterpret_cast<const int8_t*>(quants(emb));
+        a.es = reinterpret_cast<const uint16_t*>(quants(emb) + (size_t)emb.rows * emb.cols);
+        a.tok = d->tokens;
+        a.V = d->hp.vocab_size;
+        a.x_out = d->x;
+    } else {
+        a.x = d->x;
+    }
+    a.status = d->status;
+    a.w = w;
+    a.eps = d->hp.norm_eps;
+    a.D = d->hp.dim;
+    return a;
+}
+
+// LDS of a normed-input GEMV tile: the tile (codes staged in LDS) plus the D-float scratch of the norm.
+size_t norm_tile_lds(int cols, int tile_rows, int D) {
+    return gemv_tile_lds_bytes(cols, tile_rows, true) + 4 * ((size_t)D + kChainPad);
+}
+
+// Plan of the fused q/k/v launch, or false (one launch per operation) where the three projections differ in dtype
+// or the plain GEMV would stream or the tile does not fit.
+bool qkv_plan(const Decoder* d, int l, GemvPlan* p, size_t* lds) {
+    const qh_tensor &wq = lt(d, l, L_WQ), &wk = lt(d, l, L_WK), &wv = lt(d, l, L_WV);
+    if (!d->fuse || wq.dtype != wk.dtype || wq.dtype != wv.dtype) return false;
+    *p = gemv_plan(wq.dtype, wq.cols, wq.rows);
+    *lds = norm_tile_lds(wq.cols, p->tile_rows, d->hp.dim);
+    return !p->stream && *lds <= kFuseLds;
+}
+
+hipError_t launch_qkv_norm(Decoder* d, int l, const GemvPlan& p, size_t lds, const NormAct& act, hipStream_t s) {
+    const qh_tensor &wq = lt(d, l, L_WQ), &wk = lt(d, l, L_WK), &wv = lt(d, l, L_WV);
+    const int T = p.tile_rows;
+    QkvSegs a{quants(wq), quants(wk), quants(wv), scales(wq), scales(wk), scales(wv), d->q, d->k, d->v,
+              wq.rows, wk.rows, wv.rows, (wq.rows + T - 1) / T, (wk.rows + T - 1) / T};
+    const unsigned grid = (unsigned)(a.tiles0 + a.tiles1 + (wv.rows + T - 1) / T);
+    const int nb = wq.cols / QK;
+    return plan_dispatch(wq.dtype, p, [&](auto dt, auto u, auto) {
+        hipLaunchKernelGGL((gemv_qkv_norm_kernel<decltype(dt)::value, decltype(u)::value>), dim3(grid), dim3(256), lds,
+                           s, a, act, nb, T, nb_magic(nb));
+    });
+}
+
+// x += W . (xq, xd) for one token: the GEMV tile kernel with the add in its epilogue, or (a streaming-size W, or
+// one launch per operation) GEMV into d->o and a separate add.
+hipError_t residual(Decoder* d, const qh_tensor& W, const int8_t* xq, const float* xd, hipStream_t s) {
+    const GemvPlan p = gemv_plan(W.dtype, W.cols, W.rows);
+    if (d->fuse && !p.stream) {
+        const int T = p.tile_rows, nb = W.cols / QK;
+        const unsigned grid = (unsigned)((W.rows + T - 1) / T);
+        const size_t lds = gemv_lds_bytes(W.cols, T, p.act_lds);
+        return plan_dispatch(W.dtype, p, [&](auto dt, auto u, auto xl) {
+            hipLaunchKernelGGL((gemv_residual_kernel<decltype(dt)::value, decltype(u)::value, decltype(xl)::value>),
+                               dim3(grid), dim3(256), lds, s, quants(W), scales(W), xq, xd, nb, W.rows, T,
+                               nb_magic(nb), d->x);
+        });
+    }
+    QH_TRY(launch_gemv(d->o, W, xq, xd, 0, W.rows, p, s));
+    hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((W.rows + 255) / 256)), dim3(256), 0, s, d->x, d->o,
+                       W.rows);
+    return hipGetLastError();
+}
+
+hipError_t norm_quant(Decoder* d, const float* w, float* normed, hipStream_t s) {
+    hipLaunchKernelGGL(norm_quant_kernel, dim3(1), dim3(256), 0, s, d->x, w, d->hp.dim, d->hp.norm_eps, d->qa, d->da,
+                       normed);
+    return hipGetLastError();
+}
+
+// rmsnorm (ffn_norm) of one token, gate / up, SwiGLU and quantization into qb / db.
+hipError_t gate_up(Decoder* d, int l, hipStream_t s) {
+    const qh_tensor &wg = lt(d, l, L_WG), &wu = lt(d, l, L_WU);
+    const int nb = wg.cols / QK;
+    const size_t lds = norm_tile_lds(wg.cols, 2 * QK, d->hp.dim);
+    if (d->fuse && wg.dtype == wu.dtype && lds <= kFuseLds) {
+        const unsigned grid = (unsigned)(wg.rows / QK);
+        const NormAct act = make_norm(d, false, lf(d, l, L_FFN_NORM));
+        if (wg.dtype == kQ8)
+            hipLaunchKernelGGL((gemv_swiglu_norm_kernel<kQ8, 8>), dim3(grid), dim3(256), lds, s, quants(wg),
+                               scales(wg), quants(wu), scales(wu), act, nb, nb_magic(nb), d->qb, d->db);
+        else
+            hipLaunchKernelGGL((gemv_swiglu_norm_kernel<kQ4, 8>), dim3(grid), dim3(256), lds, s, quants(wg),
+                               scales(wg), quants(wu), scales(wu), act, nb, nb_magic(nb), d->qb, d->db);
+        return hipGetLastError();
+    }
+    QH_TRY(norm_quant(d, lf(d, l, L_FFN_NORM), nullptr, s));
+    QH_TRY(launch_gemv(d->g, wg, d->qa, d->da, 0, wg.rows, gemv_plan(wg.dtype, wg.cols, wg.rows), s));
+    QH_TRY(launch_gemv(d->u, wu, d->qa, d->da, 0, wu.rows, gemv_plan(wu.dtype, wu.cols, wu.rows), s));
+    const long nblk = wg.rows / QK;
+    hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g, d->u,
+                       nblk, d->qb, d->db);
+    return hipGetLastError();
+}
+
+hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
     const qh_model_desc& hp = d->hp;
-    const int D = hp.dim, F = hp.ffn_dim, hd = hp.head_dim, qd = hp.n_heads * hd, kvd = hp.n_kv_heads * hd;
-    const size_t layer_kv = (size_t)hp.ctx_len * kvd;
+    const size_t layer_k = (size_t)hp.ctx_len * hp.n_kv_heads * hp.head_dim;
+    const size_t layer_v = (size_t)v_ctx(hp.ctx_len) * hp.n_kv_heads * hp.head_dim;
+    const dim3 grid(hp.n_heads, n);
+    if (hp.head_dim == 64)
+        hipLaunchKernelGGL(attention_kernel<64>, grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
+                           bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
+                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status);
+    else
+        hipLaunchKernelGGL(attention_kernel<128>, grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
+                           bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
+                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status);
+    return hipGetLastError();
+}
+
+// One decode step's layers for the token in d->tokens[0], from its embedding. Leaves the final normed hidden state
+// in d->hidden and its quantization in qa / da for the head.
+hipError_t decode_layers(Decoder* d, hipStream_t s) {
+    const qh_model_desc& hp = d->hp;
     for (int l = 0; l < hp.n_layers; ++l) {
-        hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(n), dim3(256), 0, s, d->x, l == 0 ? nullptr : d->o,
-                           lf(d, l, L_ATTN_NORM), D, hp.norm_eps, d->xq, d->xd, nullptr);
-        QH_TRY(hipGetLastError());
-        QH_TRY(linear(d->q, lt(d, l, L_WQ), d->xq, d->xd, n, s));
-        QH_TRY(linear(d->k, lt(d, l, L_WK), d->xq, d->xd, n, s));
-        QH_TRY(linear(d->v, lt(d, l, L_WV), d->xq, d->xd, n, s));
-        hipLaunchKernelGGL(bias_rope_kv_kernel, dim3(n), dim3(256), 0, s, d->q, d->k, d->v,
-                           hp.qkv_bias ? lf(d, l, L_BQ) : nullptr, hp.qkv_bias ? lf(d, l, L_BK) : nullptr,
-                           hp.qkv_bias ? lf(d, l, L_BV) : nullptr, d->cs, d->pos, hp.n_heads, hp.n_kv_heads, hd,
-                           d->kc + l * layer_kv, d->vc + l * layer_kv);
-        QH_TRY(hipGetLastError());
-        hipLaunchKernelGGL(attention_kernel, dim3(hp.n_heads, n), dim3(256), 0, s, d->q, d->kc + l * layer_kv,
-                           d->vc + l * layer_kv, d->pos, hp.n_heads, hp.n_kv_heads, hd, d->att);
-        QH_TRY(hipGetLastError());
-        QH_TRY(launch_quantize_q8(d->att, n, qd, d->xq, d->xd, s));
-        QH_TRY(linear(d->o, lt(d, l, L_WO), d->xq, d->xd, n, s));
+        GemvPlan p;
+        size_t lds = 0;
+        if (qkv_plan(d, l, &p, &lds)) {
+            QH_TRY(launch_qkv_norm(d, l, p, lds, make_norm(d, l == 0, lf(d, l, L_ATTN_NORM)), s));
+        } else {
+            if (l == 0)
+                QH_TRY(embed(d, d->tokens, 1, s));
+            else
+                QH_TRY(norm_quant(d, lf(d, l, L_ATTN_NORM), nullptr, s));
+            const qh_tensor &wq = lt(d, l, L_WQ), &wk = lt(d, l, L_WK), &wv = lt(d, l, L_WV);
+            QH_TRY(launch_gemv(d->q, wq, d->qa, d->da, 0, wq.rows, gemv_plan(wq.dtype, wq.cols, wq.rows), s));
+            QH_TRY(launch_gemv(d->k, wk, d->qa, d->da, 0, wk.rows, gemv_plan(wk.dtype, wk.cols, wk.rows), s));
+            QH_TRY(launch_gemv(d->v, wv, d->qa, d->da, 0, wv.rows, gemv_plan(wv.dtype, wv.cols, wv.rows), s));
+        }
+        QH_TRY(attention(d, l, 1, s));
+        QH_TRY(residual(d, lt(d, l, L_WO), d->qb, d->db, s));
+        QH_TRY(gate_up(d, l, s));
+        QH_TRY(residual(d, lt(d, l, L_WD), d->qb, d->db, s));
+    }
+    return norm_quant(d, final_norm(d), d->hidden, s);
+}
+
+// All layers for a chunk of n tokens whose embeddings are in d->x[0..n) and normed inputs in qa / da, positions
+// from *d->pos. Leaves the last layer's down projection in d->o (not yet added to the residual stream).
+hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
+    const qh_model_desc& hp = d->hp;
+    const int D = hp.dim, F = hp.ffn_dim;
+    for (int l = 0; l < hp.n_layers; ++l) {
+        if (l > 0) {
+            hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(n), dim3(256), 0, s, d->x, d->o, lf(d, l, L_ATTN_NORM),
+                               D, hp.norm_eps, d->qa, d->da, nullptr);
+            QH_TRY(hipGetLastError());
+        }
+        const qh_tensor &wq = lt(d, l, L_WQ), &wk = lt(d, l, L_WK), &wv = lt(d, l, L_WV);
+        QH_TRY(launch_matmul(d->q, wq.rows, wq, d->qa, d->da, n, 0, wq.rows, s));
+        QH_TRY(launch_matmul(d->k, wk.rows, wk, d->qa, d->da, n, 0, wk.rows, s));
+        QH_TRY(launch_matmul(d->v, wv.rows, wv, d->qa, d->da, n, 0, wv.rows, s));
+        QH_TRY(attention(d, l, n, s));
+        const qh_tensor& wo = lt(d, l, L_WO);
+        QH_TRY(launch_matmul(d->o, wo.rows, wo, d->qb, d->db, n, 0, wo.rows, s));
         hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(n), dim3(256), 0, s, d->x, d->o, lf(d, l, L_FFN_NORM), D,
-                           hp.norm_eps, d->xq, d->xd, nullptr);
+                           hp.norm_eps, d->qa, d->da, nullptr);
         QH_TRY(hipGetLastError());
-        QH_TRY(linear(d->g, lt(d, l, L_WG), d->xq, d->xd, n, s));
-        QH_TRY(linear(d->u, lt(d, l, L_WU), d->xq, d->xd, n, s));
-        const long nf = (long)n * F;
-        hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((nf + 255) / 256)), dim3(256), 0, s, d->g, d->u, nf, d->hbuf);
+        const qh_tensor &wg = lt(d, l, L_WG), &wu = lt(d, l, L_WU), &wd = lt(d, l, L_WD);
+        QH_TRY(launch_matmul(d->g, wg.rows, wg, d->qa, d->da, n, 0, wg.rows, s));
+        QH_TRY(launch_matmul(d->u, wu.rows, wu, d->qa, d->da, n, 0, wu.rows, s));
+        const long nblk = (long)n * F / QK;
+        hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g,
+                           d->u, nblk, d->qb, d->db);
         QH_TRY(hipGetLastError());
-        QH_TRY(launch_quantize_q8(d->hbuf, n, F, d->xq, d->xd, s));
-        QH_TRY(linear(d->o, lt(d, l, L_WD), d->xq, d->xd, n, s));
+        QH_TRY(launch_matmul(d->o, wd.rows, wd, d->qb, d->db, n, 0, wd.rows, s));
     }
     return hipSuccess;
 }
 
-// Final residual add, norm and quantization of row `row` of d->x, then the head; top_k > 0 uses the shortlist.
-hipError_t run_head(Decoder* d, int row, int top_k, hipStream_t s) {
-    const qh_model_desc& hp = d->hp;
-    const int D = hp.dim;
-    float* xr = d->x + (size_t)row * D;
-    float* orow = d->o + (size_t)row * D;
-    hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(1), dim3(256), 0, s, xr, orow,
-                       static_cast<const float*>(d->t[T_NORM].data), D, hp.norm_eps, d->xq, d->xd, d->hidden);
-    QH_TRY(hipGetLastError());
+// The head on the quantized final hidden state in qa / da; top_k > 0 uses the shortlist.
+hipError_t run_head(Decoder* d, int top_k, hipStream_t s) {
     const qh_tensor& h8 = d->t[T_EMBED];
     if (top_k > 0 && head4(d).data) {
-        qh_head_query q{top_k, hp.vocab_size, nullptr, 0};
+        qh_head_query q{top_k, d->hp.vocab_size, nullptr, 0};
         qh_head_out out{d->logits, d->coarse, d->upper, d->rows, d->stats};
-        return launch_shortlist_head(h8, head4(d), head_err(d), d->xq, d->xd, q, out, d->head_ws, s);
+        return launch_shortlist_head(h8, head4(d), head_err(d), d->qa, d->da, q, out, d->head_ws, s);
     }
-    QH_TRY(launch_gemv(d->logits, h8, d->xq, d->xd, 0, h8.rows, gemv_plan(h8.dtype, h8.cols, h8.rows), s));
-    return launch_argmax(d->logits, hp.vocab_size, d->top1_full, d->am_ws, s);
+    QH_TRY(launch_gemv(d->logits, h8, d->qa, d->da, 0, h8.rows, gemv_plan(h8.dtype, h8.cols, h8.rows), s));
+    return launch_argmax(d->logits, d->hp.vocab_size, d->top1_full, d->am_ws, s);
 }
+
 
 }  // namespace
 
@@ -375,33 +992,37 @@ hipError_t run_head(Decoder* d, int row, int top_k, hipStream_t s) {
 int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tensors, Decoder** out) {
     auto* d = new Decoder();
     d->hp = *hp;
+    const char* fuse = getenv("QH_DECODER_FUSE");
+    d->fuse = !(fuse && strcmp(fuse, "0") == 0);
     d->t.assign(tensors, tensors + n_tensors);
     const int D = hp->dim, F = hp->ffn_dim, V = hp->vocab_size, hd = hp->head_dim;
     const size_t kvd = (size_t)hp->n_kv_heads * hd;
     const size_t kv_bytes = (size_t)hp->n_layers * hp->ctx_len * kvd * 2;
+    const size_t v_bytes = (size_t)hp->n_layers * v_ctx(hp->ctx_len) * kvd * 2;
     const int wide = D > F ? D : F;
     hipError_t e = hipSuccess;
     auto A = [&](void** p, size_t b) {
         if (e == hipSuccess) e = dalloc(d, p, b);
     };
     A((void**)&d->kc, kv_bytes);
-    A((void**)&d->vc, kv_bytes);
+    A((void**)&d->vc, v_bytes);
     A((void**)&d->cs, sizeof(float) * (size_t)hp->ctx_len * hd);
     A((void**)&d->x, sizeof(float) * kChunk * D);
     A((void**)&d->o, sizeof(float) * kChunk * D);
     A((void**)&d->q, sizeof(float) * kChunk * D);
     A((void**)&d->k, sizeof(float) * kChunk * kvd);
     A((void**)&d->v, sizeof(float) * kChunk * kvd);
-    A((void**)&d->att, sizeof(float) * kChunk * D);
     A((void**)&d->g, sizeof(float) * kChunk * F);
     A((void**)&d->u, sizeof(float) * kChunk * F);
-    A((void**)&d->hbuf, sizeof(float) * kChunk * F);
     A((void**)&d->hidden, sizeof(float) * D);
-    A((void**)&d->xq, (size_t)kChunk * wide);
-    A((void**)&d->xd, sizeof(float) * kChunk * (wide / QK));
+    A((void**)&d->qa, (size_t)kChunk * wide);
+    A((void**)&d->qb, (size_t)kChunk * wide);
+    A((void**)&d->da, sizeof(float) * kChunk * (wide / QK));
+    A((void**)&d->db, sizeof(float) * kChunk * (wide / QK));
     A((void**)&d->tokens, sizeof(int32_t) * kChunk);
     A((void**)&d->pos, 256);
     A((void**)&d->n_out, 256);
+    A((void**)&d->status, 256);
     A((void**)&d->logits, sizeof(float) * V);
     A((void**)&d->coarse, sizeof(float) * V);
     A((void**)&d->upper, sizeof(float) * V);
@@ -427,8 +1048,9 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
             cs[((size_t)p * half + i) * 2 + 1] = sinf(angle);
         }
     e = hipMemcpy(d->cs, cs.data(), sizeof(float) * cs.size(), hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemset(d->n_out, 0, 256);
-    if (e == hipSuccess) e = hipMemset(d->pos, 0, 256);
+    for (int* p : {d->n_out, d->pos, d->status})
+        if (e == hipSuccess) e = hipMemset(p, 0, 256);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         decoder_destroy(d);
         return check_hip(e, "qh_decoder_create upload");
@@ -445,33 +1067,30 @@ void decoder_destroy(Decoder* d) {
 
 hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, int top_k, hipStream_t s) {
     const qh_model_desc& hp = d->hp;
-    const qh_tensor& emb = d->t[T_EMBED];
-    const int8_t* eq = static_cast<const int8_t*>(emb.data);
-    const uint16_t* es = reinterpret_cast<const uint16_t*>(eq + (size_t)emb.rows * emb.cols);
+    const int D = hp.dim;
+    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, s, d->status, 0);
+    QH_TRY(hipGetLastError());
     int last = 0;
     for (int c0 = 0; c0 < n; c0 += kChunk) {
         const int m = n - c0 < kChunk ? n - c0 : kChunk;
-        hipLaunchKernelGGL(set_pos_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + c0);
+        hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + c0);
         QH_TRY(hipGetLastError());
-        hipLaunchKernelGGL(embed_kernel, dim3(m), dim3(256), 0, s, tokens + c0, eq, es, hp.dim, d->x);
-        QH_TRY(hipGetLastError());
-        QH_TRY(run_layers(d, m, s));
+        QH_TRY(embed(d, tokens + c0, m, s));
+        QH_TRY(prefill_layers(d, m, s));
         last = m - 1;
     }
-    QH_TRY(run_head(d, last, top_k, s));
-    hipLaunchKernelGGL(set_pos_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + n);
+    // final residual add, norm and quantization of the last token only, then the head
+    hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(1), dim3(256), 0, s, d->x + (size_t)last * D,
+                       d->o + (size_t)last * D, final_norm(d), D, hp.norm_eps, d->qa, d->da, d->hidden);
+    QH_TRY(hipGetLastError());
+    QH_TRY(run_head(d, top_k, s));
+    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + n);
     return hipGetLastError();
 }
 
 hipError_t decoder_step(Decoder* d, int top_k, hipStream_t s) {
-    const qh_model_desc& hp = d->hp;
-    const qh_tensor& emb = d->t[T_EMBED];
-    const int8_t* eq = static_cast<const int8_t*>(emb.data);
-    const uint16_t* es = reinterpret_cast<const uint16_t*>(eq + (size_t)emb.rows * emb.cols);
-    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, d->tokens, eq, es, hp.dim, d->x);
-    QH_TRY(hipGetLastError());
-    QH_TRY(run_layers(d, 1, s));
-    QH_TRY(run_head(d, 0, top_k, s));
+    QH_TRY(decode_layers(d, s));
+    QH_TRY(run_head(d, top_k, s));
     const bool sl = top_k > 0 && head4(d).data;
     hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, sl ? d->stats : nullptr, d->top1_full, d->tokens,
                        d->pos, d->n_out, d->out, d->out_cap);
@@ -481,7 +1100,7 @@ hipError_t decoder_step(Decoder* d, int top_k, hipStream_t s) {
 hipError_t decoder_begin(Decoder* d, int top_k, int32_t* out, int out_cap, hipStream_t s) {
     d->out = out;
     d->out_cap = out_cap;
-    hipLaunchKernelGGL(set_pos_kernel, dim3(1), dim3(1), 0, s, d->n_out, 0);
+    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, s, d->n_out, 0);
     QH_TRY(hipGetLastError());
     const bool sl = top_k > 0 && head4(d).data;
     hipLaunchKernelGGL(first_token_kernel, dim3(1), dim3(1), 0, s, sl ? d->stats : nullptr, d->top1_full, d->tokens,
@@ -494,8 +1113,8 @@ int decoder_ctx(const Decoder* d) { return d->hp.ctx_len; }
 void decoder_views(Decoder* d, qh_decoder_state* v) {
     v->logits = d->logits;
     v->hidden = d->hidden;
-    v->xq = d->xq;
-    v->xd = d->xd;
+    v->xq = d->qa;
+    v->xd = d->da;
     v->stats = d->stats;
     v->top1_full = d->top1_full;
     v->pos = d->pos;
@@ -503,6 +1122,7 @@ void decoder_views(Decoder* d, qh_decoder_state* v) {
     v->token = d->tokens;
     v->kcache = d->kc;
     v->vcache = d->vc;
+    v->status = d->status;
 }
 
 }  // namespace qh

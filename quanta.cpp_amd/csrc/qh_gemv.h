@@ -1,0 +1,175 @@
+// One workgroup's tile of the Q8_0 / Q4_0 integer-dot GEMV (reference ops_ref.cpp:85-120), shared by the plain
+// GEMV kernel and the decoder's fused kernels (projection + residual + norm, gate/up + SwiGLU).
+//
+// A tile is a run of consecutive rows; in the .qnt layout their quants are one contiguous byte range, streamed
+// with coalesced 16-byte loads (thread t takes chunks t, t+256, ...). A Q8_0 block is two chunks (a lane pair,
+// combined with one DPP swap), a Q4_0 block is one chunk. Each block's exact int32 dot becomes
+// p = float(s) * f16(scale) (one rounded multiply) parked in LDS at [row][block]; after one barrier, thread r runs
+// row r's serial chain acc = fma(p_b, dx_b, acc) over the blocks in order, which is the reference's float
+// association, so the result is bit-identical. Every load of a pass is issued before the first wait; longer tiles
+// prefetch the next pass while computing the current one.
+//
+// PAIR tiles hold the same rows of two matrices of one shape (gate and up): virtual rows [0, n) come from the
+// first matrix and [n, 2n) from the second, so one round trip covers both.
+#pragma once
+
+#include <limits.h>
+
+#include "qh_device.h"
+
+namespace qh {
+
+// Serial chain acc = fma(p[b], dx[b], acc) for b = 0 .. nb-1 over LDS operands (the reference's order).
+__device__ __forceinline__ float chain_lds(const float* p, const float* dx, int nb) {
+    float acc = 0.0f;
+    for (int b = 0; b < nb; ++b) acc = __builtin_fmaf(p[b], dx[b], acc);
+    return acc;
+}
+
+// One pass of a workgroup: U chunks of 16 bytes per thread, the block scale of each chunk and, unless the
+// activation is staged in LDS (XL), the activation bytes the chunk pairs with. The chunk index is clamped
+// into the tile, so every load is unconditional and all of them go out back to back.
+template <int DT, int U, bool XL, bool PAIR = false>
+struct GemvPass {
+    uint4 w[U];
+    uint4 xa[XL ? 1 : U];
+    uint4 xb[(XL || DT == kQ8) ? 1 : U];
+    uint16_t sc[U];
+    uint32_t rt[U], b[U];
+
+    // split: first chunk of the second matrix (PAIR only); base2 / sbase2 point at its tile.
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ base, const uint16_t* __restrict__ sbase,
+                                         const uint8_t* __restrict__ base2, const uint16_t* __restrict__ sbase2,
+                                         int split, const int8_t* __restrict__ xq, int c0, int last, int nb,
+                                         uint32_t nb_magic) {
+        constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int c = min(c0 + j * 256 + (int)threadIdx.x, last);
+            const uint32_t g = (uint32_t)c / kChunksPerBlock;  // block index within the tile
+            rt[j] = nb == 1 ? g : div_magic(g, nb_magic);      // tile row
+            b[j] = g - rt[j] * (uint32_t)nb;                    // block within the row
+            if constexpr (PAIR) {
+                const bool second = c >= split;
+                const int cc = second ? c - split : c;
+                w[j] = load16((second ? base2 : base) + (size_t)cc * 16);
+                sc[j] = (second ? sbase2 : sbase)[(uint32_t)cc / kChunksPerBlock];
+            } else {
+                w[j] = load16(base + (size_t)c * 16);
+                sc[j] = sbase[g];
+            }
+            if constexpr (!XL) {
+                if constexpr (DT == kQ8) {
+                    xa[j] = load16(xq + b[j] * QK + (c & 1) * 16);
+                } else {
+                    xa[j] = load16(xq + b[j] * QK);
+                    xb[j] = load16(xq + b[j] * QK + 16);
+                }
+            }
+        }
+    }
+
+    // Block products of the pass into LDS (only chunks below nchunks are stored). xs: LDS activation (XL).
+    __device__ __forceinline__ void products(float* prod, int pstride, int c0, int nchunks, const int8_t* xs) const {
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int c = c0 + j * 256 + (int)threadIdx.x;
+            if constexpr (DT == kQ8) {
+                const uint4 xv = XL ? *reinterpret_cast<const uint4*>(xs + b[j] * QK + (c & 1) * 16) : xa[XL ? 0 : j];
+                int s = dot16_i8(w[j], xv);
+                s += swap_pair(s);
+                if (c < nchunks && !(c & 1)) prod[rt[j] * pstride + b[j]] = (float)s * f16_to_f32(sc[j]);
+            } else {
+                const uint4 xlo = XL ? *reinterpret_cast<const uint4*>(xs + b[j] * QK) : xa[XL ? 0 : j];
+                const uint4 xhi = XL ? *reinterpret_cast<const uint4*>(xs + b[j] * QK + 16) : xb[XL ? 0 : j];
+                const int s = dot_q4_block(w[j], xlo, xhi);
+                if (c < nchunks) prod[rt[j] * pstride + b[j]] = (float)s * f16_to_f32(sc[j]);
+            }
+        }
+    }
+};
+
+// LDS bytes of a tile of tile_rows virtual rows (PAIR tiles count both matrices' rows).
+__host__ __device__ __forceinline__ size_t gemv_tile_lds_bytes(int cols, int tile_rows, bool xl) {
+    const int nb = cols / QK;
+    const size_t f = ((size_t)nb + (size_t)tile_rows * (nb + 1)) * 4;
+    return xl ? ((f + 15) & ~size_t(15)) + (size_t)cols : f;
+}
+
+// Stages the activation for a tile: its block scales into xds and, when the codes are read from LDS (XL), its codes
+// into xs, straight from the quantized activation in global memory. Issued right behind the first pass of weight
+// loads, so it arrives in the same round trip.
+struct GlobalAct {
+    const int8_t* __restrict__ xq;
+    const float* __restrict__ xd;
+    int nb;
+    template <bool XL>
+    __device__ __forceinline__ void fill(int8_t* xs, float* xds) const {
+        const int tid = (int)threadIdx.x, xch = nb * QK / 16;
+        uint4 xv = make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (XL) xv = load16(xq + min(tid, xch - 1) * 16);
+        const float dv = xd[min(tid, nb - 1)];
+        if (XL && tid < xch) reinterpret_cast<uint4*>(xs)[tid] = xv;
+        if (tid < nb) xds[tid] = dv;
+        if constexpr (XL)
+            for (int i = tid + 256; i < xch; i += 256) reinterpret_cast<uint4*>(xs)[i] = load16(xq + i * 16);
+        for (int i = tid + 256; i < nb; i += 256) xds[i] = xd[i];
+    }
+};
+
+// Rows [ra, ra + nrows) of W . x (and, PAIR, the same rows of W2 as virtual rows nrows .. 2*nrows-1) for one
+// workgroup of 256 threads. tile_rows: the virtual row capacity the LDS layout is sized for (>= the virtual rows).
+// Returns the value of virtual row threadIdx.x for threads below the virtual row count, 0 for the others.
+// smem: dynamic LDS of gemv_tile_lds_bytes(nb * 32, tile_rows, XL) bytes. act.fill<XL>(xs, xds) stages the
+// activation (codes in LDS when XL; it may use its own barriers, all 256 threads call it) after the first pass of
+// weight loads is issued; xq / xd are read per chunk when !XL. The LDS is free for reuse only after a barrier.
+template <int DT, int U, bool XL, bool PAIR = false, typename Act = GlobalAct>
+__device__ __forceinline__ float gemv_tile(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wscale,
+                                           const uint8_t* __restrict__ wq2, const uint16_t* __restrict__ wscale2,
+                                           const int8_t* __restrict__ xq, const float* __restrict__ xd, int nb,
+                                           int ra, int nrows, int tile_rows, uint32_t nb_magic, float* smem,
+                                           const Act& act) {
+    constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
+    constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
+    float* xds = smem;         // [nb] activation scales
+    float* prod = smem + nb;   // [tile_rows][nb + 1] block products
+    // [cols] codes (XL), 16-byte aligned after the products
+    int8_t* xs = reinterpret_cast<int8_t*>(smem) + ((((size_t)nb + (size_t)tile_rows * (nb + 1)) * 4 + 15) & ~size_t(15));
+    const int pstride = nb + 1;
+    const int tid = (int)threadIdx.x;
+    const int vrows = PAIR ? 2 * nrows : nrows;
+    const int nchunks = vrows * nb * kChunksPerBlock;
+    const int split = PAIR ? nrows * nb * kChunksPerBlock : INT_MAX;
+    const uint8_t* base = wq + (size_t)ra * nb * kBlockBytes;
+    const uint16_t* sbase = wscale + (size_t)ra * nb;
+    const uint8_t* base2 = PAIR ? wq2 + (size_t)ra * nb * kBlockBytes : nullptr;
+    const uint16_t* sbase2 = PAIR ? wscale2 + (size_t)ra * nb : nullptr;
+
+    GemvPass<DT, U, XL, PAIR> cur;
+    cur.load(base, sbase, base2, sbase2, split, xq, 0, nchunks - 1, nb, nb_magic);
+    act.template fill<XL>(xs, xds);
+    if constexpr (XL) __syncthreads();
+    for (int c0 = 0; c0 < nchunks; c0 += 256 * U) {
+        if (c0 + 256 * U < nchunks) {  // uniform: prefetch the next pass, then compute this one
+            GemvPass<DT, U, XL, PAIR> nxt;
+            nxt.load(base, sbase, base2, sbase2, split, xq, c0 + 256 * U, nchunks - 1, nb, nb_magic);
+            cur.products(prod, pstride, c0, nchunks, xs);
+            cur = nxt;
+        } else {
+            cur.products(prod, pstride, c0, nchunks, xs);
+        }
+    }
+    __syncthreads();
+    return tid < vrows ? chain_lds(prod + tid * pstride, xds, nb) : 0.0f;
+}
+
+template <int DT, int U, bool XL, bool PAIR = false>
+__device__ __forceinline__ float gemv_tile(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wscale,
+                                           const uint8_t* __restrict__ wq2, const uint16_t* __restrict__ wscale2,
+                                           const int8_t* __restrict__ xq, const float* __restrict__ xd, int nb,
+                                           int ra, int nrows, int tile_rows, uint32_t nb_magic, float* smem) {
+    return gemv_tile<DT, U, XL, PAIR>(wq, wscale, wq2, wscale2, xq, xd, nb, ra, nrows, tile_rows, nb_magic, smem,
+                                      GlobalAct{xq, xd, nb});
+}
+
+}  // namespace qh

@@ -1,21 +1,16 @@
 // Decode-side kernels: activation quantization (reference ops_ref.cpp:69-83) and the Q8_0 / Q4_0
 // integer-dot GEMV (reference ops_ref.cpp:85-120), for gfx950.
 //
-// GEMV data flow. A workgroup owns a tile of consecutive rows. In the .qnt layout the quants of those
-// rows are one contiguous byte range, so the workgroup streams it with coalesced 16-byte loads
-// (thread t takes chunks t, t+256, ...), independent of the row length. A Q8_0 block is two chunks
-// (a lane pair, combined with one DPP swap), a Q4_0 block is one chunk. Each block's exact int32 dot
-// is turned into p = float(s) * f16(scale) (one rounded multiply, order-free) and parked in LDS at
-// [row][block]. After one barrier, thread r runs row r's serial chain acc = fma(p_b, dx_b, acc) over
-// the blocks in order, which is the reference's float association, so the result is bit-identical.
-// Every load of a pass (weights, scales, the activation bytes each chunk pairs with, the activation scales)
-// is issued before the first wait, so a single-pass tile costs one memory round trip and one barrier;
-// longer tiles prefetch the next pass while computing the current one.
+// GEMV data flow: a workgroup owns a tile of consecutive rows (qh_gemv.h: coalesced 16-byte loads of the
+// tile's contiguous bytes, exact int32 block dots, one rounded product per block parked in LDS, then one serial
+// FMA chain per row in the reference's order). Small matrices use one tile per workgroup; vocabulary-sized
+// ones use the persistent streaming kernel below.
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
 #include "qh_device.h"
+#include "qh_gemv.h"
 #include "qh_internal.h"
 
 namespace qh {
@@ -46,66 +41,6 @@ hipError_t launch_quantize_q8(const float* x, int n_tok, int n, int8_t* q, float
     return hipGetLastError();
 }
 
-// Serial chain acc = fma(p[b], dx[b], acc) for b = 0 .. nb-1 over LDS operands (the reference's order).
-__device__ __forceinline__ float chain_lds(const float* p, const float* dx, int nb) {
-    float acc = 0.0f;
-    for (int b = 0; b < nb; ++b) acc = __builtin_fmaf(p[b], dx[b], acc);
-    return acc;
-}
-
-// One pass of a workgroup: U chunks of 16 bytes per thread, the block scale of each chunk and, unless the
-// activation is staged in LDS (XL), the activation bytes the chunk pairs with. The chunk index is clamped
-// into the tile, so every load is unconditional and all of them go out back to back.
-template <int DT, int U, bool XL>
-struct GemvPass {
-    uint4 w[U];
-    uint4 xa[XL ? 1 : U];
-    uint4 xb[(XL || DT == kQ8) ? 1 : U];
-    uint16_t sc[U];
-    uint32_t rt[U], b[U];
-
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ base, const uint16_t* __restrict__ sbase,
-                                         const int8_t* __restrict__ xq, int c0, int last, int nb, uint32_t nb_magic) {
-        constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
-#pragma unroll
-        for (int j = 0; j < U; ++j) {
-            const int c = min(c0 + j * 256 + (int)threadIdx.x, last);
-            const uint32_t g = (uint32_t)c / kChunksPerBlock;  // block index within the tile
-            rt[j] = nb == 1 ? g : div_magic(g, nb_magic);      // tile row
-            b[j] = g - rt[j] * (uint32_t)nb;                    // block within the row
-            w[j] = load16(base + (size_t)c * 16);
-            sc[j] = sbase[g];
-            if constexpr (!XL) {
-                if constexpr (DT == kQ8) {
-                    xa[j] = load16(xq + b[j] * QK + (c & 1) * 16);
-                } else {
-                    xa[j] = load16(xq + b[j] * QK);
-                    xb[j] = load16(xq + b[j] * QK + 16);
-                }
-            }
-        }
-    }
-
-    // Block products of the pass into LDS (only chunks below nchunks are stored). xs: LDS activation (XL).
-    __device__ __forceinline__ void products(float* prod, int pstride, int c0, int nchunks, const int8_t* xs) const {
-#pragma unroll
-        for (int j = 0; j < U; ++j) {
-            const int c = c0 + j * 256 + (int)threadIdx.x;
-            if constexpr (DT == kQ8) {
-                const uint4 xv = XL ? *reinterpret_cast<const uint4*>(xs + b[j] * QK + (c & 1) * 16) : xa[XL ? 0 : j];
-                int s = dot16_i8(w[j], xv);
-                s += swap_pair(s);
-                if (c < nchunks && !(c & 1)) prod[rt[j] * pstride + b[j]] = (float)s * f16_to_f32(sc[j]);
-            } else {
-                const uint4 xlo = XL ? *reinterpret_cast<const uint4*>(xs + b[j] * QK) : xa[XL ? 0 : j];
-                const uint4 xhi = XL ? *reinterpret_cast<const uint4*>(xs + b[j] * QK + 16) : xb[XL ? 0 : j];
-                const int s = dot_q4_block(w[j], xlo, xhi);
-                if (c < nchunks) prod[rt[j] * pstride + b[j]] = (float)s * f16_to_f32(sc[j]);
-            }
-        }
-    }
-};
-
 // XL = false: activation read with the weights (best for small, latency-bound matrices).
 // XL = true: activation staged once in LDS (best for large matrices, where per-chunk activation loads
 // would compete with the weight stream).
@@ -115,48 +50,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(float* __restrict__ out, cons
                                                    const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                    int nb, int r0, int r1, int tile_rows, uint32_t nb_magic) {
     extern __shared__ float smem[];
-    constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
-    constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
-    const int cols = nb * QK;
-    float* xds = smem;                                          // [nb] activation scales
-    float* prod = smem + nb;                                    // [tile_rows][nb + 1] block products
-    // [cols] codes (XL), 16-byte aligned after the products
-    int8_t* xs = reinterpret_cast<int8_t*>(smem) + ((((size_t)nb + (size_t)tile_rows * (nb + 1)) * 4 + 15) & ~size_t(15));
-    const int pstride = nb + 1;
-    const int tid = (int)threadIdx.x;
     const int ra = r0 + (int)blockIdx.x * tile_rows;
     const int nrows = min(tile_rows, r1 - ra);
-    const int nchunks = nrows * nb * kChunksPerBlock;
-    const uint8_t* base = wq + (size_t)ra * nb * kBlockBytes;
-    const uint16_t* sbase = wscale + (size_t)ra * nb;
-
-    GemvPass<DT, U, XL> cur;
-    cur.load(base, sbase, xq, 0, nchunks - 1, nb, nb_magic);
-    {
-        // Issued behind the first pass, so it arrives in the same round trip.
-        const int xch = cols / 16;
-        uint4 xv = make_uint4(0u, 0u, 0u, 0u);
-        if constexpr (XL) xv = load16(xq + min(tid, xch - 1) * 16);
-        const float dv = xd[min(tid, nb - 1)];
-        if (XL && tid < xch) reinterpret_cast<uint4*>(xs)[tid] = xv;
-        if (tid < nb) xds[tid] = dv;
-        if constexpr (XL)
-            for (int i = tid + 256; i < xch; i += 256) reinterpret_cast<uint4*>(xs)[i] = load16(xq + i * 16);
-        for (int i = tid + 256; i < nb; i += 256) xds[i] = xd[i];
-    }
-    if constexpr (XL) __syncthreads();
-    for (int c0 = 0; c0 < nchunks; c0 += 256 * U) {
-        if (c0 + 256 * U < nchunks) {  // uniform: prefetch the next pass, then compute this one
-            GemvPass<DT, U, XL> nxt;
-            nxt.load(base, sbase, xq, c0 + 256 * U, nchunks - 1, nb, nb_magic);
-            cur.products(prod, pstride, c0, nchunks, xs);
-            cur = nxt;
-        } else {
-            cur.products(prod, pstride, c0, nchunks, xs);
-        }
-    }
-    __syncthreads();
-    if (tid < nrows) out[ra + tid] = chain_lds(prod + tid * pstride, xds, nb);
+    const float v = gemv_tile<DT, U, XL>(wq, wscale, nullptr, nullptr, xq, xd, nb, ra, nrows, tile_rows, nb_magic,
+                                         smem);
+    if ((int)threadIdx.x < nrows) out[ra + threadIdx.x] = v;
 }
 
 // Streaming GEMV for large matrices (vocabulary-sized heads). The grid is persistent: workgroup g walks the
@@ -308,11 +206,7 @@ int device_cus() {
     return cus[dev];
 }
 
-size_t gemv_lds_bytes(int cols, int tile_rows, bool xl) {
-    const int nb = cols / QK;
-    const size_t f = ((size_t)nb + (size_t)tile_rows * (nb + 1)) * 4;
-    return xl ? ((f + 15) & ~size_t(15)) + (size_t)cols : f;
-}
+size_t gemv_lds_bytes(int cols, int tile_rows, bool xl) { return gemv_tile_lds_bytes(cols, tile_rows, xl); }
 
 static size_t gemv_stream_lds_bytes(int cols, int tile_rows) {
     const int nb = cols / QK;

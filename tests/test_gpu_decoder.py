@@ -7,7 +7,10 @@
   logits equal the oracle's decoder restatement, bit for bit;
 * the benchmark model (24 layers, vocab 151936): 512-token prompt, 256 greedy tokens equal the reference's `gen`
   stream (tests/golden/e2e_q4mix.npz), with each step's head rows and the exact logit of the chosen token;
-* one decode step captured in a HIP graph and replayed gives the same stream as eager steps.
+* one decode step captured in a HIP graph and replayed gives the same stream as eager steps;
+* head_dim 128, a context longer than one LDS stage of V rows, and the one-launch-per-operation path
+  (QH_DECODER_FUSE=0) all equal the oracle bit for bit;
+* a step past the context and an out-of-range prompt token raise the status bits and touch nothing out of bounds.
 """
 import os
 
@@ -42,6 +45,104 @@ def test_decoder_small_model_matches_reference_states(qh, gpu):
             break
         dec.step(top_k=1)
     assert (dec.outputs(n_gen) == g["out"]).all()
+
+
+def _steps_vs_oracle(oracle, orc, dec, ids, n_steps, full_every=0):
+    """Prefill `ids` on both, then n_steps greedy steps; every hidden state, logit and row count bit-equal."""
+    r = orc.forward_batch(ids, 0, top_k=1)
+    dec.prefill(ids, 0, top_k=1)
+    assert (bits(dec.hidden()) == bits(r["hidden"])).all(), "hidden state after the prefill"
+    assert (bits(dec.logits()) == bits(r["logits"])).all(), "logits after the prefill"
+    assert dec.stats()["n_rows"] == r["rows"]
+    dec.begin(n_steps + 1, top_k=1)
+    pos = len(ids)
+    tok = int(np.argmax(r["logits"]))
+    for step in range(n_steps):
+        top_k = 0 if full_every and step % full_every == full_every - 1 else 1
+        r = orc.forward(tok, pos, top_k=top_k)
+        dec.step(top_k=top_k)
+        assert (bits(dec.hidden()) == bits(r["hidden"])).all(), f"hidden state, step {step}"
+        assert (bits(dec.logits()) == bits(r["logits"])).all(), f"logits, step {step}"
+        if top_k:
+            assert dec.stats()["n_rows"] == r["rows"], step
+        else:
+            assert dec.top1_full() == oracle.argmax(r["logits"]), step
+        tok = oracle.argmax(r["logits"])
+        pos += 1
+    assert dec.status() == 0
+    return dec.outputs(n_steps + 1)
+
+
+def _narrow_hp(qnt, **kw):
+    base = dict(vocab_size=1024, dim=256, n_layers=2, n_heads=4, n_kv_heads=1, head_dim=64, ffn_dim=512)
+    base.update(kw)
+    return qnt.HParams(**base)
+
+
+def test_decoder_head_dim_128_equals_oracle(qh, oracle, gpu):
+    qnt = qnt_module()
+    hp = _narrow_hp(qnt, n_heads=2, n_kv_heads=1, head_dim=128)
+    tens = qnt.synthetic_q4mix(31, hp)
+    orc = oracle_decoder(oracle, hp, tens, ctx_len=256)
+    dec = qh.Decoder(hp, tens, ctx_len=256)
+    ids = np.random.default_rng(8).integers(0, hp.vocab_size, 45).astype(np.int32)
+    _steps_vs_oracle(oracle, orc, dec, ids, 6, full_every=3)
+
+
+def test_decoder_context_beyond_one_v_stage(qh, oracle, gpu):
+    # head_dim 64 stages 768 V rows in LDS at a time: a 1000-token prompt puts prefill chunks and decode steps past it
+    qnt = qnt_module()
+    hp = _narrow_hp(qnt)
+    tens = qnt.synthetic_q4mix(37, hp)
+    orc = oracle_decoder(oracle, hp, tens, ctx_len=1100)
+    dec = qh.Decoder(hp, tens, ctx_len=1100)
+    ids = np.random.default_rng(12).integers(0, hp.vocab_size, 1000).astype(np.int32)
+    _steps_vs_oracle(oracle, orc, dec, ids, 6)
+
+
+def test_decoder_fused_equals_one_launch_per_op(qh, oracle, gpu, monkeypatch):
+    qnt = qnt_module()
+    hp = qnt.HParams(vocab_size=4096, n_layers=2)
+    tens = qnt.synthetic_q4mix(41, hp)
+    ids = np.random.default_rng(13).integers(0, hp.vocab_size, 70).astype(np.int32)
+    outs = []
+    for fuse in ("1", "0"):
+        monkeypatch.setenv("QH_DECODER_FUSE", fuse)
+        orc = oracle_decoder(oracle, hp, tens, ctx_len=256)
+        dec = qh.Decoder(hp, tens, ctx_len=256)
+        outs.append(_steps_vs_oracle(oracle, orc, dec, ids, 10, full_every=4))
+        dec.close()
+    assert (outs[0] == outs[1]).all()
+
+
+def test_decoder_status_past_context_and_bad_token(qh, gpu):
+    qnt = qnt_module()
+    hp = _narrow_hp(qnt)
+    tens = qnt.synthetic_q4mix(43, hp)
+    ids = np.random.default_rng(14).integers(0, hp.vocab_size, 40).astype(np.int32)
+    wide = qh.Decoder(hp, tens, ctx_len=128)
+    wide.prefill(ids, 0, top_k=1)
+    wide.begin(13)
+    for _ in range(12):
+        wide.step(top_k=1)
+    dec = qh.Decoder(hp, tens, ctx_len=48)
+    dec.prefill(ids, 0, top_k=1)
+    dec.begin(13)
+    for s in range(12):
+        dec.step(top_k=1)
+        assert dec.status() == (0 if 40 + s < 48 else 1), s
+    assert dec.position() == 52
+    # the steps inside the context are the same as with room to spare
+    assert (dec.outputs(9) == wide.outputs(9)).all()
+    bad = ids.copy()
+    bad[5] = hp.vocab_size
+    dec.prefill(bad, 0, top_k=1)
+    assert dec.status() == 2
+    bad[5] = -1
+    dec.prefill(bad, 0, top_k=1)
+    assert dec.status() == 2
+    dec.prefill(ids, 0, top_k=1)
+    assert dec.status() == 0
 
 
 def test_decoder_equals_oracle_long_prompt_and_full_head(qh, oracle, gpu):
