@@ -1,22 +1,24 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized matmul hot path on one MI355X.
 
-Headline workload (one JSON line on stdout): GPTQ-style symmetric 4-bit (Q4_0) decode GEMV, batch 1,
-at the Qwen2.5-0.5B MLP shapes gate/up 4864x896 and down 896x4864. A "step" is one pass over a rotation
-of distinct weight copies (>= 1 GiB, four times the 256 MB Infinity Cache) so every byte comes from
-HBM; the pass is captured once in a HIP graph and replayed. `value` is whole-job algorithmic GB/s:
-(0.5625*N*K weight+scale bytes + 1.125*K activation bytes + 4*N output bytes) per GEMV, summed over the
-timed steps, divided by the time between two events on the launch stream.
+Headline (one JSON line on stdout): end-to-end greedy decode of a random-init q4mix model with Qwen2.5-0.5B shapes
+(configuration 5): a 512-token prompt in 32-token prefill chunks, then 256 greedy decode steps, every kernel of
+the path hand-written HIP (Q8_0 attention / Q4_0 MLP GEMVs with their norms fused, attention, Exact Shortlist
+Head). A "step" is one decode step (one token): one replay of a HIP graph holding the captured step. `value` is
+decode tokens/s between two HIP events on the replay stream; the generated stream is checked against the reference
+engine's own (tests/golden/e2e_q4mix.npz). Prefill tok/s is in `config`.
 
-`roofline` covers the same kernel: algorithmic bytes per launch / average launch duration (the timed
-region divided by the launch count) against the 8 TB/s HBM peak; `traffic` is the measured HBM bytes
-per launch when profiles/q4_gemv_traffic.txt holds rocprofv3 counter readings, else null.
-`cpu_baseline` times the reference's own CPU kernel (built from its sources, oracle/_ref) or, where
-that build is absent, the oracle's C restatement, on the host cores for a bounded sample.
-`extra` adds the other measured configurations: Q8_0 GEMV shapes, hot-cache GEMVs, prefill matmuls at
-M = 32/128/512 and the Exact Shortlist Head against the full 8-bit head.
+`roofline` covers the decode step's weight GEMV at its real shapes: Q4_0 gate/up 4864x896 + down 896x4864, batch 1,
+over a rotation of distinct weight copies (>= 1 GiB, four times the 256 MB Infinity Cache) so every byte comes
+from HBM; algorithmic bytes per launch (0.5625*N*K weights+scales + 1.125*K activation + 4*N output) / average
+launch duration, from HIP events around the graph-replayed rotation. `traffic` is the measured HBM bytes per launch
+when profiles/q4_gemv_traffic.txt holds rocprofv3 counter readings, else null.
+`cpu_baseline` runs the reference engine itself (built from its sources, oracle/_ref) on the host cores over a
+bounded sample of the same workload, or the oracle's C restatement where that build is absent.
+`extra` adds the other configurations: Q8_0 / Q4_0 GEMV shapes cold and hot, prefill matmuls at M = 32/128/512,
+the Exact Shortlist Head against the full 8-bit head, and the reference CPU GEMV.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu] [--e2e-only]
 """
 import argparse
 import importlib.util
@@ -217,22 +219,18 @@ def e2e_model():
     return hp, qnt.synthetic_q4mix(5, hp)
 
 
-def e2e_bench(qh, torch, hp, tens, steps=256, n_prompt=512, check=True):
-    """End-to-end greedy generation on the q4mix Qwen2.5-0.5B-shaped model: prefill of a 512-token prompt in 32-token
-    chunks, then `steps` decode steps, each one HIP-graph replay of a captured step (the token is fed back on the
-    device). Checks the stream against the reference's (tests/golden/e2e_q4mix.npz) when it is the same workload."""
+def e2e_bench(qh, torch, hp, tens, steps=256, warmup=3, n_prompt=512, check=True):
+    """End-to-end greedy generation on the q4mix Qwen2.5-0.5B-shaped model (configuration 5): a 512-token prompt in
+    32-token prefill chunks, then `steps` greedy decode steps, each one replay of a HIP graph holding one captured
+    decode step (the chosen token is fed back on the device). A warm-up run of `warmup` steps precedes the timed run;
+    the timed stream (positions 512 ..) is checked against the reference engine's (tests/golden/e2e_q4mix.npz)."""
     dec = qh.Decoder(hp, tens, ctx_len=4096)
     ids = np.random.default_rng(9).integers(0, hp.vocab_size, n_prompt).astype(np.int32)
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    dec.prefill(ids, 0, top_k=1)  # warm-up
-    torch.cuda.synchronize()
-    e0, e1 = ev(), ev()
-    e0.record()
+    cap = steps + 1
+    # warm-up run: prefill, capture the step, a few replays
     dec.prefill(ids, 0, top_k=1)
-    e1.record()
-    torch.cuda.synchronize()
-    prefill_s = e0.elapsed_time(e1) / 1e3
-    dec.begin(steps + 1)
+    dec.begin(cap)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     graph = torch.cuda.CUDAGraph()
@@ -240,43 +238,47 @@ def e2e_bench(qh, torch, hp, tens, steps=256, n_prompt=512, check=True):
         with torch.cuda.graph(graph, stream=side):
             dec.step(top_k=1)
     torch.cuda.current_stream().wait_stream(side)
+    for _ in range(min(warmup, steps)):
+        graph.replay()
     torch.cuda.synchronize()
-    e0, e1 = ev(), ev()
+    # timed run: prefill, then `steps` replays
+    e0, e1, e2 = ev(), ev(), ev()
     e0.record()
+    dec.prefill(ids, 0, top_k=1)
+    e1.record()
+    dec.begin(cap)
+    torch.cuda.synchronize()
+    e2.record()
     for _ in range(steps):
         graph.replay()
-    e1.record()
+    e3 = ev()
+    e3.record()
     torch.cuda.synchronize()
-    decode_s = e0.elapsed_time(e1) / 1e3
-    out = dec.outputs(steps + 1)
-    parity = None
-    gpath = os.path.join(ROOT, "tests", "golden", "e2e_q4mix.npz")
-    if check and steps >= 255 and n_prompt == 512 and os.path.exists(gpath):
-        g = np.load(gpath, allow_pickle=False)
-        parity = bool((out[:256] == g["out"]).all())
-        if not parity:
-            raise SystemExit("bench: GPU token stream differs from the reference's")
-    layer_bytes = sum(_layer_bytes(hp))
-    screen_bytes = hp.vocab_size * (hp.dim // 2 + 2 * (hp.dim // 32) * 2)
+    prefill_s = e0.elapsed_time(e1) / 1e3
+    decode_s = e2.elapsed_time(e3) / 1e3
+    out = dec.outputs(cap)
+    status = dec.status()
     dec.close()
     del graph
+    if status:
+        raise SystemExit(f"bench: decoder status {status}")
+    parity = None
+    gpath = os.path.join(ROOT, "tests", "golden", "e2e_q4mix.npz")
+    if check and n_prompt == 512 and os.path.exists(gpath):
+        g = np.load(gpath, allow_pickle=False)
+        n = min(len(g["out"]), steps)
+        parity = bool((out[:n] == g["out"][:n]).all())
+        if not parity:
+            raise SystemExit("bench: GPU token stream differs from the reference engine's")
     return {"prefill_tok_per_s": n_prompt / prefill_s, "prefill_ms": prefill_s * 1e3,
             "decode_tok_per_s": steps / decode_s, "decode_ms_per_token": decode_s / steps * 1e3,
-            "decode_weight_GBps": (layer_bytes + screen_bytes) / (decode_s / steps) / 1e9,
             "stream_equals_reference": parity, "tokens": int(steps), "prompt": int(n_prompt)}
 
 
-def _layer_bytes(hp):
-    """Weight bytes one decode step streams through the layers (Q8_0 attention, Q4_0 MLP)."""
-    qd, kvd = hp.n_heads * hp.head_dim, hp.n_kv_heads * hp.head_dim
-    for _ in range(hp.n_layers):
-        yield 1.0625 * (qd * hp.dim + 2 * kvd * hp.dim + hp.dim * qd)
-        yield 0.5625 * (3 * hp.ffn_dim * hp.dim)
-
-
-def e2e_cpu_baseline(hp, tens, n_prompt=64, n_gen=16):
-    """The reference engine's own `gen --greedy` flow (oracle/_ref) on the host cores, bounded: a 64-token prompt and
-    16 greedy tokens of the same model. Decode rate from the difference of a 16-token and a 1-token run."""
+def e2e_cpu_baseline(hp, tens, n_prompt=512, n_gen=16):
+    """The reference engine itself (oracle/_ref, built from its sources) on the host cores, bounded sample of the same
+    workload: Model::forward_batch over the 512-token prompt (32-token chunks), then n_gen greedy Model::forward
+    decode steps with the Exact Shortlist Head (top_k = 1), each timed."""
     sys.path.insert(0, ROOT)
     import ctypes as C
     import oracle as orc
@@ -287,27 +289,35 @@ def e2e_cpu_baseline(hp, tens, n_prompt=64, n_gen=16):
     L.ref_model_load.restype = C.c_void_p
     L.ref_model_load.argtypes = [C.c_char_p, C.c_int, C.c_int]
     L.ref_model_free.argtypes = [C.c_void_p]
-    L.ref_gen.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    L.ref_model_forward.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+                                    C.c_void_p]
+    L.ref_model_forward_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                          C.c_void_p, C.c_void_p]
     path = os.path.join("/tmp", f"quanta_bench_q4mix_{os.getpid()}.qnt")
     qnt.write_qnt(path, hp, tens)
     threads = max(1, min(16, os.cpu_count() or 1))
     try:
         m = L.ref_model_load(path.encode(), 4096, threads)
+        if not m:
+            return None
         ids = np.random.default_rng(9).integers(0, hp.vocab_size, n_prompt).astype(np.int32)
-        out = np.zeros(n_gen, np.int32)
-        L.ref_gen(m, ids.ctypes.data, n_prompt, 1, out.ctypes.data, None, None)  # warm-up (page-in)
+        logits = np.zeros(hp.vocab_size, np.float32)
         t0 = time.perf_counter()
-        L.ref_gen(m, ids.ctypes.data, n_prompt, 1, out.ctypes.data, None, None)
+        L.ref_model_forward_batch(m, ids.ctypes.data, n_prompt, 0, 1, logits.ctypes.data, None, None, None)
         t1 = time.perf_counter()
-        L.ref_gen(m, ids.ctypes.data, n_prompt, n_gen, out.ctypes.data, None, None)
+        tok = int(np.argmax(logits))
+        for i in range(n_gen):
+            L.ref_model_forward(m, tok, n_prompt + i, 1, logits.ctypes.data, None, None, None)
+            tok = int(np.argmax(logits))
         t2 = time.perf_counter()
         L.ref_model_free(m)
     finally:
         os.remove(path)
-    one, full = t1 - t0, t2 - t1
-    return {"prefill_tok_per_s": n_prompt / one, "decode_tok_per_s": (n_gen - 1) / max(full - one, 1e-9),
-            "cores": threads, "kind": "reference",
-            "sample": f"reference gen --greedy, {n_prompt}-token prompt, {n_gen} tokens, {threads} threads"}
+    return {"value": n_gen / (t2 - t1), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "prefill_tok_per_s": n_prompt / (t1 - t0),
+            "sample": f"reference engine (oracle/_ref): {n_prompt}-token batched prefill ({t1 - t0:.1f} s), then "
+                      f"{n_gen} greedy decode steps with the shortlist head at positions {n_prompt}.. "
+                      f"({t2 - t1:.1f} s), {threads} threads"}
 
 
 def read_traffic(path):
@@ -359,18 +369,47 @@ def cpu_baseline(synth, shapes, seconds=12.0):
                       f"in chunks of 16 over {threads} threads), {total_sec:.1f} s"}
 
 
+def e2e_cpu_port(hp, tens, oracle, n_prompt=512, n_gen=4):
+    """Fallback when the reference build is absent: the oracle's C restatement of the decoder (single thread),
+    prefill of the same prompt, then n_gen greedy steps."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from decoder_util import oracle_decoder
+    dec = oracle_decoder(oracle, hp, tens, ctx_len=4096)
+    ids = np.random.default_rng(9).integers(0, hp.vocab_size, n_prompt).astype(np.int32)
+    t0 = time.perf_counter()
+    r = dec.forward_batch(ids, 0, top_k=1)
+    t1 = time.perf_counter()
+    tok = oracle.argmax(r["logits"])
+    for i in range(n_gen):
+        r = dec.forward(tok, n_prompt + i, top_k=1)
+        tok = oracle.argmax(r["logits"])
+    t2 = time.perf_counter()
+    return {"value": n_gen / (t2 - t1), "unit": "tok/s", "cores": 1, "kind": "port",
+            "prefill_tok_per_s": n_prompt / (t1 - t0),
+            "sample": f"oracle C restatement of the decoder, one thread: {n_prompt}-token prefill ({t1 - t0:.1f} s), "
+                      f"{n_gen} greedy steps ({t2 - t1:.1f} s)"}
+
+
+# The reference's published decode rate for this model shape: q4mix-sl, Galaxy S24, best thread count (README.md:35)
+BASELINE_DECODE_TOK_S = 78.6
+
+
+def rnd(d):
+    return {k: (round(v, 3) if isinstance(v, float) else v) for k, v in d.items()}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=256, help="timed greedy decode steps")
+    ap.add_argument("--warmup", type=int, default=3, help="decode steps of the warm-up run")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end prefill + decode measurement")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path runs on a single "
-              f"MI355X; see DESIGN.md for how it would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this path runs on a single MI355X "
+              f"(row-sharding it over several GPUs is a design note, not built)", file=sys.stderr)
         return 2
     import torch
     qh = load_package()
@@ -379,35 +418,43 @@ def main():
     import oracle as orc
     qh.init(0)
     shapes = [(4864, 896), (896, 4864)]
+    hp, tens = e2e_model()
+    log(f"headline: prefill 512 + {args.steps} greedy decode steps")
+    e = e2e_bench(qh, torch, hp, tens, steps=args.steps, warmup=args.warmup)
     if args.e2e_only:
-        hp, tens = e2e_model()
-        e = e2e_bench(qh, torch, hp, tens, steps=max(args.steps, 256))
-        print(json.dumps({kk: (round(v, 3) if isinstance(v, float) else v) for kk, v in e.items()}), flush=True)
+        print(json.dumps(rnd(e)), flush=True)
         return 0
-    log("headline: Q4_0 GEMV rotation")
-    head = gemv_rotation(qh, synth, torch, 3, shapes, args.steps, args.warmup, check=orc.oracle)
     result = {
-        "metric": METRIC, "value": round(head["GBps"], 2), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(head["ms_per_step"], 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
-        "data": "synthetic (seeded: Q4_0 codes uniform [-8,7], scale |N(0,0.02)|/7 per 128 columns; x ~ N(0,1))",
-        "config": {"workload": "q4_0 GEMV batch 1, gate/up 4864x896 + down 896x4864, cold HBM rotation",
-                   "copies_per_shape": head["copies"], "launches_per_step": head["launches"] // args.steps,
-                   "parity": "bit-exact vs oracle"},
+        "metric": METRIC, "value": round(e["decode_tok_per_s"], 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(e["decode_ms_per_token"], 4),
+        "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": round(e["decode_tok_per_s"] / BASELINE_DECODE_TOK_S, 2), "dtype": "int8",
+        "data": "synthetic random-init q4mix model (seeded, quanta.cpp_amd/qnt.py seed 5; Q8_0 attention, Q4_0 MLP, "
+                "Exact Shortlist Head copy), prompt of 512 ids uniform over the vocabulary (seed 9)",
+        "config": {"workload": "q4mix Qwen2.5-0.5B-shaped greedy decode (24 layers, dim 896, 14/2 heads, MLP 4864, "
+                               "vocab 151936, f16 KV cache, ctx 4096): 512-token prompt in 32-token prefill chunks, "
+                               f"then {args.steps} decode steps, one graph-replayed step per token",
+                   "prefill_tok_per_s": round(e["prefill_tok_per_s"], 1),
+                   "stream_equals_reference": e["stream_equals_reference"],
+                   "head": "Exact Shortlist Head, top_k 1"},
     }
+    log("roofline: Q4_0 GEMV at the MLP shapes, cold HBM")
+    head = gemv_rotation(qh, synth, torch, 3, shapes, 20, 3, check=orc.oracle)
     achieved = head["bytes_per_launch"] / (head["us_per_launch"] * 1e-6) / 1e9
     traffic = read_traffic(os.path.join(ROOT, "profiles", "q4_gemv_traffic.txt"))
     result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                          "kernel": "gemv_kernel<Q4_0>", "bytes_per_launch": round(head["bytes_per_launch"], 1),
-                          "us_per_launch": round(head["us_per_launch"], 3)}
-    extra = {}
+                          "kernel": "gemv_kernel<Q4_0> (decode weight GEMV, gate/up 4864x896 + down 896x4864)",
+                          "bytes_per_launch": round(head["bytes_per_launch"], 1),
+                          "us_per_launch": round(head["us_per_launch"], 3),
+                          "copies_per_shape": head["copies"]}
+    extra = {"q4_gemv_mlp_GBps": round(head["GBps"], 2)}
     if not args.no_extra:
         log("Q8_0 / Q4_0 GEMV per shape, cold and hot")
         for dtype, name, shp in [(2, "q8", [(896, 896), (128, 896), (4864, 896), (896, 4864)]),
                                  (3, "q4", shapes)]:
             for n, k in shp:
-                cold = gemv_rotation(qh, synth, torch, dtype, [(n, k)], max(3, args.steps // 2), 2)
+                cold = gemv_rotation(qh, synth, torch, dtype, [(n, k)], 10, 2)
                 hot = gemv_rotation(qh, synth, torch, dtype, [(n, k)], 3, 1, hot=True)
                 extra[f"{name}_gemv_{n}x{k}"] = {"cold_GBps": round(cold["GBps"], 1),
                                                   "cold_us": round(cold["us_per_launch"], 3),
@@ -417,28 +464,21 @@ def main():
         for dtype, name, n, k in [(2, "q8", 896, 896), (2, "q8", 128, 896), (3, "q4", 4864, 896),
                                   (3, "q4", 896, 4864)]:
             for m in (32, 128, 512):
-                r = prefill_rotation(qh, synth, torch, dtype, n, k, m, max(3, args.steps // 4), 1)
-                extra[f"{name}_prefill_{n}x{k}_M{m}"] = {kk: round(v, 3) for kk, v in r.items()}
+                r = prefill_rotation(qh, synth, torch, dtype, n, k, m, 5, 1)
+                extra[f"{name}_prefill_{n}x{k}_M{m}"] = rnd(r)
         log("shortlist head")
-        h = head_bench(qh, synth, torch, orc.oracle, max(3, args.steps // 4), 1)
-        extra["shortlist_head_151936x896"] = {kk: (round(v, 3) if isinstance(v, float) else v) for kk, v in h.items()}
-        log("end-to-end q4mix decode")
-        hp, tens = e2e_model()
-        e = e2e_bench(qh, torch, hp, tens)
-        extra["e2e_q4mix_qwen2.5_0.5b"] = {kk: (round(v, 3) if isinstance(v, float) else v) for kk, v in e.items()}
-    if extra:
-        result["extra"] = extra
+        extra["shortlist_head_151936x896"] = rnd(head_bench(qh, synth, torch, orc.oracle, 5, 1))
+    result["extra"] = extra
     if not args.no_cpu:
-        log("CPU baseline")
-        result["cpu_baseline"] = cpu_baseline(synth, shapes)
-        result["cpu_baseline"]["value"] = round(result["cpu_baseline"]["value"], 3)
+        log("CPU baseline: the reference engine's decoder on the host cores")
+        c = e2e_cpu_baseline(hp, tens)
+        if c is None:
+            c = e2e_cpu_port(hp, tens, orc.oracle)
+        result["cpu_baseline"] = rnd(c)
         if not args.no_extra:
-            log("CPU baseline, end to end")
-            e = e2e_cpu_baseline(hp, tens)
-            if e is not None:
-                extra["e2e_q4mix_qwen2.5_0.5b_cpu_reference"] = {kk: (round(v, 3) if isinstance(v, float) else v)
-                                                                  for kk, v in e.items()}
-                result["extra"] = extra
+            log("CPU baseline: Q4_0 GEMV")
+            g = cpu_baseline(synth, shapes)
+            extra["q4_gemv_mlp_cpu"] = rnd(g)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

@@ -19,6 +19,11 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 QK = 32
 Q8_0, Q4_0 = 2, 3
+# per-layer tensor names in the decoder's order (reference model.cpp:14-33)
+LAYER_ORDER = ("input_layernorm.weight", "self_attn.q_proj.weight", "self_attn.k_proj.weight",
+               "self_attn.v_proj.weight", "self_attn.o_proj.weight", "self_attn.q_proj.bias", "self_attn.k_proj.bias",
+               "self_attn.v_proj.bias", "post_attention_layernorm.weight", "mlp.gate_proj.weight", "mlp.up_proj.weight",
+               "mlp.down_proj.weight")
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
@@ -81,6 +86,23 @@ class _Oracle:
         """hp: vocab, dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, ctx_len, qkv_bias, rope_theta, norm_eps;
         arrays / dtypes in the order of qo_decoder_create (None for absent tensors)."""
         return Decoder(self.lib, hp, arrays, dtypes)
+
+    def decoder_for(self, hp, tensors: dict, ctx_len: int | None = None) -> "Decoder":
+        """The decoder over a .qnt tensor set (name -> record with .data / .dtype, as quanta_cpp_amd.qnt writes and
+        reads them) with hyperparameters hp (an HParams record)."""
+        arrays, dtypes = [], []
+        names = ["model.embed_tokens.weight", "model.norm.weight"]
+        for l in range(hp.n_layers):
+            names += [f"model.layers.{l}.{n}" for n in LAYER_ORDER]
+        names += ["quanta.head_q4", "quanta.head_err"]
+        for name in names:
+            t = tensors.get(name)
+            arrays.append(None if t is None else np.asarray(t.data))
+            dtypes.append(-1 if t is None else t.dtype)
+        h = dict(vocab=hp.vocab_size, dim=hp.dim, n_layers=hp.n_layers, n_heads=hp.n_heads, n_kv_heads=hp.n_kv_heads,
+                 head_dim=hp.head_dim, ffn_dim=hp.ffn_dim, ctx_len=ctx_len or hp.max_seq, qkv_bias=int(hp.qkv_bias),
+                 rope_theta=hp.rope_theta, norm_eps=hp.norm_eps)
+        return Decoder(self.lib, h, arrays, dtypes)
 
     def quantize_q8(self, x: np.ndarray):
         x = np.ascontiguousarray(x, np.float32)

@@ -324,8 +324,13 @@ class Decoder:
         _check(lib().qh_decoder_prefill(self.h, _ptr(self.tokens), self.tokens.numel(), pos0, top_k, _stream()))
 
     def begin(self, out_cap: int, top_k: int = 1):
+        """Starts a greedy generation into an output list of out_cap tokens. The list's buffer is kept across calls
+        with the same capacity, so a decode step captured in a graph after one begin() stays valid after the next."""
         torch = _torch()
-        self.out = torch.zeros(out_cap, dtype=torch.int32, device=self.buf.device)
+        if self.out is None or self.out.numel() != out_cap:
+            self.out = torch.zeros(out_cap, dtype=torch.int32, device=self.buf.device)
+        else:
+            self.out.zero_()
         _check(lib().qh_decoder_begin(self.h, top_k, _ptr(self.out), out_cap, _stream()))
 
     def step(self, top_k: int = 1):
