@@ -52,6 +52,20 @@ enum { kStatusCtx = 1, kStatusToken = 2 };
 __device__ __forceinline__ float dev_expf(float x) { return expf_variant<2>(x); }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return f16_to_f32(h); }
+
+// A 16-byte register value as a native vector (register arrays of HIP's uint4 struct are not always split into
+// registers by the compiler; native vectors are).
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4u ld4(const void* p) { return *reinterpret_cast<const v4u*>(p); }
+
+// LDS DMA (global_load_lds_dwordx4): lane l's 16 bytes at g go to lds_wave + 16 l, where lds_wave is the same LDS
+// address in every lane of the wave. Counted by vmcnt; the LDS data is valid after s_waitcnt vmcnt(0). The body
+// exists only in the device pass (the host pass cannot form an LDS address).
+__device__ __forceinline__ void lds_dma16(const void* g, void* lds_wave) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave, 16, 0, 0);
+#endif
+}
 // f32 -> f16 (round to nearest even) of an already rounded f32 value, as the reference stores its f32 K / V results
 // into the f16 cache. The empty asm makes the value opaque, so the compiler cannot fuse the FMA that produced it and
 // this conversion into one v_fma_mixlo_f16, which rounds only once (straight to f16) and differs on double-rounding
@@ -338,7 +352,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int HALF = HD / 2, CPR = HD / 8;           // 16-byte chunks per f16 K row
     constexpr int kVRows = kVStageBytes / (HD * 2);      // V rows one LDS stage holds (a multiple of 8)
     constexpr int kVBlk = kVRows / 8;                    // 8-row blocks per stage
-    constexpr int kVRegs = kVBlk * HD / 256;             // 16-byte V chunks each thread preloads
     __shared__ __align__(16) float att[kMaxCtx + kChainPad];
     __shared__ __align__(16) uint4 vst[(kVBlk + 4) * HD];  // [block][dim] -> 8 rows; 4 blocks of read padding
     __shared__ __align__(16) uint16_t kloc[kChunk * HD];
@@ -357,16 +370,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const uint4* vc4 = reinterpret_cast<const uint4*>(vc);
     auto vchunk = [&](int blk, int d) { return (size_t)blk * kvd + kvh * HD + d; };  // uint4 index of (block, dim)
 
-    // V blocks [0, min(ceil(pos0 / 8), kVBlk)) of the cache: every load in flight before anything else.
-    const int ncb = min((pos0 + 7) / 8, kVBlk);
-    const int nch = ncb * HD;
-    const int clast = nch > 0 ? nch - 1 : 0;
-    uint4 vr[kVRegs];
+    // Global loads in the order the kernel needs them: this thread's cached K rows for the first score rows
+    // (registers), then the V blocks of the first stage straight into LDS (DMA, no registers; waited for before the
+    // V stage is read), then the chunk's own q / k / v rows below.
+    constexpr int kKPre = 3;  // score rows per thread loaded up front (768 positions)
+    const int grow = pos0 > 0 ? pos0 - 1 : 0;
+    v4u kpre[kKPre][CPR];
 #pragma unroll
-    for (int i = 0; i < kVRegs; ++i) {
-        const int c = min(tid + i * 256, clast);
-        vr[i] = load16(vc4 + vchunk(c / HD, c % HD));
+    for (int r = 0; r < kKPre; ++r) {
+        const uint16_t* kg = kc + (size_t)min(tid + 256 * r, grow) * kvd + kvh * HD;
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) kpre[r][i] = ld4(kg + i * 8);
     }
+    const int ncb = min((pos0 + 7) / 8, kVBlk);  // cache blocks of the first stage (the last may be partial)
+    constexpr int kDmaPerBlk = HD / 64;          // 1 KB (one wave instruction) per DMA chunk
+    for (int c = wave; c < ncb * kDmaPerBlk; c += 4)
+        lds_dma16(vc4 + vchunk(c / kDmaPerBlk, (c % kDmaPerBlk) * 64 + lane), vst + c * 64);
 
     // q of this head with bias, rotated; keys and values of the chunk's tokens 0..t (model.cpp:183-195, rope
     // ops_ref.cpp:201-214: a*c - b*s and b*c + a*s with the reference build's contraction fma(a, c, -(b*s)) and
@@ -415,47 +434,59 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int i = 0; i < HD; ++i) qv[i] = qs[i];
     const float scale = 1.0f / __builtin_sqrtf((float)HD);
     float mx = -__builtin_inff();
-    constexpr int RB = HD == 64 ? 2 : 1;  // rows per thread per batch, their loads issued together
-    const int grow = pos0 > 0 ? pos0 - 1 : 0;
-    for (int j0 = tid; j0 < nrows; j0 += 256 * RB) {
-        uint4 kk[RB][CPR];
-#pragma unroll
-        for (int r = 0; r < RB; ++r) {
-            // both sources read unconditionally (clamped rows), the row's own chosen afterwards
-            const int j = min(j0 + 256 * r, nrows - 1);
-            const uint16_t* kg = kc + (size_t)min(j, grow) * kvd + kvh * HD;
-            const uint16_t* kl = kloc + min(max(j - pos0, 0), kChunk - 1) * HD;
-#pragma unroll
-            for (int i = 0; i < CPR; ++i) {
-                const uint4 g = load16(kg + i * 8);
-                const uint4 l = *reinterpret_cast<const uint4*>(kl + i * 8);
-                kk[r][i] = j < pos0 ? g : l;
-            }
-        }
-        float sc[RB];
-#pragma unroll
-        for (int r = 0; r < RB; ++r) sc[r] = 0.0f;
+    // one dot product: s = fma(q_i, k_i, s) in dimension order
+    auto dot_row = [&](const v4u(&kk)[CPR]) {
+        float sc = 0.0f;
 #pragma unroll
         for (int i = 0; i < CPR; ++i) {
 #pragma unroll
-            for (int r = 0; r < RB; ++r) {
-                const uint32_t wv[4] = {kk[r][i].x, kk[r][i].y, kk[r][i].z, kk[r][i].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    sc[r] = __builtin_fmaf(qv[i * 8 + 2 * e], h2f((uint16_t)(wv[e] & 0xffffu)), sc[r]);
-                    sc[r] = __builtin_fmaf(qv[i * 8 + 2 * e + 1], h2f((uint16_t)(wv[e] >> 16)), sc[r]);
-                }
+            for (int e = 0; e < 4; ++e) {
+                sc = __builtin_fmaf(qv[i * 8 + 2 * e], h2f((uint16_t)(kk[i][e] & 0xffffu)), sc);
+                sc = __builtin_fmaf(qv[i * 8 + 2 * e + 1], h2f((uint16_t)(kk[i][e] >> 16)), sc);
             }
         }
+        return sc;
+    };
+    // a row of the chunk's own keys (LDS), for rows j >= pos0
+    auto kloc_row = [&](v4u(&kk)[CPR], int j) {
+        const uint16_t* kl = kloc + min(max(j - pos0, 0), kChunk - 1) * HD;
 #pragma unroll
-        for (int r = 0; r < RB; ++r) {
-            const int j = j0 + 256 * r;
+        for (int i = 0; i < CPR; ++i) kk[i] = ld4(kl + i * 8);
+    };
+    {  // the preloaded rows tid + 256 r, their chains interleaved
+        float sc[kKPre];
+        v4u kk[kKPre][CPR];
+#pragma unroll
+        for (int r = 0; r < kKPre; ++r) {
+            const int j = tid + 256 * r;
+            v4u kl[CPR];
+            kloc_row(kl, j);
+#pragma unroll
+            for (int i = 0; i < CPR; ++i) kk[r][i] = j < pos0 ? kpre[r][i] : kl[i];
+        }
+#pragma unroll
+        for (int r = 0; r < kKPre; ++r) sc[r] = dot_row(kk[r]);
+#pragma unroll
+        for (int r = 0; r < kKPre; ++r) {
+            const int j = tid + 256 * r;
             if (j < nrows) {
                 const float a = sc[r] * scale;
                 att[j] = a;
                 mx = a > mx ? a : mx;
             }
         }
+    }
+    for (int j = tid + 256 * kKPre; j < nrows; j += 256) {  // longer contexts: one row at a time
+        v4u kk[CPR], kl[CPR];
+        const uint16_t* kg = kc + (size_t)min(j, grow) * kvd + kvh * HD;
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) kk[i] = ld4(kg + i * 8);
+        kloc_row(kl, j);
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) kk[i] = j < pos0 ? kk[i] : kl[i];
+        const float a = dot_row(kk) * scale;
+        att[j] = a;
+        mx = a > mx ? a : mx;
     }
     // the maximum does not depend on the order of comparison
 #pragma unroll
@@ -468,13 +499,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     mx = red[0];
     for (int w = 1; w < 4; ++w) mx = red[w] > mx ? red[w] : mx;
     for (int j = tid; j < nrows; j += 256) att[j] = dev_expf(att[j] - mx);
-    // first V stage: the preloaded cache blocks (the block holding pos0 carries stale rows from pos0 on, replaced
-    // below), then the chunk's rows that fall inside the stage
-#pragma unroll
-    for (int i = 0; i < kVRegs; ++i) {  // unconditional stores (slots past nch go to this thread's padding slot)
-        const int c = tid + i * 256;
-        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(vst) + 8 * (c < nch ? c : kVBlk * HD + tid)) = vr[i];
-    }
+    // first V stage: the cache blocks arrive by DMA (the block holding pos0 carries stale rows from pos0 on,
+    // replaced below), then the chunk's rows that fall inside the stage are written over them
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     uint16_t* vst16 = reinterpret_cast<uint16_t*>(vst);
     const int s1 = min(nrows, kVRows);
