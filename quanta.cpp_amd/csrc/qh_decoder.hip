@@ -342,13 +342,12 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(float* __restric
 // The LDS footprint allows one workgroup per CU (one wave per SIMD); saying so lets the compiler keep the V preload
 // in registers.
 template <int HD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attention_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                        const float* __restrict__ v, const float* __restrict__ bq,
-                                                        const float* __restrict__ bk, const float* __restrict__ bv,
-                                                        const float* __restrict__ cs, const int* __restrict__ pos_dev,
-                                                        int ctx, int n_heads, int n_kv, uint16_t* __restrict__ kc,
-                                                        uint16_t* __restrict__ vc, int8_t* __restrict__ oq,
-                                                        float* __restrict__ od, int* __restrict__ status) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attention_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv,
+    const float* __restrict__ cs, const int* __restrict__ pos_dev, int ctx, int n_heads, int n_kv,
+    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int8_t* __restrict__ oq, float* __restrict__ od,
+    int* __restrict__ status) {
     constexpr int HALF = HD / 2, CPR = HD / 8;           // 16-byte chunks per f16 K row
     constexpr int kVRows = kVStageBytes / (HD * 2);      // V rows one LDS stage holds (a multiple of 8)
     constexpr int kVBlk = kVRows / 8;                    // 8-row blocks per stage
@@ -387,11 +386,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int c = wave; c < ncb * kDmaPerBlk; c += 4)
         lds_dma16(vc4 + vchunk(c / kDmaPerBlk, (c % kDmaPerBlk) * 64 + lane), vst + c * 64);
 
+    // this token's q (this head), k and v (its KV head) rows among the chunk's projections
+    const float* qsrc = q + (size_t)t * qd + h * HD;  // row r of k / v: ksrc + r * kvd
+    const float* ksrc = k + kvh * HD;
+    const float* vsrc = v + kvh * HD;
+
     // q of this head with bias, rotated; keys and values of the chunk's tokens 0..t (model.cpp:183-195, rope
     // ops_ref.cpp:201-214: a*c - b*s and b*c + a*s with the reference build's contraction fma(a, c, -(b*s)) and
     // fma(b, c, a*s)).
     if (tid < HALF) {
-        const float* qr = q + (size_t)t * qd + h * HD;
+        const float* qr = qsrc;
         float a = qr[tid], b = qr[tid + HALF];
         if (bq) {
             a = a + bq[h * HD + tid];
@@ -404,7 +408,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     for (int e = tid; e < (t + 1) * HALF; e += 256) {
         const int r = e / HALF, i = e - r * HALF;
-        const float* kr = k + (size_t)r * kvd + kvh * HD;
+        const float* kr = ksrc + (size_t)r * kvd;
         float a = kr[i], b = kr[i + HALF];
         if (bk) {
             a = a + bk[kvh * HD + i];
@@ -417,7 +421,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     for (int e = tid; e < (t + 1) * HD; e += 256) {
         const int r = e / HD, i = e - r * HD;
-        float val = v[(size_t)r * kvd + kvh * HD + i];
+        float val = vsrc[(size_t)r * kvd + i];
         if (bv) val = val + bv[kvh * HD + i];
         vloc[r * HD + i] = f2h(val);
     }
@@ -631,8 +635,9 @@ __global__ __launch_bounds__(256) void gemv_qkv_norm_kernel(QkvSegs a, NormAct a
     const int ra = blk * tile_rows;
     const int nrows = min(tile_rows, rows - ra);
     act.tmp = smem + gemv_tile_lds_bytes(nb * QK, tile_rows, true) / 4;
-    const float val = gemv_tile<DT, U, true>(w, sc, nullptr, nullptr, nullptr, nullptr, nb, ra, nrows, tile_rows,
-                                             nb_magic, smem, act);
+    constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
+    const GemvSegs<1> segs{{w + (size_t)ra * nb * kBlockBytes}, {sc + (size_t)ra * nb}};
+    const float val = gemv_tile<DT, U, true, 1>(segs, nullptr, nullptr, nb, nrows, tile_rows, nb_magic, smem, act);
     if ((int)threadIdx.x < nrows) out[ra + threadIdx.x] = val;
 }
 
@@ -647,8 +652,7 @@ __global__ __launch_bounds__(256) void gemv_residual_kernel(const uint8_t* __res
     const int tid = (int)threadIdx.x;
     const int ra = (int)blockIdx.x * tile_rows;
     const int nrows = min(tile_rows, rows - ra);
-    const float val = gemv_tile<DT, U, XL>(wq, wscale, nullptr, nullptr, xq, xd, nb, ra, nrows, tile_rows, nb_magic,
-                                           smem);
+    const float val = gemv_tile<DT, U, XL>(wq, wscale, xq, xd, nb, ra, nrows, tile_rows, nb_magic, smem);
     if (tid < nrows) x[ra + tid] = x[ra + tid] + val;
 }
 
@@ -666,8 +670,10 @@ __global__ __launch_bounds__(256) void gemv_swiglu_norm_kernel(const uint8_t* __
     __shared__ float gu[2 * QK];
     const int tid = (int)threadIdx.x, ra = (int)blockIdx.x * QK;
     act.tmp = smem + gemv_tile_lds_bytes(nb * QK, 2 * QK, true) / 4;
-    const float val = gemv_tile<DT, U, true, true>(wg, sg, wu, su, nullptr, nullptr, nb, ra, QK, 2 * QK, nb_magic,
-                                                   smem, act);
+    constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
+    const GemvSegs<2> segs{{wg + (size_t)ra * nb * kBlockBytes, wu + (size_t)ra * nb * kBlockBytes},
+                           {sg + (size_t)ra * nb, su + (size_t)ra * nb}};
+    const float val = gemv_tile<DT, U, true, 2>(segs, nullptr, nullptr, nb, QK, 2 * QK, nb_magic, smem, act);
     if (tid < 2 * QK) gu[tid] = val;
     __syncthreads();
     if (tid < QK) {
@@ -929,11 +935,11 @@ hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
     const size_t layer_v = (size_t)v_ctx(hp.ctx_len) * hp.n_kv_heads * hp.head_dim;
     const dim3 grid(hp.n_heads, n);
     if (hp.head_dim == 64)
-        hipLaunchKernelGGL(attention_kernel<64>, grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
+        hipLaunchKernelGGL((attention_kernel<64>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                            bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
                            d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status);
     else
-        hipLaunchKernelGGL(attention_kernel<128>, grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
+        hipLaunchKernelGGL((attention_kernel<128>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                            bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
                            d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status);
     return hipGetLastError();

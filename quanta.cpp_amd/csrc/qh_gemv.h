@@ -9,8 +9,8 @@
 // association, so the result is bit-identical. Every load of a pass is issued before the first wait; longer tiles
 // prefetch the next pass while computing the current one.
 //
-// PAIR tiles hold the same rows of two matrices of one shape (gate and up): virtual rows [0, n) come from the
-// first matrix and [n, 2n) from the second, so one round trip covers both.
+// A tile may span NSEG segments of equal row count from up to three matrices of one dtype and width (gate and up;
+// one head's q, k and v rows): virtual rows [s*n, (s+1)*n) come from segment s, so one round trip covers them all.
 #pragma once
 
 #include <limits.h>
@@ -29,7 +29,14 @@ __device__ __forceinline__ float chain_lds(const float* p, const float* dx, int 
 // One pass of a workgroup: U chunks of 16 bytes per thread, the block scale of each chunk and, unless the
 // activation is staged in LDS (XL), the activation bytes the chunk pairs with. The chunk index is clamped
 // into the tile, so every load is unconditional and all of them go out back to back.
-template <int DT, int U, bool XL, bool PAIR = false>
+// Tile sources: segment s starts at row 0 of w[s] / sc[s] (the caller offsets them to the tile's first row).
+template <int NSEG>
+struct GemvSegs {
+    const uint8_t* w[NSEG];
+    const uint16_t* sc[NSEG];
+};
+
+template <int DT, int U, bool XL, int NSEG = 1>
 struct GemvPass {
     uint4 w[U];
     uint4 xa[XL ? 1 : U];
@@ -37,11 +44,9 @@ struct GemvPass {
     uint16_t sc[U];
     uint32_t rt[U], b[U];
 
-    // split: first chunk of the second matrix (PAIR only); base2 / sbase2 point at its tile.
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ base, const uint16_t* __restrict__ sbase,
-                                         const uint8_t* __restrict__ base2, const uint16_t* __restrict__ sbase2,
-                                         int split, const int8_t* __restrict__ xq, int c0, int last, int nb,
-                                         uint32_t nb_magic) {
+    // split: chunks per segment (NSEG > 1).
+    __device__ __forceinline__ void load(const GemvSegs<NSEG>& sg, int split, const int8_t* __restrict__ xq, int c0,
+                                         int last, int nb, uint32_t nb_magic) {
         constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
 #pragma unroll
         for (int j = 0; j < U; ++j) {
@@ -49,14 +54,16 @@ struct GemvPass {
             const uint32_t g = (uint32_t)c / kChunksPerBlock;  // block index within the tile
             rt[j] = nb == 1 ? g : div_magic(g, nb_magic);      // tile row
             b[j] = g - rt[j] * (uint32_t)nb;                    // block within the row
-            if constexpr (PAIR) {
-                const bool second = c >= split;
-                const int cc = second ? c - split : c;
-                w[j] = load16((second ? base2 : base) + (size_t)cc * 16);
-                sc[j] = (second ? sbase2 : sbase)[(uint32_t)cc / kChunksPerBlock];
+            if constexpr (NSEG > 1) {
+                const int s1 = c >= split, s2 = NSEG > 2 && c >= 2 * split;
+                const int cc = c - (s1 + s2) * split;
+                const uint8_t* wb = s2 ? sg.w[NSEG - 1] : s1 ? sg.w[1] : sg.w[0];
+                const uint16_t* sb = s2 ? sg.sc[NSEG - 1] : s1 ? sg.sc[1] : sg.sc[0];
+                w[j] = load16(wb + (size_t)cc * 16);
+                sc[j] = sb[(uint32_t)cc / kChunksPerBlock];
             } else {
-                w[j] = load16(base + (size_t)c * 16);
-                sc[j] = sbase[g];
+                w[j] = load16(sg.w[0] + (size_t)c * 16);
+                sc[j] = sg.sc[0][g];
             }
             if constexpr (!XL) {
                 if constexpr (DT == kQ8) {
@@ -117,42 +124,35 @@ struct GlobalAct {
     }
 };
 
-// Rows [ra, ra + nrows) of W . x (and, PAIR, the same rows of W2 as virtual rows nrows .. 2*nrows-1) for one
-// workgroup of 256 threads. tile_rows: the virtual row capacity the LDS layout is sized for (>= the virtual rows).
-// Returns the value of virtual row threadIdx.x for threads below the virtual row count, 0 for the others.
-// smem: dynamic LDS of gemv_tile_lds_bytes(nb * 32, tile_rows, XL) bytes. act.fill<XL>(xs, xds) stages the
-// activation (codes in LDS when XL; it may use its own barriers, all 256 threads call it) after the first pass of
-// weight loads is issued; xq / xd are read per chunk when !XL. The LDS is free for reuse only after a barrier.
-template <int DT, int U, bool XL, bool PAIR = false, typename Act = GlobalAct>
-__device__ __forceinline__ float gemv_tile(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wscale,
-                                           const uint8_t* __restrict__ wq2, const uint16_t* __restrict__ wscale2,
-                                           const int8_t* __restrict__ xq, const float* __restrict__ xd, int nb,
-                                           int ra, int nrows, int tile_rows, uint32_t nb_magic, float* smem,
-                                           const Act& act) {
+// nrows rows of each of the NSEG segments of sg . x, for one workgroup of 256 threads: virtual row v is row v % nrows
+// of segment v / nrows. tile_rows: the virtual row capacity the LDS layout is sized for (>= NSEG * nrows). Returns
+// the value of virtual row threadIdx.x for threads below NSEG * nrows, 0 for the others. smem: dynamic LDS of
+// gemv_tile_lds_bytes(nb * 32, tile_rows, XL) bytes. act.fill<XL>(xs, xds) stages the activation (codes in LDS when
+// XL; it may use its own barriers, all 256 threads call it) after the first pass of weight loads is issued; xq / xd
+// are read per chunk when !XL. The LDS is free for reuse only after a barrier.
+template <int DT, int U, bool XL, int NSEG = 1, typename Act = GlobalAct>
+__device__ __forceinline__ float gemv_tile(const GemvSegs<NSEG>& sg, const int8_t* __restrict__ xq,
+                                           const float* __restrict__ xd, int nb, int nrows, int tile_rows,
+                                           uint32_t nb_magic, float* smem, const Act& act) {
     constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
-    constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
     float* xds = smem;         // [nb] activation scales
     float* prod = smem + nb;   // [tile_rows][nb + 1] block products
     // [cols] codes (XL), 16-byte aligned after the products
     int8_t* xs = reinterpret_cast<int8_t*>(smem) + ((((size_t)nb + (size_t)tile_rows * (nb + 1)) * 4 + 15) & ~size_t(15));
     const int pstride = nb + 1;
     const int tid = (int)threadIdx.x;
-    const int vrows = PAIR ? 2 * nrows : nrows;
+    const int vrows = NSEG * nrows;
     const int nchunks = vrows * nb * kChunksPerBlock;
-    const int split = PAIR ? nrows * nb * kChunksPerBlock : INT_MAX;
-    const uint8_t* base = wq + (size_t)ra * nb * kBlockBytes;
-    const uint16_t* sbase = wscale + (size_t)ra * nb;
-    const uint8_t* base2 = PAIR ? wq2 + (size_t)ra * nb * kBlockBytes : nullptr;
-    const uint16_t* sbase2 = PAIR ? wscale2 + (size_t)ra * nb : nullptr;
+    const int split = nrows * nb * kChunksPerBlock;
 
-    GemvPass<DT, U, XL, PAIR> cur;
-    cur.load(base, sbase, base2, sbase2, split, xq, 0, nchunks - 1, nb, nb_magic);
+    GemvPass<DT, U, XL, NSEG> cur;
+    cur.load(sg, split, xq, 0, nchunks - 1, nb, nb_magic);
     act.template fill<XL>(xs, xds);
     if constexpr (XL) __syncthreads();
     for (int c0 = 0; c0 < nchunks; c0 += 256 * U) {
         if (c0 + 256 * U < nchunks) {  // uniform: prefetch the next pass, then compute this one
-            GemvPass<DT, U, XL, PAIR> nxt;
-            nxt.load(base, sbase, base2, sbase2, split, xq, c0 + 256 * U, nchunks - 1, nb, nb_magic);
+            GemvPass<DT, U, XL, NSEG> nxt;
+            nxt.load(sg, split, xq, c0 + 256 * U, nchunks - 1, nb, nb_magic);
             cur.products(prod, pstride, c0, nchunks, xs);
             cur = nxt;
         } else {
@@ -163,13 +163,14 @@ __device__ __forceinline__ float gemv_tile(const uint8_t* __restrict__ wq, const
     return tid < vrows ? chain_lds(prod + tid * pstride, xds, nb) : 0.0f;
 }
 
-template <int DT, int U, bool XL, bool PAIR = false>
+// Rows [ra, ra + nrows) of one matrix, activation from global memory.
+template <int DT, int U, bool XL>
 __device__ __forceinline__ float gemv_tile(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wscale,
-                                           const uint8_t* __restrict__ wq2, const uint16_t* __restrict__ wscale2,
                                            const int8_t* __restrict__ xq, const float* __restrict__ xd, int nb,
                                            int ra, int nrows, int tile_rows, uint32_t nb_magic, float* smem) {
-    return gemv_tile<DT, U, XL, PAIR>(wq, wscale, wq2, wscale2, xq, xd, nb, ra, nrows, tile_rows, nb_magic, smem,
-                                      GlobalAct{xq, xd, nb});
+    constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
+    const GemvSegs<1> sg{{wq + (size_t)ra * nb * kBlockBytes}, {wscale + (size_t)ra * nb}};
+    return gemv_tile<DT, U, XL, 1>(sg, xq, xd, nb, nrows, tile_rows, nb_magic, smem, GlobalAct{xq, xd, nb});
 }
 
 }  // namespace qh

@@ -52,8 +52,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(float* __restrict__ out, cons
     extern __shared__ float smem[];
     const int ra = r0 + (int)blockIdx.x * tile_rows;
     const int nrows = min(tile_rows, r1 - ra);
-    const float v = gemv_tile<DT, U, XL>(wq, wscale, nullptr, nullptr, xq, xd, nb, ra, nrows, tile_rows, nb_magic,
-                                         smem);
+    const float v = gemv_tile<DT, U, XL>(wq, wscale, xq, xd, nb, ra, nrows, tile_rows, nb_magic, smem);
     if ((int)threadIdx.x < nrows) out[ra + threadIdx.x] = v;
 }
 
