@@ -406,6 +406,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end prefill + decode measurement")
+    ap.add_argument("--only", choices=["e2e", "roofline", "prefill"],
+                    help="one measurement alone (for counter runs): e2e = --e2e-only; roofline = a 256 MiB copy "
+                         "(counter calibration) then the Q4_0 GEMV rotation; prefill = Q4_0 4864x896 at M = 512")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this path runs on a single MI355X "
@@ -418,6 +421,21 @@ def main():
     import oracle as orc
     qh.init(0)
     shapes = [(4864, 896), (896, 4864)]
+    if args.only == "roofline":
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        head = gemv_rotation(qh, synth, torch, 3, shapes, 5, 1, check=orc.oracle)
+        print(json.dumps({"calibration_copy_bytes": src.numel() * 4, "q4_gemv": rnd(head)}), flush=True)
+        return 0
+    if args.only == "prefill":
+        r = prefill_rotation(qh, synth, torch, 3, 4864, 896, 512, 5, 1)
+        print(json.dumps({"q4_prefill_4864x896_M512": rnd(r)}), flush=True)
+        return 0
+    if args.only == "e2e":
+        args.e2e_only = True
     hp, tens = e2e_model()
     log(f"headline: prefill 512 + {args.steps} greedy decode steps")
     e = e2e_bench(qh, torch, hp, tens, steps=args.steps, warmup=args.warmup)
