@@ -154,20 +154,195 @@ struct Row4 {
     }
 };
 
+// ------------------------------------------------------------------------------ segmented sum of squares
+// rmsnorm's sum of squares is one serial chain, ss = fma(x_i, x_i, ss) for i = 0 .. D-1 in order (ops_ref.cpp:195-197):
+// D dependent FMAs, the longest dependency of a decode layer. seg_sum_squares runs it as four segments at once, one
+// per wave, and still returns the chain's value bit for bit:
+//  - wave 0 runs segment 0 from 0;
+//  - the wave of segment k >= 1 runs it from 64 start values at once, one per lane: the f32 rounding of the exact
+//    (double) sum of squares before the segment, and its neighbours 32 below to 31 above in bit order. The chain's
+//    value at the segment start differs from that guess only by the chain's own accumulated rounding (at most 26 ulps
+//    over 2*10^5 random rows of 896, including rows with outliers), so some lane almost always started at exactly
+//    the chain's value, and that lane's result is then the chain's value at the segment end;
+//  - every thread then follows the chain from segment 0 through the lanes whose start matches bit for bit; a value
+//    outside a window (rare) is continued by running that segment serially from it.
+// The chains read x through scalar loads (x is in global memory and no workgroup writes it during the kernel): one
+// 64-byte load feeds 16 FMAs of all 64 lanes with scalar operands, and the LDS stays free for the other waves.
+// Scalar loads can return out of order, so the loop waits for everything outstanding after each 32-value batch,
+// with the next batch already issued; each wave first touches every 64-byte line of its segment (SegWarm) so these
+// loads hit the scalar cache.
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef const __attribute__((address_space(4))) v16f* const_v16f_ptr;
+typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
+
+// lgkmcnt(0) with the vector-memory and export counters left alone (gfx9 s_waitcnt encoding).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+// acc = fma(g[i], g[i], acc) for i = 0 .. n-1 in order, g uniform across the wave and 64-byte aligned, n % 32 == 0.
+__device__ __forceinline__ float ss_chain_scalar(const float* g, int n, float acc) {
+    const_v16f_ptr p = (const_v16f_ptr)g;
+    const int nv = n / 16;  // even
+    v16f a0 = p[0], a1 = p[1];
+    wait_lgkm0();
+    __builtin_amdgcn_sched_barrier(0);
+    int i = 0;
+#pragma unroll 1
+    for (; i + 4 <= nv; i += 4) {
+        const v16f b0 = p[i + 2], b1 = p[i + 3];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc = __builtin_fmaf(a0[k], a0[k], acc);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc = __builtin_fmaf(a1[k], a1[k], acc);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkm0();
+        __builtin_amdgcn_sched_barrier(0);
+        a0 = p[min(i + 4, nv - 2)];
+        a1 = p[min(i + 5, nv - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc = __builtin_fmaf(b0[k], b0[k], acc);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc = __builtin_fmaf(b1[k], b1[k], acc);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkm0();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (i + 2 <= nv) {  // nv % 4 == 2: the last batch, loaded by the loop (or before it)
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc = __builtin_fmaf(a0[k], a0[k], acc);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc = __builtin_fmaf(a1[k], a1[k], acc);
+    }
+    return acc;
+}
+
+// One scalar load per 64-byte line of the first 256 values of g[0, n): brings them into the scalar cache; the values
+// are held until consume() so the loads cannot be dropped.
+struct SegWarm {
+    uint32_t v[16];
+    __device__ __forceinline__ void issue(const float* g, int n) {
+        const_u32_ptr q = (const_u32_ptr)g;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = q[min(i * 16, n - 1)];
+    }
+    __device__ __forceinline__ void consume() const {
+        asm volatile("" ::"s"(v[0]), "s"(v[1]), "s"(v[2]), "s"(v[3]), "s"(v[4]), "s"(v[5]), "s"(v[6]), "s"(v[7]));
+        asm volatile("" ::"s"(v[8]), "s"(v[9]), "s"(v[10]), "s"(v[11]), "s"(v[12]), "s"(v[13]), "s"(v[14]), "s"(v[15]));
+    }
+};
+
+// Sum over the wave of a double, in lane 63 (DPP: pairs, quads, half rows, rows, then rows 0+1 and 2+3 across).
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROWS, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROWS, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double wave_sum_lane63(double v) {
+    v += dpp_f64<0xb1>(v);         // quad_perm [1,0,3,2]
+    v += dpp_f64<0x4e>(v);         // quad_perm [2,3,0,1]
+    v += dpp_f64<0x141>(v);        // row_half_mirror
+    v += dpp_f64<0x140>(v);        // row_mirror
+    v += dpp_f64<0x142, 0xa>(v);   // row_bcast:15 into rows 1, 3
+    v += dpp_f64<0x143, 0xc>(v);   // row_bcast:31 into rows 2, 3
+    return v;
+}
+
+// Segments: [0, S0), then three of L values, L = (D / 4) rounded down to a multiple of 32, S0 = D - 3 L (>= L).
+__device__ __forceinline__ int seg_len(int D) { return (D / 4) & ~31; }
+
+// The chain's value ss of x[0, D) in every thread. x: global, 64-byte aligned, not written during the kernel;
+// xr: this thread's Row4 of x. All 256 threads of the workgroup call it (two barriers inside).
+// D % 64 == 0, 128 <= D <= 8192.
+__device__ float seg_sum_squares(const float* __restrict__ x, int D, const Row4& xr) {
+    __shared__ double part[4][4];  // [wave][k]: the wave's share of the sum of squares below segment k's start
+    __shared__ float res[256];     // every lane's chain result
+    __shared__ uint32_t gbits[4];  // segment k's guess
+    const int tid = (int)threadIdx.x, lane = tid & 63, n4 = D / 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int L = seg_len(D), S0 = D - 3 * L;
+    const int a = wave == 0 ? 0 : S0 + (wave - 1) * L;
+    const int len = wave == 0 ? S0 : L;
+    SegWarm warm;
+    warm.issue(x + a, len);
+    double p1 = 0.0, p2 = 0.0, p3 = 0.0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int i4 = tid + 256 * k;
+        if (i4 < n4) {
+            const float4 v = xr.v[k];
+            const double s = (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+            const int e = 4 * i4;
+            p1 += e < S0 ? s : 0.0;
+            p2 += e < S0 + L ? s : 0.0;
+            p3 += e < S0 + 2 * L ? s : 0.0;
+        }
+    }
+    p1 = wave_sum_lane63(p1);
+    p2 = wave_sum_lane63(p2);
+    p3 = wave_sum_lane63(p3);
+    if (lane == 63) {
+        part[wave][1] = p1;
+        part[wave][2] = p2;
+        part[wave][3] = p3;
+    }
+    __syncthreads();
+    float start = 0.0f;
+    if (wave > 0) {
+        const double g = part[0][wave] + part[1][wave] + part[2][wave] + part[3][wave];
+        const uint32_t gb = __float_as_uint((float)g);
+        start = __uint_as_float(gb + (uint32_t)lane - 32u);
+        if (lane == 0) gbits[wave] = gb;
+    }
+    warm.consume();
+    res[tid] = ss_chain_scalar(x + a, len, start);
+    __syncthreads();
+    float s = res[0];
+    const uint32_t g1 = gbits[1], g2 = gbits[2], g3 = gbits[3];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) {
+        const uint32_t j = __float_as_uint(s) - (k == 1 ? g1 : k == 2 ? g2 : g3) + 32u;
+        if (j < 64u)
+            s = res[64 * k + j];
+        else
+            s = ss_chain_scalar(x + S0 + (k - 1) * L, L, s);
+    }
+    return s;
+}
+
+// rmsnorm scale 1 / sqrt(ss / D + eps) (ops_ref.cpp:197-198).
+__device__ __forceinline__ float rms_scale(float ss, int D, float eps) {
+    return 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+}
+
+// The sum of squares of xs[0, D) (LDS, complete, kChainPad floats of slack) by thread 0, in every thread.
+__device__ __forceinline__ float lds_sum_squares(const float* xs, int D) {
+    __shared__ float ss_sh;
+    if (threadIdx.x == 0) ss_sh = lds_chain(xs, D, [](float acc, float v) { return __builtin_fmaf(v, v, acc); });
+    __syncthreads();
+    return ss_sh;
+}
+
+// y = x * scale * w of the row xs[0..D) (LDS; each thread reads and rewrites its own float4s, slot k = tid + 256 k),
+// also to `normed` when given, then quantize_q8 of y. All 256 threads call it; xs is free after its return only
+// after a barrier.
+__device__ void normalize_quant_lds(float* xs, int D, float scale, const Row4& wr, int8_t* __restrict__ oq,
+                                    float* __restrict__ od, float* __restrict__ normed);
+
 // rmsnorm of the row xs[0..D) (LDS, 16-byte aligned, complete) with weight w (loaded into wr by the caller before
 // the row was complete, so its latency is hidden), then quantize_q8 of the normed row; also written to `normed`
 // when given (ops_ref.cpp:195-199: ss += x*x as one FMA per element in order, scale = 1/sqrt(ss/n + eps),
 // y = x * scale * w). Called by all 256 threads of a workgroup; D % 64 == 0, D <= 8192.
 __device__ void norm_quant_lds(float* xs, int D, const Row4& wr, float eps, int8_t* __restrict__ oq,
                                float* __restrict__ od, float* __restrict__ normed) {
-    __shared__ float scale_sh;
+    normalize_quant_lds(xs, D, rms_scale(lds_sum_squares(xs, D), D, eps), wr, oq, od, normed);
+}
+
+__device__ void normalize_quant_lds(float* xs, int D, float scale, const Row4& wr, int8_t* __restrict__ oq,
+                                    float* __restrict__ od, float* __restrict__ normed) {
     const int tid = (int)threadIdx.x, n4 = D / 4;
-    if (tid == 0)
-        scale_sh = 1.0f / __builtin_sqrtf(lds_chain(xs, D, [](float acc, float v) { return __builtin_fmaf(v, v, acc); }) /
-                                              (float)D +
-                                          eps);
-    __syncthreads();
-    const float scale = scale_sh;
     float4* x4 = reinterpret_cast<float4*>(xs);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -209,10 +384,47 @@ struct NormAct {
     template <bool XL>
     __device__ __forceinline__ void fill(int8_t* xs, float* xds) const {
         static_assert(XL, "the normed activation is produced in LDS");
-        __shared__ float scale_sh;
         const int tid = (int)threadIdx.x, n4 = D / 4, nb = D / QK;
         Row4 wr, xr;
         wr.load(w, n4);
+        float4* t4 = reinterpret_cast<float4*>(tmp);
+        float ss;
+        if (!eq && D >= 128) {  // uniform
+            xr.load(x, n4);
+            ss = seg_sum_squares(x, D, xr);
+        } else {
+            load_row(xr, tid, n4);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int i4 = tid + 256 * k;
+                if (i4 < n4) {
+                    t4[i4] = xr.v[k];
+                    if (x_out && blockIdx.x == 0) reinterpret_cast<float4*>(x_out)[i4] = xr.v[k];
+                }
+            }
+            __syncthreads();
+            ss = lds_sum_squares(tmp, D);
+        }
+        const float scale = rms_scale(ss, D, eps);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i4 = tid + 256 * k;
+            if (i4 < n4) {
+                float4 y = xr.v[k];
+                y.x = y.x * scale * wr.v[k].x;
+                y.y = y.y * scale * wr.v[k].y;
+                y.z = y.z * scale * wr.v[k].z;
+                y.w = y.w * scale * wr.v[k].w;
+                t4[i4] = y;
+            }
+        }
+        __syncthreads();
+        for (int b = tid >> 5; b < nb; b += 8) quant_block32(tmp[b * QK + (tid & 31)], xs + b * QK, xds + b);
+    }
+
+    // The row to normalise into xr: the embedding of *tok (eq set) or x.
+    __device__ __forceinline__ void load_row(Row4& xr, int tid, int n4) const {
+        const int nb = D / QK;
         if (eq) {
             int t = *tok;
             const bool bad = t < 0 || t >= V;
@@ -233,36 +445,6 @@ struct NormAct {
         } else {
             xr.load(x, n4);
         }
-        float4* t4 = reinterpret_cast<float4*>(tmp);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int i4 = tid + 256 * k;
-            if (i4 < n4) {
-                t4[i4] = xr.v[k];
-                if (x_out && blockIdx.x == 0) reinterpret_cast<float4*>(x_out)[i4] = xr.v[k];
-            }
-        }
-        __syncthreads();
-        if (tid == 0)
-            scale_sh = 1.0f / __builtin_sqrtf(lds_chain(tmp, D, [](float acc, float v) { return __builtin_fmaf(v, v, acc); }) /
-                                                  (float)D +
-                                              eps);
-        __syncthreads();
-        const float scale = scale_sh;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int i4 = tid + 256 * k;
-            if (i4 < n4) {
-                float4 y = xr.v[k];
-                y.x = y.x * scale * wr.v[k].x;
-                y.y = y.y * scale * wr.v[k].y;
-                y.z = y.z * scale * wr.v[k].z;
-                y.w = y.w * scale * wr.v[k].w;
-                t4[i4] = y;
-            }
-        }
-        __syncthreads();
-        for (int b = tid >> 5; b < nb; b += 8) quant_block32(tmp[b * QK + (tid & 31)], xs + b * QK, xds + b);
     }
 };
 
@@ -699,8 +881,12 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(const float* __restrict
 #pragma unroll
     for (int k = 0; k < 8; ++k)
         if (tid + 256 * k < n4) reinterpret_cast<float4*>(xs)[tid + 256 * k] = xr.v[k];
-    __syncthreads();
-    norm_quant_lds(xs, D, wr, eps, oq, od, normed);
+    if (D >= 128) {  // uniform
+        normalize_quant_lds(xs, D, rms_scale(seg_sum_squares(x, D, xr), D, eps), wr, oq, od, normed);
+    } else {
+        __syncthreads();
+        norm_quant_lds(xs, D, wr, eps, oq, od, normed);
+    }
 }
 
 // Prefill / decode bookkeeping on the device.
