@@ -46,6 +46,10 @@ constexpr int kFuseLds = 65536;       // dynamic LDS limit of the fused GEMV ker
 // Positions the V cache holds per layer: the context rounded up to its 8-position blocks.
 inline int v_ctx(int ctx) { return (ctx + 7) & ~7; }
 
+// Floats per attention workgroup's exp row: the context rounded up to 16 (64-byte aligned rows) plus 64 of slack for
+// whole-batch scalar reads past the last position.
+inline int escr_stride(int ctx) { return ((ctx + 15) & ~15) + 64; }
+
 enum { kStatusCtx = 1, kStatusToken = 2 };
 
 // glibc-identical expf on the device (all 2^32 inputs checked against the host's expf in tests).
@@ -250,23 +254,123 @@ __device__ __forceinline__ double wave_sum_lane63(double v) {
     return v;
 }
 
-// Segments: [0, S0), then three of L values, L = (D / 4) rounded down to a multiple of 32, S0 = D - 3 L (>= L).
-__device__ __forceinline__ int seg_len(int D) { return (D / 4) & ~31; }
+// acc = op(acc, g[i]) for i = 0 .. n-1 in order (n >= 1), g uniform across the wave and 4-byte aligned. Whole
+// batches of 32 values are read, so up to 32 values past n must be readable.
+template <typename Op>
+__device__ __forceinline__ float chain_scalar(const float* g, int n, float acc, Op op) {
+    const_v16f_ptr p = (const_v16f_ptr)g;
+    const int nb = n >> 5, rem = n & 31;
+    auto use = [&](const v16f& x0, const v16f& x1, int cnt) {  // cnt is uniform
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if (k < cnt) acc = op(acc, x0[k]);
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if (16 + k < cnt) acc = op(acc, x1[k]);
+    };
+    v16f a0 = p[0], a1 = p[1];
+    wait_lgkm0();
+    __builtin_amdgcn_sched_barrier(0);
+    int b = 0;
+#pragma unroll 1
+    for (; b + 2 <= nb; b += 2) {
+        const v16f c0 = p[2 * b + 2], c1 = p[2 * b + 3];
+        __builtin_amdgcn_sched_barrier(0);
+        use(a0, a1, 32);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkm0();
+        __builtin_amdgcn_sched_barrier(0);
+        a0 = p[2 * b + 4];
+        a1 = p[2 * b + 5];
+        __builtin_amdgcn_sched_barrier(0);
+        use(c0, c1, 32);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkm0();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (b < nb) {  // a full batch in a, the partial one after it
+        const v16f c0 = p[2 * b + 2], c1 = p[2 * b + 3];
+        __builtin_amdgcn_sched_barrier(0);
+        use(a0, a1, 32);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkm0();
+        __builtin_amdgcn_sched_barrier(0);
+        use(c0, c1, rem);
+    } else {
+        use(a0, a1, rem);
+    }
+    return acc;
+}
 
-// The chain's value ss of x[0, D) in every thread. x: global, 64-byte aligned, not written during the kernel;
-// xr: this thread's Row4 of x. All 256 threads of the workgroup call it (two barriers inside).
-// D % 64 == 0, 128 <= D <= 8192.
-__device__ float seg_sum_squares(const float* __restrict__ x, int D, const Row4& xr) {
-    __shared__ double part[4][4];  // [wave][k]: the wave's share of the sum of squares below segment k's start
-    __shared__ float res[256];     // every lane's chain result
-    __shared__ uint32_t gbits[4];  // segment k's guess
-    const int tid = (int)threadIdx.x, lane = tid & 63, n4 = D / 4;
+// Four segments of a chain over n values, wave w running segment w: [0, b1), [b1, b1 + L), [b1 + L, b1 + 2 L),
+// [b1 + 2 L, n).
+struct Segs4 {
+    int b1, L, n;
+    __device__ __forceinline__ int start(int k) const { return k == 0 ? 0 : b1 + (k - 1) * L; }
+    __device__ __forceinline__ int len(int k) const { return k == 0 ? b1 : k == 3 ? n - b1 - 2 * L : L; }
+};
+
+// Workgroup state of one segmented chain.
+struct SegShared {
+    double part[4][4];  // [wave][k]: the wave's share of the exact sum of the chain's terms below segment k's start
+    float res[256];     // every lane's segment result
+    uint32_t gbits[4];  // segment k's guess
+};
+
+// Sums three per-lane partials over the wave into part[wave][1..3]; a barrier must follow before seg_chain_run.
+__device__ __forceinline__ void seg_partials(SegShared& sh, double p1, double p2, double p3) {
+    p1 = wave_sum_lane63(p1);
+    p2 = wave_sum_lane63(p2);
+    p3 = wave_sum_lane63(p3);
+    if ((threadIdx.x & 63) == 63) {
+        const int w = (int)threadIdx.x >> 6;
+        sh.part[w][1] = p1;
+        sh.part[w][2] = p2;
+        sh.part[w][3] = p3;
+    }
+}
+
+// Runs the segments (wave 0 from 0, the wave of segment k from the 64 candidates around its guess), a barrier, then
+// follows the chain through the candidates; returns the chain's end value in every thread. chain(k, start) runs
+// segment k from start in the calling wave (k and start uniform across the wave) and returns its end value. All 256
+// threads call it after the barrier that published part.
+template <typename Chain>
+__device__ __forceinline__ float seg_chain_run(SegShared& sh, Chain chain) {
+    const int tid = (int)threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int L = seg_len(D), S0 = D - 3 * L;
-    const int a = wave == 0 ? 0 : S0 + (wave - 1) * L;
-    const int len = wave == 0 ? S0 : L;
+    float start = 0.0f;
+    if (wave > 0) {
+        const double g = sh.part[0][wave] + sh.part[1][wave] + sh.part[2][wave] + sh.part[3][wave];
+        const uint32_t gb = __float_as_uint((float)g);
+        start = __uint_as_float(gb + (uint32_t)lane - 32u);
+        if (lane == 0) sh.gbits[wave] = gb;
+    }
+    sh.res[tid] = chain(wave, start);
+    __syncthreads();
+    float s = sh.res[0];
+    const uint32_t g1 = sh.gbits[1], g2 = sh.gbits[2], g3 = sh.gbits[3];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) {
+        const uint32_t j = __float_as_uint(s) - (k == 1 ? g1 : k == 2 ? g2 : g3) + 32u;
+        if (j < 64u)
+            s = sh.res[64 * k + j];
+        else
+            s = chain(k, s);
+    }
+    return s;
+}
+
+// The chain's value ss of x[0, D) in every thread: segments [0, S0) and three of L = (D / 4) rounded down to a
+// multiple of 32 (S0 = D - 3 L >= L). x: global, 64-byte aligned, not written during the kernel; xr: this thread's
+// Row4 of x. All 256 threads of the workgroup call it (two barriers inside). D % 64 == 0, 128 <= D <= 8192.
+__device__ float seg_sum_squares(const float* __restrict__ x, int D, const Row4& xr) {
+    __shared__ SegShared sh;
+    const int tid = (int)threadIdx.x, n4 = D / 4;
+    const int L = (D / 4) & ~31;
+    const Segs4 sg{D - 3 * L, L, D};
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     SegWarm warm;
-    warm.issue(x + a, len);
+    warm.issue(x + sg.start(wave), sg.len(wave));
     double p1 = 0.0, p2 = 0.0, p3 = 0.0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -275,41 +379,15 @@ __device__ float seg_sum_squares(const float* __restrict__ x, int D, const Row4&
             const float4 v = xr.v[k];
             const double s = (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
             const int e = 4 * i4;
-            p1 += e < S0 ? s : 0.0;
-            p2 += e < S0 + L ? s : 0.0;
-            p3 += e < S0 + 2 * L ? s : 0.0;
+            p1 += e < sg.start(1) ? s : 0.0;
+            p2 += e < sg.start(2) ? s : 0.0;
+            p3 += e < sg.start(3) ? s : 0.0;
         }
     }
-    p1 = wave_sum_lane63(p1);
-    p2 = wave_sum_lane63(p2);
-    p3 = wave_sum_lane63(p3);
-    if (lane == 63) {
-        part[wave][1] = p1;
-        part[wave][2] = p2;
-        part[wave][3] = p3;
-    }
+    seg_partials(sh, p1, p2, p3);
     __syncthreads();
-    float start = 0.0f;
-    if (wave > 0) {
-        const double g = part[0][wave] + part[1][wave] + part[2][wave] + part[3][wave];
-        const uint32_t gb = __float_as_uint((float)g);
-        start = __uint_as_float(gb + (uint32_t)lane - 32u);
-        if (lane == 0) gbits[wave] = gb;
-    }
     warm.consume();
-    res[tid] = ss_chain_scalar(x + a, len, start);
-    __syncthreads();
-    float s = res[0];
-    const uint32_t g1 = gbits[1], g2 = gbits[2], g3 = gbits[3];
-#pragma unroll
-    for (int k = 1; k < 4; ++k) {
-        const uint32_t j = __float_as_uint(s) - (k == 1 ? g1 : k == 2 ? g2 : g3) + 32u;
-        if (j < 64u)
-            s = res[64 * k + j];
-        else
-            s = ss_chain_scalar(x + S0 + (k - 1) * L, L, s);
-    }
-    return s;
+    return seg_chain_run(sh, [&](int k, float s0) { return ss_chain_scalar(x + sg.start(k), sg.len(k), s0); });
 }
 
 // rmsnorm scale 1 / sqrt(ss / D + eps) (ops_ref.cpp:197-198).
@@ -529,7 +607,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv,
     const float* __restrict__ cs, const int* __restrict__ pos_dev, int ctx, int n_heads, int n_kv,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int8_t* __restrict__ oq, float* __restrict__ od,
-    int* __restrict__ status) {
+    float* __restrict__ escr, int escr_stride, int* __restrict__ status) {
     constexpr int HALF = HD / 2, CPR = HD / 8;           // 16-byte chunks per f16 K row
     constexpr int kVRows = kVStageBytes / (HD * 2);      // V rows one LDS stage holds (a multiple of 8)
     constexpr int kVBlk = kVRows / 8;                    // 8-row blocks per stage
@@ -539,7 +617,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     __shared__ __align__(16) uint16_t vloc[kChunk * HD];
     __shared__ __align__(16) float qs[HD];
     __shared__ float red[4];
-    __shared__ float inv_sh;
+    __shared__ float sum_sh;
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos0 = *pos_dev, pos = pos0 + t, nrows = pos + 1;
     if (pos >= ctx || pos0 < 0) {  // uniform: a step past the context touches no cache row
@@ -684,9 +762,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     __syncthreads();
     mx = red[0];
     for (int w = 1; w < 4; ++w) mx = red[w] > mx ? red[w] : mx;
-    for (int j = tid; j < nrows; j += 256) att[j] = dev_expf(att[j] - mx);
+    // exp, kept in LDS and, for the segmented softmax sum, in this workgroup's global row (read back through scalar
+    // loads after the barrier below), with each lane's exact partial sums below the segment starts
+    float* erow = escr + (size_t)(t * gridDim.x + h) * escr_stride;
+    const bool seg = nrows >= 128;  // uniform; shorter rows keep the single chain
+    const int Ls = (nrows / 4) & ~15;
+    const Segs4 sg{(nrows - 3 * Ls) & ~15, Ls, nrows};
+    double p1 = 0.0, p2 = 0.0, p3 = 0.0;
+    for (int j = tid; j < nrows; j += 256) {
+        const float e = dev_expf(att[j] - mx);
+        att[j] = e;
+        erow[j] = e;
+        p1 += j < sg.start(1) ? (double)e : 0.0;
+        p2 += j < sg.start(2) ? (double)e : 0.0;
+        p3 += j < sg.start(3) ? (double)e : 0.0;
+    }
+    __shared__ SegShared ssh;
+    if (seg) seg_partials(ssh, p1, p2, p3);
     // first V stage: the cache blocks arrive by DMA (the block holding pos0 carries stale rows from pos0 on,
-    // replaced below), then the chunk's rows that fall inside the stage are written over them
+    // replaced below), then the chunk's rows that fall inside the stage are written over them. The wait also
+    // completes the exp row's stores before the barrier.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     uint16_t* vst16 = reinterpret_cast<uint16_t*>(vst);
@@ -695,11 +790,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const int r = pos0 + e / HD, d = e % HD;
         vst16[((r >> 3) * HD + d) * 8 + (r & 7)] = vloc[(r - pos0) * HD + d];
     }
-    __syncthreads();
-    if (tid == 0)  // softmax sum in position order (ops_ref.cpp:220-224)
-        inv_sh = 1.0f / lds_chain(att, nrows, [](float acc, float a) { return acc + a; });
-    __syncthreads();
-    const float inv = inv_sh;
+    // softmax sum in position order (ops_ref.cpp:220-224); the segmented run's barrier also publishes the V rows
+    auto add = [](float acc, float a) { return acc + a; };
+    float sum;
+    if (seg) {
+        sum = seg_chain_run(ssh, [&](int k, float s0) { return chain_scalar(erow + sg.start(k), sg.len(k), s0, add); });
+    } else {
+        __syncthreads();
+        if (tid == 0) sum_sh = lds_chain(att, nrows, add);
+        __syncthreads();
+        sum = sum_sh;
+    }
+    const float inv = 1.0f / sum;
     for (int j = tid; j < nrows; j += 256) att[j] = att[j] * inv;
     __syncthreads();
 
@@ -931,6 +1033,8 @@ struct Decoder {
     // int8 activations: qa holds a layer's normed input (and the head's), qb the attention / MLP inner activation
     int8_t *qa = nullptr, *qb = nullptr;
     float *da = nullptr, *db = nullptr;
+    float* escr = nullptr;      // attention: one row of exp values per (token, head) workgroup, escr_stride floats
+    int escr_stride = 0;
     int32_t* tokens = nullptr;  // [kChunk] prefill input / [0] decode input
     int* pos = nullptr;         // current position
     int* n_out = nullptr;
@@ -1123,11 +1227,11 @@ hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
     if (hp.head_dim == 64)
         hipLaunchKernelGGL((attention_kernel<64>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                            bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
-                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status);
+                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status);
     else
         hipLaunchKernelGGL((attention_kernel<128>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                            bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
-                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status);
+                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status);
     return hipGetLastError();
 }
 
@@ -1238,6 +1342,8 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
     A((void**)&d->qb, (size_t)kChunk * wide);
     A((void**)&d->da, sizeof(float) * kChunk * (wide / QK));
     A((void**)&d->db, sizeof(float) * kChunk * (wide / QK));
+    d->escr_stride = escr_stride(hp->ctx_len);
+    A((void**)&d->escr, sizeof(float) * (size_t)kChunk * hp->n_heads * d->escr_stride);
     A((void**)&d->tokens, sizeof(int32_t) * kChunk);
     A((void**)&d->pos, 256);
     A((void**)&d->n_out, 256);
