@@ -186,7 +186,9 @@ typedef struct qh_decoder_state {
     int32_t* pos;           /* next position */
     int32_t* n_out;         /* tokens written to the output list since qh_decoder_begin */
     int32_t* token;         /* the token the next step consumes */
-    uint16_t* kcache;       /* [n_layers][ctx_len][n_kv_heads * head_dim] fp16 bits */
+    uint16_t* kcache;       /* [n_layers][n_kv_heads][head_dim / 8][ctx_len][8] fp16 bits: chunks of 8 dimensions
+                               (position p, KV head h, dimension i at ((h * (head_dim / 8) + i / 8) * ctx_len + p) * 8
+                               + i % 8 within its layer) */
     uint16_t* vcache;       /* [n_layers][ceil(ctx_len / 8)][n_kv_heads * head_dim][8] fp16 bits: blocks of 8
                                positions, each dimension's 8 values contiguous (position p, column c at
                                ((p / 8) * kv_dim + c) * 8 + p % 8 within its layer) */

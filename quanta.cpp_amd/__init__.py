@@ -362,7 +362,9 @@ class Decoder:
         """The f16 KV cache bits of one layer, positions [0, n_pos): (k, v) as uint16 [n_pos][n_kv_heads*head_dim]."""
         kvd = self.hp.n_kv_heads * self.hp.head_dim
         ctx = self.desc.ctx_len
-        k = _d2h(self.views.kcache + 2 * layer * ctx * kvd, 2 * n_pos * kvd, np.uint16).reshape(n_pos, kvd)
+        # K is stored in chunks of 8 dimensions, [n_kv_heads][head_dim / 8][ctx][8]
+        rawk = _d2h(self.views.kcache + 2 * layer * ctx * kvd, 2 * ctx * kvd, np.uint16)
+        k = np.ascontiguousarray(rawk.reshape(kvd // 8, ctx, 8)[:, :n_pos].transpose(1, 0, 2).reshape(n_pos, kvd))
         # V is stored in blocks of 8 positions, [pos / 8][kv_dim][8]
         nblk = (n_pos + 7) // 8
         raw = _d2h(self.views.vcache + 2 * layer * ((ctx + 7) // 8 * 8) * kvd, 2 * nblk * 8 * kvd, np.uint16)

@@ -594,8 +594,10 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(float* __restric
 
 // Attention of token t (position pos0 + t) and query head h over positions [0, pos0 + t], for a chunk of n <= 32
 // tokens whose raw projections are q [n][n_heads*HD], k / v [n][n_kv*HD]. One workgroup per (head, token).
-// Cache layouts (f16 bits, per layer): K row-major [pos][n_kv*HD]; V in blocks of 8 positions, [pos/8][n_kv*HD][8],
-// so one 16-byte read gives a lane 8 consecutive positions of its dimension. Rows below pos0 come from the cache; the
+// Cache layouts (f16 bits, per layer): K in 16-byte chunks of 8 dimensions, [n_kv][HD/8][ctx][8], so the lanes of a
+// wave that read chunk c of 64 consecutive positions read 1 KB of contiguous memory (one row per lane, each lane's
+// row complete after HD/8 reads); V in blocks of 8 positions, [pos/8][n_kv*HD][8], so one 16-byte read gives a lane 8
+// consecutive positions of its dimension. Rows below pos0 come from the cache; the
 // chunk's own rows are rebuilt from k / v (bias, RoPE, f16 rounding, exactly as stored), and workgroups of the first
 // query head of each KV group store their token's row. The output (HD values) is quantized straight into oq / od
 // ([n][n_heads*HD] codes, one scale per 32 values).
@@ -628,6 +630,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // V block b of this head: HD uint4 at vbase + b * kvd (in uint4 units, kvd / 8 per position... see vblock())
     const uint4* vc4 = reinterpret_cast<const uint4*>(vc);
     auto vchunk = [&](int blk, int d) { return (size_t)blk * kvd + kvh * HD + d; };  // uint4 index of (block, dim)
+    // K chunk (8 dimensions, 16 bytes) c of position p of this KV head, in 16-byte units: [kv head][HD/8][ctx]
+    auto kchunk = [&](int c, int p) { return ((size_t)kvh * CPR + c) * ctx + p; };
 
     // Global loads in the order the kernel needs them: this thread's cached K rows for the first score rows
     // (registers), then the V blocks of the first stage straight into LDS (DMA, no registers; waited for before the
@@ -637,9 +641,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     v4u kpre[kKPre][CPR];
 #pragma unroll
     for (int r = 0; r < kKPre; ++r) {
-        const uint16_t* kg = kc + (size_t)min(tid + 256 * r, grow) * kvd + kvh * HD;
+        const uint16_t* kg = kc + (kchunk(0, min(tid + 256 * r, grow)) << 3);
 #pragma unroll
-        for (int i = 0; i < CPR; ++i) kpre[r][i] = ld4(kg + i * 8);
+        for (int i = 0; i < CPR; ++i) kpre[r][i] = ld4(kg + (size_t)i * ctx * 8);
     }
     const int ncb = min((pos0 + 7) / 8, kVBlk);  // cache blocks of the first stage (the last may be partial)
     constexpr int kDmaPerBlk = HD / 64;          // 1 KB (one wave instruction) per DMA chunk
@@ -688,7 +692,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     __syncthreads();
     if (h % group == 0)
         for (int i = tid; i < HD; i += 256) {
-            kc[(size_t)pos * kvd + kvh * HD + i] = kloc[t * HD + i];
+            kc[(kchunk(i >> 3, pos) << 3) + (i & 7)] = kloc[t * HD + i];
             vc[vchunk(pos / 8, i) * 8 + (pos & 7)] = vloc[t * HD + i];
         }
 
@@ -742,9 +746,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     for (int j = tid + 256 * kKPre; j < nrows; j += 256) {  // longer contexts: one row at a time
         v4u kk[CPR], kl[CPR];
-        const uint16_t* kg = kc + (size_t)min(j, grow) * kvd + kvh * HD;
+        const uint16_t* kg = kc + (kchunk(0, min(j, grow)) << 3);
 #pragma unroll
-        for (int i = 0; i < CPR; ++i) kk[i] = ld4(kg + i * 8);
+        for (int i = 0; i < CPR; ++i) kk[i] = ld4(kg + (size_t)i * ctx * 8);
         kloc_row(kl, j);
 #pragma unroll
         for (int i = 0; i < CPR; ++i) kk[i] = j < pos0 ? kk[i] : kl[i];
