@@ -33,6 +33,17 @@ _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 _int, _f = C.c_int, C.c_float
 
 
+class SamplerParams(C.Structure):
+    """qo_sampler_params: the reference's SamplerParams (sampler.h) without the seed."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("repeat_penalty", C.c_float), ("repeat_window", C.c_int)]
+
+
+def sampler_params(temperature=0.7, top_k=20, top_p=0.8, min_p=0.0, repeat_penalty=1.1, repeat_window=0):
+    """The reference's defaults (sampler.h, Qwen2.5-Instruct's generation config)."""
+    return SamplerParams(temperature, top_k, top_p, min_p, repeat_penalty, repeat_window)
+
+
 def build(ref: bool | None = None) -> None:
     """Compile liboracle.so, and the reference build too when the reference tree is present."""
     subprocess.run(["make", "-s", "-C", HERE, "oracle"], check=True)
@@ -70,6 +81,10 @@ class _Oracle:
         L.qo_decoder_forward_batch.argtypes = [C.c_void_p, _i32p, _int, _int, _int, C.c_void_p, C.c_void_p, C.c_void_p,
                                                C.c_void_p]
         L.qo_rope_table.argtypes = [_f32p, _int, _int, _f]
+        L.qo_decoder_set_must.argtypes = [C.c_void_p, C.c_void_p, _int]
+        L.qo_sampler_seed.argtypes, L.qo_sampler_seed.restype = [C.c_uint64], C.c_uint64
+        L.qo_sample.argtypes = [_f32p, _int, C.c_void_p, _int, C.POINTER(SamplerParams), C.POINTER(C.c_uint64)]
+        L.qo_sample.restype = _int
 
     def fp16_to_f32(self, h: int) -> float:
         return self.lib.qo_fp16_to_f32(h)
@@ -140,6 +155,18 @@ class _Oracle:
         logits = np.ascontiguousarray(logits, np.float32)
         return self.lib.qo_argmax(logits, logits.size if n is None else n)
 
+    def sampler_seed(self, seed: int) -> int:
+        return int(self.lib.qo_sampler_seed(seed))
+
+    def sample(self, logits, n_valid, history, params: SamplerParams, state: int):
+        """Sampler::sample on a copy of logits; returns (id, penalized logits, next generator state)."""
+        lg = np.array(logits, np.float32, copy=True)
+        hist = np.ascontiguousarray(history, np.int32)
+        st = C.c_uint64(state)
+        tid = self.lib.qo_sample(lg, n_valid, hist.ctypes.data if hist.size else None, hist.size, C.byref(params),
+                                 C.byref(st))
+        return tid, lg, int(st.value)
+
     def shortlist_head(self, head8, head4, err, V, D, xq, xd, top_k=1, n_valid=0, must=None):
         must_arr = np.ascontiguousarray(must if must is not None else [], np.int32)
         logits = np.empty(V, np.float32)
@@ -181,6 +208,12 @@ class Decoder:
         return (np.empty(self.V, np.float32), np.empty(self.D, np.float32), np.empty(self.D, np.int8),
                 np.empty(self.D // QK, np.float32))
 
+    def set_must(self, must):
+        """Must ids of the following head queries (None for none)."""
+        self._must = None if must is None else np.ascontiguousarray(must, np.int32)
+        n = 0 if self._must is None else self._must.size
+        self.lib.qo_decoder_set_must(self.h, self._must.ctypes.data if n else None, n)
+
     def forward(self, token, pos, top_k=1):
         lg, h, q, d = self._outs()
         rows = self.lib.qo_decoder_forward(self.h, token, pos, top_k, lg.ctypes.data, h.ctypes.data, q.ctypes.data,
@@ -216,6 +249,45 @@ class _Ref:
         L.ref_shortlist_head.restype = _int
         L.ref_time_matvec_q.argtypes = [_f32p, _int, _int, _int, _u8p, _i8p, _f32p, _int, _int]
         L.ref_time_matvec_q.restype = C.c_double
+        L.ref_sample.argtypes = [_f32p, _int, C.c_void_p, _int, _f, _int, _f, _f, _f, _int, C.POINTER(C.c_uint64)]
+        L.ref_sample.restype = _int
+        L.ref_model_load.argtypes, L.ref_model_load.restype = [C.c_char_p, _int, _int], C.c_void_p
+        L.ref_model_free.argtypes = [C.c_void_p]
+        L.ref_gen_sampled.argtypes = [C.c_void_p, _i32p, _int, _int, _f, _int, _f, _int, _f, _int, _f, _f, _f, _int,
+                                      C.c_uint64, _i32p, _i32p]
+        L.ref_gen_sampled.restype = _int
+
+    def sample(self, logits, n_valid, history, params: SamplerParams, state: int):
+        """The reference's Sampler::sample on a copy of logits: (id, penalized logits, next generator state)."""
+        lg = np.array(logits, np.float32, copy=True)
+        hist = np.ascontiguousarray(history, np.int32)
+        st = C.c_uint64(state)
+        tid = self.lib.ref_sample(lg, n_valid, hist.ctypes.data if hist.size else None, hist.size, params.temperature,
+                                  params.top_k, params.top_p, params.min_p, params.repeat_penalty,
+                                  params.repeat_window, C.byref(st))
+        return tid, lg, int(st.value)
+
+    def load_model(self, path: str, ctx_len: int, threads: int):
+        m = self.lib.ref_model_load(path.encode(), ctx_len, threads)
+        if not m:
+            raise ValueError(f"the reference could not load {path}")
+        return m
+
+    def free_model(self, m):
+        self.lib.ref_model_free(m)
+
+    def gen_sampled(self, m, ids, n_gen, query: SamplerParams, sampler: SamplerParams, seed: int):
+        """A batched-prefill Session whose head queries follow `query` and whose tokens come from
+        Sampler(sampler, seed): (ids, per-step head rows)."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.zeros(n_gen, np.int32)
+        rows = np.zeros(n_gen, np.int32)
+        n = self.lib.ref_gen_sampled(m, ids, ids.size, n_gen, query.temperature, query.top_k, query.repeat_penalty,
+                                     query.repeat_window, sampler.temperature, sampler.top_k, sampler.top_p,
+                                     sampler.min_p, sampler.repeat_penalty, sampler.repeat_window, seed, out, rows)
+        if n < 0:
+            raise ValueError("prompt does not fit the context")
+        return out[:n], rows[:n]
 
     def fp16_to_f32(self, h: int) -> float:
         return self.lib.ref_fp16_to_f32(h)

@@ -353,6 +353,8 @@ struct qo_decoder {
     int8_t *xq, *hq;
     float *xd, *hd;
     int* rows;
+    const int* must; /* head query must ids (caller-owned), see qo_decoder_set_must */
+    int n_must;
 };
 
 static const void* lt(const qo_decoder* d, int l, int which) { return d->t[2 + l * L_COUNT + which]; }
@@ -513,7 +515,8 @@ static int head(qo_decoder* d, int top_k, float* logits, float* hidden, int8_t* 
         int ns, tie;
         float tau;
         rows = qo_shortlist_head((const uint8_t*)d->t[0], (const uint8_t*)h4, (const uint16_t*)he, V, D, d->xq, d->xd,
-                                 top_k, V, NULL, 0, d->logits, d->coarse, d->upper, d->rows, &ns, &tau, &tie);
+                                 top_k, V, d->must, d->n_must, d->logits, d->coarse, d->upper, d->rows, &ns, &tau,
+                                 &tie);
     } else {
         qo_matvec_q(d->logits, QO_Q8_0, V, D, (const uint8_t*)d->t[0], d->xq, d->xd, 0, V);
         rows = V;
@@ -523,6 +526,11 @@ static int head(qo_decoder* d, int top_k, float* logits, float* hidden, int8_t* 
     if (hq) memcpy(hq, d->xq, (size_t)D);
     if (hd) memcpy(hd, d->xd, sizeof(float) * (size_t)(D / QO_QK));
     return rows;
+}
+
+void qo_decoder_set_must(qo_decoder* d, const int* must, int n_must) {
+    d->must = n_must > 0 ? must : NULL;
+    d->n_must = n_must > 0 ? n_must : 0;
 }
 
 int qo_decoder_forward(qo_decoder* d, int token, int pos, int top_k, float* logits, float* hidden, int8_t* hq,
@@ -540,4 +548,101 @@ int qo_decoder_forward_batch(qo_decoder* d, const int* tokens, int n, int pos0, 
         layers(d, tokens[t], pos0 + t);
     }
     return head(d, top_k, logits, hidden, hq, hd);
+}
+
+/* ------------------------------------------------------------------ sampler (sampler.cpp:10-85, sampler.h) */
+
+/* xorshift64* (sampler.cpp:16-21) and the 24-bit uniform in [0, 1) (sampler.h next_uniform). */
+static uint64_t sampler_next(uint64_t* s) {
+    *s ^= *s >> 12;
+    *s ^= *s << 25;
+    *s ^= *s >> 27;
+    return *s * 0x2545F4914F6CDD1DULL;
+}
+static float sampler_uniform(uint64_t* s) { return (float)(sampler_next(s) >> 40) * (1.0f / 16777216.0f); }
+
+uint64_t qo_sampler_seed(uint64_t seed) { return seed | 1u; }
+
+typedef struct {
+    float v;
+    int id;
+} scored;
+
+/* larger value first, then the lower id */
+static int scored_cmp(const void* a, const void* b) {
+    const scored* x = (const scored*)a;
+    const scored* y = (const scored*)b;
+    if (x->v > y->v) return -1;
+    if (x->v < y->v) return 1;
+    return (x->id > y->id) - (x->id < y->id);
+}
+
+int qo_sample(float* logits, int n_valid, const int* history, int n_hist, const qo_sampler_params* p,
+              uint64_t* state) {
+    if (n_valid <= 0) return -1;
+    /* repetition penalty over the distinct ids of the window (sampler.cpp:23-33) */
+    if (p->repeat_penalty != 1.0f && n_hist > 0) {
+        const int from = (p->repeat_window > 0 && n_hist > p->repeat_window) ? n_hist - p->repeat_window : 0;
+        uint8_t* seen = (uint8_t*)calloc((size_t)n_valid, 1);
+        for (int i = from; i < n_hist; ++i) {
+            const int id = history[i];
+            if (id < 0 || id >= n_valid || seen[id]) continue;
+            seen[id] = 1;
+            const float l = logits[id];
+            logits[id] = l > 0 ? l / p->repeat_penalty : l * p->repeat_penalty;
+        }
+        free(seen);
+    }
+    if (p->temperature <= 0.0f) return qo_argmax(logits, n_valid); /* sampler.cpp:35-37 */
+
+    /* top-k by logit (sampler.cpp:39-50) */
+    scored* c = (scored*)malloc(sizeof(scored) * (size_t)n_valid);
+    for (int i = 0; i < n_valid; ++i) {
+        c[i].v = logits[i];
+        c[i].id = i;
+    }
+    qsort(c, (size_t)n_valid, sizeof(scored), scored_cmp);
+    int k = n_valid;
+    if (p->top_k > 0 && p->top_k < k) k = p->top_k;
+
+    /* softmax with temperature (sampler.cpp:52-59) */
+    const float mx = c[0].v;
+    float sum = 0.f;
+    for (int i = 0; i < k; ++i) {
+        c[i].v = expf((c[i].v - mx) / p->temperature);
+        sum += c[i].v;
+    }
+    for (int i = 0; i < k; ++i) c[i].v /= sum;
+
+    /* min-p, top-p (sampler.cpp:61-75) */
+    int keep = k;
+    if (p->min_p > 0.f) {
+        const float floor_p = c[0].v * p->min_p;
+        while (keep > 1 && c[keep - 1].v < floor_p) --keep;
+    }
+    if (p->top_p < 1.f) {
+        float cum = 0.f;
+        for (int i = 0; i < keep; ++i) {
+            cum += c[i].v;
+            if (cum >= p->top_p) {
+                keep = i + 1;
+                break;
+            }
+        }
+    }
+
+    /* draw (sampler.cpp:77-84) */
+    float total = 0.f;
+    for (int i = 0; i < keep; ++i) total += c[i].v;
+    float r = sampler_uniform(state) * total;
+    int id = c[keep - 1].id;
+    for (int i = 0; i < keep; ++i) {
+        r -= c[i].v;
+        if (r <= 0.f) {
+            id = c[i].id;
+            break;
+        }
+    }
+    free(c);
+    return id;
 }

@@ -92,6 +92,10 @@ typedef struct qo_decoder qo_decoder;
 qo_decoder* qo_decoder_create(const int* hp, const float* hpf, const void* const* tensors, const int* dtypes);
 void qo_decoder_free(qo_decoder* d);
 
+/* The must ids of the head queries of later forward calls (HeadQuery::must, model.h:24-29; Session::head_query,
+ * session.cpp:63-79), NULL / 0 for none. The array stays caller-owned and must outlive those calls. */
+void qo_decoder_set_must(qo_decoder* d, const int* must, int n_must);
+
 /* Model::forward (model.cpp:165-228): one token at position pos; top_k > 0 runs the shortlist head with
  * n_valid = vocab, else the full head. logits [V], hidden [D] (the final normed state), hq / hd its quantization
  * (each may be NULL). Returns the 8-bit head rows read. */
@@ -109,6 +113,28 @@ void qo_decoder_kv(const qo_decoder* d, int l, int n_pos, uint16_t* k, uint16_t*
 /* RoPE table of the reference (ops_ref.cpp:201-214) for positions [0, n_pos): cs[pos][i] = (cosf, sinf) of
  * pos * powf(theta, -2 i / head_dim), i < head_dim / 2, as [n_pos][head_dim / 2][2] floats. */
 void qo_rope_table(float* cs, int n_pos, int head_dim, float theta);
+
+/* ------------------------------------------------------------------ sampler (sampler.cpp:10-85, sampler.h) */
+
+/* SamplerParams (sampler.h) without the seed. */
+typedef struct {
+    float temperature;    /* <= 0: greedy */
+    int top_k;            /* 0 = disabled */
+    float top_p;          /* 1 = disabled */
+    float min_p;          /* 0 = disabled */
+    float repeat_penalty; /* 1 = disabled; divides positive logits, multiplies negative ones */
+    int repeat_window;    /* 0 = the whole history */
+} qo_sampler_params;
+
+/* The generator state Sampler's constructor makes from a nonzero seed (sampler.cpp:10-13). */
+uint64_t qo_sampler_seed(uint64_t seed);
+
+/* Sampler::sample (sampler.cpp:22-85): repetition penalty over the distinct ids of the history window (logits
+ * modified in place), then greedy (first maximum) or top-k, softmax with temperature, min-p, top-p and a draw from
+ * the xorshift64* generator whose state is *state (advanced by one draw). Candidates with equal logits are ordered by
+ * lower id (the reference's std::sort leaves their order unspecified). */
+int qo_sample(float* logits, int n_valid, const int* history, int n_hist, const qo_sampler_params* p,
+              uint64_t* state);
 
 #ifdef __cplusplus
 }

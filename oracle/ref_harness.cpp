@@ -7,8 +7,9 @@
 // the reference's own Tensor / QuantVec / Model objects over caller buffers and call into it.
 //
 // Model::shortlist_head is private and Model has no way to load a hidden state other than by running
-// the decoder, so the Model header is included with `private` widened to `public`; all standard
-// headers it pulls in are included first so the widening reaches only the reference's own classes.
+// the decoder, and Sampler keeps its generator state private, so the Model and Sampler headers are
+// included with `private` widened to `public`; all standard headers they pull in are included first so
+// the widening reaches only the reference's own classes.
 #include <algorithm>
 #include <array>
 #include <chrono>
@@ -29,8 +30,8 @@
 
 #define private public
 #include "model.h"
-#undef private
 #include "sampler.h"
+#undef private
 #include "session.h"
 #include "tokenizer.h"
 
@@ -217,6 +218,63 @@ int ref_gen(void* mp, const int* ids, int n_ids, int n_gen, int* out, int* head_
     s.generate(sampler, n_gen, {}, [&](int id) {
         if (head_rows) head_rows[n] = m->last_head_rows_;
         if (top_logit) top_logit[n] = m->logits_[size_t(id)];
+        out[n++] = id;
+        return true;
+    }, nullptr);
+    return n;
+}
+
+// Sampler::sample (sampler.cpp:22-85) on logits[0, n_valid) (modified in place) with the generator state *state
+// (advanced; the state a Sampler constructed with seed s starts from is s | 1).
+int ref_sample(float* logits, int n_valid, const int* history, int n_hist, float temperature, int top_k, float top_p,
+               float min_p, float repeat_penalty, int repeat_window, uint64_t* state) {
+    quanta::SamplerParams sp;
+    sp.temperature = temperature;
+    sp.top_k = top_k;
+    sp.top_p = top_p;
+    sp.min_p = min_p;
+    sp.repeat_penalty = repeat_penalty;
+    sp.repeat_window = repeat_window;
+    sp.seed = 1;
+    quanta::Sampler s(sp);
+    s.state_ = *state;
+    const int id = s.sample(logits, n_valid, std::vector<int>(history, history + n_hist));
+    *state = s.state_;
+    return id;
+}
+
+// A Session over the model with the batched prefill (session.cpp:13-52): the head queries follow the query
+// parameters q* (Session::set_sampler, session.cpp:63-79: top_k when temperature > 0, else 1; the history window as
+// must ids when the repetition penalty is not 1), the tokens come from Sampler(s*, seed). With q = s this is the chat
+// flow; with a greedy s it is `quanta gen` with sampling options (tools/cli/main.cpp:232-244). Writes the n_gen ids
+// and per step the 8-bit head rows of the forward before it; returns the count (or -1 if the prompt does not fit).
+int ref_gen_sampled(void* mp, const int* ids, int n_ids, int n_gen, float q_temperature, int q_top_k,
+                    float q_repeat_penalty, int q_repeat_window, float s_temperature, int s_top_k, float s_top_p,
+                    float s_min_p, float s_repeat_penalty, int s_repeat_window, uint64_t seed, int* out,
+                    int* head_rows) {
+    auto* m = static_cast<quanta::Model*>(mp);
+    quanta::Tokenizer tok(m->file().tokenizer());
+    quanta::Session s(*m, tok);
+    s.set_batch_prefill(true);
+    quanta::SamplerParams qp;
+    qp.temperature = q_temperature;
+    qp.top_k = q_top_k;
+    qp.repeat_penalty = q_repeat_penalty;
+    qp.repeat_window = q_repeat_window;
+    s.set_sampler(&qp);
+    quanta::SamplerParams sp;
+    sp.temperature = s_temperature;
+    sp.top_k = s_top_k;
+    sp.top_p = s_top_p;
+    sp.min_p = s_min_p;
+    sp.repeat_penalty = s_repeat_penalty;
+    sp.repeat_window = s_repeat_window;
+    sp.seed = seed;
+    quanta::Sampler sampler(sp);
+    if (!s.feed(std::vector<int>(ids, ids + n_ids), nullptr)) return -1;
+    int n = 0;
+    s.generate(sampler, n_gen, {}, [&](int id) {
+        if (head_rows) head_rows[n] = m->last_head_rows_;
         out[n++] = id;
         return true;
     }, nullptr);
