@@ -235,8 +235,12 @@ int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_t
     if (!workspace || workspace_bytes < need)
         return fail(QH_ERR_NOMEM, "qh_shortlist_head: workspace %zu bytes, needs %zu", workspace_bytes, need);
     if (!aligned16(workspace)) return fail(QH_ERR_ALIGN, "qh_shortlist_head: workspace not 16-byte aligned");
-    return check_hip(launch_shortlist_head(*head8, *head4, *err, xq, xd, *query, *out, workspace, as_stream(stream)),
-                     "qh_shortlist_head launch");
+    HeadMust must;
+    must.ids = query->must;
+    must.n = query->n_must;
+    return check_hip(
+        launch_shortlist_head(*head8, *head4, *err, xq, xd, *query, must, *out, workspace, as_stream(stream)),
+        "qh_shortlist_head launch");
 }
 
 int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tensors, qh_decoder** out) {

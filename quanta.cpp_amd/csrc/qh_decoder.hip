@@ -633,9 +633,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // K chunk (8 dimensions, 16 bytes) c of position p of this KV head, in 16-byte units: [kv head][HD/8][ctx]
     auto kchunk = [&](int c, int p) { return ((size_t)kvh * CPR + c) * ctx + p; };
 
-    // Global loads in the order the kernel needs them: this thread's cached K rows for the first score rows
-    // (registers), then the V blocks of the first stage straight into LDS (DMA, no registers; waited for before the
-    // V stage is read), then the chunk's own q / k / v rows below.
+    // this token's q (this head), k and v (its KV head) rows among the chunk's projections
+    const float* qsrc = q + (size_t)t * qd + h * HD;  // row r of k / v: ksrc + r * kvd
+    const float* ksrc = k + kvh * HD;
+    const float* vsrc = v + kvh * HD;
+    const int nk = (t + 1) * HALF, nv = (t + 1) * HD;
+    // q of this head with bias, rotated; keys and values of the chunk's tokens 0..t (model.cpp:183-195, rope
+    // ops_ref.cpp:201-214: a*c - b*s and b*c + a*s with the reference build's contraction fma(a, c, -(b*s)) and
+    // fma(b, c, a*s)). A pair's inputs: the raw values a = row[i], b = row[i + HALF], their biases, cos / sin.
+    struct Pair {
+        float a, b, ba, bb, c, s;
+    };
+    auto load_pair = [&](const float* row, const float* bias, int i, const float* crow) {
+        Pair pr;
+        pr.a = row[i];
+        pr.b = row[i + HALF];
+        pr.ba = bias ? bias[i] : 0.0f;
+        pr.bb = bias ? bias[i + HALF] : 0.0f;
+        pr.c = crow[2 * i];
+        pr.s = crow[2 * i + 1];
+        return pr;
+    };
+    auto rope = [](const Pair& pr, bool has_bias, float& lo, float& hi) {
+        float a = pr.a, b = pr.b;
+        if (has_bias) {
+            a = a + pr.ba;
+            b = b + pr.bb;
+        }
+        lo = __builtin_fmaf(a, pr.c, -(b * pr.s));
+        hi = __builtin_fmaf(b, pr.c, a * pr.s);
+    };
+    const float* bqh = bq ? bq + h * HD : nullptr;
+    const float* bkh = bk ? bk + kvh * HD : nullptr;
+    // The first element of each loop below is loaded first (indices clamped, so every load is unconditional).
+    const int tq = min(tid, HALF - 1);
+    const Pair qp = load_pair(qsrc, bqh, tq, cs + (size_t)pos * HD);
+    const int ek = min(tid, nk - 1), rk = ek / HALF, ik = ek - rk * HALF;
+    const Pair kp0 = load_pair(ksrc + (size_t)rk * kvd, bkh, ik, cs + (size_t)(pos0 + rk) * HD);
+    const int ev = min(tid, nv - 1), rv = ev / HD, iv = ev - rv * HD;
+    const float v0 = vsrc[(size_t)rv * kvd + iv], vb0 = bv ? bv[kvh * HD + iv] : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);
+
+    // This thread's cached K rows for the first score rows (registers) go out behind those (a load waits for every
+    // load issued before it), and their issue, which stalls while the memory pipeline drains, covers the q / k / v
+    // latency. No row read here is written by this launch: K rows stop below pos0.
     constexpr int kKPre = 3;  // score rows per thread loaded up front (768 positions)
     const int grow = pos0 > 0 ? pos0 - 1 : 0;
     v4u kpre[kKPre][CPR];
@@ -645,48 +686,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int i = 0; i < CPR; ++i) kpre[r][i] = ld4(kg + (size_t)i * ctx * 8);
     }
-    const int ncb = min((pos0 + 7) / 8, kVBlk);  // cache blocks of the first stage (the last may be partial)
-    constexpr int kDmaPerBlk = HD / 64;          // 1 KB (one wave instruction) per DMA chunk
-    for (int c = wave; c < ncb * kDmaPerBlk; c += 4)
-        lds_dma16(vc4 + vchunk(c / kDmaPerBlk, (c % kDmaPerBlk) * 64 + lane), vst + c * 64);
 
-    // this token's q (this head), k and v (its KV head) rows among the chunk's projections
-    const float* qsrc = q + (size_t)t * qd + h * HD;  // row r of k / v: ksrc + r * kvd
-    const float* ksrc = k + kvh * HD;
-    const float* vsrc = v + kvh * HD;
-
-    // q of this head with bias, rotated; keys and values of the chunk's tokens 0..t (model.cpp:183-195, rope
-    // ops_ref.cpp:201-214: a*c - b*s and b*c + a*s with the reference build's contraction fma(a, c, -(b*s)) and
-    // fma(b, c, a*s)).
-    if (tid < HALF) {
-        const float* qr = qsrc;
-        float a = qr[tid], b = qr[tid + HALF];
-        if (bq) {
-            a = a + bq[h * HD + tid];
-            b = b + bq[h * HD + tid + HALF];
-        }
-        const float* c = cs + (size_t)pos * HD;
-        const float cc = c[2 * tid], ss = c[2 * tid + 1];
-        qs[tid] = __builtin_fmaf(a, cc, -(b * ss));
-        qs[tid + HALF] = __builtin_fmaf(b, cc, a * ss);
-    }
-    for (int e = tid; e < (t + 1) * HALF; e += 256) {
+    if (tid < HALF) rope(qp, bq != nullptr, qs[tid], qs[tid + HALF]);
+    for (int e = tid; e < nk; e += 256) {
         const int r = e / HALF, i = e - r * HALF;
-        const float* kr = ksrc + (size_t)r * kvd;
-        float a = kr[i], b = kr[i + HALF];
-        if (bk) {
-            a = a + bk[kvh * HD + i];
-            b = b + bk[kvh * HD + i + HALF];
-        }
-        const float* c = cs + (size_t)(pos0 + r) * HD;
-        const float cc = c[2 * i], ss = c[2 * i + 1];
-        kloc[r * HD + i] = f2h(__builtin_fmaf(a, cc, -(b * ss)));
-        kloc[r * HD + i + HALF] = f2h(__builtin_fmaf(b, cc, a * ss));
+        const Pair pr =
+            e == tid ? kp0 : load_pair(ksrc + (size_t)r * kvd, bkh, i, cs + (size_t)(pos0 + r) * HD);
+        float lo, hi;
+        rope(pr, bk != nullptr, lo, hi);
+        kloc[r * HD + i] = f2h(lo);
+        kloc[r * HD + i + HALF] = f2h(hi);
     }
-    for (int e = tid; e < (t + 1) * HD; e += 256) {
+    for (int e = tid; e < nv; e += 256) {
         const int r = e / HD, i = e - r * HD;
-        float val = vsrc[(size_t)r * kvd + i];
-        if (bv) val = val + bv[kvh * HD + i];
+        float val = e == tid ? v0 : vsrc[(size_t)r * kvd + i];
+        if (bv) val = val + (e == tid ? vb0 : bv[kvh * HD + i]);
         vloc[r * HD + i] = f2h(val);
     }
     __syncthreads();
@@ -756,6 +770,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         att[j] = a;
         mx = a > mx ? a : mx;
     }
+    // The V blocks of the first stage go straight into LDS (DMA, no registers; waited for before the V stage is
+    // read) only now: issued behind the K rows they would have held up the scores, and they arrive during the
+    // softmax.
+    const int ncb = min((pos0 + 7) / 8, kVBlk);  // cache blocks of the first stage (the last may be partial)
+    constexpr int kDmaPerBlk = HD / 64;          // 1 KB (one wave instruction) per DMA chunk
+    for (int c = wave; c < ncb * kDmaPerBlk; c += 4)
+        lds_dma16(vc4 + vchunk(c / kDmaPerBlk, (c % kDmaPerBlk) * 64 + lane), vst + c * 64);
     // the maximum does not depend on the order of comparison
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
@@ -1305,7 +1326,7 @@ hipError_t run_head(Decoder* d, int top_k, hipStream_t s) {
     if (top_k > 0 && head4(d).data) {
         qh_head_query q{top_k, d->hp.vocab_size, nullptr, 0};
         qh_head_out out{d->logits, d->coarse, d->upper, d->rows, d->stats};
-        return launch_shortlist_head(h8, head4(d), head_err(d), d->qa, d->da, q, out, d->head_ws, s);
+        return launch_shortlist_head(h8, head4(d), head_err(d), d->qa, d->da, q, HeadMust{}, out, d->head_ws, s);
     }
     QH_TRY(launch_gemv(d->logits, h8, d->qa, d->da, 0, h8.rows, gemv_plan(h8.dtype, h8.cols, h8.rows), s));
     return launch_argmax(d->logits, d->hp.vocab_size, d->top1_full, d->am_ws, s);

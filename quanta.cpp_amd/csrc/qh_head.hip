@@ -8,15 +8,19 @@
 //               Wave 0 owns one row per lane and keeps the workgroup's best top_k+9 eligible keys (score, then
 //               lower row first) sorted across its lanes, inserting only keys above the current cut.
 //  2. seeds     one workgroup: merges the per-workgroup lists (held in registers) into the global top_k+8 seeds
-//               plus one more key to detect a tie at the cut, dedupes the must ids (first occurrence), rescoring
-//               seeds and must rows exactly with the Q8_0 row dot, tau = k-th best exact seed.
+//               plus one more key to detect a tie at the cut, rescores the seeds exactly with the Q8_0 row dot,
+//               tau = k-th best exact seed; lists the must ids' first occurrences (valid, not seeds) in query order
+//               after the seeds: every occurrence proposes its index with an atomic minimum per row, then a block
+//               scan compacts the winners in order.
 //  3. cand      one workgroup per 256 rows: candidates {r < n_valid, unmarked, upper[r] >= tau} compacted with a
-//               ballot scan, appended to the row list, rescored exactly in the same workgroup, and the greedy argmax
-//               key folded in with a 64-bit atomic max; the last workgroup to finish writes the stats record.
+//               ballot scan, appended to the row list, rescored exactly in the same workgroup; the must rows are
+//               split over the workgroups and rescored too; the greedy argmax key is folded in with a 64-bit atomic
+//               max; the last workgroup to finish writes the stats record.
 //
 // Exact rows use the same block products and serial chain as the decode GEMV, so each rescored logit is
 // bit-identical to the full Q8_0 head. The mark array (1 byte per row) lives in the workspace: screen clears its
-// rows, seeds sets 2 (seed) and 3 (must), cand skips every marked row.
+// rows, seeds sets 2 (seed) and 3 (must), cand skips every marked row. With must ids, screen also resets its rows of
+// the first-occurrence array (one int per row) that seeds uses.
 #include "qh_device.h"
 #include "qh_internal.h"
 
@@ -34,7 +38,8 @@ struct HeadCtrl {
     int seed_tie;
 };
 
-constexpr int kMaxMust = 1024;
+constexpr int kMaxMust = 1 << 22;  // must ids per query (a history window); the screen scans them per tile
+constexpr int kNoFirst = 0x7fffffff;
 constexpr int kScreenThreads = 256;
 constexpr int kScreenU = 8;         // 16-byte weight chunks per thread per tile
 constexpr int kScreenMaxRows = 64;  // rows per tile: one per lane of wave 0
@@ -73,7 +78,7 @@ int cand_grid(int nv) {
 }
 
 struct WsLayout {
-    size_t mark, seedpart, ctrl, total;
+    size_t mark, first, seedpart, ctrl, total;
 };
 
 WsLayout ws_layout(int V, int D, int top_k) {
@@ -82,10 +87,24 @@ WsLayout ws_layout(int V, int D, int top_k) {
     const int keep = top_k + 9;
     WsLayout l;
     l.mark = 0;
-    l.seedpart = align256((size_t)V);
+    l.first = align256((size_t)V);
+    l.seedpart = l.first + align256((size_t)V * 4);
     l.ctrl = l.seedpart + align256((size_t)parts * keep * sizeof(uint64_t));
     l.total = l.ctrl + 256;
     return l;
+}
+
+// The must ids a query names, read where the kernel runs (a device-resident history is read at that point).
+__device__ __forceinline__ void must_span(const HeadMust& m, const int32_t*& ids, int& n) {
+    if (m.len_dev) {
+        const int len = *m.len_dev;
+        const int from = (m.window > 0 && len > m.window) ? len - m.window : 0;
+        ids = m.ids + from;
+        n = len > from ? len - from : 0;
+    } else {
+        ids = m.ids;
+        n = m.n;
+    }
 }
 
 // Block products of one Q8_0 row for the calling wave: lane pairs cover 32-byte blocks; p[b] receives
@@ -195,9 +214,9 @@ __device__ __forceinline__ void wave_rank(const uint64_t (&a)[NS], int n, int (&
 
 __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
     const uint8_t* __restrict__ w4, const uint16_t* __restrict__ s4, const uint32_t* __restrict__ e32,
-    const int8_t* __restrict__ xq, const float* __restrict__ xd, int V, int nb, int nv, const int32_t* __restrict__ must,
-    int n_must, int tile, uint32_t nb_magic, float* __restrict__ coarse, float* __restrict__ upper,
-    float* __restrict__ logits, uint8_t* __restrict__ mark, uint64_t* __restrict__ seedpart, int n_keep) {
+    const int8_t* __restrict__ xq, const float* __restrict__ xd, int V, int nb, int nv, HeadMust mq, int tile,
+    uint32_t nb_magic, float* __restrict__ coarse, float* __restrict__ upper, float* __restrict__ logits,
+    uint8_t* __restrict__ mark, int32_t* __restrict__ firsts, uint64_t* __restrict__ seedpart, int n_keep) {
     extern __shared__ float smem[];
     const int ps = prod_stride4(nb);
     const int nb4 = (nb + 3) & ~3;
@@ -214,6 +233,9 @@ __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
     __shared__ uint64_t lvl2[4 * 64];
 
     const int tid = (int)threadIdx.x;
+    const int32_t* must;
+    int n_must;
+    must_span(mq, must, n_must);
     lvl2[tid] = 0ull;  // ordered before its writes by the barriers of the tile loop
     const int ra = (int)((long)blockIdx.x * V / gridDim.x) & ~1;  // even, so error words stay 4-byte aligned
     const int rb = blockIdx.x + 1 == gridDim.x ? V : (int)((long)(blockIdx.x + 1) * V / gridDim.x) & ~1;
@@ -246,6 +268,7 @@ __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
         for (int i = tid; i < nrows; i += kScreenThreads) {
             mf[i] = 0;
             mark[r + i] = 0;
+            if (n_must > 0) firsts[r + i] = kNoFirst;
         }
         __syncthreads();
         if (n_must > 0) {
@@ -349,16 +372,17 @@ __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
 __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
     const uint8_t* __restrict__ w8, const uint16_t* __restrict__ s8, const int8_t* __restrict__ xq,
     const float* __restrict__ xd, int nb, int nv, int k, int n_keep, int n_parts,
-    const uint64_t* __restrict__ seedpart, const int32_t* __restrict__ must, int n_must, uint8_t* __restrict__ mark,
+    const uint64_t* __restrict__ seedpart, HeadMust mq, uint8_t* __restrict__ mark, int32_t* __restrict__ firsts,
     int32_t* __restrict__ rows, float* __restrict__ logits, HeadCtrl* __restrict__ ctrl) {
     extern __shared__ float wprod[];  // [waves][nb]
     constexpr int kWaves = kSeedThreads / 64;
     __shared__ uint64_t best[QH_HEAD_MAX_TOPK + 9];
     __shared__ uint64_t wb[2][kWaves];
     __shared__ uint64_t pool[kSeedMaxPool];
-    __shared__ int rowl[QH_HEAD_MAX_TOPK + 8 + kMaxMust];
-    __shared__ float exact[QH_HEAD_MAX_TOPK + 8 + kMaxMust];
+    __shared__ int rowl[QH_HEAD_MAX_TOPK + 8];
+    __shared__ float exact[QH_HEAD_MAX_TOPK + 8];
     __shared__ int counts[2];
+    __shared__ int wsum[kWaves];
     __shared__ int n_pool;
 
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -451,28 +475,58 @@ __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
             rows[i] = r;
             mark[r] = 2;
         }
-        int nm = 0;
-        for (int i = 0; i < n_must; ++i) {  // first occurrence of each valid id (model.cpp:324-330)
-            const int id = must[i];
-            if (id >= 0 && id < nv && mark[id] == 0) {
-                mark[id] = 3;
-                rowl[ns + nm] = id;
-                rows[ns + nm] = id;
-                ++nm;
-            }
-        }
         counts[0] = ns;
-        counts[1] = nm;
         ctrl->n_seeds = ns;
-        ctrl->n_must = nm;
         ctrl->seed_tie = (ns == n_seed && best[n_seed] != 0 && (best[n_seed] >> 32) == (best[n_seed - 1] >> 32)) ? 1 : 0;
     }
     __syncthreads();
-    const int ns = counts[0], nrow = counts[0] + counts[1];
+    const int ns = counts[0];
+    // The must ids' first occurrences, valid and not seeds, listed after the seeds in query order (model.cpp:324-330;
+    // the candidate kernel rescores them): every such occurrence proposes its index for its row with an atomic
+    // minimum, then each thread takes a run of the list, counts the occurrences that won, and a block scan of the
+    // counts gives each run its place.
+    const int32_t* must;
+    int n_must;
+    must_span(mq, must, n_must);
+    if (n_must > 0) {  // uniform
+        for (int i = tid; i < n_must; i += kSeedThreads) {
+            const int id = must[i];
+            if (id >= 0 && id < nv && mark[id] != 2) atomicMin(&firsts[id], i);
+        }
+        __syncthreads();
+        auto first_at = [&](int i, int id) {
+            return id >= 0 && id < nv && __hip_atomic_load(&firsts[id], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == i;
+        };
+        const int per = (n_must + kSeedThreads - 1) / kSeedThreads;
+        const int i0 = min(n_must, tid * per), i1 = min(n_must, i0 + per);
+        int c = 0;
+        for (int i = i0; i < i1; ++i) c += first_at(i, must[i]) ? 1 : 0;
+        int incl = c;  // inclusive scan over the wave
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int o = __shfl_up(incl, off, 64);
+            incl += lane >= off ? o : 0;
+        }
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        int base = ns;
+        for (int w = 0; w < wave; ++w) base += wsum[w];
+        int o = base + incl - c;
+        for (int i = i0; i < i1; ++i) {
+            const int id = must[i];
+            if (first_at(i, id)) {
+                rows[o++] = id;
+                mark[id] = 3;
+            }
+        }
+        if (tid == kSeedThreads - 1) ctrl->n_must = o - ns;
+    } else if (tid == 0) {
+        ctrl->n_must = 0;
+    }
     float* p = wprod + wave * nb;
-    for (int j0 = 0; j0 < nrow; j0 += kWaves) {
+    for (int j0 = 0; j0 < ns; j0 += kWaves) {
         const int j = j0 + wave;
-        const bool active = j < nrow;
+        const bool active = j < ns;
         const int r = active ? rowl[j] : 0;
         wave_row_products_q8(w8, s8, r, nb, xq, p, active);
         __syncthreads();
@@ -500,7 +554,7 @@ __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
         }
         ctrl->tau = tau;
         uint64_t kmax = 0;
-        for (int i = 0; i < nrow; ++i) {
+        for (int i = 0; i < ns; ++i) {
             const uint64_t kk = score_key(exact[i], rowl[i]);
             kmax = kk > kmax ? kk : kmax;
         }
@@ -577,6 +631,25 @@ __global__ __launch_bounds__(kCandThreads) void head_cand_kernel(
             __syncthreads();
         }
     }
+    {  // the must rows, listed after the seeds, split over the workgroups
+        const int ns = ctrl->n_seeds, nm = ctrl->n_must;
+        const int ma = (int)((long)blockIdx.x * nm / gridDim.x), mb = (int)((long)(blockIdx.x + 1) * nm / gridDim.x);
+        float* p = wprod + wave * nb;
+        for (int j0 = ma; j0 < mb; j0 += kWaves) {  // uniform bounds
+            const int j = j0 + wave;
+            const bool active = j < mb;
+            const int rr = active ? rows[ns + j] : 0;
+            wave_row_products_q8(w8, s8, rr, nb, xq, p, active);
+            __syncthreads();
+            if (active && lane == 0) {
+                const float v = chain(p, xd, nb);
+                logits[rr] = v;
+                const uint64_t kk = score_key(v, rr);
+                kbest = kk > kbest ? kk : kbest;
+            }
+            __syncthreads();
+        }
+    }
     if (lane == 0) wkey[wave] = kbest;
     __syncthreads();
     if (tid == 0) {
@@ -606,14 +679,15 @@ size_t head_workspace_bytes(int V, int D, int top_k) { return ws_layout(V, D, to
 bool head_shape_supported(int D) { return D % 64 == 0 && D <= kMaxHeadCols; }
 
 hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4, const qh_tensor& err,
-                                 const int8_t* xq, const float* xd, const qh_head_query& q, const qh_head_out& out,
-                                 void* ws, hipStream_t s) {
+                                 const int8_t* xq, const float* xd, const qh_head_query& q, const HeadMust& must,
+                                 const qh_head_out& out, void* ws, hipStream_t s) {
     const int V = head8.rows, D = head8.cols, nb = D / QK;
-    if (q.n_must > kMaxMust || !head_shape_supported(D)) return hipErrorInvalidValue;
+    if (must.n > kMaxMust || !head_shape_supported(D)) return hipErrorInvalidValue;
     const int nv = (q.n_valid > 0 && q.n_valid < V) ? q.n_valid : V;
     const WsLayout l = ws_layout(V, D, q.top_k);
     uint8_t* wsb = static_cast<uint8_t*>(ws);
     uint8_t* mark = wsb + l.mark;
+    int32_t* firsts = reinterpret_cast<int32_t*>(wsb + l.first);
     uint64_t* seedpart = reinterpret_cast<uint64_t*>(wsb + l.seedpart);
     HeadCtrl* ctrl = reinterpret_cast<HeadCtrl*>(wsb + l.ctrl);
     const uint8_t* w8 = static_cast<const uint8_t*>(head8.data);
@@ -630,12 +704,12 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
     const size_t lds1 = ((size_t)2 * ((nb + 3) & ~3) + 4 * (size_t)tile * prod_stride4(nb)) * 4 +
                         ((size_t)kScreenMaxShare + 2) * 8 + ((2 * (size_t)tile + 15) & ~size_t(15)) + (size_t)D;
     hipLaunchKernelGGL(head_screen_kernel, dim3(grid), dim3(kScreenThreads), lds1, s, w4, s4, e32, xq, xd, V, nb, nv,
-                       q.must, q.n_must, tile, magic, out.coarse, out.upper, out.logits, mark, seedpart, n_keep);
+                       must, tile, magic, out.coarse, out.upper, out.logits, mark, firsts, seedpart, n_keep);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const size_t lds2 = (size_t)(kSeedThreads / 64) * nb * 4;
     hipLaunchKernelGGL(head_seed_kernel, dim3(1), dim3(kSeedThreads), lds2, s, w8, s8, xq, xd, nb, nv, q.top_k, n_keep,
-                       grid, seedpart, q.must, q.n_must, mark, out.rows, out.logits, ctrl);
+                       grid, seedpart, must, mark, firsts, out.rows, out.logits, ctrl);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     const size_t lds3 = (size_t)(kCandThreads / 64) * nb * 4;

@@ -45,9 +45,19 @@ hipError_t launch_argmax(const float* logits, int n, int32_t* index, void* ws, h
 constexpr int kMaxHeadCols = 4096;
 bool head_shape_supported(int D);
 size_t head_workspace_bytes(int V, int D, int top_k);
+// The must ids of a head query (HeadQuery::must, model.h:24-29): ids[0, n) known on the host, or, with len_dev set,
+// the last `window` ids (all of them when window <= 0) of a device-resident history ids[0, *len_dev), which the
+// kernels read when they run (Session::head_query, session.cpp:63-79), so a captured launch follows the history.
+struct HeadMust {
+    const int32_t* ids = nullptr;
+    int n = 0;
+    const int* len_dev = nullptr;
+    int window = 0;
+};
+// q.must / q.n_must are ignored: the must ids come from `must`.
 hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4, const qh_tensor& err,
-                                 const int8_t* xq, const float* xd, const qh_head_query& q, const qh_head_out& out,
-                                 void* ws, hipStream_t s);
+                                 const int8_t* xq, const float* xd, const qh_head_query& q, const HeadMust& must,
+                                 const qh_head_out& out, void* ws, hipStream_t s);
 
 // GPU-resident decoder (qh_decoder.hip). Tensors in qh_decoder_create order; all sizes validated by the caller.
 struct Decoder;

@@ -111,6 +111,31 @@ def test_shortlist_small_vocab(qh, oracle, synth, gpu, top_k):
     _check_head(qh, oracle, head_np, sl, xq[5], xd[5], V, D, top_k, n_valid=5000, must=must)
 
 
+@pytest.mark.parametrize("top_k", [1, 20])
+def test_shortlist_long_must_list(qh, oracle, synth, gpu, top_k):
+    """A history-sized must list: 3000 ids with many repeats and some out of range. Every first occurrence of a valid
+    id comes back exact, listed after the seeds in query order (the oracle lists them last, in query order)."""
+    V, D = 6007, 896
+    head_np, (h8, h4, he) = _head(qh, synth, gpu, V, D, 41)
+    sl = qh.ShortlistHead(h8, h4, he, top_k=top_k)
+    x = synth.activations(71, 2, D, scale=0.5)
+    xq, xd = qh.quantize_q8(_dev(x, gpu))
+    rng = np.random.default_rng(5)
+    must = rng.integers(-20, V + 20, 3000)
+    must[rng.random(3000) < 0.5] = must[0]
+    for t, n_valid in ((0, 0), (1, 5500)):
+        st, o = _check_head(qh, oracle, head_np, sl, xq[t], xd[t], V, D, top_k, n_valid=n_valid, must=must.tolist())
+        nm = st["n_must"]
+        nv = n_valid if n_valid else V
+        _, first = np.unique(must, return_index=True)
+        expect = [int(must[i]) for i in sorted(first) if 0 <= must[i] < nv]
+        assert nm == len(expect) > 100
+        rows = sl.rows.cpu().numpy()
+        assert rows[st["n_seeds"]:st["n_seeds"] + nm].tolist() == expect == o["rows"][-nm:].tolist()
+    # the same list again with an empty window (the kernels reset what the previous query left)
+    _check_head(qh, oracle, head_np, sl, xq[0], xd[0], V, D, top_k)
+
+
 def test_shortlist_full_vocab(qh, oracle, synth, gpu):
     """The benchmark head: vocab 151936 x 896, k = 1, a few hidden states N(0,1)*0.5."""
     V, D = 151936, 896
