@@ -165,6 +165,38 @@ int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_t
                       const float* xd, const qh_head_query* query, const qh_head_out* out, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------ sampler */
+
+/* The reference's SamplerParams (sampler.h) without the seed: the generator state lives in device memory. */
+typedef struct qh_sampler_params {
+    float temperature;    /* <= 0: greedy (first maximum after the penalty) */
+    int32_t top_k;        /* 0 = disabled */
+    float top_p;          /* 1 = disabled */
+    float min_p;          /* 0 = disabled */
+    float repeat_penalty; /* 1 = disabled; divides positive logits, multiplies negative ones (HF semantics) */
+    int32_t repeat_window; /* how many recent history ids the penalty looks at; 0 = all */
+} qh_sampler_params;
+
+#define QH_SAMPLE_MAX_TOPK 256       /* survivors of the top-k cut the sampler handles (temperature > 0) */
+#define QH_SAMPLE_MAX_VOCAB 262144   /* n_valid limit (the history bitmap lives in LDS) */
+
+/* The generator state a reference Sampler constructed with a nonzero seed starts from (sampler.cpp:10-13). */
+uint64_t qh_sampler_state(uint64_t seed);
+
+/* One draw of Sampler::sample (sampler.cpp:22-85) on DEVICE logits: repetition penalty over the distinct ids of the
+ * history window, then greedy, or top-k, softmax with temperature, min-p, top-p and a draw from the xorshift64*
+ * generator whose state is the DEVICE uint64 *state (advanced by one draw when temperature > 0). The chosen id goes
+ * to the DEVICE int32 *out_id. The logits are not modified (the reference samples from its own copy).
+ *   rows / head_stats: the shortlist head's row list and stats (qh_shortlist_head's out.rows / out.stats), the only
+ *                      ids whose logits are finite; NULL / NULL to consider every id below n_valid.
+ *   history[0, n_hist): DEVICE token history (the session's prompt and generated ids), NULL when n_hist is 0.
+ * Requires 1 <= n_valid <= QH_SAMPLE_MAX_VOCAB and, with temperature > 0, min(top_k or n_valid, n_valid) <=
+ * QH_SAMPLE_MAX_TOPK. Ties between equal logits in the top-k go to the lower id (unspecified in the reference).
+ * Replaces: Sampler::sample (reference sampler.cpp:22-85) and Sampler's generator (sampler.cpp:10-21). */
+int qh_sample(const float* logits, int32_t n_valid, const int32_t* rows, const qh_head_stats* head_stats,
+              const int32_t* history, int32_t n_hist, const qh_sampler_params* params, uint64_t* state,
+              int32_t* out_id, void* stream);
+
 /* ------------------------------------------------------------------ GPU-resident decoder */
 
 /* Model shape (reference engine/src/model_file.h:40-45, HParams) and the context length of the KV cache. */
@@ -194,6 +226,10 @@ typedef struct qh_decoder_state {
                                ((p / 8) * kv_dim + c) * 8 + p % 8 within its layer) */
     int32_t* status;        /* 0, or bit 0: a step ran at a position >= ctx_len (it wrote nothing to the cache);
                                bit 1: a prompt token was outside [0, vocab). Cleared by qh_decoder_prefill. */
+    int32_t* history;       /* [ctx_len + 1]: the token history (the session's history_, session.cpp:13-52): the
+                               prompt ids of every prefill since position 0, then each chosen id */
+    int32_t* history_len;   /* its length */
+    uint64_t* rng_state;    /* the sampler's xorshift64* state */
 } qh_decoder_state;
 
 /* Creates a decoder over device tensors, in this order (reference model.cpp:14-33, 47-58):
@@ -224,6 +260,20 @@ int qh_decoder_begin(qh_decoder* d, int top_k, int32_t* out_dev, int out_cap, vo
 int qh_decoder_step(qh_decoder* d, int top_k, void* stream);
 
 int qh_decoder_views(qh_decoder* d, qh_decoder_state* v);
+
+/* The head queries of later prefill / begin / step calls, as Session::head_query builds them from the session's
+ * sampler parameters (session.cpp:63-79): top_k = (temperature <= 0 ? 1 : p->top_k), the full head when that is 0,
+ * and, when p->repeat_penalty != 1, the last p->repeat_window ids of the token history (all when 0) as must ids. The
+ * calls' own top_k argument is then ignored. NULL restores plain queries (the calls' top_k, no must ids).
+ * Replaces: Session::set_sampler and Session::head_query (reference session.h, session.cpp:63-79). */
+int qh_decoder_set_query(qh_decoder* d, const qh_sampler_params* p);
+
+/* The token qh_decoder_begin and qh_decoder_step choose: NULL (the default) takes the head's greedy top-1; with p,
+ * one qh_sample draw over the head's logits (its row list when the shortlist ran) with the token history, from the
+ * generator state `seed | 1` (seed nonzero). The state lives on the device and advances with each draw, so a captured
+ * step keeps sampling on replay.
+ * Replaces: the Sampler that Session::generate calls (reference sampler.cpp:10-85, session.cpp:32-52). */
+int qh_decoder_set_sampler(qh_decoder* d, const qh_sampler_params* p, uint64_t seed);
 
 #ifdef __cplusplus
 }

@@ -50,7 +50,19 @@ class qh_model_desc(C.Structure):
 
 class qh_decoder_state(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("logits", "hidden", "xq", "xd", "stats", "top1_full", "pos", "n_out",
-                                          "token", "kcache", "vcache", "status")]
+                                          "token", "kcache", "vcache", "status", "history", "history_len",
+                                          "rng_state")]
+
+
+class qh_sampler_params(C.Structure):
+    """The reference's SamplerParams (sampler.h) without the seed."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("repeat_penalty", C.c_float), ("repeat_window", C.c_int32)]
+
+
+def sampler_params(temperature=0.7, top_k=20, top_p=0.8, min_p=0.0, repeat_penalty=1.1, repeat_window=0):
+    """qh_sampler_params with the reference's defaults (sampler.h: Qwen2.5-Instruct's generation config)."""
+    return qh_sampler_params(temperature, top_k, top_p, min_p, repeat_penalty, repeat_window)
 
 
 # Every symbol include/quanta_hip.h declares, in header order.
@@ -59,8 +71,9 @@ EXPORTS = ("qh_last_error", "qh_version", "qh_init", "qh_quant_bytes", "qh_tenso
            "qh_stream_create", "qh_stream_destroy",
            "qh_quantize_q8", "qh_matvec_q", "qh_matmul_q", "qh_argmax_workspace_bytes", "qh_argmax",
            "qh_shortlist_workspace_bytes",
-           "qh_shortlist_head", "qh_decoder_create", "qh_decoder_destroy", "qh_decoder_prefill", "qh_decoder_begin",
-           "qh_decoder_step", "qh_decoder_views")
+           "qh_shortlist_head", "qh_sampler_state", "qh_sample", "qh_decoder_create", "qh_decoder_destroy",
+           "qh_decoder_prefill", "qh_decoder_begin", "qh_decoder_step", "qh_decoder_views", "qh_decoder_set_query",
+           "qh_decoder_set_sampler")
 
 
 def build() -> None:
@@ -91,6 +104,10 @@ def _bind(lib):
         "qh_decoder_begin": ([vp, i32, vp, i32, vp], i32),
         "qh_decoder_step": ([vp, i32, vp], i32),
         "qh_decoder_views": ([vp, C.POINTER(qh_decoder_state)], i32),
+        "qh_sampler_state": ([C.c_uint64], C.c_uint64),
+        "qh_sample": ([vp, i32, vp, vp, vp, i32, C.POINTER(qh_sampler_params), vp, vp, vp], i32),
+        "qh_decoder_set_query": ([vp, C.POINTER(qh_sampler_params)], i32),
+        "qh_decoder_set_sampler": ([vp, C.POINTER(qh_sampler_params), C.c_uint64], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -209,6 +226,25 @@ class Argmax:
 
 def argmax(logits, n: int | None = None):
     return Argmax(logits.numel(), device=logits.device)(logits, n)
+
+
+def sampler_state(seed: int) -> int:
+    """The generator state a reference Sampler constructed with a nonzero seed starts from."""
+    return int(lib().qh_sampler_state(seed))
+
+
+def sample(logits, params: qh_sampler_params, state, history=None, n_valid: int | None = None, head=None):
+    """One Sampler::sample draw on the device: returns the chosen id as a device int32 tensor of one element.
+    state: device uint64 tensor of one element (advanced in place); history: device int32 tensor or None;
+    head: a ShortlistHead whose last call's row list and stats restrict the candidates."""
+    torch = _torch()
+    out = torch.empty(1, dtype=torch.int32, device=logits.device)
+    nv = logits.numel() if n_valid is None else n_valid
+    nh = 0 if history is None else int(history.numel())
+    _check(lib().qh_sample(_ptr(logits), nv, _ptr(head.rows) if head is not None else None,
+                           _ptr(head.stats_dev) if head is not None else None, _ptr(history) if nh else None, nh,
+                           C.byref(params), _ptr(state), _ptr(out), _stream()))
+    return out
 
 
 class ShortlistHead:
@@ -335,6 +371,21 @@ class Decoder:
 
     def step(self, top_k: int = 1):
         _check(lib().qh_decoder_step(self.h, top_k, _stream()))
+
+    def set_query(self, params: qh_sampler_params | None):
+        """Head queries as Session::head_query builds them from these sampler parameters (None: plain queries)."""
+        self._qp = params
+        _check(lib().qh_decoder_set_query(self.h, C.byref(params) if params is not None else None))
+
+    def set_sampler(self, params: qh_sampler_params | None, seed: int = 1):
+        """Tokens from Sampler::sample with these parameters and seed (None: the head's greedy top-1)."""
+        self._sp = params
+        _check(lib().qh_decoder_set_sampler(self.h, C.byref(params) if params is not None else None, seed))
+
+    def history(self):
+        """The token history (prompt ids since position 0, then each chosen id)."""
+        n = int(_d2h(self.views.history_len, 4, np.int32)[0])
+        return _d2h(self.views.history, 4 * n, np.int32) if n else np.zeros(0, np.int32)
 
     # host copies of the device state (synchronous)
     def stats(self) -> dict:

@@ -53,6 +53,20 @@ int validate_range(int rows, int r0, int r1, const char* what) {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
+// The sampler parameters the device sampler handles (a finite temperature; at most QH_SAMPLE_MAX_TOPK survivors of
+// the top-k cut when sampling).
+int check_sampler(const qh_sampler_params& p, int n_valid, const char* who) {
+    if (!(p.temperature == p.temperature) || !(p.repeat_penalty > 0.0f) || p.top_k < 0 || p.repeat_window < 0)
+        return fail(QH_ERR_ARG, "%s: bad sampler parameters", who);
+    if (p.temperature > 0.0f) {
+        const int k = (p.top_k > 0 && p.top_k < n_valid) ? p.top_k : n_valid;
+        if (k > QH_SAMPLE_MAX_TOPK)
+            return fail(QH_ERR_UNSUPPORTED, "%s: %d survivors of the top-k cut (at most %d)", who, k,
+                        QH_SAMPLE_MAX_TOPK);
+    }
+    return QH_OK;
+}
+
 // Device checks of qh_init for the current device (gfx950), once per device.
 int qh_init_current() {
     int dev = 0;
@@ -204,6 +218,30 @@ int qh_argmax(const float* logits, int n, int32_t* index, void* workspace, size_
     return check_hip(launch_argmax(logits, n, index, workspace, as_stream(stream)), "qh_argmax launch");
 }
 
+uint64_t qh_sampler_state(uint64_t seed) { return seed | 1u; }
+
+int qh_sample(const float* logits, int32_t n_valid, const int32_t* rows, const qh_head_stats* head_stats,
+              const int32_t* history, int32_t n_hist, const qh_sampler_params* params, uint64_t* state,
+              int32_t* out_id, void* stream) {
+    if (!logits || !params || !state || !out_id) return fail(QH_ERR_ARG, "qh_sample: null argument");
+    if (n_valid < 1 || n_valid > QH_SAMPLE_MAX_VOCAB)
+        return fail(QH_ERR_UNSUPPORTED, "qh_sample: n_valid %d outside [1, %d]", n_valid, QH_SAMPLE_MAX_VOCAB);
+    if ((rows == nullptr) != (head_stats == nullptr))
+        return fail(QH_ERR_ARG, "qh_sample: rows and head_stats go together");
+    if (n_hist < 0 || (n_hist > 0 && !history)) return fail(QH_ERR_ARG, "qh_sample: bad history");
+    if (int rc = check_sampler(*params, n_valid, "qh_sample")) return rc;
+    HeadMust hist;
+    hist.ids = history;
+    hist.n = n_hist;
+    hist.window = 0;
+    if (params->repeat_window > 0 && n_hist > params->repeat_window) {  // the window, as sampler.cpp:24-27
+        hist.ids = history + (n_hist - params->repeat_window);
+        hist.n = params->repeat_window;
+    }
+    return check_hip(launch_sample(logits, n_valid, rows, head_stats, hist, *params, state, out_id, as_stream(stream)),
+                     "qh_sample launch");
+}
+
 size_t qh_shortlist_workspace_bytes(int V, int D, int top_k) {
     if (V <= 0 || D <= 0 || top_k <= 0 || top_k > QH_HEAD_MAX_TOPK || !head_shape_supported(D)) return 0;
     return head_workspace_bytes(V, D, top_k);
@@ -324,6 +362,30 @@ int qh_decoder_views(qh_decoder* d, qh_decoder_state* v) {
     if (!d || !v) return fail(QH_ERR_ARG, "qh_decoder_views: null argument");
     decoder_views(reinterpret_cast<Decoder*>(d), v);
     return QH_OK;
+}
+
+int qh_decoder_set_query(qh_decoder* d, const qh_sampler_params* p) {
+    if (!d) return fail(QH_ERR_ARG, "qh_decoder_set_query: null decoder");
+    if (p) {
+        if (!(p->repeat_penalty > 0.0f) || p->repeat_window < 0 || p->top_k < 0 || !(p->temperature == p->temperature))
+            return fail(QH_ERR_ARG, "qh_decoder_set_query: bad parameters");
+        if (p->temperature > 0.0f && p->top_k > QH_HEAD_MAX_TOPK)
+            return fail(QH_ERR_UNSUPPORTED, "qh_decoder_set_query: top_k %d above %d", p->top_k, QH_HEAD_MAX_TOPK);
+    }
+    decoder_set_query(reinterpret_cast<Decoder*>(d), p);
+    return QH_OK;
+}
+
+int qh_decoder_set_sampler(qh_decoder* d, const qh_sampler_params* p, uint64_t seed) {
+    if (!d) return fail(QH_ERR_ARG, "qh_decoder_set_sampler: null decoder");
+    if (p) {
+        if (seed == 0) return fail(QH_ERR_ARG, "qh_decoder_set_sampler: seed must be nonzero");
+        const int V = decoder_vocab(reinterpret_cast<Decoder*>(d));
+        if (V > QH_SAMPLE_MAX_VOCAB)
+            return fail(QH_ERR_UNSUPPORTED, "qh_decoder_set_sampler: vocab %d above %d", V, QH_SAMPLE_MAX_VOCAB);
+        if (int rc = check_sampler(*p, V, "qh_decoder_set_sampler")) return rc;
+    }
+    return check_hip(decoder_set_sampler(reinterpret_cast<Decoder*>(d), p, seed), "qh_decoder_set_sampler");
 }
 
 }  // extern "C"

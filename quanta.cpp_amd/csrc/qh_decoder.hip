@@ -1019,28 +1019,44 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(const float* __restrict
 // Prefill / decode bookkeeping on the device.
 __global__ void set_int_kernel(int* p, int value) { *p = value; }
 
-// After a decode step: the chosen token becomes the next input, is appended to out[] and the position advances.
-__global__ void advance_kernel(const qh_head_stats* __restrict__ stats, const int32_t* __restrict__ top1_full,
-                               int32_t* __restrict__ token, int* __restrict__ pos_dev, int* __restrict__ n_out,
-                               int32_t* __restrict__ out, int out_cap) {
-    const int id = stats ? stats->top1 : *top1_full;
+// The token a step chose: the sampler's pick when there is one, else the head's greedy top-1.
+struct Pick {
+    const int32_t* sampled;
+    const qh_head_stats* stats;
+    const int32_t* top1_full;
+    __device__ __forceinline__ int id() const { return sampled ? *sampled : stats ? stats->top1 : *top1_full; }
+};
+
+// The chosen token becomes the next input, is appended to out[] and to the token history (session.cpp:45-46), and,
+// after a decode step (advance), the position moves on.
+__global__ void advance_kernel(Pick pick, int32_t* __restrict__ token, int* __restrict__ pos_dev,
+                               int* __restrict__ n_out, int32_t* __restrict__ out, int out_cap,
+                               int32_t* __restrict__ hist, int* __restrict__ hist_len, int hist_cap, int advance) {
+    const int id = pick.id();
     *token = id;
     const int k = *n_out;
     if (k < out_cap) out[k] = id;
     *n_out = k + 1;
-    *pos_dev = *pos_dev + 1;
+    const int h = *hist_len;
+    if (h < hist_cap) {
+        hist[h] = id;
+        *hist_len = h + 1;
+    }
+    if (advance) *pos_dev = *pos_dev + 1;
 }
 
-// Chooses the first generated token from the prefill's head (the reference samples it from the prompt's logits,
-// session.cpp:39-41): copies it to the decode input without advancing the position.
-__global__ void first_token_kernel(const qh_head_stats* __restrict__ stats, const int32_t* __restrict__ top1_full,
-                                   int32_t* __restrict__ token, int* __restrict__ n_out, int32_t* __restrict__ out,
-                                   int out_cap) {
-    const int id = stats ? stats->top1 : *top1_full;
-    *token = id;
-    const int k = *n_out;
-    if (k < out_cap) out[k] = id;
-    *n_out = k + 1;
+// Appends a prompt chunk to the token history (Session::feed, session.cpp:13-30), first emptying it when the chunk
+// starts a sequence (reset). One workgroup.
+__global__ __launch_bounds__(256) void history_append_kernel(const int32_t* __restrict__ tokens, int n, int reset,
+                                                             int32_t* __restrict__ hist, int* __restrict__ hist_len,
+                                                             int hist_cap) {
+    __shared__ int base;
+    if (threadIdx.x == 0) base = reset ? 0 : *hist_len;
+    __syncthreads();
+    const int b = base;
+    for (int i = (int)threadIdx.x; i < n; i += 256)
+        if (b + i < hist_cap) hist[b + i] = tokens[i];
+    if (threadIdx.x == 0) *hist_len = b + n < hist_cap ? b + n : hist_cap;
 }
 
 }  // namespace
@@ -1061,6 +1077,13 @@ struct Decoder {
     float* escr = nullptr;      // attention: one row of exp values per (token, head) workgroup, escr_stride floats
     int escr_stride = 0;
     int32_t* tokens = nullptr;  // [kChunk] prefill input / [0] decode input
+    // token history (prompt ids since position 0, then each chosen id) and the optional query / sampler settings
+    int32_t* hist = nullptr;  // [ctx_len + 1]
+    int* hist_len = nullptr;
+    bool has_query = false, has_sampler = false;
+    qh_sampler_params qp{}, sp{};
+    uint64_t* rng = nullptr;
+    int32_t* sampled = nullptr;
     int* pos = nullptr;         // current position
     int* n_out = nullptr;
     int* status = nullptr;
@@ -1321,12 +1344,32 @@ hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
 }
 
 // The head on the quantized final hidden state in qa / da; top_k > 0 uses the shortlist.
+// The head query of a forward (Session::head_query, session.cpp:63-79): with a query set, top_k follows its
+// temperature and top_k, and its repetition penalty makes the history window the must ids; else the caller's top_k.
+int query_top_k(const Decoder* d, int top_k) {
+    if (!d->has_query) return top_k;
+    return d->qp.temperature <= 0.f ? 1 : d->qp.top_k;
+}
+
+// The token history as a device-resident id list: its last `window` ids (all when window <= 0).
+HeadMust history_window(const Decoder* d, int window) {
+    HeadMust m;
+    m.ids = d->hist;
+    m.len_dev = d->hist_len;
+    m.window = window;
+    return m;
+}
+
+bool shortlist_on(const Decoder* d, int top_k) { return query_top_k(d, top_k) > 0 && head4(d).data; }
+
 hipError_t run_head(Decoder* d, int top_k, hipStream_t s) {
     const qh_tensor& h8 = d->t[T_EMBED];
-    if (top_k > 0 && head4(d).data) {
-        qh_head_query q{top_k, d->hp.vocab_size, nullptr, 0};
+    if (shortlist_on(d, top_k)) {
+        qh_head_query q{query_top_k(d, top_k), d->hp.vocab_size, nullptr, 0};
         qh_head_out out{d->logits, d->coarse, d->upper, d->rows, d->stats};
-        return launch_shortlist_head(h8, head4(d), head_err(d), d->qa, d->da, q, HeadMust{}, out, d->head_ws, s);
+        const HeadMust must = d->has_query && d->qp.repeat_penalty != 1.f ? history_window(d, d->qp.repeat_window)
+                                                                           : HeadMust{};
+        return launch_shortlist_head(h8, head4(d), head_err(d), d->qa, d->da, q, must, out, d->head_ws, s);
     }
     QH_TRY(launch_gemv(d->logits, h8, d->qa, d->da, 0, h8.rows, gemv_plan(h8.dtype, h8.cols, h8.rows), s));
     return launch_argmax(d->logits, d->hp.vocab_size, d->top1_full, d->am_ws, s);
@@ -1370,6 +1413,10 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
     d->escr_stride = escr_stride(hp->ctx_len);
     A((void**)&d->escr, sizeof(float) * (size_t)kChunk * hp->n_heads * d->escr_stride);
     A((void**)&d->tokens, sizeof(int32_t) * kChunk);
+    A((void**)&d->hist, sizeof(int32_t) * ((size_t)hp->ctx_len + 1));
+    A((void**)&d->hist_len, 256);
+    A((void**)&d->rng, 256);
+    A((void**)&d->sampled, 256);
     A((void**)&d->pos, 256);
     A((void**)&d->n_out, 256);
     A((void**)&d->status, 256);
@@ -1398,7 +1445,7 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
             cs[((size_t)p * half + i) * 2 + 1] = sinf(angle);
         }
     e = hipMemcpy(d->cs, cs.data(), sizeof(float) * cs.size(), hipMemcpyHostToDevice);
-    for (int* p : {d->n_out, d->pos, d->status})
+    for (int* p : {d->n_out, d->pos, d->status, d->hist_len})
         if (e == hipSuccess) e = hipMemset(p, 0, 256);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -1420,6 +1467,9 @@ hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, i
     const int D = hp.dim;
     hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, s, d->status, 0);
     QH_TRY(hipGetLastError());
+    hipLaunchKernelGGL(history_append_kernel, dim3(1), dim3(256), 0, s, tokens, n, pos0 == 0 ? 1 : 0, d->hist,
+                       d->hist_len, hp.ctx_len + 1);
+    QH_TRY(hipGetLastError());
     int last = 0;
     for (int c0 = 0; c0 < n; c0 += kChunk) {
         const int m = n - c0 < kChunk ? n - c0 : kChunk;
@@ -1438,13 +1488,25 @@ hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, i
     return hipGetLastError();
 }
 
+// Picks the token from the last head call (the sampler when one is set) and feeds it back (advance: a decode step).
+hipError_t pick_and_advance(Decoder* d, int top_k, bool advance, hipStream_t s) {
+    const bool sl = shortlist_on(d, top_k);
+    Pick pick{nullptr, sl ? d->stats : nullptr, d->top1_full};
+    if (d->has_sampler) {
+        const HeadMust hist = d->sp.repeat_penalty != 1.f ? history_window(d, d->sp.repeat_window) : HeadMust{};
+        QH_TRY(launch_sample(d->logits, d->hp.vocab_size, sl ? d->rows : nullptr, sl ? d->stats : nullptr, hist,
+                             d->sp, d->rng, d->sampled, s));
+        pick.sampled = d->sampled;
+    }
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, pick, d->tokens, d->pos, d->n_out, d->out,
+                       d->out_cap, d->hist, d->hist_len, d->hp.ctx_len + 1, advance ? 1 : 0);
+    return hipGetLastError();
+}
+
 hipError_t decoder_step(Decoder* d, int top_k, hipStream_t s) {
     QH_TRY(decode_layers(d, s));
     QH_TRY(run_head(d, top_k, s));
-    const bool sl = top_k > 0 && head4(d).data;
-    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, sl ? d->stats : nullptr, d->top1_full, d->tokens,
-                       d->pos, d->n_out, d->out, d->out_cap);
-    return hipGetLastError();
+    return pick_and_advance(d, top_k, true, s);
 }
 
 hipError_t decoder_begin(Decoder* d, int top_k, int32_t* out, int out_cap, hipStream_t s) {
@@ -1452,10 +1514,7 @@ hipError_t decoder_begin(Decoder* d, int top_k, int32_t* out, int out_cap, hipSt
     d->out_cap = out_cap;
     hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, s, d->n_out, 0);
     QH_TRY(hipGetLastError());
-    const bool sl = top_k > 0 && head4(d).data;
-    hipLaunchKernelGGL(first_token_kernel, dim3(1), dim3(1), 0, s, sl ? d->stats : nullptr, d->top1_full, d->tokens,
-                       d->n_out, d->out, d->out_cap);
-    return hipGetLastError();
+    return pick_and_advance(d, top_k, false, s);
 }
 
 int decoder_ctx(const Decoder* d) { return d->hp.ctx_len; }
@@ -1473,6 +1532,25 @@ void decoder_views(Decoder* d, qh_decoder_state* v) {
     v->kcache = d->kc;
     v->vcache = d->vc;
     v->status = d->status;
+    v->history = d->hist;
+    v->history_len = d->hist_len;
+    v->rng_state = d->rng;
+}
+
+int decoder_vocab(const Decoder* d) { return d->hp.vocab_size; }
+
+int decoder_set_query(Decoder* d, const qh_sampler_params* p) {
+    d->has_query = p != nullptr;
+    if (p) d->qp = *p;
+    return 0;
+}
+
+hipError_t decoder_set_sampler(Decoder* d, const qh_sampler_params* p, uint64_t seed) {
+    d->has_sampler = p != nullptr;
+    if (!p) return hipSuccess;
+    d->sp = *p;
+    const uint64_t st = seed | 1u;  // Sampler's constructor (sampler.cpp:10-13)
+    return hipMemcpy(d->rng, &st, sizeof st, hipMemcpyHostToDevice);
 }
 
 }  // namespace qh

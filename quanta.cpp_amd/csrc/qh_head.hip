@@ -94,19 +94,6 @@ WsLayout ws_layout(int V, int D, int top_k) {
     return l;
 }
 
-// The must ids a query names, read where the kernel runs (a device-resident history is read at that point).
-__device__ __forceinline__ void must_span(const HeadMust& m, const int32_t*& ids, int& n) {
-    if (m.len_dev) {
-        const int len = *m.len_dev;
-        const int from = (m.window > 0 && len > m.window) ? len - m.window : 0;
-        ids = m.ids + from;
-        n = len > from ? len - from : 0;
-    } else {
-        ids = m.ids;
-        n = m.n;
-    }
-}
-
 // Block products of one Q8_0 row for the calling wave: lane pairs cover 32-byte blocks; p[b] receives
 // float(s_b) * f16(scale_b). Every lane of the wave must call it (DPP inside); `active` masks the work.
 __device__ void wave_row_products_q8(const uint8_t* __restrict__ w8, const uint16_t* __restrict__ s8, int row, int nb,

@@ -54,10 +54,31 @@ struct HeadMust {
     const int* len_dev = nullptr;
     int window = 0;
 };
+#if defined(__HIPCC__)
+// The must ids a query names, read where the kernel runs (a device-resident history is read at that point).
+__device__ __forceinline__ void must_span(const HeadMust& m, const int32_t*& ids, int& n) {
+    if (m.len_dev) {
+        const int len = *m.len_dev;
+        const int from = (m.window > 0 && len > m.window) ? len - m.window : 0;
+        ids = m.ids + from;
+        n = len > from ? len - from : 0;
+    } else {
+        ids = m.ids;
+        n = m.n;
+    }
+}
+#endif
 // q.must / q.n_must are ignored: the must ids come from `must`.
 hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4, const qh_tensor& err,
                                  const int8_t* xq, const float* xd, const qh_head_query& q, const HeadMust& must,
                                  const qh_head_out& out, void* ws, hipStream_t s);
+
+// Sampler::sample on the device (qh_sample.hip). Candidates: rows[0, hs->n_rows) (the shortlist head's list; every
+// other id counts as -inf) or, with rows null, every id below n_valid; the penalty looks at the ids `hist` names.
+// Requires 1 <= n_valid <= QH_SAMPLE_MAX_VOCAB, and with temperature > 0 at most QH_SAMPLE_MAX_TOPK survivors.
+hipError_t launch_sample(const float* logits, int n_valid, const int32_t* rows, const qh_head_stats* hs,
+                         const HeadMust& hist, const qh_sampler_params& p, uint64_t* state, int32_t* out_id,
+                         hipStream_t s);
 
 // GPU-resident decoder (qh_decoder.hip). Tensors in qh_decoder_create order; all sizes validated by the caller.
 struct Decoder;
@@ -67,6 +88,9 @@ hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, i
 hipError_t decoder_begin(Decoder* d, int top_k, int32_t* out, int out_cap, hipStream_t s);
 hipError_t decoder_step(Decoder* d, int top_k, hipStream_t s);
 void decoder_views(Decoder* d, qh_decoder_state* v);
+int decoder_set_query(Decoder* d, const qh_sampler_params* p);
+hipError_t decoder_set_sampler(Decoder* d, const qh_sampler_params* p, uint64_t seed);
+int decoder_vocab(const Decoder* d);
 int decoder_ctx(const Decoder* d);
 
 }  // namespace qh

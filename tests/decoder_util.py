@@ -10,3 +10,46 @@ def qnt_module():
 
 def oracle_decoder(oracle, hp, tensors, ctx_len=None):
     return oracle.decoder_for(hp, tensors, ctx_len)
+
+
+def must_window(hist, params):
+    """Session::head_query's must ids (session.cpp:63-79): the history window when the penalty is on, else None."""
+    if params is None or params.repeat_penalty == 1.0:
+        return None
+    w = params.repeat_window
+    return list(hist[-w:]) if (w > 0 and len(hist) > w) else list(hist)
+
+
+def query_top_k(params, default=1):
+    """Session::head_query's top_k: 1 when greedy, else the sampler's top_k (0 means the full head)."""
+    if params is None:
+        return default
+    return 1 if params.temperature <= 0 else params.top_k
+
+
+def oracle_session(oracle, dec, prompt, n_gen, query, sampler, seed, vocab):
+    """The oracle's restatement of a batched-prefill Session (session.cpp:13-52): Session::feed, then
+    Session::generate with Sampler(sampler, seed) (None: greedy argmax), head queries built from `query`.
+    Returns the n_gen chosen ids; out[0] comes from the prompt's logits, out[i] from the forward of out[i-1]."""
+    import numpy as np
+    hist = [int(t) for t in prompt]
+    k = query_top_k(query)
+    dec.set_must(must_window(hist, query))
+    r = dec.forward_batch(np.asarray(prompt, np.int32), 0, top_k=k)
+    state = oracle.sampler_seed(seed)
+    out = []
+    pos = len(prompt)
+    for i in range(n_gen):
+        if sampler is None:
+            tid = oracle.argmax(r["logits"], vocab)
+        else:
+            tid, _, state = oracle.sample(r["logits"], vocab, np.asarray(hist, np.int32), sampler, state)
+        out.append(tid)
+        hist.append(tid)
+        if i + 1 == n_gen:
+            break
+        dec.set_must(must_window(hist, query))
+        r = dec.forward(tid, pos, top_k=k)
+        pos += 1
+    dec.set_must(None)
+    return out, state

@@ -14,8 +14,13 @@ build, so it runs only where the reference tree is mounted; the .npz files are d
                   the per-step head rows and logit bits still depend on every operation of every forward.)
   e2e_small.npz   a 2-layer, vocab-4096 model of the same widths (seed 7): 40-id prompt, 24 generated ids, and after
                   the prefill and every decode step the final normed hidden state and its int8 quantization.
+  e2e_sampled.npz the benchmark model and prompt in sampling mode, through the reference's Session with the batched
+                  prefill: "chat" (head queries and draws from the reference's default SamplerParams -- temperature
+                  0.7, top-k 20, top-p 0.8, repetition penalty 1.1 over the whole history -- and seed 0x51A7C0DE)
+                  and "gen" (`quanta gen --top-k 20 --repeat-penalty 1.1`: top-k 20 queries with the history as
+                  must ids, greedy picks): 256 ids each and the 8-bit head rows of the forward before each pick.
 
-Usage: python tests/golden/make_e2e_golden.py [--small-only]
+Usage: python tests/golden/make_e2e_golden.py [--small-only | --sampled-only]
 """
 import ctypes as C
 import hashlib
@@ -118,14 +123,42 @@ def make_full(qnt, L):
     os.remove(path)
 
 
+SAMPLED_SEED = 0x51A7C0DE
+
+
+def make_sampled(qnt):
+    hp = qnt.HParams()
+    path = "/tmp/quanta_e2e_q4mix.qnt"
+    tens = qnt.synthetic_q4mix(5, hp)
+    qnt.write_qnt(path, hp, tens)
+    ids = np.random.default_rng(9).integers(0, hp.vocab_size, 512).astype(np.int32)
+    chat = oracle.sampler_params()
+    greedy = oracle.sampler_params(temperature=0.0, repeat_penalty=1.0)
+    gen_q = oracle.sampler_params(top_k=20, repeat_penalty=1.1)
+    res = {}
+    for name, (q, sp) in {"chat": (chat, chat), "gen": (gen_q, greedy)}.items():
+        m = oracle.ref.load_model(path, 4096, 8)
+        out, rows = oracle.ref.gen_sampled(m, ids, 256, q, sp, SAMPLED_SEED)
+        oracle.ref.free_model(m)
+        assert len(out) == 256
+        res[name + "_out"] = out
+        res[name + "_rows"] = rows
+    np.savez_compressed(os.path.join(HERE, "e2e_sampled.npz"), seed=np.int32(5), prompt=ids,
+                        sampler_seed=np.uint64(SAMPLED_SEED), **res)
+    os.remove(path)
+
+
 def main():
     if oracle.ref is None:
         raise SystemExit("oracle/_ref/libquanta_ref.so is missing: run `make -C oracle ref`")
     qnt = load_pkg()
     L = bind(oracle.ref.lib)
-    make_small(qnt, L)
+    if "--sampled-only" not in sys.argv:
+        make_small(qnt, L)
+        if "--small-only" not in sys.argv:
+            make_full(qnt, L)
     if "--small-only" not in sys.argv:
-        make_full(qnt, L)
+        make_sampled(qnt)
     for f in sorted(os.listdir(HERE)):
         if f.startswith("e2e") and f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")
