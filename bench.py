@@ -219,16 +219,27 @@ def e2e_model():
     return hp, qnt.synthetic_q4mix(5, hp)
 
 
-def e2e_bench(qh, torch, hp, tens, steps=256, warmup=3, n_prompt=512, check=True):
-    """End-to-end greedy generation on the q4mix Qwen2.5-0.5B-shaped model (configuration 5): a 512-token prompt in
-    32-token prefill chunks, then `steps` greedy decode steps, each one replay of a HIP graph holding one captured
-    decode step (the chosen token is fed back on the device). A warm-up run of `warmup` steps precedes the timed run;
-    the timed stream (positions 512 ..) is checked against the reference engine's (tests/golden/e2e_q4mix.npz)."""
+SAMPLED_SEED = 0x51A7C0DE
+
+
+def e2e_bench(qh, torch, hp, tens, steps=256, warmup=3, n_prompt=512, check=True, mode="greedy"):
+    """End-to-end generation on the q4mix Qwen2.5-0.5B-shaped model (configuration 5): a 512-token prompt in
+    32-token prefill chunks, then `steps` decode steps, each one replay of a HIP graph holding one captured decode step
+    (the chosen token is fed back on the device). A warm-up run of `warmup` steps precedes the timed run; the timed
+    stream (positions 512 ..) is checked against the reference engine's. mode "greedy": top-1 shortlist queries and
+    greedy picks (`quanta gen --greedy`, tests/golden/e2e_q4mix.npz); "chat": the reference's default sampler
+    parameters for both the head queries (top-k 20, the whole history as must ids) and the draws (temperature 0.7,
+    top-p 0.8, penalty 1.1), seed 0x51A7C0DE (tests/golden/e2e_sampled.npz)."""
     dec = qh.Decoder(hp, tens, ctx_len=4096)
+    chat = mode == "chat"
+    if chat:
+        dec.set_query(qh.sampler_params())
     ids = np.random.default_rng(9).integers(0, hp.vocab_size, n_prompt).astype(np.int32)
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     cap = steps + 1
     # warm-up run: prefill, capture the step, a few replays
+    if chat:
+        dec.set_sampler(qh.sampler_params(), SAMPLED_SEED)
     dec.prefill(ids, 0, top_k=1)
     dec.begin(cap)
     side = torch.cuda.Stream()
@@ -242,6 +253,8 @@ def e2e_bench(qh, torch, hp, tens, steps=256, warmup=3, n_prompt=512, check=True
         graph.replay()
     torch.cuda.synchronize()
     # timed run: prefill, then `steps` replays
+    if chat:
+        dec.set_sampler(qh.sampler_params(), SAMPLED_SEED)  # the generator restarts from the seed
     e0, e1, e2 = ev(), ev(), ev()
     e0.record()
     dec.prefill(ids, 0, top_k=1)
@@ -263,16 +276,50 @@ def e2e_bench(qh, torch, hp, tens, steps=256, warmup=3, n_prompt=512, check=True
     if status:
         raise SystemExit(f"bench: decoder status {status}")
     parity = None
-    gpath = os.path.join(ROOT, "tests", "golden", "e2e_q4mix.npz")
+    gpath = os.path.join(ROOT, "tests", "golden", "e2e_sampled.npz" if chat else "e2e_q4mix.npz")
+    r = {}
     if check and n_prompt == 512 and os.path.exists(gpath):
         g = np.load(gpath, allow_pickle=False)
-        n = min(len(g["out"]), steps)
-        parity = bool((out[:n] == g["out"][:n]).all())
+        want = g["chat_out"] if chat else g["out"]
+        n = min(len(want), steps)
+        parity = bool((out[:n] == want[:n]).all())
         if not parity:
-            raise SystemExit("bench: GPU token stream differs from the reference engine's")
+            raise SystemExit(f"bench: GPU token stream ({mode}) differs from the reference engine's")
+        if chat:  # the GPU head reads the same rows each step (the sampling tests check every step)
+            r = {"head_rows_mean": float(np.mean(g["chat_rows"][:n])),
+                 "head_rows_fraction": float(np.mean(g["chat_rows"][:n])) / hp.vocab_size}
     return {"prefill_tok_per_s": n_prompt / prefill_s, "prefill_ms": prefill_s * 1e3,
             "decode_tok_per_s": steps / decode_s, "decode_ms_per_token": decode_s / steps * 1e3,
-            "stream_equals_reference": parity, "tokens": int(steps), "prompt": int(n_prompt)}
+            "stream_equals_reference": parity, "tokens": int(steps), "prompt": int(n_prompt), **r}
+
+
+def e2e_cpu_sampled(hp, tens, n_prompt=512, n_gen=16):
+    """The reference's Session in the chat flow on the host cores (oracle/_ref): the batched prefill then n_gen
+    sampled tokens (default SamplerParams for the head queries and the draws), timed as two runs that differ by
+    n_gen - 1 decode steps."""
+    sys.path.insert(0, ROOT)
+    import oracle as orc
+    if orc.ref is None:
+        return None
+    import quanta_cpp_amd.qnt as qnt
+    path = os.path.join("/tmp", f"quanta_bench_q4mix_s_{os.getpid()}.qnt")
+    qnt.write_qnt(path, hp, tens)
+    threads = max(1, min(16, os.cpu_count() or 1))
+    try:
+        m = orc.ref.load_model(path, 4096, threads)
+        ids = np.random.default_rng(9).integers(0, hp.vocab_size, n_prompt).astype(np.int32)
+        sp = orc.sampler_params()
+        t = []
+        for n in (1, n_gen):
+            t0 = time.perf_counter()
+            orc.ref.gen_sampled(m, ids, n, sp, sp, SAMPLED_SEED)
+            t.append(time.perf_counter() - t0)
+        orc.ref.free_model(m)
+    finally:
+        os.remove(path)
+    return {"value": (n_gen - 1) / (t[1] - t[0]), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "sample": f"reference Session, chat flow: {n_prompt}-token prefill + 1 and + {n_gen} tokens "
+                      f"({t[0]:.1f} s, {t[1]:.1f} s), {threads} threads"}
 
 
 def e2e_cpu_baseline(hp, tens, n_prompt=512, n_gen=16):
@@ -406,7 +453,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end prefill + decode measurement")
-    ap.add_argument("--only", choices=["e2e", "roofline", "prefill"],
+    ap.add_argument("--only", choices=["e2e", "roofline", "prefill", "sampling"],
                     help="one measurement alone (for counter runs): e2e = --e2e-only; roofline = a 256 MiB copy "
                          "(counter calibration) then the Q4_0 GEMV rotation; prefill = Q4_0 4864x896 at M = 512")
     args = ap.parse_args()
@@ -433,6 +480,11 @@ def main():
     if args.only == "prefill":
         r = prefill_rotation(qh, synth, torch, 3, 4864, 896, 512, 5, 1)
         print(json.dumps({"q4_prefill_4864x896_M512": rnd(r)}), flush=True)
+        return 0
+    if args.only == "sampling":
+        hp, tens = e2e_model()
+        r = e2e_bench(qh, torch, hp, tens, steps=args.steps, warmup=args.warmup, mode="chat")
+        print(json.dumps({"sampling_chat": rnd(r)}), flush=True)
         return 0
     if args.only == "e2e":
         args.e2e_only = True
@@ -486,6 +538,9 @@ def main():
                 extra[f"{name}_prefill_{n}x{k}_M{m}"] = rnd(r)
         log("shortlist head")
         extra["shortlist_head_151936x896"] = rnd(head_bench(qh, synth, torch, orc.oracle, 5, 1))
+        log("sampling mode: prefill 512 + decode steps of the chat flow")
+        extra["sampling_chat"] = rnd(e2e_bench(qh, torch, hp, tens, steps=args.steps, warmup=args.warmup,
+                                               mode="chat"))
     result["extra"] = extra
     if not args.no_cpu:
         log("CPU baseline: the reference engine's decoder on the host cores")
@@ -497,6 +552,8 @@ def main():
             log("CPU baseline: Q4_0 GEMV")
             g = cpu_baseline(synth, shapes)
             extra["q4_gemv_mlp_cpu"] = rnd(g)
+            log("CPU baseline: the reference Session in the chat flow")
+            extra["sampling_chat_cpu"] = rnd(e2e_cpu_sampled(hp, tens))
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
