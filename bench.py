@@ -453,7 +453,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end prefill + decode measurement")
-    ap.add_argument("--only", choices=["e2e", "roofline", "prefill", "sampling"],
+    ap.add_argument("--only", choices=["e2e", "roofline", "prefill", "sampling", "head"],
                     help="one measurement alone (for counter runs): e2e = --e2e-only; roofline = a 256 MiB copy "
                          "(counter calibration) then the Q4_0 GEMV rotation; prefill = Q4_0 4864x896 at M = 512")
     args = ap.parse_args()
@@ -480,6 +480,10 @@ def main():
     if args.only == "prefill":
         r = prefill_rotation(qh, synth, torch, 3, 4864, 896, 512, 5, 1)
         print(json.dumps({"q4_prefill_4864x896_M512": rnd(r)}), flush=True)
+        return 0
+    if args.only == "head":
+        print(json.dumps({"shortlist_head_151936x896": rnd(head_bench(qh, synth, torch, orc.oracle, 5, 1))}),
+              flush=True)
         return 0
     if args.only == "sampling":
         hp, tens = e2e_model()

@@ -58,6 +58,27 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
+// Sorts a[0, p2) (p2 a power of two) largest first with a bitonic network; every thread of the workgroup (kThreads of
+// them) calls it, and a barrier ends every stage. The caller pads a to p2 with zeros.
+template <int kThreads>
+__device__ void bitonic_sort_desc_u64(uint64_t* a, int p2) {
+    const int tid = (int)threadIdx.x;
+    for (int size = 2; size <= p2; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int t = tid; t < p2 / 2; t += kThreads) {
+                const int lo = 2 * t - (t & (stride - 1)), hi = lo + stride;
+                const bool desc = (lo & size) == 0;
+                const uint64_t x = a[lo], y = a[hi];
+                if (desc ? x < y : x > y) {
+                    a[lo] = y;
+                    a[hi] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
 __device__ __forceinline__ int wave_sum_i32(int v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);

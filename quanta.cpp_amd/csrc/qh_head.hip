@@ -203,7 +203,8 @@ __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
     const uint8_t* __restrict__ w4, const uint16_t* __restrict__ s4, const uint32_t* __restrict__ e32,
     const int8_t* __restrict__ xq, const float* __restrict__ xd, int V, int nb, int nv, HeadMust mq, int tile,
     uint32_t nb_magic, float* __restrict__ coarse, float* __restrict__ upper, float* __restrict__ logits,
-    uint8_t* __restrict__ mark, int32_t* __restrict__ firsts, uint64_t* __restrict__ seedpart, int n_keep) {
+    uint8_t* __restrict__ mark, int32_t* __restrict__ firsts, uint64_t* __restrict__ seedpart, int n_keep,
+    int share_cap) {
     extern __shared__ float smem[];
     const int ps = prod_stride4(nb);
     const int nb4 = (nb + 3) & ~3;
@@ -213,8 +214,8 @@ __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
     float* prod1 = prod0 + (size_t)tile * ps;
     float* errf0 = prod1 + (size_t)tile * ps;            // [tile][ps] block errors, two buffers
     float* errf1 = errf0 + (size_t)tile * ps;
-    uint64_t* wkeys = reinterpret_cast<uint64_t*>(errf1 + (size_t)tile * ps);  // [kScreenMaxShare + 2]
-    uint8_t* mflag = reinterpret_cast<uint8_t*>(wkeys + kScreenMaxShare + 2);  // [2][tile]
+    uint64_t* wkeys = reinterpret_cast<uint64_t*>(errf1 + (size_t)tile * ps);  // [share_cap]
+    uint8_t* mflag = reinterpret_cast<uint8_t*>(wkeys + share_cap);             // [2][tile]
     int8_t* xs = reinterpret_cast<int8_t*>(mflag + ((2 * (size_t)tile + 15) & ~size_t(15)));  // [nb * 32]
     __shared__ int n_elig;
     __shared__ uint64_t lvl2[4 * 64];
@@ -374,11 +375,9 @@ __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
 
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n_seed = n_keep - 1;
-    // Each share's list holds its best n_keep keys, best first. Any n_keep distinct keys bound the global n_keep-th
-    // key from below; here each wave takes a slice of the list heads and offers its n_keep-th best head, and L is
-    // the largest offer (0 if no slice has n_keep heads). Only keys >= L can be selected.
-    __shared__ unsigned long long L_sh;
-    // Every partial key in registers, loaded together with the list heads below (one round trip).
+    // Every partial key in registers. Any n_keep distinct keys bound the global n_keep-th key from below: each
+    // wave offers the n_keep-th largest of its lanes' maxima (distinct keys), and L is the largest offer (0 if no
+    // wave has n_keep nonzero maxima). Only keys >= L can be selected.
     const int total = n_parts * n_keep;
     uint64_t kv[kSeedKeysPerThread];
 #pragma unroll
@@ -387,28 +386,20 @@ __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
         kv[j] = i < total ? seedpart[i] : 0ull;
     }
     if (tid < QH_HEAD_MAX_TOPK + 9) best[tid] = 0ull;
-    if (tid == 0) {
-        n_pool = 0;
-        L_sh = 0ull;
-    }
-    __syncthreads();
+    if (tid == 0) n_pool = 0;
     {
-        const int H = (n_parts + kWaves - 1) / kWaves;  // <= 128 (n_parts <= 2048)
-        const int h0 = min(n_parts, wave * H), h1 = min(n_parts, h0 + H);
-        uint64_t a[2];
-        int rk[2];
+        uint64_t lm[1] = {0ull};
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-            const int t = h0 + s2 * 64 + lane;
-            a[s2] = t < h1 ? seedpart[(size_t)t * n_keep] : 0ull;
-        }
-        wave_rank<2>(a, h1 - h0, rk);
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-            if (a[s2] != 0 && rk[s2] == n_keep - 1) atomicMax(&L_sh, (unsigned long long)a[s2]);
+        for (int j = 0; j < kSeedKeysPerThread; ++j) lm[0] = kv[j] > lm[0] ? kv[j] : lm[0];
+        int rk[1];
+        wave_rank<1>(lm, 64, rk);
+        const uint64_t offer = wave_max_u64((lm[0] != 0 && rk[0] == n_keep - 1) ? lm[0] : 0ull);
+        if (lane == 0) wb[0][wave] = offer;
     }
     __syncthreads();
-    const uint64_t L = L_sh;
+    uint64_t L = wb[0][0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) L = wb[0][w] > L ? wb[0][w] : L;
 #pragma unroll
     for (int j = 0; j < kSeedKeysPerThread; ++j) {
         const uint64_t v = kv[j];
@@ -419,19 +410,13 @@ __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
     }
     __syncthreads();
     const int np = n_pool;
-    if (np <= 256) {
-        if (wave == 0) {  // rank selection within the pool (keys are unique)
-            uint64_t a[4];
-            int rk[4];
-#pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) {
-                const int i = s2 * 64 + lane;
-                a[s2] = i < np ? pool[i] : 0ull;
-            }
-            wave_rank<4>(a, np, rk);
-#pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2)
-                if (a[s2] != 0 && rk[s2] < n_keep) best[rk[s2]] = a[s2];
+    if (np <= kSeedThreads) {  // uniform: rank each pool key against the pool (broadcast LDS reads); keys are unique
+        if (wave * 64 < np) {  // uniform per wave: only the waves that hold pool keys
+            const uint64_t mine = tid < np ? pool[tid] : 0ull;
+            int rank = 0;
+#pragma unroll 8
+            for (int j = 0; j < np; ++j) rank += pool[j] > mine ? 1 : 0;
+            if (tid < np && rank < n_keep) best[rank] = mine;
         }
     } else {
         // Many survivors (e.g. many equal scores): n_keep rounds of a block-wide maximum over every partial key.
@@ -440,11 +425,11 @@ __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
 #pragma unroll
             for (int j = 0; j < kSeedKeysPerThread; ++j) m = kv[j] > m ? kv[j] : m;
             const uint64_t g = wave_max_u64(m);
-            if (lane == 0) wb[i & 1][wave] = g;
+            if (lane == 0) wb[(i + 1) & 1][wave] = g;
             __syncthreads();
-            uint64_t gb = wb[i & 1][0];
+            uint64_t gb = wb[(i + 1) & 1][0];
 #pragma unroll
-            for (int w = 1; w < kWaves; ++w) gb = wb[i & 1][w] > gb ? wb[i & 1][w] : gb;
+            for (int w = 1; w < kWaves; ++w) gb = wb[(i + 1) & 1][w] > gb ? wb[(i + 1) & 1][w] : gb;
             if (gb != 0 && m == gb) {
 #pragma unroll
                 for (int j = 0; j < kSeedKeysPerThread; ++j) kv[j] = kv[j] == gb ? 0ull : kv[j];
@@ -453,18 +438,21 @@ __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        int ns = 0;
-        while (ns < n_seed && best[ns] != 0) ++ns;
-        for (int i = 0; i < ns; ++i) {
-            const int r = key_row(best[i]);
-            rowl[i] = r;
-            rows[i] = r;
+    if (wave == 0) {  // one lane per seed: the selected keys are best[0, ns), nonzero, best first
+        const bool have = lane < n_seed && best[lane] != 0;
+        const int ns = __popcll(__ballot(have));
+        if (have) {
+            const int r = key_row(best[lane]);
+            rowl[lane] = r;
+            rows[lane] = r;
             mark[r] = 2;
         }
-        counts[0] = ns;
-        ctrl->n_seeds = ns;
-        ctrl->seed_tie = (ns == n_seed && best[n_seed] != 0 && (best[n_seed] >> 32) == (best[n_seed - 1] >> 32)) ? 1 : 0;
+        if (lane == 0) {
+            counts[0] = ns;
+            ctrl->n_seeds = ns;
+            ctrl->seed_tie =
+                (ns == n_seed && best[n_seed] != 0 && (best[n_seed] >> 32) == (best[n_seed - 1] >> 32)) ? 1 : 0;
+        }
     }
     __syncthreads();
     const int ns = counts[0];
@@ -524,30 +512,28 @@ __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
         }
         __syncthreads();
     }
-    if (tid == 0) {
+    if (wave == 0) {  // one lane per seed
+        const bool have = lane < ns;
+        const float e = have ? exact[lane] : -__builtin_inff();
         float tau = -__builtin_inff();
-        if (ns >= k) {  // k-th largest exact seed logit (model.cpp:308-313)
-            float sel[QH_HEAD_MAX_TOPK + 8];
-            for (int i = 0; i < ns; ++i) sel[i] = exact[i];
-            for (int i = 0; i < k; ++i) {
-                int m = i;
-                for (int q = i + 1; q < ns; ++q)
-                    if (sel[q] > sel[m]) m = q;
-                const float t = sel[i];
-                sel[i] = sel[m];
-                sel[m] = t;
+        if (ns >= k) {  // k-th largest exact seed logit (model.cpp:308-313): fewer than k above it, k at or above
+            int gt = 0, ge = 0;
+            const int nsu = __builtin_amdgcn_readfirstlane(ns);
+            for (int j = 0; j < nsu; ++j) {
+                const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+                gt += ej > e ? 1 : 0;
+                ge += ej >= e ? 1 : 0;
             }
-            tau = sel[k - 1];
+            const uint64_t at = __ballot(have && gt < k && ge >= k);  // equal values wherever it is set
+            tau = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), __ffsll((long long)at) - 1));
         }
-        ctrl->tau = tau;
-        uint64_t kmax = 0;
-        for (int i = 0; i < ns; ++i) {
-            const uint64_t kk = score_key(exact[i], rowl[i]);
-            kmax = kk > kmax ? kk : kmax;
+        const uint64_t kmax = wave_max_u64(have ? score_key(e, rowl[lane]) : 0ull);
+        if (lane == 0) {
+            ctrl->tau = tau;
+            ctrl->argmax_key = kmax;
+            ctrl->n_cand = 0u;
+            ctrl->done = 0u;
         }
-        ctrl->argmax_key = kmax;
-        ctrl->n_cand = 0u;
-        ctrl->done = 0u;
     }
 }
 
@@ -688,10 +674,14 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
     const int n_keep = q.top_k + 9;
     if (grid * n_keep > kSeedThreads * kSeedKeysPerThread || grid > kSeedMaxPool) return hipErrorInvalidValue;
     const uint32_t magic = nb == 1 ? 0u : (uint32_t)((0x100000000ull + (uint64_t)nb - 1) / (uint64_t)nb);
+    // A share holds at most V / grid + 3 rows (its ends are rounded down to even rows); sizing its key array by that
+    // instead of kScreenMaxShare keeps the LDS under 40 KB, so four workgroups fit on a CU.
+    const int share_cap = V / grid + 4;
     const size_t lds1 = ((size_t)2 * ((nb + 3) & ~3) + 4 * (size_t)tile * prod_stride4(nb)) * 4 +
-                        ((size_t)kScreenMaxShare + 2) * 8 + ((2 * (size_t)tile + 15) & ~size_t(15)) + (size_t)D;
+                        (size_t)share_cap * 8 + ((2 * (size_t)tile + 15) & ~size_t(15)) + (size_t)D;
     hipLaunchKernelGGL(head_screen_kernel, dim3(grid), dim3(kScreenThreads), lds1, s, w4, s4, e32, xq, xd, V, nb, nv,
-                       must, tile, magic, out.coarse, out.upper, out.logits, mark, firsts, seedpart, n_keep);
+                       must, tile, magic, out.coarse, out.upper, out.logits, mark, firsts, seedpart, n_keep,
+                       share_cap);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const size_t lds2 = (size_t)(kSeedThreads / 64) * nb * 4;

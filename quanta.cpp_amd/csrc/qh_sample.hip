@@ -137,20 +137,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const float* __restric
         while (p2 < count) p2 <<= 1;
         for (int i = count + tid; i < p2; i += kThreads) pool[i] = 0ull;
         __syncthreads();
-        for (int size = 2; size <= p2; size <<= 1) {  // bitonic sort, largest first
-            for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                for (int t = tid; t < p2 / 2; t += kThreads) {
-                    const int lo = 2 * t - (t & (stride - 1)), hi = lo + stride;
-                    const bool desc = (lo & size) == 0;
-                    const uint64_t a = pool[lo], b = pool[hi];
-                    if (desc ? a < b : a > b) {
-                        pool[lo] = b;
-                        pool[hi] = a;
-                    }
-                }
-                __syncthreads();
-            }
-        }
+        bitonic_sort_desc_u64<kThreads>(pool, p2);
     } else {  // k rounds: the largest key below the previous one
         uint64_t prev = ~0ull;
         for (int r = 0; r < k; ++r) {
