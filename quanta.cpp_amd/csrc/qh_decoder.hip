@@ -81,15 +81,58 @@ __device__ __forceinline__ uint16_t f2h(float f) {
 
 // quantize_q8 of one 32-block held one value per lane of a half-wave (ops_ref.cpp:69-83): the block's absolute
 // maximum / 127, codes rounded half away from zero. Every lane of the half-wave must be active.
+// Maximum over the whole wave (every lane active) with the select o > a ? o : a at each step: DPP within rows of
+// 16, then the gfx950 row swaps (16 and 32 lanes apart).
+__device__ __forceinline__ float wave_max_sel(float a) {
+    auto step = [](float x, float o) { return o > x ? o : x; };
+    a = step(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0xB1, 0xF, 0xF, false)));
+    a = step(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x4E, 0xF, 0xF, false)));
+    a = step(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x141, 0xF, 0xF, false)));
+    a = step(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x140, 0xF, 0xF, false)));
+    uint32_t u = __builtin_bit_cast(uint32_t, a);
+    const auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    a = step(__builtin_bit_cast(float, (uint32_t)s16[0]), __builtin_bit_cast(float, (uint32_t)s16[1]));
+    u = __builtin_bit_cast(uint32_t, a);
+    const auto s32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return step(__builtin_bit_cast(float, (uint32_t)s32[0]), __builtin_bit_cast(float, (uint32_t)s32[1]));
+}
+
+// quantize_q8 of one 32-block (ops_ref.cpp:69-83) held one value per lane by an aligned group of 32 lanes: amax
+// (the maximum does not depend on the order of comparison), d = amax / 127, inv = d > 0 ? 1 / d : 0, and
+// q = lround(v * inv).
 __device__ __forceinline__ void quant_block32(float v, int8_t* __restrict__ q, float* __restrict__ d) {
-    float a = __builtin_fabsf(v);
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) a = __builtin_fmaxf(a, __shfl_xor(a, off, 64));
+    const float a = max32_lanes(__builtin_fabsf(v));
     const float sc = a / 127.0f;
     const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
     const int i = (int)threadIdx.x & 31;
     q[i] = (int8_t)(int)round_half_away(v * inv);
     if (i == 0) *d = sc;
+}
+
+// The same for a block held four consecutive values per lane by an aligned group of 8 lanes (lane j of the group
+// holds elements 4j .. 4j + 3): one 4-byte store of codes per lane.
+__device__ __forceinline__ void quant_block_x8(float4 v, int8_t* __restrict__ q, float* __restrict__ d) {
+    const float a = max8_lanes(__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+                                               __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w))));
+    const float sc = a / 127.0f;
+    const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
+    const int j = (int)threadIdx.x & 7;
+    const uint32_t c0 = (uint32_t)(uint8_t)(int8_t)(int)round_half_away(v.x * inv);
+    const uint32_t c1 = (uint32_t)(uint8_t)(int8_t)(int)round_half_away(v.y * inv);
+    const uint32_t c2 = (uint32_t)(uint8_t)(int8_t)(int)round_half_away(v.z * inv);
+    const uint32_t c3 = (uint32_t)(uint8_t)(int8_t)(int)round_half_away(v.w * inv);
+    *reinterpret_cast<uint32_t*>(q + 4 * j) = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+    if (j == 0) *d = sc;
+}
+
+// quantize_q8 of the row xs[0, D) (16-byte aligned, D % 32 == 0) into q / d: 8 lanes per block, 32 blocks per pass
+// of 256 threads.
+__device__ __forceinline__ void quant_row_x8(const float* xs, int D, int8_t* __restrict__ q, float* __restrict__ d) {
+    const int nb = D / QK;
+    for (int t = (int)threadIdx.x; t < nb * 8; t += 256) {  // whole 8-lane groups
+        const int b = t >> 3;
+        quant_block_x8(reinterpret_cast<const float4*>(xs)[t], q + b * QK, d + b);
+    }
 }
 
 // acc = op(acc, p[i]) for i = 0 .. n-1 in order, by one thread, over floats in LDS (16-byte aligned, n >= 1). A wave
@@ -436,9 +479,7 @@ __device__ void normalize_quant_lds(float* xs, int D, float scale, const Row4& w
         }
     }
     __syncthreads();
-    const int nb = D / QK;
-    for (int b = tid >> 5; b < nb; b += 8)  // a half-wave per 32-block (uniform within the half-wave)
-        quant_block32(xs[b * QK + (tid & 31)], oq + b * QK, od + b);
+    quant_row_x8(xs, D, oq, od);
 }
 
 // Activation fill for a GEMV tile whose input is rmsnorm(x) * w quantized (the decode step's q/k/v and gate/up
@@ -462,7 +503,7 @@ struct NormAct {
     template <bool XL>
     __device__ __forceinline__ void fill(int8_t* xs, float* xds) const {
         static_assert(XL, "the normed activation is produced in LDS");
-        const int tid = (int)threadIdx.x, n4 = D / 4, nb = D / QK;
+        const int tid = (int)threadIdx.x, n4 = D / 4;
         Row4 wr, xr;
         wr.load(w, n4);
         float4* t4 = reinterpret_cast<float4*>(tmp);
@@ -497,7 +538,7 @@ struct NormAct {
             }
         }
         __syncthreads();
-        for (int b = tid >> 5; b < nb; b += 8) quant_block32(tmp[b * QK + (tid & 31)], xs + b * QK, xds + b);
+        quant_row_x8(tmp, D, xs, xds);
     }
 
     // The row to normalise into xr: the embedding of *tok (eq set) or x.
@@ -778,11 +819,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int c = wave; c < ncb * kDmaPerBlk; c += 4)
         lds_dma16(vc4 + vchunk(c / kDmaPerBlk, (c % kDmaPerBlk) * 64 + lane), vst + c * 64);
     // the maximum does not depend on the order of comparison
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float o = __shfl_xor(mx, off, 64);
-        mx = o > mx ? o : mx;
-    }
+    mx = wave_max_sel(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
     mx = red[0];
@@ -961,8 +998,9 @@ __global__ __launch_bounds__(256) void gemv_residual_kernel(const uint8_t* __res
     const int tid = (int)threadIdx.x;
     const int ra = (int)blockIdx.x * tile_rows;
     const int nrows = min(tile_rows, rows - ra);
+    const float x0 = x[ra + min(tid, nrows - 1)];  // the residual row, in flight with the weights
     const float val = gemv_tile<DT, U, XL>(wq, wscale, xq, xd, nb, ra, nrows, tile_rows, nb_magic, smem);
-    if (tid < nrows) x[ra + tid] = x[ra + tid] + val;
+    if (tid < nrows) x[ra + tid] = x0 + val;
 }
 
 // One token's gate and up GEMVs over the same 32 rows of both matrices, from the normed MLP input each workgroup

@@ -8,6 +8,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace qh {
 
 constexpr int QK = 32;
@@ -49,13 +52,74 @@ __device__ __forceinline__ uint64_t score_key(float score, int row) {
 __device__ __forceinline__ int key_row(uint64_t k) { return (int)(0xffffffffu - (uint32_t)k); }
 __device__ __forceinline__ float key_score(uint64_t k) { return from_ordered_bits((uint32_t)(k >> 32)); }
 
+// Whole-wave reductions (every lane active) in registers: DPP exchanges within rows of 16 lanes (quad_perm
+// [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then the gfx950 row swaps 16 and 32 lanes apart; every lane
+// ends with the result. No LDS round trips.
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce32x2(T v, Op op) {
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
+    auto dpp = [](T x, auto ctrl) {
+        if constexpr (sizeof(T) == 4) {
+            return __builtin_bit_cast(T, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), decltype(ctrl)::value,
+                                                                  0xF, 0xF, false));
+        } else {
+            const uint64_t u = __builtin_bit_cast(uint64_t, x);
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)u, decltype(ctrl)::value, 0xF, 0xF, false);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(u >> 32), decltype(ctrl)::value, 0xF,
+                                                                  0xF, false);
+            return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+        }
+    };
+    auto swap = [](T x, auto rows32) {  // {x of this lane's pair partner row or half, x}
+        if constexpr (sizeof(T) == 4) {
+            const uint32_t u = __builtin_bit_cast(uint32_t, x);
+            const auto r = decltype(rows32)::value ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                                                   : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+            return std::pair<T, T>{__builtin_bit_cast(T, (uint32_t)r[0]), __builtin_bit_cast(T, (uint32_t)r[1])};
+        } else {
+            const uint64_t u = __builtin_bit_cast(uint64_t, x);
+            const uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
+            const auto a = decltype(rows32)::value ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                                                   : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+            const auto b = decltype(rows32)::value ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                                                   : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+            return std::pair<T, T>{__builtin_bit_cast(T, ((uint64_t)(uint32_t)b[0] << 32) | (uint32_t)a[0]),
+                                   __builtin_bit_cast(T, ((uint64_t)(uint32_t)b[1] << 32) | (uint32_t)a[1])};
+        }
+    };
+    v = op(v, dpp(v, std::integral_constant<int, 0xB1>{}));
+    v = op(v, dpp(v, std::integral_constant<int, 0x4E>{}));
+    v = op(v, dpp(v, std::integral_constant<int, 0x141>{}));
+    v = op(v, dpp(v, std::integral_constant<int, 0x140>{}));
+    const auto p16 = swap(v, std::false_type{});
+    v = op(p16.first, p16.second);
+    const auto p32 = swap(v, std::true_type{});
+    return op(p32.first, p32.second);
+}
+
+// Lane exchanges for block maxima, all in registers (DPP and the gfx950 row swap; no LDS round trips).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_max(float a) {
+    const float o = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), kCtrl, 0xF, 0xF, false));
+    return __builtin_fmaxf(a, o);
+}
+// Maximum over each aligned group of 8 lanes (every lane of the group active).
+__device__ __forceinline__ float max8_lanes(float a) {
+    a = dpp_max<0xB1>(a);   // quad_perm [1,0,3,2]
+    a = dpp_max<0x4E>(a);   // quad_perm [2,3,0,1]
+    return dpp_max<0x141>(a);  // row_half_mirror: lane i <-> 7 - i within each 8
+}
+// Maximum over each aligned group of 32 lanes (every lane of the group active).
+__device__ __forceinline__ float max32_lanes(float a) {
+    a = max8_lanes(a);
+    a = dpp_max<0x140>(a);  // row_mirror: lane i <-> 15 - i within each 16
+    const uint32_t u = __builtin_bit_cast(uint32_t, a);
+    const auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);  // rows 0 <-> 1 and 2 <-> 3
+    return __builtin_fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
+}
+
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const uint64_t o = __shfl_xor(v, off, 64);
-        v = o > v ? o : v;
-    }
-    return v;
+    return wave_reduce32x2(v, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
 }
 
 // Sorts a[0, p2) (p2 a power of two) largest first with a bitonic network; every thread of the workgroup (kThreads of
@@ -80,9 +144,7 @@ __device__ void bitonic_sort_desc_u64(uint64_t* a, int p2) {
 }
 
 __device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    return wave_reduce32x2(v, [](int a, int b) { return a + b; });
 }
 
 // 16 signed int8 weights . 16 signed int8 activations.
@@ -132,6 +194,73 @@ __device__ __forceinline__ float chain_lds4(const float* p, const float* dx, int
         acc = __builtin_fmaf(pv.w, xv.w, acc);
     }
     for (; b < nb; ++b) acc = __builtin_fmaf(p[b], dx[b], acc);
+    return acc;
+}
+
+// Pipelined chain rows (chain_lds_pipe): a row of nb operands is stored as chain_len32(nb) - nb zeros followed by
+// the nb operands, rows chain_stride32(nb) floats apart (16-byte aligned, 4 mod 32 floats, so 16-byte reads of
+// neighbouring rows fall in different banks), and kChainPipePad readable floats follow the last row.
+constexpr int kChainPipePad = 32;
+__host__ __device__ __forceinline__ int chain_len32(int nb) { return (nb + 31) & ~31; }
+__host__ __device__ __forceinline__ int chain_stride32(int nb) { return chain_len32(nb) + 4; }
+
+// The serial chain over a padded row: acc = fma(p[i], dx[i], acc) for i in [0, L), L a multiple of 32. The leading
+// zeros of p and dx leave acc = +0 exactly (fma(0, 0, +0) = +0), so the result is the chain over the nb operands
+// from +0, the reference's order. Operands arrive 8 at a time (two 16-byte LDS reads of each) in four rotating
+// batches, three in flight while one is consumed, so the chain runs at the FMA latency rather than the LDS
+// latency; the reads reach 32 floats past p + L and dx + L. p and dx are 16-byte aligned.
+__device__ __forceinline__ float chain_lds_pipe(const float* p, const float* dx, int L) {
+    struct Batch {
+        float4 p0, p1, x0, x1;
+    };
+    auto ld = [&](Batch& q, int b) {
+        q.p0 = *reinterpret_cast<const float4*>(p + b);
+        q.p1 = *reinterpret_cast<const float4*>(p + b + 4);
+        q.x0 = *reinterpret_cast<const float4*>(dx + b);
+        q.x1 = *reinterpret_cast<const float4*>(dx + b + 4);
+    };
+    float acc = 0.0f;
+    auto use = [&](const Batch& q) {
+        acc = __builtin_fmaf(q.p0.x, q.x0.x, acc);
+        acc = __builtin_fmaf(q.p0.y, q.x0.y, acc);
+        acc = __builtin_fmaf(q.p0.z, q.x0.z, acc);
+        acc = __builtin_fmaf(q.p0.w, q.x0.w, acc);
+        acc = __builtin_fmaf(q.p1.x, q.x1.x, acc);
+        acc = __builtin_fmaf(q.p1.y, q.x1.y, acc);
+        acc = __builtin_fmaf(q.p1.z, q.x1.z, acc);
+        acc = __builtin_fmaf(q.p1.w, q.x1.w, acc);
+    };
+    // The first four batches pass through an empty asm: the loop's reload of a batch is then not merged with its
+    // first load into one load at the top of the loop, which would leave nothing in flight across iterations.
+    auto pin = [](Batch& q) {
+        asm volatile("" : "+v"(q.p0.x), "+v"(q.p0.y), "+v"(q.p0.z), "+v"(q.p0.w), "+v"(q.p1.x), "+v"(q.p1.y),
+                     "+v"(q.p1.z), "+v"(q.p1.w));
+        asm volatile("" : "+v"(q.x0.x), "+v"(q.x0.y), "+v"(q.x0.z), "+v"(q.x0.w), "+v"(q.x1.x), "+v"(q.x1.y),
+                     "+v"(q.x1.z), "+v"(q.x1.w));
+    };
+    Batch A, B, C, D;
+    ld(A, 0);
+    ld(B, 8);
+    ld(C, 16);
+    ld(D, 24);
+    pin(A);
+    pin(B);
+    pin(C);
+    pin(D);
+    for (int b = 0; b < L; b += 32) {  // the scheduling barriers keep each batch's reads ahead of the next FMAs
+        use(A);
+        ld(A, b + 32);
+        __builtin_amdgcn_sched_barrier(0);
+        use(B);
+        ld(B, b + 40);
+        __builtin_amdgcn_sched_barrier(0);
+        use(C);
+        ld(C, b + 48);
+        __builtin_amdgcn_sched_barrier(0);
+        use(D);
+        ld(D, b + 56);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     return acc;
 }
 

@@ -19,13 +19,6 @@
 
 namespace qh {
 
-// Serial chain acc = fma(p[b], dx[b], acc) for b = 0 .. nb-1 over LDS operands (the reference's order).
-__device__ __forceinline__ float chain_lds(const float* p, const float* dx, int nb) {
-    float acc = 0.0f;
-    for (int b = 0; b < nb; ++b) acc = __builtin_fmaf(p[b], dx[b], acc);
-    return acc;
-}
-
 // One pass of a workgroup: U chunks of 16 bytes per thread, the block scale of each chunk and, unless the
 // activation is staged in LDS (XL), the activation bytes the chunk pairs with. The chunk index is clamped
 // into the tile, so every load is unconditional and all of them go out back to back.
@@ -96,11 +89,34 @@ struct GemvPass {
     }
 };
 
+// LDS floats of a tile before the staged codes: activation scales and block products as padded chain rows
+// (chain_lds_pipe: [chain_len32(nb)] scales, then [tile_rows][chain_stride32(nb)] products) and the chain's read
+// slack.
+__host__ __device__ __forceinline__ size_t gemv_tile_lds_floats(int nb, int tile_rows) {
+    return (size_t)chain_len32(nb) + (size_t)tile_rows * chain_stride32(nb) + kChainPipePad;
+}
+
+// Zeros in front of the padded chain rows of the activation scales (dxs) and of rows [0, nrows) of the products.
+__device__ __forceinline__ void zero_chain_prefix(float* dxs, float* prod, int nb, int nrows) {
+    const int zp = chain_len32(nb) - nb, ps = chain_stride32(nb), tid = (int)threadIdx.x;
+    if (zp == 0) return;
+    if ((zp & 3) == 0) {  // uniform (nb % 4 == 0): thread r writes the 16-byte zero groups of padded row r
+        for (int r = tid; r <= nrows; r += 256) {
+            float4* z = reinterpret_cast<float4*>(r == 0 ? dxs : prod + (size_t)(r - 1) * ps);
+            for (int k = 0; k < (zp >> 2); ++k) z[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        return;
+    }
+    for (int i = tid; i < (nrows + 1) * 32; i += 256) {  // 256-thread workgroups
+        const int r = i >> 5, j = i & 31;
+        if (j < zp) (r == 0 ? dxs : prod + (size_t)(r - 1) * ps)[j] = 0.0f;
+    }
+}
+
 // LDS bytes of a tile of tile_rows virtual rows (PAIR tiles count both matrices' rows).
 __host__ __device__ __forceinline__ size_t gemv_tile_lds_bytes(int cols, int tile_rows, bool xl) {
-    const int nb = cols / QK;
-    const size_t f = ((size_t)nb + (size_t)tile_rows * (nb + 1)) * 4;
-    return xl ? ((f + 15) & ~size_t(15)) + (size_t)cols : f;
+    const size_t f = gemv_tile_lds_floats(cols / QK, tile_rows) * 4;
+    return xl ? f + (size_t)cols : f;
 }
 
 // Stages the activation for a tile: its block scales into xds and, when the codes are read from LDS (XL), its codes
@@ -135,11 +151,11 @@ __device__ __forceinline__ float gemv_tile(const GemvSegs<NSEG>& sg, const int8_
                                            const float* __restrict__ xd, int nb, int nrows, int tile_rows,
                                            uint32_t nb_magic, float* smem, const Act& act) {
     constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
-    float* xds = smem;         // [nb] activation scales
-    float* prod = smem + nb;   // [tile_rows][nb + 1] block products
-    // [cols] codes (XL), 16-byte aligned after the products
-    int8_t* xs = reinterpret_cast<int8_t*>(smem) + ((((size_t)nb + (size_t)tile_rows * (nb + 1)) * 4 + 15) & ~size_t(15));
-    const int pstride = nb + 1;
+    const int L = chain_len32(nb), zp = L - nb, pstride = chain_stride32(nb);
+    float* dxs = smem;                          // [L] activation scales, zp zeros first
+    float* xds = dxs + zp;
+    float* prod = smem + L;                     // [tile_rows][pstride] block products, zp zeros first per row
+    int8_t* xs = reinterpret_cast<int8_t*>(smem + gemv_tile_lds_floats(nb, tile_rows));  // [cols] codes (XL)
     const int tid = (int)threadIdx.x;
     const int vrows = NSEG * nrows;
     const int nchunks = vrows * nb * kChunksPerBlock;
@@ -148,19 +164,25 @@ __device__ __forceinline__ float gemv_tile(const GemvSegs<NSEG>& sg, const int8_
     GemvPass<DT, U, XL, NSEG> cur;
     cur.load(sg, split, xq, 0, nchunks - 1, nb, nb_magic);
     act.template fill<XL>(xs, xds);
+    zero_chain_prefix(dxs, prod, nb, vrows);
     if constexpr (XL) __syncthreads();
-    for (int c0 = 0; c0 < nchunks; c0 += 256 * U) {
-        if (c0 + 256 * U < nchunks) {  // uniform: prefetch the next pass, then compute this one
-            GemvPass<DT, U, XL, NSEG> nxt;
-            nxt.load(sg, split, xq, c0 + 256 * U, nchunks - 1, nb, nb_magic);
-            cur.products(prod, pstride, c0, nchunks, xs);
-            cur = nxt;
-        } else {
-            cur.products(prod, pstride, c0, nchunks, xs);
+    float* prow = prod + zp;
+    if (nchunks <= 256 * U) {  // uniform: a single pass
+        cur.products(prow, pstride, 0, nchunks, xs);
+    } else {
+        for (int c0 = 0; c0 < nchunks; c0 += 256 * U) {
+            if (c0 + 256 * U < nchunks) {  // uniform: prefetch the next pass, then compute this one
+                GemvPass<DT, U, XL, NSEG> nxt;
+                nxt.load(sg, split, xq, c0 + 256 * U, nchunks - 1, nb, nb_magic);
+                cur.products(prow, pstride, c0, nchunks, xs);
+                cur = nxt;
+            } else {
+                cur.products(prow, pstride, c0, nchunks, xs);
+            }
         }
     }
     __syncthreads();
-    return tid < vrows ? chain_lds(prod + tid * pstride, xds, nb) : 0.0f;
+    return tid < vrows ? chain_lds_pipe(prod + tid * pstride, dxs, L) : 0.0f;
 }
 
 // Rows [ra, ra + nrows) of one matrix, activation from global memory.

@@ -22,9 +22,7 @@ __global__ __launch_bounds__(256) void quantize_q8_kernel(const float* __restric
     const int i = threadIdx.x & 31;
     const bool ok = blk < total_blocks;
     const float v = ok ? x[blk * QK + i] : 0.0f;
-    float a = __builtin_fabsf(v);
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) a = __builtin_fmaxf(a, __shfl_xor(a, off, 64));
+    const float a = max32_lanes(__builtin_fabsf(v));  // every lane takes part (v = 0 past the end)
     const float scale = a / 127.0f;
     const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
     if (ok) {
@@ -49,7 +47,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(float* __restrict__ out, cons
                                                    const uint16_t* __restrict__ wscale,
                                                    const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                    int nb, int r0, int r1, int tile_rows, uint32_t nb_magic) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     const int ra = r0 + (int)blockIdx.x * tile_rows;
     const int nrows = min(tile_rows, r1 - ra);
     const float v = gemv_tile<DT, U, XL>(wq, wscale, xq, xd, nb, ra, nrows, tile_rows, nb_magic, smem);
@@ -111,15 +109,16 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(float* __restrict__ ou
                                                           const uint16_t* __restrict__ wscale,
                                                           const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                           int nb, int r0, int r1, int tile_rows, uint32_t nb_magic) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
     constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
     const int cols = nb * QK;
-    const int pstride = prod_stride4(nb);
-    float* xds = smem;                                          // [nb], padded to 4
-    float* prod0 = smem + ((nb + 3) & ~3);                      // [tile_rows][pstride]
+    const int L = chain_len32(nb), zp = L - nb, pstride = chain_stride32(nb);
+    float* dxs = smem;                                          // [L] padded chain row (zp zeros first)
+    float* xds = dxs + zp;
+    float* prod0 = smem + L;                                    // [tile_rows][pstride] padded chain rows
     float* prod1 = prod0 + (size_t)tile_rows * pstride;
-    int8_t* xs = reinterpret_cast<int8_t*>(prod1 + (size_t)tile_rows * pstride);  // [cols]
+    int8_t* xs = reinterpret_cast<int8_t*>(prod1 + (size_t)tile_rows * pstride + kChainPipePad);  // [cols]
     const int tid = (int)threadIdx.x;
     // Rows [ra, rb) of this workgroup: an even split, so no workgroup carries more than one extra partial tile.
     const int n = r1 - r0;
@@ -134,14 +133,15 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(float* __restrict__ ou
     A.load(wq + (size_t)ra * row_bytes, wscale + (size_t)ra * nb, chunks_of(ra));
     for (int i = tid; i < cols / 16; i += 256) reinterpret_cast<uint4*>(xs)[i] = load16(xq + i * 16);
     for (int i = tid; i < nb; i += 256) xds[i] = xd[i];
+    zero_chain_prefix(dxs, prod0, nb, 2 * tile_rows);  // both product buffers (contiguous)
     __syncthreads();
 
     // One tile: block products into `prod`, then one barrier, then one chain thread per row.
     auto tile_body = [&](const StreamRegs<DT, U>& regs, int r, float* prod) {
         const int nrows = min(tile_rows, rb - r);
-        regs.products(prod, pstride, nrows * nb * kChunksPerBlock, nb, nb_magic, xs);
+        regs.products(prod + zp, pstride, nrows * nb * kChunksPerBlock, nb, nb_magic, xs);
         __syncthreads();
-        if (tid < nrows) out[r + tid] = chain_lds4(prod + tid * pstride, xds, nb);
+        if (tid < nrows) out[r + tid] = chain_lds_pipe(prod + tid * pstride, dxs, L);
     };
     // Loads in the steady-state loop are unconditional (a conditional load makes the compiler's wait counting
     // assume the worst at the join); the last one or two tiles are peeled.
@@ -209,13 +209,13 @@ size_t gemv_lds_bytes(int cols, int tile_rows, bool xl) { return gemv_tile_lds_b
 
 static size_t gemv_stream_lds_bytes(int cols, int tile_rows) {
     const int nb = cols / QK;
-    return ((size_t)((nb + 3) & ~3) + 2 * (size_t)tile_rows * prod_stride4(nb)) * 4 + (size_t)cols;
+    return ((size_t)chain_len32(nb) + 2 * (size_t)tile_rows * chain_stride32(nb) + kChainPipePad) * 4 + (size_t)cols;
 }
 
 GemvPlan gemv_plan(int dtype, int cols, int rows) {
     const int nb = cols / QK;
     const int cpr = dtype == kQ8 ? 2 * nb : nb;  // 16-byte chunks per row
-    const int lds_rows = (65536 - 16 - cols - nb * 4) / ((nb + 1) * 4);  // LDS <= 64 KB
+    const int lds_rows = (65536 - cols - 4 * (chain_len32(nb) + kChainPipePad)) / (chain_stride32(nb) * 4);  // 64 KB
     GemvPlan p;
     p.stream = false;
     p.grid = 0;
@@ -242,7 +242,7 @@ GemvPlan gemv_plan(int dtype, int cols, int rows) {
     if (p.stream) {
         // Rows per tile: as many whole rows as unroll * 256 chunk slots hold, within 64 KB of LDS.
         int t = p.unroll * 256 / cpr;
-        const int lds_stream_rows = (65536 - cols - (nb + 4) * 4) / (2 * prod_stride4(nb) * 4);
+        const int lds_stream_rows = (65536 - cols - 4 * (chain_len32(nb) + kChainPipePad)) / (2 * chain_stride32(nb) * 4);
         t = t < 1 ? 1 : t;
         t = t > 256 ? 256 : t;  // one chain thread per row
         t = t > lds_stream_rows ? lds_stream_rows : t;
