@@ -190,16 +190,19 @@ __device__ __forceinline__ float lds_chain(const float* p, int n, Op op) {
     return acc;
 }
 
-// Up to 8 float4 per thread of a row of n4 float4 (n4 <= 2048) with every load issued before the first use:
-// slot k holds element tid + 256 k (clamped onto the last element, so the loads are unconditional).
-struct Row4 {
-    float4 v[8];
+// R float4 per thread of a row of n4 <= 256 R float4 with every load issued before the first use: slot k holds
+// element tid + 256 k (clamped onto the last element, so the loads are unconditional). Kernels take R = row_slots(n4):
+// one load per thread up to D = 1024, eight (D <= 8192) above.
+template <int R>
+struct RowF4 {
+    float4 v[R];
     __device__ __forceinline__ void load(const float* __restrict__ src, int n4) {
         const float4* s4 = reinterpret_cast<const float4*>(src);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = s4[min((int)threadIdx.x + 256 * k, n4 - 1)];
+        for (int k = 0; k < R; ++k) v[k] = s4[min((int)threadIdx.x + 256 * k, n4 - 1)];
     }
 };
+constexpr int row_slots(int n4) { return n4 <= 256 ? 1 : 8; }
 
 // ------------------------------------------------------------------------------ segmented sum of squares
 // rmsnorm's sum of squares is one serial chain, ss = fma(x_i, x_i, ss) for i = 0 .. D-1 in order (ops_ref.cpp:195-197):
@@ -405,18 +408,29 @@ __device__ __forceinline__ float seg_chain_run(SegShared& sh, Chain chain) {
 
 // The chain's value ss of x[0, D) in every thread: segments [0, S0) and three of L = (D / 4) rounded down to a
 // multiple of 32 (S0 = D - 3 L >= L). x: global, 64-byte aligned, not written during the kernel; xr: this thread's
-// Row4 of x. All 256 threads of the workgroup call it (two barriers inside). D % 64 == 0, 128 <= D <= 8192.
-__device__ float seg_sum_squares(const float* __restrict__ x, int D, const Row4& xr) {
-    __shared__ SegShared sh;
-    const int tid = (int)threadIdx.x, n4 = D / 4;
+// RowF4 of x; warm: seg_warm(x, D), issued by the same thread. All 256 threads of the workgroup call it (two barriers
+// inside). D % 64 == 0, 128 <= D <= 8192.
+__device__ __forceinline__ Segs4 seg_split(int D) {
     const int L = (D / 4) & ~31;
-    const Segs4 sg{D - 3 * L, L, D};
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    return Segs4{D - 3 * L, L, D};
+}
+// The scalar loads that bring this wave's segment of x into the scalar cache (issued early, consumed by
+// seg_sum_squares).
+__device__ __forceinline__ SegWarm seg_warm(const float* __restrict__ x, int D) {
+    const Segs4 sg = seg_split(D);
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     SegWarm warm;
     warm.issue(x + sg.start(wave), sg.len(wave));
+    return warm;
+}
+template <int R>
+__device__ float seg_sum_squares(const float* __restrict__ x, int D, const RowF4<R>& xr, const SegWarm& warm) {
+    __shared__ SegShared sh;
+    const int tid = (int)threadIdx.x, n4 = D / 4;
+    const Segs4 sg = seg_split(D);
     double p1 = 0.0, p2 = 0.0, p3 = 0.0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < R; ++k) {
         const int i4 = tid + 256 * k;
         if (i4 < n4) {
             const float4 v = xr.v[k];
@@ -449,24 +463,13 @@ __device__ __forceinline__ float lds_sum_squares(const float* xs, int D) {
 // y = x * scale * w of the row xs[0..D) (LDS; each thread reads and rewrites its own float4s, slot k = tid + 256 k),
 // also to `normed` when given, then quantize_q8 of y. All 256 threads call it; xs is free after its return only
 // after a barrier.
-__device__ void normalize_quant_lds(float* xs, int D, float scale, const Row4& wr, int8_t* __restrict__ oq,
-                                    float* __restrict__ od, float* __restrict__ normed);
-
-// rmsnorm of the row xs[0..D) (LDS, 16-byte aligned, complete) with weight w (loaded into wr by the caller before
-// the row was complete, so its latency is hidden), then quantize_q8 of the normed row; also written to `normed`
-// when given (ops_ref.cpp:195-199: ss += x*x as one FMA per element in order, scale = 1/sqrt(ss/n + eps),
-// y = x * scale * w). Called by all 256 threads of a workgroup; D % 64 == 0, D <= 8192.
-__device__ void norm_quant_lds(float* xs, int D, const Row4& wr, float eps, int8_t* __restrict__ oq,
-                               float* __restrict__ od, float* __restrict__ normed) {
-    normalize_quant_lds(xs, D, rms_scale(lds_sum_squares(xs, D), D, eps), wr, oq, od, normed);
-}
-
-__device__ void normalize_quant_lds(float* xs, int D, float scale, const Row4& wr, int8_t* __restrict__ oq,
+template <int R>
+__device__ void normalize_quant_lds(float* xs, int D, float scale, const RowF4<R>& wr, int8_t* __restrict__ oq,
                                     float* __restrict__ od, float* __restrict__ normed) {
     const int tid = (int)threadIdx.x, n4 = D / 4;
     float4* x4 = reinterpret_cast<float4*>(xs);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < R; ++k) {
         const int i4 = tid + 256 * k;
         if (i4 < n4) {
             float4 xv = x4[i4];
@@ -480,6 +483,16 @@ __device__ void normalize_quant_lds(float* xs, int D, float scale, const Row4& w
     }
     __syncthreads();
     quant_row_x8(xs, D, oq, od);
+}
+
+// rmsnorm of the row xs[0..D) (LDS, 16-byte aligned, complete) with weight w (loaded into wr by the caller before
+// the row was complete, so its latency is hidden), then quantize_q8 of the normed row; also written to `normed`
+// when given (ops_ref.cpp:195-199: ss += x*x as one FMA per element in order, scale = 1/sqrt(ss/n + eps),
+// y = x * scale * w). Called by all 256 threads of a workgroup; D % 64 == 0, D <= 8192.
+template <int R>
+__device__ void norm_quant_lds(float* xs, int D, const RowF4<R>& wr, float eps, int8_t* __restrict__ oq,
+                               float* __restrict__ od, float* __restrict__ normed) {
+    normalize_quant_lds(xs, D, rms_scale(lds_sum_squares(xs, D), D, eps), wr, oq, od, normed);
 }
 
 // Activation fill for a GEMV tile whose input is rmsnorm(x) * w quantized (the decode step's q/k/v and gate/up
@@ -500,21 +513,38 @@ struct NormAct {
     float eps;
     int D;
     float* tmp;
-    template <bool XL>
-    __device__ __forceinline__ void fill(int8_t* xs, float* xds) const {
+
+    // The loads the norm starts from (issued before the tile's weight loads, whose issue would otherwise hold them
+    // up): the residual row and its scalar-cache warm-up, and the norm weight.
+    template <int R>
+    struct Pre {
+        RowF4<R> wr, xr;
+        SegWarm warm;
+    };
+    // EMB: the row is the embedding of *tok (eq set); the same loads whatever the branch below, so the compiler counts
+    // the outstanding loads exactly where the row is first used.
+    template <int R, bool EMB>
+    __device__ __forceinline__ Pre<R> begin() const {
+        Pre<R> p;
+        load_row<R, EMB>(p.xr, (int)threadIdx.x, D / 4);
+        if (!EMB && D >= 128) p.warm = seg_warm(x, D);  // uniform
+        p.wr.load(w, D / 4);
+        return p;
+    }
+
+    template <bool XL, int R, bool EMB>
+    __device__ __forceinline__ void fill(const Pre<R>& p, int8_t* xs, float* xds) const {
         static_assert(XL, "the normed activation is produced in LDS");
         const int tid = (int)threadIdx.x, n4 = D / 4;
-        Row4 wr, xr;
-        wr.load(w, n4);
+        const RowF4<R>& wr = p.wr;
+        const RowF4<R>& xr = p.xr;
         float4* t4 = reinterpret_cast<float4*>(tmp);
         float ss;
-        if (!eq && D >= 128) {  // uniform
-            xr.load(x, n4);
-            ss = seg_sum_squares(x, D, xr);
+        if (!EMB && D >= 128) {  // uniform
+            ss = seg_sum_squares(x, D, xr, p.warm);
         } else {
-            load_row(xr, tid, n4);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
+            for (int k = 0; k < R; ++k) {
                 const int i4 = tid + 256 * k;
                 if (i4 < n4) {
                     t4[i4] = xr.v[k];
@@ -526,7 +556,7 @@ struct NormAct {
         }
         const float scale = rms_scale(ss, D, eps);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < R; ++k) {
             const int i4 = tid + 256 * k;
             if (i4 < n4) {
                 float4 y = xr.v[k];
@@ -541,10 +571,11 @@ struct NormAct {
         quant_row_x8(tmp, D, xs, xds);
     }
 
-    // The row to normalise into xr: the embedding of *tok (eq set) or x.
-    __device__ __forceinline__ void load_row(Row4& xr, int tid, int n4) const {
+    // The row to normalise into xr: the embedding of *tok (EMB) or x.
+    template <int R, bool EMB>
+    __device__ __forceinline__ void load_row(RowF4<R>& xr, int tid, int n4) const {
         const int nb = D / QK;
-        if (eq) {
+        if constexpr (EMB) {
             int t = *tok;
             const bool bad = t < 0 || t >= V;
             if (bad && tid == 0 && blockIdx.x == 0) atomicOr(status, kStatusToken);
@@ -552,7 +583,7 @@ struct NormAct {
             const int8_t* er = eq + (size_t)t * D;
             const uint16_t* sr = es + (size_t)t * nb;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
+            for (int k = 0; k < R; ++k) {
                 const int i4 = min(tid + 256 * k, n4 - 1);
                 const uint32_t c4 = *reinterpret_cast<const uint32_t*>(er + 4 * i4);
                 const float sc = h2f(sr[i4 / (QK / 4)]);
@@ -567,10 +598,24 @@ struct NormAct {
     }
 };
 
+// A NormAct with its row slots (R = row_slots(D / 4)) and row source (EMB: the embedding, eq set) fixed, in the
+// interface gemv_tile takes.
+template <int R, bool EMB>
+struct NormActR {
+    NormAct a;
+    template <bool XL>
+    __device__ __forceinline__ NormAct::Pre<R> begin() const { return a.template begin<R, EMB>(); }
+    template <bool XL>
+    __device__ __forceinline__ void fill(const NormAct::Pre<R>& p, int8_t* xs, float* xds) const {
+        a.template fill<XL, R, EMB>(p, xs, xds);
+    }
+};
+
 // ------------------------------------------------------------------------------------------------------ kernels
 
 // x[t] = embedding row of tokens[t] (Q8_0 get_row, ops_ref.cpp:176-181: code * f16 scale, exact in f32), then the
 // first layer's rmsnorm and quantization. One workgroup per token.
+template <int R>
 __global__ __launch_bounds__(256) void embed_norm_quant_kernel(const int32_t* __restrict__ tokens,
                                                                const int8_t* __restrict__ eq,
                                                                const uint16_t* __restrict__ es, int D, int V,
@@ -579,7 +624,7 @@ __global__ __launch_bounds__(256) void embed_norm_quant_kernel(const int32_t* __
                                                                float* __restrict__ od, int* __restrict__ status) {
     __shared__ __align__(16) float xs[8192 + kChainPad];
     const int t = blockIdx.x, tid = threadIdx.x;
-    Row4 wr;
+    RowF4<R> wr;
     wr.load(w, D / 4);
     int tok = tokens[t];
     const bool bad = tok < 0 || tok >= V;
@@ -606,18 +651,19 @@ __global__ __launch_bounds__(256) void embed_norm_quant_kernel(const int32_t* __
 
 // One workgroup per token: residual add x += o, then rmsnorm with weight w and int8 quantization of the normed row;
 // the normed row is also written to `normed` when given. D <= 8192.
+template <int R>
 __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(float* __restrict__ x, const float* __restrict__ o,
                                                                 const float* __restrict__ w, int D, float eps,
                                                                 int8_t* __restrict__ xq, float* __restrict__ xd,
                                                                 float* __restrict__ normed) {
     __shared__ __align__(16) float xs[8192 + kChainPad];
     const int t = blockIdx.x, tid = threadIdx.x, n4 = D / 4;
-    Row4 wr, xr, orow;
+    RowF4<R> wr, xr, orow;
     wr.load(w, n4);
     xr.load(x + (size_t)t * D, n4);
     orow.load(o + (size_t)t * D, n4);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < R; ++k) {
         const int i4 = tid + 256 * k;
         if (i4 < n4) {
             float4 v = xr.v[k];
@@ -960,7 +1006,7 @@ struct QkvSegs {
     int tiles0, tiles1;
 };
 
-template <int DT, int U>
+template <int DT, int U, int R, bool EMB>
 __global__ __launch_bounds__(256) void gemv_qkv_norm_kernel(QkvSegs a, NormAct act, int nb, int tile_rows,
                                                             uint32_t nb_magic) {
     extern __shared__ __align__(16) float smem[];
@@ -983,7 +1029,9 @@ __global__ __launch_bounds__(256) void gemv_qkv_norm_kernel(QkvSegs a, NormAct a
     act.tmp = smem + gemv_tile_lds_bytes(nb * QK, tile_rows, true) / 4;
     constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
     const GemvSegs<1> segs{{w + (size_t)ra * nb * kBlockBytes}, {sc + (size_t)ra * nb}};
-    const float val = gemv_tile<DT, U, true, 1>(segs, nullptr, nullptr, nb, nrows, tile_rows, nb_magic, smem, act);
+    const float val =
+        gemv_tile<DT, U, true, 1>(segs, nullptr, nullptr, nb, nrows, tile_rows, nb_magic, smem,
+                                  NormActR<R, EMB>{act});
     if ((int)threadIdx.x < nrows) out[ra + threadIdx.x] = val;
 }
 
@@ -1006,7 +1054,7 @@ __global__ __launch_bounds__(256) void gemv_residual_kernel(const uint8_t* __res
 // One token's gate and up GEMVs over the same 32 rows of both matrices, from the normed MLP input each workgroup
 // builds itself (NormAct), then h = g / (1 + expf(-g)) * u and the quantization of those 32 values (one block) for
 // the down projection.
-template <int DT, int U>
+template <int DT, int U, int R>
 __global__ __launch_bounds__(256) void gemv_swiglu_norm_kernel(const uint8_t* __restrict__ wg,
                                                                const uint16_t* __restrict__ sg,
                                                                const uint8_t* __restrict__ wu,
@@ -1020,7 +1068,8 @@ __global__ __launch_bounds__(256) void gemv_swiglu_norm_kernel(const uint8_t* __
     constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
     const GemvSegs<2> segs{{wg + (size_t)ra * nb * kBlockBytes, wu + (size_t)ra * nb * kBlockBytes},
                            {sg + (size_t)ra * nb, su + (size_t)ra * nb}};
-    const float val = gemv_tile<DT, U, true, 2>(segs, nullptr, nullptr, nb, QK, 2 * QK, nb_magic, smem, act);
+    const float val =
+        gemv_tile<DT, U, true, 2>(segs, nullptr, nullptr, nb, QK, 2 * QK, nb_magic, smem, NormActR<R, false>{act});
     if (tid < 2 * QK) gu[tid] = val;
     __syncthreads();
     if (tid < QK) {
@@ -1035,19 +1084,21 @@ __global__ __launch_bounds__(256) void residual_add_kernel(float* __restrict__ x
 }
 
 // rmsnorm + quantization of one row (the final norm before the head), normed row also to `normed`.
+template <int R>
 __global__ __launch_bounds__(256) void norm_quant_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                          int D, float eps, int8_t* __restrict__ oq,
                                                          float* __restrict__ od, float* __restrict__ normed) {
     __shared__ __align__(16) float xs[8192 + kChainPad];
     const int tid = threadIdx.x, n4 = D / 4;
-    Row4 wr, xr;
-    wr.load(w, n4);
+    RowF4<R> wr, xr;
     xr.load(x, n4);
+    const SegWarm warm = D >= 128 ? seg_warm(x, D) : SegWarm{};
+    wr.load(w, n4);
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < R; ++k)
         if (tid + 256 * k < n4) reinterpret_cast<float4*>(xs)[tid + 256 * k] = xr.v[k];
     if (D >= 128) {  // uniform
-        normalize_quant_lds(xs, D, rms_scale(seg_sum_squares(x, D, xr), D, eps), wr, oq, od, normed);
+        normalize_quant_lds(xs, D, rms_scale(seg_sum_squares(x, D, xr, warm), D, eps), wr, oq, od, normed);
     } else {
         __syncthreads();
         norm_quant_lds(xs, D, wr, eps, oq, od, normed);
@@ -1172,6 +1223,15 @@ hipError_t dalloc(Decoder* d, void** p, size_t bytes) {
 
 // Calls f(dt, u, xl) with std::integral_constant arguments for the plan's dtype, unroll and activation staging, so a
 // caller can launch KERNEL<dt, u, xl> for any plan gemv_plan makes.
+// Calls f with the row-slot count (std::integral_constant) of rows of D floats.
+template <typename F>
+void by_row_slots(int D, F&& f) {
+    if (row_slots(D / 4) == 1)
+        f(std::integral_constant<int, 1>{});
+    else
+        f(std::integral_constant<int, 8>{});
+}
+
 template <typename F>
 hipError_t plan_dispatch(int dtype, const GemvPlan& p, F&& f) {
     using std::integral_constant;
@@ -1198,10 +1258,12 @@ hipError_t plan_dispatch(int dtype, const GemvPlan& p, F&& f) {
 
 hipError_t embed(Decoder* d, const int32_t* tokens, int n, hipStream_t s) {
     const qh_tensor& emb = d->t[T_EMBED];
-    hipLaunchKernelGGL(embed_norm_quant_kernel, dim3(n), dim3(256), 0, s, tokens,
-                       reinterpret_cast<const int8_t*>(quants(emb)),
-                       reinterpret_cast<const uint16_t*>(quants(emb) + (size_t)emb.rows * emb.cols), d->hp.dim,
-                       d->hp.vocab_size, d->x, lf(d, 0, L_ATTN_NORM), d->hp.norm_eps, d->qa, d->da, d->status);
+    by_row_slots(d->hp.dim, [&](auto r) {
+        hipLaunchKernelGGL((embed_norm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, tokens,
+                           reinterpret_cast<const int8_t*>(quants(emb)),
+                           reinterpret_cast<const uint16_t*>(quants(emb) + (size_t)emb.rows * emb.cols), d->hp.dim,
+                           d->hp.vocab_size, d->x, lf(d, 0, L_ATTN_NORM), d->hp.norm_eps, d->qa, d->da, d->status);
+    });
     return hipGetLastError();
 }
 
@@ -1249,8 +1311,16 @@ hipError_t launch_qkv_norm(Decoder* d, int l, const GemvPlan& p, size_t lds, con
     const unsigned grid = (unsigned)(a.tiles0 + a.tiles1 + (wv.rows + T - 1) / T);
     const int nb = wq.cols / QK;
     return plan_dispatch(wq.dtype, p, [&](auto dt, auto u, auto) {
-        hipLaunchKernelGGL((gemv_qkv_norm_kernel<decltype(dt)::value, decltype(u)::value>), dim3(grid), dim3(256), lds,
-                           s, a, act, nb, T, nb_magic(nb));
+        by_row_slots(act.D, [&](auto r) {
+            if (act.eq)
+                hipLaunchKernelGGL((gemv_qkv_norm_kernel<decltype(dt)::value, decltype(u)::value, decltype(r)::value,
+                                                         true>),
+                                   dim3(grid), dim3(256), lds, s, a, act, nb, T, nb_magic(nb));
+            else
+                hipLaunchKernelGGL((gemv_qkv_norm_kernel<decltype(dt)::value, decltype(u)::value, decltype(r)::value,
+                                                         false>),
+                                   dim3(grid), dim3(256), lds, s, a, act, nb, T, nb_magic(nb));
+        });
     });
 }
 
@@ -1275,8 +1345,10 @@ hipError_t residual(Decoder* d, const qh_tensor& W, const int8_t* xq, const floa
 }
 
 hipError_t norm_quant(Decoder* d, const float* w, float* normed, hipStream_t s) {
-    hipLaunchKernelGGL(norm_quant_kernel, dim3(1), dim3(256), 0, s, d->x, w, d->hp.dim, d->hp.norm_eps, d->qa, d->da,
-                       normed);
+    by_row_slots(d->hp.dim, [&](auto r) {
+        hipLaunchKernelGGL((norm_quant_kernel<decltype(r)::value>), dim3(1), dim3(256), 0, s, d->x, w, d->hp.dim,
+                           d->hp.norm_eps, d->qa, d->da, normed);
+    });
     return hipGetLastError();
 }
 
@@ -1288,12 +1360,15 @@ hipError_t gate_up(Decoder* d, int l, hipStream_t s) {
     if (d->fuse && wg.dtype == wu.dtype && lds <= kFuseLds) {
         const unsigned grid = (unsigned)(wg.rows / QK);
         const NormAct act = make_norm(d, false, lf(d, l, L_FFN_NORM));
-        if (wg.dtype == kQ8)
-            hipLaunchKernelGGL((gemv_swiglu_norm_kernel<kQ8, 8>), dim3(grid), dim3(256), lds, s, quants(wg),
-                               scales(wg), quants(wu), scales(wu), act, nb, nb_magic(nb), d->qb, d->db);
-        else
-            hipLaunchKernelGGL((gemv_swiglu_norm_kernel<kQ4, 8>), dim3(grid), dim3(256), lds, s, quants(wg),
-                               scales(wg), quants(wu), scales(wu), act, nb, nb_magic(nb), d->qb, d->db);
+        by_row_slots(d->hp.dim, [&](auto r) {
+            constexpr int R = decltype(r)::value;
+            if (wg.dtype == kQ8)
+                hipLaunchKernelGGL((gemv_swiglu_norm_kernel<kQ8, 8, R>), dim3(grid), dim3(256), lds, s, quants(wg),
+                                   scales(wg), quants(wu), scales(wu), act, nb, nb_magic(nb), d->qb, d->db);
+            else
+                hipLaunchKernelGGL((gemv_swiglu_norm_kernel<kQ4, 8, R>), dim3(grid), dim3(256), lds, s, quants(wg),
+                                   scales(wg), quants(wu), scales(wu), act, nb, nb_magic(nb), d->qb, d->db);
+        });
         return hipGetLastError();
     }
     QH_TRY(norm_quant(d, lf(d, l, L_FFN_NORM), nullptr, s));
@@ -1355,8 +1430,10 @@ hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
     const int D = hp.dim, F = hp.ffn_dim;
     for (int l = 0; l < hp.n_layers; ++l) {
         if (l > 0) {
-            hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(n), dim3(256), 0, s, d->x, d->o, lf(d, l, L_ATTN_NORM),
-                               D, hp.norm_eps, d->qa, d->da, nullptr);
+            by_row_slots(D, [&](auto r) {
+                hipLaunchKernelGGL((add_rmsnorm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, d->x,
+                                   d->o, lf(d, l, L_ATTN_NORM), D, hp.norm_eps, d->qa, d->da, nullptr);
+            });
             QH_TRY(hipGetLastError());
         }
         const qh_tensor &wq = lt(d, l, L_WQ), &wk = lt(d, l, L_WK), &wv = lt(d, l, L_WV);
@@ -1366,8 +1443,10 @@ hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
         QH_TRY(attention(d, l, n, s));
         const qh_tensor& wo = lt(d, l, L_WO);
         QH_TRY(launch_matmul(d->o, wo.rows, wo, d->qb, d->db, n, 0, wo.rows, s));
-        hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(n), dim3(256), 0, s, d->x, d->o, lf(d, l, L_FFN_NORM), D,
-                           hp.norm_eps, d->qa, d->da, nullptr);
+        by_row_slots(D, [&](auto r) {
+            hipLaunchKernelGGL((add_rmsnorm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, d->x, d->o,
+                               lf(d, l, L_FFN_NORM), D, hp.norm_eps, d->qa, d->da, nullptr);
+        });
         QH_TRY(hipGetLastError());
         const qh_tensor &wg = lt(d, l, L_WG), &wu = lt(d, l, L_WU), &wd = lt(d, l, L_WD);
         QH_TRY(launch_matmul(d->g, wg.rows, wg, d->qa, d->da, n, 0, wg.rows, s));
@@ -1518,8 +1597,11 @@ hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, i
         last = m - 1;
     }
     // final residual add, norm and quantization of the last token only, then the head
-    hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(1), dim3(256), 0, s, d->x + (size_t)last * D,
-                       d->o + (size_t)last * D, final_norm(d), D, hp.norm_eps, d->qa, d->da, d->hidden);
+    by_row_slots(D, [&](auto r) {
+        hipLaunchKernelGGL((add_rmsnorm_quant_kernel<decltype(r)::value>), dim3(1), dim3(256), 0, s,
+                           d->x + (size_t)last * D, d->o + (size_t)last * D, final_norm(d), D, hp.norm_eps, d->qa,
+                           d->da, d->hidden);
+    });
     QH_TRY(hipGetLastError());
     QH_TRY(run_head(d, top_k, s));
     hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + n);

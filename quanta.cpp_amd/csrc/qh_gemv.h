@@ -120,20 +120,29 @@ __host__ __device__ __forceinline__ size_t gemv_tile_lds_bytes(int cols, int til
 }
 
 // Stages the activation for a tile: its block scales into xds and, when the codes are read from LDS (XL), its codes
-// into xs, straight from the quantized activation in global memory. Issued right behind the first pass of weight
-// loads, so it arrives in the same round trip.
+// into xs, straight from the quantized activation in global memory: begin() issues the first loads (ahead of the
+// tile's weight loads), fill() stores them and loads the rest.
 struct GlobalAct {
     const int8_t* __restrict__ xq;
     const float* __restrict__ xd;
     int nb;
+    struct Pre {
+        uint4 xv;
+        float dv;
+    };
     template <bool XL>
-    __device__ __forceinline__ void fill(int8_t* xs, float* xds) const {
+    __device__ __forceinline__ Pre begin() const {
         const int tid = (int)threadIdx.x, xch = nb * QK / 16;
-        uint4 xv = make_uint4(0u, 0u, 0u, 0u);
-        if constexpr (XL) xv = load16(xq + min(tid, xch - 1) * 16);
-        const float dv = xd[min(tid, nb - 1)];
-        if (XL && tid < xch) reinterpret_cast<uint4*>(xs)[tid] = xv;
-        if (tid < nb) xds[tid] = dv;
+        Pre p{make_uint4(0u, 0u, 0u, 0u), 0.0f};
+        if constexpr (XL) p.xv = load16(xq + min(tid, xch - 1) * 16);
+        p.dv = xd[min(tid, nb - 1)];
+        return p;
+    }
+    template <bool XL>
+    __device__ __forceinline__ void fill(const Pre& p, int8_t* xs, float* xds) const {
+        const int tid = (int)threadIdx.x, xch = nb * QK / 16;
+        if (XL && tid < xch) reinterpret_cast<uint4*>(xs)[tid] = p.xv;
+        if (tid < nb) xds[tid] = p.dv;
         if constexpr (XL)
             for (int i = tid + 256; i < xch; i += 256) reinterpret_cast<uint4*>(xs)[i] = load16(xq + i * 16);
         for (int i = tid + 256; i < nb; i += 256) xds[i] = xd[i];
@@ -143,9 +152,10 @@ struct GlobalAct {
 // nrows rows of each of the NSEG segments of sg . x, for one workgroup of 256 threads: virtual row v is row v % nrows
 // of segment v / nrows. tile_rows: the virtual row capacity the LDS layout is sized for (>= NSEG * nrows). Returns
 // the value of virtual row threadIdx.x for threads below NSEG * nrows, 0 for the others. smem: dynamic LDS of
-// gemv_tile_lds_bytes(nb * 32, tile_rows, XL) bytes. act.fill<XL>(xs, xds) stages the activation (codes in LDS when
-// XL; it may use its own barriers, all 256 threads call it) after the first pass of weight loads is issued; xq / xd
-// are read per chunk when !XL. The LDS is free for reuse only after a barrier.
+// gemv_tile_lds_bytes(nb * 32, tile_rows, XL) bytes. act.begin<XL>() issues the activation's first loads, before the
+// first pass of weight loads; act.fill<XL>(pre, xs, xds) then stages the activation (codes in LDS when XL; it may use
+// its own barriers, all 256 threads call it); xq / xd are read per chunk when !XL. The LDS is free for reuse only
+// after a barrier.
 template <int DT, int U, bool XL, int NSEG = 1, typename Act = GlobalAct>
 __device__ __forceinline__ float gemv_tile(const GemvSegs<NSEG>& sg, const int8_t* __restrict__ xq,
                                            const float* __restrict__ xd, int nb, int nrows, int tile_rows,
@@ -161,9 +171,10 @@ __device__ __forceinline__ float gemv_tile(const GemvSegs<NSEG>& sg, const int8_
     const int nchunks = vrows * nb * kChunksPerBlock;
     const int split = nrows * nb * kChunksPerBlock;
 
+    const auto pre = act.template begin<XL>();  // the activation's loads go out first: the products wait for them
     GemvPass<DT, U, XL, NSEG> cur;
     cur.load(sg, split, xq, 0, nchunks - 1, nb, nb_magic);
-    act.template fill<XL>(xs, xds);
+    act.template fill<XL>(pre, xs, xds);
     zero_chain_prefix(dxs, prod, nb, vrows);
     if constexpr (XL) __syncthreads();
     float* prow = prod + zp;
