@@ -873,6 +873,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // exp, kept in LDS and, for the segmented softmax sum, in this workgroup's global row (read back through scalar
     // loads after the barrier below), with each lane's exact partial sums below the segment starts
     float* erow = escr + (size_t)(t * gridDim.x + h) * escr_stride;
+    // the normalized weights, for the V chain's scalar loads (lines of their own: none of them is in the scalar cache
+    // with older contents)
+    float* arow = escr + (size_t)((gridDim.y + t) * gridDim.x + h) * escr_stride;
     const bool seg = nrows >= 128;  // uniform; shorter rows keep the single chain
     const int Ls = (nrows / 4) & ~15;
     const Segs4 sg{(nrows - 3 * Ls) & ~15, Ls, nrows};
@@ -910,57 +913,84 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         sum = sum_sh;
     }
     const float inv = 1.0f / sum;
-    for (int j = tid; j < nrows; j += 256) att[j] = att[j] * inv;
+    for (int j = tid; j < nrows; j += 256) {
+        const float a = att[j] * inv;
+        att[j] = a;
+        arow[j] = a;
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the weight row's stores are complete before the barrier
     __syncthreads();
 
     // out_i = sum_j a_j * v_ji, one FMA per position in order (model.cpp:131-135): thread i per dimension, over
-    // the rows of each LDS stage. Batches of 32 rows (4 V reads, 8 broadcast reads of the weights) at immediate
-    // offsets, two register sets alternating; reads past the stage stay inside the padding.
+    // the rows of each LDS stage. The weights come as scalar operands (scalar loads of arow, 32 per batch, the next
+    // batch's loads and V reads in flight while one batch is consumed), so a batch of 32 positions is 4 V reads and
+    // 32 FMAs; the waves without dimensions bring the weight row into the scalar cache meanwhile. V reads past the
+    // stage stay inside its padding, weight reads inside arow's slack (64 floats past the context).
     float acc = 0.0f;
     for (int s0 = 0;;) {
         const int se = min(nrows, s0 + kVRows);
         if (tid < HD) {
-            uint4 vA[4], vB[4];
-            float4 aA[8], aB[8];
-            auto ld = [&](uint4(&vv)[4], float4(&aa)[8], int jr) {  // rows s0 + jr .. + 31 (jr % 32 == 0)
+            const_v16f_ptr wp = (const_v16f_ptr)(arow + s0);  // s0 is a multiple of 32: 64-byte aligned
+            auto ldv = [&](uint4(&vv)[4], int jr) {  // rows s0 + jr .. + 31 (jr % 32 == 0)
                 const uint4* vp = vst + (jr >> 3) * HD + tid;
-                const float4* ap = reinterpret_cast<const float4*>(lane_ptr(att + s0) + jr);
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) vv[q4] = vp[q4 * HD];
-#pragma unroll
-                for (int q4 = 0; q4 < 8; ++q4) aa[q4] = ap[q4];
             };
-            auto use = [&](const uint4(&vv)[4], const float4(&aa)[8], int cnt) {
+            auto use = [&](const uint4(&vv)[4], const v16f& w0, const v16f& w1, int cnt) {
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) {
                     const uint32_t w[4] = {vv[q4].x, vv[q4].y, vv[q4].z, vv[q4].w};
-                    const float a8[8] = {aa[2 * q4].x, aa[2 * q4].y, aa[2 * q4].z, aa[2 * q4].w,
-                                         aa[2 * q4 + 1].x, aa[2 * q4 + 1].y, aa[2 * q4 + 1].z, aa[2 * q4 + 1].w};
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (8 * q4 + e < cnt)
-                            acc = __builtin_fmaf(a8[e], h2f((uint16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xffffu)),
-                                                 acc);
+                    for (int e = 0; e < 8; ++e) {
+                        const int k = 8 * q4 + e;
+                        if (k < cnt)
+                            acc = __builtin_fmaf(k < 16 ? w0[k & 15] : w1[k & 15],
+                                                 h2f((uint16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xffffu)), acc);
+                    }
                 }
             };
             const int n = se - s0;
+            uint4 vA[4], vB[4];
+            v16f wA0 = wp[0], wA1 = wp[1], wB0, wB1;
+            ldv(vA, 0);
             int jr = 0;
-            ld(vA, aA, 0);
+#pragma unroll 1
             for (; jr + 64 <= n; jr += 64) {
-                ld(vB, aB, jr + 32);
+                wait_lgkm0();
                 __builtin_amdgcn_sched_barrier(0);
-                use(vA, aA, 32);
-                ld(vA, aA, jr + 64);
+                wB0 = wp[(jr + 32) / 16];
+                wB1 = wp[(jr + 32) / 16 + 1];
+                ldv(vB, jr + 32);
                 __builtin_amdgcn_sched_barrier(0);
-                use(vB, aB, 32);
+                use(vA, wA0, wA1, 32);
+                wait_lgkm0();
+                __builtin_amdgcn_sched_barrier(0);
+                wA0 = wp[(jr + 64) / 16];
+                wA1 = wp[(jr + 64) / 16 + 1];
+                ldv(vA, jr + 64);
+                __builtin_amdgcn_sched_barrier(0);
+                use(vB, wB0, wB1, 32);
             }
+            wait_lgkm0();
+            __builtin_amdgcn_sched_barrier(0);
             if (jr + 32 <= n) {
-                ld(vB, aB, jr + 32);
+                wB0 = wp[(jr + 32) / 16];
+                wB1 = wp[(jr + 32) / 16 + 1];
+                ldv(vB, jr + 32);
                 __builtin_amdgcn_sched_barrier(0);
-                use(vA, aA, 32);
-                use(vB, aB, n - jr - 32);
+                use(vA, wA0, wA1, 32);
+                wait_lgkm0();
+                __builtin_amdgcn_sched_barrier(0);
+                use(vB, wB0, wB1, n - jr - 32);
             } else {
-                use(vA, aA, n - jr);
+                use(vA, wA0, wA1, n - jr);
+            }
+        } else if (s0 == 0) {  // waves without dimensions: 16 lines of the weight row per scalar-load batch
+            const int nw = 4 - HD / 64, wi = __builtin_amdgcn_readfirstlane(wave - HD / 64);
+            for (int b = wi * 256; b < nrows; b += nw * 256) {
+                SegWarm warm;
+                warm.issue(arow + b, nrows - b);
+                warm.consume();
             }
         }
         s0 = se;
@@ -1163,7 +1193,7 @@ struct Decoder {
     // int8 activations: qa holds a layer's normed input (and the head's), qb the attention / MLP inner activation
     int8_t *qa = nullptr, *qb = nullptr;
     float *da = nullptr, *db = nullptr;
-    float* escr = nullptr;      // attention: one row of exp values per (token, head) workgroup, escr_stride floats
+    float* escr = nullptr;      // attention: rows of exp values, then of weights, per (token, head) workgroup
     int escr_stride = 0;
     int32_t* tokens = nullptr;  // [kChunk] prefill input / [0] decode input
     // token history (prompt ids since position 0, then each chosen id) and the optional query / sampler settings
@@ -1528,7 +1558,7 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
     A((void**)&d->da, sizeof(float) * kChunk * (wide / QK));
     A((void**)&d->db, sizeof(float) * kChunk * (wide / QK));
     d->escr_stride = escr_stride(hp->ctx_len);
-    A((void**)&d->escr, sizeof(float) * (size_t)kChunk * hp->n_heads * d->escr_stride);
+    A((void**)&d->escr, sizeof(float) * 2 * (size_t)kChunk * hp->n_heads * d->escr_stride);  // exp rows, weight rows
     A((void**)&d->tokens, sizeof(int32_t) * kChunk);
     A((void**)&d->hist, sizeof(int32_t) * ((size_t)hp->ctx_len + 1));
     A((void**)&d->hist_len, 256);
