@@ -180,29 +180,30 @@ __device__ __forceinline__ int dot_q4_block(const uint4 w, const uint4 xlo, cons
 
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
-// The same chain over 16-byte aligned operands, read four blocks per LDS access.
-__device__ __forceinline__ float chain_lds4(const float* p, const float* dx, int nb) {
-    float acc = 0.0f;
-    int b = 0;
-#pragma unroll 4
-    for (; b + 4 <= nb; b += 4) {
-        const float4 pv = *reinterpret_cast<const float4*>(p + b);
-        const float4 xv = *reinterpret_cast<const float4*>(dx + b);
-        acc = __builtin_fmaf(pv.x, xv.x, acc);
-        acc = __builtin_fmaf(pv.y, xv.y, acc);
-        acc = __builtin_fmaf(pv.z, xv.z, acc);
-        acc = __builtin_fmaf(pv.w, xv.w, acc);
-    }
-    for (; b < nb; ++b) acc = __builtin_fmaf(p[b], dx[b], acc);
-    return acc;
-}
-
 // Pipelined chain rows (chain_lds_pipe): a row of nb operands is stored as chain_len32(nb) - nb zeros followed by
 // the nb operands, rows chain_stride32(nb) floats apart (16-byte aligned, 4 mod 32 floats, so 16-byte reads of
 // neighbouring rows fall in different banks), and kChainPipePad readable floats follow the last row.
 constexpr int kChainPipePad = 32;
 __host__ __device__ __forceinline__ int chain_len32(int nb) { return (nb + 31) & ~31; }
 __host__ __device__ __forceinline__ int chain_stride32(int nb) { return chain_len32(nb) + 4; }
+
+// Zeros in front of the padded chain rows of dxs and of rows [0, nrows) of prod (rows chain_stride32(nb) apart), by a
+// workgroup of 256 threads.
+__device__ __forceinline__ void zero_chain_prefix(float* dxs, float* prod, int nb, int nrows) {
+    const int zp = chain_len32(nb) - nb, ps = chain_stride32(nb), tid = (int)threadIdx.x;
+    if (zp == 0) return;
+    if ((zp & 3) == 0) {  // uniform (nb % 4 == 0): thread r writes the 16-byte zero groups of padded row r
+        for (int r = tid; r <= nrows; r += 256) {
+            float4* z = reinterpret_cast<float4*>(r == 0 ? dxs : prod + (size_t)(r - 1) * ps);
+            for (int k = 0; k < (zp >> 2); ++k) z[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        return;
+    }
+    for (int i = tid; i < (nrows + 1) * 32; i += 256) {  // 256-thread workgroups
+        const int r = i >> 5, j = i & 31;
+        if (j < zp) (r == 0 ? dxs : prod + (size_t)(r - 1) * ps)[j] = 0.0f;
+    }
+}
 
 // The serial chain over a padded row: acc = fma(p[i], dx[i], acc) for i in [0, L), L a multiple of 32. The leading
 // zeros of p and dx leave acc = +0 exactly (fma(0, 0, +0) = +0), so the result is the chain over the nb operands
@@ -263,13 +264,5 @@ __device__ __forceinline__ float chain_lds_pipe(const float* p, const float* dx,
     }
     return acc;
 }
-
-// Row stride (floats) of an LDS product tile read by chain_lds4: a multiple of 4, and not a multiple of 32, so
-// the 16-byte reads of neighbouring rows fall in different banks.
-__host__ __device__ __forceinline__ int prod_stride4(int nb) {
-    const int p = (nb + 3) & ~3;
-    return (p & 31) == 0 ? p + 4 : p;
-}
-
 
 }  // namespace qh

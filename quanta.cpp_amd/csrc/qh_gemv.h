@@ -96,23 +96,6 @@ __host__ __device__ __forceinline__ size_t gemv_tile_lds_floats(int nb, int tile
     return (size_t)chain_len32(nb) + (size_t)tile_rows * chain_stride32(nb) + kChainPipePad;
 }
 
-// Zeros in front of the padded chain rows of the activation scales (dxs) and of rows [0, nrows) of the products.
-__device__ __forceinline__ void zero_chain_prefix(float* dxs, float* prod, int nb, int nrows) {
-    const int zp = chain_len32(nb) - nb, ps = chain_stride32(nb), tid = (int)threadIdx.x;
-    if (zp == 0) return;
-    if ((zp & 3) == 0) {  // uniform (nb % 4 == 0): thread r writes the 16-byte zero groups of padded row r
-        for (int r = tid; r <= nrows; r += 256) {
-            float4* z = reinterpret_cast<float4*>(r == 0 ? dxs : prod + (size_t)(r - 1) * ps);
-            for (int k = 0; k < (zp >> 2); ++k) z[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-        return;
-    }
-    for (int i = tid; i < (nrows + 1) * 32; i += 256) {  // 256-thread workgroups
-        const int r = i >> 5, j = i & 31;
-        if (j < zp) (r == 0 ? dxs : prod + (size_t)(r - 1) * ps)[j] = 0.0f;
-    }
-}
-
 // LDS bytes of a tile of tile_rows virtual rows (PAIR tiles count both matrices' rows).
 __host__ __device__ __forceinline__ size_t gemv_tile_lds_bytes(int cols, int tile_rows, bool xl) {
     const size_t f = gemv_tile_lds_floats(cols / QK, tile_rows) * 4;

@@ -205,26 +205,28 @@ __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
     uint32_t nb_magic, float* __restrict__ coarse, float* __restrict__ upper, float* __restrict__ logits,
     uint8_t* __restrict__ mark, int32_t* __restrict__ firsts, uint64_t* __restrict__ seedpart, int n_keep,
     int share_cap) {
-    extern __shared__ float smem[];
-    const int ps = prod_stride4(nb);
-    const int nb4 = (nb + 3) & ~3;
-    float* xds = smem;                                   // [nb4]
-    float* xnorm = xds + nb4;                            // [nb4]
-    float* prod0 = xnorm + nb4;                          // [tile][ps] block products, two buffers
+    extern __shared__ __align__(16) float smem[];
+    // Padded chain rows (chain_lds_pipe): zp zeros, then the nb operands.
+    const int L = chain_len32(nb), zp = L - nb, ps = chain_stride32(nb);
+    float* xdsp = smem;                                  // [L] activation scales
+    float* xnormp = xdsp + L;                            // [L] activation block norms
+    float* prod0 = xnormp + L;                           // [tile][ps] block products, two buffers
     float* prod1 = prod0 + (size_t)tile * ps;
     float* errf0 = prod1 + (size_t)tile * ps;            // [tile][ps] block errors, two buffers
     float* errf1 = errf0 + (size_t)tile * ps;
-    uint64_t* wkeys = reinterpret_cast<uint64_t*>(errf1 + (size_t)tile * ps);  // [share_cap]
+    float* bsh = errf1 + (size_t)tile * ps + kChainPipePad;  // [2][64] bounds of a tile (wave 1 -> wave 0)
+    uint64_t* wkeys = reinterpret_cast<uint64_t*>(bsh + 128);                   // [share_cap]
     uint8_t* mflag = reinterpret_cast<uint8_t*>(wkeys + share_cap);             // [2][tile]
     int8_t* xs = reinterpret_cast<int8_t*>(mflag + ((2 * (size_t)tile + 15) & ~size_t(15)));  // [nb * 32]
+    uint64_t* lvl2 = reinterpret_cast<uint64_t*>(prod0);  // [4 * 64] after the tile loop
+    float* xds = xdsp + zp;
+    float* xnorm = xnormp + zp;
     __shared__ int n_elig;
-    __shared__ uint64_t lvl2[4 * 64];
 
     const int tid = (int)threadIdx.x;
     const int32_t* must;
     int n_must;
     must_span(mq, must, n_must);
-    lvl2[tid] = 0ull;  // ordered before its writes by the barriers of the tile loop
     const int ra = (int)((long)blockIdx.x * V / gridDim.x) & ~1;  // even, so error words stay 4-byte aligned
     const int rb = blockIdx.x + 1 == gridDim.x ? V : (int)((long)(blockIdx.x + 1) * V / gridDim.x) & ~1;
     if (ra >= rb) {  // uniform per workgroup: an empty share still publishes an empty list
@@ -234,6 +236,8 @@ __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
 
     ScreenRegs A, B;
     A.load(w4, s4, e32, ra, min(tile, rb - ra), nb);
+    zero_chain_prefix(xdsp, prod0, nb, 2 * tile);   // both product buffers
+    zero_chain_prefix(xnormp, errf0, nb, 2 * tile);  // both error buffers
     const int cols = nb * QK;
     for (int i = tid; i < cols / 16; i += kScreenThreads) reinterpret_cast<uint4*>(xs)[i] = load16(xq + i * 16);
     for (int i = tid; i < nb; i += kScreenThreads) xds[i] = xd[i];
@@ -249,10 +253,19 @@ __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
     }
 
     int elig = 0;  // wave 0: eligible keys so far
-    // One tile whose chunks sit in `regs`: stage into LDS, then wave 0 (one row per lane) runs both chains.
+    // wave 0: the previous tile's rows, coarse scores and bounds buffer, finished once wave 1's bounds are ordered
+    // before it by the next barrier
+    int prev_r = 0, prev_n = 0, prev_buf = 0;
+    float prev_c = 0.0f;
+    auto finish_prev = [&]() {
+        if (tid < prev_n) upper[prev_r + tid] = prev_c + bsh[prev_buf * 64 + tid];
+    };
+    // One tile whose chunks sit in `regs`: stage into LDS, then wave 0 (one row per lane) runs the coarse chains and
+    // wave 1 the bound chains (model.cpp:263-271).
+    int buf = 0;
     auto tile_body = [&](const ScreenRegs& regs, int r, float* prod, float* errf, uint8_t* mf) {
         const int nrows = min(tile, rb - r);
-        regs.stage(prod, errf, ps, nrows, nb, nb_magic, xs);
+        regs.stage(prod + zp, errf + zp, ps, nrows, nb, nb_magic, xs);
         for (int i = tid; i < nrows; i += kScreenThreads) {
             mf[i] = 0;
             mark[r + i] = 0;
@@ -267,20 +280,27 @@ __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
             __syncthreads();
         }
         if (tid < 64) {
+            finish_prev();
             uint64_t key = 0;
+            float c = 0.0f;
             if (tid < nrows) {
                 const int row = r + tid;
-                const float c = chain_lds4(prod + tid * ps, xds, nb);
-                float bound = chain_lds4(errf + tid * ps, xnorm, nb);
-                bound = __builtin_fmaf(bound, 1.001f, 1e-5f);  // model.cpp:271
+                c = chain_lds_pipe(prod + tid * ps, xdsp, L);
                 coarse[row] = c;
-                upper[row] = c + bound;
                 logits[row] = -__builtin_inff();
                 if (row < nv && !mf[tid]) key = score_key(c, row);
                 wkeys[row - ra] = key;
             }
             elig += __popcll(__ballot(key != 0));
+            prev_r = r, prev_n = nrows, prev_buf = buf, prev_c = c;
+        } else if (tid < 128) {
+            const int l = tid - 64;
+            if (l < nrows) {
+                const float bound = chain_lds_pipe(errf + l * ps, xnormp, L);
+                bsh[buf * 64 + l] = __builtin_fmaf(bound, 1.001f, 1e-5f);  // model.cpp:271
+            }
         }
+        buf ^= 1;
     };
     // Two register sets in straight-line halves, so the wait before staging one set leaves the other's loads in
     // flight. Loads in the steady-state loop are unconditional (a conditional load makes the compiler's wait
@@ -303,6 +323,9 @@ __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
     }
     const int R = rb - ra;
     if (tid == 0) n_elig = elig;
+    __syncthreads();
+    if (tid < 64) finish_prev();
+    lvl2[tid] = 0ull;  // over the first product buffer, free now
     __syncthreads();
     // The share's best n_keep keys (keys are unique). Level 1: each wave ranks its quarter of the share (at most
     // 256 keys) and keeps its best n_keep; level 2: wave 0 ranks the 4 * n_keep survivors.
@@ -677,7 +700,7 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
     // A share holds at most V / grid + 3 rows (its ends are rounded down to even rows); sizing its key array by that
     // instead of kScreenMaxShare keeps the LDS under 40 KB, so four workgroups fit on a CU.
     const int share_cap = V / grid + 4;
-    const size_t lds1 = ((size_t)2 * ((nb + 3) & ~3) + 4 * (size_t)tile * prod_stride4(nb)) * 4 +
+    const size_t lds1 = ((size_t)2 * chain_len32(nb) + 4 * (size_t)tile * chain_stride32(nb) + kChainPipePad + 128) * 4 +
                         (size_t)share_cap * 8 + ((2 * (size_t)tile + 15) & ~size_t(15)) + (size_t)D;
     hipLaunchKernelGGL(head_screen_kernel, dim3(grid), dim3(kScreenThreads), lds1, s, w4, s4, e32, xq, xd, V, nb, nv,
                        must, tile, magic, out.coarse, out.upper, out.logits, mark, firsts, seedpart, n_keep,
