@@ -207,10 +207,13 @@ __device__ __forceinline__ void zero_chain_prefix(float* dxs, float* prod, int n
 
 // The serial chain over a padded row: acc = fma(p[i], dx[i], acc) for i in [0, L), L a multiple of 32. The leading
 // zeros of p and dx leave acc = +0 exactly (fma(0, 0, +0) = +0), so the result is the chain over the nb operands
-// from +0, the reference's order. Operands arrive 8 at a time (two 16-byte LDS reads of each) in four rotating
-// batches, three in flight while one is consumed, so the chain runs at the FMA latency rather than the LDS
-// latency; the reads reach 32 floats past p + L and dx + L. p and dx are 16-byte aligned.
+// from +0, the reference's order. Operands arrive 8 at a time (two 16-byte LDS reads of each) in NB rotating
+// batches, NB - 1 in flight while one is consumed, so the chain runs at the FMA latency rather than the LDS
+// latency (NB = 4; NB = 2 holds 32 fewer registers); the reads reach 32 floats past p + L and dx + L. p and dx are
+// 16-byte aligned.
+template <int NB = 4>
 __device__ __forceinline__ float chain_lds_pipe(const float* p, const float* dx, int L) {
+    static_assert(NB == 2 || NB == 4, "two or four batches");
     struct Batch {
         float4 p0, p1, x0, x1;
     };
@@ -231,36 +234,26 @@ __device__ __forceinline__ float chain_lds_pipe(const float* p, const float* dx,
         acc = __builtin_fmaf(q.p1.z, q.x1.z, acc);
         acc = __builtin_fmaf(q.p1.w, q.x1.w, acc);
     };
-    // The first four batches pass through an empty asm: the loop's reload of a batch is then not merged with its
-    // first load into one load at the top of the loop, which would leave nothing in flight across iterations.
+    // The first batches pass through an empty asm: the loop's reload of a batch is then not merged with its first
+    // load into one load at the top of the loop, which would leave nothing in flight across iterations.
     auto pin = [](Batch& q) {
         asm volatile("" : "+v"(q.p0.x), "+v"(q.p0.y), "+v"(q.p0.z), "+v"(q.p0.w), "+v"(q.p1.x), "+v"(q.p1.y),
                      "+v"(q.p1.z), "+v"(q.p1.w));
         asm volatile("" : "+v"(q.x0.x), "+v"(q.x0.y), "+v"(q.x0.z), "+v"(q.x0.w), "+v"(q.x1.x), "+v"(q.x1.y),
                      "+v"(q.x1.z), "+v"(q.x1.w));
     };
-    Batch A, B, C, D;
-    ld(A, 0);
-    ld(B, 8);
-    ld(C, 16);
-    ld(D, 24);
-    pin(A);
-    pin(B);
-    pin(C);
-    pin(D);
-    for (int b = 0; b < L; b += 32) {  // the scheduling barriers keep each batch's reads ahead of the next FMAs
-        use(A);
-        ld(A, b + 32);
-        __builtin_amdgcn_sched_barrier(0);
-        use(B);
-        ld(B, b + 40);
-        __builtin_amdgcn_sched_barrier(0);
-        use(C);
-        ld(C, b + 48);
-        __builtin_amdgcn_sched_barrier(0);
-        use(D);
-        ld(D, b + 56);
-        __builtin_amdgcn_sched_barrier(0);
+    Batch q[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) ld(q[i], 8 * i);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) pin(q[i]);
+    for (int b = 0; b < L; b += 8 * NB) {  // the scheduling barriers keep each batch's reads ahead of the next FMAs
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            use(q[i]);
+            ld(q[i], b + 8 * (NB + i));
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     return acc;
 }

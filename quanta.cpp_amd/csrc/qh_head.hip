@@ -41,9 +41,9 @@ struct HeadCtrl {
 constexpr int kMaxMust = 1 << 22;  // must ids per query (a history window); the screen scans them per tile
 constexpr int kNoFirst = 0x7fffffff;
 constexpr int kScreenThreads = 256;
-constexpr int kScreenU = 8;         // 16-byte weight chunks per thread per tile
+constexpr int kScreenU = 5;         // 16-byte weight chunks per thread per tile (two sets fit 128 VGPRs)
 constexpr int kScreenMaxRows = 64;  // rows per tile: one per lane of wave 0
-constexpr int kScreenErrU = 4;      // 4-byte error words per thread per tile
+constexpr int kScreenErrU = (kScreenU + 1) / 2;  // 4-byte error words per thread per tile (tile * nb / 2 <= 128 U)
 constexpr int kScreenMaxShare = 1024;  // rows per screen workgroup: their keys sit in LDS until the final selection
 constexpr int kSeedThreads = 1024;
 constexpr int kSeedMaxPool = 2048;     // keys that survive the seed threshold, held in LDS
@@ -199,7 +199,7 @@ __device__ __forceinline__ void wave_rank(const uint64_t (&a)[NS], int n, int (&
 
 }  // namespace
 
-__global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
+__global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void head_screen_kernel(
     const uint8_t* __restrict__ w4, const uint16_t* __restrict__ s4, const uint32_t* __restrict__ e32,
     const int8_t* __restrict__ xq, const float* __restrict__ xd, int V, int nb, int nv, HeadMust mq, int tile,
     uint32_t nb_magic, float* __restrict__ coarse, float* __restrict__ upper, float* __restrict__ logits,
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
             float c = 0.0f;
             if (tid < nrows) {
                 const int row = r + tid;
-                c = chain_lds_pipe(prod + tid * ps, xdsp, L);
+                c = chain_lds_pipe<2>(prod + tid * ps, xdsp, L);
                 coarse[row] = c;
                 logits[row] = -__builtin_inff();
                 if (row < nv && !mf[tid]) key = score_key(c, row);
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(kScreenThreads) void head_screen_kernel(
         } else if (tid < 128) {
             const int l = tid - 64;
             if (l < nrows) {
-                const float bound = chain_lds_pipe(errf + l * ps, xnormp, L);
+                const float bound = chain_lds_pipe<2>(errf + l * ps, xnormp, L);
                 bsh[buf * 64 + l] = __builtin_fmaf(bound, 1.001f, 1e-5f);  // model.cpp:271
             }
         }

@@ -41,7 +41,7 @@ size_t argmax_workspace_bytes(int n);
 hipError_t launch_argmax(const float* logits, int n, int32_t* index, void* ws, hipStream_t s);
 
 // Shortlist head. Workspace layout is private to qh_head.hip. Supported hidden sizes: D % 64 == 0 (whole 4-byte
-// words of f16 block errors per row) and D <= kMaxHeadCols (a 64-row tile's errors fit one register pass).
+// words of f16 block errors per row) and D <= kMaxHeadCols (a tile's errors fit one register pass).
 constexpr int kMaxHeadCols = 4096;
 bool head_shape_supported(int D);
 size_t head_workspace_bytes(int V, int D, int top_k);
