@@ -63,11 +63,19 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ v4u ld4(const void* p) { return *reinterpret_cast<const v4u*>(p); }
 
 // LDS DMA (global_load_lds_dwordx4): lane l's 16 bytes at g go to lds_wave + 16 l, where lds_wave is the same LDS
-// address in every lane of the wave. Counted by vmcnt; the LDS data is valid after s_waitcnt vmcnt(0). The body
+// address in every lane of the wave. Counted by vmcnt; the LDS data is valid after s_waitcnt vmcnt(0). Issued in
+// inline assembly, behind the compiler's back: the compiler counts a DMA it knows of as a transfer that may complete
+// out of order, so after one it waits for every outstanding load (vmcnt(0)) before using any earlier load's result
+// and before any LDS access. This way the earlier loads keep their waits, LDS accesses wait for nothing, the caller
+// waits for the transfer itself (s_waitcnt vmcnt(0)) before reading its LDS, and the compiler's waits for loads
+// issued before it become conservative (they also cover the transfers), never short. M0, which the transfer takes
+// its LDS address from, is set right before it (the compiler keeps no value in M0 across code here). The body
 // exists only in the device pass (the host pass cannot form an LDS address).
-__device__ __forceinline__ void lds_dma16(const void* g, void* lds_wave) {
+__device__ __forceinline__ void lds_dma16_async(const void* g, void* lds_wave) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave, 16, 0, 0);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_wave);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(g) : "memory");
 #endif
 }
 // f32 -> f16 (round to nearest even) of an already rounded f32 value, as the reference stores its f32 K / V results
@@ -773,7 +781,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int i = 0; i < CPR; ++i) kpre[r][i] = ld4(kg + (size_t)i * ctx * 8);
     }
-
     if (tid < HALF) rope(qp, bq != nullptr, qs[tid], qs[tid + HALF]);
     for (int e = tid; e < nk; e += 256) {
         const int r = e / HALF, i = e - r * HALF;
@@ -816,57 +823,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
         return sc;
     };
-    // a row of the chunk's own keys (LDS), for rows j >= pos0
-    auto kloc_row = [&](v4u(&kk)[CPR], int j) {
-        const uint16_t* kl = kloc + min(max(j - pos0, 0), kChunk - 1) * HD;
+    // the chunk's own rows j >= pos0 (keys in LDS), before the V DMA below: after it, the first LDS access waits for
+    // the DMA to land (the compiler cannot tell its LDS destination from the other arrays)
+    for (int j = pos0 + tid; j < nrows; j += 256) {
+        v4u kk[CPR];
+        const uint16_t* kl = kloc + (j - pos0) * HD;
 #pragma unroll
         for (int i = 0; i < CPR; ++i) kk[i] = ld4(kl + i * 8);
-    };
-    {  // the preloaded rows tid + 256 r, their chains interleaved
-        float sc[kKPre];
-        v4u kk[kKPre][CPR];
-#pragma unroll
-        for (int r = 0; r < kKPre; ++r) {
-            const int j = tid + 256 * r;
-            v4u kl[CPR];
-            kloc_row(kl, j);
-#pragma unroll
-            for (int i = 0; i < CPR; ++i) kk[r][i] = j < pos0 ? kpre[r][i] : kl[i];
-        }
-#pragma unroll
-        for (int r = 0; r < kKPre; ++r) sc[r] = dot_row(kk[r]);
-#pragma unroll
-        for (int r = 0; r < kKPre; ++r) {
-            const int j = tid + 256 * r;
-            if (j < nrows) {
-                const float a = sc[r] * scale;
-                att[j] = a;
-                mx = a > mx ? a : mx;
-            }
-        }
-    }
-    for (int j = tid + 256 * kKPre; j < nrows; j += 256) {  // longer contexts: one row at a time
-        v4u kk[CPR], kl[CPR];
-        const uint16_t* kg = kc + (kchunk(0, min(j, grow)) << 3);
-#pragma unroll
-        for (int i = 0; i < CPR; ++i) kk[i] = ld4(kg + (size_t)i * ctx * 8);
-        kloc_row(kl, j);
-#pragma unroll
-        for (int i = 0; i < CPR; ++i) kk[i] = j < pos0 ? kk[i] : kl[i];
         const float a = dot_row(kk) * scale;
         att[j] = a;
         mx = a > mx ? a : mx;
     }
-    // The V blocks of the first stage go straight into LDS (DMA, no registers; waited for before the V stage is
-    // read) only now: issued behind the K rows they would have held up the scores, and they arrive during the
-    // softmax.
+    // The first stage's V blocks go straight into LDS (DMA, no registers; waited for before the stage is read) now,
+    // while the cached K rows are still in flight: the memory pipeline takes them behind the K rows, and the scores
+    // below use registers only. A fixed number per wave, the whole stage (clamped onto the last block, whose repeats
+    // write the same data), so the compiler's waits for the K rows count them exactly. Cache blocks stop below
+    // pos0: none is written by this launch (the block holding pos0 carries stale rows from pos0 on, replaced when
+    // the stage is built).
     const int ncb = min((pos0 + 7) / 8, kVBlk);  // cache blocks of the first stage (the last may be partial)
     constexpr int kDmaPerBlk = HD / 64;          // 1 KB (one wave instruction) per DMA chunk
-    for (int c = wave; c < ncb * kDmaPerBlk; c += 4)
-        lds_dma16(vc4 + vchunk(c / kDmaPerBlk, (c % kDmaPerBlk) * 64 + lane), vst + c * 64);
+    constexpr int kVEarly = kVBlk * kDmaPerBlk / 4;  // DMA chunks per wave
+    {
+        const int last = max(ncb * kDmaPerBlk - 1, 0);
+#pragma unroll
+        for (int e = 0; e < kVEarly; ++e) {
+            const int c = min(wave + 4 * e, last);
+            lds_dma16_async(vc4 + vchunk(c / kDmaPerBlk, (c % kDmaPerBlk) * 64 + lane), vst + c * 64);
+        }
+    }
+
+    // the cached rows tid + 256 r (registers only), their chains interleaved; stored after the barrier below
+    float sc[kKPre];
+    {
+#pragma unroll
+        for (int r = 0; r < kKPre; ++r) sc[r] = dot_row(kpre[r]) * scale;
+#pragma unroll
+        for (int r = 0; r < kKPre; ++r) {
+            const int j = tid + 256 * r;
+            if (j < pos0) mx = sc[r] > mx ? sc[r] : mx;
+        }
+    }
+    for (int j = tid + 256 * kKPre; j < pos0; j += 256) {  // longer contexts: one row at a time
+        v4u kk[CPR];
+        const uint16_t* kg = kc + (kchunk(0, j) << 3);
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) kk[i] = ld4(kg + (size_t)i * ctx * 8);
+        const float a = dot_row(kk) * scale;
+        att[j] = a;
+        mx = a > mx ? a : mx;
+    }
     // the maximum does not depend on the order of comparison
     mx = wave_max_sel(mx);
     if (lane == 0) red[wave] = mx;
+#pragma unroll
+    for (int r = 0; r < kKPre; ++r) {
+        const int j = tid + 256 * r;
+        if (j < pos0) att[j] = sc[r];
+    }
     __syncthreads();
     mx = red[0];
     for (int w = 1; w < 4; ++w) mx = red[w] > mx ? red[w] : mx;
