@@ -37,6 +37,15 @@ struct HeadCtrl {
     int n_must;
     int seed_tie;
 };
+// Completion counters of the candidate workgroups, two levels: workgroup b counts into group b % kDoneGroups (one
+// 128-byte line each, after the 256 bytes of HeadCtrl), each group's last workgroup into HeadCtrl::done. Atomics on
+// one address are performed one at a time, so 16 groups of 16 finish sooner than one counter of 256.
+constexpr int kDoneGroups = 16;
+constexpr int kDoneStride = 32;  // unsigned ints per group counter
+static_assert(sizeof(HeadCtrl) <= 256, "the group counters follow HeadCtrl's 256 bytes");
+__device__ __forceinline__ unsigned* group_done(HeadCtrl* ctrl) {
+    return reinterpret_cast<unsigned*>(reinterpret_cast<uint8_t*>(ctrl) + 256);
+}
 
 constexpr int kMaxMust = 1 << 22;  // must ids per query (a history window); the screen scans them per tile
 constexpr int kNoFirst = 0x7fffffff;
@@ -90,7 +99,7 @@ WsLayout ws_layout(int V, int D, int top_k) {
     l.first = align256((size_t)V);
     l.seedpart = l.first + align256((size_t)V * 4);
     l.ctrl = l.seedpart + align256((size_t)parts * keep * sizeof(uint64_t));
-    l.total = l.ctrl + 256;
+    l.total = l.ctrl + 256 + (size_t)kDoneGroups * kDoneStride * 4;
     return l;
 }
 
@@ -557,6 +566,7 @@ __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
             ctrl->n_cand = 0u;
             ctrl->done = 0u;
         }
+        if (lane < kDoneGroups) group_done(ctrl)[lane * kDoneStride] = 0u;
     }
 }
 
@@ -651,11 +661,18 @@ __global__ __launch_bounds__(kCandThreads) void head_cand_kernel(
     if (tid == 0) {
         uint64_t m = wkey[0];
         for (int w = 1; w < kWaves; ++w) m = wkey[w] > m ? wkey[w] : m;
-        if (m) atomicMax(&ctrl->argmax_key, (unsigned long long)m);
-        __threadfence();
-        const unsigned prev = atomicAdd(&ctrl->done, 1u);
-        if (prev == gridDim.x - 1) {  // last workgroup: every append and atomic max is visible
-            __threadfence();
+        // The maximum is performed (its old value has returned) before the completion count moves, so the last
+        // workgroup's atomic reads see every maximum and every count (n_cand's were returned before the rescoring).
+        // It reads nothing else another workgroup of this launch wrote, so no cache write-back fence is needed.
+        // Workgroups without a scored row skip the maximum: atomics on one address serialize.
+        if (m) {
+            const unsigned long long old = atomicMax(&ctrl->argmax_key, (unsigned long long)m);
+            asm volatile("" ::"v"(old));
+        }
+        const unsigned g = blockIdx.x % kDoneGroups, gsize = (gridDim.x - g + kDoneGroups - 1) / kDoneGroups;
+        const bool group_last = atomicAdd(group_done(ctrl) + g * kDoneStride, 1u) == gsize - 1;
+        const unsigned ngroups = gridDim.x < (unsigned)kDoneGroups ? gridDim.x : (unsigned)kDoneGroups;
+        if (group_last && atomicAdd(&ctrl->done, 1u) == ngroups - 1) {  // last workgroup
             const unsigned long long key = atomicAdd(&ctrl->argmax_key, 0ull);
             const int n_cand = (int)atomicAdd(&ctrl->n_cand, 0u);
             stats->top1 = key_row(key);
