@@ -1161,21 +1161,7 @@ struct Pick {
 
 // The chosen token becomes the next input, is appended to out[] and to the token history (session.cpp:45-46), and,
 // after a decode step (advance), the position moves on.
-__global__ void advance_kernel(Pick pick, int32_t* __restrict__ token, int* __restrict__ pos_dev,
-                               int* __restrict__ n_out, int32_t* __restrict__ out, int out_cap,
-                               int32_t* __restrict__ hist, int* __restrict__ hist_len, int hist_cap, int advance) {
-    const int id = pick.id();
-    *token = id;
-    const int k = *n_out;
-    if (k < out_cap) out[k] = id;
-    *n_out = k + 1;
-    const int h = *hist_len;
-    if (h < hist_cap) {
-        hist[h] = id;
-        *hist_len = h + 1;
-    }
-    if (advance) *pos_dev = *pos_dev + 1;
-}
+__global__ void advance_kernel(Pick pick, TokenFeedback fb, int advance) { fb.apply(pick.id(), advance != 0); }
 
 // Appends a prompt chunk to the token history (Session::feed, session.cpp:13-30), first emptying it when the chunk
 // starts a sequence (reset). One workgroup.
@@ -1522,14 +1508,31 @@ HeadMust history_window(const Decoder* d, int window) {
 
 bool shortlist_on(const Decoder* d, int top_k) { return query_top_k(d, top_k) > 0 && head4(d).data; }
 
-hipError_t run_head(Decoder* d, int top_k, hipStream_t s) {
+// The feedback of a chosen token into the decoder's state.
+TokenFeedback token_feedback(Decoder* d) {
+    TokenFeedback fb;
+    fb.token = d->tokens;
+    fb.pos = d->pos;
+    fb.n_out = d->n_out;
+    fb.out = d->out;
+    fb.out_cap = d->out_cap;
+    fb.hist = d->hist;
+    fb.hist_len = d->hist_len;
+    fb.hist_cap = d->hp.ctx_len + 1;
+    return fb;
+}
+
+// advance: a greedy decode step through the shortlist head, whose last kernel then also feeds the token back.
+hipError_t run_head(Decoder* d, int top_k, hipStream_t s, bool advance = false) {
     const qh_tensor& h8 = d->t[T_EMBED];
     if (shortlist_on(d, top_k)) {
         qh_head_query q{query_top_k(d, top_k), d->hp.vocab_size, nullptr, 0};
         qh_head_out out{d->logits, d->coarse, d->upper, d->rows, d->stats};
         const HeadMust must = d->has_query && d->qp.repeat_penalty != 1.f ? history_window(d, d->qp.repeat_window)
                                                                            : HeadMust{};
-        return launch_shortlist_head(h8, head4(d), head_err(d), d->qa, d->da, q, must, out, d->head_ws, s);
+        const TokenFeedback fb = token_feedback(d);
+        return launch_shortlist_head(h8, head4(d), head_err(d), d->qa, d->da, q, must, out, d->head_ws, s,
+                                     advance ? &fb : nullptr);
     }
     QH_TRY(launch_gemv(d->logits, h8, d->qa, d->da, 0, h8.rows, gemv_plan(h8.dtype, h8.cols, h8.rows), s));
     return launch_argmax(d->logits, d->hp.vocab_size, d->top1_full, d->am_ws, s);
@@ -1661,13 +1664,13 @@ hipError_t pick_and_advance(Decoder* d, int top_k, bool advance, hipStream_t s) 
                              d->sp, d->rng, d->sampled, s));
         pick.sampled = d->sampled;
     }
-    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, pick, d->tokens, d->pos, d->n_out, d->out,
-                       d->out_cap, d->hist, d->hist_len, d->hp.ctx_len + 1, advance ? 1 : 0);
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, pick, token_feedback(d), advance ? 1 : 0);
     return hipGetLastError();
 }
 
 hipError_t decoder_step(Decoder* d, int top_k, hipStream_t s) {
     QH_TRY(decode_layers(d, s));
+    if (!d->has_sampler && shortlist_on(d, top_k)) return run_head(d, top_k, s, true);  // greedy: fed back there
     QH_TRY(run_head(d, top_k, s));
     return pick_and_advance(d, top_k, true, s);
 }

@@ -574,7 +574,7 @@ __global__ __launch_bounds__(kCandThreads) void head_cand_kernel(
     const uint8_t* __restrict__ w8, const uint16_t* __restrict__ s8, const int8_t* __restrict__ xq,
     const float* __restrict__ xd, int nb, int nv, const float* __restrict__ upper, const uint8_t* __restrict__ mark,
     int32_t* __restrict__ rows, float* __restrict__ logits, HeadCtrl* __restrict__ ctrl,
-    qh_head_stats* __restrict__ stats) {
+    qh_head_stats* __restrict__ stats, TokenFeedback fb) {
     extern __shared__ float wprod[];  // [waves][nb]
     constexpr int kWaves = kCandThreads / 64;
     __shared__ int candl[kCandRowsPerThread * kCandThreads];
@@ -683,6 +683,7 @@ __global__ __launch_bounds__(kCandThreads) void head_cand_kernel(
             stats->n_rows = ctrl->n_seeds + ctrl->n_must + n_cand;
             stats->seed_tie = ctrl->seed_tie;
             stats->tau = ctrl->tau;
+            if (fb.token) fb.apply(key_row(key), true);
         }
     }
 }
@@ -693,7 +694,7 @@ bool head_shape_supported(int D) { return D % 64 == 0 && D <= kMaxHeadCols; }
 
 hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4, const qh_tensor& err,
                                  const int8_t* xq, const float* xd, const qh_head_query& q, const HeadMust& must,
-                                 const qh_head_out& out, void* ws, hipStream_t s) {
+                                 const qh_head_out& out, void* ws, hipStream_t s, const TokenFeedback* advance) {
     const int V = head8.rows, D = head8.cols, nb = D / QK;
     if (must.n > kMaxMust || !head_shape_supported(D)) return hipErrorInvalidValue;
     const int nv = (q.n_valid > 0 && q.n_valid < V) ? q.n_valid : V;
@@ -730,7 +731,8 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     const size_t lds3 = (size_t)(kCandThreads / 64) * nb * 4;
-    hipLaunchKernelGGL(head_cand_kernel, dim3((unsigned)cand_grid(nv)), dim3(kCandThreads), lds3, s, w8, s8, xq, xd, nb, nv, out.upper, mark, out.rows, out.logits, ctrl, out.stats);
+    hipLaunchKernelGGL(head_cand_kernel, dim3((unsigned)cand_grid(nv)), dim3(kCandThreads), lds3, s, w8, s8, xq, xd, nb, nv, out.upper, mark, out.rows, out.logits, ctrl, out.stats,
+                       advance ? *advance : TokenFeedback{});
     return hipGetLastError();
 }
 

@@ -68,10 +68,38 @@ __device__ __forceinline__ void must_span(const HeadMust& m, const int32_t*& ids
     }
 }
 #endif
-// q.must / q.n_must are ignored: the must ids come from `must`.
+// The decoder's feedback of a chosen token (session.cpp:45-46): it becomes the next input, is appended to the output
+// list and to the token history, and, after a decode step (advance), the position moves on.
+struct TokenFeedback {
+    int32_t* token = nullptr;
+    int* pos = nullptr;
+    int* n_out = nullptr;
+    int32_t* out = nullptr;
+    int out_cap = 0;
+    int32_t* hist = nullptr;
+    int* hist_len = nullptr;
+    int hist_cap = 0;
+#if defined(__HIPCC__)
+    __device__ __forceinline__ void apply(int id, bool advance) const {
+        const int k = *n_out, h = *hist_len;
+        const int p = advance ? *pos : 0;
+        *token = id;
+        if (k < out_cap) out[k] = id;
+        *n_out = k + 1;
+        if (h < hist_cap) {
+            hist[h] = id;
+            *hist_len = h + 1;
+        }
+        if (advance) *pos = p + 1;
+    }
+#endif
+};
+// q.must / q.n_must are ignored: the must ids come from `must`. With `advance` set (greedy decoding), the last
+// candidate workgroup also feeds the top-1 token back (TokenFeedback::apply with advance), which saves a launch.
 hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4, const qh_tensor& err,
                                  const int8_t* xq, const float* xd, const qh_head_query& q, const HeadMust& must,
-                                 const qh_head_out& out, void* ws, hipStream_t s);
+                                 const qh_head_out& out, void* ws, hipStream_t s,
+                                 const TokenFeedback* advance = nullptr);
 
 // Sampler::sample on the device (qh_sample.hip). Candidates: rows[0, hs->n_rows) (the shortlist head's list; every
 // other id counts as -inf) or, with rows null, every id below n_valid; the penalty looks at the ids `hist` names.
