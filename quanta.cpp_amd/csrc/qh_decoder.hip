@@ -823,8 +823,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
         return sc;
     };
-    // the chunk's own rows j >= pos0 (keys in LDS), before the V DMA below: after it, the first LDS access waits for
-    // the DMA to land (the compiler cannot tell its LDS destination from the other arrays)
+    // the chunk's own rows j >= pos0 (keys in LDS)
     for (int j = pos0 + tid; j < nrows; j += 256) {
         v4u kk[CPR];
         const uint16_t* kl = kloc + (j - pos0) * HD;
@@ -834,23 +833,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         att[j] = a;
         mx = a > mx ? a : mx;
     }
-    // The first stage's V blocks go straight into LDS (DMA, no registers; waited for before the stage is read) now,
-    // while the cached K rows are still in flight: the memory pipeline takes them behind the K rows, and the scores
-    // below use registers only. A fixed number per wave, the whole stage (clamped onto the last block, whose repeats
-    // write the same data), so the compiler's waits for the K rows count them exactly. Cache blocks stop below
-    // pos0: none is written by this launch (the block holding pos0 carries stale rows from pos0 on, replaced when
-    // the stage is built).
+    // The first stage's V blocks go straight into LDS (DMA, no registers), in two halves of the whole stage per wave
+    // (clamped onto the last block, whose repeats write the same data): the first once the scores are done and the
+    // second after the exp row (the issue of a half stalls its wave while the memory pipeline drains, so neither
+    // holds up the scores, and the second is issued after the wait that completes the first and the exp row's
+    // stores). Everything is waited for before the stage is built. Cache blocks stop below pos0: none is written by
+    // this launch (the block holding pos0 carries stale rows from pos0 on, replaced when the stage is built).
     const int ncb = min((pos0 + 7) / 8, kVBlk);  // cache blocks of the first stage (the last may be partial)
     constexpr int kDmaPerBlk = HD / 64;          // 1 KB (one wave instruction) per DMA chunk
     constexpr int kVEarly = kVBlk * kDmaPerBlk / 4;  // DMA chunks per wave
-    {
+    auto dma_v = [&](int e0, int e1) {           // chunks wave + 4 e, e in [e0, e1)
         const int last = max(ncb * kDmaPerBlk - 1, 0);
 #pragma unroll
-        for (int e = 0; e < kVEarly; ++e) {
+        for (int e = e0; e < e1; ++e) {
             const int c = min(wave + 4 * e, last);
             lds_dma16_async(vc4 + vchunk(c / kDmaPerBlk, (c % kDmaPerBlk) * 64 + lane), vst + c * 64);
         }
-    }
+    };
 
     // the cached rows tid + 256 r (registers only), their chains interleaved; stored after the barrier below
     float sc[kKPre];
@@ -875,6 +874,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // the maximum does not depend on the order of comparison
     mx = wave_max_sel(mx);
     if (lane == 0) red[wave] = mx;
+    dma_v(0, kVEarly / 2);
 #pragma unroll
     for (int r = 0; r < kKPre; ++r) {
         const int j = tid + 256 * r;
@@ -903,18 +903,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     __shared__ SegShared ssh;
     if (seg) seg_partials(ssh, p1, p2, p3);
-    // first V stage: the cache blocks arrive by DMA (the block holding pos0 carries stale rows from pos0 on,
-    // replaced below), then the chunk's rows that fall inside the stage are written over them. The wait also
-    // completes the exp row's stores before the barrier.
-    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_waitcnt(0);  // the exp row's stores (read through scalar loads after the barrier)
+    dma_v(kVEarly / 2, kVEarly);
     __syncthreads();
-    uint16_t* vst16 = reinterpret_cast<uint16_t*>(vst);
-    const int s1 = min(nrows, kVRows);
-    for (int e = tid; e < (s1 - pos0) * HD; e += 256) {  // empty when pos0 >= kVRows
-        const int r = pos0 + e / HD, d = e % HD;
-        vst16[((r >> 3) * HD + d) * 8 + (r & 7)] = vloc[(r - pos0) * HD + d];
-    }
-    // softmax sum in position order (ops_ref.cpp:220-224); the segmented run's barrier also publishes the V rows
+    // softmax sum in position order (ops_ref.cpp:220-224)
     auto add = [](float acc, float a) { return acc + a; };
     float sum;
     if (seg) {
@@ -931,8 +923,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         att[j] = a;
         arow[j] = a;
     }
-    __builtin_amdgcn_s_waitcnt(0);  // the weight row's stores are complete before the barrier
+    // the weight row's stores and the V DMA are complete before the barrier; then the chunk's rows that fall inside
+    // the first stage are written over the DMA's blocks
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    uint16_t* vst16 = reinterpret_cast<uint16_t*>(vst);
+    {
+        const int s1 = min(nrows, kVRows);
+        for (int e = tid; e < (s1 - pos0) * HD; e += 256) {  // empty when pos0 >= kVRows
+            const int r = pos0 + e / HD, d = e % HD;
+            vst16[((r >> 3) * HD + d) * 8 + (r & 7)] = vloc[(r - pos0) * HD + d];
+        }
+        __syncthreads();
+    }
 
     // out_i = sum_j a_j * v_ji, one FMA per position in order (model.cpp:131-135): thread i per dimension, over
     // the rows of each LDS stage. The weights come as scalar operands (scalar loads of arow, 32 per batch, the next
