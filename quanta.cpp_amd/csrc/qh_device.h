@@ -234,8 +234,9 @@ __device__ __forceinline__ float chain_lds_pipe(const float* p, const float* dx,
         acc = __builtin_fmaf(q.p1.z, q.x1.z, acc);
         acc = __builtin_fmaf(q.p1.w, q.x1.w, acc);
     };
-    // The first batches pass through an empty asm: the loop's reload of a batch is then not merged with its first
-    // load into one load at the top of the loop, which would leave nothing in flight across iterations.
+    // The first batch passes through an empty asm: the loop's reload of a batch is then not merged with its first
+    // load into one load at the top of the loop, which would leave nothing in flight across iterations. Only the
+    // first: the asm waits for its operands, and the other batches' reads stay in flight into the loop.
     auto pin = [](Batch& q) {
         asm volatile("" : "+v"(q.p0.x), "+v"(q.p0.y), "+v"(q.p0.z), "+v"(q.p0.w), "+v"(q.p1.x), "+v"(q.p1.y),
                      "+v"(q.p1.z), "+v"(q.p1.w));
@@ -245,8 +246,7 @@ __device__ __forceinline__ float chain_lds_pipe(const float* p, const float* dx,
     Batch q[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) ld(q[i], 8 * i);
-#pragma unroll
-    for (int i = 0; i < NB; ++i) pin(q[i]);
+    pin(q[0]);
     for (int b = 0; b < L; b += 8 * NB) {  // the scheduling barriers keep each batch's reads ahead of the next FMAs
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
