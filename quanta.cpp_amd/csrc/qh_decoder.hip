@@ -54,6 +54,15 @@ enum { kStatusCtx = 1, kStatusToken = 2 };
 
 // glibc-identical expf on the device (all 2^32 inputs checked against the host's expf in tests).
 __device__ __forceinline__ float dev_expf(float x) { return expf_variant<2>(x); }
+// The same with its table in LDS (ExpTab): a table read from global memory costs a cache round trip per call.
+struct ExpTab {
+    uint64_t v;  // thread t < 32: entry t, loaded first thing
+    __device__ __forceinline__ void load() { v = expf_detail::kTab[min((int)threadIdx.x, 31)]; }
+    __device__ __forceinline__ void store(uint64_t* lds) const {
+        if (threadIdx.x < 32) lds[threadIdx.x] = v;
+    }
+};
+__device__ __forceinline__ float dev_expf(float x, const uint64_t* lds_tab) { return expf_variant<2>(x, lds_tab); }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return f16_to_f32(h); }
 
@@ -715,6 +724,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     __shared__ __align__(16) float qs[HD];
     __shared__ float red[4];
     __shared__ float sum_sh;
+    __shared__ uint64_t exptab[32];
+    ExpTab et;
+    et.load();
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos0 = *pos_dev, pos = pos0 + t, nrows = pos + 1;
     if (pos >= ctx || pos0 < 0) {  // uniform: a step past the context touches no cache row
@@ -797,6 +809,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         if (bv) val = val + (e == tid ? vb0 : bv[kvh * HD + i]);
         vloc[r * HD + i] = f2h(val);
     }
+    et.store(exptab);
     __syncthreads();
     if (h % group == 0)
         for (int i = tid; i < HD; i += 256) {
@@ -894,7 +907,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const Segs4 sg{(nrows - 3 * Ls) & ~15, Ls, nrows};
     double p1 = 0.0, p2 = 0.0, p3 = 0.0;
     for (int j = tid; j < nrows; j += 256) {
-        const float e = dev_expf(att[j] - mx);
+        const float e = dev_expf(att[j] - mx, exptab);
         att[j] = e;
         erow[j] = e;
         p1 += j < sg.start(1) ? (double)e : 0.0;
@@ -1109,6 +1122,9 @@ __global__ __launch_bounds__(256) void gemv_swiglu_norm_kernel(const uint8_t* __
                                                                float* __restrict__ od) {
     extern __shared__ __align__(16) float smem[];
     __shared__ float gu[2 * QK];
+    __shared__ uint64_t exptab[32];
+    ExpTab et;
+    et.load();
     const int tid = (int)threadIdx.x, ra = (int)blockIdx.x * QK;
     act.tmp = smem + gemv_tile_lds_bytes(nb * QK, 2 * QK, true) / 4;
     constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
@@ -1117,10 +1133,11 @@ __global__ __launch_bounds__(256) void gemv_swiglu_norm_kernel(const uint8_t* __
     const float val =
         gemv_tile<DT, U, true, 2>(segs, nullptr, nullptr, nb, QK, 2 * QK, nb_magic, smem, NormActR<R, false>{act});
     if (tid < 2 * QK) gu[tid] = val;
+    et.store(exptab);
     __syncthreads();
     if (tid < QK) {
         const float g = gu[tid], u = gu[QK + tid];
-        quant_block32(g / (1.0f + dev_expf(-g)) * u, oq + ra, od + blockIdx.x);
+        quant_block32(g / (1.0f + dev_expf(-g, exptab)) * u, oq + ra, od + blockIdx.x);
     }
 }
 

@@ -59,8 +59,9 @@ QH_HD inline double from_bits_f64(uint64_t u) {
 
 // FUSED: 0 = no multiply-add fused, 1 = the polynomial's three multiply-adds fused, 2 = also x * 32/ln2 fused
 // into the rounding shift and the reduction.
+// tab: the 32-entry table (kTab, or a copy of it, e.g. in LDS).
 template <int FUSED>
-QH_HD inline float expf_variant(float x) {
+QH_HD inline float expf_variant(float x, const uint64_t* tab = expf_detail::kTab) {
     using namespace expf_detail;
     const uint32_t abstop = (bits_f32(x) >> 20) & 0x7ffu;
     if (abstop >= (bits_f32(88.0f) >> 20)) {
@@ -83,7 +84,7 @@ QH_HD inline float expf_variant(float x) {
     } else {
         r = kInvLn2N * xd - kd;
     }
-    uint64_t t = kTab[ki % 32];
+    uint64_t t = tab[ki % 32];
     t += ki << 47;
     const double s = from_bits_f64(t);
     double z, y;
