@@ -26,8 +26,6 @@ constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kPool = 4096;
 
-__device__ __forceinline__ float sample_expf(float x) { return expf_variant<2>(x); }
-
 // xorshift64* (sampler.cpp:16-21) and the 24-bit uniform of sampler.h.
 __device__ __forceinline__ uint64_t xorshift64s(uint64_t& s) {
     s ^= s >> 12;
@@ -63,7 +61,9 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const float* __restric
     __shared__ int cid[QH_SAMPLE_MAX_TOPK];
     __shared__ int pool_n;
     __shared__ float sum_sh;
+    __shared__ uint64_t exptab[32];  // expf's table in LDS: the softmax below reads it without a cache round trip
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t tabv = expf_detail::kTab[min(tid, 31)];
     const bool pen = p.repeat_penalty != 1.0f;
     if (pen) {
         for (int i = tid; i < (n_valid + 31) / 32; i += kThreads) seen[i] = 0u;
@@ -98,6 +98,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const float* __restric
     }
 
     const int k = (p.top_k > 0 && p.top_k < n_valid) ? p.top_k : n_valid;  // <= QH_SAMPLE_MAX_TOPK (host check)
+    if (tid < 32) exptab[tid] = tabv;  // read after the barriers below
     {  // lower bound on the k-th largest key: the k-th largest of the wave's 64 candidates (when k <= 64)
         const int i = wave * 64 + lane;
         const uint64_t a = i < n ? key_of(i) : 0ull;
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const float* __restric
     // softmax with temperature over the survivors (sampler.cpp:52-59)
     const float mx = key_score(pool[0]);
     for (int i = tid; i < kk; i += kThreads) {
-        cval[i] = sample_expf((key_score(pool[i]) - mx) / p.temperature);
+        cval[i] = expf_variant<2>((key_score(pool[i]) - mx) / p.temperature, exptab);
         cid[i] = key_row(pool[i]);
     }
     __syncthreads();
