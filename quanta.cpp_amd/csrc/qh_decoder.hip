@@ -572,20 +572,33 @@ struct NormAct {
             ss = lds_sum_squares(tmp, D);
         }
         const float scale = rms_scale(ss, D, eps);
-#pragma unroll
-        for (int k = 0; k < R; ++k) {
-            const int i4 = tid + 256 * k;
-            if (i4 < n4) {
-                float4 y = xr.v[k];
-                y.x = y.x * scale * wr.v[k].x;
-                y.y = y.y * scale * wr.v[k].y;
-                y.z = y.z * scale * wr.v[k].z;
-                y.w = y.w * scale * wr.v[k].w;
-                t4[i4] = y;
+        if constexpr (R == 1) {
+            // thread t holds float4 t, so the 8-lane groups of quant_block_x8 are the row's 32-blocks: each thread
+            // quantizes its own values, with no LDS round trip and no barrier (n4 % 8 == 0: whole groups)
+            if (tid < n4) {
+                float4 y = xr.v[0];
+                y.x = y.x * scale * wr.v[0].x;
+                y.y = y.y * scale * wr.v[0].y;
+                y.z = y.z * scale * wr.v[0].z;
+                y.w = y.w * scale * wr.v[0].w;
+                quant_block_x8(y, xs + (tid >> 3) * QK, xds + (tid >> 3));
             }
+        } else {
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                const int i4 = tid + 256 * k;
+                if (i4 < n4) {
+                    float4 y = xr.v[k];
+                    y.x = y.x * scale * wr.v[k].x;
+                    y.y = y.y * scale * wr.v[k].y;
+                    y.z = y.z * scale * wr.v[k].z;
+                    y.w = y.w * scale * wr.v[k].w;
+                    t4[i4] = y;
+                }
+            }
+            __syncthreads();
+            quant_row_x8(tmp, D, xs, xds);
         }
-        __syncthreads();
-        quant_row_x8(tmp, D, xs, xds);
     }
 
     // The row to normalise into xr: the embedding of *tok (EMB) or x.
