@@ -1134,7 +1134,6 @@ __global__ __launch_bounds__(256) void gemv_swiglu_norm_kernel(const uint8_t* __
                                                                uint32_t nb_magic, int8_t* __restrict__ oq,
                                                                float* __restrict__ od) {
     extern __shared__ __align__(16) float smem[];
-    __shared__ float gu[2 * QK];
     __shared__ uint64_t exptab[32];
     ExpTab et;
     et.load();
@@ -1145,12 +1144,14 @@ __global__ __launch_bounds__(256) void gemv_swiglu_norm_kernel(const uint8_t* __
                            {sg + (size_t)ra * nb, su + (size_t)ra * nb}};
     const float val =
         gemv_tile<DT, U, true, 2>(segs, nullptr, nullptr, nb, QK, 2 * QK, nb_magic, smem, NormActR<R, false>{act});
-    if (tid < 2 * QK) gu[tid] = val;
-    et.store(exptab);
-    __syncthreads();
-    if (tid < QK) {
-        const float g = gu[tid], u = gu[QK + tid];
-        quant_block32(g / (1.0f + dev_expf(-g, exptab)) * u, oq + ra, od + blockIdx.x);
+    // wave 0 holds the block's 32 gate rows in lanes 0-31 and its 32 up rows in lanes 32-63: one half swap hands
+    // lane l its up value (the exp table is stored by lanes 0-31 of the same wave, so no barrier is needed)
+    if (tid < 2 * QK) {  // wave 0
+        et.store(exptab);
+        const uint32_t vb = __builtin_bit_cast(uint32_t, val);
+        const auto sw = __builtin_amdgcn_permlane32_swap(vb, vb, false, false);
+        const float u = __builtin_bit_cast(float, (uint32_t)sw[1]);
+        if (tid < QK) quant_block32(val / (1.0f + dev_expf(-val, exptab)) * u, oq + ra, od + blockIdx.x);
     }
 }
 
