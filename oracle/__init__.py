@@ -267,6 +267,13 @@ class _Ref:
                                   params.repeat_window, C.byref(st))
         return tid, lg, int(st.value)
 
+    def load_error(self, path: str):
+        """The reference Model::load's verdict on a file: None if it loads, else its error message."""
+        L = self.lib
+        L.ref_model_load_error.argtypes, L.ref_model_load_error.restype = [C.c_char_p, C.c_char_p, _int], _int
+        buf = C.create_string_buffer(512)
+        return None if L.ref_model_load_error(path.encode(), buf, 512) else buf.value.decode()
+
     def load_model(self, path: str, ctx_len: int, threads: int):
         m = self.lib.ref_model_load(path.encode(), ctx_len, threads)
         if not m:

@@ -154,6 +154,20 @@ void* ref_model_load(const char* path, int ctx_len, int n_threads) {
 
 void ref_model_free(void* m) { delete static_cast<quanta::Model*>(m); }
 
+// Model::load's verdict on a file (model.cpp:10-106, model_file.cpp:104-218): 1 if it loads, else 0 with the
+// reference's error message copied into msg[cap].
+int ref_model_load_error(const char* path, char* msg, int cap) {
+    quanta::Model m;
+    std::string err;
+    const bool ok = m.load(path, 16, &err, 1, true);
+    if (cap > 0) {
+        const size_t n = std::min(err.size(), size_t(cap - 1));
+        std::memcpy(msg, err.data(), n);
+        msg[n] = '\0';
+    }
+    return ok ? 1 : 0;
+}
+
 // Copies the state a forward leaves behind: logits [V] (exact where the head computed them, -inf elsewhere with the
 // shortlist), the final normed hidden state [dim] and its quantization; returns last_head_rows().
 static int ref_dump(quanta::Model* m, float* logits, float* hidden, int8_t* hq, float* hd) {

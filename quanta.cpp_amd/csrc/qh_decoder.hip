@@ -78,13 +78,14 @@ __device__ __forceinline__ v4u ld4(const void* p) { return *reinterpret_cast<con
 // and before any LDS access. This way the earlier loads keep their waits, LDS accesses wait for nothing, the caller
 // waits for the transfer itself (s_waitcnt vmcnt(0)) before reading its LDS, and the compiler's waits for loads
 // issued before it become conservative (they also cover the transfers), never short. M0, which the transfer takes
-// its LDS address from, is set right before it (the compiler keeps no value in M0 across code here). The body
+// its LDS address from, is an input operand of the asm ("{m0}" constraint): the compiler writes it and knows what M0
+// holds afterwards. The s_nop covers the wait state between an M0 write and the transfer that reads it. The body
 // exists only in the device pass (the host pass cannot form an LDS address).
 __device__ __forceinline__ void lds_dma16_async(const void* g, void* lds_wave) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_wave);
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(g) : "memory");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0) : "memory");
 #endif
 }
 // f32 -> f16 (round to nearest even) of an already rounded f32 value, as the reference stores its f32 K / V results

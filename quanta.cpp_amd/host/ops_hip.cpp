@@ -1,5 +1,11 @@
 // Host-pointer implementation of quanta_ops.h over the C-ABI (quanta_hip.h). Host C++ only: it needs no
 // HIP headers and can be built with any C++17 compiler.
+//
+// Built with QUANTA_HIP_ENGINE inside the reference engine, it takes the place of engine/src/ops_dispatch.cpp
+// (matvec_q, matmul_q, matvec_q_kernel_name, available_*, ops.h:57-71): quantize_q8 then stays the engine's own
+// (ops_ref.cpp:69-83, bit-identical to the GPU's), and the kernel lists name the engine's scalar "ref" kernels first,
+// as ops_dispatch.cpp does, so kernel_selftest (checks.cpp:64-146) times both families and checks "hip" against
+// "ref".
 #include "quanta_ops.h"
 
 #include <memory>
@@ -91,6 +97,7 @@ void hip_matmul(float* out, int ldo, const Tensor& W, const QuantVec* x, int n, 
 
 }  // namespace
 
+#if !defined(QUANTA_HIP_ENGINE)
 void quantize_q8(const float* x, int n, QuantVec& out) {
     Staging& s = staging();
     const int nb = n / QK;
@@ -107,6 +114,7 @@ void quantize_q8(const float* x, int n, QuantVec& out) {
     check(qh_memcpy_d2h(out.q.data(), dev + oq, size_t(n), s.stream), "qh_memcpy_d2h");
     check(qh_memcpy_d2h(out.d.data(), dev + od, sizeof(float) * nb, s.stream), "qh_memcpy_d2h");
 }
+#endif
 
 void matvec_q(float* out, const Tensor& W, const QuantVec& x, int r0, int r1) {
     if (r0 >= r1) return;
@@ -151,9 +159,19 @@ void matmul_q(float* out, int ldo, const Tensor& W, const QuantVec* x, int n, in
 
 const char* matvec_q_kernel_name() { return "hip"; }
 
+#if defined(QUANTA_HIP_ENGINE)
+std::vector<std::pair<const char*, MatvecQFn>> available_matvec_q_kernels() {
+    return {{"ref", matvec_q_ref}, {"hip", hip_matvec}};
+}
+
+std::vector<std::pair<const char*, MatmulQFn>> available_matmul_q_kernels() {
+    return {{"ref", matmul_q_ref}, {"hip", hip_matmul}};
+}
+#else
 std::vector<std::pair<const char*, MatvecQFn>> available_matvec_q_kernels() { return {{"hip", hip_matvec}}; }
 
 std::vector<std::pair<const char*, MatmulQFn>> available_matmul_q_kernels() { return {{"hip", hip_matmul}}; }
+#endif
 
 int shortlist_head(const Tensor& head8, const Tensor& head4, const Tensor& err, const QuantVec& xq,
                    const HeadQuery& hq, float* logits, int* top1, float* coarse, float* upper) {

@@ -8,6 +8,17 @@
 //   matvec_q_kernel_name / available_matvec_q_kernels / available_matmul_q_kernels   ops.h:62-71
 //   shortlist_head   reference Model::shortlist_head (model.cpp:240-334) as a free function
 //
+// Two ways to build against it:
+//
+//  - Standalone (the default): this header defines Tensor, QuantVec, DType, QK and HeadQuery itself, with the
+//    reference's field layouts, and libquanta_ops.so provides every function above.
+//  - Inside the reference engine (QUANTA_HIP_ENGINE defined, the engine's engine/src on the include path): the
+//    types come from the engine's own model_file.h / ops.h / model.h, and this header only adds what the engine
+//    lacks (HipError, shortlist_head, release_device_tensors). ops_hip.cpp built the same way replaces the engine's
+//    ops_dispatch.cpp (matvec_q, matmul_q, matvec_q_kernel_name, available_*); quantize_q8 and the scalar
+//    matvec_q_ref / matmul_q_ref stay the engine's own (ops_ref.cpp), so kernel_selftest checks the GPU kernels
+//    against them.
+//
 // Pointers are HOST pointers, as in the reference. Each quantized Tensor is uploaded to the GPU the
 // first time it is used (keyed by Tensor::data, so the tensor bytes must not change afterwards) and
 // stays resident; activations are staged per calling thread. Calls are thread-safe and may overlap on
@@ -24,6 +35,12 @@
 #include <stdexcept>
 #include <utility>
 #include <vector>
+
+#if defined(QUANTA_HIP_ENGINE)
+
+#include "model.h"  // the engine's Tensor, DType, QK (model_file.h), QuantVec and kernels (ops.h), HeadQuery
+
+#else
 
 namespace quanta {
 
@@ -66,10 +83,6 @@ struct HeadQuery {
     int n_must = 0;
 };
 
-struct HipError : std::runtime_error {
-    using std::runtime_error::runtime_error;
-};
-
 inline bool is_quantized(DType t) { return t == DType::Q8_0 || t == DType::Q4_0; }
 
 void quantize_q8(const float* x, int n, QuantVec& out);
@@ -82,6 +95,16 @@ std::vector<std::pair<const char*, MatvecQFn>> available_matvec_q_kernels();
 using MatmulQFn = void (*)(float* out, int ldo, const Tensor& W, const QuantVec* x, int n, int r0, int r1);
 void matmul_q(float* out, int ldo, const Tensor& W, const QuantVec* x, int n, int r0, int r1);
 std::vector<std::pair<const char*, MatmulQFn>> available_matmul_q_kernels();
+
+}  // namespace quanta
+
+#endif  // QUANTA_HIP_ENGINE
+
+namespace quanta {
+
+struct HipError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
 
 // Exact Shortlist Head for the hidden state already quantized in xq: fills logits[V] (exact for the
 // rescored rows, -inf elsewhere) and, if given, coarse[V] / upper[V]; returns the number of 8-bit rows

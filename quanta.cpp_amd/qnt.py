@@ -103,48 +103,149 @@ def write_qnt(path: str, hp: HParams, tensors: dict[str, TensorRec], n_tokens: i
             f.write(np.ascontiguousarray(tensors[n].data).tobytes())
 
 
-def read_qnt(path: str):
-    """(HParams, n_tokens, {name: TensorRec}) with tensor data as read-only views into a memory map."""
-    mm = np.memmap(path, dtype=np.uint8, mode="r")
-    buf = memoryview(mm)
-    p = 0
+class QntError(ValueError):
+    """A .qnt file the reference's loader would refuse; the message is the reference's (model_file.cpp:104-218,
+    model.cpp:10-58)."""
 
-    def take(n):
-        nonlocal p
-        if p + n > len(buf):
-            raise ValueError("model file truncated")
-        b = buf[p:p + n]
-        p += n
+
+class _Cursor:
+    """Bounds-checked little-endian reader (model_file.cpp:43-84): reading past the end raises
+    'model file truncated'."""
+
+    def __init__(self, buf, p=0, end=None):
+        self.buf, self.p, self.end = buf, p, len(buf) if end is None else end
+
+    def need(self, n):
+        if self.end - self.p < n:
+            raise QntError("model file truncated")
+
+    def take(self, n):
+        self.need(n)
+        b = self.buf[self.p:self.p + n]
+        self.p += n
         return b
 
-    if bytes(take(4)) != MAGIC:
-        raise ValueError("bad magic (not a .qnt file)")
-    version = struct.unpack("<I", take(4))[0]
-    if version not in (1, 2):
-        raise ValueError(f"unsupported version {version}")
-    v = struct.unpack("<8I2f2I", take(48))
-    flags = struct.unpack("<I", take(4))[0] if version >= 2 else 0
-    hp = HParams(*v[:8], float(v[8]), float(v[9]), bool(v[10]), bool(v[11]), flags)
-    tok_len = struct.unpack("<I", take(4))[0]
-    tok = take(tok_len)
-    n_tokens = struct.unpack("<I", tok[:4])[0]
-    n_tensors = struct.unpack("<I", take(4))[0]
+    def u32(self):
+        return struct.unpack("<I", self.take(4))[0]
+
+    def u64(self):
+        return struct.unpack("<Q", self.take(8))[0]
+
+    def f32(self):
+        return struct.unpack("<f", self.take(4))[0]
+
+    def str(self):
+        return bytes(self.take(self.u32()))
+
+    def ranges(self):
+        return [(self.u32(), self.u32()) for _ in range(self.u32())]
+
+
+def read_qnt(path: str):
+    """(HParams, n_tokens, {name: TensorRec}) with tensor data as read-only views into a memory map. Raises QntError
+    with the reference reader's message for a file it would refuse (ModelFile::open, model_file.cpp:104-218): bad
+    magic or version, a truncated header, tokenizer section or tensor table, a tensor with ndim outside {1, 2}, an
+    offset past the end or a tensor running past it. Stricter than the reference in one point: a dtype outside
+    F32 / F16 / Q8_0 / Q4_0 is refused here (the reference would size it as 0 bytes)."""
+    mm = np.memmap(path, dtype=np.uint8, mode="r")
+    buf = memoryview(mm)
+    c = _Cursor(buf)
+    c.need(4)
+    if bytes(c.take(4)) != MAGIC:
+        raise QntError("bad magic (not a .qnt file)")
+    version = c.u32()
+    if version < 1 or version > 2:
+        raise QntError(f"unsupported version {version}")
+    v = [c.u32() for _ in range(8)]
+    rope_theta, norm_eps = c.f32(), c.f32()
+    tied, bias = c.u32() != 0, c.u32() != 0
+    flags = c.u32() if version >= 2 else 0
+    hp = HParams(*v, float(rope_theta), float(norm_eps), tied, bias, flags)
+    tok_len = c.u32()
+    c.need(tok_len)
+    t = _Cursor(buf, c.p, c.p + tok_len)  # the tokenizer section, parsed with its own cursor (model_file.cpp:152-170)
+    c.p += tok_len
+    n_tokens = t.u32()
+    for _ in range(n_tokens):
+        t.str()
+    for _ in range(t.u32()):
+        t.u32(), t.u32(), t.u32()
+    for _ in range(t.u32()):
+        t.u32(), t.str()
+    for _ in range(3):
+        t.ranges()
+    n_tensors = c.u32()
     tensors = {}
     for _ in range(n_tensors):
-        nl = struct.unpack("<I", take(4))[0]
-        name = bytes(take(nl)).decode()
-        dtype, ndim = struct.unpack("<II", take(8))
+        name = c.str().decode(errors="replace")
+        dtype, ndim = c.u32(), c.u32()
         if ndim == 1:
-            rows, cols = 1, struct.unpack("<I", take(4))[0]
+            rows, cols = 1, c.u32()
         elif ndim == 2:
-            rows, cols = struct.unpack("<II", take(8))
+            rows, cols = c.u32(), c.u32()
         else:
-            raise ValueError(f"unsupported ndim for {name}")
-        off = struct.unpack("<Q", take(8))[0]
+            raise QntError(f"unsupported ndim for {name}")
+        off = c.u64()
+        if off > len(mm):
+            raise QntError(f"bad offset for {name}")
+        if dtype not in (F32, F16, Q8_0, Q4_0):
+            raise QntError(f"unsupported dtype {dtype} for {name}")
         size = synth.tensor_bytes(dtype, rows, cols)
         if off + size > len(mm):
-            raise ValueError(f"tensor out of bounds: {name}")
-        tensors[name] = TensorRec(dtype, rows, cols, mm[off:off + size], ndim)
+            raise QntError(f"tensor out of bounds: {name}")
+        if name not in tensors:  # a repeated name keeps its first entry, as the reference's map emplace does
+            tensors[name] = TensorRec(dtype, rows, cols, mm[off:off + size], ndim)
+    return hp, n_tokens, tensors
+
+
+FLAG_HADAMARD_DOWN = 1  # model_file.h:21
+
+LAYER_TENSORS = ("input_layernorm.weight", "self_attn.q_proj.weight", "self_attn.k_proj.weight",
+                 "self_attn.v_proj.weight", "self_attn.o_proj.weight", "self_attn.q_proj.bias", "self_attn.k_proj.bias",
+                 "self_attn.v_proj.bias", "post_attention_layernorm.weight", "mlp.gate_proj.weight",
+                 "mlp.up_proj.weight", "mlp.down_proj.weight")
+
+
+def check_model(hp: HParams, tensors: dict) -> None:
+    """Model::load's checks after the file is read (model.cpp:13-58), in its order and with its messages: every tensor
+    the forward reads is present (q/k/v biases only with qkv_bias; lm_head.weight only without tied embeddings), the
+    Hadamard flag's width rule, the head configuration, and the shortlist tensors' types and shapes. Two more refusals
+    mark what the GPU decoder does not run: an untied LM head and Hadamard-rotated down projections."""
+    def get(name):
+        if name not in tensors:
+            raise QntError(f"missing tensor: {name}")
+        return tensors[name]
+
+    get("model.embed_tokens.weight")
+    get("model.norm.weight")
+    lm_head = get("model.embed_tokens.weight") if hp.tied_embeddings else get("lm_head.weight")
+    for l in range(hp.n_layers):
+        for n in LAYER_TENSORS:
+            if n.endswith(".bias") and not hp.qkv_bias:
+                continue
+            get(f"model.layers.{l}.{n}")
+    if (hp.flags & FLAG_HADAMARD_DOWN) and hp.ffn_dim % 256 != 0:
+        raise QntError("hadamard flag needs ffn_dim % 256 == 0")
+    if hp.n_kv_heads <= 0 or hp.n_heads * hp.head_dim != hp.dim or hp.n_heads % hp.n_kv_heads != 0:
+        raise QntError("unsupported head configuration")
+    h4, he = tensors.get("quanta.head_q4"), tensors.get("quanta.head_err")
+    if h4 is not None or he is not None:
+        ok = (h4 is not None and he is not None and h4.dtype == Q4_0 and he.dtype == F16 and lm_head.dtype == Q8_0 and
+              h4.rows == lm_head.rows and h4.cols == lm_head.cols and he.rows == lm_head.rows and
+              he.cols == lm_head.cols // 32)
+        if not ok:
+            raise QntError("bad shortlist head tensors")
+    if not hp.tied_embeddings:
+        raise QntError("untied lm_head.weight: the GPU decoder runs tied embeddings only")
+    if hp.flags & FLAG_HADAMARD_DOWN:
+        raise QntError("Hadamard-rotated down projections: not supported by the GPU decoder")
+
+
+def load_model(path: str):
+    """read_qnt + check_model: (HParams, n_tokens, tensors) of a file the GPU decoder can run, as Model::load
+    accepts it; QntError with the reference's message otherwise."""
+    hp, n_tokens, tensors = read_qnt(path)
+    check_model(hp, tensors)
     return hp, n_tokens, tensors
 
 

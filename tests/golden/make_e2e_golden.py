@@ -9,9 +9,11 @@ build, so it runs only where the reference tree is mounted; the .npz files are d
 
   e2e_q4mix.npz   the benchmark model (24 layers, vocab 151936, Qwen2.5-0.5B shapes), seed 5: a 512-id prompt
                   uniform over the vocabulary (seed 9), the 256 generated ids, per step the 8-bit head rows the
-                  forward read and the exact logit of the chosen id, and digests of a few tensors so a GPU host can
-                  show it rebuilt the same file. (A random-init model with a tied embedding soon repeats one token;
-                  the per-step head rows and logit bits still depend on every operation of every forward.)
+                  forward read and the exact logit of the chosen id, after the prefill and every step a digest of the
+                  final normed hidden state and of its int8 quantization (state_digests, [257][2] uint64), and
+                  digests of a few tensors so a GPU host can show it rebuilt the same file. (A random-init model with
+                  a tied embedding soon repeats one token; the per-step state digests, head rows and logit bits
+                  depend on every operation of every forward.)
   e2e_small.npz   a 2-layer, vocab-4096 model of the same widths (seed 7): 40-id prompt, 24 generated ids, and after
                   the prefill and every decode step the final normed hidden state and its int8 quantization.
   e2e_sampled.npz the benchmark model and prompt in sampling mode, through the reference's Session with the batched
@@ -20,7 +22,7 @@ build, so it runs only where the reference tree is mounted; the .npz files are d
                   and "gen" (`quanta gen --top-k 20 --repeat-penalty 1.1`: top-k 20 queries with the history as
                   must ids, greedy picks): 256 ids each and the 8-bit head rows of the forward before each pick.
 
-Usage: python tests/golden/make_e2e_golden.py [--small-only | --sampled-only]
+Usage: python tests/golden/make_e2e_golden.py [--small-only | --full-only | --sampled-only]
 """
 import ctypes as C
 import hashlib
@@ -101,6 +103,15 @@ def make_small(qnt, L):
     os.remove(path)
 
 
+def state_digest(hidden, hq, hd) -> np.ndarray:
+    """8 bytes (as uint64) of the sha256 of a forward's final normed hidden state, then of its int8 quantization and
+    block scales: a fingerprint of every operation of that forward."""
+    h1 = hashlib.sha256(np.ascontiguousarray(hidden, np.float32).tobytes()).digest()[:8]
+    h2 = hashlib.sha256(np.ascontiguousarray(hq, np.int8).tobytes() +
+                        np.ascontiguousarray(hd, np.float32).tobytes()).digest()[:8]
+    return np.frombuffer(h1 + h2, np.uint64)
+
+
 def make_full(qnt, L):
     hp = qnt.HParams()
     path = "/tmp/quanta_e2e_q4mix.qnt"
@@ -115,10 +126,31 @@ def make_full(qnt, L):
     n = L.ref_gen(m, ids.ctypes.data, len(ids), 256, out.ctypes.data, rows.ctypes.data, top.ctypes.data)
     assert n == 256
     L.ref_model_free(m)
+    # the same flow by hand (forward_batch, then forward of each greedy token), recording a digest of the final normed
+    # hidden state and of its quantization after the prefill and after every decode step: the random-init model soon
+    # repeats one token, so the stream alone says little about the forwards behind it
+    m = L.ref_model_load(path.encode(), 4096, 8)
+    D, V = hp.dim, hp.vocab_size
+    logits = np.zeros(V, np.float32)
+    hidden = np.zeros(D, np.float32)
+    hq = np.zeros(D, np.int8)
+    hd = np.zeros(D // 32, np.float32)
+    dig = np.zeros((257, 2), np.uint64)
+    L.ref_model_forward_batch(m, ids.ctypes.data, len(ids), 0, 1, logits.ctypes.data, hidden.ctypes.data,
+                              hq.ctypes.data, hd.ctypes.data)
+    dig[0] = state_digest(hidden, hq, hd)
+    pos = len(ids)
+    for s in range(256):
+        tok = int(np.argmax(logits))
+        assert tok == out[s], "hand-run gen flow differs from Session::generate"
+        L.ref_model_forward(m, tok, pos, 1, logits.ctypes.data, hidden.ctypes.data, hq.ctypes.data, hd.ctypes.data)
+        dig[s + 1] = state_digest(hidden, hq, hd)
+        pos += 1
+    L.ref_model_free(m)
     names = ["model.embed_tokens.weight", "quanta.head_q4", "quanta.head_err", "model.layers.23.mlp.down_proj.weight",
              "model.layers.0.self_attn.q_proj.bias"]
     np.savez_compressed(os.path.join(HERE, "e2e_q4mix.npz"), seed=np.int32(5), prompt=ids, out=out, head_rows=rows,
-                        top_logit=top,
+                        top_logit=top, state_digests=dig,
                         digest_names=np.array(names), digests=np.array([digest(tens[k].data) for k in names]))
     os.remove(path)
 
@@ -154,10 +186,11 @@ def main():
     qnt = load_pkg()
     L = bind(oracle.ref.lib)
     if "--sampled-only" not in sys.argv:
-        make_small(qnt, L)
+        if "--full-only" not in sys.argv:
+            make_small(qnt, L)
         if "--small-only" not in sys.argv:
             make_full(qnt, L)
-    if "--small-only" not in sys.argv:
+    if "--small-only" not in sys.argv and "--full-only" not in sys.argv:
         make_sampled(qnt)
     for f in sorted(os.listdir(HERE)):
         if f.startswith("e2e") and f.endswith(".npz"):

@@ -5,8 +5,11 @@
   (tests/golden/e2e_small.npz), bit for bit;
 * another seed, 3 layers, a prompt longer than one 32-token chunk, shortlist and full-head steps: hidden states and
   logits equal the oracle's decoder restatement, bit for bit;
-* the benchmark model (24 layers, vocab 151936): 512-token prompt, 256 greedy tokens equal the reference's `gen`
-  stream (tests/golden/e2e_q4mix.npz), with each step's head rows and the exact logit of the chosen token;
+* the benchmark model (24 layers, vocab 151936), written to a .qnt file and read back by qnt.load_model: 512-token
+  prompt, 256 greedy tokens equal the reference's `gen` stream (tests/golden/e2e_q4mix.npz), with each step's head
+  rows, the exact logit of the chosen token and a digest of the final normed hidden state and its quantization;
+* a chat's second turn: a prefill at pos0 > 0 (after a prefill, and after decode steps) equals the oracle's, cache and
+  history included;
 * one decode step captured in a HIP graph and replayed gives the same stream as eager steps;
 * head_dim 128, a context longer than one LDS stage of V rows, and the one-launch-per-operation path
   (QH_DECODER_FUSE=0) all equal the oracle bit for bit;
@@ -177,34 +180,59 @@ def test_decoder_equals_oracle_long_prompt_and_full_head(qh, oracle, gpu):
     assert dec.outputs(9)[1:].tolist() == [int(x) for x in dec.outputs(9)[1:]]
 
 
+def state_digest(hidden, hq, hd):
+    """The golden's per-forward fingerprint (tests/golden/make_e2e_golden.py): 8 bytes of the sha256 of the final normed
+    hidden state, then of its int8 quantization and block scales."""
+    import hashlib
+    h1 = hashlib.sha256(np.ascontiguousarray(hidden, np.float32).tobytes()).digest()[:8]
+    h2 = hashlib.sha256(np.ascontiguousarray(hq, np.int8).tobytes() +
+                        np.ascontiguousarray(hd, np.float32).tobytes()).digest()[:8]
+    return np.frombuffer(h1 + h2, np.uint64)
+
+
 @pytest.fixture(scope="module")
-def q4mix(qh, gpu):
+def q4mix(qh, gpu, tmp_path_factory):
+    """The benchmark model from a file on disk: written by qnt.write_qnt, read back by qnt.load_model (the .qnt reader
+    and Model::load's checks, model_file.cpp:104-218, model.cpp:10-58), uploaded by Decoder."""
     qnt = qnt_module()
     import hashlib
     g = _golden("e2e_q4mix.npz")
-    hp = qnt.HParams()
-    tens = qnt.synthetic_q4mix(int(g["seed"]), hp)
+    path = str(tmp_path_factory.mktemp("q4mix") / "q4mix.qnt")
+    qnt.write_qnt(path, qnt.HParams(), qnt.synthetic_q4mix(int(g["seed"]), qnt.HParams()))
+    hp, n_tokens, tens = qnt.load_model(path)
+    want = qnt.HParams()
+    assert n_tokens == hp.vocab_size and (hp.vocab_size, hp.dim, hp.n_layers, hp.max_seq) == (
+        want.vocab_size, want.dim, want.n_layers, want.max_seq)
+    assert np.float32(hp.norm_eps) == np.float32(want.norm_eps) and hp.rope_theta == want.rope_theta
     for name, want in zip(g["digest_names"], g["digests"]):
         got = hashlib.sha256(np.ascontiguousarray(tens[str(name)].data).view(np.uint8).tobytes()).hexdigest()
-        assert got == str(want), f"regenerated {name} differs from the one the golden stream was made with"
+        assert got == str(want), f"{name} read from the file differs from the one the golden stream was made with"
     dec = qh.Decoder(hp, tens, ctx_len=4096)
+    del tens
     return dec, g
 
 
 def test_decoder_q4mix_stream_equals_reference(qh, q4mix):
+    """256 greedy tokens after the 512-token prompt equal the reference's gen stream, with each forward's head rows,
+    chosen logit and final-state digest."""
     dec, g = q4mix
     n_gen = len(g["out"])
     dec.prefill(g["prompt"], 0, top_k=1)
     dec.begin(n_gen + 1)
-    rows, tops = [], []
+    rows, tops, digs = [], [], []
     for s in range(n_gen):
         st = dec.stats()
         rows.append(st["n_rows"])
         tops.append(st["top1_logit"])
+        digs.append(state_digest(dec.hidden(), *dec.hq()))
         dec.step(top_k=1)
+    digs.append(state_digest(dec.hidden(), *dec.hq()))
     out = dec.outputs(n_gen)
     first = int(np.nonzero(out != g["out"])[0][0]) if (out != g["out"]).any() else -1
     assert first < 0, f"token stream differs from step {first}: {out[first:first + 4]} vs {g['out'][first:first + 4]}"
+    digs = np.array(digs)
+    bad = np.nonzero((digs != g["state_digests"]).any(axis=1))[0]
+    assert bad.size == 0, f"final normed state differs after forward {bad[:4]} (0 = the prefill)"
     assert rows == g["head_rows"].tolist()
     assert (bits(np.array(tops, np.float32)) == bits(g["top_logit"])).all()
 
@@ -231,3 +259,55 @@ def test_decoder_graph_replay_equals_eager(qh, q4mix):
         graph.replay()
         torch.cuda.synchronize()  # eager work of the program between replays
     assert (dec.outputs(n + 1) == eager).all()
+
+
+@pytest.mark.parametrize("n_steps", [0, 3])
+def test_decoder_second_turn_prefill(qh, oracle, gpu, n_steps):
+    """A chat's second turn (check_batch's pos0 = 40, n = 45, engine/src/checks.cpp:148-176; session.cpp:13-31): a
+    prefill at pos0 > 0 over the cache of an earlier prefill, directly and after three decode steps (pos0 = 43 starts
+    inside an 8-position V block that holds decode rows). Logits, hidden state, head rows, every layer's K/V cache rows
+    and the token history equal the oracle's; the batched logits also equal one-token prefills at every position."""
+    qnt = qnt_module()
+    hp = qnt.HParams(vocab_size=3072, n_layers=3)
+    tens = qnt.synthetic_q4mix(23, hp)
+    ctx = 512
+    ids = np.random.default_rng(31).integers(0, hp.vocab_size, 85).astype(np.int32)
+    orc = oracle_decoder(oracle, hp, tens, ctx_len=ctx)
+    dec = qh.Decoder(hp, tens, ctx_len=ctx)
+    r = orc.forward_batch(ids[:40], 0, top_k=1)
+    dec.prefill(ids[:40], 0, top_k=1)
+    assert (bits(dec.logits()) == bits(r["logits"])).all()
+    hist = ids[:40].tolist()
+    pos = 40
+    if n_steps:
+        dec.begin(n_steps + 1, top_k=1)
+        hist.append(oracle.argmax(r["logits"]))
+        for _ in range(n_steps):
+            r = orc.forward(hist[-1], pos, top_k=1)
+            dec.step(top_k=1)
+            assert (bits(dec.hidden()) == bits(r["hidden"])).all()
+            hist.append(oracle.argmax(r["logits"]))
+            pos += 1
+        assert dec.outputs(n_steps + 1).tolist() == hist[40:]
+    assert dec.position() == pos
+    print(f"second turn: prefill 45 tokens at pos0 {pos}", flush=True)
+    r = orc.forward_batch(ids[40:85], pos, top_k=1)
+    dec.prefill(ids[40:85], pos, top_k=1)
+    assert (bits(dec.hidden()) == bits(r["hidden"])).all()
+    assert (bits(dec.logits()) == bits(r["logits"])).all()
+    assert dec.stats()["n_rows"] == r["rows"]
+    assert dec.position() == pos + 45 and dec.status() == 0
+    assert dec.history().tolist() == hist + ids[40:85].tolist()
+    kvd = hp.n_kv_heads * hp.head_dim
+    for l in range(hp.n_layers):
+        gk, gv = dec.kv(l, pos + 45)
+        ok, ov = orc.kv(l, pos + 45, kvd)
+        assert (gk == ok).all() and (gv == ov).all(), l
+    if n_steps == 0:  # check_batch: the batched logits equal the token-by-token ones (one-token prefills)
+        want = dec.logits().copy()
+        for p in range(85):
+            dec.prefill(ids[p:p + 1], p, top_k=0)
+        assert (bits(dec.logits()) == bits(orc.forward(int(ids[84]), 84, top_k=0)["logits"])).all()
+        full = dec.logits()
+        rows = np.isfinite(want)
+        assert (bits(full[rows]) == bits(want[rows])).all()

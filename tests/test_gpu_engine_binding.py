@@ -1,0 +1,90 @@
+"""The reference engine bound to the GPU path, run on the GPU.
+
+oracle/_ref/quanta_hip is the reference's own engine and CLI (engine/src/*.cpp, tools/cli/main.cpp) built by
+`make -C oracle engine` with the binding a maintainer adds: engine/src/ops_dispatch.cpp replaced by
+quanta.cpp_amd/host/ops_hip.cpp (matvec_q / matmul_q over the HIP library, ops.h:57-71) and Model::shortlist_head's
+body replaced by one quanta::shortlist_head call (model.cpp:240-334). Through it this file runs the reference's own
+checks (engine/src/checks.cpp) on a 2-layer, vocabulary-4096 q4mix model of the Qwen2.5-0.5B widths written by
+quanta.cpp_amd/qnt.py:
+
+- kernel_selftest (checks.cpp:64-146): the "hip" matvec against the scalar matvec_q_ref for Q8_0 and Q4_0 at
+  4864x896, and the "hip" matmul (32 and 7 tokens) bit-exact against the "hip" matvec per token;
+- check_batch (checks.cpp:148-176): batched prefill logits equal token-by-token logits for n = 1, 31, 32, 33, 100
+  from position 0, a second turn (pos0 = 40, n = 45) and the whole prompt, every matrix product on the GPU;
+- check_head (checks.cpp:178-239): the GPU shortlist head against the GPU full head for top-k 1 and 20 with the
+  last 64 ids as must ids, the bound over every row, exact rows bit-identical;
+- `gen --greedy` (tools/cli/main.cpp:216-251), with the shortlist head and with --full-head: the 24-id stream equals
+  the reference CPU engine's (tests/golden/e2e_small.npz, same model and prompt).
+"""
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, ROOT
+
+ENGINE = os.path.join(ROOT, "oracle", "_ref", "quanta_hip")
+TEXT = ("The keeper climbed the narrow stairs every night, cleaned the lens and lit the lamp so that ships could "
+        "find their way through the rocks in winter storms.")
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def small_model(gpu, tmp_path_factory):
+    if not os.path.exists(ENGINE):
+        pytest.skip("oracle/_ref/quanta_hip is not built (make -C oracle engine, where the reference is mounted)")
+    import quanta_cpp_amd.qnt as qnt
+    hp = qnt.HParams(vocab_size=4096, n_layers=2)
+    path = str(tmp_path_factory.mktemp("engine") / "small.qnt")
+    qnt.write_qnt(path, hp, qnt.synthetic_q4mix(7, hp))
+    return path
+
+
+def run_engine(*args):
+    print("engine:", " ".join(args[:3]), flush=True)
+    r = subprocess.run([ENGINE, *args], capture_output=True, text=True, timeout=150)
+    print(r.stdout[-4000:], r.stderr[-2000:], flush=True)
+    return r
+
+
+def test_reference_selftest(small_model):
+    r = run_engine("selftest")
+    assert r.returncode == 0, r.stderr
+    lines = r.stdout.splitlines()
+    assert "kernel: hip" in lines
+    for dt in ("q8_0", "q4_0"):
+        mv = [l for l in lines if l.startswith(dt) and " hip " in l and " matvec max err " in l]
+        mm = [l for l in lines if l.startswith(dt) and " hip " in l and " matmul x32: " in l]
+        assert len(mv) == 1 and "max err 0.00e+00" in mv[0] and "PASS" in mv[0], mv
+        assert len(mm) == 1 and "bit-exact PASS" in mm[0], mm
+    assert "FAIL" not in r.stdout
+
+
+def test_reference_check_batch(small_model):
+    r = run_engine("checkbatch", "-m", small_model, "-p", TEXT, "-t", "8")
+    assert r.returncode == 0, r.stderr
+    passed = [l for l in r.stdout.splitlines() if l.startswith("batch ") and l.endswith("PASS")]
+    cases = {tuple(int(v) for v in re.match(r"batch pos0=\s*(\d+) n=\s*(\d+)", l).groups()) for l in passed}
+    assert {(0, 1), (0, 31), (0, 32), (0, 33), (0, 100), (40, 45), (0, len(TEXT))} <= cases, cases
+    assert "FAIL" not in r.stdout
+
+
+def test_reference_check_head(small_model):
+    r = run_engine("checkhead", "-m", small_model, "-p", TEXT, "-t", "8")
+    assert r.returncode == 0, r.stderr
+    assert "head bound violations: 0   mismatches: 0   PASS" in r.stdout
+    assert r.stdout.count("head top_k=") == 2
+
+
+@pytest.mark.parametrize("full_head", [False, True])
+def test_reference_gen_stream(small_model, full_head):
+    g = np.load(os.path.join(GOLDEN, "e2e_small.npz"))
+    ids = ",".join(str(int(i)) for i in g["prompt"])
+    args = ["gen", "-m", small_model, "--ids", ids, "-n", str(len(g["out"])), "--greedy", "-t", "8"]
+    r = run_engine(*(args + (["--full-head"] if full_head else [])))
+    assert r.returncode == 0, r.stderr
+    got = [int(t) for t in r.stdout.strip().split(",")]
+    assert got == g["out"].tolist()

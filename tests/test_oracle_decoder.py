@@ -93,3 +93,36 @@ def test_oracle_decoder_equals_reference_build(oracle, ref, tmp_path):
         assert (bits(r["logits"]) == bits(lg)).all(), step
         pos += 1
     ref.ref_model_free(m)
+
+
+def test_oracle_second_turn_prefill_equals_reference_build(oracle, ref, tmp_path):
+    """check_batch's second turn (engine/src/checks.cpp:148-176; session.cpp:13-31): a prefill at pos0 > 0 over a cache
+    filled by an earlier prefill, directly (pos0 = 40, n = 45) and after three decode steps (pos0 = 43, not a multiple
+    of the V cache's 8-position blocks); hidden state, logits and head rows equal the reference build's."""
+    qnt = qnt_module()
+    hp = qnt.HParams(vocab_size=3072, n_layers=3)
+    tens = qnt.synthetic_q4mix(23, hp)
+    path = str(tmp_path / "m.qnt")
+    qnt.write_qnt(path, hp, tens)
+    V, D = hp.vocab_size, hp.dim
+    ids = np.random.default_rng(31).integers(0, V, 85).astype(np.int32)
+    lg, h = np.empty(V, np.float32), np.empty(D, np.float32)
+    for n_steps in (0, 3):
+        m = ref.ref_model_load(path.encode(), 512, 4)
+        dec = oracle_decoder(oracle, hp, tens, ctx_len=512)
+        ref.ref_model_forward_batch(m, ids.ctypes.data, 40, 0, 1, lg.ctypes.data, h.ctypes.data, None, None)
+        r = dec.forward_batch(ids[:40], 0, top_k=1)
+        assert (bits(r["logits"]) == bits(lg)).all()
+        pos = 40
+        for _ in range(n_steps):
+            tok = int(np.argmax(lg))
+            ref.ref_model_forward(m, tok, pos, 1, lg.ctypes.data, h.ctypes.data, None, None)
+            r = dec.forward(tok, pos, top_k=1)
+            assert (bits(r["logits"]) == bits(lg)).all()
+            pos += 1
+        second = np.ascontiguousarray(ids[40:85])
+        rows = ref.ref_model_forward_batch(m, second.ctypes.data, 45, pos, 1, lg.ctypes.data, h.ctypes.data, None,
+                                           None)
+        r = dec.forward_batch(second, pos, top_k=1)
+        assert r["rows"] == rows and (bits(r["hidden"]) == bits(h)).all() and (bits(r["logits"]) == bits(lg)).all()
+        ref.ref_model_free(m)
