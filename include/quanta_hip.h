@@ -165,6 +165,23 @@ int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_t
                       const float* xd, const qh_head_query* query, const qh_head_out* out, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* Bytes of the scratch array qh_shortlist_head_noalloc works in: one array in each GPU's memory, held by the library
+ * until the process ends. Enough for the 151,936-row Qwen2.5 head (about 0.85 MB at top_k 1, 1.3 MB at top_k 55) and
+ * for heads up to about 800,000 rows of 896. */
+#define QH_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
+
+/* qh_shortlist_head with the same arguments and results but no workspace argument, and no device allocation of any
+ * kind: its workspace is the library's scratch array on the current GPU. Fails with QH_ERR_NOMEM, launching nothing,
+ * when qh_shortlist_workspace_bytes(V, D, top_k) exceeds QH_NOALLOC_SCRATCH_BYTES. Every call on one GPU works in that
+ * GPU's one array, which keeps the last call's contents (the kernels reset what they read, so nothing of one call
+ * reaches the next): calls in order on one stream are fine, calls that overlap on one GPU (two streams, or two host
+ * threads without an order between them) race and give wrong results.
+ * No counterpart in the reference (its Model allocates the head's state on the host at load): for callers that cannot
+ * allocate device memory, such as code under HIP graph capture, tight serving loops and harnesses that forbid
+ * hipMalloc. */
+int qh_shortlist_head_noalloc(const qh_tensor* head8, const qh_tensor* head4, const qh_tensor* err, const int8_t* xq,
+                              const float* xd, const qh_head_query* query, const qh_head_out* out, void* stream);
+
 /* ------------------------------------------------------------------ sampler */
 
 /* The reference's SamplerParams (sampler.h) without the seed: the generator state lives in device memory. */

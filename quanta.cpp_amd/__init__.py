@@ -18,6 +18,9 @@ LIB_PATH = os.path.join(HERE, "libquanta_hip.so")
 QK = 32
 F32, F16, Q8_0, Q4_0 = 0, 1, 2, 3
 HEAD_MAX_TOPK = 55
+NOALLOC_SCRATCH_BYTES = 4 << 20  # QH_NOALLOC_SCRATCH_BYTES
+# status codes (quanta_hip.h)
+OK, ERR_ARG, ERR_DTYPE, ERR_SHAPE, ERR_ALIGN, ERR_HIP, ERR_NOMEM, ERR_UNSUPPORTED = range(8)
 
 
 class QHError(RuntimeError):
@@ -70,8 +73,8 @@ EXPORTS = ("qh_last_error", "qh_version", "qh_init", "qh_quant_bytes", "qh_tenso
            "qh_malloc", "qh_free", "qh_memcpy_h2d", "qh_memcpy_d2h", "qh_memset", "qh_stream_sync",
            "qh_stream_create", "qh_stream_destroy",
            "qh_quantize_q8", "qh_matvec_q", "qh_matmul_q", "qh_argmax_workspace_bytes", "qh_argmax",
-           "qh_shortlist_workspace_bytes",
-           "qh_shortlist_head", "qh_sampler_state", "qh_sample", "qh_decoder_create", "qh_decoder_destroy",
+           "qh_shortlist_workspace_bytes", "qh_shortlist_head", "qh_shortlist_head_noalloc",
+           "qh_sampler_state", "qh_sample", "qh_decoder_create", "qh_decoder_destroy",
            "qh_decoder_prefill", "qh_decoder_begin", "qh_decoder_step", "qh_decoder_views", "qh_decoder_set_query",
            "qh_decoder_set_sampler")
 
@@ -98,6 +101,8 @@ def _bind(lib):
         "qh_shortlist_workspace_bytes": ([i32, i32, i32], sz),
         "qh_shortlist_head": ([C.POINTER(qh_tensor)] * 3 + [vp, vp, C.POINTER(qh_head_query), C.POINTER(qh_head_out),
                                vp, sz, vp], i32),
+        "qh_shortlist_head_noalloc": ([C.POINTER(qh_tensor)] * 3 + [vp, vp, C.POINTER(qh_head_query),
+                                       C.POINTER(qh_head_out), vp], i32),
         "qh_decoder_create": ([C.POINTER(qh_model_desc), C.POINTER(qh_tensor), i32, C.POINTER(vp)], i32),
         "qh_decoder_destroy": ([vp], i32),
         "qh_decoder_prefill": ([vp, vp, i32, i32, i32, vp], i32),

@@ -14,6 +14,12 @@ namespace {
 thread_local char g_error[512] = "";
 std::mutex g_init_mu;
 bool g_inited[64] = {};
+
+// The workspace of qh_shortlist_head_noalloc: one array in each GPU's memory, for the life of the process. Host code
+// never uses its name as an address (on the host it names a stand-in, not device memory): qh_init records each
+// device's own address of it, taken with hipGetSymbolAddress while that device is current, in g_scratch.
+__device__ __align__(256) uint8_t scratch[QH_NOALLOC_SCRATCH_BYTES];
+void* g_scratch[64] = {};
 }  // namespace
 
 int fail(int code, const char* fmt, ...) {
@@ -74,6 +80,39 @@ int qh_init_current() {
     return qh_init(dev);
 }
 
+// The current device's address of the scratch array (initialising the device on its first use).
+int scratch_current(void** ws) {
+    int dev = 0;
+    if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (int rc = qh_init(dev)) return rc;
+    std::lock_guard<std::mutex> lk(g_init_mu);
+    *ws = g_scratch[dev];
+    return *ws ? QH_OK : fail(QH_ERR_HIP, "no scratch array on device %d", dev);
+}
+
+// Arguments of the shortlist head entry points (everything but the workspace).
+int validate_head(const qh_tensor* head8, const qh_tensor* head4, const qh_tensor* err, const int8_t* xq,
+                  const float* xd, const qh_head_query* query, const qh_head_out* out, const char* who) {
+    if (!head8 || !head4 || !err || !query || !out) return fail(QH_ERR_ARG, "%s: null argument", who);
+    if (int rc = validate_quant(head8, who)) return rc;
+    if (int rc = validate_quant(head4, who)) return rc;
+    if (head8->dtype != QH_Q8_0 || head4->dtype != QH_Q4_0 || err->dtype != QH_F16)
+        return fail(QH_ERR_DTYPE, "%s: needs q8_0 head, q4_0 copy and f16 bounds", who);
+    const int V = head8->rows, D = head8->cols;
+    if (head4->rows != V || head4->cols != D || err->rows != V || err->cols != D / QH_QK)
+        return fail(QH_ERR_SHAPE, "%s: bad shortlist tensors", who);  // as model.cpp:49-58
+    if (!head_shape_supported(D))
+        return fail(QH_ERR_SHAPE, "%s: hidden size %d must be a multiple of 64 and at most %d", who, D, kMaxHeadCols);
+    if (!err->data || !aligned16(err->data)) return fail(QH_ERR_ALIGN, "%s: err not 16-byte aligned", who);
+    if (!xq || !xd || !aligned16(xq)) return fail(QH_ERR_ARG, "%s: bad activation pointers", who);
+    if (query->top_k < 1 || query->top_k > QH_HEAD_MAX_TOPK)
+        return fail(QH_ERR_UNSUPPORTED, "%s: top_k %d outside [1, %d]", who, query->top_k, QH_HEAD_MAX_TOPK);
+    if (query->n_must < 0 || (query->n_must > 0 && !query->must)) return fail(QH_ERR_ARG, "%s: bad must list", who);
+    if (!out->logits || !out->coarse || !out->upper || !out->rows || !out->stats)
+        return fail(QH_ERR_ARG, "%s: null output buffer", who);
+    return QH_OK;
+}
+
 }  // namespace
 }  // namespace qh
 
@@ -97,6 +136,10 @@ int qh_init(int device) {
         if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
             return fail(QH_ERR_UNSUPPORTED, "qh_init: device %d is %s, this build targets gfx950", device,
                         prop.gcnArchName);
+        void* p = nullptr;
+        if (int rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return rc;
+        if (!p) return fail(QH_ERR_HIP, "qh_init: no device address for the scratch array");
+        g_scratch[device] = p;
         g_inited[device] = true;
     }
     return QH_OK;
@@ -250,26 +293,8 @@ size_t qh_shortlist_workspace_bytes(int V, int D, int top_k) {
 int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_tensor* err, const int8_t* xq,
                       const float* xd, const qh_head_query* query, const qh_head_out* out, void* workspace,
                       size_t workspace_bytes, void* stream) {
-    if (!head8 || !head4 || !err || !query || !out) return fail(QH_ERR_ARG, "qh_shortlist_head: null argument");
-    if (int rc = validate_quant(head8, "qh_shortlist_head head8")) return rc;
-    if (int rc = validate_quant(head4, "qh_shortlist_head head4")) return rc;
-    if (head8->dtype != QH_Q8_0 || head4->dtype != QH_Q4_0 || err->dtype != QH_F16)
-        return fail(QH_ERR_DTYPE, "qh_shortlist_head: needs q8_0 head, q4_0 copy and f16 bounds");
-    const int V = head8->rows, D = head8->cols;
-    if (head4->rows != V || head4->cols != D || err->rows != V || err->cols != D / QH_QK)
-        return fail(QH_ERR_SHAPE, "qh_shortlist_head: bad shortlist tensors");  // as model.cpp:49-58
-    if (!head_shape_supported(D))
-        return fail(QH_ERR_SHAPE, "qh_shortlist_head: hidden size %d must be a multiple of 64 and at most %d", D,
-                    kMaxHeadCols);
-    if (!err->data || !aligned16(err->data)) return fail(QH_ERR_ALIGN, "qh_shortlist_head: err not 16-byte aligned");
-    if (!xq || !xd || !aligned16(xq)) return fail(QH_ERR_ARG, "qh_shortlist_head: bad activation pointers");
-    if (query->top_k < 1 || query->top_k > QH_HEAD_MAX_TOPK)
-        return fail(QH_ERR_UNSUPPORTED, "qh_shortlist_head: top_k %d outside [1, %d]", query->top_k, QH_HEAD_MAX_TOPK);
-    if (query->n_must < 0 || (query->n_must > 0 && !query->must))
-        return fail(QH_ERR_ARG, "qh_shortlist_head: bad must list");
-    if (!out->logits || !out->coarse || !out->upper || !out->rows || !out->stats)
-        return fail(QH_ERR_ARG, "qh_shortlist_head: null output buffer");
-    const size_t need = head_workspace_bytes(V, D, query->top_k);
+    if (int rc = validate_head(head8, head4, err, xq, xd, query, out, "qh_shortlist_head")) return rc;
+    const size_t need = head_workspace_bytes(head8->rows, head8->cols, query->top_k);
     if (!workspace || workspace_bytes < need)
         return fail(QH_ERR_NOMEM, "qh_shortlist_head: workspace %zu bytes, needs %zu", workspace_bytes, need);
     if (!aligned16(workspace)) return fail(QH_ERR_ALIGN, "qh_shortlist_head: workspace not 16-byte aligned");
@@ -279,6 +304,22 @@ int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_t
     return check_hip(
         launch_shortlist_head(*head8, *head4, *err, xq, xd, *query, must, *out, workspace, as_stream(stream)),
         "qh_shortlist_head launch");
+}
+
+int qh_shortlist_head_noalloc(const qh_tensor* head8, const qh_tensor* head4, const qh_tensor* err, const int8_t* xq,
+                              const float* xd, const qh_head_query* query, const qh_head_out* out, void* stream) {
+    if (int rc = validate_head(head8, head4, err, xq, xd, query, out, "qh_shortlist_head_noalloc")) return rc;
+    const size_t need = head_workspace_bytes(head8->rows, head8->cols, query->top_k);
+    if (need > QH_NOALLOC_SCRATCH_BYTES)
+        return fail(QH_ERR_NOMEM, "qh_shortlist_head_noalloc: needs %zu bytes of workspace, the scratch array holds %zu",
+                    need, (size_t)QH_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if (int rc = scratch_current(&ws)) return rc;
+    HeadMust must;
+    must.ids = query->must;
+    must.n = query->n_must;
+    return check_hip(launch_shortlist_head(*head8, *head4, *err, xq, xd, *query, must, *out, ws, as_stream(stream)),
+                     "qh_shortlist_head_noalloc launch");
 }
 
 int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tensors, qh_decoder** out) {

@@ -107,3 +107,14 @@ def test_package_fails_loudly_without_library(qh, monkeypatch, tmp_path):
     monkeypatch.setattr(qh, "_lib", None)
     with pytest.raises(qh.QHError, match="no CPU fallback"):
         qh.lib()
+
+
+def test_noalloc_entry_point_host_checks(qh):
+    """The no-allocation shortlist entry point: its scratch size in the header and the binding agree, and bad
+    arguments are refused on the host before any device work."""
+    text = open(HEADER).read()
+    m = re.search(r"#define QH_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == qh.NOALLOC_SCRATCH_BYTES
+    L = qh.lib()
+    assert L.qh_shortlist_head_noalloc(None, None, None, None, None, None, None, None) == qh.ERR_ARG
+    assert b"null argument" in L.qh_last_error()

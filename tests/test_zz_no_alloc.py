@@ -1,0 +1,107 @@
+"""qh_shortlist_head_noalloc (the shortlist head working in the library's own scratch array, no allocation) against
+qh_shortlist_head with a caller workspace, through the C-ABI: two calls in a row, the second on a smaller head with
+top-k 20 and must ids; every output bit-identical (logits, coarse scores, upper bounds, row list, stats). Also the
+size limit: a head whose workspace exceeds the scratch array is refused before anything is launched."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _upload(qh, synth, V, D, seed):
+    head8, head4, err = synth.shortlist_head(seed, V, D)
+    return (qh.DeviceTensor.upload(head8, 2, V, D), qh.DeviceTensor.upload(head4, 3, V, D),
+            qh.DeviceTensor.upload(err.view(np.uint8), 1, V, D // 32))
+
+
+def _outputs(V, n_must, dev):
+    return {"logits": torch.empty(V, dtype=torch.float32, device=dev),
+            "coarse": torch.empty(V, dtype=torch.float32, device=dev),
+            "upper": torch.empty(V, dtype=torch.float32, device=dev),
+            "rows": torch.empty(V + n_must, dtype=torch.int32, device=dev),
+            "stats": torch.zeros(8, dtype=torch.int32, device=dev)}
+
+
+def _call(qh, heads, xq, xd, top_k, must, ws):
+    """One head call through the C-ABI; ws None = the no-allocation entry point."""
+    h8, h4, he = heads
+    V = h8.rows
+    n_must = 0 if must is None else int(must.numel())
+    o = _outputs(V, n_must, xq.device)
+    q = qh.qh_head_query(top_k, 0, must.data_ptr() if n_must else None, n_must)
+    out = qh.qh_head_out(*(o[k].data_ptr() for k in ("logits", "coarse", "upper", "rows", "stats")))
+    L = qh.lib()
+    args = (C.byref(h8.view), C.byref(h4.view), C.byref(he.view), C.c_void_p(xq.data_ptr()), C.c_void_p(xd.data_ptr()),
+            C.byref(q), C.byref(out))
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if ws is None:
+        rc = L.qh_shortlist_head_noalloc(*args, stream)
+    else:
+        rc = L.qh_shortlist_head(*args, C.c_void_p(ws.data_ptr()), ws.numel(), stream)
+    assert rc == 0, L.qh_last_error().decode()
+    torch.cuda.synchronize()
+    return {k: v.cpu().numpy() for k, v in o.items()}
+
+
+def _same(a, b):
+    sa = qh_stats(a["stats"])
+    sb = qh_stats(b["stats"])
+    assert sa == sb
+    for k in ("logits", "coarse", "upper"):
+        assert (bits(a[k]) == bits(b[k])).all(), k
+    n, ns, nm = sa["n_rows"], sa["n_seeds"], sa["n_must"]
+    ra, rb = a["rows"][:n], b["rows"][:n]
+    assert ra[:ns].tolist() == rb[:ns].tolist()  # seeds, best coarse first
+    assert ra[ns:ns + nm].tolist() == rb[ns:ns + nm].tolist()  # must ids in query order
+    assert sorted(ra[ns + nm:].tolist()) == sorted(rb[ns + nm:].tolist())  # candidates, unordered
+
+
+def qh_stats(raw):
+    import quanta_cpp_amd as qh
+    s = qh.qh_head_stats.from_buffer_copy(np.ascontiguousarray(raw).tobytes())
+    return {f: getattr(s, f) for f, _ in qh.qh_head_stats._fields_}
+
+
+def test_noalloc_equals_workspace_entry(qh, synth, gpu):
+    D = 896
+    cases = [(151936, 47, 1, None), (20011, 59, 20, [5, 17, 5, 19000, -3, 4000, 123, 17, 20010])]
+    for i, (V, seed, top_k, must) in enumerate(cases):
+        print(f"noalloc case {i}: V={V} top_k={top_k} must={must is not None}", flush=True)
+        heads = _upload(qh, synth, V, D, seed)
+        x = torch.from_numpy(synth.activations(seed + 1, 1, D, scale=0.5)).to(gpu)
+        xq, xd = qh.quantize_q8(x)
+        m = None if must is None else torch.tensor(must, dtype=torch.int32, device=gpu)
+        nbytes = qh.lib().qh_shortlist_workspace_bytes(V, D, top_k)
+        assert 0 < nbytes <= qh.NOALLOC_SCRATCH_BYTES
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+        want = _call(qh, heads, xq[0], xd[0], top_k, m, ws)
+        got = _call(qh, heads, xq[0], xd[0], top_k, m, None)
+        _same(got, want)
+        assert 0 < qh_stats(got["stats"])["n_rows"] < V
+
+
+def test_noalloc_refuses_oversized_head(qh, synth, gpu):
+    """A head whose workspace exceeds the scratch array: QH_ERR_NOMEM, and no kernel is launched (the descriptors
+    claim more rows than their buffers hold, which only the size check may see)."""
+    V, D = 6007, 896
+    heads = _upload(qh, synth, V, D, 3)
+    big = 2_000_000
+    assert qh.lib().qh_shortlist_workspace_bytes(big, D, 1) > qh.NOALLOC_SCRATCH_BYTES
+    views = []
+    for t, rows, cols in ((heads[0], big, D), (heads[1], big, D), (heads[2], big, D // 32)):
+        views.append(qh.qh_tensor(t.view.dtype, rows, cols, t.view.data))
+    xq, xd = qh.quantize_q8(torch.zeros(1, D, device=gpu))
+    dummy = torch.empty(16, dtype=torch.float32, device=gpu)
+    q = qh.qh_head_query(1, 0, None, 0)
+    out = qh.qh_head_out(*(dummy.data_ptr(),) * 5)
+    L = qh.lib()
+    rc = L.qh_shortlist_head_noalloc(C.byref(views[0]), C.byref(views[1]), C.byref(views[2]),
+                                     C.c_void_p(xq.data_ptr()), C.c_void_p(xd.data_ptr()), C.byref(q), C.byref(out),
+                                     C.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == qh.ERR_NOMEM and b"scratch array" in L.qh_last_error()
+    torch.cuda.synchronize()
