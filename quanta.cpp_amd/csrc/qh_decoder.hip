@@ -1058,6 +1058,405 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
+// ------------------------------------------------------------------------------ decode attention, 16 waves per head
+// Timeline stamps for phase measurements: compiled in only with -DQH_TIMELINE (thread 0 of workgroup 0 records the
+// shader clock at each stamp; qh_timeline_read copies them out).
+#if defined(QH_TIMELINE)
+__device__ uint64_t qh_tl[64];
+#define QH_STAMP(i)                                                                    \
+    do {                                                                               \
+        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) qh_tl[i] = __builtin_readcyclecounter(); \
+    } while (0)
+#else
+#define QH_STAMP(i) \
+    do {            \
+    } while (0)
+#endif
+
+// Brings every 64-byte line of g[0, n) (g uniform across the wave, 4-byte aligned) into the scalar cache: one scalar
+// load per line, all in flight at once, then one wait. The loads land in one scratch register, since only their
+// cache fill matters.
+__device__ __forceinline__ void warm_lines(const float* g, int n) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    uint32_t sink;
+    for (int i = 0; i < n; i += 16)
+        asm volatile("s_load_dword %0, %1, 0x0" : "=s"(sink) : "s"(g + i) : "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#endif
+}
+
+// Workgroup state of a four-segment chain run by waves 0-3 of a 16-wave workgroup (seg16_*).
+struct SegShared16 {
+    double part[16][4];  // [wave][k]: the wave's share of the exact sum of the chain's terms below segment k's start
+    float res[256];      // every lane's segment result (waves 0-3)
+    uint32_t gbits[4];   // segment k's guess
+};
+
+// Sums three per-lane partials over the wave into part[wave][1..3]; a barrier must follow before seg16_run.
+__device__ __forceinline__ void seg16_partials(SegShared16& sh, double p1, double p2, double p3) {
+    p1 = wave_sum_lane63(p1);
+    p2 = wave_sum_lane63(p2);
+    p3 = wave_sum_lane63(p3);
+    if ((threadIdx.x & 63) == 63) {
+        const int w = (int)threadIdx.x >> 6;
+        sh.part[w][1] = p1;
+        sh.part[w][2] = p2;
+        sh.part[w][3] = p3;
+    }
+}
+
+// seg_chain_run for a 16-wave workgroup: waves 0-3 run the four segments (wave 0 from 0, wave k from the 64 candidates
+// around its guess, the f32 rounding of the exact sum below the segment), the others wait at the barrier; then every
+// thread follows the chain through the candidates and returns its end value. chain(k, start) runs segment k from
+// start in the calling wave (k and start uniform across the wave). All 1024 threads call it after the barrier that
+// published part.
+template <typename Chain>
+__device__ __forceinline__ float seg16_run(SegShared16& sh, Chain chain) {
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (wave < 4) {
+        float start = 0.0f;
+        if (wave > 0) {
+            double g = 0.0;
+#pragma unroll
+            for (int w = 0; w < 16; ++w) g += sh.part[w][wave];
+            const uint32_t gb = __float_as_uint((float)g);
+            start = __uint_as_float(gb + (uint32_t)lane - 32u);
+            if (lane == 0) sh.gbits[wave] = gb;
+        }
+        sh.res[tid] = chain(wave, start);
+    }
+    __syncthreads();
+    float s = sh.res[0];
+    const uint32_t g1 = sh.gbits[1], g2 = sh.gbits[2], g3 = sh.gbits[3];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) {
+        const uint32_t j = __float_as_uint(s) - (k == 1 ? g1 : k == 2 ? g2 : g3) + 32u;
+        if (j < 64u)
+            s = sh.res[64 * k + j];
+        else
+            s = chain(k, s);
+    }
+    return s;
+}
+
+// Decode attention of one token (position *pos_dev) for query head h = blockIdx.x over positions [0, pos], head_dim 64:
+// the same arithmetic, order and cache layouts as attention_kernel with one token, spread over 16 waves. Every thread
+// scores one cached row held in registers (rows beyond 1024 in a loop), the 16 waves share the V DMA of the first LDS
+// stage (a few transfers each, issued after their scores, so the scores keep exact load waits), and the exp and
+// normalisation run one position per thread. The serial softmax sum runs as four segments on waves 0-3 (seg16_run), the
+// weighted V chain on wave 0 with the weights as scalar operands while the other waves bring the weight row into the
+// scalar cache. Workgroups of the first query head of each KV group store the token's K / V row.
+// Grid (group, n_kv) with group = n_heads / n_kv: query head h = blockIdx.y * group + blockIdx.x of KV head blockIdx.y,
+// so no division is needed. The arguments the first loads need come first: the first 16 dwords arrive in registers at
+// dispatch, the rest (and the grid's size) take a load.
+template <int HD>
+__global__ __launch_bounds__(1024) void attention_decode_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    uint16_t* __restrict__ kc, const int* __restrict__ pos_dev, int ctx, int group, const float* __restrict__ bq,
+    const float* __restrict__ bk, int n_kv, const float* __restrict__ bv, const float* __restrict__ cs,
+    uint16_t* __restrict__ vc, int8_t* __restrict__ oq, float* __restrict__ od, float* __restrict__ escr,
+    int escr_stride, int* __restrict__ status) {
+    static_assert(HD == 64, "one chain wave and one K row of 8 chunks per thread");
+    constexpr int NT = 1024, NW = NT / 64;
+    constexpr int HALF = HD / 2, CPR = HD / 8;
+    constexpr int kVRows = kVStageBytes / (HD * 2);  // V rows one LDS stage holds (a multiple of 8)
+    constexpr int kVBlk = kVRows / 8;                // 8-row blocks per stage
+    __shared__ __align__(16) float att[kMaxCtx + kChainPad];
+    __shared__ __align__(16) uint4 vst[(kVBlk + 4) * HD];  // [block][dim] -> 8 rows; 4 blocks of read padding
+    __shared__ __align__(16) uint16_t kloc[HD];
+    __shared__ __align__(16) uint16_t vloc[HD];
+    __shared__ __align__(16) float qs[HD];
+    __shared__ float red[NW];
+    __shared__ float sum_sh;
+    __shared__ uint64_t exptab[32];
+    __shared__ SegShared16 ssh;
+    QH_STAMP(0);
+    const int n_heads = group * n_kv;
+    const int kvh = (int)blockIdx.y, h = kvh * group + (int)blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvd = n_kv * HD;
+    // The token's raw q (wave 0), k (wave 1) and v (wave 2) values and biases do not depend on the position: their
+    // loads go out before it arrives.
+    float pa = 0.0f, pb = 0.0f, ba = 0.0f, bb = 0.0f, pc = 0.0f, ps = 0.0f;
+    if (wave < 2 && lane < HALF) {
+        const float* src = wave == 0 ? q + h * HD : k + kvh * HD;
+        const float* bias = wave == 0 ? (bq ? bq + h * HD : nullptr) : (bk ? bk + kvh * HD : nullptr);
+        pa = src[lane];
+        pb = src[lane + HALF];
+        ba = bias ? bias[lane] : 0.0f;
+        bb = bias ? bias[lane + HALF] : 0.0f;
+    } else if (wave == 2) {
+        pa = v[kvh * HD + lane];
+        ba = bv ? bv[kvh * HD + lane] : 0.0f;
+    }
+    ExpTab et;
+    et.load();
+    const uint4* vc4 = reinterpret_cast<const uint4*>(vc);
+    auto vchunk = [&](int blk, int d) { return (size_t)blk * kvd + kvh * HD + d; };  // uint4 index of (block, dim)
+    auto kchunk = [&](int c, int p) { return ((size_t)kvh * CPR + c) * ctx + p; };    // 16-byte K chunk c of row p
+    // This thread's K row (row tid, inside the cache) goes out before the position arrives too: its transfer is the
+    // longest of the kernel's first loads. Rows at or beyond the position are read and ignored (row pos may be being
+    // written by this launch).
+    v4u kk[CPR];
+    {
+        const uint16_t* kg = kc + (kchunk(0, min(tid, ctx - 1)) << 3);
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) kk[i] = ld4(kg + (size_t)i * ctx * 8);
+    }
+    const int pos = *pos_dev, nrows = pos + 1;
+    if (pos >= ctx || pos < 0) {  // uniform: a step past the context touches no cache row
+        if (tid == 0 && h == 0) atomicOr(status, kStatusCtx);
+        return;
+    }
+    QH_STAMP(8);
+    // Then the RoPE angles of the position (ops_ref.cpp:201-214, with the reference build's contraction).
+    if (wave < 2 && lane < HALF) {
+        const float* crow = cs + (size_t)pos * HD;
+        pc = crow[2 * lane];
+        ps = crow[2 * lane + 1];
+    }
+    const bool has_bias = wave == 0 ? bq != nullptr : wave == 1 ? bk != nullptr : bv != nullptr;
+    if (wave < 2 && lane < HALF) {
+        float a = pa, b = pb;
+        if (has_bias) {
+            a = a + ba;
+            b = b + bb;
+        }
+        const float lo = __builtin_fmaf(a, pc, -(b * ps)), hi = __builtin_fmaf(b, pc, a * ps);
+        QH_STAMP(9);
+        if (wave == 0) {
+            qs[lane] = lo;
+            qs[lane + HALF] = hi;
+        } else {
+            kloc[lane] = f2h(lo);
+            kloc[lane + HALF] = f2h(hi);
+        }
+    } else if (wave == 2) {
+        vloc[lane] = f2h(has_bias ? pa + ba : pa);
+    }
+    et.store(exptab);
+    __syncthreads();
+    QH_STAMP(1);
+    if (h % group == 0 && tid < HD) {
+        kc[(kchunk(tid >> 3, pos) << 3) + (tid & 7)] = kloc[tid];
+        vc[vchunk(pos / 8, tid) * 8 + (pos & 7)] = vloc[tid];
+    }
+
+    // scores s_j = (sum_i q_i * k_ji as one FMA per element in dimension order) * (1 / sqrt(HD)) (model.cpp:122-125);
+    // q comes from LDS by broadcast reads (every lane the same address), which keeps the kernel within the 128
+    // registers a 16-wave workgroup allows
+    const float scale = 1.0f / __builtin_sqrtf((float)HD);
+    const float4* q4 = reinterpret_cast<const float4*>(lane_ptr(qs));
+    auto dot_row = [&](const v4u(&r)[CPR], const float4* q4) {
+        float sc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) {
+            const float4 qa = q4[2 * i], qb = q4[2 * i + 1];
+            const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sc = __builtin_fmaf(qq[2 * e], h2f((uint16_t)(r[i][e] & 0xffffu)), sc);
+                sc = __builtin_fmaf(qq[2 * e + 1], h2f((uint16_t)(r[i][e] >> 16)), sc);
+            }
+        }
+        return sc;
+    };
+    float mx = -__builtin_inff();
+    if (tid < nrows) {  // row tid: the cached row in registers, or the token's own row (tid == pos)
+        if (tid == pos) {
+#pragma unroll
+            for (int i = 0; i < CPR; ++i) kk[i] = ld4(kloc + i * 8);
+        }
+        const float a = dot_row(kk, q4) * scale;
+        att[tid] = a;
+        mx = a;
+    }
+    if (pos >= NT) {  // contexts beyond NT positions: the other cached rows one at a time, then the token's own row
+        for (int j = tid + NT; j < pos; j += NT) {
+            const uint16_t* kg = kc + (kchunk(0, j) << 3);
+#pragma unroll
+            for (int i = 0; i < CPR; ++i) kk[i] = ld4(kg + (size_t)i * ctx * 8);
+            const float4* qo = q4;
+            asm volatile("" : "+v"(qo));  // keeps the q reads inside the loop (hoisted, they would not fit)
+            const float a = dot_row(kk, qo) * scale;
+            att[j] = a;
+            mx = a > mx ? a : mx;
+        }
+        if (tid == pos % NT) {
+#pragma unroll
+            for (int i = 0; i < CPR; ++i) kk[i] = ld4(kloc + i * 8);
+            const float a = dot_row(kk, q4) * scale;
+            att[pos] = a;
+            mx = a > mx ? a : mx;
+        }
+    }
+    QH_STAMP(2);
+    mx = wave_max_sel(mx);  // the maximum does not depend on the order of comparison
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mx = red[w] > mx ? red[w] : mx;
+    QH_STAMP(3);
+    // exp (the exp row also goes to global memory for the segmented sum's scalar loads), with each lane's exact partial
+    // sums below the segment starts
+    float* erow = escr + (size_t)h * escr_stride;
+    float* arow = escr + (size_t)(n_heads + h) * escr_stride;
+    const bool seg = nrows >= 128;  // uniform; shorter rows keep the single chain
+    const int Ls = (nrows / 4) & ~15;
+    const Segs4 sg{(nrows - 3 * Ls) & ~15, Ls, nrows};
+    double p1 = 0.0, p2 = 0.0, p3 = 0.0;
+    for (int j = tid; j < nrows; j += NT) {
+        const float e = dev_expf(att[j] - mx, exptab);
+        att[j] = e;
+        erow[j] = e;
+        p1 += j < sg.start(1) ? (double)e : 0.0;
+        p2 += j < sg.start(2) ? (double)e : 0.0;
+        p3 += j < sg.start(3) ? (double)e : 0.0;
+    }
+    QH_STAMP(10);
+    if (seg) seg16_partials(ssh, p1, p2, p3);
+    QH_STAMP(11);
+    __builtin_amdgcn_s_waitcnt(0);  // the exp row's stores (read through scalar loads after the barrier)
+    QH_STAMP(12);
+    __syncthreads();
+    QH_STAMP(4);
+    // The first stage's V blocks straight into LDS by DMA while waves 0-3 run the softmax sum: waves 4-15 take 1 KB
+    // chunks wave - 4, wave + 8, ... (clamped onto the last chunk, whose repeats write the same data). A wave's DMA
+    // issue waits while the memory pipeline drains, so the chain waves issue none. Cache blocks stop below pos: the
+    // block holding pos, if any, carries a stale row pos that the stage build replaces. The normalisation's
+    // s_waitcnt(0) completes the transfers before the barrier that precedes the V chain.
+    const int ncb = min((pos + 7) / 8, kVBlk);
+    if (wave >= 4) {
+        constexpr int kDmaWaves = NW - 4, kPerWave = (kVBlk + kDmaWaves - 1) / kDmaWaves;
+        const int last = max(ncb - 1, 0);
+#pragma unroll
+        for (int e = 0; e < kPerWave; ++e) {
+            const int c = min(wave - 4 + kDmaWaves * e, last);
+            lds_dma16_async(vc4 + vchunk(c, lane), vst + c * 64);
+        }
+    }
+    // softmax sum in position order (ops_ref.cpp:220-224)
+    auto add = [](float acc, float a) { return acc + a; };
+    float sum;
+    if (seg) {
+        sum = seg16_run(ssh, [&](int kk_, float s0) {
+            warm_lines(erow + sg.start(kk_), sg.len(kk_));  // the exp row was just written: not in the scalar cache
+            return chain_scalar(erow + sg.start(kk_), sg.len(kk_), s0, add);
+        });
+    } else {
+        if (tid == 0) sum_sh = lds_chain(att, nrows, add);
+        __syncthreads();
+        sum = sum_sh;
+    }
+    QH_STAMP(5);
+    const float inv = 1.0f / sum;
+    for (int j = tid; j < nrows; j += NT) {
+        const float a = att[j] * inv;
+        att[j] = a;
+        arow[j] = a;
+    }
+    QH_STAMP(13);
+    // the weight row's stores and the V DMA complete before the barrier; then the token's own row, if it falls inside
+    // the first stage, is written over the DMA's block
+    __builtin_amdgcn_s_waitcnt(0);
+    QH_STAMP(14);
+    __syncthreads();
+    uint16_t* vst16 = reinterpret_cast<uint16_t*>(vst);
+    if (pos < kVRows && tid < HD) vst16[((pos >> 3) * HD + tid) * 8 + (pos & 7)] = vloc[tid];
+    __syncthreads();
+    QH_STAMP(6);
+
+    // out_i = sum_j a_j * v_ji, one FMA per position in order (model.cpp:131-135): lane i of wave 0 per dimension,
+    // the weights as scalar operands (as in attention_kernel); the other waves warm the weight row's lines.
+    float acc = 0.0f;
+    for (int s0 = 0;;) {
+        const int se = min(nrows, s0 + kVRows);
+        if (tid < HD) {
+            const_v16f_ptr wp = (const_v16f_ptr)(arow + s0);  // s0 is a multiple of 32: 64-byte aligned
+            auto ldv = [&](uint4(&vv)[4], int jr) {  // rows s0 + jr .. + 31 (jr % 32 == 0)
+                const uint4* vp = vst + (jr >> 3) * HD + tid;
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) vv[q4] = vp[q4 * HD];
+            };
+            auto use = [&](const uint4(&vv)[4], const v16f& w0, const v16f& w1, int cnt) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const uint32_t w[4] = {vv[q4].x, vv[q4].y, vv[q4].z, vv[q4].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int kx = 8 * q4 + e;
+                        if (kx < cnt)
+                            acc = __builtin_fmaf(kx < 16 ? w0[kx & 15] : w1[kx & 15],
+                                                 h2f((uint16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xffffu)), acc);
+                    }
+                }
+            };
+            const int n = se - s0;
+            uint4 vA[4], vB[4];
+            v16f wA0 = wp[0], wA1 = wp[1], wB0, wB1;
+            ldv(vA, 0);
+            int jr = 0;
+#pragma unroll 1
+            for (; jr + 64 <= n; jr += 64) {
+                wait_lgkm0();
+                __builtin_amdgcn_sched_barrier(0);
+                wB0 = wp[(jr + 32) / 16];
+                wB1 = wp[(jr + 32) / 16 + 1];
+                ldv(vB, jr + 32);
+                __builtin_amdgcn_sched_barrier(0);
+                use(vA, wA0, wA1, 32);
+                wait_lgkm0();
+                __builtin_amdgcn_sched_barrier(0);
+                wA0 = wp[(jr + 64) / 16];
+                wA1 = wp[(jr + 64) / 16 + 1];
+                ldv(vA, jr + 64);
+                __builtin_amdgcn_sched_barrier(0);
+                use(vB, wB0, wB1, 32);
+            }
+            wait_lgkm0();
+            __builtin_amdgcn_sched_barrier(0);
+            if (jr + 32 <= n) {
+                wB0 = wp[(jr + 32) / 16];
+                wB1 = wp[(jr + 32) / 16 + 1];
+                ldv(vB, jr + 32);
+                __builtin_amdgcn_sched_barrier(0);
+                use(vA, wA0, wA1, 32);
+                wait_lgkm0();
+                __builtin_amdgcn_sched_barrier(0);
+                use(vB, wB0, wB1, n - jr - 32);
+            } else {
+                use(vA, wA0, wA1, n - jr);
+            }
+        } else if (s0 == 0) {  // the other waves: 16 lines of the weight row per scalar-load batch
+            const int wi = __builtin_amdgcn_readfirstlane(wave - 1);
+            for (int b = wi * 256; b < nrows; b += (NW - 1) * 256) {
+                SegWarm warm;
+                warm.issue(arow + b, nrows - b);
+                warm.consume();
+            }
+        }
+        s0 = se;
+        if (s0 >= nrows) break;
+        __syncthreads();  // the stage is consumed; load rows [s0, min(nrows, s0 + kVRows)) (s0 % 8 == 0)
+        const int sn = min(nrows, s0 + kVRows);
+        const int nb8 = (sn - s0 + 7) / 8;
+        for (int c = tid; c < nb8 * HD; c += NT) {  // whole cache blocks; the token's row is written after
+            const int blk = s0 / 8 + c / HD, d = c % HD;
+            vst[c] = blk * 8 < pos ? vc4[vchunk(blk, d)] : make_uint4(0u, 0u, 0u, 0u);
+        }
+        __syncthreads();
+        if (pos >= s0 && pos < sn && tid < HD) vst16[(((pos - s0) >> 3) * HD + tid) * 8 + (pos & 7)] = vloc[tid];
+        __syncthreads();
+    }
+    QH_STAMP(7);
+    if (tid < HD) {  // quantize_q8 of the attention output, two 32-blocks per 64 dimensions
+        const int col = h * HD + (tid & ~31);
+        quant_block32(acc, oq + col, od + col / QK);
+    }
+}
+
 // h = g / (1 + expf(-g)) * u (ops_ref.cpp:243-248) over n_blocks 32-blocks, quantized per block.
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                            long n_blocks, int8_t* __restrict__ oq,
@@ -1449,7 +1848,12 @@ hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
     const size_t layer_k = (size_t)hp.ctx_len * hp.n_kv_heads * hp.head_dim;
     const size_t layer_v = (size_t)v_ctx(hp.ctx_len) * hp.n_kv_heads * hp.head_dim;
     const dim3 grid(hp.n_heads, n);
-    if (hp.head_dim == 64)
+    if (n == 1 && hp.head_dim == 64 && d->fuse)  // decode: one 16-wave workgroup per head
+        hipLaunchKernelGGL((attention_decode_kernel<64>), dim3(hp.n_heads / hp.n_kv_heads, hp.n_kv_heads), dim3(1024), 0,
+                           s, d->q, d->k, d->v, d->kc + l * layer_k, d->pos, hp.ctx_len, hp.n_heads / hp.n_kv_heads,
+                           bias(d, l, L_BQ), bias(d, l, L_BK), hp.n_kv_heads, bias(d, l, L_BV), d->cs,
+                           d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status);
+    else if (hp.head_dim == 64)
         hipLaunchKernelGGL((attention_kernel<64>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                            bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
                            d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status);
@@ -1719,6 +2123,12 @@ hipError_t decoder_begin(Decoder* d, int top_k, int32_t* out, int out_cap, hipSt
 }
 
 int decoder_ctx(const Decoder* d) { return d->hp.ctx_len; }
+
+#if defined(QH_TIMELINE)
+extern "C" int qh_timeline_read(uint64_t* host, int n) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(qh_tl), sizeof(uint64_t) * (size_t)n);
+}
+#endif
 
 void decoder_views(Decoder* d, qh_decoder_state* v) {
     v->logits = d->logits;
