@@ -212,6 +212,69 @@ def head_bench(qh, synth, torch, oracle, steps, warmup):
             "shortlist_GBps": sl_bytes / sl_us / 1e3, "full_head_GBps": full_bytes / full_us / 1e3}
 
 
+def stage_bytes(hp, pos):
+    """Algorithmic bytes of each decode stage of one layer at position pos (weights with their scales, the activation
+    and residual rows read and written, the K/V rows attention reads), and of the final norm and shortlist screen."""
+    D, F, hd = hp.dim, hp.ffn_dim, hp.head_dim
+    qd, kvd = hp.n_heads * hd, hp.n_kv_heads * hd
+    q8, q4 = 1 + 2 / 32, 0.5 + 2 / 32
+    act = lambda n: n + 4 * n // 32  # noqa: E731  int8 codes + f32 block scales
+    return {
+        "qkv": (qd + 2 * kvd) * D * q8 + 2 * 4 * D + 4 * (qd + 2 * kvd),
+        "attention": 4 * (qd + 2 * kvd) + 2 * 2 * kvd * pos + 2 * 2 * kvd + act(qd),
+        "o": D * qd * q8 + act(qd) + 2 * 4 * D,
+        "gate_up": 2 * F * D * q4 + 2 * 4 * D + act(F),
+        "down": D * F * q4 + act(F) + 2 * 4 * D,
+    }
+
+
+def decode_stages(qh, torch, hp, tens, n_prompt=512, reps=20):
+    """Device time of every kernel of a greedy decode step, from position n_prompt on: `reps` steps through
+    qh_decoder_step_timed (each kernel launched with start / stop events, the dispatch's own timestamps), each queued
+    behind a spin kernel of about 2 ms (torch.cuda._sleep) so the host has enqueued the whole step before the GPU
+    reaches it and the kernels run back to back as in a replayed graph. Returns per-stage means over layers and steps
+    (kernel time only, the dispatch gaps between kernels excluded), with the algorithmic bytes and the rate they imply,
+    and the sum over the step."""
+    import ctypes as C
+    dec = qh.Decoder(hp, tens, ctx_len=4096)
+    ids = np.random.default_rng(9).integers(0, hp.vocab_size, n_prompt).astype(np.int32)
+    dec.prefill(ids, 0, top_k=1)
+    dec.begin(reps + 2)
+    stream = torch.cuda.current_stream()
+    cap = 512
+    us = np.zeros(cap, np.float32)
+    stage = np.zeros(cap, np.int32)
+    n = C.c_int32(0)
+    kinds = ("qkv", "attention", "o", "gate_up", "down")
+    acc, total = {}, 0.0
+    torch.cuda.synchronize()
+    for rep in range(reps + 1):
+        torch.cuda._sleep(4_000_000)
+        qh._check(qh.lib().qh_decoder_step_timed(dec.h, 1, C.c_void_p(stream.cuda_stream), us.ctypes.data,
+                                                 stage.ctypes.data, cap, C.byref(n)))
+        if rep == 0:
+            continue  # warm-up
+        for i in range(n.value):
+            sid = int(stage[i])
+            kind = ("final_norm" if sid == qh.STAGE_FINAL_NORM else "head" if sid == qh.STAGE_HEAD else
+                    "pick" if sid == qh.STAGE_PICK else kinds[sid % qh.STAGES_PER_LAYER])
+            acc.setdefault(kind, []).append(float(us[i]))
+            total += float(us[i])
+    dec.close()
+    pos = n_prompt + reps // 2
+    nbytes = stage_bytes(hp, pos)
+    out = {"kernels_per_step": int(n.value), "kernel_us_per_step": total / reps, "position": pos}
+    for k, v in acc.items():
+        per = len(v) / reps  # kernels of this stage per step
+        row = {"us_per_kernel": float(np.mean(v)), "kernels_per_step": per}
+        if k in nbytes and per == hp.n_layers:
+            row["bytes"] = nbytes[k]
+            row["GBps"] = nbytes[k] / row["us_per_kernel"] / 1e3
+            row["frac_of_hbm_peak"] = row["GBps"] / HBM_PEAK_GBS
+        out[k] = row
+    return out
+
+
 def e2e_model():
     import quanta_cpp_amd.qnt as qnt
     hp = qnt.HParams()
@@ -322,10 +385,28 @@ def e2e_cpu_sampled(hp, tens, n_prompt=512, n_gen=16):
                       f"({t[0]:.1f} s, {t[1]:.1f} s), {threads} threads"}
 
 
-def e2e_cpu_baseline(hp, tens, n_prompt=512, n_gen=16):
+# Host threads one GPU's share of the box allows (the CPU share a one-GPU job gets, whatever os.cpu_count() reports).
+BOX_CPU_SHARE = 16
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (what lscpu prints as "Model name"), from /proc/cpuinfo."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def e2e_cpu_baseline(hp, tens, n_prompt=512, n_gen=16, n_gen_sweep=8):
     """The reference engine itself (oracle/_ref, built from its sources) on the host cores, bounded sample of the same
-    workload: Model::forward_batch over the 512-token prompt (32-token chunks), then n_gen greedy Model::forward
-    decode steps with the Exact Shortlist Head (top_k = 1), each timed."""
+    workload: Model::forward_batch over the 512-token prompt (32-token chunks) on the box's CPU share, then greedy
+    Model::forward decode steps with the Exact Shortlist Head (top_k = 1) at three thread counts, each on the same
+    cache: the CPU share (BOX_CPU_SHARE threads, the headline `value`), the reference's default min(8, hardware
+    threads / 2) (threadpool.cpp:21-25) and one thread. The model's thread pool is swapped between them
+    (ref_model_set_threads)."""
     sys.path.insert(0, ROOT)
     import ctypes as C
     import oracle as orc
@@ -336,15 +417,19 @@ def e2e_cpu_baseline(hp, tens, n_prompt=512, n_gen=16):
     L.ref_model_load.restype = C.c_void_p
     L.ref_model_load.argtypes = [C.c_char_p, C.c_int, C.c_int]
     L.ref_model_free.argtypes = [C.c_void_p]
+    L.ref_model_set_threads.argtypes = [C.c_void_p, C.c_int]
     L.ref_model_forward.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p]
     L.ref_model_forward_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
                                           C.c_void_p, C.c_void_p]
+    hw = os.cpu_count() or 1
+    share = max(1, min(BOX_CPU_SHARE, hw))
+    default = int(L.ref_default_threads())
     path = os.path.join("/tmp", f"quanta_bench_q4mix_{os.getpid()}.qnt")
     qnt.write_qnt(path, hp, tens)
-    threads = max(1, min(16, os.cpu_count() or 1))
+    sweep = {}
     try:
-        m = L.ref_model_load(path.encode(), 4096, threads)
+        m = L.ref_model_load(path.encode(), 4096, share)
         if not m:
             return None
         ids = np.random.default_rng(9).integers(0, hp.vocab_size, n_prompt).astype(np.int32)
@@ -353,18 +438,25 @@ def e2e_cpu_baseline(hp, tens, n_prompt=512, n_gen=16):
         L.ref_model_forward_batch(m, ids.ctypes.data, n_prompt, 0, 1, logits.ctypes.data, None, None, None)
         t1 = time.perf_counter()
         tok = int(np.argmax(logits))
-        for i in range(n_gen):
-            L.ref_model_forward(m, tok, n_prompt + i, 1, logits.ctypes.data, None, None, None)
-            tok = int(np.argmax(logits))
-        t2 = time.perf_counter()
+        pos = n_prompt
+        for threads, steps in ((share, n_gen), (default, n_gen_sweep), (1, n_gen_sweep)):
+            used = L.ref_model_set_threads(m, threads)
+            ta = time.perf_counter()
+            for _ in range(steps):
+                L.ref_model_forward(m, tok, pos, 1, logits.ctypes.data, None, None, None)
+                tok = int(np.argmax(logits))
+                pos += 1
+            sweep[str(used)] = {"decode_tok_per_s": round(steps / (time.perf_counter() - ta), 3), "steps": steps}
         L.ref_model_free(m)
     finally:
         os.remove(path)
-    return {"value": n_gen / (t2 - t1), "unit": "tok/s", "cores": threads, "kind": "reference",
-            "prefill_tok_per_s": n_prompt / (t1 - t0),
-            "sample": f"reference engine (oracle/_ref): {n_prompt}-token batched prefill ({t1 - t0:.1f} s), then "
-                      f"{n_gen} greedy decode steps with the shortlist head at positions {n_prompt}.. "
-                      f"({t2 - t1:.1f} s), {threads} threads"}
+    return {"value": sweep[str(share)]["decode_tok_per_s"], "unit": "tok/s", "cores": share, "kind": "reference",
+            "prefill_tok_per_s": n_prompt / (t1 - t0), "threads_sweep": sweep, "hardware_concurrency": hw,
+            "default_threads": default, "cpu_model": cpu_model(),
+            "sample": f"reference engine (oracle/_ref): {n_prompt}-token batched prefill on {share} threads "
+                      f"({t1 - t0:.1f} s), then greedy decode steps with the shortlist head from position "
+                      f"{n_prompt}: {n_gen} on {share} threads (the value; the CPU share of one GPU of this "
+                      f"{hw}-thread host), {n_gen_sweep} on the reference default {default}, {n_gen_sweep} on 1"}
 
 
 def read_traffic(path):
@@ -453,7 +545,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end prefill + decode measurement")
-    ap.add_argument("--only", choices=["e2e", "roofline", "prefill", "sampling", "head"],
+    ap.add_argument("--only", choices=["e2e", "roofline", "prefill", "sampling", "head", "stages"],
                     help="one measurement alone (for counter runs): e2e = --e2e-only; roofline = a 256 MiB copy "
                          "(counter calibration) then the Q4_0 GEMV rotation; prefill = Q4_0 4864x896 at M = 512")
     args = ap.parse_args()
@@ -490,6 +582,10 @@ def main():
         r = e2e_bench(qh, torch, hp, tens, steps=args.steps, warmup=args.warmup, mode="chat")
         print(json.dumps({"sampling_chat": rnd(r)}), flush=True)
         return 0
+    if args.only == "stages":
+        hp, tens = e2e_model()
+        print(json.dumps({"decode_stages": decode_stages(qh, torch, hp, tens)}, default=float), flush=True)
+        return 0
     if args.only == "e2e":
         args.e2e_only = True
     hp, tens = e2e_model()
@@ -523,6 +619,17 @@ def main():
                           "us_per_launch": round(head["us_per_launch"], 3),
                           "copies_per_shape": head["copies"]}
     extra = {"q4_gemv_mlp_GBps": round(head["GBps"], 2)}
+    log("decode stages: one traced step per replay")
+    st = decode_stages(qh, torch, hp, tens)
+    if st is not None:
+        nb = stage_bytes(hp, st["position"])
+        head_bytes = hp.vocab_size * (hp.dim // 2 + 2 * (hp.dim // 32) * 2) + 200 * (hp.dim + 2 * (hp.dim // 32))
+        step_bytes = hp.n_layers * sum(nb.values()) + head_bytes
+        extra["decode_stages"] = {k: (rnd(v) if isinstance(v, dict) else v) for k, v in st.items()}
+        extra["decode_step_bytes"] = round(step_bytes)
+        extra["decode_step_GBps"] = round(step_bytes / (e["decode_ms_per_token"] * 1e-3) / 1e9, 1)
+        extra["decode_step_frac_of_hbm_peak"] = round(step_bytes / (e["decode_ms_per_token"] * 1e-3) / 1e9 /
+                                                      HBM_PEAK_GBS, 4)
     if not args.no_extra:
         log("Q8_0 / Q4_0 GEMV per shape, cold and hot")
         for dtype, name, shp in [(2, "q8", [(896, 896), (128, 896), (4864, 896), (896, 4864)]),

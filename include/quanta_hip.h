@@ -150,8 +150,8 @@ typedef struct qh_head_out {
 } qh_head_out;
 
 /* Workspace bytes qh_shortlist_head needs for a V x D head and top_k (0 if unsupported: D must be a multiple
- * of 64 and at most 4096). The workspace needs no initialisation (each call resets what it uses); calls that
- * overlap must not share one. */
+ * of 64 and at most 4096, V at most 1,048,576 on a 256-CU GPU). The workspace needs no initialisation (each call
+ * resets what it uses); calls that overlap must not share one. */
 size_t qh_shortlist_workspace_bytes(int V, int D, int top_k);
 
 /* Exact Shortlist Head on one quantized hidden state (xq [D] int8, xd [D/32] f32):
@@ -277,6 +277,30 @@ int qh_decoder_begin(qh_decoder* d, int top_k, int32_t* out_dev, int out_cap, vo
 int qh_decoder_step(qh_decoder* d, int top_k, void* stream);
 
 int qh_decoder_views(qh_decoder* d, qh_decoder_state* v);
+
+/* Stages of a decode step, as qh_decoder_step_timed names them: per layer l, id l * QH_STAGES_PER_LAYER + one of
+ * QH_STAGE_QKV (rmsnorm + q/k/v projections), QH_STAGE_ATTENTION, QH_STAGE_O (o projection + residual),
+ * QH_STAGE_GATE_UP (rmsnorm + gate/up projections + SwiGLU), QH_STAGE_DOWN (down projection + residual); then
+ * QH_STAGE_FINAL_NORM, QH_STAGE_HEAD and, when a sampler picks the token, QH_STAGE_PICK. With the fused kernels (the
+ * default) each per-layer stage is one kernel. */
+enum {
+    QH_STAGE_QKV = 0,
+    QH_STAGE_ATTENTION = 1,
+    QH_STAGE_O = 2,
+    QH_STAGE_GATE_UP = 3,
+    QH_STAGE_DOWN = 4,
+    QH_STAGES_PER_LAYER = 8,
+    QH_STAGE_FINAL_NORM = 1 << 20,
+    QH_STAGE_HEAD = (1 << 20) + 1,
+    QH_STAGE_PICK = (1 << 20) + 2
+};
+
+/* One qh_decoder_step with every kernel it launches timed on the device by the dispatch's own start and stop
+ * timestamps (no extra packets between the kernels): for the i-th kernel, us_host[i] microseconds and stage_host[i]
+ * its stage id; *n_host = the number of kernels (QH_ERR_NOMEM if more than cap). Host arrays; synchronises the stream.
+ * No counterpart in the reference (its CLI times whole tokens); for profiling. */
+int qh_decoder_step_timed(qh_decoder* d, int top_k, void* stream, float* us_host, int32_t* stage_host, int cap,
+                          int32_t* n_host);
 
 /* The head queries of later prefill / begin / step calls, as Session::head_query builds them from the session's
  * sampler parameters (session.cpp:63-79): top_k = (temperature <= 0 ? 1 : p->top_k), the full head when that is 0,

@@ -154,6 +154,22 @@ void* ref_model_load(const char* path, int ctx_len, int n_threads) {
 
 void ref_model_free(void* m) { delete static_cast<quanta::Model*>(m); }
 
+// Replaces a loaded model's thread pool with one of n_threads (n <= 0: ThreadPool::default_threads()), resizing the
+// per-thread shortlist state as Model::load sizes it (model.cpp:59, 93-94); returns the pool's size. Lets one
+// prefilled cache be decoded at several thread counts.
+int ref_model_set_threads(void* mp, int n_threads) {
+    auto* m = static_cast<quanta::Model*>(mp);
+    m->pool_ = std::make_unique<quanta::ThreadPool>(n_threads);
+    if (m->head_q4_) {
+        m->heap_.resize(size_t(m->pool_->size()));
+        m->cand_.resize(size_t(m->pool_->size()));
+    }
+    return m->pool_->size();
+}
+
+// ThreadPool::default_threads() (threadpool.cpp:21-25): min(8, hardware threads / 2).
+int ref_default_threads() { return quanta::ThreadPool::default_threads(); }
+
 // Model::load's verdict on a file (model.cpp:10-106, model_file.cpp:104-218): 1 if it loads, else 0 with the
 // reference's error message copied into msg[cap].
 int ref_model_load_error(const char* path, char* msg, int cap) {

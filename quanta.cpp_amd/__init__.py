@@ -68,6 +68,9 @@ def sampler_params(temperature=0.7, top_k=20, top_p=0.8, min_p=0.0, repeat_penal
     return qh_sampler_params(temperature, top_k, top_p, min_p, repeat_penalty, repeat_window)
 
 
+STAGE_QKV, STAGE_ATTENTION, STAGE_O, STAGE_GATE_UP, STAGE_DOWN, STAGES_PER_LAYER = 0, 1, 2, 3, 4, 8
+STAGE_FINAL_NORM, STAGE_HEAD, STAGE_PICK = 1 << 20, (1 << 20) + 1, (1 << 20) + 2
+
 # Every symbol include/quanta_hip.h declares, in header order.
 EXPORTS = ("qh_last_error", "qh_version", "qh_init", "qh_quant_bytes", "qh_tensor_bytes", "qh_validate_tensor",
            "qh_malloc", "qh_free", "qh_memcpy_h2d", "qh_memcpy_d2h", "qh_memset", "qh_stream_sync",
@@ -75,7 +78,8 @@ EXPORTS = ("qh_last_error", "qh_version", "qh_init", "qh_quant_bytes", "qh_tenso
            "qh_quantize_q8", "qh_matvec_q", "qh_matmul_q", "qh_argmax_workspace_bytes", "qh_argmax",
            "qh_shortlist_workspace_bytes", "qh_shortlist_head", "qh_shortlist_head_noalloc",
            "qh_sampler_state", "qh_sample", "qh_decoder_create", "qh_decoder_destroy",
-           "qh_decoder_prefill", "qh_decoder_begin", "qh_decoder_step", "qh_decoder_views", "qh_decoder_set_query",
+           "qh_decoder_prefill", "qh_decoder_begin", "qh_decoder_step", "qh_decoder_views", "qh_decoder_step_timed",
+           "qh_decoder_set_query",
            "qh_decoder_set_sampler")
 
 
@@ -109,6 +113,7 @@ def _bind(lib):
         "qh_decoder_begin": ([vp, i32, vp, i32, vp], i32),
         "qh_decoder_step": ([vp, i32, vp], i32),
         "qh_decoder_views": ([vp, C.POINTER(qh_decoder_state)], i32),
+        "qh_decoder_step_timed": ([vp, i32, vp, vp, vp, i32, vp], i32),
         "qh_sampler_state": ([C.c_uint64], C.c_uint64),
         "qh_sample": ([vp, i32, vp, vp, vp, i32, C.POINTER(qh_sampler_params), vp, vp, vp], i32),
         "qh_decoder_set_query": ([vp, C.POINTER(qh_sampler_params)], i32),

@@ -10,6 +10,11 @@
 
 namespace qh {
 
+KernelTimer*& kernel_timer() {
+    thread_local KernelTimer* t = nullptr;
+    return t;
+}
+
 namespace {
 thread_local char g_error[512] = "";
 std::mutex g_init_mu;
@@ -108,6 +113,8 @@ int validate_head(const qh_tensor* head8, const qh_tensor* head4, const qh_tenso
     if (query->top_k < 1 || query->top_k > QH_HEAD_MAX_TOPK)
         return fail(QH_ERR_UNSUPPORTED, "%s: top_k %d outside [1, %d]", who, query->top_k, QH_HEAD_MAX_TOPK);
     if (query->n_must < 0 || (query->n_must > 0 && !query->must)) return fail(QH_ERR_ARG, "%s: bad must list", who);
+    if (!head_select_supported(V, D, query->top_k))
+        return fail(QH_ERR_UNSUPPORTED, "%s: %d rows with top_k %d exceed the seed selection", who, V, query->top_k);
     if (!out->logits || !out->coarse || !out->upper || !out->rows || !out->stats)
         return fail(QH_ERR_ARG, "%s: null output buffer", who);
     return QH_OK;
@@ -366,6 +373,9 @@ int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_t
             return fail(QH_ERR_SHAPE, "qh_decoder_create: bad shortlist head tensors");  // as model.cpp:49-58
     }
     if (int rc = qh_init_current()) return rc;
+    if (h4.data && !head_select_supported(hp->vocab_size, D, 1))
+        return fail(QH_ERR_UNSUPPORTED, "qh_decoder_create: a %d x %d shortlist head is beyond the seed selection",
+                    hp->vocab_size, D);
     Decoder* d = nullptr;
     if (int rc = decoder_create(hp, tensors, n_tensors, &d)) return rc;
     *out = reinterpret_cast<qh_decoder*>(d);
@@ -397,6 +407,15 @@ int qh_decoder_step(qh_decoder* d, int top_k, void* stream) {
     if (!d) return fail(QH_ERR_ARG, "qh_decoder_step: null decoder");
     if (top_k < 0 || top_k > QH_HEAD_MAX_TOPK) return fail(QH_ERR_UNSUPPORTED, "qh_decoder_step: top_k %d", top_k);
     return check_hip(decoder_step(reinterpret_cast<Decoder*>(d), top_k, as_stream(stream)), "qh_decoder_step");
+}
+
+int qh_decoder_step_timed(qh_decoder* d, int top_k, void* stream, float* us_host, int32_t* stage_host, int cap,
+                          int32_t* n_host) {
+    if (!d || !us_host || !stage_host || !n_host || cap <= 0) return fail(QH_ERR_ARG, "qh_decoder_step_timed: bad argument");
+    if (top_k < 0 || top_k > QH_HEAD_MAX_TOPK) return fail(QH_ERR_UNSUPPORTED, "qh_decoder_step_timed: top_k %d", top_k);
+    *n_host = 0;
+    return decoder_step_timed(reinterpret_cast<Decoder*>(d), top_k, as_stream(stream), us_host, stage_host, cap + 1,
+                              n_host);
 }
 
 int qh_decoder_views(qh_decoder* d, qh_decoder_state* v) {

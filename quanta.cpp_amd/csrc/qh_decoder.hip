@@ -1652,6 +1652,10 @@ struct Decoder {
     int32_t* top1_full = nullptr;
     bool fuse = true;  // fused decode kernels (QH_DECODER_FUSE=0 at creation selects one launch per operation)
     std::vector<void*> allocs;
+    // The stage the kernels launched since the previous mark belong to (qh_decoder_step_timed).
+    void mark(int id) const {
+        if (KernelTimer* t = kernel_timer()) t->mark(id);
+    }
 };
 
 namespace {
@@ -1722,7 +1726,7 @@ hipError_t plan_dispatch(int dtype, const GemvPlan& p, F&& f) {
 hipError_t embed(Decoder* d, const int32_t* tokens, int n, hipStream_t s) {
     const qh_tensor& emb = d->t[T_EMBED];
     by_row_slots(d->hp.dim, [&](auto r) {
-        hipLaunchKernelGGL((embed_norm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, tokens,
+        qh_launch((embed_norm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, tokens,
                            reinterpret_cast<const int8_t*>(quants(emb)),
                            reinterpret_cast<const uint16_t*>(quants(emb) + (size_t)emb.rows * emb.cols), d->hp.dim,
                            d->hp.vocab_size, d->x, lf(d, 0, L_ATTN_NORM), d->hp.norm_eps, d->qa, d->da, d->status);
@@ -1776,11 +1780,11 @@ hipError_t launch_qkv_norm(Decoder* d, int l, const GemvPlan& p, size_t lds, con
     return plan_dispatch(wq.dtype, p, [&](auto dt, auto u, auto) {
         by_row_slots(act.D, [&](auto r) {
             if (act.eq)
-                hipLaunchKernelGGL((gemv_qkv_norm_kernel<decltype(dt)::value, decltype(u)::value, decltype(r)::value,
+                qh_launch((gemv_qkv_norm_kernel<decltype(dt)::value, decltype(u)::value, decltype(r)::value,
                                                          true>),
                                    dim3(grid), dim3(256), lds, s, a, act, nb, T, nb_magic(nb));
             else
-                hipLaunchKernelGGL((gemv_qkv_norm_kernel<decltype(dt)::value, decltype(u)::value, decltype(r)::value,
+                qh_launch((gemv_qkv_norm_kernel<decltype(dt)::value, decltype(u)::value, decltype(r)::value,
                                                          false>),
                                    dim3(grid), dim3(256), lds, s, a, act, nb, T, nb_magic(nb));
         });
@@ -1796,20 +1800,20 @@ hipError_t residual(Decoder* d, const qh_tensor& W, const int8_t* xq, const floa
         const unsigned grid = (unsigned)((W.rows + T - 1) / T);
         const size_t lds = gemv_lds_bytes(W.cols, T, p.act_lds);
         return plan_dispatch(W.dtype, p, [&](auto dt, auto u, auto xl) {
-            hipLaunchKernelGGL((gemv_residual_kernel<decltype(dt)::value, decltype(u)::value, decltype(xl)::value>),
+            qh_launch((gemv_residual_kernel<decltype(dt)::value, decltype(u)::value, decltype(xl)::value>),
                                dim3(grid), dim3(256), lds, s, quants(W), scales(W), xq, xd, nb, W.rows, T,
                                nb_magic(nb), d->x);
         });
     }
     QH_TRY(launch_gemv(d->o, W, xq, xd, 0, W.rows, p, s));
-    hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((W.rows + 255) / 256)), dim3(256), 0, s, d->x, d->o,
+    qh_launch(residual_add_kernel, dim3((unsigned)((W.rows + 255) / 256)), dim3(256), 0, s, d->x, d->o,
                        W.rows);
     return hipGetLastError();
 }
 
 hipError_t norm_quant(Decoder* d, const float* w, float* normed, hipStream_t s) {
     by_row_slots(d->hp.dim, [&](auto r) {
-        hipLaunchKernelGGL((norm_quant_kernel<decltype(r)::value>), dim3(1), dim3(256), 0, s, d->x, w, d->hp.dim,
+        qh_launch((norm_quant_kernel<decltype(r)::value>), dim3(1), dim3(256), 0, s, d->x, w, d->hp.dim,
                            d->hp.norm_eps, d->qa, d->da, normed);
     });
     return hipGetLastError();
@@ -1826,10 +1830,10 @@ hipError_t gate_up(Decoder* d, int l, hipStream_t s) {
         by_row_slots(d->hp.dim, [&](auto r) {
             constexpr int R = decltype(r)::value;
             if (wg.dtype == kQ8)
-                hipLaunchKernelGGL((gemv_swiglu_norm_kernel<kQ8, 8, R>), dim3(grid), dim3(256), lds, s, quants(wg),
+                qh_launch((gemv_swiglu_norm_kernel<kQ8, 8, R>), dim3(grid), dim3(256), lds, s, quants(wg),
                                    scales(wg), quants(wu), scales(wu), act, nb, nb_magic(nb), d->qb, d->db);
             else
-                hipLaunchKernelGGL((gemv_swiglu_norm_kernel<kQ4, 8, R>), dim3(grid), dim3(256), lds, s, quants(wg),
+                qh_launch((gemv_swiglu_norm_kernel<kQ4, 8, R>), dim3(grid), dim3(256), lds, s, quants(wg),
                                    scales(wg), quants(wu), scales(wu), act, nb, nb_magic(nb), d->qb, d->db);
         });
         return hipGetLastError();
@@ -1838,7 +1842,7 @@ hipError_t gate_up(Decoder* d, int l, hipStream_t s) {
     QH_TRY(launch_gemv(d->g, wg, d->qa, d->da, 0, wg.rows, gemv_plan(wg.dtype, wg.cols, wg.rows), s));
     QH_TRY(launch_gemv(d->u, wu, d->qa, d->da, 0, wu.rows, gemv_plan(wu.dtype, wu.cols, wu.rows), s));
     const long nblk = wg.rows / QK;
-    hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g, d->u,
+    qh_launch(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g, d->u,
                        nblk, d->qb, d->db);
     return hipGetLastError();
 }
@@ -1849,16 +1853,16 @@ hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
     const size_t layer_v = (size_t)v_ctx(hp.ctx_len) * hp.n_kv_heads * hp.head_dim;
     const dim3 grid(hp.n_heads, n);
     if (n == 1 && hp.head_dim == 64 && d->fuse)  // decode: one 16-wave workgroup per head
-        hipLaunchKernelGGL((attention_decode_kernel<64>), dim3(hp.n_heads / hp.n_kv_heads, hp.n_kv_heads), dim3(1024), 0,
+        qh_launch((attention_decode_kernel<64>), dim3(hp.n_heads / hp.n_kv_heads, hp.n_kv_heads), dim3(1024), 0,
                            s, d->q, d->k, d->v, d->kc + l * layer_k, d->pos, hp.ctx_len, hp.n_heads / hp.n_kv_heads,
                            bias(d, l, L_BQ), bias(d, l, L_BK), hp.n_kv_heads, bias(d, l, L_BV), d->cs,
                            d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status);
     else if (hp.head_dim == 64)
-        hipLaunchKernelGGL((attention_kernel<64>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
+        qh_launch((attention_kernel<64>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                            bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
                            d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status);
     else
-        hipLaunchKernelGGL((attention_kernel<128>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
+        qh_launch((attention_kernel<128>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                            bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
                            d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status);
     return hipGetLastError();
@@ -1883,12 +1887,19 @@ hipError_t decode_layers(Decoder* d, hipStream_t s) {
             QH_TRY(launch_gemv(d->k, wk, d->qa, d->da, 0, wk.rows, gemv_plan(wk.dtype, wk.cols, wk.rows), s));
             QH_TRY(launch_gemv(d->v, wv, d->qa, d->da, 0, wv.rows, gemv_plan(wv.dtype, wv.cols, wv.rows), s));
         }
+        d->mark(l * QH_STAGES_PER_LAYER + QH_STAGE_QKV);
         QH_TRY(attention(d, l, 1, s));
+        d->mark(l * QH_STAGES_PER_LAYER + QH_STAGE_ATTENTION);
         QH_TRY(residual(d, lt(d, l, L_WO), d->qb, d->db, s));
+        d->mark(l * QH_STAGES_PER_LAYER + QH_STAGE_O);
         QH_TRY(gate_up(d, l, s));
+        d->mark(l * QH_STAGES_PER_LAYER + QH_STAGE_GATE_UP);
         QH_TRY(residual(d, lt(d, l, L_WD), d->qb, d->db, s));
+        d->mark(l * QH_STAGES_PER_LAYER + QH_STAGE_DOWN);
     }
-    return norm_quant(d, final_norm(d), d->hidden, s);
+    QH_TRY(norm_quant(d, final_norm(d), d->hidden, s));
+    d->mark(QH_STAGE_FINAL_NORM);
+    return hipSuccess;
 }
 
 // All layers for a chunk of n tokens whose embeddings are in d->x[0..n) and normed inputs in qa / da, positions
@@ -1899,7 +1910,7 @@ hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
     for (int l = 0; l < hp.n_layers; ++l) {
         if (l > 0) {
             by_row_slots(D, [&](auto r) {
-                hipLaunchKernelGGL((add_rmsnorm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, d->x,
+                qh_launch((add_rmsnorm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, d->x,
                                    d->o, lf(d, l, L_ATTN_NORM), D, hp.norm_eps, d->qa, d->da, nullptr);
             });
             QH_TRY(hipGetLastError());
@@ -1912,7 +1923,7 @@ hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
         const qh_tensor& wo = lt(d, l, L_WO);
         QH_TRY(launch_matmul(d->o, wo.rows, wo, d->qb, d->db, n, 0, wo.rows, s));
         by_row_slots(D, [&](auto r) {
-            hipLaunchKernelGGL((add_rmsnorm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, d->x, d->o,
+            qh_launch((add_rmsnorm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, d->x, d->o,
                                lf(d, l, L_FFN_NORM), D, hp.norm_eps, d->qa, d->da, nullptr);
         });
         QH_TRY(hipGetLastError());
@@ -1920,7 +1931,7 @@ hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
         QH_TRY(launch_matmul(d->g, wg.rows, wg, d->qa, d->da, n, 0, wg.rows, s));
         QH_TRY(launch_matmul(d->u, wu.rows, wu, d->qa, d->da, n, 0, wu.rows, s));
         const long nblk = (long)n * F / QK;
-        hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g,
+        qh_launch(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g,
                            d->u, nblk, d->qb, d->db);
         QH_TRY(hipGetLastError());
         QH_TRY(launch_matmul(d->o, wd.rows, wd, d->qb, d->db, n, 0, wd.rows, s));
@@ -2028,8 +2039,10 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
     A((void**)&d->rows, sizeof(int32_t) * (size_t)(V + 64));
     A((void**)&d->stats, sizeof(qh_head_stats));
     A((void**)&d->top1_full, 256);
-    d->head_ws_bytes = head_workspace_bytes(V, D, QH_HEAD_MAX_TOPK);
-    A(&d->head_ws, d->head_ws_bytes);
+    if (head4(d).data) {
+        d->head_ws_bytes = head_workspace_bytes(V, D, 1);  // the same for every top_k the selection holds
+        A(&d->head_ws, d->head_ws_bytes);
+    }
     d->am_ws_bytes = argmax_workspace_bytes(V);
     A(&d->am_ws, d->am_ws_bytes);
     if (e != hipSuccess) {
@@ -2067,15 +2080,15 @@ void decoder_destroy(Decoder* d) {
 hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, int top_k, hipStream_t s) {
     const qh_model_desc& hp = d->hp;
     const int D = hp.dim;
-    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, s, d->status, 0);
+    qh_launch(set_int_kernel, dim3(1), dim3(1), 0, s, d->status, 0);
     QH_TRY(hipGetLastError());
-    hipLaunchKernelGGL(history_append_kernel, dim3(1), dim3(256), 0, s, tokens, n, pos0 == 0 ? 1 : 0, d->hist,
+    qh_launch(history_append_kernel, dim3(1), dim3(256), 0, s, tokens, n, pos0 == 0 ? 1 : 0, d->hist,
                        d->hist_len, hp.ctx_len + 1);
     QH_TRY(hipGetLastError());
     int last = 0;
     for (int c0 = 0; c0 < n; c0 += kChunk) {
         const int m = n - c0 < kChunk ? n - c0 : kChunk;
-        hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + c0);
+        qh_launch(set_int_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + c0);
         QH_TRY(hipGetLastError());
         QH_TRY(embed(d, tokens + c0, m, s));
         QH_TRY(prefill_layers(d, m, s));
@@ -2083,13 +2096,13 @@ hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, i
     }
     // final residual add, norm and quantization of the last token only, then the head
     by_row_slots(D, [&](auto r) {
-        hipLaunchKernelGGL((add_rmsnorm_quant_kernel<decltype(r)::value>), dim3(1), dim3(256), 0, s,
+        qh_launch((add_rmsnorm_quant_kernel<decltype(r)::value>), dim3(1), dim3(256), 0, s,
                            d->x + (size_t)last * D, d->o + (size_t)last * D, final_norm(d), D, hp.norm_eps, d->qa,
                            d->da, d->hidden);
     });
     QH_TRY(hipGetLastError());
     QH_TRY(run_head(d, top_k, s));
-    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + n);
+    qh_launch(set_int_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + n);
     return hipGetLastError();
 }
 
@@ -2103,21 +2116,53 @@ hipError_t pick_and_advance(Decoder* d, int top_k, bool advance, hipStream_t s) 
                              d->sp, d->rng, d->sampled, s));
         pick.sampled = d->sampled;
     }
-    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, pick, token_feedback(d), advance ? 1 : 0);
+    qh_launch(advance_kernel, dim3(1), dim3(1), 0, s, pick, token_feedback(d), advance ? 1 : 0);
     return hipGetLastError();
 }
 
 hipError_t decoder_step(Decoder* d, int top_k, hipStream_t s) {
     QH_TRY(decode_layers(d, s));
-    if (!d->has_sampler && shortlist_on(d, top_k)) return run_head(d, top_k, s, true);  // greedy: fed back there
+    if (!d->has_sampler && shortlist_on(d, top_k)) {  // greedy: fed back in the head
+        QH_TRY(run_head(d, top_k, s, true));
+        d->mark(QH_STAGE_HEAD);
+        return hipSuccess;
+    }
     QH_TRY(run_head(d, top_k, s));
-    return pick_and_advance(d, top_k, true, s);
+    d->mark(QH_STAGE_HEAD);
+    QH_TRY(pick_and_advance(d, top_k, true, s));
+    d->mark(QH_STAGE_PICK);
+    return hipSuccess;
+}
+
+int decoder_step_timed(Decoder* d, int top_k, hipStream_t s, float* us, int32_t* stage, int cap, int32_t* n) {
+    KernelTimer t;
+    t.ev.assign(2 * (size_t)cap, nullptr);
+    int rc = QH_OK;
+    for (hipEvent_t& e : t.ev)
+        if (!rc) rc = check_hip(hipEventCreate(&e), "hipEventCreate");
+    if (!rc) {
+        kernel_timer() = &t;
+        const hipError_t e = decoder_step(d, top_k, s);
+        kernel_timer() = nullptr;
+        rc = check_hip(e, "qh_decoder_step_timed");
+    }
+    if (!rc) rc = check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+    if (!rc && t.n >= cap) rc = fail(QH_ERR_NOMEM, "qh_decoder_step_timed: the step launches more than %d kernels", cap - 1);
+    for (int i = 0; !rc && i < t.n; ++i) {
+        rc = check_hip(hipEventElapsedTime(&us[i], t.ev[2 * i], t.ev[2 * i + 1]), "hipEventElapsedTime");
+        us[i] *= 1e3f;
+        stage[i] = t.stage[i];
+    }
+    for (hipEvent_t e : t.ev)
+        if (e) (void)hipEventDestroy(e);
+    if (!rc) *n = t.n;
+    return rc;
 }
 
 hipError_t decoder_begin(Decoder* d, int top_k, int32_t* out, int out_cap, hipStream_t s) {
     d->out = out;
     d->out_cap = out_cap;
-    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, s, d->n_out, 0);
+    qh_launch(set_int_kernel, dim3(1), dim3(1), 0, s, d->n_out, 0);
     QH_TRY(hipGetLastError());
     return pick_and_advance(d, top_k, false, s);
 }

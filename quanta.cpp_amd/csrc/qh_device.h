@@ -20,6 +20,17 @@ constexpr int kQ4 = 3;
 // IEEE binary16 bits -> binary32 (exact for every input, subnormals included): v_cvt_f32_f16.
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
+// The f16 bits at p (2-byte aligned) through a 4-byte load of the aligned word holding them: 16-bit global loads cost
+// gfx950 far more than 32-bit ones (measured: eight per lane add about 1.8 us to a scattered row fetch against 0.2 us
+// as words). The word starts inside the array, so it stays inside the allocation's granule even where it reaches
+// 2 bytes past the array's last element.
+// The word's address is p stepped back by one element (not an integer cast), so the load keeps p's address space.
+__device__ __forceinline__ uint16_t load_f16_bits(const uint16_t* p) {
+    const int odd = (int)((reinterpret_cast<uintptr_t>(p) >> 1) & 1);
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(p - odd);
+    return (uint16_t)(odd ? (w >> 16) : w);
+}
+
 // Round half away from zero (lroundf semantics) of a value whose magnitude is below 2^23.
 __device__ __forceinline__ float round_half_away(float y) {
     const float t = __builtin_truncf(y);

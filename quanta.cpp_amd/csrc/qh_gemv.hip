@@ -35,7 +35,7 @@ hipError_t launch_quantize_q8(const float* x, int n_tok, int n, int8_t* q, float
     const long total = (long)n_tok * (n / QK);
     const long threads = total * QK;
     const unsigned grid = (unsigned)((threads + 255) / 256);
-    hipLaunchKernelGGL(quantize_q8_kernel, dim3(grid), dim3(256), 0, s, x, total, q, d);
+    qh_launch(quantize_q8_kernel, dim3(grid), dim3(256), 0, s, x, total, q, d);
     return hipGetLastError();
 }
 
@@ -268,7 +268,7 @@ static void launch_gemv_t(float* out, const qh_tensor& W, const int8_t* xq, cons
     const uint32_t magic = nb == 1 ? 0u : (uint32_t)((0x100000000ull + (uint64_t)nb - 1) / (uint64_t)nb);
     const unsigned grid = (unsigned)((r1 - r0 + tile_rows - 1) / tile_rows);
     const size_t lds = gemv_lds_bytes(W.cols, tile_rows, XL);
-    hipLaunchKernelGGL((gemv_kernel<DT, U, XL>), dim3(grid), dim3(256), lds, s, out, wq, ws, xq, xd, nb, r0, r1,
+    qh_launch((gemv_kernel<DT, U, XL>), dim3(grid), dim3(256), lds, s, out, wq, ws, xq, xd, nb, r0, r1,
                        tile_rows, magic);
 }
 
@@ -287,7 +287,7 @@ static void launch_gemv_stream_t(float* out, const qh_tensor& W, const int8_t* x
     const int k = (per + tile_rows - 1) / tile_rows;
     tile_rows = (per + k - 1) / k;
     const size_t lds = gemv_stream_lds_bytes(W.cols, tile_rows);
-    hipLaunchKernelGGL((gemv_stream_kernel<DT, U>), dim3((unsigned)g), dim3(256), lds, s, out, wq, ws, xq, xd, nb, r0,
+    qh_launch((gemv_stream_kernel<DT, U>), dim3((unsigned)g), dim3(256), lds, s, out, wq, ws, xq, xd, nb, r0,
                        r1, tile_rows, magic);
 }
 
@@ -372,10 +372,10 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(const uint
 hipError_t launch_argmax(const float* logits, int n, int32_t* index, void* ws, hipStream_t s) {
     const int parts = argmax_parts(n);
     uint64_t* part = static_cast<uint64_t*>(ws);
-    hipLaunchKernelGGL(argmax_part_kernel, dim3((unsigned)parts), dim3(kArgmaxThreads), 0, s, logits, n, part);
+    qh_launch(argmax_part_kernel, dim3((unsigned)parts), dim3(kArgmaxThreads), 0, s, logits, n, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, part, parts, index);
+    qh_launch(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, part, parts, index);
     return hipGetLastError();
 }
 

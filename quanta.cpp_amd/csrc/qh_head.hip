@@ -1,50 +1,68 @@
-// Exact Shortlist Head (reference engine/src/model.cpp:240-334) on gfx950, three launches:
+// Exact Shortlist Head (reference engine/src/model.cpp:240-334) on gfx950, two launches:
 //
-//  1. screen    persistent streaming grid over the vocabulary rows (even row split per workgroup, tiles of up to 64
+//  1. screen    persistent streaming grid over the vocabulary rows (an even row share per workgroup, tiles of up to 64
 //               rows, the next tile's Q4_0 chunks and f16 block errors in flight while the current tile is reduced).
 //               Per row: the 4-bit score chain (same block products and association as the decode GEMV), the bound
 //               chain over the f16 block errors and the activation's block norms
-//               (bound = fma(sum_b fma(err_b, xnorm_b), 1.001f, 1e-5f)), upper = coarse + bound, logits = -inf.
-//               Wave 0 owns one row per lane and keeps the workgroup's best top_k+9 eligible keys (score, then
-//               lower row first) sorted across its lanes, inserting only keys above the current cut.
-//  2. seeds     one workgroup: merges the per-workgroup lists (held in registers) into the global top_k+8 seeds
-//               plus one more key to detect a tie at the cut, rescores the seeds exactly with the Q8_0 row dot,
-//               tau = k-th best exact seed; lists the must ids' first occurrences (valid, not seeds) in query order
-//               after the seeds: every occurrence proposes its index with an atomic minimum per row, then a block
-//               scan compacts the winners in order.
-//  3. cand      one workgroup per 256 rows: candidates {r < n_valid, unmarked, upper[r] >= tau} compacted with a
-//               ballot scan, appended to the row list, rescored exactly in the same workgroup; the must rows are
-//               split over the workgroups and rescored too; the greedy argmax key is folded in with a 64-bit atomic
-//               max; the last workgroup to finish writes the stats record.
+//               (bound = fma(sum_b fma(err_b, xnorm_b), 1.001f, 1e-5f)), upper = coarse + bound, logits = -inf, and
+//               the row's mark (1: a valid must id, else 0). Each share publishes its kTops best eligible keys
+//               (score, then lower row first; must ids and rows >= n_valid are not eligible).
+//  2. select    one workgroup per band of at most 1024 rows. Every workgroup first finds the seeds itself, from the
+//               published keys: the top_k+9 best keys overall lie in the top_k+9 shares with the best maxima and are
+//               at or above the (top_k+9)-th best maximum T, and a share's published keys hold all of its keys >= T
+//               unless its last published key is >= T too (then its rows are read again). The top_k+8 best are the
+//               seeds (one more key detects a tie at the cut), rescored exactly; tau = k-th best exact seed. Then
+//               the band's candidates {unmarked, not a seed, upper >= tau} and must rows are rescored exactly, the
+//               candidates appended to the row list, and the greedy argmax key folded in with 64-bit atomic maxima.
+//               The last workgroup to finish lists the must ids' first occurrences in query order after the
+//               candidates (every occurrence proposed its index with an atomic minimum per row) and writes the stats.
 //
 // Exact rows use the same block products and serial chain as the decode GEMV, so each rescored logit is
-// bit-identical to the full Q8_0 head. The mark array (1 byte per row) lives in the workspace: screen clears its
-// rows, seeds sets 2 (seed) and 3 (must), cand skips every marked row. With must ids, screen also resets its rows of
-// the first-occurrence array (one int per row) that seeds uses.
+// bit-identical to the full Q8_0 head. Workspace: the marks (1 byte per row), the first-occurrence array (one int per
+// row, reset by the screen when the query has must ids), the published keys and the control words.
 #include "qh_device.h"
 #include "qh_internal.h"
 
 namespace qh {
 
+// Timeline stamps for phase measurements, compiled in only with -DQH_TIMELINE: thread 0 of every workgroup records the
+// constant-rate real-time clock (comparable across compute units) at each stamp of the head kernels
+// (qh_timeline_head_read copies them out: [kernel][workgroup < 1024][stamp < 4]).
+#if defined(QH_TIMELINE)
+__device__ uint64_t qh_tl_head[3][1024][4];
+#define QH_HSTAMP(k, i)                                                                                   \
+    do {                                                                                                  \
+        if (threadIdx.x == 0 && blockIdx.x < 1024) qh_tl_head[k][blockIdx.x][i] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+extern "C" int qh_timeline_head_read(uint64_t* host) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(qh_tl_head), sizeof(qh_tl_head));
+}
+#else
+#define QH_HSTAMP(k, i) \
+    do {                \
+    } while (0)
+#endif
+
 namespace {
 
+// Control words of one call, reset by the screen's first workgroup for the select kernel that follows: the candidate
+// count (each workgroup's base in the row list) and two-level completion counters. Workgroup b counts into group
+// b % kDoneGroups and folds its best key into that group's key (one 128-byte line per group after the 256 bytes of
+// HeadCtrl); each group's last workgroup counts into HeadCtrl::done. Atomics on one address are performed one at a
+// time, so 16 groups finish sooner than one counter.
 struct HeadCtrl {
-    unsigned long long argmax_key;
     unsigned int n_cand;
     unsigned int done;
-    float tau;
-    int n_seeds;
-    int n_must;
-    int seed_tie;
 };
-// Completion counters of the candidate workgroups, two levels: workgroup b counts into group b % kDoneGroups (one
-// 128-byte line each, after the 256 bytes of HeadCtrl), each group's last workgroup into HeadCtrl::done. Atomics on
-// one address are performed one at a time, so 16 groups of 16 finish sooner than one counter of 256.
 constexpr int kDoneGroups = 16;
-constexpr int kDoneStride = 32;  // unsigned ints per group counter
-static_assert(sizeof(HeadCtrl) <= 256, "the group counters follow HeadCtrl's 256 bytes");
-__device__ __forceinline__ unsigned* group_done(HeadCtrl* ctrl) {
-    return reinterpret_cast<unsigned*>(reinterpret_cast<uint8_t*>(ctrl) + 256);
+constexpr int kDoneLine = 128;  // bytes per group: the count, then the group's best key at byte 8
+constexpr size_t kCtrlBytes = 256 + (size_t)kDoneGroups * kDoneLine;
+static_assert(sizeof(HeadCtrl) <= 256, "the group lines follow HeadCtrl's 256 bytes");
+__device__ __forceinline__ unsigned* group_done(HeadCtrl* ctrl, int g) {
+    return reinterpret_cast<unsigned*>(reinterpret_cast<uint8_t*>(ctrl) + 256 + g * kDoneLine);
+}
+__device__ __forceinline__ unsigned long long* group_key(HeadCtrl* ctrl, int g) {
+    return reinterpret_cast<unsigned long long*>(reinterpret_cast<uint8_t*>(ctrl) + 256 + g * kDoneLine + 8);
 }
 
 constexpr int kMaxMust = 1 << 22;  // must ids per query (a history window); the screen scans them per tile
@@ -53,12 +71,16 @@ constexpr int kScreenThreads = 256;
 constexpr int kScreenU = 5;         // 16-byte weight chunks per thread per tile (two sets fit 128 VGPRs)
 constexpr int kScreenMaxRows = 64;  // rows per tile: one per lane of wave 0
 constexpr int kScreenErrU = (kScreenU + 1) / 2;  // 4-byte error words per thread per tile (tile * nb / 2 <= 128 U)
-constexpr int kScreenMaxShare = 1024;  // rows per screen workgroup: their keys sit in LDS until the final selection
-constexpr int kSeedThreads = 1024;
-constexpr int kSeedMaxPool = 2048;     // keys that survive the seed threshold, held in LDS
-constexpr int kSeedKeysPerThread = 32; // fallback when more survive: every partial key in registers
-constexpr int kCandThreads = 256;
-constexpr int kCandRowsPerThread = 4;
+constexpr int kScreenMaxShare = 1024;  // rows per screen workgroup at most (the grid grows for larger vocabularies)
+constexpr int kTops = 4;               // best keys each screen share publishes
+static_assert(kTops == 4, "a share's keys are written as two 16-byte stores");
+constexpr int kSelThreads = 256;
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kSelShares = 4;   // screen shares per select thread: at most kSelShares * kSelThreads shares
+constexpr int kSelRows = 4;     // rows per select thread in the candidate scan
+constexpr int kPoolCap = 1024;  // keys an LDS selection pool holds
+constexpr int kMaxKeep = QH_HEAD_MAX_TOPK + 9;
+static_assert(kMaxKeep <= 64, "the seeds and the key after them fit one wave, one per lane");
 
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
@@ -70,62 +92,48 @@ int screen_tile_rows(int nb) {
     return t < 2 ? 2 : t;
 }
 
-int screen_grid(int V, int tile) {
-    int g = 4 * device_cus();
-    const int min_g = (V + kScreenMaxShare - 3) / (kScreenMaxShare - 2);  // shares are rounded to even rows
-    g = g > min_g ? g : min_g;
-    const int tiles = (V + tile - 1) / tile;
-    return g < tiles ? g : tiles;
+// Screen shares: four per compute unit, an even number of rows (whole 4-byte error words), at least one tile and at
+// most kScreenMaxShare rows each; share p holds rows [p * share, min((p + 1) * share, V)).
+struct ScreenShape {
+    int tile, share, grid;
+};
+ScreenShape screen_shape(int V, int nb) {
+    ScreenShape sh;
+    sh.tile = screen_tile_rows(nb);
+    const int g = 4 * device_cus();
+    int share = ((V + g - 1) / g + 1) & ~1;
+    share = share > sh.tile ? share : sh.tile;
+    share = share < kScreenMaxShare ? share : kScreenMaxShare;
+    sh.share = share;
+    sh.grid = (V + share - 1) / share;
+    return sh;
 }
 
-int cand_grid(int nv) {
-    int g = device_cus();
-    const int min_g = (nv + kCandRowsPerThread * kCandThreads - 1) / (kCandRowsPerThread * kCandThreads);
-    g = g > min_g ? g : min_g;
-    const int chunks = (nv + kCandThreads - 1) / kCandThreads;
-    return g < chunks ? g : chunks;
+// Select bands: one workgroup per compute unit, 256 to kSelRows * kSelThreads rows each, a multiple of kSelRows;
+// workgroup b scans rows [b * band, min((b + 1) * band, n_valid)). Fewer workgroups queue fewer atomics on the
+// candidate count and repeat the seed selection fewer times.
+int select_band(int nv) {
+    static_assert(kSelRows == 4, "a thread's marks are one 4-byte word");
+    const int g = device_cus();
+    int band = ((nv + g - 1) / g + kSelRows - 1) / kSelRows * kSelRows;
+    band = band > kSelThreads ? band : kSelThreads;
+    return band < kSelRows * kSelThreads ? band : kSelRows * kSelThreads;
 }
 
+// Workspace: marks [V], first occurrences [V], published keys [shares][kTops], control words.
 struct WsLayout {
-    size_t mark, first, seedpart, ctrl, total;
+    size_t mark, first, tops, ctrl, total;
 };
 
-WsLayout ws_layout(int V, int D, int top_k) {
-    const int nb = D / QK;
-    const int parts = screen_grid(V, screen_tile_rows(nb));
-    const int keep = top_k + 9;
+WsLayout ws_layout(int V, int D) {
+    const int parts = screen_shape(V, D / QK).grid;
     WsLayout l;
     l.mark = 0;
     l.first = align256((size_t)V);
-    l.seedpart = l.first + align256((size_t)V * 4);
-    l.ctrl = l.seedpart + align256((size_t)parts * keep * sizeof(uint64_t));
-    l.total = l.ctrl + 256 + (size_t)kDoneGroups * kDoneStride * 4;
+    l.tops = l.first + align256((size_t)V * 4);
+    l.ctrl = l.tops + align256((size_t)parts * kTops * sizeof(uint64_t));
+    l.total = l.ctrl + kCtrlBytes;
     return l;
-}
-
-// Block products of one Q8_0 row for the calling wave: lane pairs cover 32-byte blocks; p[b] receives
-// float(s_b) * f16(scale_b). Every lane of the wave must call it (DPP inside); `active` masks the work.
-__device__ void wave_row_products_q8(const uint8_t* __restrict__ w8, const uint16_t* __restrict__ s8, int row, int nb,
-                                     const int8_t* __restrict__ xq, float* p, bool active) {
-    const int lane = (int)threadIdx.x & 63;
-    const uint8_t* wr = w8 + (size_t)row * nb * QK;
-    const int nch = 2 * nb;
-    for (int c0 = 0; c0 < nch; c0 += 64) {
-        const int c = c0 + lane;
-        const bool ok = active && c < nch;
-        const uint4 w = ok ? load16(wr + (size_t)c * 16) : make_uint4(0u, 0u, 0u, 0u);
-        const int b = min(c >> 1, nb - 1);
-        const uint4 xv = load16(xq + b * QK + (c & 1) * 16);
-        int s = dot16_i8(w, xv);
-        s += swap_pair(s);
-        if (ok && !(c & 1)) p[b] = (float)s * f16_to_f32(s8[(size_t)row * nb + b]);
-    }
-}
-
-__device__ float chain(const float* p, const float* __restrict__ xd, int nb) {
-    float acc = 0.0f;
-    for (int b = 0; b < nb; ++b) acc = __builtin_fmaf(p[b], xd[b], acc);
-    return acc;
 }
 
 // Register set of one screen tile: the Q4_0 chunks with their block scales, and the f16 error words.
@@ -144,7 +152,7 @@ struct ScreenRegs {
         for (int j = 0; j < kScreenU; ++j) {
             const int c = min(j * kScreenThreads + tid, nch - 1);
             w[j] = load16(base + (size_t)c * 16);
-            sc[j] = sbase[c];
+            sc[j] = load_f16_bits(sbase + c);
         }
         // nb is even, so a tile's errors are nrows * nb / 2 whole 4-byte words starting 4-byte aligned.
         const int n32 = nrows * nb / 2;
@@ -183,38 +191,232 @@ struct ScreenRegs {
         }
     }
 };
+}  // namespace
 
-// Ranks within a wave: a[s] holds key number s*64 + lane of n keys (n <= 64*NS, missing keys are 0); rank[s]
-// receives how many of the n keys are larger than a[s]. Keys are broadcast lane by lane through scalar registers
-// (v_readlane), so every lane reads different LDS words beforehand and nothing serialises on one address.
-// Every lane of the wave must call it with the same n.
-template <int NS>
-__device__ __forceinline__ void wave_rank(const uint64_t (&a)[NS], int n, int (&rank)[NS]) {
+namespace {
+
+
+// Workgroup state of block_kth_threshold.
+struct RadixShared {
+    uint32_t hist[256];
+    int digit, need, count;
+};
+
+// A threshold for the k largest (k >= 1) of the keys the workgroup's NT threads enumerate (for_each(visit) calls
+// visit(key) for each of the thread's keys; 0 = no key; nonzero keys unique): exactly min(k, number of nonzero keys)
+// nonzero keys are >= the value returned. MSB-first radix select over 8-bit digits with a 256-bin LDS histogram, one
+// pass (one enumeration) per digit, stopping as soon as the digit's bin holds exactly the keys still needed. Every
+// thread of the workgroup calls it (barriers inside); the result is uniform.
+template <int NT, typename ForEach>
+__device__ uint64_t block_kth_threshold(ForEach for_each, int k, RadixShared& sh) {
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint64_t prefix = 0;  // the digits chosen so far
+    int need = k;         // keys still to take among those with that prefix, largest first
+    for (int shift = 56;; shift -= 8) {
+        for (int i = tid; i < 256; i += NT) sh.hist[i] = 0u;
+        __syncthreads();
+        const uint64_t hi = shift == 56 ? 0ull : (~0ull << (shift + 8));
+        for_each([&](uint64_t v) {
+            if (v != 0 && (v & hi) == prefix) atomicAdd(&sh.hist[(uint32_t)(v >> shift) & 255u], 1u);
+        });
+        __syncthreads();
+        if (wave == 0) {  // lane l counts bins 255 - 4l .. 252 - 4l, so the scan over lanes runs from the top digit
+            uint32_t c[4], tot = 0;
 #pragma unroll
-    for (int t = 0; t < NS; ++t) rank[t] = 0;
+            for (int q = 0; q < 4; ++q) {
+                c[q] = sh.hist[255 - 4 * lane - q];
+                tot += c[q];
+            }
+            uint32_t incl = tot;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        if (s * 64 >= n) break;
-        const int lo = (int)(uint32_t)a[s], hi = (int)(uint32_t)(a[s] >> 32);
-#pragma unroll 16
-        for (int j = 0; j < 64; ++j) {
-            const uint64_t kj = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi, j) << 32) |
-                                (uint64_t)(uint32_t)__builtin_amdgcn_readlane(lo, j);
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t o = (uint32_t)__shfl_up((int)incl, off, 64);
+                incl += lane >= off ? o : 0u;
+            }
+            const uint32_t excl = incl - tot;
+            if (excl < (uint32_t)need && (uint32_t)need <= incl) {
+                uint32_t above = excl;
+                int d = -1, cnt = 0;
 #pragma unroll
-            for (int t = 0; t < NS; ++t) rank[t] += kj > a[t] ? 1 : 0;
+                for (int q = 0; q < 4; ++q) {
+                    if (d < 0) {
+                        if (above + c[q] >= (uint32_t)need) {
+                            d = 255 - 4 * lane - q;
+                            cnt = (int)c[q];
+                        } else {
+                            above += c[q];
+                        }
+                    }
+                }
+                sh.digit = d;
+                sh.need = need - (int)above;
+                sh.count = cnt;
+            }
+            if (lane == 63 && incl < (uint32_t)need) sh.digit = -1;  // fewer keys than k (first pass only)
         }
+        __syncthreads();
+        const int d = sh.digit, cnt = sh.count, nd = sh.need;
+        __syncthreads();  // everyone has read sh before the next pass clears it
+        if (d < 0) return 1ull;  // every nonzero key is in
+        prefix |= (uint64_t)d << shift;
+        need = nd;
+        if (cnt == need || shift == 0) return prefix;  // the digit's bin holds exactly the keys still needed
     }
+}
+
+// Wave-aggregated append to an LDS list: the lanes with `pred` take consecutive slots from *counter, one LDS atomic
+// per wave. Every lane of the wave calls it; returns the lane's slot, or -1 without pred.
+__device__ __forceinline__ int wave_append(bool pred, int* counter) {
+    const uint64_t b = __ballot(pred);
+    if (b == 0) return -1;
+    const int lane = (int)threadIdx.x & 63;
+    const int leader = __ffsll((unsigned long long)b) - 1;
+    int base = 0;
+    if (lane == leader) base = atomicAdd(counter, __popcll(b));
+    base = __shfl(base, leader, 64);
+    return pred ? base + __popcll(b & ((1ull << lane) - 1ull)) : -1;
+}
+
+// wave_append for N predicates per lane at once: slot[j] receives the position of lane's value j (or -1 without
+// pred[j]); one LDS atomic per wave. Every lane of the wave calls it.
+template <int N>
+__device__ __forceinline__ void wave_append_n(const bool (&pred)[N], int* counter, int (&slot)[N]) {
+    const int lane = (int)threadIdx.x & 63;
+    uint64_t m[N];
+    int tot = 0;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        m[j] = __ballot(pred[j]);
+        tot += __popcll(m[j]);
+    }
+    int base = 0;
+    if (tot != 0) {  // uniform
+        if (lane == 0) base = atomicAdd(counter, tot);
+        base = __builtin_amdgcn_readfirstlane(base);
+    }
+    const uint64_t below = (1ull << lane) - 1ull;
+    int off = base;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        slot[j] = pred[j] ? off + __popcll(m[j] & below) : -1;
+        off += __popcll(m[j]);
+    }
+}
+
+// Sum over each group of 4 lanes (DPP quad permutations; every lane active).
+__device__ __forceinline__ int quad_sum(int v) {
+    v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // lanes 1,0,3,2
+    v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);  // lanes 2,3,0,1
+    return v;
+}
+
+// The rank of every entry of an LDS list of np keys (how many entries are larger), four threads per entry: f(i, rank)
+// runs once per entry. Every thread of the workgroup calls it with the same np.
+template <typename F>
+__device__ __forceinline__ void list_ranks(const uint64_t* a, int np, F f) {
+    const int tid = (int)threadIdx.x, part = tid & 3;
+    for (int i0 = 0; i0 < np; i0 += kSelThreads / 4) {
+        const int i = i0 + (tid >> 2);
+        const uint64_t mine = i < np ? a[i] : ~0ull;
+        int rank = 0;
+#pragma unroll 4
+        for (int j = part; j < np; j += 4) rank += a[j] > mine ? 1 : 0;
+        rank = quad_sum(rank);
+        if (i < np && part == 0) f(i, rank);
+    }
+}
+
+// A list of screen shares whose rows are read again, as one range of n * share indexes: index i is row
+// p[i / share] * share + i % share (rows >= V past the head's last share are no rows); `below` is the share's last
+// published key (keys at or above it were published).
+struct ShareRows {
+    int n;
+    int p[kMaxKeep];
+    uint64_t below[kMaxKeep];
+};
+
+// Exact Q8_0 logits of the rows of two LDS lists, a[0, na) then b[0, nb_), for the activation staged in LDS (codes xs
+// [nb * 32], scales xds [nb]); na and nb_ are uniform across the workgroup. Passes of 32 rows: each row's 16-byte
+// chunks are loaded by a group of 8 lanes with every load of a pass in flight at once, block products go to LDS prod
+// [32][nb] (lane pairs cover a 32-byte block), then one lane per row runs the reference chain acc = fma(p_b, dx_b,
+// acc) in block order (the decode GEMV's association, so each logit is bit-identical to the full head's) and writes
+// it to out[i] (LDS, by list index) when to_out is set, else to logits[row]. Every thread of the workgroup calls it
+// (barriers inside). Returns, in each row's chain lane, the best key of the rows it scored (0 elsewhere).
+constexpr int kRescoreLanes = 8, kRescoreRows = kSelThreads / kRescoreLanes;
+__device__ uint64_t rescore_lists(const int* a, int na, const int* b, int nb_, const uint8_t* __restrict__ w8,
+                                  const uint16_t* __restrict__ s8, const int8_t* xs, const float* xds, int nb,
+                                  float* prod, float* out, bool to_out, float* __restrict__ logits) {
+    constexpr int kPer = 8;  // chunks per lane per batch: one batch for rows of up to 1024 columns
+    const int tid = (int)threadIdx.x, g = tid / kRescoreLanes, j = tid % kRescoreLanes;
+    const int nch = 2 * nb, cnt = na + nb_;
+    uint64_t kbest = 0;
+    for (int p0 = 0; p0 < cnt; p0 += kRescoreRows) {
+        const int i = p0 + g;
+        const bool act = i < cnt;
+        const int r = !act ? 0 : i < na ? a[i] : b[i - na];
+        const uint8_t* wr = w8 + (size_t)r * nb * QK;
+        const uint16_t* sr = s8 + (size_t)r * nb;
+        for (int c0 = 0; c0 < nch; c0 += kRescoreLanes * kPer) {  // uniform
+            uint4 w[kPer];
+            uint16_t sc[kPer];
+#pragma unroll
+            for (int c = 0; c < kPer; ++c) {  // unconditional (clamped) loads: all in flight before the first wait
+                const int ch = min(c0 + j + kRescoreLanes * c, nch - 1);
+                w[c] = load16(wr + (size_t)ch * 16);
+                sc[c] = load_f16_bits(sr + (ch >> 1));
+            }
+            float scf[kPer];
+#pragma unroll
+            for (int c = 0; c < kPer; ++c) {
+                // Used here, outside the store's branch: otherwise the compiler sinks each scale load into that
+                // branch and waits for it there, one round trip per chunk.
+                scf[c] = f16_to_f32(sc[c]);
+                asm volatile("" : "+v"(scf[c]));
+            }
+#pragma unroll
+            for (int c = 0; c < kPer; ++c) {
+                const int ch = c0 + j + kRescoreLanes * c;
+                const int blk = min(ch >> 1, nb - 1);
+                const uint4 xv = *reinterpret_cast<const uint4*>(xs + blk * QK + (ch & 1) * 16);
+                int sdot = dot16_i8(w[c], xv);
+                sdot += swap_pair(sdot);
+                if (act && ch < nch && !(ch & 1)) prod[g * nb + blk] = (float)sdot * scf[c];
+            }
+        }
+        __syncthreads();
+        if (to_out && p0 == 0) QH_HSTAMP(2, 1);
+        if (act && j == 0) {
+            float acc = 0.0f;  // nb is even: pairs of operands, reads issued ahead of the serial chain
+            const float2* pp = reinterpret_cast<const float2*>(prod + g * nb);
+            const float2* xp = reinterpret_cast<const float2*>(xds);
+#pragma unroll 8
+            for (int h = 0; h < nb / 2; ++h) {
+                const float2 pv = pp[h], xv2 = xp[h];
+                acc = __builtin_fmaf(pv.x, xv2.x, acc);
+                acc = __builtin_fmaf(pv.y, xv2.y, acc);
+            }
+            if (to_out)
+                out[i] = acc;
+            else
+                logits[r] = acc;
+            const uint64_t kk = score_key(acc, r);
+            kbest = kk > kbest ? kk : kbest;
+        }
+        __syncthreads();
+        if (to_out && p0 == 0) QH_HSTAMP(2, 2);
+    }
+    return kbest;
 }
 
 }  // namespace
 
 __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void head_screen_kernel(
     const uint8_t* __restrict__ w4, const uint16_t* __restrict__ s4, const uint32_t* __restrict__ e32,
-    const int8_t* __restrict__ xq, const float* __restrict__ xd, int V, int nb, int nv, HeadMust mq, int tile,
+    const int8_t* __restrict__ xq, const float* __restrict__ xd, int V, int nb, int nv, HeadMust mq, int tile, int share,
     uint32_t nb_magic, float* __restrict__ coarse, float* __restrict__ upper, float* __restrict__ logits,
-    uint8_t* __restrict__ mark, int32_t* __restrict__ firsts, uint64_t* __restrict__ seedpart, int n_keep,
-    int share_cap) {
+    uint8_t* __restrict__ mark, int32_t* __restrict__ firsts, uint64_t* __restrict__ tops, HeadCtrl* __restrict__ ctrl) {
     extern __shared__ __align__(16) float smem[];
+    QH_HSTAMP(0, 0);
     // Padded chain rows (chain_lds_pipe): zp zeros, then the nb operands.
     const int L = chain_len32(nb), zp = L - nb, ps = chain_stride32(nb);
     float* xdsp = smem;                                  // [L] activation scales
@@ -224,47 +426,72 @@ __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(
     float* errf0 = prod1 + (size_t)tile * ps;            // [tile][ps] block errors, two buffers
     float* errf1 = errf0 + (size_t)tile * ps;
     float* bsh = errf1 + (size_t)tile * ps + kChainPipePad;  // [2][64] bounds of a tile (wave 1 -> wave 0)
-    uint64_t* wkeys = reinterpret_cast<uint64_t*>(bsh + 128);                   // [share_cap]
-    uint8_t* mflag = reinterpret_cast<uint8_t*>(wkeys + share_cap);             // [2][tile]
-    int8_t* xs = reinterpret_cast<int8_t*>(mflag + ((2 * (size_t)tile + 15) & ~size_t(15)));  // [nb * 32]
-    uint64_t* lvl2 = reinterpret_cast<uint64_t*>(prod0);  // [4 * 64] after the tile loop
+    uint8_t* mshare = reinterpret_cast<uint8_t*>(bsh + 128);                    // [kScreenMaxShare] must flags
+    int8_t* xs = reinterpret_cast<int8_t*>(mshare + kScreenMaxShare);            // [nb * 32]
     float* xds = xdsp + zp;
     float* xnorm = xnormp + zp;
-    __shared__ int n_elig;
 
     const int tid = (int)threadIdx.x;
+    if (blockIdx.x == 0 && tid < kDoneGroups) {  // the select kernel's counters, which it cannot reset itself
+        *group_done(ctrl, tid) = 0u;
+        *group_key(ctrl, tid) = 0ull;
+        if (tid == 0) {
+            ctrl->n_cand = 0u;
+            ctrl->done = 0u;
+        }
+    }
     const int32_t* must;
     int n_must;
     must_span(mq, must, n_must);
-    const int ra = (int)((long)blockIdx.x * V / gridDim.x) & ~1;  // even, so error words stay 4-byte aligned
-    const int rb = blockIdx.x + 1 == gridDim.x ? V : (int)((long)(blockIdx.x + 1) * V / gridDim.x) & ~1;
-    if (ra >= rb) {  // uniform per workgroup: an empty share still publishes an empty list
-        if (tid < n_keep) seedpart[(size_t)blockIdx.x * n_keep + tid] = 0ull;
-        return;
-    }
+    const int ra = (int)blockIdx.x * share, rb = min(ra + share, V);  // even ra: error words stay 4-byte aligned
 
+    // The activation first, then the first tile: loads return in order, so the block norms below wait only for the
+    // activation while the tile is in flight.
+    const int cols = nb * QK;
+    const int nx = cols / 16;
+    uint4 xv[kMaxHeadCols / 16 / kScreenThreads];
+    float xdv = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxHeadCols / 16 / kScreenThreads; ++j)
+        if (tid + j * kScreenThreads < nx) xv[j] = load16(xq + (tid + j * kScreenThreads) * 16);
+    if (tid < nb) xdv = xd[tid];
     ScreenRegs A, B;
     A.load(w4, s4, e32, ra, min(tile, rb - ra), nb);
+    for (int i = 4 * tid; i < share; i += 4 * kScreenThreads) *reinterpret_cast<uint32_t*>(mshare + i) = 0u;
     zero_chain_prefix(xdsp, prod0, nb, 2 * tile);   // both product buffers
     zero_chain_prefix(xnormp, errf0, nb, 2 * tile);  // both error buffers
-    const int cols = nb * QK;
-    for (int i = tid; i < cols / 16; i += kScreenThreads) reinterpret_cast<uint4*>(xs)[i] = load16(xq + i * 16);
-    for (int i = tid; i < nb; i += kScreenThreads) xds[i] = xd[i];
+#pragma unroll
+    for (int j = 0; j < kMaxHeadCols / 16 / kScreenThreads; ++j)
+        if (tid + j * kScreenThreads < nx) reinterpret_cast<uint4*>(xs)[tid + j * kScreenThreads] = xv[j];
+    if (tid < nb) xds[tid] = xdv;
     __syncthreads();
-    // xnorm_b = d_b * sqrt(sum q^2) (model.cpp:247-251); the sum is an exact integer in f32.
+    // xnorm_b = d_b * sqrt(sum q^2) (model.cpp:247-251): every partial sum is an integer below 2^24, so the reference's
+    // float accumulation is exact and equals this integer dot.
     for (int b = tid; b < nb; b += kScreenThreads) {
-        float ss = 0.0f;
-        for (int i = 0; i < QK; ++i) {
-            const float v = (float)xs[b * QK + i];
-            ss = __builtin_fmaf(v, v, ss);
+        const uint4 lo = *reinterpret_cast<const uint4*>(xs + b * QK), hi = *reinterpret_cast<const uint4*>(xs + b * QK + 16);
+        const int ss = dot16_i8(lo, lo) + dot16_i8(hi, hi);
+        xnorm[b] = xds[b] * __builtin_sqrtf((float)ss);
+    }
+    // The share's must ids as LDS flags (read once; loads batched so they are in flight together), and with must ids
+    // the share's rows of the first-occurrence array reset for the select kernel.
+    if (n_must > 0) {  // uniform
+        constexpr int kB = 8;
+        for (int i0 = 0; i0 < n_must; i0 += kScreenThreads * kB) {
+            int id[kB];
+#pragma unroll
+            for (int q = 0; q < kB; ++q) id[q] = must[min(i0 + q * kScreenThreads + tid, n_must - 1)];
+#pragma unroll
+            for (int q = 0; q < kB; ++q)
+                if (i0 + q * kScreenThreads + tid < n_must && id[q] >= ra && id[q] < rb && id[q] < nv) mshare[id[q] - ra] = 1;
         }
-        xnorm[b] = xds[b] * __builtin_sqrtf(ss);
+        for (int i = tid; i < rb - ra; i += kScreenThreads) firsts[ra + i] = kNoFirst;
+        __syncthreads();
     }
 
-    int elig = 0;  // wave 0: eligible keys so far
     // wave 0: the previous tile's rows, coarse scores and bounds buffer, finished once wave 1's bounds are ordered
     // before it by the next barrier
     int prev_r = 0, prev_n = 0, prev_buf = 0;
+    uint64_t kt[kTops] = {};  // wave 0: each lane's best eligible keys, best first
     float prev_c = 0.0f;
     auto finish_prev = [&]() {
         if (tid < prev_n) upper[prev_r + tid] = prev_c + bsh[prev_buf * 64 + tid];
@@ -272,22 +499,11 @@ __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(
     // One tile whose chunks sit in `regs`: stage into LDS, then wave 0 (one row per lane) runs the coarse chains and
     // wave 1 the bound chains (model.cpp:263-271).
     int buf = 0;
-    auto tile_body = [&](const ScreenRegs& regs, int r, float* prod, float* errf, uint8_t* mf) {
+    auto tile_body = [&](const ScreenRegs& regs, int r, float* prod, float* errf) {
         const int nrows = min(tile, rb - r);
+        const uint8_t* mf = mshare + (r - ra);
         regs.stage(prod + zp, errf + zp, ps, nrows, nb, nb_magic, xs);
-        for (int i = tid; i < nrows; i += kScreenThreads) {
-            mf[i] = 0;
-            mark[r + i] = 0;
-            if (n_must > 0) firsts[r + i] = kNoFirst;
-        }
         __syncthreads();
-        if (n_must > 0) {
-            for (int i = tid; i < n_must; i += kScreenThreads) {
-                const int id = must[i];
-                if (id >= r && id < r + nrows && id < nv) mf[id - r] = 1;
-            }
-            __syncthreads();
-        }
         if (tid < 64) {
             finish_prev();
             uint64_t key = 0;
@@ -297,10 +513,15 @@ __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(
                 c = chain_lds_pipe<2>(prod + tid * ps, xdsp, L);
                 coarse[row] = c;
                 logits[row] = -__builtin_inff();
+                mark[row] = mf[tid];  // 1: a must id (never a seed or candidate), else 0
                 if (row < nv && !mf[tid]) key = score_key(c, row);
-                wkeys[row - ra] = key;
+#pragma unroll
+                for (int j = 0; j < kTops; ++j) {  // insertion into the sorted list
+                    const uint64_t hi = kt[j] > key ? kt[j] : key;
+                    key = kt[j] > key ? key : kt[j];
+                    kt[j] = hi;
+                }
             }
-            elig += __popcll(__ballot(key != 0));
             prev_r = r, prev_n = nrows, prev_buf = buf, prev_c = c;
         } else if (tid < 128) {
             const int l = tid - 64;
@@ -316,198 +537,382 @@ __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(
     // counting assume the worst at the join); the last one or two tiles are peeled.
     const int n_tiles = (rb - ra + tile - 1) / tile;
     int t = 0;
+    QH_HSTAMP(0, 1);
     while (t + 2 < n_tiles) {
         B.load(w4, s4, e32, ra + (t + 1) * tile, min(tile, rb - ra - (t + 1) * tile), nb);
-        tile_body(A, ra + t * tile, prod0, errf0, mflag);
+        tile_body(A, ra + t * tile, prod0, errf0);
         A.load(w4, s4, e32, ra + (t + 2) * tile, min(tile, rb - ra - (t + 2) * tile), nb);
-        tile_body(B, ra + (t + 1) * tile, prod1, errf1, mflag + tile);
+        tile_body(B, ra + (t + 1) * tile, prod1, errf1);
         t += 2;
     }
     if (t + 1 < n_tiles) {
         B.load(w4, s4, e32, ra + (t + 1) * tile, min(tile, rb - ra - (t + 1) * tile), nb);
-        tile_body(A, ra + t * tile, prod0, errf0, mflag);
-        tile_body(B, ra + (t + 1) * tile, prod1, errf1, mflag + tile);
+        tile_body(A, ra + t * tile, prod0, errf0);
+        tile_body(B, ra + (t + 1) * tile, prod1, errf1);
     } else {
-        tile_body(A, ra + t * tile, prod0, errf0, mflag);
+        tile_body(A, ra + t * tile, prod0, errf0);
     }
-    const int R = rb - ra;
-    if (tid == 0) n_elig = elig;
-    __syncthreads();
+    __syncthreads();  // wave 1's bounds of the last tile
     if (tid < 64) finish_prev();
-    lvl2[tid] = 0ull;  // over the first product buffer, free now
-    __syncthreads();
-    // The share's best n_keep keys (keys are unique). Level 1: each wave ranks its quarter of the share (at most
-    // 256 keys) and keeps its best n_keep; level 2: wave 0 ranks the 4 * n_keep survivors.
-    const int lane = tid & 63, wave = tid >> 6;
-    const int Q = (R + 3) / 4;
-    const int q0 = min(R, wave * Q), q1 = min(R, q0 + Q);
-    {
-        uint64_t a[4];
-        int rk[4];
+    QH_HSTAMP(0, 2);
+    // The share's kTops best eligible keys, best first (0 where it has fewer), from the lanes' sorted lists: a wave
+    // maximum per rank, whose lane (keys are unique) then moves its list up.
+    if (tid < 64) {
+        uint64_t best[kTops];
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) {
-            const int i = q0 + s2 * 64 + lane;
-            a[s2] = i < q1 ? wkeys[i] : 0ull;
-        }
-        if (Q <= 128) {  // uniform
-            uint64_t a2[2] = {a[0], a[1]};
-            int rk2[2];
-            wave_rank<2>(a2, q1 - q0, rk2);
-            rk[0] = rk2[0];
-            rk[1] = rk2[1];
-            rk[2] = rk[3] = n_keep;
-        } else {
-            wave_rank<4>(a, q1 - q0, rk);
-        }
+        for (int j = 0; j < kTops; ++j) {
+            best[j] = wave_max_u64(kt[0]);
+            if (kt[0] == best[j]) {
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2)
-            if (a[s2] != 0 && rk[s2] < n_keep) lvl2[wave * n_keep + rk[s2]] = a[s2];
+                for (int i = 0; i + 1 < kTops; ++i) kt[i] = kt[i + 1];
+                kt[kTops - 1] = 0ull;
+            }
+        }
+        if (tid == 0) {
+            uint4* t = reinterpret_cast<uint4*>(tops + (size_t)blockIdx.x * kTops);
+            t[0] = make_uint4((uint32_t)best[0], (uint32_t)(best[0] >> 32), (uint32_t)best[1], (uint32_t)(best[1] >> 32));
+            t[1] = make_uint4((uint32_t)best[2], (uint32_t)(best[2] >> 32), (uint32_t)best[3], (uint32_t)(best[3] >> 32));
+        }
     }
-    __syncthreads();
-    if (wave == 0) {
-        uint64_t* part = seedpart + (size_t)blockIdx.x * n_keep;
-        uint64_t a[4];
-        int rk[4];
-#pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) {
-            const int i = s2 * 64 + lane;
-            a[s2] = i < 4 * n_keep ? lvl2[i] : 0ull;
-        }
-        if (4 * n_keep <= 64) {  // uniform
-            uint64_t a1[1] = {a[0]};
-            int rk1[1];
-            wave_rank<1>(a1, 4 * n_keep, rk1);
-            rk[0] = rk1[0];
-            rk[1] = rk[2] = rk[3] = n_keep;
-        } else {
-            wave_rank<4>(a, 4 * n_keep, rk);
-        }
-#pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2)
-            if (a[s2] != 0 && rk[s2] < n_keep) part[rk[s2]] = a[s2];
-        if (lane < n_keep && lane >= n_elig) part[lane] = 0ull;
-    }
+    QH_HSTAMP(0, 3);
 }
 
-__global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
+__global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     const uint8_t* __restrict__ w8, const uint16_t* __restrict__ s8, const int8_t* __restrict__ xq,
-    const float* __restrict__ xd, int nb, int nv, int k, int n_keep, int n_parts,
-    const uint64_t* __restrict__ seedpart, HeadMust mq, uint8_t* __restrict__ mark, int32_t* __restrict__ firsts,
-    int32_t* __restrict__ rows, float* __restrict__ logits, HeadCtrl* __restrict__ ctrl) {
-    extern __shared__ float wprod[];  // [waves][nb]
-    constexpr int kWaves = kSeedThreads / 64;
-    __shared__ uint64_t best[QH_HEAD_MAX_TOPK + 9];
-    __shared__ uint64_t wb[2][kWaves];
-    __shared__ uint64_t pool[kSeedMaxPool];
-    __shared__ int rowl[QH_HEAD_MAX_TOPK + 8];
-    __shared__ float exact[QH_HEAD_MAX_TOPK + 8];
-    __shared__ int counts[2];
-    __shared__ int wsum[kWaves];
-    __shared__ int n_pool;
+    const float* __restrict__ xd, int nb, int nv, int k, int n_parts, int share, int band,
+    const uint64_t* __restrict__ tops, const float* __restrict__ coarse, const float* __restrict__ upper,
+    const uint8_t* __restrict__ mark, int32_t* __restrict__ firsts, HeadMust mq, int32_t* __restrict__ rows,
+    float* __restrict__ logits, HeadCtrl* __restrict__ ctrl, qh_head_stats* __restrict__ stats, TokenFeedback fb) {
+    extern __shared__ __align__(16) float ssm[];  // products [32][nb], activation codes [nb * 32], scales [nb]
+    float* prod = ssm;
+    int8_t* xs = reinterpret_cast<int8_t*>(ssm + kRescoreRows * nb);
+    float* xds = reinterpret_cast<float*>(xs + nb * QK);
+    __shared__ uint64_t pool[kPoolCap];
+    __shared__ int prow[kPoolCap];
+    __shared__ float pexact[kPoolCap];
+    __shared__ uint64_t gmax[kSelThreads / 4];
+    __shared__ uint64_t best[kMaxKeep];
+    __shared__ int seedrow[kMaxKeep];
+    __shared__ float exact[kMaxKeep];
+    __shared__ ShareRows inc;  // shares whose published keys may miss keys at or above the cut
+    __shared__ int selp[kMaxKeep];
+    __shared__ RadixShared rsh;
+    __shared__ int candl[kSelRows * kSelThreads], mustl[kSelRows * kSelThreads];
+    __shared__ int n_pool, n_sel, n_c, n_m, ns_sh, base_sh, last_sh, n_cand_sh;
+    __shared__ uint64_t thr_sh, key_sh;
+    __shared__ float tau_sh;
+    __shared__ int wsum[kSelWaves];
+    __shared__ uint64_t wkey[kSelWaves];
 
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n_seed = n_keep - 1;
-    // Every partial key in registers. Any n_keep distinct keys bound the global n_keep-th key from below: each
-    // wave offers the n_keep-th largest of its lanes' maxima (distinct keys), and L is the largest offer (0 if no
-    // wave has n_keep nonzero maxima). Only keys >= L can be selected.
-    const int total = n_parts * n_keep;
-    uint64_t kv[kSeedKeysPerThread];
-#pragma unroll
-    for (int j = 0; j < kSeedKeysPerThread; ++j) {
-        const int i = j * kSeedThreads + tid;
-        kv[j] = i < total ? seedpart[i] : 0ull;
-    }
-    if (tid < QH_HEAD_MAX_TOPK + 9) best[tid] = 0ull;
-    if (tid == 0) n_pool = 0;
+    const int n_keep = k + 9, n_seed = k + 8;
+    QH_HSTAMP(1, 0);
+    // Every load that depends on nothing else first: the band's bounds and marks, the published keys of this thread's
+    // shares (tid + s * kSelThreads), the activation.
+    // Thread t scans rows r0 = ca + 4t .. r0 + 3 (band is a multiple of 4), their marks one 4-byte word.
+    const int ca = (int)blockIdx.x * band, cb = min(ca + band, nv), r0 = ca + kSelRows * tid;
+    float up[kSelRows];
+    uint8_t mk[kSelRows];
     {
-        uint64_t lm[1] = {0ull};
+        const uint32_t mw = r0 < cb ? *reinterpret_cast<const uint32_t*>(mark + r0) : 0u;
 #pragma unroll
-        for (int j = 0; j < kSeedKeysPerThread; ++j) lm[0] = kv[j] > lm[0] ? kv[j] : lm[0];
-        int rk[1];
-        wave_rank<1>(lm, 64, rk);
-        const uint64_t offer = wave_max_u64((lm[0] != 0 && rk[0] == n_keep - 1) ? lm[0] : 0ull);
-        if (lane == 0) wb[0][wave] = offer;
-    }
-    __syncthreads();
-    uint64_t L = wb[0][0];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) L = wb[0][w] > L ? wb[0][w] : L;
-#pragma unroll
-    for (int j = 0; j < kSeedKeysPerThread; ++j) {
-        const uint64_t v = kv[j];
-        if (v != 0 && v >= L) {
-            const int at = atomicAdd(&n_pool, 1);
-            if (at < kSeedMaxPool) pool[at] = v;
+        for (int j = 0; j < kSelRows; ++j) {
+            up[j] = upper[min(r0 + j, cb - 1)];
+            mk[j] = (uint8_t)(mw >> (8 * j));
         }
     }
-    __syncthreads();
-    const int np = n_pool;
-    if (np <= kSeedThreads) {  // uniform: rank each pool key against the pool (broadcast LDS reads); keys are unique
-        if (wave * 64 < np) {  // uniform per wave: only the waves that hold pool keys
-            const uint64_t mine = tid < np ? pool[tid] : 0ull;
-            int rank = 0;
-#pragma unroll 8
-            for (int j = 0; j < np; ++j) rank += pool[j] > mine ? 1 : 0;
-            if (tid < np && rank < n_keep) best[rank] = mine;
+    uint64_t tk[kSelShares][kTops];
+#pragma unroll
+    for (int s = 0; s < kSelShares; ++s) {
+        const int p = tid + s * kSelThreads;
+        uint4 a = make_uint4(0u, 0u, 0u, 0u), b = a;
+        if (p < n_parts) {
+            a = load16(tops + (size_t)p * kTops);
+            b = load16(tops + (size_t)p * kTops + 2);
         }
-    } else {
-        // Many survivors (e.g. many equal scores): n_keep rounds of a block-wide maximum over every partial key.
-        for (int i = 0; i < n_keep; ++i) {
-            uint64_t m = 0;
-#pragma unroll
-            for (int j = 0; j < kSeedKeysPerThread; ++j) m = kv[j] > m ? kv[j] : m;
-            const uint64_t g = wave_max_u64(m);
-            if (lane == 0) wb[(i + 1) & 1][wave] = g;
-            __syncthreads();
-            uint64_t gb = wb[(i + 1) & 1][0];
-#pragma unroll
-            for (int w = 1; w < kWaves; ++w) gb = wb[(i + 1) & 1][w] > gb ? wb[(i + 1) & 1][w] : gb;
-            if (gb != 0 && m == gb) {
-#pragma unroll
-                for (int j = 0; j < kSeedKeysPerThread; ++j) kv[j] = kv[j] == gb ? 0ull : kv[j];
-            }
-            if (tid == 0) best[i] = gb;
-        }
+        tk[s][0] = ((uint64_t)a.y << 32) | a.x;
+        tk[s][1] = ((uint64_t)a.w << 32) | a.z;
+        tk[s][2] = ((uint64_t)b.y << 32) | b.x;
+        tk[s][3] = ((uint64_t)b.w << 32) | b.z;
     }
-    __syncthreads();
-    if (wave == 0) {  // one lane per seed: the selected keys are best[0, ns), nonzero, best first
-        const bool have = lane < n_seed && best[lane] != 0;
-        const int ns = __popcll(__ballot(have));
-        if (have) {
-            const int r = key_row(best[lane]);
-            rowl[lane] = r;
-            rows[lane] = r;
-            mark[r] = 2;
-        }
-        if (lane == 0) {
-            counts[0] = ns;
-            ctrl->n_seeds = ns;
-            ctrl->seed_tie =
-                (ns == n_seed && best[n_seed] != 0 && (best[n_seed] >> 32) == (best[n_seed - 1] >> 32)) ? 1 : 0;
-        }
+    for (int i = tid; i < nb * 2; i += kSelThreads) reinterpret_cast<uint4*>(xs)[i] = load16(xq + (size_t)i * 16);
+    for (int i = tid; i < nb; i += kSelThreads) xds[i] = xd[i];
+    if (tid < kMaxKeep) best[tid] = 0ull;
+    if (tid == 0) {
+        n_pool = 0;
+        n_sel = 0;
+        n_c = 0;
+        n_m = 0;
+        inc.n = 0;
+        thr_sh = 1ull;
     }
-    __syncthreads();
-    const int ns = counts[0];
-    // The must ids' first occurrences, valid and not seeds, listed after the seeds in query order (model.cpp:324-330;
-    // the candidate kernel rescores them): every such occurrence proposes its index for its row with an atomic
-    // minimum, then each thread takes a run of the list, counts the occurrences that won, and a block scan of the
-    // counts gives each run its place.
+    // The must ids' first occurrences: each occurrence in this workgroup's slice of the list proposes its index for its
+    // row with an atomic minimum (the screen reset the rows); the last workgroup lists the winners.
     const int32_t* must;
     int n_must;
     must_span(mq, must, n_must);
-    if (n_must > 0) {  // uniform
-        for (int i = tid; i < n_must; i += kSeedThreads) {
+    unsigned mdep = 0;  // the minima's returned values: each has been performed before this workgroup's completion
+    if (n_must > 0) {
+        const int per = (n_must + (int)gridDim.x - 1) / (int)gridDim.x;
+        const int ma = min(n_must, (int)blockIdx.x * per), mb = min(n_must, ma + per);
+        for (int i = ma + tid; i < mb; i += kSelThreads) {
             const int id = must[i];
-            if (id >= 0 && id < nv && mark[id] != 2) atomicMin(&firsts[id], i);
+            if (id >= 0 && id < nv) mdep |= (unsigned)atomicMin(&firsts[id], i);
+        }
+    }
+
+    // 1. A cut L at most the n_keep-th best key: the n_keep-th best of the maxima of 64 groups of shares (16 each),
+    // since n_keep distinct keys reach it (1 or 0 when fewer groups have an eligible row: every key). Every key >= L
+    // goes to the pool: the published ones, and the unpublished ones of shares whose last published key is >= L
+    // (read again; rare). The pool holds the n_keep best keys; ranking it orders them.
+    uint64_t m = 0;
+#pragma unroll
+    for (int s = 0; s < kSelShares; ++s) m = tk[s][0] > m ? tk[s][0] : m;
+#pragma unroll
+    for (int off = 1; off < 4; off <<= 1) {  // over groups of 4 lanes
+        const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(m >> 32), off, 64) << 32) |
+                           (uint32_t)__shfl_xor((int)(uint32_t)m, off, 64);
+        m = o > m ? o : m;
+    }
+    if ((lane & 3) == 0) gmax[tid >> 2] = m;
+    __syncthreads();
+    list_ranks(gmax, kSelThreads / 4, [&](int i, int rank) {
+        if (rank == n_keep - 1) thr_sh = gmax[i];  // zero maxima rank below every nonzero one
+    });
+    __syncthreads();
+    const uint64_t L = thr_sh;
+    {
+        bool pr[kSelShares * kTops];
+        int slot[kSelShares * kTops];
+#pragma unroll
+        for (int s = 0; s < kSelShares; ++s)
+#pragma unroll
+            for (int r = 0; r < kTops; ++r) pr[s * kTops + r] = tk[s][r] != 0 && tk[s][r] >= L;
+        wave_append_n(pr, &n_pool, slot);
+#pragma unroll
+        for (int s = 0; s < kSelShares; ++s)
+#pragma unroll
+            for (int r = 0; r < kTops; ++r)
+                if (slot[s * kTops + r] >= 0 && slot[s * kTops + r] < kPoolCap) {
+                    pool[slot[s * kTops + r]] = tk[s][r];
+                    prow[slot[s * kTops + r]] = key_row(tk[s][r]);
+                }
+        bool pi[kSelShares];
+        int si[kSelShares];
+#pragma unroll
+        for (int s = 0; s < kSelShares; ++s) pi[s] = pr[s * kTops + kTops - 1];
+        wave_append_n(pi, &inc.n, si);
+#pragma unroll
+        for (int s = 0; s < kSelShares; ++s)
+            if (si[s] >= 0 && si[s] < kMaxKeep) {
+                inc.p[si[s]] = tid + s * kSelThreads;
+                inc.below[si[s]] = tk[s][kTops - 1];
+            }
+    }
+    __syncthreads();
+    QH_HSTAMP(2, 0);
+    if (inc.n > 0 && inc.n <= kMaxKeep) {  // uniform; rare: a share holding kTops of the keys >= L
+        const int n = inc.n * share;
+#pragma unroll 1
+        for (int i0 = 0; i0 < n; i0 += kSelThreads) {  // uniform trip count: wave_append needs whole waves
+            const int i = i0 + tid;
+            uint64_t v = 0;
+            if (i < n) {
+                const int sh = i / share, r = inc.p[sh] * share + (i - sh * share);
+                if (r < nv && mark[r] == 0) v = score_key(coarse[r], r);
+                if (v >= inc.below[sh]) v = 0;  // published
+            }
+            const int slot = wave_append(v != 0 && v >= L, &n_pool);
+            if (slot >= 0 && slot < kPoolCap) {
+                pool[slot] = v;
+                prow[slot] = key_row(v);
+            }
         }
         __syncthreads();
-        auto first_at = [&](int i, int id) {
-            return id >= 0 && id < nv && __hip_atomic_load(&firsts[id], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == i;
+    }
+    if (n_pool > kPoolCap || inc.n > kMaxKeep) {  // uniform; a pathological tie structure
+        // The exact n_keep-th best share maximum T (radix select), then the n_keep-th best key th over the rows of the
+        // shares reaching T (radix select, streaming their rows), and the keys >= th.
+        const uint64_t T = block_kth_threshold<kSelThreads>(
+            [&](auto visit) {
+#pragma unroll
+                for (int s = 0; s < kSelShares; ++s) visit(tk[s][0]);
+            },
+            n_keep, rsh);
+#pragma unroll 1
+        for (int s = 0; s < kSelShares; ++s) {
+            const int slot = wave_append(tk[s][0] != 0 && tk[s][0] >= T, &n_sel);  // at most n_keep shares
+            if (slot >= 0) selp[slot] = tid + s * kSelThreads;
+        }
+        __syncthreads();
+        const int n = n_sel * share;
+        auto key_at = [&](int i) -> uint64_t {
+            const int sh = i / share, r = selp[sh] * share + (i - sh * share);
+            return (r < nv && mark[r] == 0) ? score_key(coarse[r], r) : 0ull;
         };
-        const int per = (n_must + kSeedThreads - 1) / kSeedThreads;
-        const int i0 = min(n_must, tid * per), i1 = min(n_must, i0 + per);
-        int c = 0;
-        for (int i = i0; i < i1; ++i) c += first_at(i, must[i]) ? 1 : 0;
+        const uint64_t th = block_kth_threshold<kSelThreads>(
+            [&](auto visit) {
+                for (int i = tid; i < n; i += kSelThreads) visit(key_at(i));
+            },
+            n_keep, rsh);
+        if (tid == 0) n_pool = 0;
+        __syncthreads();
+        for (int i0 = 0; i0 < n; i0 += kSelThreads) {
+            const int i = i0 + tid;
+            const uint64_t v = i < n ? key_at(i) : 0ull;
+            const int slot = wave_append(v != 0 && v >= th, &n_pool);  // exactly min(n_keep, eligible rows)
+            if (slot >= 0) {
+                pool[slot] = v;
+                prow[slot] = key_row(v);
+            }
+        }
+        __syncthreads();
+    }
+    const int np = n_pool;
+
+    // 2. The seeds: the pool's n_seed best keys (model.cpp:295-304), rescored exactly (model.cpp:305-307); tau = the
+    // k-th best exact seed logit (model.cpp:308-313). A pool of up to two rescoring passes is rescored whole before it
+    // is ranked, which takes the ranking off the path to the rows' loads. 3. The band's candidates {unmarked, not a
+    // seed, upper >= tau} (model.cpp:315-322) and must rows, rescored exactly. One loop of two passes, so the
+    // rescoring code runs twice from one copy.
+    const bool early = np <= 2 * kRescoreRows;  // uniform
+    auto rank_pool = [&]() {
+        list_ranks(pool, np, [&](int i, int rank) {  // keys are unique
+            if (rank < n_keep) {
+                best[rank] = pool[i];
+                if (rank < n_seed) {
+                    seedrow[rank] = prow[i];
+                    if (early) exact[rank] = pexact[i];
+                }
+            }
+        });
+        __syncthreads();
+    };
+    if (!early) rank_pool();
+    float tau = 0.0f;
+    int ns = 0, nc = 0, nm = 0;
+    unsigned base = 0;
+    uint64_t kbest = 0;
+#pragma unroll 1
+    for (int pass = 0;; ++pass) {
+        const int* la = pass == 1 ? candl : early ? prow : seedrow;
+        const int na = pass == 1 ? nc : early ? np : min(np, n_seed);
+        const uint64_t kb = rescore_lists(la, na, mustl, pass == 0 ? 0 : nm, w8, s8, xs, xds, nb, prod,
+                                          early ? pexact : exact, pass == 0, logits);
+        if (pass == 1) {
+            kbest = kb;
+            break;
+        }
+        if (early) rank_pool();
+        QH_HSTAMP(2, 3);
+        QH_HSTAMP(1, 1);
+        if (wave == 0) {  // one lane per seed
+            ns = __popcll(__ballot(lane < n_seed && best[lane] != 0));
+            const bool have = lane < ns;
+            const float e = have ? exact[lane] : -__builtin_inff();
+            float t = -__builtin_inff();
+            if (ns >= k) {  // fewer than k seeds above it, k at or above
+                int gt = 0, ge = 0;
+                for (int j = 0; j < ns; ++j) {
+                    const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+                    gt += ej > e ? 1 : 0;
+                    ge += ej >= e ? 1 : 0;
+                }
+                const uint64_t at = __ballot(have && gt < k && ge >= k);  // equal values wherever it is set
+                t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), __ffsll((long long)at) - 1));
+            }
+            const uint64_t ks = wave_max_u64(have ? score_key(e, seedrow[lane]) : 0ull);
+            if (lane == 0) {
+                tau_sh = t;
+                key_sh = ks;
+                ns_sh = ns;
+            }
+        }
+        __syncthreads();
+        tau = tau_sh;
+        ns = ns_sh;
+        if (blockIdx.x == 0)
+            for (int i = tid; i < ns; i += kSelThreads) {
+                rows[i] = seedrow[i];
+                logits[seedrow[i]] = exact[i];
+            }
+        QH_HSTAMP(1, 2);
+#pragma unroll
+        for (int j = 0; j < kSelRows; ++j) {
+            const int r = r0 + j;
+            bool c = r < cb && mk[j] == 0 && up[j] >= tau;
+            if (__ballot(c) != 0)
+                for (int i = 0; i < ns; ++i) c = c && seedrow[i] != r;
+            int slot = wave_append(c, &n_c);
+            if (slot >= 0) candl[slot] = r;
+            slot = wave_append(r < cb && mk[j] == 1, &n_m);
+            if (slot >= 0) mustl[slot] = r;
+        }
+        __syncthreads();
+        nc = n_c;
+        nm = n_m;
+        if (tid == 0 && nc > 0) base = atomicAdd(&ctrl->n_cand, (unsigned)nc);  // returned during the rescoring
+    }
+    if (tid == 0) base_sh = (int)base;
+    if (blockIdx.x == 0 && tid == 0) kbest = key_sh > kbest ? key_sh : kbest;  // the seeds' best key, once
+    kbest = wave_max_u64(kbest);
+    if (lane == 0) wkey[wave] = kbest;
+    asm volatile("" ::"v"(mdep));  // the must minima have returned
+    __syncthreads();
+    for (int i = tid; i < nc; i += kSelThreads) rows[ns + base_sh + i] = candl[i];
+    QH_HSTAMP(1, 3);
+
+    // 4. Completion. The maxima are performed (their old values have returned) before the counts move, so the last
+    // workgroup's atomic reads see every maximum, every count and every first occurrence. It reads nothing else
+    // another workgroup of this launch wrote, so no cache write-back fence is needed.
+    if (tid == 0) {
+        uint64_t kw = wkey[0];
+        for (int w = 1; w < kSelWaves; ++w) kw = wkey[w] > kw ? wkey[w] : kw;
+        const int g = (int)(blockIdx.x % kDoneGroups);
+        if (kw) {
+            const unsigned long long old = atomicMax(group_key(ctrl, g), (unsigned long long)kw);
+            asm volatile("" ::"v"(old));
+        }
+        const unsigned gsize = (gridDim.x - (unsigned)g + kDoneGroups - 1) / kDoneGroups;
+        const bool group_last = atomicAdd(group_done(ctrl, g), 1u) == gsize - 1;
+        const unsigned ngroups = gridDim.x < (unsigned)kDoneGroups ? gridDim.x : (unsigned)kDoneGroups;
+        last_sh = group_last && atomicAdd(&ctrl->done, 1u) == ngroups - 1;
+    }
+    __syncthreads();
+    if (!last_sh) return;
+    if (wave == 0) {  // the group keys, one lane each, and the candidate count, all in flight at once
+        const unsigned nc_all = __hip_atomic_load(&ctrl->n_cand, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t v = __hip_atomic_load(group_key(ctrl, lane < kDoneGroups ? lane : 0), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t key = wave_max_u64(lane < kDoneGroups ? v : 0ull);
+        if (lane == 0) {
+            key_sh = key;
+            n_cand_sh = (int)nc_all;
+        }
+    }
+    __syncthreads();
+    const int n_cand = n_cand_sh;
+    // The must ids' first occurrences, valid (model.cpp:324-330: must ids are never seeds), after the candidates in
+    // query order. Batches of kSelThreads * kMustBatch ids: each thread takes a run of up to kMustBatch, loads its ids
+    // and then their first-occurrence words (every load in flight before the first wait), counts the occurrences that
+    // won, and a block scan of the counts gives each run its place.
+    int n_listed = 0;
+    constexpr int kMustBatch = 16;
+    for (int b0 = 0; b0 < n_must; b0 += kSelThreads * kMustBatch) {  // uniform
+        const int bn = min(n_must - b0, kSelThreads * kMustBatch);
+        const int per = (bn + kSelThreads - 1) / kSelThreads;
+        const int i0 = b0 + min(bn, tid * per), i1 = b0 + min(bn, tid * per + per);
+        int id[kMustBatch], fw[kMustBatch];
+#pragma unroll
+        for (int q = 0; q < kMustBatch; ++q) id[q] = must[min(i0 + q, n_must - 1)];
+#pragma unroll
+        for (int q = 0; q < kMustBatch; ++q)
+            fw[q] = __hip_atomic_load(&firsts[min(max(id[q], 0), nv - 1)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned wins = 0;  // bit q: occurrence i0 + q is its id's first
+#pragma unroll
+        for (int q = 0; q < kMustBatch; ++q)
+            wins |= (i0 + q < i1 && id[q] >= 0 && id[q] < nv && fw[q] == i0 + q) ? 1u << q : 0u;
+        const int c = __popc(wins);
         int incl = c;  // inclusive scan over the wave
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -516,179 +921,40 @@ __global__ __launch_bounds__(kSeedThreads) void head_seed_kernel(
         }
         if (lane == 63) wsum[wave] = incl;
         __syncthreads();
-        int base = ns;
-        for (int w = 0; w < wave; ++w) base += wsum[w];
-        int o = base + incl - c;
-        for (int i = i0; i < i1; ++i) {
-            const int id = must[i];
-            if (first_at(i, id)) {
-                rows[o++] = id;
-                mark[id] = 3;
-            }
+        int before = 0, total = 0;
+        for (int w = 0; w < kSelWaves; ++w) {
+            before += w < wave ? wsum[w] : 0;
+            total += wsum[w];
         }
-        if (tid == kSeedThreads - 1) ctrl->n_must = o - ns;
-    } else if (tid == 0) {
-        ctrl->n_must = 0;
-    }
-    float* p = wprod + wave * nb;
-    for (int j0 = 0; j0 < ns; j0 += kWaves) {
-        const int j = j0 + wave;
-        const bool active = j < ns;
-        const int r = active ? rowl[j] : 0;
-        wave_row_products_q8(w8, s8, r, nb, xq, p, active);
-        __syncthreads();
-        if (active && lane == 0) {
-            const float v = chain(p, xd, nb);
-            logits[r] = v;
-            exact[j] = v;
-        }
-        __syncthreads();
-    }
-    if (wave == 0) {  // one lane per seed
-        const bool have = lane < ns;
-        const float e = have ? exact[lane] : -__builtin_inff();
-        float tau = -__builtin_inff();
-        if (ns >= k) {  // k-th largest exact seed logit (model.cpp:308-313): fewer than k above it, k at or above
-            int gt = 0, ge = 0;
-            const int nsu = __builtin_amdgcn_readfirstlane(ns);
-            for (int j = 0; j < nsu; ++j) {
-                const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-                gt += ej > e ? 1 : 0;
-                ge += ej >= e ? 1 : 0;
-            }
-            const uint64_t at = __ballot(have && gt < k && ge >= k);  // equal values wherever it is set
-            tau = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), __ffsll((long long)at) - 1));
-        }
-        const uint64_t kmax = wave_max_u64(have ? score_key(e, rowl[lane]) : 0ull);
-        if (lane == 0) {
-            ctrl->tau = tau;
-            ctrl->argmax_key = kmax;
-            ctrl->n_cand = 0u;
-            ctrl->done = 0u;
-        }
-        if (lane < kDoneGroups) group_done(ctrl)[lane * kDoneStride] = 0u;
-    }
-}
-
-__global__ __launch_bounds__(kCandThreads) void head_cand_kernel(
-    const uint8_t* __restrict__ w8, const uint16_t* __restrict__ s8, const int8_t* __restrict__ xq,
-    const float* __restrict__ xd, int nb, int nv, const float* __restrict__ upper, const uint8_t* __restrict__ mark,
-    int32_t* __restrict__ rows, float* __restrict__ logits, HeadCtrl* __restrict__ ctrl,
-    qh_head_stats* __restrict__ stats, TokenFeedback fb) {
-    extern __shared__ float wprod[];  // [waves][nb]
-    constexpr int kWaves = kCandThreads / 64;
-    __shared__ int candl[kCandRowsPerThread * kCandThreads];
-    __shared__ int wcount[kCandRowsPerThread][kWaves];
-    __shared__ int base_sh;
-    __shared__ uint64_t wkey[kWaves];
-    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // Rows [ca, cb) of this workgroup (at most kCandRowsPerThread per thread): every row's bound and mark are
-    // loaded up front, candidates are compacted with ballots and rescored, one row per wave at a time.
-    const int ca = (int)((long)blockIdx.x * nv / gridDim.x), cb = (int)((long)(blockIdx.x + 1) * nv / gridDim.x);
-    const float tau = ctrl->tau;
-    const int row_base = ctrl->n_seeds + ctrl->n_must;
-    float up[kCandRowsPerThread];
-    uint8_t mk[kCandRowsPerThread];
+        int o = ns + n_cand + n_listed + before + incl - c;
 #pragma unroll
-    for (int j = 0; j < kCandRowsPerThread; ++j) {
-        const int r = min(ca + j * kCandThreads + tid, cb - 1);
-        up[j] = upper[r];
-        mk[j] = mark[r];
+        for (int q = 0; q < kMustBatch; ++q)
+            if (wins >> q & 1u) rows[o++] = id[q];
+        n_listed += total;
+        __syncthreads();  // wsum is read before the next batch writes it
     }
-    bool cand[kCandRowsPerThread];
-    int pos[kCandRowsPerThread];
-#pragma unroll
-    for (int j = 0; j < kCandRowsPerThread; ++j) {
-        const int r = ca + j * kCandThreads + tid;
-        cand[j] = r < cb && mk[j] == 0 && up[j] >= tau;
-        const uint64_t ball = __ballot(cand[j]);
-        pos[j] = __popcll(ball & ((1ull << lane) - 1ull));
-        if (lane == 0) wcount[j][wave] = __popcll(ball);
-    }
-    __syncthreads();
-    int count = 0;
-#pragma unroll
-    for (int j = 0; j < kCandRowsPerThread; ++j) {
-        int off = count;
-        for (int w = 0; w < kWaves; ++w) {
-            off += w < wave ? wcount[j][w] : 0;
-            count += wcount[j][w];
-        }
-        if (cand[j]) candl[off + pos[j]] = ca + j * kCandThreads + tid;
-    }
-    uint64_t kbest = 0;
-    if (count > 0) {
-        if (tid == 0) base_sh = (int)atomicAdd(&ctrl->n_cand, (unsigned)count);
-        __syncthreads();
-        for (int i = tid; i < count; i += kCandThreads) rows[row_base + base_sh + i] = candl[i];
-        float* p = wprod + wave * nb;
-        for (int j0 = 0; j0 < count; j0 += kWaves) {
-            const int j = j0 + wave;
-            const bool active = j < count;
-            const int rr = active ? candl[j] : 0;
-            wave_row_products_q8(w8, s8, rr, nb, xq, p, active);
-            __syncthreads();
-            if (active && lane == 0) {
-                const float v = chain(p, xd, nb);
-                logits[rr] = v;
-                const uint64_t kk = score_key(v, rr);
-                kbest = kk > kbest ? kk : kbest;
-            }
-            __syncthreads();
-        }
-    }
-    {  // the must rows, listed after the seeds, split over the workgroups
-        const int ns = ctrl->n_seeds, nm = ctrl->n_must;
-        const int ma = (int)((long)blockIdx.x * nm / gridDim.x), mb = (int)((long)(blockIdx.x + 1) * nm / gridDim.x);
-        float* p = wprod + wave * nb;
-        for (int j0 = ma; j0 < mb; j0 += kWaves) {  // uniform bounds
-            const int j = j0 + wave;
-            const bool active = j < mb;
-            const int rr = active ? rows[ns + j] : 0;
-            wave_row_products_q8(w8, s8, rr, nb, xq, p, active);
-            __syncthreads();
-            if (active && lane == 0) {
-                const float v = chain(p, xd, nb);
-                logits[rr] = v;
-                const uint64_t kk = score_key(v, rr);
-                kbest = kk > kbest ? kk : kbest;
-            }
-            __syncthreads();
-        }
-    }
-    if (lane == 0) wkey[wave] = kbest;
-    __syncthreads();
     if (tid == 0) {
-        uint64_t m = wkey[0];
-        for (int w = 1; w < kWaves; ++w) m = wkey[w] > m ? wkey[w] : m;
-        // The maximum is performed (its old value has returned) before the completion count moves, so the last
-        // workgroup's atomic reads see every maximum and every count (n_cand's were returned before the rescoring).
-        // It reads nothing else another workgroup of this launch wrote, so no cache write-back fence is needed.
-        // Workgroups without a scored row skip the maximum: atomics on one address serialize.
-        if (m) {
-            const unsigned long long old = atomicMax(&ctrl->argmax_key, (unsigned long long)m);
-            asm volatile("" ::"v"(old));
-        }
-        const unsigned g = blockIdx.x % kDoneGroups, gsize = (gridDim.x - g + kDoneGroups - 1) / kDoneGroups;
-        const bool group_last = atomicAdd(group_done(ctrl) + g * kDoneStride, 1u) == gsize - 1;
-        const unsigned ngroups = gridDim.x < (unsigned)kDoneGroups ? gridDim.x : (unsigned)kDoneGroups;
-        if (group_last && atomicAdd(&ctrl->done, 1u) == ngroups - 1) {  // last workgroup
-            const unsigned long long key = atomicAdd(&ctrl->argmax_key, 0ull);
-            const int n_cand = (int)atomicAdd(&ctrl->n_cand, 0u);
-            stats->top1 = key_row(key);
-            stats->top1_logit = key_score(key);
-            stats->n_seeds = ctrl->n_seeds;
-            stats->n_must = ctrl->n_must;
-            stats->n_cand = n_cand;
-            stats->n_rows = ctrl->n_seeds + ctrl->n_must + n_cand;
-            stats->seed_tie = ctrl->seed_tie;
-            stats->tau = ctrl->tau;
-            if (fb.token) fb.apply(key_row(key), true);
-        }
+        const uint64_t key = key_sh;
+        stats->top1 = key_row(key);
+        stats->top1_logit = key_score(key);
+        stats->n_seeds = ns;
+        stats->n_must = n_listed;
+        stats->n_cand = n_cand;
+        stats->n_rows = ns + n_cand + n_listed;
+        stats->seed_tie =
+            (ns == n_seed && best[n_seed] != 0 && (best[n_seed] >> 32) == (best[n_seed - 1] >> 32)) ? 1 : 0;
+        stats->tau = tau;
+        if (fb.token) fb.apply(key_row(key), true);
     }
 }
 
-size_t head_workspace_bytes(int V, int D, int top_k) { return ws_layout(V, D, top_k).total; }
+bool head_select_supported(int V, int D, int top_k) {
+    return top_k >= 1 && top_k <= QH_HEAD_MAX_TOPK && screen_shape(V, D / QK).grid <= kSelShares * kSelThreads;
+}
+
+size_t head_workspace_bytes(int V, int D, int top_k) {
+    return head_select_supported(V, D, top_k) ? ws_layout(V, D).total : 0;
+}
 
 bool head_shape_supported(int D) { return D % 64 == 0 && D <= kMaxHeadCols; }
 
@@ -696,13 +962,14 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
                                  const int8_t* xq, const float* xd, const qh_head_query& q, const HeadMust& must,
                                  const qh_head_out& out, void* ws, hipStream_t s, const TokenFeedback* advance) {
     const int V = head8.rows, D = head8.cols, nb = D / QK;
-    if (must.n > kMaxMust || !head_shape_supported(D)) return hipErrorInvalidValue;
+    if (must.n > kMaxMust || !head_shape_supported(D) || !head_select_supported(V, D, q.top_k))
+        return hipErrorInvalidValue;
     const int nv = (q.n_valid > 0 && q.n_valid < V) ? q.n_valid : V;
-    const WsLayout l = ws_layout(V, D, q.top_k);
+    const WsLayout l = ws_layout(V, D);
     uint8_t* wsb = static_cast<uint8_t*>(ws);
     uint8_t* mark = wsb + l.mark;
     int32_t* firsts = reinterpret_cast<int32_t*>(wsb + l.first);
-    uint64_t* seedpart = reinterpret_cast<uint64_t*>(wsb + l.seedpart);
+    uint64_t* tops = reinterpret_cast<uint64_t*>(wsb + l.tops);
     HeadCtrl* ctrl = reinterpret_cast<HeadCtrl*>(wsb + l.ctrl);
     const uint8_t* w8 = static_cast<const uint8_t*>(head8.data);
     const uint16_t* s8 = reinterpret_cast<const uint16_t*>(w8 + qh_quant_bytes(QH_Q8_0, V, D));
@@ -710,29 +977,20 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
     const uint16_t* s4 = reinterpret_cast<const uint16_t*>(w4 + qh_quant_bytes(QH_Q4_0, V, D));
     const uint32_t* e32 = static_cast<const uint32_t*>(err.data);
 
-    const int tile = screen_tile_rows(nb);
-    const int grid = screen_grid(V, tile);
-    const int n_keep = q.top_k + 9;
-    if (grid * n_keep > kSeedThreads * kSeedKeysPerThread || grid > kSeedMaxPool) return hipErrorInvalidValue;
+    const ScreenShape sh = screen_shape(V, nb);
+    const int tile = sh.tile;
     const uint32_t magic = nb == 1 ? 0u : (uint32_t)((0x100000000ull + (uint64_t)nb - 1) / (uint64_t)nb);
-    // A share holds at most V / grid + 3 rows (its ends are rounded down to even rows); sizing its key array by that
-    // instead of kScreenMaxShare keeps the LDS under 40 KB, so four workgroups fit on a CU.
-    const int share_cap = V / grid + 4;
     const size_t lds1 = ((size_t)2 * chain_len32(nb) + 4 * (size_t)tile * chain_stride32(nb) + kChainPipePad + 128) * 4 +
-                        (size_t)share_cap * 8 + ((2 * (size_t)tile + 15) & ~size_t(15)) + (size_t)D;
-    hipLaunchKernelGGL(head_screen_kernel, dim3(grid), dim3(kScreenThreads), lds1, s, w4, s4, e32, xq, xd, V, nb, nv,
-                       must, tile, magic, out.coarse, out.upper, out.logits, mark, firsts, seedpart, n_keep,
-                       share_cap);
+                        kScreenMaxShare + (size_t)D;
+    qh_launch(head_screen_kernel, dim3(sh.grid), dim3(kScreenThreads), lds1, s, w4, s4, e32, xq, xd, V, nb, nv, must,
+              tile, sh.share, magic, out.coarse, out.upper, out.logits, mark, firsts, tops, ctrl);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const size_t lds2 = (size_t)(kSeedThreads / 64) * nb * 4;
-    hipLaunchKernelGGL(head_seed_kernel, dim3(1), dim3(kSeedThreads), lds2, s, w8, s8, xq, xd, nb, nv, q.top_k, n_keep,
-                       grid, seedpart, must, mark, firsts, out.rows, out.logits, ctrl);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const size_t lds3 = (size_t)(kCandThreads / 64) * nb * 4;
-    hipLaunchKernelGGL(head_cand_kernel, dim3((unsigned)cand_grid(nv)), dim3(kCandThreads), lds3, s, w8, s8, xq, xd, nb, nv, out.upper, mark, out.rows, out.logits, ctrl, out.stats,
-                       advance ? *advance : TokenFeedback{});
+    const int band = select_band(nv);
+    const size_t lds2 = (size_t)kRescoreRows * nb * 4 + (size_t)nb * QK + (size_t)nb * 4;
+    qh_launch(head_select_kernel, dim3((unsigned)((nv + band - 1) / band)), dim3(kSelThreads), lds2, s, w8, s8, xq, xd,
+              nb, nv, q.top_k, sh.grid, sh.share, band, tops, out.coarse, out.upper, mark, firsts, must, out.rows,
+              out.logits, ctrl, out.stats, advance ? *advance : TokenFeedback{});
     return hipGetLastError();
 }
 

@@ -1,13 +1,45 @@
 // Host-side declarations shared between the C-ABI layer (qh_api.hip) and the kernel files.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
+#include <utility>
+#include <vector>
+
 #include "quanta_hip.h"
 
 namespace qh {
+
+// Device timing of the kernels a call launches (qh_decoder_step_timed): while a timer is set on the calling thread,
+// qh_launch launches with start / stop events (hipExtLaunchKernel, the dispatch's own timestamps, no extra packets)
+// and records the stage each kernel belongs to.
+struct KernelTimer {
+    std::vector<hipEvent_t> ev;  // [2 * cap]: start, stop of kernel i
+    std::vector<int> stage;      // per timed kernel; -1 until its stage is marked
+    int n = 0;
+    bool full() const { return 2 * (size_t)n + 1 >= ev.size(); }
+    void mark(int id) {  // the kernels launched since the previous mark belong to stage id
+        for (int i = n - 1; i >= 0 && stage[i] < 0; --i) stage[i] = id;
+    }
+};
+KernelTimer*& kernel_timer();
+
+// Launch of a kernel (hipLaunchKernelGGL's arguments), timed when a KernelTimer is set on this thread.
+template <typename... P, typename... A>
+inline void qh_launch(void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipStream_t s, A&&... args) {
+    KernelTimer* t = kernel_timer();
+    if (t && !t->full()) {
+        const hipEvent_t a = t->ev[2 * t->n], b = t->ev[2 * t->n + 1];
+        t->stage.push_back(-1);
+        ++t->n;
+        hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)lds, s, a, b, 0u, static_cast<P>(args)...);
+        return;
+    }
+    kernel<<<grid, block, lds, s>>>(static_cast<P>(args)...);
+}
 
 // Records a formatted message as this thread's last error and returns `code`.
 int fail(int code, const char* fmt, ...);
@@ -44,7 +76,10 @@ hipError_t launch_argmax(const float* logits, int n, int32_t* index, void* ws, h
 // words of f16 block errors per row) and D <= kMaxHeadCols (a tile's errors fit one register pass).
 constexpr int kMaxHeadCols = 4096;
 bool head_shape_supported(int D);
+// 0 when the seed selection cannot hold the rows of the top_k + 9 screen shares (very large vocabularies with a
+// large top_k).
 size_t head_workspace_bytes(int V, int D, int top_k);
+bool head_select_supported(int V, int D, int top_k);
 // The must ids of a head query (HeadQuery::must, model.h:24-29): ids[0, n) known on the host, or, with len_dev set,
 // the last `window` ids (all of them when window <= 0) of a device-resident history ids[0, *len_dev), which the
 // kernels read when they run (Session::head_query, session.cpp:63-79), so a captured launch follows the history.
@@ -115,6 +150,7 @@ void decoder_destroy(Decoder* d);
 hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, int top_k, hipStream_t s);
 hipError_t decoder_begin(Decoder* d, int top_k, int32_t* out, int out_cap, hipStream_t s);
 hipError_t decoder_step(Decoder* d, int top_k, hipStream_t s);
+int decoder_step_timed(Decoder* d, int top_k, hipStream_t s, float* us, int32_t* stage, int cap, int32_t* n);
 void decoder_views(Decoder* d, qh_decoder_state* v);
 int decoder_set_query(Decoder* d, const qh_sampler_params* p);
 hipError_t decoder_set_sampler(Decoder* d, const qh_sampler_params* p, uint64_t seed);

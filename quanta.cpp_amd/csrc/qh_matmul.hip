@@ -393,7 +393,7 @@ void launch_mm_lds(float* out, int ldo, const uint8_t* wq, const uint16_t* ws, c
                    int cols, int n, int r0, int r1, hipStream_t s) {
     const int row_tiles = (r1 - r0 + 15) / 16;
     const int n_tg = (n + 16 * TT - 1) / (16 * TT);
-    hipLaunchKernelGGL((matmul_lds_kernel<DT, TT, KC>), dim3((unsigned)(row_tiles * n_tg)), dim3(kMmThreads), 0, s,
+    qh_launch((matmul_lds_kernel<DT, TT, KC>), dim3((unsigned)(row_tiles * n_tg)), dim3(kMmThreads), 0, s,
                        out, ldo, wq, ws, xq, xd, cols, n, r0, r1, n_tg);
 }
 
@@ -403,7 +403,7 @@ void launch_mm_reg(float* out, int ldo, const uint8_t* wq, const uint16_t* ws, c
     const int row_tiles = (r1 - r0 + 15) / 16;
     const int waves = (n + 16 * TT - 1) / (16 * TT);
     const int n_tg = (waves + NW - 1) / NW;
-    hipLaunchKernelGGL((matmul_reg_kernel<DT, TT, NW, VEC>), dim3((unsigned)(row_tiles * n_tg)), dim3(64 * NW), 0, s,
+    qh_launch((matmul_reg_kernel<DT, TT, NW, VEC>), dim3((unsigned)(row_tiles * n_tg)), dim3(64 * NW), 0, s,
                        out, ldo, wq, ws, xq, xd, cols, n, r0, r1, n_tg);
 }
 

@@ -208,7 +208,7 @@ size_t sample_lds_bytes(int n_valid) { return (size_t)((n_valid + 31) / 32) * 4;
 hipError_t launch_sample(const float* logits, int n_valid, const int32_t* rows, const qh_head_stats* hs,
                          const HeadMust& hist, const qh_sampler_params& p, uint64_t* state, int32_t* out_id,
                          hipStream_t s) {
-    hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kThreads), sample_lds_bytes(n_valid), s, logits, n_valid, rows, hs,
+    qh_launch(sample_kernel, dim3(1), dim3(kThreads), sample_lds_bytes(n_valid), s, logits, n_valid, rows, hs,
                        hist, p, state, out_id);
     return hipGetLastError();
 }

@@ -89,6 +89,9 @@ def _check_head(qh, oracle, head_np, sl, xq, xd, V, D, top_k, n_valid=0, must=No
     rows = sl.rows.cpu().numpy()[: st["n_rows"]]
     assert sorted(rows.tolist()) == sorted(o["rows"].tolist())
     assert rows[: st["n_seeds"]].tolist() == o["rows"][: o["n_seeds"]].tolist(), "seed order"
+    nm = st["n_must"]
+    if nm:
+        assert rows[len(rows) - nm:].tolist() == o["rows"][len(o["rows"]) - nm:].tolist(), "must ids last, query order"
     assert (bits(sl.logits.cpu().numpy()) == bits(o["logits"])).all(), "logits"
     assert np.float32(st["tau"]).tobytes() == np.float32(o["tau"]).tobytes()
     nv = n_valid if 0 < n_valid < V else V
@@ -114,7 +117,7 @@ def test_shortlist_small_vocab(qh, oracle, synth, gpu, top_k):
 @pytest.mark.parametrize("top_k", [1, 20])
 def test_shortlist_long_must_list(qh, oracle, synth, gpu, top_k):
     """A history-sized must list: 3000 ids with many repeats and some out of range. Every first occurrence of a valid
-    id comes back exact, listed after the seeds in query order (the oracle lists them last, in query order)."""
+    id comes back exact, listed last in query order, as the oracle lists them."""
     V, D = 6007, 896
     head_np, (h8, h4, he) = _head(qh, synth, gpu, V, D, 41)
     sl = qh.ShortlistHead(h8, h4, he, top_k=top_k)
@@ -131,9 +134,57 @@ def test_shortlist_long_must_list(qh, oracle, synth, gpu, top_k):
         expect = [int(must[i]) for i in sorted(first) if 0 <= must[i] < nv]
         assert nm == len(expect) > 100
         rows = sl.rows.cpu().numpy()
-        assert rows[st["n_seeds"]:st["n_seeds"] + nm].tolist() == expect == o["rows"][-nm:].tolist()
+        n = st["n_rows"]
+        assert rows[n - nm:n].tolist() == expect == o["rows"][-nm:].tolist()
     # the same list again with an empty window (the kernels reset what the previous query left)
     _check_head(qh, oracle, head_np, sl, xq[0], xd[0], V, D, top_k)
+
+
+def _cluster_head(synth, V, D, seed, r0, n, x):
+    """A random Q8_0 head whose rows [r0, r0 + n) share one code pattern aligned with x, with consecutive f16 scales:
+    their scores rise row by row far above the rest, so the best keys crowd a few screen shares. The codes are
+    multiples of 8 in [-56, 56] with -64 first in every block, so the 4-bit copy is exact (scale 8 d, zero error) and
+    no two coarse scores of the cluster tie."""
+    head8 = synth.q8_tensor(seed, V, D)
+    q = head8[: V * D].view(np.int8).reshape(V, D)
+    d = head8[V * D:].view(np.float16).reshape(V, D // 32)
+    c = (np.clip(np.rint(x / np.abs(x).max() * 7.0), -7, 7) * 8).astype(np.int8)
+    c[::32] = -64
+    q[r0:r0 + n] = c
+    first = int(np.float16(1e-3).view(np.uint16))
+    d[r0:r0 + n] = np.arange(first, first + n, dtype=np.uint16).view(np.float16)[:, None]
+    head4, err = synth.shortlist_copy(head8, V, D)
+    return head8, head4, err
+
+
+@pytest.mark.parametrize("top_k,r0,n", [(1, 70001, 300), (20, 5, 700), (55, 40000, 9600)])
+def test_shortlist_crowded_shares(qh, oracle, synth, gpu, top_k, r0, n):
+    """The best keys crowd a few screen shares: each share publishes only its best four keys, so shares holding more
+    than four of them are read again (a few hundred keys), and past 1024 keys at or above the cut the selection falls
+    back to a radix select over the selected shares' rows (55: about 9,300 keys)."""
+    V, D = 151936, 896
+    x = synth.activations(211, 1, D, scale=0.5)
+    head_np = _cluster_head(synth, V, D, 209, r0, n, x[0])
+    h8, h4, he = (qh.DeviceTensor.upload(head_np[0], 2, V, D), qh.DeviceTensor.upload(head_np[1], 3, V, D),
+                  qh.DeviceTensor.upload(head_np[2].view(np.uint8), 1, V, D // 32))
+    sl = qh.ShortlistHead(h8, h4, he, top_k=top_k)
+    xq, xd = qh.quantize_q8(_dev(x, gpu))
+    st, o = _check_head(qh, oracle, head_np, sl, xq[0], xd[0], V, D, top_k)
+    assert r0 + n - top_k - 8 <= min(sl.rows[: st["n_seeds"]].cpu().numpy().tolist())  # the cluster's last rows
+    must = [r0 + n - 1, r0 + n - 3, 17, r0 + n - 1]  # the best rows as must ids: not seeds, listed last
+    _check_head(qh, oracle, head_np, sl, xq[0], xd[0], V, D, top_k, must=must)
+
+
+def test_shortlist_fewer_shares_than_seeds(qh, oracle, synth, gpu):
+    """A vocabulary of a few screen shares (fewer than top_k + 9): every eligible row is a seed candidate."""
+    V, D = 300, 896
+    head_np, (h8, h4, he) = _head(qh, synth, gpu, V, D, 223)
+    x = synth.activations(227, 2, D, scale=0.5)
+    xq, xd = qh.quantize_q8(_dev(x, gpu))
+    for top_k in (1, 20, 55):
+        sl = qh.ShortlistHead(h8, h4, he, top_k=top_k)
+        _check_head(qh, oracle, head_np, sl, xq[0], xd[0], V, D, top_k)
+        _check_head(qh, oracle, head_np, sl, xq[1], xd[1], V, D, top_k, n_valid=250, must=[3, 299, 3, 7])
 
 
 def test_shortlist_full_vocab(qh, oracle, synth, gpu):

@@ -57,8 +57,8 @@ def _same(a, b):
     n, ns, nm = sa["n_rows"], sa["n_seeds"], sa["n_must"]
     ra, rb = a["rows"][:n], b["rows"][:n]
     assert ra[:ns].tolist() == rb[:ns].tolist()  # seeds, best coarse first
-    assert ra[ns:ns + nm].tolist() == rb[ns:ns + nm].tolist()  # must ids in query order
-    assert sorted(ra[ns + nm:].tolist()) == sorted(rb[ns + nm:].tolist())  # candidates, unordered
+    assert ra[n - nm:].tolist() == rb[n - nm:].tolist()  # must ids in query order, last
+    assert sorted(ra[ns:n - nm].tolist()) == sorted(rb[ns:n - nm].tolist())  # candidates, unordered
 
 
 def qh_stats(raw):
@@ -90,7 +90,7 @@ def test_noalloc_refuses_oversized_head(qh, synth, gpu):
     claim more rows than their buffers hold, which only the size check may see)."""
     V, D = 6007, 896
     heads = _upload(qh, synth, V, D, 3)
-    big = 2_000_000
+    big = 1_000_000  # supported (at most 1,048,576 rows), with a workspace beyond the scratch array
     assert qh.lib().qh_shortlist_workspace_bytes(big, D, 1) > qh.NOALLOC_SCRATCH_BYTES
     views = []
     for t, rows, cols in ((heads[0], big, D), (heads[1], big, D), (heads[2], big, D // 32)):
