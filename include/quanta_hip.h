@@ -76,6 +76,12 @@ int qh_validate_tensor(const qh_tensor* W);
 
 /* Thin device-memory helpers so C/C++ callers need no HIP headers. */
 int qh_malloc(void** ptr, size_t bytes);
+
+/* Forced allocation failure, for tests of the error paths: after `after` more device allocations by the library
+ * (qh_malloc and the decoder's own buffers), the next one fails with QH_ERR_NOMEM before any HIP call, and the hook
+ * disarms itself; after < 0 disarms it. Process-wide. No counterpart in the reference: it is the fault hook its
+ * failure handling is tested with (an allocation failure maps to an error code, nothing is leaked). */
+int qh_fault_alloc(int after);
 int qh_free(void* ptr);
 int qh_memcpy_h2d(void* dst, const void* src_host, size_t bytes, void* stream); /* async */
 int qh_memcpy_d2h(void* dst_host, const void* src, size_t bytes, void* stream); /* synchronous */

@@ -73,7 +73,7 @@ STAGE_FINAL_NORM, STAGE_HEAD, STAGE_PICK = 1 << 20, (1 << 20) + 1, (1 << 20) + 2
 
 # Every symbol include/quanta_hip.h declares, in header order.
 EXPORTS = ("qh_last_error", "qh_version", "qh_init", "qh_quant_bytes", "qh_tensor_bytes", "qh_validate_tensor",
-           "qh_malloc", "qh_free", "qh_memcpy_h2d", "qh_memcpy_d2h", "qh_memset", "qh_stream_sync",
+           "qh_malloc", "qh_fault_alloc", "qh_free", "qh_memcpy_h2d", "qh_memcpy_d2h", "qh_memset", "qh_stream_sync",
            "qh_stream_create", "qh_stream_destroy",
            "qh_quantize_q8", "qh_matvec_q", "qh_matmul_q", "qh_argmax_workspace_bytes", "qh_argmax",
            "qh_shortlist_workspace_bytes", "qh_shortlist_head", "qh_shortlist_head_noalloc",
@@ -94,6 +94,7 @@ def _bind(lib):
         "qh_last_error": ([], C.c_char_p), "qh_version": ([], C.c_char_p), "qh_init": ([i32], i32),
         "qh_quant_bytes": ([i32, i32, i32], sz), "qh_tensor_bytes": ([i32, i32, i32], sz),
         "qh_validate_tensor": ([C.POINTER(qh_tensor)], i32), "qh_malloc": ([C.POINTER(vp), sz], i32),
+        "qh_fault_alloc": ([i32], i32),
         "qh_free": ([vp], i32), "qh_memcpy_h2d": ([vp, vp, sz, vp], i32), "qh_memcpy_d2h": ([vp, vp, sz, vp], i32),
         "qh_memset": ([vp, i32, sz, vp], i32), "qh_stream_sync": ([vp], i32),
         "qh_stream_create": ([C.POINTER(vp)], i32), "qh_stream_destroy": ([vp], i32),

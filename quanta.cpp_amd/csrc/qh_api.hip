@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "qh_internal.h"
@@ -37,6 +38,7 @@ int fail(int code, const char* fmt, ...) {
 
 int check_hip(hipError_t e, const char* what) {
     if (e == hipSuccess) return QH_OK;
+    if (e == hipErrorOutOfMemory) return fail(QH_ERR_NOMEM, "%s: %s", what, hipGetErrorString(e));
     return fail(QH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
@@ -121,6 +123,16 @@ int validate_head(const qh_tensor* head8, const qh_tensor* head4, const qh_tenso
 }
 
 }  // namespace
+
+std::atomic<int> g_fault_alloc{-1};  // allocations to let through before the forced failure; -1: disarmed
+
+bool fault_alloc_fires() {
+    int n = g_fault_alloc.load(std::memory_order_relaxed);
+    while (n >= 0) {
+        if (g_fault_alloc.compare_exchange_weak(n, n - 1, std::memory_order_relaxed)) return n == 0;
+    }
+    return false;
+}
 }  // namespace qh
 
 using namespace qh;
@@ -180,10 +192,16 @@ int qh_validate_tensor(const qh_tensor* W) {
     return validate_quant(W, "qh_validate_tensor");
 }
 
+int qh_fault_alloc(int after) {
+    g_fault_alloc.store(after < 0 ? -1 : after, std::memory_order_relaxed);
+    return QH_OK;
+}
+
 int qh_malloc(void** ptr, size_t bytes) {
     if (!ptr) return fail(QH_ERR_ARG, "qh_malloc: null out pointer");
     *ptr = nullptr;
     if (bytes == 0) return QH_OK;
+    if (fault_alloc_fires()) return fail(QH_ERR_NOMEM, "qh_malloc: forced allocation failure (%zu bytes)", bytes);
     hipError_t e = hipMalloc(ptr, bytes);
     if (e == hipErrorOutOfMemory) return fail(QH_ERR_NOMEM, "qh_malloc: out of memory (%zu bytes)", bytes);
     return check_hip(e, "hipMalloc");

@@ -442,7 +442,9 @@ __device__ __forceinline__ SegWarm seg_warm(const float* __restrict__ x, int D) 
     return warm;
 }
 template <int R>
-__device__ float seg_sum_squares(const float* __restrict__ x, int D, const RowF4<R>& xr, const SegWarm& warm) {
+__device__ float seg_sum_squares(const float* __restrict__ x, int D, const RowF4<R>& xr, const SegWarm& warm,
+                                 int tlk = -1) {
+    (void)tlk;
     __shared__ SegShared sh;
     const int tid = (int)threadIdx.x, n4 = D / 4;
     const Segs4 sg = seg_split(D);
@@ -461,8 +463,11 @@ __device__ float seg_sum_squares(const float* __restrict__ x, int D, const RowF4
     }
     seg_partials(sh, p1, p2, p3);
     __syncthreads();
+    QH_WSTAMP(tlk, 4);
     warm.consume();
-    return seg_chain_run(sh, [&](int k, float s0) { return ss_chain_scalar(x + sg.start(k), sg.len(k), s0); });
+    const float r = seg_chain_run(sh, [&](int k, float s0) { return ss_chain_scalar(x + sg.start(k), sg.len(k), s0); });
+    QH_WSTAMP(tlk, 5);
+    return r;
 }
 
 // rmsnorm scale 1 / sqrt(ss / D + eps) (ops_ref.cpp:197-198).
@@ -531,6 +536,7 @@ struct NormAct {
     float eps;
     int D;
     float* tmp;
+    int tlk;  // timeline id of the kernel (stamps compiled in only with QH_TIMELINE)
 
     // The loads the norm starts from (issued before the tile's weight loads, whose issue would otherwise hold them
     // up): the residual row and its scalar-cache warm-up, and the norm weight.
@@ -559,7 +565,7 @@ struct NormAct {
         float4* t4 = reinterpret_cast<float4*>(tmp);
         float ss;
         if (!EMB && D >= 128) {  // uniform
-            ss = seg_sum_squares(x, D, xr, p.warm);
+            ss = seg_sum_squares(x, D, xr, p.warm, tlk);
         } else {
 #pragma unroll
             for (int k = 0; k < R; ++k) {
@@ -1172,6 +1178,7 @@ __global__ __launch_bounds__(1024) void attention_decode_kernel(
     __shared__ uint64_t exptab[32];
     __shared__ SegShared16 ssh;
     QH_STAMP(0);
+    QH_WSTAMP(1, 0);
     const int n_heads = group * n_kv;
     const int kvh = (int)blockIdx.y, h = kvh * group + (int)blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1451,6 +1458,7 @@ __global__ __launch_bounds__(1024) void attention_decode_kernel(
         __syncthreads();
     }
     QH_STAMP(7);
+    QH_WSTAMP(1, 3);
     if (tid < HD) {  // quantize_q8 of the attention output, two 32-blocks per 64 dimensions
         const int col = h * HD + (tid & ~31);
         quant_block32(acc, oq + col, od + col / QK);
@@ -1482,6 +1490,7 @@ template <int DT, int U, int R, bool EMB>
 __global__ __launch_bounds__(256) void gemv_qkv_norm_kernel(QkvSegs a, NormAct act, int nb, int tile_rows,
                                                             uint32_t nb_magic) {
     extern __shared__ __align__(16) float smem[];
+    QH_WSTAMP(0, 0);
     int blk = (int)blockIdx.x;
     const uint8_t* w = a.w0;
     const uint16_t* sc = a.s0;
@@ -1503,7 +1512,8 @@ __global__ __launch_bounds__(256) void gemv_qkv_norm_kernel(QkvSegs a, NormAct a
     const GemvSegs<1> segs{{w + (size_t)ra * nb * kBlockBytes}, {sc + (size_t)ra * nb}};
     const float val =
         gemv_tile<DT, U, true, 1>(segs, nullptr, nullptr, nb, nrows, tile_rows, nb_magic, smem,
-                                  NormActR<R, EMB>{act});
+                                  NormActR<R, EMB>{act}, 0);
+    QH_WSTAMP(0, 3);
     if ((int)threadIdx.x < nrows) out[ra + threadIdx.x] = val;
 }
 
@@ -1515,11 +1525,15 @@ __global__ __launch_bounds__(256) void gemv_residual_kernel(const uint8_t* __res
                                                             const float* __restrict__ xd, int nb, int rows,
                                                             int tile_rows, uint32_t nb_magic, float* __restrict__ x) {
     extern __shared__ __align__(16) float smem[];
+    const int tlk = nb > 64 ? 4 : 2;  // timeline id: the down projection (K = 4864) or o (K = 896)
+    (void)tlk;
+    QH_WSTAMP(tlk, 0);
     const int tid = (int)threadIdx.x;
     const int ra = (int)blockIdx.x * tile_rows;
     const int nrows = min(tile_rows, rows - ra);
     const float x0 = x[ra + min(tid, nrows - 1)];  // the residual row, in flight with the weights
-    const float val = gemv_tile<DT, U, XL>(wq, wscale, xq, xd, nb, ra, nrows, tile_rows, nb_magic, smem);
+    const float val = gemv_tile<DT, U, XL>(wq, wscale, xq, xd, nb, ra, nrows, tile_rows, nb_magic, smem, tlk);
+    QH_WSTAMP(tlk, 3);
     if (tid < nrows) x[ra + tid] = x0 + val;
 }
 
@@ -1535,6 +1549,7 @@ __global__ __launch_bounds__(256) void gemv_swiglu_norm_kernel(const uint8_t* __
                                                                float* __restrict__ od) {
     extern __shared__ __align__(16) float smem[];
     __shared__ uint64_t exptab[32];
+    QH_WSTAMP(3, 0);
     ExpTab et;
     et.load();
     const int tid = (int)threadIdx.x, ra = (int)blockIdx.x * QK;
@@ -1543,7 +1558,8 @@ __global__ __launch_bounds__(256) void gemv_swiglu_norm_kernel(const uint8_t* __
     const GemvSegs<2> segs{{wg + (size_t)ra * nb * kBlockBytes, wu + (size_t)ra * nb * kBlockBytes},
                            {sg + (size_t)ra * nb, su + (size_t)ra * nb}};
     const float val =
-        gemv_tile<DT, U, true, 2>(segs, nullptr, nullptr, nb, QK, 2 * QK, nb_magic, smem, NormActR<R, false>{act});
+        gemv_tile<DT, U, true, 2>(segs, nullptr, nullptr, nb, QK, 2 * QK, nb_magic, smem, NormActR<R, false>{act}, 3);
+    QH_WSTAMP(3, 3);
     // wave 0 holds the block's 32 gate rows in lanes 0-31 and its 32 up rows in lanes 32-63: one half swap hands
     // lane l its up value (the exp table is stored by lanes 0-31 of the same wave, so no barrier is needed)
     if (tid < 2 * QK) {  // wave 0
@@ -1677,6 +1693,7 @@ const uint16_t* scales(const qh_tensor& W) {
 uint32_t nb_magic(int nb) { return nb == 1 ? 0u : (uint32_t)((0x100000000ull + (uint64_t)nb - 1) / (uint64_t)nb); }
 
 hipError_t dalloc(Decoder* d, void** p, size_t bytes) {
+    if (fault_alloc_fires()) return hipErrorOutOfMemory;  // qh_fault_alloc's forced failure
     hipError_t e = hipMalloc(p, bytes < 256 ? 256 : bytes);
     if (e == hipSuccess) d->allocs.push_back(*p);
     return e;
@@ -1752,6 +1769,7 @@ NormAct make_norm(Decoder* d, bool embedding, const float* w) {
     a.w = w;
     a.eps = d->hp.norm_eps;
     a.D = d->hp.dim;
+    a.tlk = -1;
     return a;
 }
 
@@ -1826,7 +1844,8 @@ hipError_t gate_up(Decoder* d, int l, hipStream_t s) {
     const size_t lds = norm_tile_lds(wg.cols, 2 * QK, d->hp.dim);
     if (d->fuse && wg.dtype == wu.dtype && lds <= kFuseLds) {
         const unsigned grid = (unsigned)(wg.rows / QK);
-        const NormAct act = make_norm(d, false, lf(d, l, L_FFN_NORM));
+        NormAct act = make_norm(d, false, lf(d, l, L_FFN_NORM));
+        act.tlk = 3;
         by_row_slots(d->hp.dim, [&](auto r) {
             constexpr int R = decltype(r)::value;
             if (wg.dtype == kQ8)
@@ -1876,7 +1895,9 @@ hipError_t decode_layers(Decoder* d, hipStream_t s) {
         GemvPlan p;
         size_t lds = 0;
         if (qkv_plan(d, l, &p, &lds)) {
-            QH_TRY(launch_qkv_norm(d, l, p, lds, make_norm(d, l == 0, lf(d, l, L_ATTN_NORM)), s));
+            NormAct act = make_norm(d, l == 0, lf(d, l, L_ATTN_NORM));
+            act.tlk = 0;
+            QH_TRY(launch_qkv_norm(d, l, p, lds, act, s));
         } else {
             if (l == 0)
                 QH_TRY(embed(d, d->tokens, 1, s));
@@ -2172,6 +2193,9 @@ int decoder_ctx(const Decoder* d) { return d->hp.ctx_len; }
 #if defined(QH_TIMELINE)
 extern "C" int qh_timeline_read(uint64_t* host, int n) {
     return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(qh_tl), sizeof(uint64_t) * (size_t)n);
+}
+extern "C" int qh_timeline_wg_read(uint64_t* host) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(qh_tl_wg), sizeof(qh_tl_wg));
 }
 #endif
 

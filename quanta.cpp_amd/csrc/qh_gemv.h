@@ -19,6 +19,22 @@
 
 namespace qh {
 
+// Per-workgroup timeline stamps of the decode GEMV kernels, compiled in only with -DQH_TIMELINE: thread 0 of each
+// workgroup records the constant-rate real-time clock ([kernel][workgroup < 1024][stamp < 6]; each translation unit
+// has its own array, read out by the decoder's qh_timeline_wg_read).
+#if defined(QH_TIMELINE)
+static __device__ uint64_t qh_tl_wg[8][1024][6];
+#define QH_WSTAMP(k, i)                                                                                     \
+    do {                                                                                                    \
+        if ((k) >= 0 && threadIdx.x == 0 && blockIdx.x < 1024 && blockIdx.y == 0)                          \
+            qh_tl_wg[(k)][blockIdx.x][(i)] = __builtin_amdgcn_s_memrealtime();                              \
+    } while (0)
+#else
+#define QH_WSTAMP(k, i) \
+    do {                \
+    } while (0)
+#endif
+
 // One pass of a workgroup: U chunks of 16 bytes per thread, the block scale of each chunk and, unless the
 // activation is staged in LDS (XL), the activation bytes the chunk pairs with. The chunk index is clamped
 // into the tile, so every load is unconditional and all of them go out back to back.
@@ -142,7 +158,8 @@ struct GlobalAct {
 template <int DT, int U, bool XL, int NSEG = 1, typename Act = GlobalAct>
 __device__ __forceinline__ float gemv_tile(const GemvSegs<NSEG>& sg, const int8_t* __restrict__ xq,
                                            const float* __restrict__ xd, int nb, int nrows, int tile_rows,
-                                           uint32_t nb_magic, float* smem, const Act& act) {
+                                           uint32_t nb_magic, float* smem, const Act& act, int tlk = -1) {
+    (void)tlk;
     constexpr int kChunksPerBlock = DT == kQ8 ? 2 : 1;
     const int L = chain_len32(nb), zp = L - nb, pstride = chain_stride32(nb);
     float* dxs = smem;                          // [L] activation scales, zp zeros first
@@ -160,6 +177,7 @@ __device__ __forceinline__ float gemv_tile(const GemvSegs<NSEG>& sg, const int8_
     act.template fill<XL>(pre, xs, xds);
     zero_chain_prefix(dxs, prod, nb, vrows);
     if constexpr (XL) __syncthreads();
+    QH_WSTAMP(tlk, 1);
     float* prow = prod + zp;
     if (nchunks <= 256 * U) {  // uniform: a single pass
         cur.products(prow, pstride, 0, nchunks, xs);
@@ -175,6 +193,7 @@ __device__ __forceinline__ float gemv_tile(const GemvSegs<NSEG>& sg, const int8_
             }
         }
     }
+    QH_WSTAMP(tlk, 2);
     __syncthreads();
     return tid < vrows ? chain_lds_pipe(prod + tid * pstride, dxs, L) : 0.0f;
 }
@@ -183,10 +202,11 @@ __device__ __forceinline__ float gemv_tile(const GemvSegs<NSEG>& sg, const int8_
 template <int DT, int U, bool XL>
 __device__ __forceinline__ float gemv_tile(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wscale,
                                            const int8_t* __restrict__ xq, const float* __restrict__ xd, int nb,
-                                           int ra, int nrows, int tile_rows, uint32_t nb_magic, float* smem) {
+                                           int ra, int nrows, int tile_rows, uint32_t nb_magic, float* smem,
+                                           int tlk = -1) {
     constexpr int kBlockBytes = DT == kQ8 ? QK : QK / 2;
     const GemvSegs<1> sg{{wq + (size_t)ra * nb * kBlockBytes}, {wscale + (size_t)ra * nb}};
-    return gemv_tile<DT, U, XL, 1>(sg, xq, xd, nb, nrows, tile_rows, nb_magic, smem, GlobalAct{xq, xd, nb});
+    return gemv_tile<DT, U, XL, 1>(sg, xq, xd, nb, nrows, tile_rows, nb_magic, smem, GlobalAct{xq, xd, nb}, tlk);
 }
 
 }  // namespace qh

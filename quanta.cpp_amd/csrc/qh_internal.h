@@ -46,6 +46,8 @@ int fail(int code, const char* fmt, ...);
 
 // Maps a HIP status to QH_ERR_HIP with context, QH_OK otherwise.
 int check_hip(hipError_t e, const char* what);
+// True when qh_fault_alloc's forced failure is due for this allocation (counts allocations down while armed).
+bool fault_alloc_fires();
 
 // Launch configuration of the decode GEMV for one (dtype, cols) pair.
 struct GemvPlan {

@@ -118,3 +118,18 @@ def test_noalloc_entry_point_host_checks(qh):
     L = qh.lib()
     assert L.qh_shortlist_head_noalloc(None, None, None, None, None, None, None, None) == qh.ERR_ARG
     assert b"null argument" in L.qh_last_error()
+
+
+def test_forced_allocation_failure(qh):
+    """qh_fault_alloc: the armed allocation fails with QH_ERR_NOMEM before any HIP call (so on a machine without a
+    GPU too), the out pointer is cleared, and the hook disarms itself after firing."""
+    L = qh.lib()
+    p = C.c_void_p(1234)
+    try:
+        assert L.qh_fault_alloc(0) == 0
+        assert L.qh_malloc(C.byref(p), 4096) == qh.ERR_NOMEM
+        assert p.value is None
+        assert b"forced allocation failure" in L.qh_last_error()
+        assert L.qh_malloc(C.byref(p), 0) == 0  # an empty allocation is no allocation: nothing to fail
+    finally:
+        L.qh_fault_alloc(-1)
