@@ -92,15 +92,16 @@ int screen_tile_rows(int nb) {
     return t < 2 ? 2 : t;
 }
 
-// Screen shares: four per compute unit, an even number of rows (whole 4-byte error words), at least one tile and at
-// most kScreenMaxShare rows each; share p holds rows [p * share, min((p + 1) * share, V)).
+// Screen shares: two per compute unit (against four, 1 us less for the 151,936-row head: each workgroup's start-up
+// is spread over more tiles), an even number of rows (whole 4-byte error words), at least one tile and at most
+// kScreenMaxShare rows each; share p holds rows [p * share, min((p + 1) * share, V)).
 struct ScreenShape {
     int tile, share, grid;
 };
 ScreenShape screen_shape(int V, int nb) {
     ScreenShape sh;
     sh.tile = screen_tile_rows(nb);
-    const int g = 4 * device_cus();
+    const int g = 2 * device_cus();
     int share = ((V + g - 1) / g + 1) & ~1;
     share = share > sh.tile ? share : sh.tile;
     share = share < kScreenMaxShare ? share : kScreenMaxShare;
