@@ -1923,6 +1923,17 @@ hipError_t decode_layers(Decoder* d, hipStream_t s) {
     return hipSuccess;
 }
 
+// Matrices over one activation, in as few launches as their formats allow: runs of one dtype and width share one.
+hipError_t matmul_group(const MmOut* m, int k, const int8_t* xq, const float* xd, int n, hipStream_t s) {
+    for (int i = 0; i < k;) {
+        int j = i + 1;
+        while (j < k && m[j].W->dtype == m[i].W->dtype && m[j].W->cols == m[i].W->cols) ++j;
+        QH_TRY(launch_matmul_segs(m + i, j - i, xq, xd, n, s));
+        i = j;
+    }
+    return hipSuccess;
+}
+
 // All layers for a chunk of n tokens whose embeddings are in d->x[0..n) and normed inputs in qa / da, positions
 // from *d->pos. Leaves the last layer's down projection in d->o (not yet added to the residual stream).
 hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
@@ -1937,9 +1948,9 @@ hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
             QH_TRY(hipGetLastError());
         }
         const qh_tensor &wq = lt(d, l, L_WQ), &wk = lt(d, l, L_WK), &wv = lt(d, l, L_WV);
-        QH_TRY(launch_matmul(d->q, wq.rows, wq, d->qa, d->da, n, 0, wq.rows, s));
-        QH_TRY(launch_matmul(d->k, wk.rows, wk, d->qa, d->da, n, 0, wk.rows, s));
-        QH_TRY(launch_matmul(d->v, wv.rows, wv, d->qa, d->da, n, 0, wv.rows, s));
+        const MmOut qkv[3] = {{&wq, d->q, wq.rows, 0, wq.rows}, {&wk, d->k, wk.rows, 0, wk.rows},
+                              {&wv, d->v, wv.rows, 0, wv.rows}};
+        QH_TRY(matmul_group(qkv, 3, d->qa, d->da, n, s));
         QH_TRY(attention(d, l, n, s));
         const qh_tensor& wo = lt(d, l, L_WO);
         QH_TRY(launch_matmul(d->o, wo.rows, wo, d->qb, d->db, n, 0, wo.rows, s));
@@ -1949,8 +1960,8 @@ hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
         });
         QH_TRY(hipGetLastError());
         const qh_tensor &wg = lt(d, l, L_WG), &wu = lt(d, l, L_WU), &wd = lt(d, l, L_WD);
-        QH_TRY(launch_matmul(d->g, wg.rows, wg, d->qa, d->da, n, 0, wg.rows, s));
-        QH_TRY(launch_matmul(d->u, wu.rows, wu, d->qa, d->da, n, 0, wu.rows, s));
+        const MmOut gu[2] = {{&wg, d->g, wg.rows, 0, wg.rows}, {&wu, d->u, wu.rows, 0, wu.rows}};
+        QH_TRY(matmul_group(gu, 2, d->qa, d->da, n, s));
         const long nblk = (long)n * F / QK;
         qh_launch(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g,
                            d->u, nblk, d->qb, d->db);

@@ -71,6 +71,14 @@ hipError_t launch_gemv(float* out, const qh_tensor& W, const int8_t* xq, const f
                        const GemvPlan& plan, hipStream_t s);
 hipError_t launch_matmul(float* out, int ldo, const qh_tensor& W, const int8_t* xq, const float* xd, int n,
                          int r0, int r1, hipStream_t s);
+// One matrix of a fused launch: rows [r0, r1) of W, output row r of token t at out[t * ldo + r].
+struct MmOut {
+    const qh_tensor* W;
+    float* out;
+    int ldo, r0, r1;
+};
+// Up to three matrices of one dtype and width over the same activation in one launch (prefill q / k / v, gate / up).
+hipError_t launch_matmul_segs(const MmOut* m, int n_mats, const int8_t* xq, const float* xd, int n, hipStream_t s);
 size_t argmax_workspace_bytes(int n);
 hipError_t launch_argmax(const float* logits, int n, int32_t* index, void* ws, hipStream_t s);
 

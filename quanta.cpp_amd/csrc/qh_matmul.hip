@@ -56,12 +56,46 @@ struct MmRegs {
 
 }  // namespace
 
+// Up to three matrices of one dtype and width, same activation, in one launch (q / k / v, gate / up): their row tiles
+// are numbered one after another, segment s covering rows [r0[s], r1[s]) of its matrix and writing its output rows to
+// out[s][token * ldo[s] + row].
+struct MmSegs {
+    const uint8_t* wq[3];
+    const uint16_t* ws[3];
+    float* out[3];
+    int ldo[3], r0[3], r1[3];
+    int tiles[3];  // row tiles of 16 per segment (0 for unused ones)
+};
+
+// The segment of row tile rt (launch-wide numbering) and its matrix, rows and output; rt becomes the tile's index
+// within the segment. Uniform per workgroup: all of it stays in scalar registers.
+struct MmSeg {
+    const uint8_t* wq;
+    const uint16_t* ws;
+    float* out;
+    int ldo, r0, r1;
+    __device__ __forceinline__ MmSeg(const MmSegs& sg, int& rt) {
+        int s = 0;
+        if (rt >= sg.tiles[0]) {
+            rt -= sg.tiles[0];
+            s = 1;
+            if (rt >= sg.tiles[1]) {
+                rt -= sg.tiles[1];
+                s = 2;
+            }
+        }
+        wq = s == 0 ? sg.wq[0] : s == 1 ? sg.wq[1] : sg.wq[2];
+        ws = s == 0 ? sg.ws[0] : s == 1 ? sg.ws[1] : sg.ws[2];
+        out = s == 0 ? sg.out[0] : s == 1 ? sg.out[1] : sg.out[2];
+        ldo = s == 0 ? sg.ldo[0] : s == 1 ? sg.ldo[1] : sg.ldo[2];
+        r0 = s == 0 ? sg.r0[0] : s == 1 ? sg.r0[1] : sg.r0[2];
+        r1 = s == 0 ? sg.r1[0] : s == 1 ? sg.r1[1] : sg.r1[2];
+    }
+};
+
 template <int DT, int TT, int KC>
-__global__ __launch_bounds__(kMmThreads) void matmul_lds_kernel(float* __restrict__ out, int ldo,
-                                                            const uint8_t* __restrict__ wq,
-                                                            const uint16_t* __restrict__ wscale,
-                                                            const int8_t* __restrict__ xq, const float* __restrict__ xd,
-                                                            int cols, int n, int r0, int r1, int n_tg) {
+__global__ __launch_bounds__(kMmThreads) void matmul_lds_kernel(MmSegs segs, const int8_t* __restrict__ xq,
+                                                            const float* __restrict__ xd, int cols, int n, int n_tg) {
     using S = MmShape<TT, KC>;
     constexpr int kTok = S::kTok, kTokPad = S::kTokPad, kBpw = S::kBpw;
     __shared__ int sl[KC][16][kTokPad];     // int32 block sums
@@ -75,7 +109,13 @@ __global__ __launch_bounds__(kMmThreads) void matmul_lds_kernel(float* __restric
     const int G = (int)gridDim.x, p = (int)blockIdx.x;
     const int xcd = p % kXcds, per = G / kXcds, rem = G % kXcds;
     const int logical = xcd * per + min(xcd, rem) + p / kXcds;
-    const int rt = logical / n_tg, tg = logical % n_tg;
+    int rt = logical / n_tg;
+    const int tg = logical % n_tg;
+    const MmSeg sg(segs, rt);
+    const uint8_t* __restrict__ wq = sg.wq;
+    const uint16_t* __restrict__ wscale = sg.ws;
+    float* __restrict__ out = sg.out;
+    const int ldo = sg.ldo, r0 = sg.r0, r1 = sg.r1;
     const int rbase = r0 + rt * 16, tbase = tg * kTok;
 
     // MFMA operands: row (rbase + li) for the weights, tokens (tbase + tt*16 + li) for the activations; rows and
@@ -215,18 +255,21 @@ struct RegChunk {
 };
 
 template <int DT, int TT, int NW, bool VEC>
-__global__ __launch_bounds__(64 * NW) void matmul_reg_kernel(float* __restrict__ out, int ldo,
-                                                            const uint8_t* __restrict__ wq,
-                                                            const uint16_t* __restrict__ wscale,
-                                                            const int8_t* __restrict__ xq, const float* __restrict__ xd,
-                                                            int cols, int n, int r0, int r1, int n_tg) {
+__global__ __launch_bounds__(64 * NW) void matmul_reg_kernel(MmSegs segs, const int8_t* __restrict__ xq,
+                                                            const float* __restrict__ xd, int cols, int n, int n_tg) {
     const int nb = cols / QK;
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
     const int G = (int)gridDim.x, p = (int)blockIdx.x;
     const int xcd = p % kXcds, per = G / kXcds, rem = G % kXcds;
     const int logical = xcd * per + min(xcd, rem) + p / kXcds;
-    const int rt = logical / n_tg, tg = logical % n_tg;
+    int rt = logical / n_tg;
+    const int tg = logical % n_tg;
+    const MmSeg sg(segs, rt);
+    const uint8_t* __restrict__ wq = sg.wq;
+    const uint16_t* __restrict__ wscale = sg.ws;
+    float* __restrict__ out = sg.out;
+    const int ldo = sg.ldo, r0 = sg.r0, r1 = sg.r1;
     const int rbase = r0 + rt * 16;
     const int tbase = (tg * NW + wave) * TT * 16;
     if (tbase >= n) return;  // uniform per wave; nothing below synchronises across waves
@@ -389,50 +432,61 @@ MmPlan matmul_plan(int rows, int cols, int n) {
 }
 
 template <int DT, int TT, int KC>
-void launch_mm_lds(float* out, int ldo, const uint8_t* wq, const uint16_t* ws, const int8_t* xq, const float* xd,
-                   int cols, int n, int r0, int r1, hipStream_t s) {
-    const int row_tiles = (r1 - r0 + 15) / 16;
+void launch_mm_lds(const MmSegs& sg, int row_tiles, const int8_t* xq, const float* xd, int cols, int n, hipStream_t s) {
     const int n_tg = (n + 16 * TT - 1) / (16 * TT);
-    qh_launch((matmul_lds_kernel<DT, TT, KC>), dim3((unsigned)(row_tiles * n_tg)), dim3(kMmThreads), 0, s,
-                       out, ldo, wq, ws, xq, xd, cols, n, r0, r1, n_tg);
+    qh_launch((matmul_lds_kernel<DT, TT, KC>), dim3((unsigned)(row_tiles * n_tg)), dim3(kMmThreads), 0, s, sg, xq,
+              xd, cols, n, n_tg);
 }
 
 template <int DT, int TT, int NW, bool VEC>
-void launch_mm_reg(float* out, int ldo, const uint8_t* wq, const uint16_t* ws, const int8_t* xq, const float* xd,
-                   int cols, int n, int r0, int r1, hipStream_t s) {
-    const int row_tiles = (r1 - r0 + 15) / 16;
+void launch_mm_reg(const MmSegs& sg, int row_tiles, const int8_t* xq, const float* xd, int cols, int n, hipStream_t s) {
     const int waves = (n + 16 * TT - 1) / (16 * TT);
     const int n_tg = (waves + NW - 1) / NW;
-    qh_launch((matmul_reg_kernel<DT, TT, NW, VEC>), dim3((unsigned)(row_tiles * n_tg)), dim3(64 * NW), 0, s,
-                       out, ldo, wq, ws, xq, xd, cols, n, r0, r1, n_tg);
+    qh_launch((matmul_reg_kernel<DT, TT, NW, VEC>), dim3((unsigned)(row_tiles * n_tg)), dim3(64 * NW), 0, s, sg, xq,
+              xd, cols, n, n_tg);
 }
 
 }  // namespace
 
-hipError_t launch_matmul(float* out, int ldo, const qh_tensor& W, const int8_t* xq, const float* xd, int n, int r0,
-                         int r1, hipStream_t s) {
-    const uint8_t* wq = static_cast<const uint8_t*>(W.data);
-    const uint16_t* ws = reinterpret_cast<const uint16_t*>(wq + qh_quant_bytes(W.dtype, W.rows, W.cols));
-    const MmPlan pl = matmul_plan(r1 - r0, W.cols, n);
+// The matrices of one launch: up to three of one dtype and width (row ranges [r0, r1) each), same activation.
+hipError_t launch_matmul_segs(const MmOut* m, int n_mats, const int8_t* xq, const float* xd, int n, hipStream_t s) {
+    if (n_mats < 1 || n_mats > 3) return hipErrorInvalidValue;
+    MmSegs sg{};
+    int row_tiles = 0;
+    const qh_tensor& W = *m[0].W;
+    for (int i = 0; i < n_mats; ++i) {
+        const qh_tensor& Wi = *m[i].W;
+        if (Wi.dtype != W.dtype || Wi.cols != W.cols) return hipErrorInvalidValue;
+        const uint8_t* wq = static_cast<const uint8_t*>(Wi.data);
+        sg.wq[i] = wq;
+        sg.ws[i] = reinterpret_cast<const uint16_t*>(wq + qh_quant_bytes(Wi.dtype, Wi.rows, Wi.cols));
+        sg.out[i] = m[i].out;
+        sg.ldo[i] = m[i].ldo;
+        sg.r0[i] = m[i].r0;
+        sg.r1[i] = m[i].r1;
+        sg.tiles[i] = (m[i].r1 - m[i].r0 + 15) / 16;
+        row_tiles += sg.tiles[i];
+    }
+    const MmPlan pl = matmul_plan(row_tiles * 16, W.cols, n);
     const bool vec = (W.cols / QK) % 4 == 0 && (reinterpret_cast<uintptr_t>(xd) & 15u) == 0;
     if (!pl.reg) {
-#define QH_MM_LDS(DT, TT, KC)                                                          \
-        if (W.dtype == DT && pl.tt == TT) {                                            \
-            launch_mm_lds<DT, TT, KC>(out, ldo, wq, ws, xq, xd, W.cols, n, r0, r1, s); \
-            return hipGetLastError();                                                  \
+#define QH_MM_LDS(DT, TT, KC)                                                  \
+        if (W.dtype == DT && pl.tt == TT) {                                    \
+            launch_mm_lds<DT, TT, KC>(sg, row_tiles, xq, xd, W.cols, n, s);    \
+            return hipGetLastError();                                          \
         }
         QH_MM_LDS(kQ8, 1, 16) QH_MM_LDS(kQ8, 2, 16) QH_MM_LDS(kQ8, 4, 8)
         QH_MM_LDS(kQ4, 1, 16) QH_MM_LDS(kQ4, 2, 16) QH_MM_LDS(kQ4, 4, 8)
 #undef QH_MM_LDS
         return hipErrorInvalidValue;
     }
-#define QH_MM_REG(DT, TT, NW)                                                                          \
-    if (W.dtype == DT && pl.tt == TT && pl.nw == NW) {                                                 \
-        if (vec)                                                                                       \
-            launch_mm_reg<DT, TT, NW, true>(out, ldo, wq, ws, xq, xd, W.cols, n, r0, r1, s);           \
-        else                                                                                           \
-            launch_mm_reg<DT, TT, NW, false>(out, ldo, wq, ws, xq, xd, W.cols, n, r0, r1, s);          \
-        return hipGetLastError();                                                                      \
+#define QH_MM_REG(DT, TT, NW)                                                                \
+    if (W.dtype == DT && pl.tt == TT && pl.nw == NW) {                                       \
+        if (vec)                                                                             \
+            launch_mm_reg<DT, TT, NW, true>(sg, row_tiles, xq, xd, W.cols, n, s);            \
+        else                                                                                 \
+            launch_mm_reg<DT, TT, NW, false>(sg, row_tiles, xq, xd, W.cols, n, s);           \
+        return hipGetLastError();                                                            \
     }
     QH_MM_REG(kQ8, 1, 1) QH_MM_REG(kQ8, 1, 2) QH_MM_REG(kQ8, 1, 4) QH_MM_REG(kQ8, 2, 1) QH_MM_REG(kQ8, 2, 2)
     QH_MM_REG(kQ8, 2, 4) QH_MM_REG(kQ8, 4, 1) QH_MM_REG(kQ8, 4, 2) QH_MM_REG(kQ8, 4, 4)
@@ -440,6 +494,12 @@ hipError_t launch_matmul(float* out, int ldo, const qh_tensor& W, const int8_t* 
     QH_MM_REG(kQ4, 2, 4) QH_MM_REG(kQ4, 4, 1) QH_MM_REG(kQ4, 4, 2) QH_MM_REG(kQ4, 4, 4)
 #undef QH_MM_REG
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_matmul(float* out, int ldo, const qh_tensor& W, const int8_t* xq, const float* xd, int n, int r0,
+                         int r1, hipStream_t s) {
+    const MmOut m{&W, out, ldo, r0, r1};
+    return launch_matmul_segs(&m, 1, xq, xd, n, s);
 }
 
 }  // namespace qh
