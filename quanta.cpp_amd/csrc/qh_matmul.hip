@@ -20,6 +20,7 @@
 // (workgroups are dealt to the 8 XCDs round-robin), where the weights they all read stay in that XCD's L2.
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include "qh_device.h"
 #include "qh_internal.h"
@@ -209,19 +210,24 @@ __global__ __launch_bounds__(kMmThreads) void matmul_lds_kernel(MmSegs segs, con
         __syncthreads();
     };
 
+    // sched_barrier keeps each chunk's loads issued ahead of the reduction they overlap (the scheduler would otherwise
+    // sink them below that reduction's waits, leaving no load in flight while a chunk is reduced).
     const int n_chunks = (nb + KC - 1) / KC;
     MmRegs<DT, TT, KC> A, B;
     load(A, 0);
     int c = 0;
     while (c + 2 < n_chunks) {
         load(B, (c + 1) * KC);
+        __builtin_amdgcn_sched_barrier(0);
         reduce(A, c * KC);
         load(A, (c + 2) * KC);
+        __builtin_amdgcn_sched_barrier(0);
         reduce(B, (c + 1) * KC);
         c += 2;
     }
     if (c + 1 < n_chunks) {
         load(B, (c + 1) * KC);
+        __builtin_amdgcn_sched_barrier(0);
         reduce(A, c * KC);
         reduce(B, (c + 1) * KC);
     } else {
@@ -236,6 +242,179 @@ __global__ __launch_bounds__(kMmThreads) void matmul_lds_kernel(MmSegs segs, con
             if (r < r1) out[(size_t)tok * ldo + r] = acc[j];
         }
     }
+}
+
+// Staged variant for few (row tile, token tile) pairs: the chunk's weights, activation codes and scales are brought
+// into LDS by coalesced 16-byte loads (8 full cache lines per wave instruction, against 16 partly used lines for an
+// operand loaded in MFMA layout, whose per-CU address processing bounds the other kernels at 32 tokens), two chunks
+// ahead in registers; the waves then read their MFMA operands from LDS. Tile, block split across waves, block sums and
+// chains are the LDS kernel's: wave w multiplies blocks 4w..4w+3 of each 16-block chunk, all 256 threads run one
+// (row, token) chain each.
+constexpr int kStKC = 16;  // blocks per chunk
+template <int DT>
+struct StageRegs {
+    static constexpr int kBw = DT == kQ8 ? QK : QK / 2;         // weight bytes per block
+    static constexpr int kAu = 16 * kStKC * kBw / 16 / kMmThreads;  // 16-byte weight units per thread (2 / 1)
+    static constexpr int kXu = 16 * kStKC * QK / 16 / kMmThreads;   // 16-byte activation units per thread (2)
+    uint4 a[kAu];
+    uint4 x[kXu];
+    uint16_t dw;  // row tid / 16, block tid % 16
+    float dx;     // token tid / 16, block tid % 16
+};
+
+template <int DT>
+__global__ __launch_bounds__(kMmThreads) void matmul_stage_kernel(MmSegs segs, const int8_t* __restrict__ xq,
+                                                              const float* __restrict__ xd, int cols, int n,
+                                                              int n_tg) {
+    using R = StageRegs<DT>;
+    constexpr int KC = kStKC, kBw = R::kBw;
+    constexpr int kArow = KC * kBw + 16;  // LDS row strides in bytes: = 4 dwords mod 64 banks, so the 16 rows x 2
+    constexpr int kXrow = KC * QK + 16;   // lane groups of a half-wave operand read hit 64 distinct banks
+    constexpr int kAupr = KC * kBw / 16, kXupr = KC * QK / 16;  // 16-byte units per row
+    __shared__ __align__(16) uint8_t as[2][16 * kArow];
+    __shared__ __align__(16) int8_t xs[2][16 * kXrow];
+    __shared__ float dws[2][16][KC + 1];
+    __shared__ float dxs[2][16][KC + 1];
+    __shared__ int sl[KC][16][20];
+    const int nb = cols / QK;
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lq = lane >> 4;
+
+    const int G = (int)gridDim.x, p = (int)blockIdx.x;
+    const int xcd = p % kXcds, per = G / kXcds, rem = G % kXcds;
+    const int logical = xcd * per + min(xcd, rem) + p / kXcds;
+    int rt = logical / n_tg;
+    const int tg = logical % n_tg;
+    const MmSeg sg(segs, rt);
+    const int r0 = sg.r0, r1 = sg.r1;
+    const int rbase = r0 + rt * 16, tbase = tg * 16;
+    const size_t wrow_bytes = (size_t)nb * kBw;
+
+    // Per-thread source rows of the staged units (rows and tokens past the end clamped: loaded, never stored).
+    const uint8_t* asrc[R::kAu];
+    int aoff[R::kAu];
+#pragma unroll
+    for (int j = 0; j < R::kAu; ++j) {
+        const int e = j * kMmThreads + tid;
+        asrc[j] = sg.wq + (size_t)min(rbase + e / kAupr, r1 - 1) * wrow_bytes;
+        aoff[j] = (e % kAupr) * 16;
+    }
+    const int8_t* xsrc[R::kXu];
+    int xoff[R::kXu];
+#pragma unroll
+    for (int j = 0; j < R::kXu; ++j) {
+        const int e = j * kMmThreads + tid;
+        xsrc[j] = xq + (size_t)min(tbase + e / kXupr, n - 1) * cols;
+        xoff[j] = (e % kXupr) * 16;
+    }
+    const uint16_t* dwsrc = sg.ws + (size_t)min(rbase + tid / 16, r1 - 1) * nb;
+    const float* dxsrc = xd + (size_t)min(tbase + tid / 16, n - 1) * nb;
+    const int sk = tid % 16;
+
+    // Chunk c0's operands into registers; byte offsets past the end of a row are clamped to its last unit.
+    auto load = [&](R& S, int c0) {
+#pragma unroll
+        for (int j = 0; j < R::kAu; ++j)
+            S.a[j] = load16(asrc[j] + min((size_t)c0 * kBw + aoff[j], wrow_bytes - 16));
+#pragma unroll
+        for (int j = 0; j < R::kXu; ++j)
+            S.x[j] = load16(xsrc[j] + min(c0 * QK + xoff[j], cols - 16));
+        const int b = min(c0 + sk, nb - 1);
+        S.dw = dwsrc[b];
+        S.dx = dxsrc[b];
+    };
+    auto stage = [&](const R& S, int buf) {
+#pragma unroll
+        for (int j = 0; j < R::kAu; ++j) {
+            const int e = j * kMmThreads + tid;
+            *reinterpret_cast<uint4*>(&as[buf][(e / kAupr) * kArow + (e % kAupr) * 16]) = S.a[j];
+        }
+#pragma unroll
+        for (int j = 0; j < R::kXu; ++j) {
+            const int e = j * kMmThreads + tid;
+            *reinterpret_cast<uint4*>(&xs[buf][(e / kXupr) * kXrow + (e % kXupr) * 16]) = S.x[j];
+        }
+        dws[buf][tid / 16][sk] = f16_to_f32(S.dw);
+        dxs[buf][tid / 16][sk] = S.dx;
+    };
+    const int shift = DT == kQ8 ? 0 : (lq >> 1) * 4;
+    // The wave's 4 blocks: operands read together, 4 independent MFMAs, then the block sums out.
+    auto products = [&](int buf) {
+        long a[4], x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int bl = wave * 4 + i;
+            a[i] = *reinterpret_cast<const long*>(&as[buf][li * kArow + bl * kBw + (DT == kQ8 ? lq * 8 : (lq & 1) * 8)]);
+            x[i] = *reinterpret_cast<const long*>(&xs[buf][li * kXrow + bl * QK + lq * 8]);
+        }
+        v4i c[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            long ai = a[i];
+            if (DT == kQ4) {
+                const uint64_t v = (uint64_t)ai;
+                const uint32_t lo = nibbles_to_i8(((uint32_t)v >> shift) & 0x0F0F0F0Fu);
+                const uint32_t hi = nibbles_to_i8(((uint32_t)(v >> 32) >> shift) & 0x0F0F0F0Fu);
+                ai = (long)(((uint64_t)hi << 32) | lo);
+            }
+            c[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ai, x[i], (v4i){0, 0, 0, 0}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) sl[wave * 4 + i][4 * lq + k][li] = c[i][k];
+    };
+    // Chain of this thread: row tid / 16, token tid % 16 (the LDS kernel's pairing at one token tile).
+    const int crow = tid / 16, ctok = tid % 16;
+    float acc = 0.0f;
+    auto chains = [&](int buf, int c0) {
+        const int nblk = min(KC, nb - c0);
+        float pv[KC], dxv[KC];
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+            pv[k] = (float)sl[k][crow][ctok] * dws[buf][crow][k];
+            dxv[k] = dxs[buf][ctok][k];
+        }
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+            const float nx = __builtin_fmaf(pv[k], dxv[k], acc);
+            acc = k < nblk ? nx : acc;
+        }
+    };
+
+    // Chunk c is in LDS buffer c % 2 when its products start; the register sets hold chunks c + 1 and c + 2 (loads
+    // in flight), and each set is refilled with the chunk two past the one it hands to LDS. Loads past the last chunk
+    // are clamped re-reads whose values are never used.
+    const int n_chunks = (nb + KC - 1) / KC;
+    R S0, S1;
+    load(S0, 0);
+    load(S1, KC);
+    __builtin_amdgcn_sched_barrier(0);
+    stage(S0, 0);
+    load(S0, 2 * KC);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    for (int c = 0;; c += 2) {
+        products(0);
+        __syncthreads();
+        chains(0, c * KC);
+        if (c + 1 >= n_chunks) break;
+        stage(S1, 1);
+        load(S1, (c + 3) * KC);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        products(1);
+        __syncthreads();
+        chains(1, (c + 1) * KC);
+        if (c + 2 >= n_chunks) break;
+        stage(S0, 0);
+        load(S0, (c + 4) * KC);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+    }
+
+    const int tok = tbase + ctok, r = rbase + crow;
+    if (tok < n && r < r1) sg.out[(size_t)tok * sg.ldo + r] = acc;
 }
 
 // Register-chain variant: a wave owns 16 rows x 16*TT tokens over all of K and runs the chains of its own MFMA
@@ -368,19 +547,23 @@ __global__ __launch_bounds__(64 * NW) void matmul_reg_kernel(MmSegs segs, const 
         }
     };
 
+    // sched_barrier: as in the LDS kernel, each chunk's loads stay issued ahead of the reduction they overlap.
     const int n_chunks = (nb + 3) / 4;
     RegChunk<DT, TT, VEC> A, B;
     load(A, 0);
     int c = 0;
     while (c + 2 < n_chunks) {
         load(B, (c + 1) * 4);
+        __builtin_amdgcn_sched_barrier(0);
         reduce(A, c * 4);
         load(A, (c + 2) * 4);
+        __builtin_amdgcn_sched_barrier(0);
         reduce(B, (c + 1) * 4);
         c += 2;
     }
     if (c + 1 < n_chunks) {
         load(B, (c + 1) * 4);
+        __builtin_amdgcn_sched_barrier(0);
         reduce(A, c * 4);
         reduce(B, (c + 1) * 4);
     } else {
@@ -403,10 +586,11 @@ __global__ __launch_bounds__(64 * NW) void matmul_reg_kernel(MmSegs segs, const 
 namespace {
 
 // Launch plan: kernel family, token tiles (per workgroup for the LDS kernel, per wave for the register kernel) and
-// waves per workgroup. QH_MM="lds:TT" or "reg:TT:NW" overrides the heuristic (tuning sweeps).
+// waves per workgroup. QH_MM="stage", "lds:TT" or "reg:TT:NW" overrides the heuristic (tuning sweeps).
 struct MmPlan {
     bool reg;
     int tt, nw;
+    bool stage = false;  // the LDS-staged kernel (one token tile per workgroup)
 };
 
 MmPlan matmul_plan(int rows, int cols, int n) {
@@ -415,6 +599,7 @@ MmPlan matmul_plan(int rows, int cols, int n) {
     if (env) {
         int a = 0, b = 0;
         if (sscanf(env, "lds:%d", &a) == 1 && (a == 1 || a == 2 || a == 4)) return MmPlan{false, a, 4};
+        if (strcmp(env, "stage") == 0) return MmPlan{false, 1, 4, true};
         if (sscanf(env, "reg:%d:%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && (b == 1 || b == 2 || b == 4))
             return MmPlan{true, a, b};
     }
@@ -425,7 +610,9 @@ MmPlan matmul_plan(int rows, int cols, int n) {
     // tiles take 4 token tiles per wave, others 2, with 2 waves per workgroup once a row tile has 8 waves or more.
     const int row_tiles = (rows + 15) / 16;
     const int tiles = (n + 15) / 16;
-    if ((long)row_tiles * tiles < 1024) return MmPlan{false, 1, 4};
+    // The LDS-staged kernel (coalesced operand loads, one token tile per workgroup) measured 4-12% under the LDS and
+    // register kernels at 32 tokens (q/k/v, o, gate/up, down), and under the LDS kernel wherever that one was chosen.
+    if (tiles <= 2 || (long)row_tiles * tiles < 1024) return MmPlan{false, 1, 4, true};
     pl.tt = row_tiles < 128 ? 4 : 2;
     pl.nw = (pl.tt == 2 && tiles / pl.tt >= 8) ? 2 : 1;
     return pl;
@@ -469,6 +656,18 @@ hipError_t launch_matmul_segs(const MmOut* m, int n_mats, const int8_t* xq, cons
     }
     const MmPlan pl = matmul_plan(row_tiles * 16, W.cols, n);
     const bool vec = (W.cols / QK) % 4 == 0 && (reinterpret_cast<uintptr_t>(xd) & 15u) == 0;
+    bool aligned = (reinterpret_cast<uintptr_t>(xq) & 15u) == 0;
+    for (int i = 0; i < n_mats; ++i) aligned = aligned && (reinterpret_cast<uintptr_t>(sg.wq[i]) & 15u) == 0;
+    if (pl.stage && aligned) {
+        const int n_tg = (n + 15) / 16;
+        if (W.dtype == kQ8)
+            qh_launch(matmul_stage_kernel<kQ8>, dim3((unsigned)(row_tiles * n_tg)), dim3(kMmThreads), 0, s, sg, xq, xd,
+                      W.cols, n, n_tg);
+        else
+            qh_launch(matmul_stage_kernel<kQ4>, dim3((unsigned)(row_tiles * n_tg)), dim3(kMmThreads), 0, s, sg, xq, xd,
+                      W.cols, n, n_tg);
+        return hipGetLastError();
+    }
     if (!pl.reg) {
 #define QH_MM_LDS(DT, TT, KC)                                                  \
         if (W.dtype == DT && pl.tt == TT) {                                    \

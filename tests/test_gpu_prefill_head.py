@@ -205,7 +205,7 @@ def test_shortlist_full_vocab(qh, oracle, synth, gpu):
     assert np.float32(st["top1_logit"]).tobytes() == full[st["top1"]].cpu().numpy().tobytes()
 
 
-@pytest.mark.parametrize("tt", ["lds:1", "lds:2", "lds:4", "reg:1:1", "reg:1:4", "reg:2:2", "reg:4:1", "reg:4:4"])
+@pytest.mark.parametrize("tt", ["stage", "lds:1", "lds:2", "lds:4", "reg:1:1", "reg:1:4", "reg:2:2", "reg:4:1", "reg:4:4"])
 @pytest.mark.parametrize("dtype,N,K", [(2, 200, 896), (3, 200, 896), (2, 40, 4864), (3, 40, 4864)])
 def test_matmul_every_token_tiling(qh, oracle, synth, gpu, monkeypatch, tt, dtype, N, K):
     """Both prefill kernels at every token tiling (LDS-staged block sums, register chains) on ragged shapes: rows not a
