@@ -178,6 +178,16 @@ def head_bench(qh, synth, torch, oracle, steps, warmup):
     for t in range(n_vec):
         heads[0](xq[t], xd[t])
         rows.append(heads[0].stats()["n_rows"])
+    # rescored rows over 1,024 seeded N(0,1)*0.5 hidden states (check_head's statistics, checks.cpp:178-239)
+    n_sweep = 1024
+    xs = torch.from_numpy(synth.activations(502, n_sweep, D, scale=0.5)).cuda()
+    sq, sd = qh.quantize_q8(xs)
+    sweep_rows = []
+    for t in range(n_sweep):
+        heads[0](sq[t], sd[t])
+        sweep_rows.append(heads[0].stats()["n_rows"])
+    sweep_rows = np.array(sweep_rows, np.float64)
+    del xs, sq, sd
 
     def sl_step():
         for c in range(copies):
@@ -207,9 +217,16 @@ def head_bench(qh, synth, torch, oracle, steps, warmup):
     sl_bytes = screen + mean_rows * row8
     full_bytes = V * row8
     del g, heads, r8, r4, re
+    sweep_bytes = screen + sweep_rows * row8
     return {"shortlist_us": sl_us, "full_head_us": full_us, "mean_rows": mean_rows, "rows": rows,
             "shortlist_bytes": sl_bytes, "full_head_bytes": full_bytes,
-            "shortlist_GBps": sl_bytes / sl_us / 1e3, "full_head_GBps": full_bytes / full_us / 1e3}
+            "shortlist_GBps": sl_bytes / sl_us / 1e3, "full_head_GBps": full_bytes / full_us / 1e3,
+            "sweep_1024": {"vectors": n_sweep, "x_seed": 502, "rows_mean": float(sweep_rows.mean()),
+                           "rows_median": float(np.median(sweep_rows)),
+                           "rows_p99": float(np.percentile(sweep_rows, 99)), "rows_max": float(sweep_rows.max()),
+                           "rows_mean_frac_of_vocab": float(sweep_rows.mean() / V),
+                           "bytes_mean": float(sweep_bytes.mean()),
+                           "bytes_mean_frac_of_full_head": float(sweep_bytes.mean() / full_bytes)}}
 
 
 def stage_bytes(hp, pos):
@@ -619,6 +636,12 @@ def main():
                           "us_per_launch": round(head["us_per_launch"], 3),
                           "copies_per_shape": head["copies"]}
     extra = {"q4_gemv_mlp_GBps": round(head["GBps"], 2)}
+    if args.steps != 256:
+        log("decode over 256 steps (positions 512-767) beside the timed run's")
+        e256 = e2e_bench(qh, torch, hp, tens, steps=256, warmup=args.warmup)
+        extra["decode_256_steps"] = {"decode_tok_per_s": round(e256["decode_tok_per_s"], 2),
+                                     "decode_ms_per_token": round(e256["decode_ms_per_token"], 4),
+                                     "stream_equals_reference": e256["stream_equals_reference"]}
     log("decode stages: one traced step per replay")
     st = decode_stages(qh, torch, hp, tens)
     if st is not None:
