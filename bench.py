@@ -564,7 +564,8 @@ def main():
     ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end prefill + decode measurement")
     ap.add_argument("--only", choices=["e2e", "roofline", "prefill", "sampling", "head", "stages"],
                     help="one measurement alone (for counter runs): e2e = --e2e-only; roofline = a 256 MiB copy "
-                         "(counter calibration) then the Q4_0 GEMV rotation; prefill = Q4_0 4864x896 at M = 512")
+                         "(counter calibration) then the Q4_0 GEMV rotation; prefill = Q4_0 4864x896 at M = 512, then "
+                         "9728x896 (the decoder's gate + up rows) at M = 32")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this path runs on a single MI355X "
@@ -587,8 +588,9 @@ def main():
         print(json.dumps({"calibration_copy_bytes": src.numel() * 4, "q4_gemv": rnd(head)}), flush=True)
         return 0
     if args.only == "prefill":
-        r = prefill_rotation(qh, synth, torch, 3, 4864, 896, 512, 5, 1)
-        print(json.dumps({"q4_prefill_4864x896_M512": rnd(r)}), flush=True)
+        out = {"q4_prefill_4864x896_M512": rnd(prefill_rotation(qh, synth, torch, 3, 4864, 896, 512, 5, 1))}
+        out["q4_prefill_9728x896_M32"] = rnd(prefill_rotation(qh, synth, torch, 3, 9728, 896, 32, 5, 1))
+        print(json.dumps(out), flush=True)
         return 0
     if args.only == "head":
         print(json.dumps({"shortlist_head_151936x896": rnd(head_bench(qh, synth, torch, orc.oracle, 5, 1))}),

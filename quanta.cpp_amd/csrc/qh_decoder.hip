@@ -3,24 +3,28 @@
 // greedy token is bit-identical to the reference.
 //
 // Decode (one token) runs five kernels per layer, each with its elementwise work fused in:
-//   qkv        one launch for the q, k and v GEMVs (three row segments, same activation)   (model.cpp:180-182)
-//   attention  per query head: biases, RoPE (host table of glibc powf/cosf/sinf of the reference's formula), this
-//              token's f16 K/V row into the cache, scores (serial FMA dot over head_dim), max, glibc-identical expf,
-//              serial sum in position order, normalise, serial weighted V sum in position order, and the int8
-//              quantization of the head's two 32-blocks of output        (model.cpp:115-137, 183-208, ops_ref.cpp:201-226)
-//   o          GEMV, residual add, then the workgroup that finishes last runs rmsnorm (serial FMA sum of squares, one
-//              rounded 1/sqrt) and quantizes the normed row for the MLP   (model.cpp:208-213, ops_ref.cpp:195-199)
-//   gate/up    one GEMV over the same rows of both matrices, g / (1 + expf(-g)) * u, quantization (ops_ref.cpp:243-248)
-//   down       GEMV, residual add, and the last workgroup normalises for the next layer (or the final norm)
-// then the head (Exact Shortlist Head for top-k queries, full 8-bit head + argmax otherwise). The position and the
-// token live on the device, so a decode step is a fixed launch sequence that can be captured in a HIP graph and
-// replayed: the step reads the token the previous step chose, and its last kernel writes the new token, appends it to
-// the output list and advances the position. A step at a position beyond the context writes nothing into the cache
-// and raises bit 0 of the status word; a prompt token outside the vocabulary raises bit 1.
+//   qkv        one launch for the q, k and v GEMVs (three row segments, same activation); every workgroup first runs
+//              the layer's rmsnorm (serial FMA sum of squares, one rounded 1/sqrt) and quantizes the normed row into
+//              its LDS (layer 0: the token's embedding row)                (model.cpp:179-182, ops_ref.cpp:195-199)
+//   attention  one 16-wave workgroup per query head: biases, RoPE (host table of glibc powf/cosf/sinf of the
+//              reference's formula), this token's f16 K/V row into the cache, scores (serial FMA dot over head_dim),
+//              max, glibc-identical expf, serial sum in position order, normalise, serial weighted V sum in position
+//              order, and the int8 quantization of the head's two 32-blocks of output
+//                                                                         (model.cpp:115-137, 183-208, ops_ref.cpp:201-226)
+//   o          GEMV and residual add                                     (model.cpp:207-209)
+//   gate/up    the MLP's rmsnorm in every workgroup's prologue as above, one GEMV over the same rows of both matrices,
+//              g / (1 + expf(-g)) * u, quantization                     (model.cpp:212-218, ops_ref.cpp:243-248)
+//   down       GEMV and residual add                                     (model.cpp:219-221)
+// then the final norm and the head (Exact Shortlist Head for top-k queries, full 8-bit head + argmax otherwise). The
+// position and the token live on the device, so a decode step is a fixed launch sequence that can be captured in a HIP
+// graph and replayed: the step reads the token the previous step chose, and its last kernel writes the new token,
+// appends it to the output list and advances the position. A step at a position beyond the context writes nothing
+// into the cache and raises bit 0 of the status word; a prompt token outside the vocabulary raises bit 1.
 //
-// Prefill (chunks of up to 32 tokens) uses the int8-MFMA matmul for every projection and the same attention kernel
-// over a (head, token) grid: a token's keys and values for the chunk's positions come from the chunk's own
-// projections, so no kernel reads a cache row another workgroup of the same launch writes.
+// Prefill (chunks of up to 32 tokens) uses the int8-MFMA matmul for every projection (q / k / v in one launch, gate /
+// up in one launch) and an attention kernel over a (head, token) grid: a token's keys and values for the chunk's
+// positions come from the chunk's own projections, so no kernel reads a cache row another workgroup of the same launch
+// writes.
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
