@@ -1206,19 +1206,19 @@ __global__ __launch_bounds__(1024) void attention_decode_kernel(
     const uint4* vc4 = reinterpret_cast<const uint4*>(vc);
     auto vchunk = [&](int blk, int d) { return (size_t)blk * kvd + kvh * HD + d; };  // uint4 index of (block, dim)
     auto kchunk = [&](int c, int p) { return ((size_t)kvh * CPR + c) * ctx + p; };    // 16-byte K chunk c of row p
-    // This thread's K row (row tid, inside the cache) goes out before the position arrives too: its transfer is the
-    // longest of the kernel's first loads. Rows at or beyond the position are read and ignored (row pos may be being
-    // written by this launch).
-    v4u kk[CPR];
-    {
-        const uint16_t* kg = kc + (kchunk(0, min(tid, ctx - 1)) << 3);
-#pragma unroll
-        for (int i = 0; i < CPR; ++i) kk[i] = ld4(kg + (size_t)i * ctx * 8);
-    }
+    // The position (a scalar load, back before the vector loads above), then this thread's K row: cached rows only
+    // (tid < pos; row pos is the token's own, written by this launch). The K rows are the largest of the kernel's first
+    // transfers and one CU issues them at ~40 bytes per cycle, so rows past the position are not read.
     const int pos = *pos_dev, nrows = pos + 1;
     if (pos >= ctx || pos < 0) {  // uniform: a step past the context touches no cache row
         if (tid == 0 && h == 0) atomicOr(status, kStatusCtx);
         return;
+    }
+    v4u kk[CPR];
+    if (tid < pos) {
+        const uint16_t* kg = kc + (kchunk(0, tid) << 3);
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) kk[i] = ld4(kg + (size_t)i * ctx * 8);
     }
     QH_STAMP(8);
     // Then the RoPE angles of the position (ops_ref.cpp:201-214, with the reference build's contraction).
