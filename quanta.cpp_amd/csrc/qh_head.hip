@@ -94,19 +94,35 @@ int screen_tile_rows(int nb) {
 
 // Screen shares: two per compute unit (against four, 1 us less for the 151,936-row head: each workgroup's start-up
 // is spread over more tiles), an even number of rows (whole 4-byte error words), at least one tile and at most
-// kScreenMaxShare rows each; share p holds rows [p * share, min((p + 1) * share, V)).
+// kScreenMaxShare rows each. The first n1 shares (one per compute unit: the workgroups dispatched first, which the
+// compute unit's arbitration favours over the second ones) hold s1 rows, the others s2 <= s1: share p holds rows
+// [start(p), min(start(p) + len(p), V)).
+struct ShareMap {
+    int n1, s1, s2;
+    __host__ __device__ int start(int p) const { return p < n1 ? p * s1 : n1 * s1 + (p - n1) * s2; }
+    __host__ __device__ int len(int p) const { return p < n1 ? s1 : s2; }
+};
 struct ScreenShape {
-    int tile, share, grid;
+    int tile, grid;
+    ShareMap map;
 };
 ScreenShape screen_shape(int V, int nb) {
     ScreenShape sh;
     sh.tile = screen_tile_rows(nb);
-    const int g = 2 * device_cus();
-    int share = ((V + g - 1) / g + 1) & ~1;
-    share = share > sh.tile ? share : sh.tile;
-    share = share < kScreenMaxShare ? share : kScreenMaxShare;
-    sh.share = share;
-    sh.grid = (V + share - 1) / share;
+    const int cus = device_cus(), g = 2 * cus;
+    auto even_clamp = [&](long x) {
+        int v = (int)((x + 1) & ~1L);
+        v = v > sh.tile ? v : sh.tile;
+        return v < kScreenMaxShare ? v : kScreenMaxShare;
+    };
+    // 15% of a share moves from the second workgroups to the first: with equal shares the second ones ended ~2.4 us
+    // after the first (151,936 x 896), with 15% both end together and the screen's span drops 17.8 -> 16.5 us (10%
+    // and 20% measured less).
+    const long base = (V + g - 1) / g, skew = base * 15 / 100;
+    const int s1 = even_clamp(base + skew), s2 = even_clamp(base - skew);
+    sh.map = ShareMap{cus, s1, s2};
+    const long first = (long)cus * s1;
+    sh.grid = V <= first ? (int)((V + s1 - 1) / s1) : cus + (int)((V - first + s2 - 1) / s2);
     return sh;
 }
 
@@ -413,7 +429,7 @@ __device__ uint64_t rescore_lists(const int* a, int na, const int* b, int nb_, c
 
 __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void head_screen_kernel(
     const uint8_t* __restrict__ w4, const uint16_t* __restrict__ s4, const uint32_t* __restrict__ e32,
-    const int8_t* __restrict__ xq, const float* __restrict__ xd, int V, int nb, int nv, HeadMust mq, int tile, int share,
+    const int8_t* __restrict__ xq, const float* __restrict__ xd, int V, int nb, int nv, HeadMust mq, int tile, ShareMap sm,
     uint32_t nb_magic, float* __restrict__ coarse, float* __restrict__ upper, float* __restrict__ logits,
     uint8_t* __restrict__ mark, int32_t* __restrict__ firsts, uint64_t* __restrict__ tops, HeadCtrl* __restrict__ ctrl) {
     extern __shared__ __align__(16) float smem[];
@@ -444,7 +460,8 @@ __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(
     const int32_t* must;
     int n_must;
     must_span(mq, must, n_must);
-    const int ra = (int)blockIdx.x * share, rb = min(ra + share, V);  // even ra: error words stay 4-byte aligned
+    const int share = sm.len((int)blockIdx.x);
+    const int ra = sm.start((int)blockIdx.x), rb = min(ra + share, V);  // even ra: error words stay 4-byte aligned
 
     // The activation first, then the first tile: loads return in order, so the block norms below wait only for the
     // activation while the tile is in flight.
@@ -580,7 +597,7 @@ __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(
 
 __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     const uint8_t* __restrict__ w8, const uint16_t* __restrict__ s8, const int8_t* __restrict__ xq,
-    const float* __restrict__ xd, int nb, int nv, int k, int n_parts, int share, int band,
+    const float* __restrict__ xd, int nb, int nv, int k, int n_parts, ShareMap sm, int band,
     const uint64_t* __restrict__ tops, const float* __restrict__ coarse, const float* __restrict__ upper,
     const uint8_t* __restrict__ mark, int32_t* __restrict__ firsts, HeadMust mq, int32_t* __restrict__ rows,
     float* __restrict__ logits, HeadCtrl* __restrict__ ctrl, qh_head_stats* __restrict__ stats, TokenFeedback fb) {
@@ -590,7 +607,6 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     float* xds = reinterpret_cast<float*>(xs + nb * QK);
     __shared__ uint64_t pool[kPoolCap];
     __shared__ int prow[kPoolCap];
-    __shared__ float pexact[kPoolCap];
     __shared__ uint64_t gmax[kSelThreads / 4];
     __shared__ uint64_t best[kMaxKeep];
     __shared__ int seedrow[kMaxKeep];
@@ -598,8 +614,10 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     __shared__ ShareRows inc;  // shares whose published keys may miss keys at or above the cut
     __shared__ int selp[kMaxKeep];
     __shared__ RadixShared rsh;
-    __shared__ int candl[kSelRows * kSelThreads], mustl[kSelRows * kSelThreads];
-    __shared__ int n_pool, n_sel, n_c, n_m, ns_sh, base_sh, last_sh, n_cand_sh;
+    __shared__ int candl[kSelRows * kSelThreads], mustl[kSelRows * kSelThreads], candf[kSelRows * kSelThreads];
+    __shared__ float candu[kSelRows * kSelThreads];              // the speculative candidates' upper bounds
+    __shared__ float rx[2 * kRescoreRows + kSelRows * kSelThreads];  // exact logits: seeds (or pool), then candl
+    __shared__ int n_pool, n_sel, n_c, n_m, n_x, n_cf, ns_sh, base_sh, last_sh, n_cand_sh;
     __shared__ uint64_t thr_sh, key_sh;
     __shared__ float tau_sh;
     __shared__ int wsum[kSelWaves];
@@ -644,6 +662,8 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
         n_sel = 0;
         n_c = 0;
         n_m = 0;
+        n_x = 0;
+        n_cf = 0;
         inc.n = 0;
         thr_sh = 1ull;
     }
@@ -713,13 +733,14 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     __syncthreads();
     QH_HSTAMP(2, 0);
     if (inc.n > 0 && inc.n <= kMaxKeep) {  // uniform; rare: a share holding kTops of the keys >= L
-        const int n = inc.n * share;
+        const int smax = sm.s1, n = inc.n * smax;
 #pragma unroll 1
         for (int i0 = 0; i0 < n; i0 += kSelThreads) {  // uniform trip count: wave_append needs whole waves
             const int i = i0 + tid;
             uint64_t v = 0;
             if (i < n) {
-                const int sh = i / share, r = inc.p[sh] * share + (i - sh * share);
+                const int sh = i / smax, off = i - sh * smax;
+                const int r = off < sm.len(inc.p[sh]) ? sm.start(inc.p[sh]) + off : nv;
                 if (r < nv && mark[r] == 0) v = score_key(coarse[r], r);
                 if (v >= inc.below[sh]) v = 0;  // published
             }
@@ -746,9 +767,10 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
             if (slot >= 0) selp[slot] = tid + s * kSelThreads;
         }
         __syncthreads();
-        const int n = n_sel * share;
+        const int smax = sm.s1, n = n_sel * smax;
         auto key_at = [&](int i) -> uint64_t {
-            const int sh = i / share, r = selp[sh] * share + (i - sh * share);
+            const int sh = i / smax, off = i - sh * smax;
+            const int r = off < sm.len(selp[sh]) ? sm.start(selp[sh]) + off : nv;
             return (r < nv && mark[r] == 0) ? score_key(coarse[r], r) : 0ull;
         };
         const uint64_t th = block_kth_threshold<kSelThreads>(
@@ -772,95 +794,160 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     const int np = n_pool;
 
     // 2. The seeds: the pool's n_seed best keys (model.cpp:295-304), rescored exactly (model.cpp:305-307); tau = the
-    // k-th best exact seed logit (model.cpp:308-313). A pool of up to two rescoring passes is rescored whole before it
-    // is ranked, which takes the ranking off the path to the rows' loads. 3. The band's candidates {unmarked, not a
-    // seed, upper >= tau} (model.cpp:315-322) and must rows, rescored exactly. One loop of two passes, so the
-    // rescoring code runs twice from one copy.
-    const bool early = np <= 2 * kRescoreRows;  // uniform
+    // k-th best exact seed logit (model.cpp:308-313). 3. The band's candidates {unmarked, not a seed, upper >= tau}
+    // (model.cpp:315-322) and must rows, rescored exactly. The candidates are rescored in the seeds' pass, before tau
+    // is known: every unmarked band row with upper >= cut, the cut a sixteenth below the k-th best coarse score (the
+    // k-th best exact seed logit is that score within its rounding error, whose bound is loose but whose actual size is
+    // small), and once tau is known the rows with upper >= tau that are no seeds are kept. Rows with tau <= upper < cut
+    // (tau below the cut, rare) take a second pass. For greedy queries a pool of up to two rescoring passes is rescored
+    // whole in that pass and ranked after it, which keeps the ranking off the path to the rows' loads.
+    const bool early = k == 1 && np <= 2 * kRescoreRows;  // uniform
     auto rank_pool = [&]() {
         list_ranks(pool, np, [&](int i, int rank) {  // keys are unique
             if (rank < n_keep) {
                 best[rank] = pool[i];
                 if (rank < n_seed) {
                     seedrow[rank] = prow[i];
-                    if (early) exact[rank] = pexact[i];
+                    if (early) exact[rank] = rx[i];
                 }
             }
         });
         __syncthreads();
     };
-    if (!early) rank_pool();
-    float tau = 0.0f;
-    int ns = 0, nc = 0, nm = 0;
-    unsigned base = 0;
-    uint64_t kbest = 0;
-#pragma unroll 1
-    for (int pass = 0;; ++pass) {
-        const int* la = pass == 1 ? candl : early ? prow : seedrow;
-        const int na = pass == 1 ? nc : early ? np : min(np, n_seed);
-        const uint64_t kb = rescore_lists(la, na, mustl, pass == 0 ? 0 : nm, w8, s8, xs, xds, nb, prod,
-                                          early ? pexact : exact, pass == 0, logits);
-        if (pass == 1) {
-            kbest = kb;
-            break;
-        }
-        if (early) rank_pool();
-        QH_HSTAMP(2, 3);
-        QH_HSTAMP(1, 1);
-        if (wave == 0) {  // one lane per seed
-            ns = __popcll(__ballot(lane < n_seed && best[lane] != 0));
-            const bool have = lane < ns;
-            const float e = have ? exact[lane] : -__builtin_inff();
-            float t = -__builtin_inff();
-            if (ns >= k) {  // fewer than k seeds above it, k at or above
-                int gt = 0, ge = 0;
-                for (int j = 0; j < ns; ++j) {
-                    const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-                    gt += ej > e ? 1 : 0;
-                    ge += ej >= e ? 1 : 0;
-                }
-                const uint64_t at = __ballot(have && gt < k && ge >= k);  // equal values wherever it is set
-                t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), __ffsll((long long)at) - 1));
-            }
-            const uint64_t ks = wave_max_u64(have ? score_key(e, seedrow[lane]) : 0ull);
-            if (lane == 0) {
-                tau_sh = t;
-                key_sh = ks;
-                ns_sh = ns;
-            }
-        }
+    uint64_t kth;  // the k-th best eligible coarse key (0: fewer eligible rows)
+    if (early) {
+        uint64_t m = 0;
+        for (int i = tid; i < np; i += kSelThreads) m = pool[i] > m ? pool[i] : m;
+        m = wave_max_u64(m);
+        if (lane == 0) wkey[wave] = m;
         __syncthreads();
-        tau = tau_sh;
-        ns = ns_sh;
-        if (blockIdx.x == 0)
-            for (int i = tid; i < ns; i += kSelThreads) {
-                rows[i] = seedrow[i];
-                logits[seedrow[i]] = exact[i];
+        kth = wkey[0];
+#pragma unroll
+        for (int w = 1; w < kSelWaves; ++w) kth = wkey[w] > kth ? wkey[w] : kth;
+    } else {
+        rank_pool();
+        kth = best[k - 1];
+    }
+    float cut = -__builtin_inff();
+    if (kth != 0) {
+        const float c = key_score(kth);
+        cut = c - (__builtin_fabsf(c) * 0.0625f + 1e-3f);
+    }
+#pragma unroll
+    for (int j = 0; j < kSelRows; ++j) {
+        const int r = r0 + j;
+        int slot = wave_append(r < cb && mk[j] == 0 && up[j] >= cut, &n_c);
+        if (slot >= 0) {
+            candl[slot] = r;
+            candu[slot] = up[j];
+        }
+        slot = wave_append(r < cb && mk[j] == 1, &n_m);
+        if (slot >= 0) mustl[slot] = r;
+    }
+    __syncthreads();
+    const int nsp = n_c, nm = n_m;  // the must rows follow the speculative candidates in candl (at most band rows)
+    for (int i = tid; i < nm; i += kSelThreads) candl[nsp + i] = mustl[i];
+    __syncthreads();
+    const int na = early ? np : min(np, n_seed);
+    rescore_lists(early ? prow : seedrow, na, candl, nsp + nm, w8, s8, xs, xds, nb, prod, rx, true, logits);
+    if (early) {
+        rank_pool();
+    } else {
+        for (int i = tid; i < na; i += kSelThreads) exact[i] = rx[i];
+        __syncthreads();
+    }
+    QH_HSTAMP(2, 3);
+    QH_HSTAMP(1, 1);
+    int ns = 0;
+    if (wave == 0) {  // one lane per seed
+        ns = __popcll(__ballot(lane < n_seed && best[lane] != 0));
+        const bool have = lane < ns;
+        const float e = have ? exact[lane] : -__builtin_inff();
+        float t = -__builtin_inff();
+        if (ns >= k) {  // fewer than k seeds above it, k at or above
+            int gt = 0, ge = 0;
+            for (int j = 0; j < ns; ++j) {
+                const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+                gt += ej > e ? 1 : 0;
+                ge += ej >= e ? 1 : 0;
             }
-        QH_HSTAMP(1, 2);
+            const uint64_t at = __ballot(have && gt < k && ge >= k);  // equal values wherever it is set
+            t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), __ffsll((long long)at) - 1));
+        }
+        const uint64_t ks = wave_max_u64(have ? score_key(e, seedrow[lane]) : 0ull);
+        if (lane == 0) {
+            tau_sh = t;
+            key_sh = ks;
+            ns_sh = ns;
+        }
+    }
+    __syncthreads();
+    const float tau = tau_sh;
+    ns = ns_sh;
+    if (blockIdx.x == 0)
+        for (int i = tid; i < ns; i += kSelThreads) {
+            rows[i] = seedrow[i];
+            logits[seedrow[i]] = exact[i];
+        }
+    QH_HSTAMP(1, 2);
+    // The kept candidates and the must rows: logits out, their best key.
+    uint64_t kbest = 0;
+    auto not_seed = [&](int r) {
+        bool ok = true;
+        for (int q = 0; q < ns; ++q) ok = ok && seedrow[q] != r;
+        return ok;
+    };
+    for (int i0 = 0; i0 < nsp + nm; i0 += kSelThreads) {  // uniform trip count: wave_append needs whole waves
+        const int i = i0 + tid;
+        bool keep = false;
+        int r = 0;
+        if (i < nsp + nm) {
+            r = candl[i];
+            keep = i < nsp && candu[i] >= tau && not_seed(r);
+            if (keep || i >= nsp) {
+                const float e = rx[na + i];
+                logits[r] = e;
+                const uint64_t kk = score_key(e, r);
+                kbest = kk > kbest ? kk : kbest;
+            }
+        }
+        const int slot = wave_append(keep, &n_cf);
+        if (slot >= 0) candf[slot] = r;
+    }
+    const bool extra = tau < cut;  // uniform
+    unsigned base = 0;
+    if (!extra) {  // the count is final: its slot request goes out before the completion work
+        __syncthreads();
+        if (tid == 0 && n_cf > 0) base = atomicAdd(&ctrl->n_cand, (unsigned)n_cf);
+    }
+    if (extra) {  // the rows between tau and the cut, in a pass of their own
 #pragma unroll
         for (int j = 0; j < kSelRows; ++j) {
             const int r = r0 + j;
-            bool c = r < cb && mk[j] == 0 && up[j] >= tau;
-            if (__ballot(c) != 0)
-                for (int i = 0; i < ns; ++i) c = c && seedrow[i] != r;
-            int slot = wave_append(c, &n_c);
-            if (slot >= 0) candl[slot] = r;
-            slot = wave_append(r < cb && mk[j] == 1, &n_m);
+            const bool c = r < cb && mk[j] == 0 && up[j] >= tau && up[j] < cut && not_seed(r);
+            const int slot = wave_append(c, &n_x);
             if (slot >= 0) mustl[slot] = r;
         }
         __syncthreads();
-        nc = n_c;
-        nm = n_m;
-        if (tid == 0 && nc > 0) base = atomicAdd(&ctrl->n_cand, (unsigned)nc);  // returned during the rescoring
+        const int nx = n_x;
+        const uint64_t kb = rescore_lists(mustl, nx, candl, 0, w8, s8, xs, xds, nb, prod, rx, false, logits);
+        kbest = kb > kbest ? kb : kbest;
+        for (int i0 = 0; i0 < nx; i0 += kSelThreads) {
+            const int i = i0 + tid;
+            const int slot = wave_append(i < nx, &n_cf);
+            if (slot >= 0) candf[slot] = mustl[i];
+        }
     }
+    __syncthreads();
+    const int nc = n_cf;
+    if (extra && tid == 0 && nc > 0) base = atomicAdd(&ctrl->n_cand, (unsigned)nc);
     if (tid == 0) base_sh = (int)base;
     if (blockIdx.x == 0 && tid == 0) kbest = key_sh > kbest ? key_sh : kbest;  // the seeds' best key, once
     kbest = wave_max_u64(kbest);
     if (lane == 0) wkey[wave] = kbest;
     asm volatile("" ::"v"(mdep));  // the must minima have returned
     __syncthreads();
-    for (int i = tid; i < nc; i += kSelThreads) rows[ns + base_sh + i] = candl[i];
+    for (int i = tid; i < nc; i += kSelThreads) rows[ns + base_sh + i] = candf[i];
     QH_HSTAMP(1, 3);
 
     // 4. Completion. The maxima are performed (their old values have returned) before the counts move, so the last
@@ -984,13 +1071,13 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
     const size_t lds1 = ((size_t)2 * chain_len32(nb) + 4 * (size_t)tile * chain_stride32(nb) + kChainPipePad + 128) * 4 +
                         kScreenMaxShare + (size_t)D;
     qh_launch(head_screen_kernel, dim3(sh.grid), dim3(kScreenThreads), lds1, s, w4, s4, e32, xq, xd, V, nb, nv, must,
-              tile, sh.share, magic, out.coarse, out.upper, out.logits, mark, firsts, tops, ctrl);
+              tile, sh.map, magic, out.coarse, out.upper, out.logits, mark, firsts, tops, ctrl);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int band = select_band(nv);
     const size_t lds2 = (size_t)kRescoreRows * nb * 4 + (size_t)nb * QK + (size_t)nb * 4;
     qh_launch(head_select_kernel, dim3((unsigned)((nv + band - 1) / band)), dim3(kSelThreads), lds2, s, w8, s8, xq, xd,
-              nb, nv, q.top_k, sh.grid, sh.share, band, tops, out.coarse, out.upper, mark, firsts, must, out.rows,
+              nb, nv, q.top_k, sh.grid, sh.map, band, tops, out.coarse, out.upper, mark, firsts, must, out.rows,
               out.logits, ctrl, out.stats, advance ? *advance : TokenFeedback{});
     return hipGetLastError();
 }
