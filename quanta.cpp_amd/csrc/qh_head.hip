@@ -618,7 +618,7 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     __shared__ float candu[kSelRows * kSelThreads];              // the speculative candidates' upper bounds
     __shared__ float rx[2 * kRescoreRows + kSelRows * kSelThreads];  // exact logits: seeds (or pool), then candl
     __shared__ int n_pool, n_sel, n_c, n_m, n_x, n_cf, ns_sh, base_sh, last_sh, n_cand_sh;
-    __shared__ uint64_t thr_sh, key_sh;
+    __shared__ uint64_t thr_sh, key_sh, top_sh;
     __shared__ float tau_sh;
     __shared__ int wsum[kSelWaves];
     __shared__ uint64_t wkey[kSelWaves];
@@ -666,6 +666,7 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
         n_cf = 0;
         inc.n = 0;
         thr_sh = 1ull;
+        top_sh = 0ull;
     }
     // The must ids' first occurrences: each occurrence in this workgroup's slice of the list proposes its index for its
     // row with an atomic minimum (the screen reset the rows); the last workgroup lists the winners.
@@ -696,12 +697,40 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
         m = o > m ? o : m;
     }
     if ((lane & 3) == 0) gmax[tid >> 2] = m;
-    __syncthreads();
+    __syncthreads();  // (also orders the counters' reset before their first use)
+    // The band's must rows open the candidate list (their count is final after the next barrier).
+#pragma unroll
+    for (int j = 0; j < kSelRows; ++j) {
+        const int slot = wave_append(r0 + j < cb && mk[j] == 1, &n_m);
+        if (slot >= 0) candl[slot] = r0 + j;
+    }
     list_ranks(gmax, kSelThreads / 4, [&](int i, int rank) {
         if (rank == n_keep - 1) thr_sh = gmax[i];  // zero maxima rank below every nonzero one
+        if (rank == 0) top_sh = gmax[i];
     });
     __syncthreads();
     const uint64_t L = thr_sh;
+    const int nm = n_m;
+    // The speculative candidates' cut, a sixteenth of the k-th best coarse score below it: for k = 1 the best key
+    // overall, known here (the best group maximum); for k > 1 once the pool is ranked.
+    auto cut_below = [](uint64_t kth) {
+        if (kth == 0) return -__builtin_inff();
+        const float c = key_score(kth);
+        return c - (__builtin_fabsf(c) * 0.0625f + 1e-3f);
+    };
+    // The band's unmarked rows with upper >= cut follow the must rows in candl, their bounds in candu.
+    auto spec_append = [&](float cut) {
+#pragma unroll
+        for (int j = 0; j < kSelRows; ++j) {
+            const int slot = wave_append(r0 + j < cb && mk[j] == 0 && up[j] >= cut, &n_c);
+            if (slot >= 0) {
+                candl[nm + slot] = r0 + j;
+                candu[slot] = up[j];
+            }
+        }
+    };
+    float cut = k == 1 ? cut_below(top_sh) : 0.0f;
+    if (k == 1) spec_append(cut);  // in the pool's phase: no barrier of its own
     {
         bool pr[kSelShares * kTops];
         int slot[kSelShares * kTops];
@@ -796,9 +825,9 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     // 2. The seeds: the pool's n_seed best keys (model.cpp:295-304), rescored exactly (model.cpp:305-307); tau = the
     // k-th best exact seed logit (model.cpp:308-313). 3. The band's candidates {unmarked, not a seed, upper >= tau}
     // (model.cpp:315-322) and must rows, rescored exactly. The candidates are rescored in the seeds' pass, before tau
-    // is known: every unmarked band row with upper >= cut, the cut a sixteenth below the k-th best coarse score (the
-    // k-th best exact seed logit is that score within its rounding error, whose bound is loose but whose actual size is
-    // small), and once tau is known the rows with upper >= tau that are no seeds are kept. Rows with tau <= upper < cut
+    // is known: every unmarked band row with upper >= cut (listed above: the cut sits a sixteenth below the k-th best
+    // coarse score, and the k-th best exact seed logit is that score within its rounding error, whose bound is loose
+    // but whose actual size is small), and once tau is known the rows with upper >= tau that are no seeds are kept. Rows with tau <= upper < cut
     // (tau below the cut, rare) take a second pass. For greedy queries a pool of up to two rescoring passes is rescored
     // whole in that pass and ranked after it, which keeps the ranking off the path to the rows' loads.
     const bool early = k == 1 && np <= 2 * kRescoreRows;  // uniform
@@ -814,42 +843,15 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
         });
         __syncthreads();
     };
-    uint64_t kth;  // the k-th best eligible coarse key (0: fewer eligible rows)
-    if (early) {
-        uint64_t m = 0;
-        for (int i = tid; i < np; i += kSelThreads) m = pool[i] > m ? pool[i] : m;
-        m = wave_max_u64(m);
-        if (lane == 0) wkey[wave] = m;
+    if (!early) rank_pool();
+    if (k > 1) {
+        cut = cut_below(best[k - 1]);
+        spec_append(cut);
         __syncthreads();
-        kth = wkey[0];
-#pragma unroll
-        for (int w = 1; w < kSelWaves; ++w) kth = wkey[w] > kth ? wkey[w] : kth;
-    } else {
-        rank_pool();
-        kth = best[k - 1];
     }
-    float cut = -__builtin_inff();
-    if (kth != 0) {
-        const float c = key_score(kth);
-        cut = c - (__builtin_fabsf(c) * 0.0625f + 1e-3f);
-    }
-#pragma unroll
-    for (int j = 0; j < kSelRows; ++j) {
-        const int r = r0 + j;
-        int slot = wave_append(r < cb && mk[j] == 0 && up[j] >= cut, &n_c);
-        if (slot >= 0) {
-            candl[slot] = r;
-            candu[slot] = up[j];
-        }
-        slot = wave_append(r < cb && mk[j] == 1, &n_m);
-        if (slot >= 0) mustl[slot] = r;
-    }
-    __syncthreads();
-    const int nsp = n_c, nm = n_m;  // the must rows follow the speculative candidates in candl (at most band rows)
-    for (int i = tid; i < nm; i += kSelThreads) candl[nsp + i] = mustl[i];
-    __syncthreads();
+    const int nsp = n_c;  // candl: nm must rows, then nsp speculative candidates (at most band rows in all)
     const int na = early ? np : min(np, n_seed);
-    rescore_lists(early ? prow : seedrow, na, candl, nsp + nm, w8, s8, xs, xds, nb, prod, rx, true, logits);
+    rescore_lists(early ? prow : seedrow, na, candl, nm + nsp, w8, s8, xs, xds, nb, prod, rx, true, logits);
     if (early) {
         rank_pool();
     } else {
@@ -864,7 +866,10 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
         const bool have = lane < ns;
         const float e = have ? exact[lane] : -__builtin_inff();
         float t = -__builtin_inff();
-        if (ns >= k) {  // fewer than k seeds above it, k at or above
+        const uint64_t ks = wave_max_u64(have ? score_key(e, seedrow[lane]) : 0ull);
+        if (k == 1) {  // the best exact seed logit
+            if (ns >= 1) t = key_score(ks);
+        } else if (ns >= k) {  // fewer than k seeds above it, k at or above
             int gt = 0, ge = 0;
             for (int j = 0; j < ns; ++j) {
                 const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
@@ -874,7 +879,6 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
             const uint64_t at = __ballot(have && gt < k && ge >= k);  // equal values wherever it is set
             t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), __ffsll((long long)at) - 1));
         }
-        const uint64_t ks = wave_max_u64(have ? score_key(e, seedrow[lane]) : 0ull);
         if (lane == 0) {
             tau_sh = t;
             key_sh = ks;
@@ -897,14 +901,14 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
         for (int q = 0; q < ns; ++q) ok = ok && seedrow[q] != r;
         return ok;
     };
-    for (int i0 = 0; i0 < nsp + nm; i0 += kSelThreads) {  // uniform trip count: wave_append needs whole waves
+    for (int i0 = 0; i0 < nm + nsp; i0 += kSelThreads) {  // uniform trip count: wave_append needs whole waves
         const int i = i0 + tid;
         bool keep = false;
         int r = 0;
-        if (i < nsp + nm) {
+        if (i < nm + nsp) {
             r = candl[i];
-            keep = i < nsp && candu[i] >= tau && not_seed(r);
-            if (keep || i >= nsp) {
+            keep = i >= nm && candu[i - nm] >= tau && not_seed(r);
+            if (keep || i < nm) {
                 const float e = rx[na + i];
                 logits[r] = e;
                 const uint64_t kk = score_key(e, r);
