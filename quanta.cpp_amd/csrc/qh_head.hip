@@ -699,10 +699,15 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     if ((lane & 3) == 0) gmax[tid >> 2] = m;
     __syncthreads();  // (also orders the counters' reset before their first use)
     // The band's must rows open the candidate list (their count is final after the next barrier).
+    {
+        bool pm[kSelRows];
+        int sm_[kSelRows];
 #pragma unroll
-    for (int j = 0; j < kSelRows; ++j) {
-        const int slot = wave_append(r0 + j < cb && mk[j] == 1, &n_m);
-        if (slot >= 0) candl[slot] = r0 + j;
+        for (int j = 0; j < kSelRows; ++j) pm[j] = r0 + j < cb && mk[j] == 1;
+        wave_append_n(pm, &n_m, sm_);
+#pragma unroll
+        for (int j = 0; j < kSelRows; ++j)
+            if (sm_[j] >= 0) candl[sm_[j]] = r0 + j;
     }
     list_ranks(gmax, kSelThreads / 4, [&](int i, int rank) {
         if (rank == n_keep - 1) thr_sh = gmax[i];  // zero maxima rank below every nonzero one
@@ -720,14 +725,17 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     };
     // The band's unmarked rows with upper >= cut follow the must rows in candl, their bounds in candu.
     auto spec_append = [&](float cut) {
+        bool pc[kSelRows];
+        int sc_[kSelRows];
 #pragma unroll
-        for (int j = 0; j < kSelRows; ++j) {
-            const int slot = wave_append(r0 + j < cb && mk[j] == 0 && up[j] >= cut, &n_c);
-            if (slot >= 0) {
-                candl[nm + slot] = r0 + j;
-                candu[slot] = up[j];
+        for (int j = 0; j < kSelRows; ++j) pc[j] = r0 + j < cb && mk[j] == 0 && up[j] >= cut;
+        wave_append_n(pc, &n_c, sc_);
+#pragma unroll
+        for (int j = 0; j < kSelRows; ++j)
+            if (sc_[j] >= 0) {
+                candl[nm + sc_[j]] = r0 + j;
+                candu[sc_[j]] = up[j];
             }
-        }
     };
     float cut = k == 1 ? cut_below(top_sh) : 0.0f;
     if (k == 1) spec_append(cut);  // in the pool's phase: no barrier of its own
