@@ -595,6 +595,7 @@ __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(
     QH_HSTAMP(0, 3);
 }
 
+template <int SH>  // screen shares per thread: 2 for grids of up to 512 shares, else SH
 __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     const uint8_t* __restrict__ w8, const uint16_t* __restrict__ s8, const int8_t* __restrict__ xq,
     const float* __restrict__ xd, int nb, int nv, int k, int n_parts, ShareMap sm, int band,
@@ -640,9 +641,9 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
             mk[j] = (uint8_t)(mw >> (8 * j));
         }
     }
-    uint64_t tk[kSelShares][kTops];
+    uint64_t tk[SH][kTops];
 #pragma unroll
-    for (int s = 0; s < kSelShares; ++s) {
+    for (int s = 0; s < SH; ++s) {
         const int p = tid + s * kSelThreads;
         uint4 a = make_uint4(0u, 0u, 0u, 0u), b = a;
         if (p < n_parts) {
@@ -689,7 +690,7 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     // (read again; rare). The pool holds the n_keep best keys; ranking it orders them.
     uint64_t m = 0;
 #pragma unroll
-    for (int s = 0; s < kSelShares; ++s) m = tk[s][0] > m ? tk[s][0] : m;
+    for (int s = 0; s < SH; ++s) m = tk[s][0] > m ? tk[s][0] : m;
 #pragma unroll
     for (int off = 1; off < 4; off <<= 1) {  // over groups of 4 lanes
         const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(m >> 32), off, 64) << 32) |
@@ -740,28 +741,28 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     float cut = k == 1 ? cut_below(top_sh) : 0.0f;
     if (k == 1) spec_append(cut);  // in the pool's phase: no barrier of its own
     {
-        bool pr[kSelShares * kTops];
-        int slot[kSelShares * kTops];
+        bool pr[SH * kTops];
+        int slot[SH * kTops];
 #pragma unroll
-        for (int s = 0; s < kSelShares; ++s)
+        for (int s = 0; s < SH; ++s)
 #pragma unroll
             for (int r = 0; r < kTops; ++r) pr[s * kTops + r] = tk[s][r] != 0 && tk[s][r] >= L;
         wave_append_n(pr, &n_pool, slot);
 #pragma unroll
-        for (int s = 0; s < kSelShares; ++s)
+        for (int s = 0; s < SH; ++s)
 #pragma unroll
             for (int r = 0; r < kTops; ++r)
                 if (slot[s * kTops + r] >= 0 && slot[s * kTops + r] < kPoolCap) {
                     pool[slot[s * kTops + r]] = tk[s][r];
                     prow[slot[s * kTops + r]] = key_row(tk[s][r]);
                 }
-        bool pi[kSelShares];
-        int si[kSelShares];
+        bool pi[SH];
+        int si[SH];
 #pragma unroll
-        for (int s = 0; s < kSelShares; ++s) pi[s] = pr[s * kTops + kTops - 1];
+        for (int s = 0; s < SH; ++s) pi[s] = pr[s * kTops + kTops - 1];
         wave_append_n(pi, &inc.n, si);
 #pragma unroll
-        for (int s = 0; s < kSelShares; ++s)
+        for (int s = 0; s < SH; ++s)
             if (si[s] >= 0 && si[s] < kMaxKeep) {
                 inc.p[si[s]] = tid + s * kSelThreads;
                 inc.below[si[s]] = tk[s][kTops - 1];
@@ -795,11 +796,11 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
         const uint64_t T = block_kth_threshold<kSelThreads>(
             [&](auto visit) {
 #pragma unroll
-                for (int s = 0; s < kSelShares; ++s) visit(tk[s][0]);
+                for (int s = 0; s < SH; ++s) visit(tk[s][0]);
             },
             n_keep, rsh);
 #pragma unroll 1
-        for (int s = 0; s < kSelShares; ++s) {
+        for (int s = 0; s < SH; ++s) {
             const int slot = wave_append(tk[s][0] != 0 && tk[s][0] >= T, &n_sel);  // at most n_keep shares
             if (slot >= 0) selp[slot] = tid + s * kSelThreads;
         }
@@ -1088,9 +1089,10 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
     if (e != hipSuccess) return e;
     const int band = select_band(nv);
     const size_t lds2 = (size_t)kRescoreRows * nb * 4 + (size_t)nb * QK + (size_t)nb * 4;
-    qh_launch(head_select_kernel, dim3((unsigned)((nv + band - 1) / band)), dim3(kSelThreads), lds2, s, w8, s8, xq, xd,
-              nb, nv, q.top_k, sh.grid, sh.map, band, tops, out.coarse, out.upper, mark, firsts, must, out.rows,
-              out.logits, ctrl, out.stats, advance ? *advance : TokenFeedback{});
+    auto* sel = sh.grid <= 2 * kSelThreads ? head_select_kernel<2> : head_select_kernel<kSelShares>;
+    qh_launch(sel, dim3((unsigned)((nv + band - 1) / band)), dim3(kSelThreads), lds2, s, w8, s8, xq, xd, nb, nv,
+              q.top_k, sh.grid, sh.map, band, tops, out.coarse, out.upper, mark, firsts, must, out.rows, out.logits,
+              ctrl, out.stats, advance ? *advance : TokenFeedback{});
     return hipGetLastError();
 }
 
