@@ -290,7 +290,7 @@ __device__ __forceinline__ int wave_append(bool pred, int* counter) {
     const int leader = __ffsll((unsigned long long)b) - 1;
     int base = 0;
     if (lane == leader) base = atomicAdd(counter, __popcll(b));
-    base = __shfl(base, leader, 64);
+    base = __builtin_amdgcn_readlane(base, leader);  // leader is uniform: no LDS round trip
     return pred ? base + __popcll(b & ((1ull << lane) - 1ull)) : -1;
 }
 
@@ -325,6 +325,15 @@ __device__ __forceinline__ int quad_sum(int v) {
     v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // lanes 1,0,3,2
     v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);  // lanes 2,3,0,1
     return v;
+}
+
+// One step of a 64-bit maximum over groups of 4 lanes: the other lane by the DPP quad permutation CTRL.
+template <int CTRL>
+__device__ __forceinline__ uint64_t quad_max_step(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    return o > v ? o : v;
 }
 
 // The rank of every entry of an LDS list of np keys (how many entries are larger), four threads per entry: f(i, rank)
@@ -691,12 +700,9 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     uint64_t m = 0;
 #pragma unroll
     for (int s = 0; s < SH; ++s) m = tk[s][0] > m ? tk[s][0] : m;
-#pragma unroll
-    for (int off = 1; off < 4; off <<= 1) {  // over groups of 4 lanes
-        const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(m >> 32), off, 64) << 32) |
-                           (uint32_t)__shfl_xor((int)(uint32_t)m, off, 64);
-        m = o > m ? o : m;
-    }
+    // maximum over groups of 4 lanes by DPP quad permutations (lanes 1,0,3,2, then 2,3,0,1): no LDS round trip
+    m = quad_max_step<0xB1>(m);
+    m = quad_max_step<0x4E>(m);
     if ((lane & 3) == 0) gmax[tid >> 2] = m;
     __syncthreads();  // (also orders the counters' reset before their first use)
     // The band's must rows open the candidate list (their count is final after the next barrier).
