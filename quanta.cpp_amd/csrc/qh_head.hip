@@ -367,15 +367,23 @@ struct ShareRows {
 // [32][nb] (lane pairs cover a 32-byte block), then one lane per row runs the reference chain acc = fma(p_b, dx_b,
 // acc) in block order (the decode GEMV's association, so each logit is bit-identical to the full head's) and writes
 // it to out[i] (LDS, by list index) when to_out is set, else to logits[row]. Every thread of the workgroup calls it
-// (barriers inside). Returns, in each row's chain lane, the best key of the rows it scored (0 elsewhere).
+// (barriers inside). mid() runs once, by every thread, while the first pass's loads are in flight (it may hold
+// barriers and must not touch prod). Returns, in each row's chain lane, the best key of the rows it scored (0
+// elsewhere).
 constexpr int kRescoreLanes = 8, kRescoreRows = kSelThreads / kRescoreLanes;
+struct NoMid {
+    __device__ void operator()() const {}
+};
+template <typename Mid = NoMid>
 __device__ uint64_t rescore_lists(const int* a, int na, const int* b, int nb_, const uint8_t* __restrict__ w8,
                                   const uint16_t* __restrict__ s8, const int8_t* xs, const float* xds, int nb,
-                                  float* prod, float* out, bool to_out, float* __restrict__ logits) {
+                                  float* prod, float* out, bool to_out, float* __restrict__ logits,
+                                  const Mid& mid = Mid()) {
     constexpr int kPer = 8;  // chunks per lane per batch: one batch for rows of up to 1024 columns
     const int tid = (int)threadIdx.x, g = tid / kRescoreLanes, j = tid % kRescoreLanes;
     const int nch = 2 * nb, cnt = na + nb_;
     uint64_t kbest = 0;
+    if (cnt == 0) mid();
     for (int p0 = 0; p0 < cnt; p0 += kRescoreRows) {
         const int i = p0 + g;
         const bool act = i < cnt;
@@ -391,6 +399,7 @@ __device__ uint64_t rescore_lists(const int* a, int na, const int* b, int nb_, c
                 w[c] = load16(wr + (size_t)ch * 16);
                 sc[c] = load_f16_bits(sr + (ch >> 1));
             }
+            if (p0 == 0 && c0 == 0) mid();  // with the first pass's loads in flight
             float scf[kPer];
 #pragma unroll
             for (int c = 0; c < kPer; ++c) {
@@ -620,6 +629,7 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     __shared__ uint64_t gmax[kSelThreads / 4];
     __shared__ uint64_t best[kMaxKeep];
     __shared__ int seedrow[kMaxKeep];
+    __shared__ int seedidx[kMaxKeep];  // early: pool index of the seed of each rank
     __shared__ float exact[kMaxKeep];
     __shared__ ShareRows inc;  // shares whose published keys may miss keys at or above the cut
     __shared__ int selp[kMaxKeep];
@@ -844,7 +854,7 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     // coarse score, and the k-th best exact seed logit is that score within its rounding error, whose bound is loose
     // but whose actual size is small), and once tau is known the rows with upper >= tau that are no seeds are kept. Rows with tau <= upper < cut
     // (tau below the cut, rare) take a second pass. For greedy queries a pool of up to two rescoring passes is rescored
-    // whole in that pass and ranked after it, which keeps the ranking off the path to the rows' loads.
+    // whole in that pass and ranked while its loads are in flight, which keeps the ranking off the path.
     const bool early = k == 1 && np <= 2 * kRescoreRows;  // uniform
     auto rank_pool = [&]() {
         list_ranks(pool, np, [&](int i, int rank) {  // keys are unique
@@ -852,7 +862,7 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
                 best[rank] = pool[i];
                 if (rank < n_seed) {
                     seedrow[rank] = prow[i];
-                    if (early) exact[rank] = rx[i];
+                    if (early) seedidx[rank] = i;
                 }
             }
         });
@@ -866,13 +876,13 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     }
     const int nsp = n_c;  // candl: nm must rows, then nsp speculative candidates (at most band rows in all)
     const int na = early ? np : min(np, n_seed);
-    rescore_lists(early ? prow : seedrow, na, candl, nm + nsp, w8, s8, xs, xds, nb, prod, rx, true, logits);
-    if (early) {
-        rank_pool();
-    } else {
-        for (int i = tid; i < na; i += kSelThreads) exact[i] = rx[i];
-        __syncthreads();
-    }
+    // (early: the pool is ranked while the pass's loads are in flight)
+    rescore_lists(early ? prow : seedrow, na, candl, nm + nsp, w8, s8, xs, xds, nb, prod, rx, true, logits,
+                  [&]() {
+                      if (early) rank_pool();
+                  });
+    for (int i = tid; i < min(np, n_seed); i += kSelThreads) exact[i] = rx[early ? seedidx[i] : i];
+    __syncthreads();
     QH_HSTAMP(2, 3);
     QH_HSTAMP(1, 1);
     int ns = 0;
