@@ -943,13 +943,7 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
         const int slot = wave_append(keep, &n_cf);
         if (slot >= 0) candf[slot] = r;
     }
-    const bool extra = tau < cut;  // uniform
-    unsigned base = 0;
-    if (!extra) {  // the count is final: its slot request goes out before the completion work
-        __syncthreads();
-        if (tid == 0 && n_cf > 0) base = atomicAdd(&ctrl->n_cand, (unsigned)n_cf);
-    }
-    if (extra) {  // the rows between tau and the cut, in a pass of their own
+    if (tau < cut) {  // uniform; the rows between tau and the cut, in a pass of their own
 #pragma unroll
         for (int j = 0; j < kSelRows; ++j) {
             const int r = r0 + j;
@@ -967,34 +961,35 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
             if (slot >= 0) candf[slot] = mustl[i];
         }
     }
-    __syncthreads();
-    const int nc = n_cf;
-    if (extra && tid == 0 && nc > 0) base = atomicAdd(&ctrl->n_cand, (unsigned)nc);
-    if (tid == 0) base_sh = (int)base;
     if (blockIdx.x == 0 && tid == 0) kbest = key_sh > kbest ? key_sh : kbest;  // the seeds' best key, once
     kbest = wave_max_u64(kbest);
     if (lane == 0) wkey[wave] = kbest;
     asm volatile("" ::"v"(mdep));  // the must minima have returned
     __syncthreads();
-    for (int i = tid; i < nc; i += kSelThreads) rows[ns + base_sh + i] = candf[i];
+    const int nc = n_cf;
     QH_HSTAMP(1, 3);
 
-    // 4. Completion. The maxima are performed (their old values have returned) before the counts move, so the last
-    // workgroup's atomic reads see every maximum, every count and every first occurrence. It reads nothing else
-    // another workgroup of this launch wrote, so no cache write-back fence is needed.
+    // 4. Completion. The candidates' slot request and the maximum go out together; both are performed (their old
+    // values have returned) before the counts move, so the last workgroup's atomic reads see every maximum, every
+    // count and every first occurrence. It reads nothing else another workgroup of this launch wrote, so no cache
+    // write-back fence is needed; the candidate rows are written after the counts (nothing in this launch reads them).
     if (tid == 0) {
         uint64_t kw = wkey[0];
         for (int w = 1; w < kSelWaves; ++w) kw = wkey[w] > kw ? wkey[w] : kw;
         const int g = (int)(blockIdx.x % kDoneGroups);
-        if (kw) {
-            const unsigned long long old = atomicMax(group_key(ctrl, g), (unsigned long long)kw);
-            asm volatile("" ::"v"(old));
-        }
+        unsigned base = 0;
+        unsigned long long old = 0;
+        if (nc > 0) base = atomicAdd(&ctrl->n_cand, (unsigned)nc);
+        if (kw) old = atomicMax(group_key(ctrl, g), (unsigned long long)kw);
+        asm volatile("" ::"v"(base), "v"(old));
+        base_sh = (int)base;
         const unsigned gsize = (gridDim.x - (unsigned)g + kDoneGroups - 1) / kDoneGroups;
         const bool group_last = atomicAdd(group_done(ctrl, g), 1u) == gsize - 1;
         const unsigned ngroups = gridDim.x < (unsigned)kDoneGroups ? gridDim.x : (unsigned)kDoneGroups;
         last_sh = group_last && atomicAdd(&ctrl->done, 1u) == ngroups - 1;
     }
+    __syncthreads();
+    for (int i = tid; i < nc; i += kSelThreads) rows[ns + base_sh + i] = candf[i];
     __syncthreads();
     if (!last_sh) return;
     if (wave == 0) {  // the group keys, one lane each, and the candidate count, all in flight at once
