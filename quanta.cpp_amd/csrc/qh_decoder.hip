@@ -529,6 +529,7 @@ __device__ void norm_quant_lds(float* xs, int D, const RowF4<R>& wr, float eps, 
 // workgroup 0 also stores it as the residual stream x_out. tmp: LDS scratch of D + kChainPad floats (16-byte
 // aligned).
 struct NormAct {
+    static constexpr bool kGlobalScales = false;  // the scales are computed into LDS
     const float* x;
     const int8_t* eq;
     const uint16_t* es;
@@ -643,6 +644,7 @@ struct NormAct {
 // interface gemv_tile takes.
 template <int R, bool EMB>
 struct NormActR {
+    static constexpr bool kGlobalScales = false;
     NormAct a;
     template <bool XL>
     __device__ __forceinline__ NormAct::Pre<R> begin() const { return a.template begin<R, EMB>(); }

@@ -118,10 +118,80 @@ __host__ __device__ __forceinline__ size_t gemv_tile_lds_bytes(int cols, int til
     return xl ? f + (size_t)cols : f;
 }
 
+// The serial row chain acc = fma(p_b, dx_b, acc) for b in [0, nb) (nb % 4 == 0, nb >= 32) with the products p from
+// LDS (16-byte aligned) and the activation scales dx as scalar operands straight from global memory (dx uniform across
+// the wave, 4-byte aligned, nothing in the kernel writes it): per 32 blocks, two 64-byte scalar loads and eight
+// 16-byte LDS reads instead of sixteen LDS reads, so a long chain runs at the FMA latency (chain_lds_pipe is bound by
+// its LDS read issue: ~13 cycles per block at 152 blocks). Scalar loads return out of order, so each batch waits for
+// everything outstanding, the next batch being issued right after that wait; the last batch is read from
+// dx + nb - 32, so nothing past dx + nb is read. Every lane of the wave calls it (lanes without a row ignore the result).
+typedef float gv16f __attribute__((ext_vector_type(16)));
+typedef const __attribute__((address_space(4))) gv16f* const_gv16f_ptr;
+__device__ __forceinline__ void gemv_wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }  // lgkmcnt(0) only
+__device__ __forceinline__ float chain_lds_sdx(const float* p, const float* dx, int nb) {
+    struct Batch {
+        gv16f d0, d1;
+        float4 q[8];
+    };
+    const int nfull = nb & ~31;  // blocks in whole batches of 32
+    auto ld = [&](Batch& bt, int b) {  // b: a whole batch's start, or the tail's nb - 32
+        const const_gv16f_ptr d = (const_gv16f_ptr)(dx + b);
+        bt.d0 = d[0];
+        bt.d1 = d[1];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) bt.q[i] = *reinterpret_cast<const float4*>(p + b + 4 * i);
+    };
+    float acc = 0.0f;
+    auto use = [&](const Batch& bt, int from) {  // blocks from .. 31 of the batch (from uniform, a multiple of 4)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (4 * i < from) continue;
+            const gv16f& d = i < 4 ? bt.d0 : bt.d1;
+            const int o = (4 * i) & 15;
+            acc = __builtin_fmaf(bt.q[i].x, d[o], acc);
+            acc = __builtin_fmaf(bt.q[i].y, d[o + 1], acc);
+            acc = __builtin_fmaf(bt.q[i].z, d[o + 2], acc);
+            acc = __builtin_fmaf(bt.q[i].w, d[o + 3], acc);
+        }
+    };
+    Batch A, B;
+    ld(A, nfull > 0 ? 0 : nb - 32);
+    int b = 0;
+#pragma unroll 1
+    for (; b + 64 <= nfull; b += 64) {
+        gemv_wait_lgkm0();
+        __builtin_amdgcn_sched_barrier(0);
+        ld(B, b + 32);
+        __builtin_amdgcn_sched_barrier(0);
+        use(A, 0);
+        gemv_wait_lgkm0();
+        __builtin_amdgcn_sched_barrier(0);
+        ld(A, b + 64 < nfull ? b + 64 : nb - 32);
+        __builtin_amdgcn_sched_barrier(0);
+        use(B, 0);
+    }
+    gemv_wait_lgkm0();
+    __builtin_amdgcn_sched_barrier(0);
+    if (b < nfull) {  // one whole batch left in A, then the tail (if any)
+        if (nfull < nb) ld(B, nb - 32);
+        __builtin_amdgcn_sched_barrier(0);
+        use(A, 0);
+        if (nfull < nb) {
+            gemv_wait_lgkm0();
+            __builtin_amdgcn_sched_barrier(0);
+            use(B, 32 - (nb - nfull));
+        }
+    } else if (nfull < nb) {  // A holds the tail
+        use(A, 32 - (nb - nfull));
+    }
+    return acc;
+}
+
 // Stages the activation for a tile: its block scales into xds and, when the codes are read from LDS (XL), its codes
 // into xs, straight from the quantized activation in global memory: begin() issues the first loads (ahead of the
 // tile's weight loads), fill() stores them and loads the rest.
 struct GlobalAct {
+    static constexpr bool kGlobalScales = true;  // xd holds the scales in global memory (scalar-operand chains)
     const int8_t* __restrict__ xq;
     const float* __restrict__ xd;
     int nb;
@@ -174,6 +244,19 @@ __device__ __forceinline__ float gemv_tile(const GemvSegs<NSEG>& sg, const int8_
     const auto pre = act.template begin<XL>();  // the activation's loads go out first: the products wait for them
     GemvPass<DT, U, XL, NSEG> cur;
     cur.load(sg, split, xq, 0, nchunks - 1, nb, nb_magic);
+    // The scalar-operand chain's scales: one scalar load per 64-byte line into the scalar cache, on the chain's wave,
+    // while the weights stream.
+    constexpr int kWarm = 16;
+    uint32_t warm[kWarm];
+    bool warmed = false;
+    if constexpr (Act::kGlobalScales) {
+        warmed = nb >= 64 && (nb & 3) == 0 && NSEG * nrows <= 64;
+        if (warmed && tid < 64) {
+            const __attribute__((address_space(4))) uint32_t* q = (const __attribute__((address_space(4))) uint32_t*)act.xd;
+#pragma unroll
+            for (int i = 0; i < kWarm; ++i) warm[i] = q[min(i * 16, nb - 1)];
+        }
+    }
     act.template fill<XL>(pre, xs, xds);
     zero_chain_prefix(dxs, prod, nb, vrows);
     if constexpr (XL) __syncthreads();
@@ -194,7 +277,23 @@ __device__ __forceinline__ float gemv_tile(const GemvSegs<NSEG>& sg, const int8_
         }
     }
     QH_WSTAMP(tlk, 2);
+    if constexpr (Act::kGlobalScales) {
+        if (warmed && tid < 64) {  // the warm-up loads are held until here, so they cannot be dropped
+            asm volatile("" ::"s"(warm[0]), "s"(warm[1]), "s"(warm[2]), "s"(warm[3]), "s"(warm[4]), "s"(warm[5]),
+                         "s"(warm[6]), "s"(warm[7]));
+            asm volatile("" ::"s"(warm[8]), "s"(warm[9]), "s"(warm[10]), "s"(warm[11]), "s"(warm[12]), "s"(warm[13]),
+                         "s"(warm[14]), "s"(warm[15]));
+        }
+    }
     __syncthreads();
+    if constexpr (Act::kGlobalScales) {
+        // Long rows: the scalar-operand chain, on the wave holding the row lanes (vrows <= 64, uniform).
+        if (warmed) {
+            if (tid >= 64) return 0.0f;
+            const float v = chain_lds_sdx(prod + min(tid, vrows - 1) * pstride + zp, act.xd, nb);
+            return tid < vrows ? v : 0.0f;
+        }
+    }
     return tid < vrows ? chain_lds_pipe(prod + tid * pstride, dxs, L) : 0.0f;
 }
 
