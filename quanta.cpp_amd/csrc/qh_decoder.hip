@@ -172,14 +172,14 @@ __device__ __forceinline__ const T* lane_ptr(const T* p) {
 }
 
 template <typename Op>
-__device__ __forceinline__ float lds_chain(const float* p, int n, Op op) {
+__device__ __forceinline__ float lds_chain(const float* p, int n, Op op, float acc0 = 0.0f) {
     float4 a[8], b[8];
     auto ld = [](float4(&r)[8], const float* q) {
         const float4* q4 = reinterpret_cast<const float4*>(q);
 #pragma unroll
         for (int k = 0; k < 8; ++k) r[k] = q4[k];
     };
-    float acc = 0.0f;
+    float acc = acc0;
     auto use = [&](const float4(&r)[8], int cnt) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -474,6 +474,36 @@ __device__ float seg_sum_squares(const float* __restrict__ x, int D, const RowF4
     return r;
 }
 
+// seg_sum_squares for a row held in LDS (xs, complete, 16-byte aligned, kChainPad floats of slack; written in this
+// kernel, so not readable through scalar loads): the same segments and candidate starts, each segment's chain reading
+// its operands from LDS (the four waves' broadcast reads slow each other, ~12 cycles per element, against ~6 for
+// scalar operands, still a quarter of the serial chain). xr: this thread's RowF4 of the row's values. All 256 threads
+// call it (two barriers inside).
+template <int R>
+__device__ float seg_sum_squares_lds(const float* xs, int D, const RowF4<R>& xr) {
+    __shared__ SegShared sh;
+    const int tid = (int)threadIdx.x, n4 = D / 4;
+    const Segs4 sg = seg_split(D);
+    double p1 = 0.0, p2 = 0.0, p3 = 0.0;
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        const int i4 = tid + 256 * k;
+        if (i4 < n4) {
+            const float4 v = xr.v[k];
+            const double s = (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+            const int e = 4 * i4;
+            p1 += e < sg.start(1) ? s : 0.0;
+            p2 += e < sg.start(2) ? s : 0.0;
+            p3 += e < sg.start(3) ? s : 0.0;
+        }
+    }
+    seg_partials(sh, p1, p2, p3);
+    __syncthreads();
+    return seg_chain_run(sh, [&](int k, float s0) {
+        return lds_chain(xs + sg.start(k), sg.len(k), [](float acc, float v) { return __builtin_fmaf(v, v, acc); }, s0);
+    });
+}
+
 // rmsnorm scale 1 / sqrt(ss / D + eps) (ops_ref.cpp:197-198).
 __device__ __forceinline__ float rms_scale(float ss, int D, float eps) {
     return 1.0f / __builtin_sqrtf(ss / (float)D + eps);
@@ -714,12 +744,14 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(float* __restric
             v.y = v.y + orow.v[k].y;
             v.z = v.z + orow.v[k].z;
             v.w = v.w + orow.v[k].w;
+            xr.v[k] = v;
             reinterpret_cast<float4*>(x + (size_t)t * D)[i4] = v;
             reinterpret_cast<float4*>(xs)[i4] = v;
         }
     }
     __syncthreads();
-    norm_quant_lds(xs, D, wr, eps, xq + (size_t)t * D, xd + (size_t)t * (D / QK), normed);
+    const float ss = D >= 128 ? seg_sum_squares_lds(xs, D, xr) : lds_sum_squares(xs, D);  // uniform
+    normalize_quant_lds(xs, D, rms_scale(ss, D, eps), wr, xq + (size_t)t * D, xd + (size_t)t * (D / QK), normed);
 }
 
 // Attention of token t (position pos0 + t) and query head h over positions [0, pos0 + t], for a chunk of n <= 32
