@@ -926,7 +926,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     float sc[kKPre];
     {
 #pragma unroll
-        for (int r = 0; r < kKPre; ++r) sc[r] = dot_row(kpre[r]) * scale;
+        for (int r = 0; r < kKPre; ++r)  // uniform: no thread has a cached row tid + 256 r at or past pos0
+            sc[r] = 256 * r < pos0 ? dot_row(kpre[r]) * scale : 0.0f;
 #pragma unroll
         for (int r = 0; r < kKPre; ++r) {
             const int j = tid + 256 * r;
