@@ -763,17 +763,19 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(float* __restric
 // chunk's own rows are rebuilt from k / v (bias, RoPE, f16 rounding, exactly as stored), and workgroups of the first
 // query head of each KV group store their token's row. The output (HD values) is quantized straight into oq / od
 // ([n][n_heads*HD] codes, one scale per 32 values).
-// The LDS footprint allows one workgroup per CU (one wave per SIMD); saying so lets the compiler keep the V preload
-// in registers.
-template <int HD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attention_kernel(
+// WPE = 1: a 96 KB V stage, one workgroup per CU (one wave per SIMD, which lets the compiler keep three cached K rows
+// per thread in registers). WPE = 2 (prefill chunks at head_dim 64): a 32 KB stage (256 rows) and two cached K rows
+// per thread, so two workgroups share a CU (LDS under 80 KB, registers under 256 each) and the 448 workgroups of a
+// 14-head chunk run in one round instead of two; their serial chains leave each SIMD mostly idle.
+template <int HD, int WPE = 1>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void attention_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv,
     const float* __restrict__ cs, const int* __restrict__ pos_dev, int ctx, int n_heads, int n_kv,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int8_t* __restrict__ oq, float* __restrict__ od,
     float* __restrict__ escr, int escr_stride, int* __restrict__ status) {
     constexpr int HALF = HD / 2, CPR = HD / 8;           // 16-byte chunks per f16 K row
-    constexpr int kVRows = kVStageBytes / (HD * 2);      // V rows one LDS stage holds (a multiple of 8)
+    constexpr int kVRows = (WPE == 1 ? kVStageBytes : 32 * 1024) / (HD * 2);  // V rows one LDS stage holds (mult. of 8)
     constexpr int kVBlk = kVRows / 8;                    // 8-row blocks per stage
     __shared__ __align__(16) float att[kMaxCtx + kChainPad];
     __shared__ __align__(16) uint4 vst[(kVBlk + 4) * HD];  // [block][dim] -> 8 rows; 4 blocks of read padding
@@ -842,7 +844,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // This thread's cached K rows for the first score rows (registers) go out behind those (a load waits for every
     // load issued before it), and their issue, which stalls while the memory pipeline drains, covers the q / k / v
     // latency. No row read here is written by this launch: K rows stop below pos0.
-    constexpr int kKPre = 3;  // score rows per thread loaded up front (768 positions)
+    constexpr int kKPre = WPE == 1 ? 3 : 2;  // score rows per thread loaded up front (768 / 512 positions)
     const int grow = pos0 > 0 ? pos0 - 1 : 0;
     v4u kpre[kKPre][CPR];
 #pragma unroll
@@ -1916,7 +1918,7 @@ hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
                            bias(d, l, L_BQ), bias(d, l, L_BK), hp.n_kv_heads, bias(d, l, L_BV), d->cs,
                            d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status);
     else if (hp.head_dim == 64)
-        qh_launch((attention_kernel<64>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
+        qh_launch((attention_kernel<64, 2>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                            bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
                            d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status);
     else
