@@ -262,8 +262,8 @@ struct StageRegs {
     float dx;     // token tid / 16, block tid % 16
 };
 
-template <int DT>
-__global__ __launch_bounds__(kMmThreads) void matmul_stage_kernel(MmSegs segs, const int8_t* __restrict__ xq,
+template <int DT, int NS>
+__global__ __launch_bounds__(NS == 0 ? kMmThreads : 2 * kMmThreads) void matmul_stage_kernel(MmSegs segs, const int8_t* __restrict__ xq,
                                                               const float* __restrict__ xd, int cols, int n,
                                                               int n_tg) {
     using R = StageRegs<DT>;
@@ -273,9 +273,12 @@ __global__ __launch_bounds__(kMmThreads) void matmul_stage_kernel(MmSegs segs, c
     constexpr int kAupr = KC * kBw / 16, kXupr = KC * QK / 16;  // 16-byte units per row
     __shared__ __align__(16) uint8_t as[2][16 * kArow];
     __shared__ __align__(16) int8_t xs[2][16 * kXrow];
-    __shared__ float dws[2][16][KC + 1];
-    __shared__ float dxs[2][16][KC + 1];
-    __shared__ int sl[KC][16][20];
+    // Block sums and token scales by (row or token, block): a chain reads its chunk as 16-byte units, unit u of
+    // token t stored at u ^ ((t >> 2) & 3) so that 8 lanes of consecutive tokens hit distinct banks.
+    constexpr int kSb = NS == 0 ? 2 : 3, kLb = NS == 0 ? 1 : 2;  // scale and block-sum buffers
+    __shared__ float4 dws[kSb][16][KC / 4];  // [row][block]: chunk c in buffer c % kSb
+    __shared__ float4 dxs[kSb][16][KC / 4];  // [token][block], swizzled
+    __shared__ int4 sl[kLb][16][16][KC / 4];  // [row][token][block], swizzled: chunk c in buffer c % kLb
     const int nb = cols / QK;
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
@@ -323,7 +326,7 @@ __global__ __launch_bounds__(kMmThreads) void matmul_stage_kernel(MmSegs segs, c
         S.dw = dwsrc[b];
         S.dx = dxsrc[b];
     };
-    auto stage = [&](const R& S, int buf) {
+    auto stage = [&](const R& S, int buf, int sbuf) {
 #pragma unroll
         for (int j = 0; j < R::kAu; ++j) {
             const int e = j * kMmThreads + tid;
@@ -334,12 +337,15 @@ __global__ __launch_bounds__(kMmThreads) void matmul_stage_kernel(MmSegs segs, c
             const int e = j * kMmThreads + tid;
             *reinterpret_cast<uint4*>(&xs[buf][(e / kXupr) * kXrow + (e % kXupr) * 16]) = S.x[j];
         }
-        dws[buf][tid / 16][sk] = f16_to_f32(S.dw);
-        dxs[buf][tid / 16][sk] = S.dx;
+        const int t = tid / 16;
+        uint32_t h = S.dw;
+        asm volatile("" : "+v"(h));  // keeps the conversion here (hoisted, it would wait for every set's loads)
+        reinterpret_cast<float*>(&dws[sbuf][t][0])[sk] = f16_to_f32((uint16_t)h);
+        reinterpret_cast<float*>(&dxs[sbuf][t][0])[4 * ((sk >> 2) ^ ((t >> 2) & 3)) + (sk & 3)] = S.dx;
     };
     const int shift = DT == kQ8 ? 0 : (lq >> 1) * 4;
     // The wave's 4 blocks: operands read together, 4 independent MFMAs, then the block sums out.
-    auto products = [&](int buf) {
+    auto products = [&](int buf, int lbuf) {
         long a[4], x[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -359,21 +365,30 @@ __global__ __launch_bounds__(kMmThreads) void matmul_stage_kernel(MmSegs segs, c
             }
             c[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ai, x[i], (v4i){0, 0, 0, 0}, 0, 0, 0);
         }
+        // row 4 lq + k, token li: the sums of blocks 4 wave .. 4 wave + 3 as one unit
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int k = 0; k < 4; ++k) sl[wave * 4 + i][4 * lq + k][li] = c[i][k];
+        for (int k = 0; k < 4; ++k) sl[lbuf][4 * lq + k][li][wave ^ ((li >> 2) & 3)] = (int4){c[0][k], c[1][k], c[2][k], c[3][k]};
     };
     // Chain of this thread: row tid / 16, token tid % 16 (the LDS kernel's pairing at one token tile).
-    const int crow = tid / 16, ctok = tid % 16;
+    const int ctid = NS == 0 ? tid : tid - kMmThreads;
+    const int crow = ctid / 16, ctok = ctid % 16;
     float acc = 0.0f;
-    auto chains = [&](int buf, int c0) {
+    auto chains = [&](int lbuf, int sbuf, int c0) {
         const int nblk = min(KC, nb - c0);
         float pv[KC], dxv[KC];
+        const int sw = (ctok >> 2) & 3;
 #pragma unroll
-        for (int k = 0; k < KC; ++k) {
-            pv[k] = (float)sl[k][crow][ctok] * dws[buf][crow][k];
-            dxv[k] = dxs[buf][ctok][k];
+        for (int u = 0; u < KC / 4; ++u) {
+            const int4 si = sl[lbuf][crow][ctok][u ^ sw];
+            const float4 w = dws[sbuf][crow][u], d = dxs[sbuf][ctok][u ^ sw];
+            pv[4 * u + 0] = (float)si.x * w.x;
+            pv[4 * u + 1] = (float)si.y * w.y;
+            pv[4 * u + 2] = (float)si.z * w.z;
+            pv[4 * u + 3] = (float)si.w * w.w;
+            dxv[4 * u + 0] = d.x;
+            dxv[4 * u + 1] = d.y;
+            dxv[4 * u + 2] = d.z;
+            dxv[4 * u + 3] = d.w;
         }
 #pragma unroll
         for (int k = 0; k < KC; ++k) {
@@ -382,35 +397,68 @@ __global__ __launch_bounds__(kMmThreads) void matmul_stage_kernel(MmSegs segs, c
         }
     };
 
-    // Chunk c is in LDS buffer c % 2 when its products start; the register sets hold chunks c + 1 and c + 2 (loads
-    // in flight), and each set is refilled with the chunk two past the one it hands to LDS. Loads past the last chunk
-    // are clamped re-reads whose values are never used.
-    const int n_chunks = (nb + KC - 1) / KC;
-    R S0, S1;
-    load(S0, 0);
-    load(S1, KC);
-    __builtin_amdgcn_sched_barrier(0);
-    stage(S0, 0);
-    load(S0, 2 * KC);
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    for (int c = 0;; c += 2) {
-        products(0);
-        __syncthreads();
-        chains(0, c * KC);
-        if (c + 1 >= n_chunks) break;
-        stage(S1, 1);
-        load(S1, (c + 3) * KC);
+    if constexpr (NS == 0) {
+        // At most two chunks (nb <= 2 KC), straight-line with one block-sum buffer (the LDS of three workgroups per
+        // CU): a chain past nb adds nothing, and the products of a chunk past nb read clamped rows no chain uses.
+        R A, B;
+        load(A, 0);
+        load(B, KC);
+        __builtin_amdgcn_sched_barrier(0);
+        stage(A, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
-        products(1);
+        products(0, 0);
+        stage(B, 1, 1);
         __syncthreads();
-        chains(1, (c + 1) * KC);
-        if (c + 2 >= n_chunks) break;
-        stage(S0, 0);
-        load(S0, (c + 4) * KC);
-        __builtin_amdgcn_sched_barrier(0);
+        chains(0, 0, 0);
         __syncthreads();
+        products(1, 0);
+        __syncthreads();
+        chains(0, 1, KC);
+    } else {
+        // Eight waves: waves 0-3 load, stage and multiply, waves 4-7 run the chains, each SIMD holding one wave of
+        // each; the two kinds run separate loops that meet at one barrier per chunk (1 + n_chunks barriers each).
+        // Between two barriers the products of chunk c + 1 (operand buffer (c + 1) % 2 -> block sums (c + 1) % 2)
+        // and the chains of chunk c (block sums c % 2, scales c % 3) run together, and chunk c + 2 is staged
+        // (operands into buffer c % 2, last read by chunk c's products; scales into c + 2 mod 3). NS register sets,
+        // set k holding a chunk = k mod NS, each refilled with the chunk NS past the one it stages; loads and stages
+        // past the last chunk are clamped re-reads into buffers no later phase reads, issued on every pass so that
+        // each wait counts only the loads it needs.
+        const int n_chunks = (nb + KC - 1) / KC;
+        if (tid < kMmThreads) {
+            R S[NS];
+#pragma unroll
+            for (int i = 0; i < NS; ++i) load(S[i], i * KC);
+            __builtin_amdgcn_sched_barrier(0);
+            stage(S[0], 0, 0);
+            load(S[0], NS * KC);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+            products(0, 0);
+            stage(S[1], 1, 1);
+            load(S[1], (NS + 1) * KC);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+            for (int c = 0;; c += NS) {
+#pragma unroll
+                for (int j = 0; j < NS; ++j) {
+                    const int cc = c + j;
+                    if (cc + 1 >= n_chunks) return;
+                    products((cc + 1) & 1, (cc + 1) & 1);
+                    stage(S[(j + 2) % NS], cc & 1, (cc + 2) % 3);
+                    load(S[(j + 2) % NS], (cc + 2 + NS) * KC);
+                    __builtin_amdgcn_sched_barrier(0);
+                    __syncthreads();
+                }
+            }
+        }
+        __syncthreads();
+        __syncthreads();
+        for (int cc = 0;; ++cc) {
+            chains(cc & 1, cc % 3, cc * KC);
+            if (cc + 1 >= n_chunks) break;
+            __syncthreads();
+        }
     }
 
     const int tok = tbase + ctok, r = rbase + crow;
@@ -586,11 +634,12 @@ __global__ __launch_bounds__(64 * NW) void matmul_reg_kernel(MmSegs segs, const 
 namespace {
 
 // Launch plan: kernel family, token tiles (per workgroup for the LDS kernel, per wave for the register kernel) and
-// waves per workgroup. QH_MM="stage", "lds:TT" or "reg:TT:NW" overrides the heuristic (tuning sweeps).
+// waves per workgroup. QH_MM="stage", "stage:NS", "lds:TT" or "reg:TT:NW" overrides the heuristic (tuning sweeps).
 struct MmPlan {
     bool reg;
     int tt, nw;
     bool stage = false;  // the LDS-staged kernel (one token tile per workgroup)
+    int ns = 0;          // its register sets in flight past two chunks (2, 3 or 4; 0: default)
 };
 
 MmPlan matmul_plan(int rows, int cols, int n) {
@@ -600,6 +649,7 @@ MmPlan matmul_plan(int rows, int cols, int n) {
         int a = 0, b = 0;
         if (sscanf(env, "lds:%d", &a) == 1 && (a == 1 || a == 2 || a == 4)) return MmPlan{false, a, 4};
         if (strcmp(env, "stage") == 0) return MmPlan{false, 1, 4, true};
+        if (sscanf(env, "stage:%d", &a) == 1 && a >= 2 && a <= 4) return MmPlan{false, 1, 4, true, a};
         if (sscanf(env, "reg:%d:%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && (b == 1 || b == 2 || b == 4))
             return MmPlan{true, a, b};
     }
@@ -660,12 +710,16 @@ hipError_t launch_matmul_segs(const MmOut* m, int n_mats, const int8_t* xq, cons
     for (int i = 0; i < n_mats; ++i) aligned = aligned && (reinterpret_cast<uintptr_t>(sg.wq[i]) & 15u) == 0;
     if (pl.stage && aligned) {
         const int n_tg = (n + 15) / 16;
-        if (W.dtype == kQ8)
-            qh_launch(matmul_stage_kernel<kQ8>, dim3((unsigned)(row_tiles * n_tg)), dim3(kMmThreads), 0, s, sg, xq, xd,
-                      W.cols, n, n_tg);
-        else
-            qh_launch(matmul_stage_kernel<kQ4>, dim3((unsigned)(row_tiles * n_tg)), dim3(kMmThreads), 0, s, sg, xq, xd,
-                      W.cols, n, n_tg);
+        // Register sets in flight: the two chunks of short rows, else pl.ns (default 2)
+        const int ns = W.cols / QK <= 2 * kStKC ? 0 : pl.ns ? pl.ns : 2;
+        const dim3 grid((unsigned)(row_tiles * n_tg));
+#define QH_MM_STAGE(DT, NS)                                                                                \
+    if (W.dtype == DT && ns == NS)                                                                         \
+        qh_launch((matmul_stage_kernel<DT, NS>), grid, dim3(NS ? 2 * kMmThreads : kMmThreads), 0, s, sg, xq, xd, \
+                  W.cols, n, n_tg);
+        QH_MM_STAGE(kQ8, 0) QH_MM_STAGE(kQ8, 2) QH_MM_STAGE(kQ8, 3) QH_MM_STAGE(kQ8, 4)
+        QH_MM_STAGE(kQ4, 0) QH_MM_STAGE(kQ4, 2) QH_MM_STAGE(kQ4, 3) QH_MM_STAGE(kQ4, 4)
+#undef QH_MM_STAGE
         return hipGetLastError();
     }
     if (!pl.reg) {

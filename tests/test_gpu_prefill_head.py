@@ -205,6 +205,24 @@ def test_shortlist_full_vocab(qh, oracle, synth, gpu):
     assert np.float32(st["top1_logit"]).tobytes() == full[st["top1"]].cpu().numpy().tobytes()
 
 
+@pytest.mark.parametrize("tt", ["stage", "stage:2", "stage:3", "stage:4"])
+@pytest.mark.parametrize("K", [512, 1536, 2560, 3584, 5632, 8192])
+@pytest.mark.parametrize("dtype", [2, 3])
+def test_matmul_staged_chunk_counts(qh, oracle, synth, gpu, monkeypatch, tt, dtype, K):
+    """The LDS-staged kernel at every chunk count it plans for (16 blocks a chunk): one chunk, the straight-line short
+    rows, all chunks held in registers (4 / 6 / 8 / 12 sets, odd counts with a clamped spare) and the refilled
+    2 / 3 / 4 set pipeline past that."""
+    monkeypatch.setenv("QH_MM", tt)
+    N = 40
+    buf = synth.q8_tensor(83 + K, N, K) if dtype == 2 else synth.q4_tensor(89 + K, N, K)
+    W = qh.DeviceTensor.upload(buf, dtype, N, K)
+    for M in (1, 17, 40):
+        xq, xd = qh.quantize_q8(_dev(synth.activations(97 + M, M, K), gpu))
+        got = qh.matmul_q(W, xq, xd).cpu().numpy()
+        want = oracle.matmul_q(dtype, N, K, buf, xq.cpu().numpy(), xd.cpu().numpy(), threads=8)
+        assert (bits(got) == bits(want)).all(), (tt, M)
+
+
 @pytest.mark.parametrize("tt", ["stage", "lds:1", "lds:2", "lds:4", "reg:1:1", "reg:1:4", "reg:2:2", "reg:4:1", "reg:4:4"])
 @pytest.mark.parametrize("dtype,N,K", [(2, 200, 896), (3, 200, 896), (2, 40, 4864), (3, 40, 4864)])
 def test_matmul_every_token_tiling(qh, oracle, synth, gpu, monkeypatch, tt, dtype, N, K):
