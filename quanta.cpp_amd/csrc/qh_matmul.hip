@@ -246,10 +246,11 @@ __global__ __launch_bounds__(kMmThreads) void matmul_lds_kernel(MmSegs segs, con
 
 // Staged variant for few (row tile, token tile) pairs: the chunk's weights, activation codes and scales are brought
 // into LDS by coalesced 16-byte loads (8 full cache lines per wave instruction, against 16 partly used lines for an
-// operand loaded in MFMA layout, whose per-CU address processing bounds the other kernels at 32 tokens), two chunks
-// ahead in registers; the waves then read their MFMA operands from LDS. Tile, block split across waves, block sums and
-// chains are the LDS kernel's: wave w multiplies blocks 4w..4w+3 of each 16-block chunk, all 256 threads run one
-// (row, token) chain each.
+// operand loaded in MFMA layout, whose per-CU address processing bounds the other kernels at 32 tokens), chunks ahead
+// in registers; the waves then read their MFMA operands from LDS. Tile and block split as in the LDS kernel: wave w
+// multiplies blocks 4w..4w+3 of each 16-block chunk, 256 threads run one (row, token) chain each. Rows of one or two
+// chunks run on 4 waves (the same threads multiply and chain); longer rows on 8, four that load, stage and multiply
+// and four that run the chains of the chunk before.
 constexpr int kStKC = 16;  // blocks per chunk
 template <int DT>
 struct StageRegs {
