@@ -832,13 +832,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     };
     const float* bqh = bq ? bq + h * HD : nullptr;
     const float* bkh = bk ? bk + kvh * HD : nullptr;
-    // The first element of each loop below is loaded first (indices clamped, so every load is unconditional).
+    // Every element this thread rebuilds is loaded before any is used (indices clamped, so every load is
+    // unconditional and the loads are one round trip): K pair elements tid + 256 i and V elements tid + 256 i of the
+    // chunk's rows 0..t. 256 is a multiple of HD, so a thread's elements share their dimension, and its biases.
+    static_assert(256 % HD == 0, "a thread's rebuilt elements share one dimension");
+    constexpr int KPT = kChunk * HALF / 256, VPT = kChunk * HD / 256;  // elements per thread at n = kChunk
     const int tq = min(tid, HALF - 1);
     const Pair qp = load_pair(qsrc, bqh, tq, cs + (size_t)pos * HD);
-    const int ek = min(tid, nk - 1), rk = ek / HALF, ik = ek - rk * HALF;
-    const Pair kp0 = load_pair(ksrc + (size_t)rk * kvd, bkh, ik, cs + (size_t)(pos0 + rk) * HD);
-    const int ev = min(tid, nv - 1), rv = ev / HD, iv = ev - rv * HD;
-    const float v0 = vsrc[(size_t)rv * kvd + iv], vb0 = bv ? bv[kvh * HD + iv] : 0.0f;
+    const int ik = tid % HALF, iv = tid % HD;
+    const float kba = bkh ? bkh[ik] : 0.0f, kbb = bkh ? bkh[ik + HALF] : 0.0f;
+    const float vb = bv ? bv[kvh * HD + iv] : 0.0f;
+    float ka[KPT], kb[KPT], vv[VPT];
+    float2 kcs[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        const int rk = min(tid + 256 * i, nk - 1) / HALF;
+        const float* row = ksrc + (size_t)rk * kvd;
+        ka[i] = row[ik];
+        kb[i] = row[ik + HALF];
+        kcs[i] = *reinterpret_cast<const float2*>(cs + (size_t)(pos0 + rk) * HD + 2 * ik);
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) vv[i] = vsrc[(size_t)(min(tid + 256 * i, nv - 1) / HD) * kvd + iv];
     __builtin_amdgcn_sched_barrier(0);
 
     // This thread's cached K rows for the first score rows (registers) go out behind those (a load waits for every
@@ -854,20 +869,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
         for (int i = 0; i < CPR; ++i) kpre[r][i] = ld4(kg + (size_t)i * ctx * 8);
     }
     if (tid < HALF) rope(qp, bq != nullptr, qs[tid], qs[tid + HALF]);
-    for (int e = tid; e < nk; e += 256) {
-        const int r = e / HALF, i = e - r * HALF;
-        const Pair pr =
-            e == tid ? kp0 : load_pair(ksrc + (size_t)r * kvd, bkh, i, cs + (size_t)(pos0 + r) * HD);
-        float lo, hi;
-        rope(pr, bk != nullptr, lo, hi);
-        kloc[r * HD + i] = f2h(lo);
-        kloc[r * HD + i + HALF] = f2h(hi);
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        const int e = tid + 256 * i;
+        if (e < nk) {
+            const int r = e / HALF;
+            float lo, hi;
+            rope(Pair{ka[i], kb[i], kba, kbb, kcs[i].x, kcs[i].y}, bk != nullptr, lo, hi);
+            kloc[r * HD + ik] = f2h(lo);
+            kloc[r * HD + ik + HALF] = f2h(hi);
+        }
     }
-    for (int e = tid; e < nv; e += 256) {
-        const int r = e / HD, i = e - r * HD;
-        float val = e == tid ? v0 : vsrc[(size_t)r * kvd + i];
-        if (bv) val = val + (e == tid ? vb0 : bv[kvh * HD + i]);
-        vloc[r * HD + i] = f2h(val);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int e = tid + 256 * i;
+        if (e < nv) vloc[(e / HD) * HD + iv] = f2h(bv ? vv[i] + vb : vv[i]);
     }
     et.store(exptab);
     __syncthreads();
@@ -960,9 +976,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     // exp, kept in LDS and, for the segmented softmax sum, in this workgroup's global row (read back through scalar
     // loads after the barrier below), with each lane's exact partial sums below the segment starts
     float* erow = escr + (size_t)(t * gridDim.x + h) * escr_stride;
-    // the normalized weights, for the V chain's scalar loads (lines of their own: none of them is in the scalar cache
-    // with older contents)
-    float* arow = escr + (size_t)((gridDim.y + t) * gridDim.x + h) * escr_stride;
     const bool seg = nrows >= 128;  // uniform; shorter rows keep the single chain
     const int Ls = (nrows / 4) & ~15;
     const Segs4 sg{(nrows - 3 * Ls) & ~15, Ls, nrows};
@@ -993,11 +1006,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     }
     const float inv = 1.0f / sum;
     for (int j = tid; j < nrows; j += 256) {
-        const float a = att[j] * inv;
-        att[j] = a;
-        arow[j] = a;
+        att[j] = att[j] * inv;
     }
-    // the weight row's stores and the V DMA are complete before the barrier; then the chunk's rows that fall inside
+    // the V DMA is complete before the barrier; then the chunk's rows that fall inside
     // the first stage are written over the DMA's blocks
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -1012,75 +1023,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     }
 
     // out_i = sum_j a_j * v_ji, one FMA per position in order (model.cpp:131-135): thread i per dimension, over
-    // the rows of each LDS stage. The weights come as scalar operands (scalar loads of arow, 32 per batch, the next
-    // batch's loads and V reads in flight while one batch is consumed), so a batch of 32 positions is 4 V reads and
-    // 32 FMAs; the waves without dimensions bring the weight row into the scalar cache meanwhile. V reads past the
-    // stage stay inside its padding, weight reads inside arow's slack (64 floats past the context).
+    // the rows of each LDS stage. The weights are broadcast LDS reads of att (every lane the same address), so a
+    // batch of 32 positions is 4 V reads, 8 weight reads and 32 FMAs, the next batch's reads in flight while one is
+    // consumed. (With scalar operands from a global copy of the weights, written just before, the first stage's
+    // chain ran 1.4x slower at two workgroups per CU.) V reads past the stage stay inside its padding, weight reads
+    // inside att's padding.
+    // Past the first stage, the threads without a dimension load the next stage's cache blocks into registers while
+    // the chain runs (kPreload: at most 12 16-byte units each), so only LDS stores stand between two stages.
+    constexpr int kLoaders = 256 - HD, kPre = (kVBlk * HD + kLoaders - 1) / kLoaders;
+    constexpr bool kPreload = kPre <= 12;
+    uint4 nxt[kPreload ? kPre : 1];
     float acc = 0.0f;
     for (int s0 = 0;;) {
         const int se = min(nrows, s0 + kVRows);
+        if (kPreload && tid >= HD && se < nrows) {  // uniform per wave; pos0 >= 1 here (a second stage)
+            const int nb8 = (min(nrows, se + kVRows) - se + 7) / 8, lastc = (pos0 - 1) / 8;
+#pragma unroll
+            for (int u = 0; u < kPre; ++u) {
+                const int c = tid - HD + kLoaders * u, blk = se / 8 + c / HD, d = c % HD;
+                const uint4 x = vc4[vchunk(min(blk, lastc), d)];
+                nxt[u] = c < nb8 * HD && blk * 8 < pos0 ? x : make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
         if (tid < HD) {
-            const_v16f_ptr wp = (const_v16f_ptr)(arow + s0);  // s0 is a multiple of 32: 64-byte aligned
-            auto ldv = [&](uint4(&vv)[4], int jr) {  // rows s0 + jr .. + 31 (jr % 32 == 0)
+            // The weights are LDS broadcast reads of att (one 16-byte read gives every lane 4 weights), a batch
+            // ahead of the chain.
+            const float4* ap = reinterpret_cast<const float4*>(att + s0);  // s0 is a multiple of 32
+            auto ldv = [&](uint4(&vv)[4], float4(&w)[8], int jr) {  // rows s0 + jr .. + 31 (jr % 32 == 0)
                 const uint4* vp = vst + (jr >> 3) * HD + tid;
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) vv[q4] = vp[q4 * HD];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) w[q] = ap[jr / 4 + q];
             };
-            auto use = [&](const uint4(&vv)[4], const v16f& w0, const v16f& w1, int cnt) {
+            auto use = [&](const uint4(&vv)[4], const float4(&w)[8], int cnt) {
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) {
-                    const uint32_t w[4] = {vv[q4].x, vv[q4].y, vv[q4].z, vv[q4].w};
+                    const uint32_t v[4] = {vv[q4].x, vv[q4].y, vv[q4].z, vv[q4].w};
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int k = 8 * q4 + e;
+                        const float4 wq = w[k >> 2];
+                        const float wk = (k & 3) == 0 ? wq.x : (k & 3) == 1 ? wq.y : (k & 3) == 2 ? wq.z : wq.w;
                         if (k < cnt)
-                            acc = __builtin_fmaf(k < 16 ? w0[k & 15] : w1[k & 15],
-                                                 h2f((uint16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xffffu)), acc);
+                            acc = __builtin_fmaf(wk, h2f((uint16_t)(e & 1 ? v[e >> 1] >> 16 : v[e >> 1] & 0xffffu)),
+                                                 acc);
                     }
                 }
             };
             const int n = se - s0;
             uint4 vA[4], vB[4];
-            v16f wA0 = wp[0], wA1 = wp[1], wB0, wB1;
-            ldv(vA, 0);
+            float4 wA[8], wB[8];
+            ldv(vA, wA, 0);
             int jr = 0;
 #pragma unroll 1
             for (; jr + 64 <= n; jr += 64) {
-                wait_lgkm0();
-                __builtin_amdgcn_sched_barrier(0);
-                wB0 = wp[(jr + 32) / 16];
-                wB1 = wp[(jr + 32) / 16 + 1];
-                ldv(vB, jr + 32);
-                __builtin_amdgcn_sched_barrier(0);
-                use(vA, wA0, wA1, 32);
-                wait_lgkm0();
-                __builtin_amdgcn_sched_barrier(0);
-                wA0 = wp[(jr + 64) / 16];
-                wA1 = wp[(jr + 64) / 16 + 1];
-                ldv(vA, jr + 64);
-                __builtin_amdgcn_sched_barrier(0);
-                use(vB, wB0, wB1, 32);
+                ldv(vB, wB, jr + 32);
+                use(vA, wA, 32);
+                ldv(vA, wA, jr + 64);
+                use(vB, wB, 32);
             }
-            wait_lgkm0();
-            __builtin_amdgcn_sched_barrier(0);
             if (jr + 32 <= n) {
-                wB0 = wp[(jr + 32) / 16];
-                wB1 = wp[(jr + 32) / 16 + 1];
-                ldv(vB, jr + 32);
-                __builtin_amdgcn_sched_barrier(0);
-                use(vA, wA0, wA1, 32);
-                wait_lgkm0();
-                __builtin_amdgcn_sched_barrier(0);
-                use(vB, wB0, wB1, n - jr - 32);
+                ldv(vB, wB, jr + 32);
+                use(vA, wA, 32);
+                use(vB, wB, n - jr - 32);
             } else {
-                use(vA, wA0, wA1, n - jr);
-            }
-        } else if (s0 == 0) {  // waves without dimensions: 16 lines of the weight row per scalar-load batch
-            const int nw = 4 - HD / 64, wi = __builtin_amdgcn_readfirstlane(wave - HD / 64);
-            for (int b = wi * 256; b < nrows; b += nw * 256) {
-                SegWarm warm;
-                warm.issue(arow + b, nrows - b);
-                warm.consume();
+                use(vA, wA, n - jr);
             }
         }
         s0 = se;
@@ -1088,9 +1096,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
         __syncthreads();  // the stage is consumed; load rows [s0, min(nrows, s0 + kVRows)) (s0 % 8 == 0)
         const int sn = min(nrows, s0 + kVRows);
         const int nb8 = (sn - s0 + 7) / 8;
-        for (int c = tid; c < nb8 * HD; c += 256) {  // whole cache blocks; the chunk's rows are written after
-            const int blk = s0 / 8 + c / HD, d = c % HD;
-            vst[c] = blk * 8 < pos0 ? vc4[vchunk(blk, d)] : make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (kPreload) {
+            if (tid >= HD) {
+#pragma unroll
+                for (int u = 0; u < kPre; ++u) {
+                    const int c = tid - HD + kLoaders * u;
+                    if (c < nb8 * HD) vst[c] = nxt[u];
+                }
+            }
+        } else {
+            for (int c = tid; c < nb8 * HD; c += 256) {  // whole cache blocks; the chunk's rows are written after
+                const int blk = s0 / 8 + c / HD, d = c % HD;
+                vst[c] = blk * 8 < pos0 ? vc4[vchunk(blk, d)] : make_uint4(0u, 0u, 0u, 0u);
+            }
         }
         __syncthreads();
         for (int e = tid; e < (sn - max(s0, pos0)) * HD; e += 256) {
