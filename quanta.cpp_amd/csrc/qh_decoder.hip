@@ -1535,6 +1535,220 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
     quant_block32(gv / (1.0f + dev_expf(-gv)) * u[i], oq + blk * QK, od + blk);
 }
 
+// Prefill gate / up, SwiGLU and quantization of the down projection's input in one launch (model.cpp:212-218 for a
+// chunk of n tokens; ops_ref.cpp:122-160, 243-248, 69-83). Workgroup (b, g): rows [32 b, 32 b + 32) of gate and of up
+// for tokens [16 g, 16 g + 16). The chunk's 64 weight rows, 16 activation rows and their scales are staged in LDS
+// by coalesced 16-byte loads, 16 blocks at a time (the next chunk's loads in flight); wave w multiplies row tile w
+// (gate rows 0-15, 16-31, up rows 0-15, 16-31 of the block) by the token tile with one int8 MFMA per block and runs
+// the chains of its own results in registers: lane l holds rows 4 (l / 16) + i, token l % 16, acc = fma(float(s) *
+// dw, dx, acc) in block order, as the other matmul kernels. Then h = g / (1 + expf(-g)) * u and the quantization of
+// each token's 32 values (one block of the down projection's input) by 32 lanes. SHORT: at most two chunks
+// (cols <= 1024), straight-line.
+constexpr int kSwKC = 16;  // blocks per chunk
+template <int DT>
+struct SwRegs {
+    static constexpr int kBw = DT == kQ8 ? QK : QK / 2;           // weight bytes per block
+    static constexpr int kAu = 64 * kSwKC * kBw / 16 / 256;        // 16-byte weight units per thread (8 / 4)
+    static constexpr int kXu = 16 * kSwKC * QK / 16 / 256;         // 16-byte activation units per thread (2)
+    static constexpr int kWu = 64 * kSwKC / 256;                   // row scales per thread (4)
+    uint4 a[kAu];
+    uint4 x[kXu];
+    uint16_t dw[kWu];
+    float dx;
+};
+
+template <int DT, bool SHORT>
+__global__ __launch_bounds__(256) void matmul_swiglu_kernel(const uint8_t* __restrict__ wg,
+                                                            const uint16_t* __restrict__ sgt,
+                                                            const uint8_t* __restrict__ wu,
+                                                            const uint16_t* __restrict__ sut,
+                                                            const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                            int cols, int rows, int n, int n_tg,
+                                                            int8_t* __restrict__ oq, float* __restrict__ od) {
+    using R = SwRegs<DT>;
+    constexpr int KC = kSwKC, kBw = R::kBw;
+    constexpr int kArow = KC * kBw + 16;  // LDS row strides in bytes (= 4 dwords mod 64 banks: the 16 rows of an
+    constexpr int kXrow = KC * QK + 16;   // operand read hit distinct banks)
+    constexpr int kAupr = KC * kBw / 16, kXupr = KC * QK / 16;
+    constexpr int kDxRow = KC + 4;        // token scale row stride (floats): 16-byte reads of 16 tokens, no conflict
+    __shared__ __align__(16) uint8_t as[2][64 * kArow];
+    __shared__ __align__(16) int8_t xs[2][16 * kXrow];
+    __shared__ __align__(16) float dws[2][64 * KC];
+    __shared__ __align__(16) float dxs[2][16 * kDxRow];
+    __shared__ float hg[32][17], hu[32][17];
+    __shared__ uint64_t exptab[32];
+    ExpTab et;
+    et.load();
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lq = lane >> 4;
+    // workgroups of one row block (its token groups) are numbered onto one XCD, as in the matmul kernels
+    const int G = (int)gridDim.x, p = (int)blockIdx.x;
+    const int xcd = p % 8, per = G / 8, rem = G % 8;
+    const int logical = xcd * per + min(xcd, rem) + p / 8;
+    const int rb = logical / n_tg, tg = logical % n_tg;
+    const int r0 = rb * 32, tbase = tg * 16;
+    const int nb = cols / QK;
+    const size_t wrow = (size_t)nb * kBw;
+
+    // staged row s (0..63): gate row r0 + s for s < 32, else up row r0 + s - 32; tokens past n are clamped
+    const uint8_t* asrc[R::kAu];
+    int aoff[R::kAu];
+#pragma unroll
+    for (int j = 0; j < R::kAu; ++j) {
+        const int e = j * 256 + tid, r = e / kAupr;
+        asrc[j] = r < 32 ? wg + (size_t)(r0 + r) * wrow : wu + (size_t)(r0 + r - 32) * wrow;
+        aoff[j] = (e % kAupr) * 16;
+    }
+    const int8_t* xsrc[R::kXu];
+    int xoff[R::kXu];
+#pragma unroll
+    for (int j = 0; j < R::kXu; ++j) {
+        const int e = j * 256 + tid;
+        xsrc[j] = xq + (size_t)min(tbase + e / kXupr, n - 1) * cols;
+        xoff[j] = (e % kXupr) * 16;
+    }
+    const uint16_t* wsrc[R::kWu];
+#pragma unroll
+    for (int j = 0; j < R::kWu; ++j) {
+        const int r = (j * 256 + tid) / KC;
+        wsrc[j] = r < 32 ? sgt + (size_t)(r0 + r) * nb : sut + (size_t)(r0 + r - 32) * nb;
+    }
+    const float* dxsrc = xd + (size_t)min(tbase + tid / KC, n - 1) * nb;
+    const int sk = tid % KC;  // the block of this thread's staged scales (256 is a multiple of KC)
+
+    auto load = [&](R& S, int c0) {
+#pragma unroll
+        for (int j = 0; j < R::kAu; ++j)
+            S.a[j] = load16(asrc[j] + min((size_t)c0 * kBw + aoff[j], wrow - 16));
+#pragma unroll
+        for (int j = 0; j < R::kXu; ++j) S.x[j] = load16(xsrc[j] + min(c0 * QK + xoff[j], cols - 16));
+        const int b = min(c0 + sk, nb - 1);
+#pragma unroll
+        for (int j = 0; j < R::kWu; ++j) S.dw[j] = wsrc[j][b];
+        S.dx = dxsrc[b];
+    };
+    auto stage = [&](const R& S, int buf) {
+#pragma unroll
+        for (int j = 0; j < R::kAu; ++j) {
+            const int e = j * 256 + tid;
+            *reinterpret_cast<uint4*>(&as[buf][(e / kAupr) * kArow + (e % kAupr) * 16]) = S.a[j];
+        }
+#pragma unroll
+        for (int j = 0; j < R::kXu; ++j) {
+            const int e = j * 256 + tid;
+            *reinterpret_cast<uint4*>(&xs[buf][(e / kXupr) * kXrow + (e % kXupr) * 16]) = S.x[j];
+        }
+#pragma unroll
+        for (int j = 0; j < R::kWu; ++j) {
+            uint32_t h = S.dw[j];
+            asm volatile("" : "+v"(h));  // keeps the conversion here (hoisted, it would wait for later loads)
+            dws[buf][j * 256 + tid] = f16_to_f32((uint16_t)h);
+        }
+        dxs[buf][(tid / KC) * kDxRow + sk] = S.dx;
+    };
+    // wave w: staged rows 16 w + li (operand) / 16 w + 4 lq + i (results); chains acc[i] of (row 16 w + 4 lq + i,
+    // token li)
+    const int shift = DT == kQ8 ? 0 : (lq >> 1) * 4;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](int buf, int c0) {
+        const int nblk = min(KC, nb - c0);
+        const float4* dw4 = reinterpret_cast<const float4*>(dws[buf]) + (16 * wave + 4 * lq) * (KC / 4);
+        const float4* dx4 = reinterpret_cast<const float4*>(dxs[buf] + li * kDxRow);
+#pragma unroll
+        for (int g4 = 0; g4 < KC / 4; ++g4) {
+            long a[4], x[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int b = 4 * g4 + i;
+                a[i] = *reinterpret_cast<const long*>(
+                    &as[buf][(16 * wave + li) * kArow + b * kBw + (DT == kQ8 ? lq * 8 : (lq & 1) * 8)]);
+                x[i] = *reinterpret_cast<const long*>(&xs[buf][li * kXrow + b * QK + lq * 8]);
+            }
+            float4 dwv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dwv[r] = dw4[r * (KC / 4) + g4];
+            const float4 dxv = dx4[g4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                long ai = a[i];
+                if (DT == kQ4) {
+                    const uint64_t v = (uint64_t)ai;
+                    const uint32_t lo = nibbles_to_i8(((uint32_t)v >> shift) & 0x0F0F0F0Fu);
+                    const uint32_t hi = nibbles_to_i8(((uint32_t)(v >> 32) >> shift) & 0x0F0F0F0Fu);
+                    ai = (long)(((uint64_t)hi << 32) | lo);
+                }
+                const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(ai, x[i], (v4i){0, 0, 0, 0}, 0, 0, 0);
+                const float dx = i == 0 ? dxv.x : i == 1 ? dxv.y : i == 2 ? dxv.z : dxv.w;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float dw = i == 0 ? dwv[r].x : i == 1 ? dwv[r].y : i == 2 ? dwv[r].z : dwv[r].w;
+                    const float nx = __builtin_fmaf((float)c[r] * dw, dx, acc[r]);
+                    acc[r] = 4 * g4 + i < nblk ? nx : acc[r];
+                }
+            }
+        }
+    };
+
+    const int n_chunks = (nb + KC - 1) / KC;
+    if constexpr (SHORT) {
+        R A, B;
+        load(A, 0);
+        load(B, KC);
+        __builtin_amdgcn_sched_barrier(0);
+        stage(A, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        compute(0, 0);
+        stage(B, 1);  // buffer 1 is not read by chunk 0
+        __syncthreads();
+        compute(1, KC);  // a chunk past nb adds nothing
+    } else {
+        // chunk c in buffer c % 2 and register set c % 2, refilled with chunk c + 2 once staged (clamped re-reads
+        // past the last chunk)
+        R S[2];
+        load(S[0], 0);
+        load(S[1], KC);
+        __builtin_amdgcn_sched_barrier(0);
+        stage(S[0], 0);
+        load(S[0], 2 * KC);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        for (int c = 0;; c += 2) {
+            compute(0, c * KC);
+            if (c + 1 >= n_chunks) break;
+            stage(S[1], 1);
+            load(S[1], (c + 3) * KC);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+            compute(1, (c + 1) * KC);
+            if (c + 2 >= n_chunks) break;
+            stage(S[0], 0);
+            load(S[0], (c + 4) * KC);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+        }
+    }
+    (void)n_chunks;
+
+    // h = g / (1 + expf(-g)) * u (ops_ref.cpp:243-248) and its quantization per token: 32 lanes per block
+    {
+        float(*dst)[17] = wave < 2 ? hg : hu;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[16 * (wave & 1) + 4 * lq + r][li] = acc[r];
+    }
+    et.store(exptab);
+    __syncthreads();
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        const int tk = pass * 8 + tid / 32, rr = tid % 32, tok = tbase + tk;
+        if (tok < n) {  // uniform per 32-lane group
+            const float gv = hg[rr][tk], uv = hu[rr][tk];
+            quant_block32(gv / (1.0f + dev_expf(-gv, exptab)) * uv, oq + (size_t)tok * rows + r0,
+                          od + (size_t)tok * (rows / QK) + rb);
+        }
+    }
+}
+
 // q, k and v GEMVs of one token in one launch: three row segments of one dtype and width over one activation,
 // the layer's normed input, which every workgroup builds itself (NormAct).
 struct QkvSegs {
@@ -1983,6 +2197,38 @@ hipError_t decode_layers(Decoder* d, hipStream_t s) {
 }
 
 // Matrices over one activation, in as few launches as their formats allow: runs of one dtype and width share one.
+// Gate / up / SwiGLU / quantization of a prefill chunk as one launch (matmul_swiglu_kernel) into qb / db, or false
+// (the matmul launch and swiglu_quant_kernel instead: one launch per operation, different formats or widths, rows
+// not a multiple of 32, unaligned operands).
+bool swiglu_fused(Decoder* d, const qh_tensor& wg, const qh_tensor& wu, int n, hipStream_t s) {
+    if (!d->fuse || wg.dtype != wu.dtype || wg.rows != wu.rows || wg.cols != wu.cols || wg.rows % QK != 0 ||
+        (wg.dtype != kQ8 && wg.dtype != kQ4) || wg.cols % QK != 0 || wg.cols < 2 * QK)
+        return false;
+    const uint8_t *qg = quants(wg), *qu = quants(wu);
+    if (((reinterpret_cast<uintptr_t>(qg) | reinterpret_cast<uintptr_t>(qu) | reinterpret_cast<uintptr_t>(d->qa)) &
+         15u) != 0)
+        return false;
+    const int n_tg = (n + 15) / 16;
+    const dim3 grid((unsigned)(wg.rows / QK * n_tg));
+    const bool short_rows = wg.cols / QK <= 2 * kSwKC;
+#define QH_SW(DT, SH)                                                                                            \
+    qh_launch((matmul_swiglu_kernel<DT, SH>), grid, dim3(256), 0, s, qg, scales(wg), qu, scales(wu), d->qa, d->da, \
+              wg.cols, wg.rows, n, n_tg, d->qb, d->db)
+    if (wg.dtype == kQ4) {
+        if (short_rows)
+            QH_SW(kQ4, true);
+        else
+            QH_SW(kQ4, false);
+    } else {
+        if (short_rows)
+            QH_SW(kQ8, true);
+        else
+            QH_SW(kQ8, false);
+    }
+#undef QH_SW
+    return true;
+}
+
 hipError_t matmul_group(const MmOut* m, int k, const int8_t* xq, const float* xd, int n, hipStream_t s) {
     for (int i = 0; i < k;) {
         int j = i + 1;
@@ -2019,11 +2265,13 @@ hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
         });
         QH_TRY(hipGetLastError());
         const qh_tensor &wg = lt(d, l, L_WG), &wu = lt(d, l, L_WU), &wd = lt(d, l, L_WD);
-        const MmOut gu[2] = {{&wg, d->g, wg.rows, 0, wg.rows}, {&wu, d->u, wu.rows, 0, wu.rows}};
-        QH_TRY(matmul_group(gu, 2, d->qa, d->da, n, s));
-        const long nblk = (long)n * F / QK;
-        qh_launch(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g,
-                           d->u, nblk, d->qb, d->db);
+        if (!swiglu_fused(d, wg, wu, n, s)) {
+            const MmOut gu[2] = {{&wg, d->g, wg.rows, 0, wg.rows}, {&wu, d->u, wu.rows, 0, wu.rows}};
+            QH_TRY(matmul_group(gu, 2, d->qa, d->da, n, s));
+            const long nblk = (long)n * F / QK;
+            qh_launch(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g,
+                               d->u, nblk, d->qb, d->db);
+        }
         QH_TRY(hipGetLastError());
         QH_TRY(launch_matmul(d->o, wd.rows, wd, d->qb, d->db, n, 0, wd.rows, s));
     }

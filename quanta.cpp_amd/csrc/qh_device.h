@@ -191,6 +191,12 @@ __device__ __forceinline__ int dot_q4_block(const uint4 w, const uint4 xlo, cons
 
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// Accumulator of one 16x16x32 int8 MFMA.
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Nibbles (0..15 per byte) -> signed bytes (nibble - 8), no borrow between bytes.
+__device__ __forceinline__ uint32_t nibbles_to_i8(uint32_t v) { return ((v | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
+
 // Pipelined chain rows (chain_lds_pipe): a row of nb operands is stored as chain_len32(nb) - nb zeros followed by
 // the nb operands, rows chain_stride32(nb) floats apart (16-byte aligned, 4 mod 32 floats, so 16-byte reads of
 // neighbouring rows fall in different banks), and kChainPipePad readable floats follow the last row.

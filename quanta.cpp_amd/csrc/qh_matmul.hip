@@ -27,15 +27,10 @@
 
 namespace qh {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-
 namespace {
 
 constexpr int kMmThreads = 256;  // 4 waves
 constexpr int kXcds = 8;
-
-// Nibbles (0..15 per byte) -> signed bytes (nibble - 8), no borrow between bytes.
-__device__ __forceinline__ uint32_t nibbles_to_i8(uint32_t v) { return ((v | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
 
 template <int TT, int KC>
 struct MmShape {

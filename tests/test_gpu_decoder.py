@@ -92,6 +92,20 @@ def test_decoder_head_dim_128_equals_oracle(qh, oracle, gpu):
     _steps_vs_oracle(oracle, orc, dec, ids, 6, full_every=3)
 
 
+@pytest.mark.parametrize("dim,ffn", [(1280, 1024), (2560, 512)])
+def test_decoder_wide_rows_equal_oracle(qh, oracle, gpu, dim, ffn):
+    """Rows of more than two 16-block chunks: the prefill's fused gate / up / SwiGLU launch in its chunk loop (40 and
+    80 blocks a row), the staged matmul's longer rows and the decode GEMVs at those widths; 45 prompt tokens end in a
+    partial token tile."""
+    qnt = qnt_module()
+    hp = _narrow_hp(qnt, dim=dim, n_heads=dim // 64, n_kv_heads=dim // 320, ffn_dim=ffn, n_layers=1)
+    tens = qnt.synthetic_q4mix(33, hp)
+    orc = oracle_decoder(oracle, hp, tens, ctx_len=128)
+    dec = qh.Decoder(hp, tens, ctx_len=128)
+    ids = np.random.default_rng(9).integers(0, hp.vocab_size, 45).astype(np.int32)
+    _steps_vs_oracle(oracle, orc, dec, ids, 3, full_every=2)
+
+
 def test_decoder_context_beyond_one_v_stage(qh, oracle, gpu):
     # head_dim 64 stages 768 V rows in LDS at a time: a 1000-token prompt puts prefill chunks and decode steps past it
     qnt = qnt_module()
