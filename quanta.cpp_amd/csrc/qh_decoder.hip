@@ -773,7 +773,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv,
     const float* __restrict__ cs, const int* __restrict__ pos_dev, int ctx, int n_heads, int n_kv,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int8_t* __restrict__ oq, float* __restrict__ od,
-    float* __restrict__ escr, int escr_stride, int* __restrict__ status) {
+    int* __restrict__ status) {
     constexpr int HALF = HD / 2, CPR = HD / 8;           // 16-byte chunks per f16 K row
     constexpr int kVRows = (WPE == 1 ? kVStageBytes : 32 * 1024) / (HD * 2);  // V rows one LDS stage holds (mult. of 8)
     constexpr int kVBlk = kVRows / 8;                    // 8-row blocks per stage
@@ -1914,7 +1914,7 @@ struct Decoder {
     // int8 activations: qa holds a layer's normed input (and the head's), qb the attention / MLP inner activation
     int8_t *qa = nullptr, *qb = nullptr;
     float *da = nullptr, *db = nullptr;
-    float* escr = nullptr;      // attention: rows of exp values, then of weights, per (token, head) workgroup
+    float* escr = nullptr;      // decode attention: a row of exp values, then one of weights, per head
     int escr_stride = 0;
     int32_t* tokens = nullptr;  // [kChunk] prefill input / [0] decode input
     // token history (prompt ids since position 0, then each chosen id) and the optional query / sampler settings
@@ -2151,11 +2151,11 @@ hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
     else if (hp.head_dim == 64)
         qh_launch((attention_kernel<64, 2>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                            bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
-                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status);
+                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status);
     else
         qh_launch((attention_kernel<128>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                            bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
-                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status);
+                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status);
     return hipGetLastError();
 }
 
@@ -2362,7 +2362,7 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
     A((void**)&d->da, sizeof(float) * kChunk * (wide / QK));
     A((void**)&d->db, sizeof(float) * kChunk * (wide / QK));
     d->escr_stride = escr_stride(hp->ctx_len);
-    A((void**)&d->escr, sizeof(float) * 2 * (size_t)kChunk * hp->n_heads * d->escr_stride);  // exp rows, weight rows
+    A((void**)&d->escr, sizeof(float) * 2 * (size_t)hp->n_heads * d->escr_stride);  // exp rows, weight rows
     A((void**)&d->tokens, sizeof(int32_t) * kChunk);
     A((void**)&d->hist, sizeof(int32_t) * ((size_t)hp->ctx_len + 1));
     A((void**)&d->hist_len, 256);
