@@ -1073,17 +1073,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
             const int n = se - s0;
             uint4 vA[4], vB[4];
             float4 wA[8], wB[8];
+            // sched_barrier keeps each batch's reads ahead of the chain steps they overlap (the scheduler would sink
+            // them next to their first use)
             ldv(vA, wA, 0);
             int jr = 0;
 #pragma unroll 1
             for (; jr + 64 <= n; jr += 64) {
                 ldv(vB, wB, jr + 32);
+                __builtin_amdgcn_sched_barrier(0);
                 use(vA, wA, 32);
                 ldv(vA, wA, jr + 64);
+                __builtin_amdgcn_sched_barrier(0);
                 use(vB, wB, 32);
             }
             if (jr + 32 <= n) {
                 ldv(vB, wB, jr + 32);
+                __builtin_amdgcn_sched_barrier(0);
                 use(vA, wA, 32);
                 use(vB, wB, n - jr - 32);
             } else {
