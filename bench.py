@@ -302,6 +302,16 @@ def e2e_model():
 SAMPLED_SEED = 0x51A7C0DE
 
 
+def state_digest(hidden, hq, hd):
+    """The end-to-end golden's per-forward fingerprint (tests/golden/make_e2e_golden.py): 8 bytes of the sha256 of the
+    final normed hidden state, then 8 of the sha256 of its int8 quantization and block scales, as two uint64."""
+    import hashlib
+    h1 = hashlib.sha256(np.ascontiguousarray(hidden, np.float32).tobytes()).digest()[:8]
+    h2 = hashlib.sha256(np.ascontiguousarray(hq, np.int8).tobytes() +
+                        np.ascontiguousarray(hd, np.float32).tobytes()).digest()[:8]
+    return np.frombuffer(h1 + h2, np.uint64)
+
+
 def e2e_bench(qh, torch, hp, tens, steps=256, warmup=3, n_prompt=512, check=True, mode="greedy"):
     """End-to-end generation on the q4mix Qwen2.5-0.5B-shaped model (configuration 5): a 512-token prompt in
     32-token prefill chunks, then `steps` decode steps, each one replay of a HIP graph holding one captured decode step
@@ -351,11 +361,15 @@ def e2e_bench(qh, torch, hp, tens, steps=256, warmup=3, n_prompt=512, check=True
     decode_s = e2.elapsed_time(e3) / 1e3
     out = dec.outputs(cap)
     status = dec.status()
+    # the state after the last timed forward: a digest of the final normed hidden state and its quantization, and the
+    # exact logit of the chosen id (a decoder that lands on the same tokens with other states differs here)
+    digest = state_digest(dec.hidden(), *dec.hq())
+    top_logit = np.float32(dec.stats()["top1_logit"])
     dec.close()
     del graph
     if status:
         raise SystemExit(f"bench: decoder status {status}")
-    parity = None
+    parity = state_parity = None
     gpath = os.path.join(ROOT, "tests", "golden", "e2e_sampled.npz" if chat else "e2e_q4mix.npz")
     r = {}
     if check and n_prompt == 512 and os.path.exists(gpath):
@@ -365,6 +379,14 @@ def e2e_bench(qh, torch, hp, tens, steps=256, warmup=3, n_prompt=512, check=True
         parity = bool((out[:n] == want[:n]).all())
         if not parity:
             raise SystemExit(f"bench: GPU token stream ({mode}) differs from the reference engine's")
+        if not chat:
+            # state_digests[s] follows forward s (0 = the prefill), top_logit[s] is forward s's chosen logit
+            state_parity = bool((digest == g["state_digests"][steps]).all())
+            if steps < len(g["top_logit"]):
+                state_parity &= bool(top_logit.view(np.uint32) == g["top_logit"][steps].view(np.uint32))
+            if not state_parity:
+                raise SystemExit(f"bench: GPU decoder state after {steps} steps differs from the reference engine's")
+            r["state_equals_reference"] = state_parity
         if chat:  # the GPU head reads the same rows each step (the sampling tests check every step)
             r = {"head_rows_mean": float(np.mean(g["chat_rows"][:n])),
                  "head_rows_fraction": float(np.mean(g["chat_rows"][:n])) / hp.vocab_size}
@@ -626,6 +648,7 @@ def main():
                                f"then {args.steps} decode steps, one graph-replayed step per token",
                    "prefill_tok_per_s": round(e["prefill_tok_per_s"], 1),
                    "stream_equals_reference": e["stream_equals_reference"],
+                   "state_equals_reference": e.get("state_equals_reference"),
                    "head": "Exact Shortlist Head, top_k 1"},
     }
     log("roofline: Q4_0 GEMV at the MLP shapes, cold HBM")
@@ -644,7 +667,8 @@ def main():
         e256 = e2e_bench(qh, torch, hp, tens, steps=256, warmup=args.warmup)
         extra["decode_256_steps"] = {"decode_tok_per_s": round(e256["decode_tok_per_s"], 2),
                                      "decode_ms_per_token": round(e256["decode_ms_per_token"], 4),
-                                     "stream_equals_reference": e256["stream_equals_reference"]}
+                                     "stream_equals_reference": e256["stream_equals_reference"],
+                                     "state_equals_reference": e256.get("state_equals_reference")}
     log("decode stages: one traced step per replay")
     st = decode_stages(qh, torch, hp, tens)
     if st is not None:

@@ -181,7 +181,9 @@ int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_t
  * when qh_shortlist_workspace_bytes(V, D, top_k) exceeds QH_NOALLOC_SCRATCH_BYTES. Every call on one GPU works in that
  * GPU's one array, which keeps the last call's contents (the kernels reset what they read, so nothing of one call
  * reaches the next): calls in order on one stream are fine, calls that overlap on one GPU (two streams, or two host
- * threads without an order between them) race and give wrong results.
+ * threads without an order between them) race and give wrong results. The first call on a device runs qh_init for it
+ * (device checks and the scratch array's address); under HIP graph capture, call qh_init for the device (or this entry
+ * point once, eagerly) before the capture begins, so that the captured call only launches kernels.
  * No counterpart in the reference (its Model allocates the head's state on the host at load): for callers that cannot
  * allocate device memory, such as code under HIP graph capture, tight serving loops and harnesses that forbid
  * hipMalloc. */
@@ -303,7 +305,10 @@ enum {
 
 /* One qh_decoder_step with every kernel it launches timed on the device by the dispatch's own start and stop
  * timestamps (no extra packets between the kernels): for the i-th kernel, us_host[i] microseconds and stage_host[i]
- * its stage id; *n_host = the number of kernels (QH_ERR_NOMEM if more than cap). Host arrays; synchronises the stream.
+ * its stage id; *n_host = the number of kernels. Host arrays; synchronises the stream. When the step launches more
+ * than cap kernels the result is QH_ERR_NOMEM with *n_host set to the number it launched (the capacity it needs) and
+ * us_host / stage_host unset; the step itself has run all the same (the decoder has advanced one token), so a caller
+ * that retries with a larger cap takes the next step.
  * No counterpart in the reference (its CLI times whole tokens); for profiling. */
 int qh_decoder_step_timed(qh_decoder* d, int top_k, void* stream, float* us_host, int32_t* stage_host, int cap,
                           int32_t* n_host);

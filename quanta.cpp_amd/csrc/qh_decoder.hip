@@ -2490,7 +2490,9 @@ int decoder_step_timed(Decoder* d, int top_k, hipStream_t s, float* us, int32_t*
         rc = check_hip(e, "qh_decoder_step_timed");
     }
     if (!rc) rc = check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
-    if (!rc && t.n >= cap) rc = fail(QH_ERR_NOMEM, "qh_decoder_step_timed: the step launches more than %d kernels", cap - 1);
+    if (!rc && t.launched > cap)
+        rc = fail(QH_ERR_NOMEM, "qh_decoder_step_timed: the step launched %d kernels, more than the %d timing slots (the "
+                  "step has run)", t.launched, cap);
     for (int i = 0; !rc && i < t.n; ++i) {
         rc = check_hip(hipEventElapsedTime(&us[i], t.ev[2 * i], t.ev[2 * i + 1]), "hipEventElapsedTime");
         us[i] *= 1e3f;
@@ -2498,7 +2500,7 @@ int decoder_step_timed(Decoder* d, int top_k, hipStream_t s, float* us, int32_t*
     }
     for (hipEvent_t e : t.ev)
         if (e) (void)hipEventDestroy(e);
-    if (!rc) *n = t.n;
+    if (!rc || t.launched > cap) *n = t.launched;
     return rc;
 }
 

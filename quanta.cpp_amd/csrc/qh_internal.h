@@ -19,7 +19,8 @@ namespace qh {
 struct KernelTimer {
     std::vector<hipEvent_t> ev;  // [2 * cap]: start, stop of kernel i
     std::vector<int> stage;      // per timed kernel; -1 until its stage is marked
-    int n = 0;
+    int n = 0;                   // kernels timed
+    int launched = 0;            // kernels launched while the timer was set (timed or not)
     bool full() const { return 2 * (size_t)n + 1 >= ev.size(); }
     void mark(int id) {  // the kernels launched since the previous mark belong to stage id
         for (int i = n - 1; i >= 0 && stage[i] < 0; --i) stage[i] = id;
@@ -31,6 +32,7 @@ KernelTimer*& kernel_timer();
 template <typename... P, typename... A>
 inline void qh_launch(void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipStream_t s, A&&... args) {
     KernelTimer* t = kernel_timer();
+    if (t) ++t->launched;
     if (t && !t->full()) {
         const hipEvent_t a = t->ev[2 * t->n], b = t->ev[2 * t->n + 1];
         t->stage.push_back(-1);

@@ -120,6 +120,22 @@ def test_noalloc_entry_point_host_checks(qh):
     assert b"null argument" in L.qh_last_error()
 
 
+def test_noalloc_refuses_oversized_head(qh):
+    """A head whose workspace exceeds the scratch array: QH_ERR_NOMEM from the size check, which runs before the
+    library touches a device (the descriptors point at no memory, so nothing may be launched)."""
+    L = qh.lib()
+    V, D = 1_000_000, 896  # supported (at most 1,048,576 rows), with a workspace beyond the scratch array
+    assert L.qh_shortlist_workspace_bytes(V, D, 1) > qh.NOALLOC_SCRATCH_BYTES
+    h8 = qh.qh_tensor(qh.Q8_0, V, D, 4096)
+    h4 = qh.qh_tensor(qh.Q4_0, V, D, 8192)
+    he = qh.qh_tensor(qh.F16, V, D // 32, 16384)
+    out = qh.qh_head_out(16, 16, 16, 16, 16)
+    q = qh.qh_head_query(1, 0, None, 0)
+    rc = L.qh_shortlist_head_noalloc(C.byref(h8), C.byref(h4), C.byref(he), C.c_void_p(16), C.c_void_p(16),
+                                     C.byref(q), C.byref(out), None)
+    assert rc == qh.ERR_NOMEM and b"scratch array" in L.qh_last_error()
+
+
 def test_forced_allocation_failure(qh):
     """qh_fault_alloc: the armed allocation fails with QH_ERR_NOMEM before any HIP call (so on a machine without a
     GPU too), the out pointer is cleared, and the hook disarms itself after firing."""

@@ -117,6 +117,20 @@ def test_decoder_context_beyond_one_v_stage(qh, oracle, gpu):
     _steps_vs_oracle(oracle, orc, dec, ids, 6)
 
 
+@pytest.mark.parametrize("n_prompt,n_steps", [(1020, 580), (2290, 30)])
+def test_decoder_decode_past_1024_positions(qh, oracle, gpu, n_prompt, n_steps):
+    """Decode steps across positions 1024, 1536, 2048 and 2304: the decode attention scores positions beyond its
+    1024 threads in a loop (the token's own row by thread pos % 1024 there), and the V rows pass through three and
+    four LDS stages of 768. Every step's hidden state and logits equal the oracle's bit for bit."""
+    qnt = qnt_module()
+    hp = _narrow_hp(qnt)
+    tens = qnt.synthetic_q4mix(39, hp)
+    orc = oracle_decoder(oracle, hp, tens, ctx_len=2400)
+    dec = qh.Decoder(hp, tens, ctx_len=2400)
+    ids = np.random.default_rng(15).integers(0, hp.vocab_size, n_prompt).astype(np.int32)
+    _steps_vs_oracle(oracle, orc, dec, ids, n_steps)
+
+
 def test_decoder_fused_equals_one_launch_per_op(qh, oracle, gpu, monkeypatch):
     qnt = qnt_module()
     hp = qnt.HParams(vocab_size=4096, n_layers=2)
@@ -325,3 +339,51 @@ def test_decoder_second_turn_prefill(qh, oracle, gpu, n_steps):
         full = dec.logits()
         rows = np.isfinite(want)
         assert (bits(full[rows]) == bits(want[rows])).all()
+
+
+def test_decoder_step_timed_equals_step(qh, gpu):
+    """qh_decoder_step_timed runs the same step as qh_decoder_step: the same token, hidden state and logits, with one
+    device time and a valid stage id per kernel (five per layer, the final norm, the head's two); with too few timing
+    slots it reports QH_ERR_NOMEM and the count it needs, and the step has still run."""
+    import ctypes as C
+    import torch
+    qnt = qnt_module()
+    g = _golden("e2e_small.npz")
+    hp = qnt.HParams(vocab_size=int(g["vocab"]), n_layers=int(g["n_layers"]))
+    dec = qh.Decoder(hp, qnt.synthetic_q4mix(int(g["seed"]), hp), ctx_len=256)
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    L = qh.lib()
+
+    def timed(cap):
+        us = np.zeros(max(cap, 1), np.float32)
+        stage = np.full(max(cap, 1), -7, np.int32)
+        n = C.c_int32(-1)
+        rc = L.qh_decoder_step_timed(dec.h, 1, stream, us.ctypes.data, stage.ctypes.data, cap, C.byref(n))
+        return rc, n.value, us, stage
+
+    def run(mode):
+        dec.prefill(g["prompt"], 0, top_k=1)
+        dec.begin(4)
+        if mode == "plain":
+            dec.step(top_k=1)
+            dec.step(top_k=1)
+            return None
+        rc, n, us, stage = timed(64)
+        assert rc == 0, L.qh_last_error().decode()
+        rc2, n2, _, _ = timed(3)  # too few slots: refused after the step ran
+        assert rc2 == qh.ERR_NOMEM and b"the step has run" in L.qh_last_error()
+        assert n2 == n
+        return n, us, stage
+
+    run("plain")
+    want = (dec.outputs(3).tolist(), bits(dec.hidden()), bits(dec.logits()), dec.position())
+    n, us, stage = run("timed")
+    got = (dec.outputs(3).tolist(), bits(dec.hidden()), bits(dec.logits()), dec.position())
+    assert got[0] == want[0] and (got[1] == want[1]).all() and (got[2] == want[2]).all() and got[3] == want[3]
+    assert n == 5 * hp.n_layers + 3
+    ids = stage[:n].tolist()
+    per_layer = [s for s in ids if s < qh.STAGE_FINAL_NORM]
+    assert per_layer == [l * qh.STAGES_PER_LAYER + k for l in range(hp.n_layers) for k in range(5)]
+    assert ids[5 * hp.n_layers:] == [qh.STAGE_FINAL_NORM, qh.STAGE_HEAD, qh.STAGE_HEAD]
+    assert (us[:n] > 0).all() and (us[:n] < 1e5).all()
+    assert dec.status() == 0

@@ -157,6 +157,55 @@ def _cluster_head(synth, V, D, seed, r0, n, x):
     return head8, head4, err
 
 
+def _decoy_head(synth, V, D, seed, x, n_decoy, factor):
+    """A random Q8_0 head with its 4-bit copy, where n_decoy rows that score well below the best (ranks 40 on under the
+    exact head for the hidden state x, dequantized) get 4-bit scales `factor` times too large, their error bounds
+    recomputed from the real difference (rounded up to f16, as synth.shortlist_copy does). Their coarse scores then
+    lead, so they are the seeds, and their exact logits (the k-th best of which is tau) sit far below their coarse
+    scores: the rows with tau <= upper bound < the select kernel's speculative cut need the second rescoring pass."""
+    head8 = synth.q8_tensor(seed, V, D)
+    head4, err = synth.shortlist_copy(head8, V, D)
+    w = synth.dequant_q8(head8, V, D)
+    decoys = np.argsort(-(w @ x))[40:40 + n_decoy]
+    nb = D // 32
+    s4 = head4[V * D // 2:].view(np.float16).reshape(V, nb)
+    nib = head4[:V * D // 2].reshape(V, nb, 16)
+    codes = np.concatenate([nib & 15, nib >> 4], axis=2).astype(np.float64) - 8.0  # [V][block][32], element order
+    for r in decoys:
+        s4[r] = (s4[r].astype(np.float32) * factor).astype(np.float16)
+        diff = codes[r] * s4[r].astype(np.float64)[:, None] - w[r].reshape(nb, 32).astype(np.float64)
+        e = np.sqrt((diff * diff).sum(axis=1))
+        e16 = e.astype(np.float16)
+        low = e16.astype(np.float64) < e
+        e16[low] = np.nextafter(e16[low], np.float16(np.inf))
+        err[r] = e16
+    return head8, head4, err, decoys
+
+
+@pytest.mark.parametrize("top_k", [1, 20])
+def test_shortlist_second_rescoring_pass(qh, oracle, synth, gpu, top_k):
+    """tau below the speculative cut (the seeds' 4-bit copies overstate them): the rows with tau <= upper < cut, which
+    the first pass leaves out, are rescored in the second, and every output equals the oracle's bit for bit."""
+    V, D = 6007, 896
+    x = synth.activations(43, 1, D, scale=0.5)
+    xq, xd = oracle.quantize_q8(x)
+    xf = (xq[0].reshape(-1, 32).astype(np.float32) * xd[0][:, None]).reshape(-1)
+    head8, head4, err, decoys = _decoy_head(synth, V, D, 41, xf, top_k + 12, 2.0)
+    o = oracle.shortlist_head(head8, head4, err, V, D, xq[0], xd[0], top_k=top_k)
+    # the case on the CPU: every seed a decoy, tau below the cut, rows between them
+    ck = np.sort(o["coarse"])[::-1][top_k - 1]
+    cut = np.float32(ck - (np.float32(abs(ck)) * np.float32(0.0625) + np.float32(1e-3)))
+    tau = np.float32(o["tau"])
+    assert np.isin(o["rows"][:o["n_seeds"]], decoys).all()
+    assert tau < cut and ((o["upper"] >= tau) & (o["upper"] < cut)).sum() > 100
+    dev = (qh.DeviceTensor.upload(head8, 2, V, D), qh.DeviceTensor.upload(head4, 3, V, D),
+           qh.DeviceTensor.upload(err.view(np.uint8), 1, V, D // 32))
+    sl = qh.ShortlistHead(*dev, top_k=top_k)
+    xq_d, xd_d = qh.quantize_q8(_dev(x, gpu))
+    st, _ = _check_head(qh, oracle, (head8, head4, err), sl, xq_d[0], xd_d[0], V, D, top_k)
+    assert st["n_rows"] == o["n_rows"] > 500
+
+
 @pytest.mark.parametrize("top_k,r0,n", [(1, 70001, 300), (20, 5, 700), (55, 40000, 9600)])
 def test_shortlist_crowded_shares(qh, oracle, synth, gpu, top_k, r0, n):
     """The best keys crowd a few screen shares: each share publishes only its best four keys, so shares holding more

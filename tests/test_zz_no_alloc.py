@@ -1,7 +1,8 @@
 """qh_shortlist_head_noalloc (the shortlist head working in the library's own scratch array, no allocation) against
 qh_shortlist_head with a caller workspace, through the C-ABI: two calls in a row, the second on a smaller head with
-top-k 20 and must ids; every output bit-identical (logits, coarse scores, upper bounds, row list, stats). Also the
-size limit: a head whose workspace exceeds the scratch array is refused before anything is launched."""
+top-k 20 and must ids; every output bit-identical (logits, coarse scores, upper bounds, row list, stats). The size
+limit (a head whose workspace exceeds the scratch array is refused before anything is launched) is checked on the host
+in test_cpu_abi.py, with no device buffers behind the descriptors."""
 import ctypes as C
 
 import numpy as np
@@ -85,23 +86,42 @@ def test_noalloc_equals_workspace_entry(qh, synth, gpu):
         assert 0 < qh_stats(got["stats"])["n_rows"] < V
 
 
-def test_noalloc_refuses_oversized_head(qh, synth, gpu):
-    """A head whose workspace exceeds the scratch array: QH_ERR_NOMEM, and no kernel is launched (the descriptors
-    claim more rows than their buffers hold, which only the size check may see)."""
-    V, D = 6007, 896
-    heads = _upload(qh, synth, V, D, 3)
-    big = 1_000_000  # supported (at most 1,048,576 rows), with a workspace beyond the scratch array
-    assert qh.lib().qh_shortlist_workspace_bytes(big, D, 1) > qh.NOALLOC_SCRATCH_BYTES
-    views = []
-    for t, rows, cols in ((heads[0], big, D), (heads[1], big, D), (heads[2], big, D // 32)):
-        views.append(qh.qh_tensor(t.view.dtype, rows, cols, t.view.data))
-    xq, xd = qh.quantize_q8(torch.zeros(1, D, device=gpu))
-    dummy = torch.empty(16, dtype=torch.float32, device=gpu)
-    q = qh.qh_head_query(1, 0, None, 0)
-    out = qh.qh_head_out(*(dummy.data_ptr(),) * 5)
+def test_noalloc_under_graph_capture(qh, synth, gpu):
+    """qh_shortlist_head_noalloc captured in a HIP graph (after the device's first call, which runs qh_init outside
+    the capture) and replayed on two different hidden states: each replay equals an eager call on the same input,
+    with the program's own eager work between the replays."""
+    V, D = 20011, 896
+    heads = _upload(qh, synth, V, D, 71)
+    h8, h4, he = heads
+    xs = torch.from_numpy(synth.activations(72, 3, D, scale=0.5)).to(gpu)
+    xq_all, xd_all = qh.quantize_q8(xs)
+    xq = xq_all[0].clone()
+    xd = xd_all[0].clone()
+    must = torch.tensor([7, 19999, 7, 123], dtype=torch.int32, device=gpu)
+    _call(qh, heads, xq, xd, 20, must, None)  # first call on the device: qh_init, outside the capture
+    o = _outputs(V, int(must.numel()), gpu)
+    q = qh.qh_head_query(20, 0, must.data_ptr(), int(must.numel()))
+    out = qh.qh_head_out(*(o[k].data_ptr() for k in ("logits", "coarse", "upper", "rows", "stats")))
     L = qh.lib()
-    rc = L.qh_shortlist_head_noalloc(C.byref(views[0]), C.byref(views[1]), C.byref(views[2]),
-                                     C.c_void_p(xq.data_ptr()), C.c_void_p(xd.data_ptr()), C.byref(q), C.byref(out),
-                                     C.c_void_p(torch.cuda.current_stream().cuda_stream))
-    assert rc == qh.ERR_NOMEM and b"scratch array" in L.qh_last_error()
-    torch.cuda.synchronize()
+    args = (C.byref(h8.view), C.byref(h4.view), C.byref(he.view), C.c_void_p(xq.data_ptr()), C.c_void_p(xd.data_ptr()),
+            C.byref(q), C.byref(out))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rc = L.qh_shortlist_head_noalloc(*args, C.c_void_p(side.cuda_stream))
+    torch.cuda.current_stream().wait_stream(side)
+    assert rc == 0, L.qh_last_error().decode()
+    for r in (1, 2):
+        print(f"noalloc graph replay {r}", flush=True)
+        xq.copy_(xq_all[r])
+        xd.copy_(xd_all[r])
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = {k: v.cpu().numpy() for k, v in o.items()}
+        want = _call(qh, heads, xq_all[r], xd_all[r], 20, must, None)
+        _same(got, want)
+        assert 0 < qh_stats(got["stats"])["n_rows"] < V
+    del graph
