@@ -461,6 +461,244 @@ __global__ __launch_bounds__(NS == 0 ? kMmThreads : 2 * kMmThreads) void matmul_
     if (tok < n && r < r1) sg.out[(size_t)tok * sg.ldo + r] = acc;
 }
 
+// Tile variant for batches of 64 tokens and more: a workgroup of 4 waves owns 64 rows x 64 tokens over all of K, in
+// chunks of 8 blocks brought into LDS by coalesced 16-byte loads (a row's chunk is 128 (Q4_0) or 256 (Q8_0) contiguous
+// bytes, a token's 256; 16 rows x 2 lane groups of a half-wave operand read hit 64 distinct banks), double-buffered:
+// the loads of chunk c + 1 are in flight while chunk c is multiplied. Wave (wr, wt) multiplies rows 32 wr .. + 31 by
+// tokens 32 wt .. + 31: per block four MFMAs (2 row tiles x 2 token tiles), each weight operand read once for two
+// token tiles and each activation operand once for two row tiles, and the wave runs the 16 chains of its lanes'
+// outputs in registers (lane l: rows 4 (l / 16) + i of each row tile, token l % 16 of each token tile), so no block
+// sum goes through LDS. Operand loads in MFMA layout (8 bytes per lane from 16 rows) kept the texture-address units
+// busy for most of the register kernel's time at 512 tokens.
+// Timeline stamps of workgroup 0, wave 0 (compiled in only with -DQH_TIMELINE; qh_timeline_mm_read copies them out).
+#if defined(QH_TIMELINE)
+__device__ uint64_t qh_tl_mm[64];
+#define QH_MMSTAMP(i)                                                                                     \
+    do {                                                                                                  \
+        if (blockIdx.x == 0 && threadIdx.x == 0 && (i) < 64) qh_tl_mm[i] = __builtin_readcyclecounter(); \
+    } while (0)
+#else
+#define QH_MMSTAMP(i) \
+    do {              \
+    } while (0)
+#endif
+template <int DT, int KC>
+struct TileRegs {
+    static constexpr int kBw = DT == kQ8 ? QK : QK / 2;           // weight bytes per block
+    static constexpr int kAu = 64 * KC * kBw / 16 / kMmThreads;  // 16-byte weight units per thread
+    static constexpr int kXu = 64 * KC * QK / 16 / kMmThreads;   // 16-byte activation units per thread
+    static constexpr int kSp = KC / 4;                           // scales per thread and chunk
+    uint4 a[kAu];
+    uint4 x[kXu];
+    uint16_t dw[kSp];  // row tid / 4, blocks kSp (tid % 4) + j of the chunk
+    float dx[kSp];     // token tid / 4, blocks kSp (tid % 4) + j of the chunk
+};
+
+template <int DT, int KC>
+__global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, const int8_t* __restrict__ xq,
+                                                                const float* __restrict__ xd, int cols, int n,
+                                                                int n_tg) {
+    using R = TileRegs<DT, KC>;
+    constexpr int kBw = R::kBw, kSp = R::kSp;
+    constexpr int kArow = KC * kBw + 16, kXrow = KC * QK + 16;  // LDS row strides (bytes)
+    constexpr int kAupr = KC * kBw / 16, kXupr = KC * QK / 16;  // 16-byte units per row and chunk
+    __shared__ __align__(16) uint8_t as[2][64 * kArow];
+    __shared__ __align__(16) int8_t xs[2][64 * kXrow];
+    __shared__ __align__(16) float dws[2][KC][64];  // [block][row], f32
+    __shared__ __align__(16) float dxs[2][KC][64];  // [block][token]
+    const int nb = cols / QK;
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lq = lane >> 4;
+    const int wr = wave >> 1, wt = wave & 1;
+
+    // XCD-aware numbering as in the other variants; segment tiles count 64-row tiles here
+    const int G = (int)gridDim.x, p = (int)blockIdx.x;
+    const int xcd = p % kXcds, per = G / kXcds, rem = G % kXcds;
+    const int logical = xcd * per + min(xcd, rem) + p / kXcds;
+    int rt = logical / n_tg;
+    const int tg = logical % n_tg;
+    const MmSeg sg(segs, rt);
+    const int r1 = sg.r1;
+    const int rbase = sg.r0 + rt * 64, tbase = tg * 64;
+    const size_t wrow_bytes = (size_t)nb * kBw;
+
+    // Source rows of this thread's staged units; rows and tokens past the end are clamped (loaded, never stored), and
+    // byte offsets past the end of a row onto its last unit (blocks no chain adds).
+    const uint8_t* asrc[R::kAu];
+    int aoff[R::kAu];
+#pragma unroll
+    for (int j = 0; j < R::kAu; ++j) {
+        const int e = j * kMmThreads + tid;
+        asrc[j] = sg.wq + (size_t)min(rbase + e / kAupr, r1 - 1) * wrow_bytes;
+        aoff[j] = (e % kAupr) * 16;
+    }
+    const int8_t* xsrc[R::kXu];
+    int xoff[R::kXu];
+#pragma unroll
+    for (int j = 0; j < R::kXu; ++j) {
+        const int e = j * kMmThreads + tid;
+        xsrc[j] = xq + (size_t)min(tbase + e / kXupr, n - 1) * cols;
+        xoff[j] = (e % kXupr) * 16;
+    }
+    const uint16_t* dwsrc = sg.ws + (size_t)min(rbase + tid / 4, r1 - 1) * nb;
+    const float* dxsrc = xd + (size_t)min(tbase + tid / 4, n - 1) * nb;
+    const int sk = kSp * (tid % 4);
+
+    auto load = [&](R& S, int c0) {
+#pragma unroll
+        for (int j = 0; j < R::kAu; ++j)
+            S.a[j] = load16(asrc[j] + min((size_t)c0 * kBw + aoff[j], wrow_bytes - 16));
+#pragma unroll
+        for (int j = 0; j < R::kXu; ++j)
+            S.x[j] = load16(xsrc[j] + min(c0 * QK + xoff[j], cols - 16));
+#pragma unroll
+        for (int j = 0; j < kSp; ++j) {
+            const int b = min(c0 + sk + j, nb - 1);
+            S.dw[j] = dwsrc[b];
+            S.dx[j] = dxsrc[b];
+        }
+    };
+    auto stage = [&](const R& S, int buf) {
+#pragma unroll
+        for (int j = 0; j < R::kAu; ++j) {
+            const int e = j * kMmThreads + tid;
+            *reinterpret_cast<uint4*>(&as[buf][(e / kAupr) * kArow + (e % kAupr) * 16]) = S.a[j];
+        }
+#pragma unroll
+        for (int j = 0; j < R::kXu; ++j) {
+            const int e = j * kMmThreads + tid;
+            *reinterpret_cast<uint4*>(&xs[buf][(e / kXupr) * kXrow + (e % kXupr) * 16]) = S.x[j];
+        }
+        const int t = tid / 4;
+#pragma unroll
+        for (int j = 0; j < kSp; ++j) {
+            uint32_t h = S.dw[j];
+            asm volatile("" : "+v"(h));  // keeps the conversion here (hoisted, it would wait for the next loads)
+            dws[buf][sk + j][t] = f16_to_f32((uint16_t)h);
+            dxs[buf][sk + j][t] = S.dx[j];
+        }
+    };
+
+    float acc[2][2][4];
+#pragma unroll
+    for (int rs = 0; rs < 2; ++rs)
+#pragma unroll
+        for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[rs][ts][i] = 0.0f;
+    const int shift = DT == kQ8 ? 0 : (lq >> 1) * 4;
+    const int aoff_l = DT == kQ8 ? lq * 8 : (lq & 1) * 8;
+    // One block's operands (two weight tiles, two token tiles) and its products.
+    struct Ops {
+        long a[2], x[2];
+        float4 dw[2];
+        float dx[2];
+    };
+    auto ld_ops = [&](Ops& o, int buf, int b) {
+#pragma unroll
+        for (int rs = 0; rs < 2; ++rs) {
+            o.a[rs] = *reinterpret_cast<const long*>(&as[buf][(wr * 32 + rs * 16 + li) * kArow + b * kBw + aoff_l]);
+            o.dw[rs] = *reinterpret_cast<const float4*>(&dws[buf][b][wr * 32 + rs * 16 + 4 * lq]);
+        }
+#pragma unroll
+        for (int ts = 0; ts < 2; ++ts) {
+            o.x[ts] = *reinterpret_cast<const long*>(&xs[buf][(wt * 32 + ts * 16 + li) * kXrow + b * QK + lq * 8]);
+            o.dx[ts] = dxs[buf][b][wt * 32 + ts * 16 + li];
+        }
+    };
+    auto mma = [&](const Ops& o, v4i(&c)[2][2]) {
+#pragma unroll
+        for (int rs = 0; rs < 2; ++rs) {
+            long a = o.a[rs];
+            if (DT == kQ4) {
+                const uint64_t v = (uint64_t)a;
+                const uint32_t lo = nibbles_to_i8(((uint32_t)v >> shift) & 0x0F0F0F0Fu);
+                const uint32_t hi = nibbles_to_i8(((uint32_t)(v >> 32) >> shift) & 0x0F0F0F0Fu);
+                a = (long)(((uint64_t)hi << 32) | lo);
+            }
+#pragma unroll
+            for (int ts = 0; ts < 2; ++ts)
+                c[rs][ts] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, o.x[ts], (v4i){0, 0, 0, 0}, 0, 0, 0);
+        }
+    };
+    // acc = fma(float(s) * dw, dx, acc) (ops_ref.cpp:97-98) for one block
+    auto chain = [&](const Ops& o, const v4i(&c)[2][2]) {
+#pragma unroll
+        for (int rs = 0; rs < 2; ++rs) {
+            const float dwv[4] = {o.dw[rs].x, o.dw[rs].y, o.dw[rs].z, o.dw[rs].w};
+#pragma unroll
+            for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[rs][ts][i] = __builtin_fmaf((float)c[rs][ts][i] * dwv[i], o.dx[ts], acc[rs][ts][i]);
+        }
+    };
+    // Blocks 0 .. nblk - 1 of buffer buf in order, software-pipelined: block b + 1's operands are read and its
+    // products issued while block b's chains run.
+    auto compute = [&](int buf, int nblk) {
+        Ops o0, o1;
+        v4i c0[2][2], c1[2][2];
+        ld_ops(o0, buf, 0);
+        mma(o0, c0);
+        int b = 0;
+        for (; b + 2 <= nblk; b += 2) {
+            ld_ops(o1, buf, b + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(o0, c0);
+            mma(o1, c1);
+            if (b + 2 < nblk) ld_ops(o0, buf, b + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(o1, c1);
+            if (b + 2 < nblk) mma(o0, c0);
+        }
+        if (b < nblk) chain(o0, c0);
+    };
+
+    // Two register sets, chunk j in set j % 2: chunk c + 1 is staged after chunk c is multiplied (its buffer was last
+    // read by chunk c - 1, before the previous barrier), and the loads of chunk c + 3 go into the set it leaves, so
+    // two chunks' products cover each load.
+    const int n_chunks = (nb + KC - 1) / KC;
+    QH_MMSTAMP(0);
+    R S0, S1;
+    load(S0, 0);
+    if (n_chunks > 1) load(S1, KC);
+    stage(S0, 0);
+    if (n_chunks > 2) load(S0, 2 * KC);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    QH_MMSTAMP(1);
+    auto step = [&](int c, R& Sn) {  // Sn holds chunk c + 1
+        compute(c & 1, min(KC, nb - c * KC));
+        QH_MMSTAMP(2 + 3 * c);
+        if (c + 1 < n_chunks) {
+            stage(Sn, (c + 1) & 1);
+            QH_MMSTAMP(3 + 3 * c);
+            if (c + 3 < n_chunks) load(Sn, (c + 3) * KC);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __syncthreads();
+        QH_MMSTAMP(4 + 3 * c);
+    };
+    for (int c = 0; c < n_chunks; c += 2) {
+        step(c, S1);
+        if (c + 1 < n_chunks) step(c + 1, S0);
+    }
+
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts) {
+        const int tok = tbase + wt * 32 + ts * 16 + li;
+        if (tok < n) {
+#pragma unroll
+            for (int rs = 0; rs < 2; ++rs)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = rbase + wr * 32 + rs * 16 + 4 * lq + i;
+                    if (r < r1) sg.out[(size_t)tok * sg.ldo + r] = acc[rs][ts][i];
+                }
+        }
+    }
+}
+
 // Register-chain variant: a wave owns 16 rows x 16*TT tokens over all of K and runs the chains of its own MFMA
 // outputs in registers (lane l: rows 4*(l/16)+i, token l%16 of each tile), so no block sum goes through LDS. The NW
 // waves of a workgroup share the 16 rows (their weight loads hit L1) and take consecutive token tiles. Blocks go in
@@ -630,12 +868,15 @@ __global__ __launch_bounds__(64 * NW) void matmul_reg_kernel(MmSegs segs, const 
 namespace {
 
 // Launch plan: kernel family, token tiles (per workgroup for the LDS kernel, per wave for the register kernel) and
-// waves per workgroup. QH_MM="stage", "stage:NS", "lds:TT" or "reg:TT:NW" overrides the heuristic (tuning sweeps).
+// waves per workgroup. QH_MM="stage", "stage:NS", "tile", "tile:KC", "lds:TT" or "reg:TT:NW" overrides the heuristic
+// (tuning sweeps).
 struct MmPlan {
     bool reg;
     int tt, nw;
     bool stage = false;  // the LDS-staged kernel (one token tile per workgroup)
     int ns = 0;          // its register sets in flight past two chunks (2, 3 or 4; 0: default)
+    bool tile = false;   // the 64 x 64 tile kernel
+    int kc = 4;          // its blocks per chunk (4 or 8)
 };
 
 MmPlan matmul_plan(int rows, int cols, int n) {
@@ -645,23 +886,23 @@ MmPlan matmul_plan(int rows, int cols, int n) {
         int a = 0, b = 0;
         if (sscanf(env, "lds:%d", &a) == 1 && (a == 1 || a == 2 || a == 4)) return MmPlan{false, a, 4};
         if (strcmp(env, "stage") == 0) return MmPlan{false, 1, 4, true};
+        if (strcmp(env, "tile") == 0) return MmPlan{false, 1, 4, false, 0, true, 4};
+        if (sscanf(env, "tile:%d", &a) == 1 && (a == 4 || a == 8)) return MmPlan{false, 1, 4, false, 0, true, a};
         if (sscanf(env, "stage:%d", &a) == 1 && a >= 2 && a <= 4) return MmPlan{false, 1, 4, true, a};
         if (sscanf(env, "reg:%d:%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && (b == 1 || b == 2 || b == 4))
             return MmPlan{true, a, b};
     }
-    (void)cols;
-    // From a sweep on MI355X (cold weights) at the Qwen2.5-0.5B shapes, M = 32 / 128 / 512: with few (row tile,
-    // token tile) pairs the LDS-staged kernel wins (its 4 waves split each chunk's blocks, so more of the chip works
-    // on few tiles); with 1024 or more the register-chain kernel wins (no LDS round trip for the block sums). Few row
-    // tiles take 4 token tiles per wave, others 2, with 2 waves per workgroup once a row tile has 8 waves or more.
-    const int row_tiles = (rows + 15) / 16;
-    const int tiles = (n + 15) / 16;
-    // The LDS-staged kernel (coalesced operand loads, one token tile per workgroup) measured 4-12% under the LDS and
-    // register kernels at 32 tokens (q/k/v, o, gate/up, down), and under the LDS kernel wherever that one was chosen.
-    if (tiles <= 2 || (long)row_tiles * tiles < 1024) return MmPlan{false, 1, 4, true};
-    pl.tt = row_tiles < 128 ? 4 : 2;
-    pl.nw = (pl.tt == 2 && tiles / pl.tt >= 8) ? 2 : 1;
-    return pl;
+    (void)pl;
+    // From sweeps on MI355X (cold weights) at the Qwen2.5-0.5B shapes, M = 32 / 64 / 128 / 512: the 64 x 64 tile
+    // kernel wins from 128 tokens on rows of up to 64 blocks once there are about 96 tiles or more (Q4_0 4864x896 at
+    // M = 512: 22.1 us, against 45.0 staged and 54.2 register-chain; M = 128: 13.1 against 14.5; Q8_0 896x896 at
+    // M = 512: 11.9 against 13.3); everywhere else the LDS-staged kernel wins, also over the register-chain kernel
+    // (Q4_0 896x4864 at M = 512: 40.5 against 49.6 us; the tile kernel 45.7, its 112 tiles run 152-block chains on a
+    // quarter of the SIMDs). The LDS-staged kernel measured 4-12% under the LDS and register kernels at 32 tokens
+    // (q/k/v, o, gate/up, down).
+    const long tiles64 = (long)((rows + 63) / 64) * ((n + 63) / 64);
+    if (n >= 128 && cols <= 2048 && tiles64 >= 96) return MmPlan{false, 1, 4, false, 0, true, 4};
+    return MmPlan{false, 1, 4, true};
 }
 
 template <int DT, int TT, int KC>
@@ -704,6 +945,22 @@ hipError_t launch_matmul_segs(const MmOut* m, int n_mats, const int8_t* xq, cons
     const bool vec = (W.cols / QK) % 4 == 0 && (reinterpret_cast<uintptr_t>(xd) & 15u) == 0;
     bool aligned = (reinterpret_cast<uintptr_t>(xq) & 15u) == 0;
     for (int i = 0; i < n_mats; ++i) aligned = aligned && (reinterpret_cast<uintptr_t>(sg.wq[i]) & 15u) == 0;
+    if (pl.tile && aligned) {
+        MmSegs sg64 = sg;
+        int row_tiles64 = 0;
+        for (int i = 0; i < n_mats; ++i) {
+            sg64.tiles[i] = (m[i].r1 - m[i].r0 + 63) / 64;
+            row_tiles64 += sg64.tiles[i];
+        }
+        const int n_tg = (n + 63) / 64;
+        const dim3 grid((unsigned)(row_tiles64 * n_tg));
+#define QH_MM_TILE(DT, KC)                                                                                     \
+    if (W.dtype == DT && pl.kc == KC)                                                                             \
+        qh_launch((matmul_tile_kernel<DT, KC>), grid, dim3(kMmThreads), 0, s, sg64, xq, xd, W.cols, n, n_tg);
+        QH_MM_TILE(kQ8, 4) QH_MM_TILE(kQ8, 8) QH_MM_TILE(kQ4, 4) QH_MM_TILE(kQ4, 8)
+#undef QH_MM_TILE
+        return hipGetLastError();
+    }
     if (pl.stage && aligned) {
         const int n_tg = (n + 15) / 16;
         // Register sets in flight: the two chunks of short rows, else pl.ns (default 2)
@@ -744,6 +1001,12 @@ hipError_t launch_matmul_segs(const MmOut* m, int n_mats, const int8_t* xq, cons
 #undef QH_MM_REG
     return hipErrorInvalidValue;
 }
+
+#if defined(QH_TIMELINE)
+extern "C" int qh_timeline_mm_read(uint64_t* host, int n) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(qh_tl_mm), sizeof(uint64_t) * (size_t)n);
+}
+#endif
 
 hipError_t launch_matmul(float* out, int ldo, const qh_tensor& W, const int8_t* xq, const float* xd, int n, int r0,
                          int r1, hipStream_t s) {

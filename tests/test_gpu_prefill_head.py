@@ -36,18 +36,18 @@ def test_matmul_matches_oracle(qh, oracle, synth, gpu, dtype, N, K, M):
 @pytest.mark.parametrize("dtype,N,K", PREFILL)
 @pytest.mark.parametrize("M", [128, 512])
 def test_matmul_rows_equal_gemv(qh, oracle, synth, gpu, dtype, N, K, M):
-    """Large M: every token row equals the decode GEMV of that token; a slice of rows against the oracle."""
+    """Large M (the 64 x 64 tile kernel): every output equals the oracle's, and every token row the decode GEMV of
+    that token, bit for bit."""
     import torch
     buf = synth.q8_tensor(21 + N, N, K) if dtype == 2 else synth.q4_tensor(23 + N, N, K)
     x = synth.activations(29 + M, M, K)
     W = qh.DeviceTensor.upload(buf, dtype, N, K)
     xq, xd = qh.quantize_q8(_dev(x, gpu))
     got = qh.matmul_q(W, xq, xd)
+    want = oracle.matmul_q(dtype, N, K, buf, xq.cpu().numpy(), xd.cpu().numpy(), threads=8)
+    assert (bits(got.cpu().numpy()) == bits(want)).all()
     per_tok = torch.stack([qh.matvec_q(W, xq[t], xd[t]) for t in range(M)])
     assert torch.equal(got.view(torch.int32), per_tok.view(torch.int32))
-    r0, r1 = 64, 96
-    want = oracle.matmul_q(dtype, N, K, buf, xq.cpu().numpy(), xd.cpu().numpy(), r0=r0, r1=r1)
-    assert (bits(got.cpu().numpy()[:, r0:r1]) == bits(want[:, r0:r1])).all()
 
 
 def test_matmul_row_range_and_ldo(qh, oracle, synth, gpu):
@@ -254,7 +254,7 @@ def test_shortlist_full_vocab(qh, oracle, synth, gpu):
     assert np.float32(st["top1_logit"]).tobytes() == full[st["top1"]].cpu().numpy().tobytes()
 
 
-@pytest.mark.parametrize("tt", ["stage", "stage:2", "stage:3", "stage:4"])
+@pytest.mark.parametrize("tt", ["stage", "stage:2", "stage:3", "stage:4", "tile"])
 @pytest.mark.parametrize("K", [512, 1536, 2560, 3584, 5632, 8192])
 @pytest.mark.parametrize("dtype", [2, 3])
 def test_matmul_staged_chunk_counts(qh, oracle, synth, gpu, monkeypatch, tt, dtype, K):
@@ -272,7 +272,8 @@ def test_matmul_staged_chunk_counts(qh, oracle, synth, gpu, monkeypatch, tt, dty
         assert (bits(got) == bits(want)).all(), (tt, M)
 
 
-@pytest.mark.parametrize("tt", ["stage", "lds:1", "lds:2", "lds:4", "reg:1:1", "reg:1:4", "reg:2:2", "reg:4:1", "reg:4:4"])
+@pytest.mark.parametrize("tt", ["stage", "tile", "tile:8", "lds:1", "lds:2", "lds:4", "reg:1:1", "reg:1:4", "reg:2:2", "reg:4:1",
+                                "reg:4:4"])
 @pytest.mark.parametrize("dtype,N,K", [(2, 200, 896), (3, 200, 896), (2, 40, 4864), (3, 40, 4864)])
 def test_matmul_every_token_tiling(qh, oracle, synth, gpu, monkeypatch, tt, dtype, N, K):
     """Both prefill kernels at every token tiling (LDS-staged block sums, register chains) on ragged shapes: rows not a
@@ -280,7 +281,7 @@ def test_matmul_every_token_tiling(qh, oracle, synth, gpu, monkeypatch, tt, dtyp
     monkeypatch.setenv("QH_MM", tt)
     buf = synth.q8_tensor(61 + N, N, K) if dtype == 2 else synth.q4_tensor(67 + N, N, K)
     W = qh.DeviceTensor.upload(buf, dtype, N, K)
-    for M in (1, 15, 17, 40, 65):
+    for M in (1, 15, 17, 40, 65, 130):
         xq, xd = qh.quantize_q8(_dev(synth.activations(71 + M, M, K), gpu))
         got = qh.matmul_q(W, xq, xd).cpu().numpy()
         want = oracle.matmul_q(dtype, N, K, buf, xq.cpu().numpy(), xd.cpu().numpy(), threads=8)
