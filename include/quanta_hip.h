@@ -131,7 +131,7 @@ typedef struct qh_head_query {
     int32_t n_must;
 } qh_head_query;
 
-#define QH_HEAD_MAX_TOPK 55 /* seeds = top_k + 8, kept with one more key in a 64-lane wave */
+#define QH_HEAD_MAX_TOPK 256 /* seeds = top_k + 8 (the sampler's survivor limit, QH_SAMPLE_MAX_TOPK) */
 
 /* Device-side summary of one shortlist call. */
 typedef struct qh_head_stats {

@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libquanta_hip.so")
 QK = 32
 F32, F16, Q8_0, Q4_0 = 0, 1, 2, 3
-HEAD_MAX_TOPK = 55
+HEAD_MAX_TOPK = 256
 NOALLOC_SCRATCH_BYTES = 4 << 20  # QH_NOALLOC_SCRATCH_BYTES
 # status codes (quanta_hip.h)
 OK, ERR_ARG, ERR_DTYPE, ERR_SHAPE, ERR_ALIGN, ERR_HIP, ERR_NOMEM, ERR_UNSUPPORTED = range(8)

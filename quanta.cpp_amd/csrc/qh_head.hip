@@ -79,8 +79,9 @@ constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kSelShares = 4;   // screen shares per select thread: at most kSelShares * kSelThreads shares
 constexpr int kSelRows = 4;     // rows per select thread in the candidate scan
 constexpr int kPoolCap = 1024;  // keys an LDS selection pool holds
-constexpr int kMaxKeep = QH_HEAD_MAX_TOPK + 9;
-static_assert(kMaxKeep <= 64, "the seeds and the key after them fit one wave, one per lane");
+constexpr int kMaxKeep = QH_HEAD_MAX_TOPK + 9;  // the seeds and the key after them
+constexpr int kWaveKeep = 64;                    // up to this many, one lane per key in one wave
+constexpr int kBandWords = kSelRows * kSelThreads / 32;  // a bit per band row
 
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
@@ -318,6 +319,13 @@ __device__ __forceinline__ void wave_append_n(const bool (&pred)[N], int* counte
         slot[j] = pred[j] ? off + __popcll(m[j] & below) : -1;
         off += __popcll(m[j]);
     }
+}
+
+// Sum over the wave (every lane active).
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
 }
 
 // Sum over each group of 4 lanes (DPP quad permutations; every lane active).
@@ -636,10 +644,12 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     __shared__ RadixShared rsh;
     __shared__ int candl[kSelRows * kSelThreads], mustl[kSelRows * kSelThreads], candf[kSelRows * kSelThreads];
     __shared__ float candu[kSelRows * kSelThreads];              // the speculative candidates' upper bounds
-    __shared__ float rx[2 * kRescoreRows + kSelRows * kSelThreads];  // exact logits: seeds (or pool), then candl
+    constexpr int kRxHead = kMaxKeep > 2 * kRescoreRows ? kMaxKeep : 2 * kRescoreRows;
+    __shared__ float rx[kRxHead + kSelRows * kSelThreads];  // exact logits: seeds (or pool), then candl
     __shared__ int n_pool, n_sel, n_c, n_m, n_x, n_cf, ns_sh, base_sh, last_sh, n_cand_sh;
     __shared__ uint64_t thr_sh, key_sh, top_sh;
     __shared__ float tau_sh;
+    __shared__ uint32_t seedmap[kBandWords];  // more than kWaveKeep seeds: the band's seed rows
     __shared__ int wsum[kSelWaves];
     __shared__ uint64_t wkey[kSelWaves];
 
@@ -676,7 +686,8 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     }
     for (int i = tid; i < nb * 2; i += kSelThreads) reinterpret_cast<uint4*>(xs)[i] = load16(xq + (size_t)i * 16);
     for (int i = tid; i < nb; i += kSelThreads) xds[i] = xd[i];
-    if (tid < kMaxKeep) best[tid] = 0ull;
+    for (int i = tid; i < kMaxKeep; i += kSelThreads) best[i] = 0ull;
+    if (tid < kBandWords) seedmap[tid] = 0u;
     if (tid == 0) {
         n_pool = 0;
         n_sel = 0;
@@ -731,7 +742,17 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
         if (rank == 0) top_sh = gmax[i];
     });
     __syncthreads();
-    const uint64_t L = thr_sh;
+    // More keys than group maxima (uniform): the cut is the n_keep-th best published key instead (n_keep distinct keys
+    // reach it; radix select over every share's published keys)
+    const uint64_t L = n_keep <= kSelThreads / 4 ? thr_sh
+                                                 : block_kth_threshold<kSelThreads>(
+                                                       [&](auto visit) {
+#pragma unroll
+                                                           for (int s = 0; s < SH; ++s)
+#pragma unroll
+                                                               for (int r = 0; r < kTops; ++r) visit(tk[s][r]);
+                                                       },
+                                                       n_keep, rsh);
     const int nm = n_m;
     // The speculative candidates' cut, a sixteenth of the k-th best coarse score below it: for k = 1 the best key
     // overall, known here (the best group maximum); for k > 1 once the pool is ranked.
@@ -886,31 +907,81 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     QH_HSTAMP(2, 3);
     QH_HSTAMP(1, 1);
     int ns = 0;
-    if (wave == 0) {  // one lane per seed
-        ns = __popcll(__ballot(lane < n_seed && best[lane] != 0));
-        const bool have = lane < ns;
-        const float e = have ? exact[lane] : -__builtin_inff();
-        float t = -__builtin_inff();
-        const uint64_t ks = wave_max_u64(have ? score_key(e, seedrow[lane]) : 0ull);
-        if (k == 1) {  // the best exact seed logit
-            if (ns >= 1) t = key_score(ks);
-        } else if (ns >= k) {  // fewer than k seeds above it, k at or above
-            int gt = 0, ge = 0;
-            for (int j = 0; j < ns; ++j) {
-                const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-                gt += ej > e ? 1 : 0;
-                ge += ej >= e ? 1 : 0;
+    if (n_seed < kWaveKeep) {  // uniform
+        if (wave == 0) {  // one lane per seed
+            ns = __popcll(__ballot(lane < n_seed && best[lane] != 0));
+            const bool have = lane < ns;
+            const float e = have ? exact[lane] : -__builtin_inff();
+            float t = -__builtin_inff();
+            const uint64_t ks = wave_max_u64(have ? score_key(e, seedrow[lane]) : 0ull);
+            if (k == 1) {  // the best exact seed logit
+                if (ns >= 1) t = key_score(ks);
+            } else if (ns >= k) {  // fewer than k seeds above it, k at or above
+                int gt = 0, ge = 0;
+                for (int j = 0; j < ns; ++j) {
+                    const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+                    gt += ej > e ? 1 : 0;
+                    ge += ej >= e ? 1 : 0;
+                }
+                const uint64_t at = __ballot(have && gt < k && ge >= k);  // equal values wherever it is set
+                t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), __ffsll((long long)at) - 1));
             }
-            const uint64_t at = __ballot(have && gt < k && ge >= k);  // equal values wherever it is set
-            t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), __ffsll((long long)at) - 1));
+            if (lane == 0) {
+                tau_sh = t;
+                key_sh = ks;
+                ns_sh = ns;
+            }
         }
+        __syncthreads();
+    } else {
+        // Many seeds (k > 55): the same over the workgroup. The ranked keys are nonzero first, so ns counts them; tau
+        // is the exact logit with fewer than k seeds above it and k at or above (equal values wherever that holds).
+        int have = 0;
+        uint64_t ks = 0;
+        for (int i = tid; i < n_seed; i += kSelThreads) {
+            if (best[i] != 0) {
+                ++have;
+                const uint64_t kk = score_key(exact[i], seedrow[i]);
+                ks = kk > ks ? kk : ks;
+            }
+        }
+        have = wave_sum_int(have);
+        ks = wave_max_u64(ks);
         if (lane == 0) {
-            tau_sh = t;
+            wsum[wave] = have;
+            wkey[wave] = ks;
+        }
+        if (tid == 0) tau_sh = -__builtin_inff();
+        __syncthreads();
+        ns = 0;
+        ks = 0;
+#pragma unroll
+        for (int w = 0; w < kSelWaves; ++w) {
+            ns += wsum[w];
+            ks = wkey[w] > ks ? wkey[w] : ks;
+        }
+        if (ns >= k)
+            for (int i = tid; i < ns; i += kSelThreads) {
+                const float e = exact[i];
+                int gt = 0, ge = 0;
+                for (int j = 0; j < ns; ++j) {
+                    const float ej = exact[j];
+                    gt += ej > e ? 1 : 0;
+                    ge += ej >= e ? 1 : 0;
+                }
+                if (gt < k && ge >= k) tau_sh = e;
+            }
+        // the band's seed rows as bits, for the candidate filter below
+        for (int i = tid; i < ns; i += kSelThreads) {
+            const int r = seedrow[i];
+            if (r >= ca && r < cb) atomicOr(&seedmap[(r - ca) >> 5], 1u << ((r - ca) & 31));
+        }
+        if (tid == 0) {
             key_sh = ks;
             ns_sh = ns;
         }
+        __syncthreads();
     }
-    __syncthreads();
     const float tau = tau_sh;
     ns = ns_sh;
     if (blockIdx.x == 0)
@@ -921,7 +992,8 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     QH_HSTAMP(1, 2);
     // The kept candidates and the must rows: logits out, their best key.
     uint64_t kbest = 0;
-    auto not_seed = [&](int r) {
+    auto not_seed = [&](int r) {  // r is a row of the band
+        if (n_seed >= kWaveKeep) return ((seedmap[(r - ca) >> 5] >> ((r - ca) & 31)) & 1u) == 0u;
         bool ok = true;
         for (int q = 0; q < ns; ++q) ok = ok && seedrow[q] != r;
         return ok;

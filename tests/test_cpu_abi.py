@@ -41,8 +41,8 @@ def test_sizes_follow_qnt_layout(qh):
     assert L.qh_tensor_bytes(qh.Q4_0, 4864, 896) == 2451456  # 0.5625 B per weight
     assert L.qh_tensor_bytes(qh.F16, 151936, 28) == 151936 * 28 * 2
     assert L.qh_shortlist_workspace_bytes(151936, 896, 1) > 151936
-    assert L.qh_shortlist_workspace_bytes(151936, 896, 56) == 0  # above the top_k limit
-    assert L.qh_shortlist_workspace_bytes(151936, 896, 55) > 0
+    assert L.qh_shortlist_workspace_bytes(151936, 896, 257) == 0  # above the top_k limit
+    assert L.qh_shortlist_workspace_bytes(151936, 896, 256) > 0
     assert L.qh_shortlist_workspace_bytes(151936, 96, 1) == 0  # hidden size not a multiple of 64
     assert L.qh_shortlist_workspace_bytes(151936, 896, 0) == 0
 
@@ -95,7 +95,7 @@ def test_shortlist_argument_checks(qh):
     assert call(bad, q, ws) == 3                     # bound tensor shape (model.cpp:49-58)
     assert call(he, q, ws - 1) == 6                  # workspace too small
     assert call(he, qh.qh_head_query(0, 0, None, 0), ws) == 7
-    assert call(he, qh.qh_head_query(56, 0, None, 0), ws) == 7
+    assert call(he, qh.qh_head_query(257, 0, None, 0), ws) == 7
     assert call(he, qh.qh_head_query(1, 0, None, 3), ws) == 1  # must count without a list
     swapped = lambda: L.qh_shortlist_head(C.byref(h4), C.byref(h8), C.byref(he), C.c_void_p(16), C.c_void_p(16),
                                           C.byref(q), C.byref(out), C.c_void_p(4096), ws, None)

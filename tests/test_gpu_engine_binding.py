@@ -14,7 +14,9 @@ quanta.cpp_amd/qnt.py:
 - check_head (checks.cpp:178-239): the GPU shortlist head against the GPU full head for top-k 1 and 20 with the
   last 64 ids as must ids, the bound over every row, exact rows bit-identical;
 - `gen --greedy` (tools/cli/main.cpp:216-251), with the shortlist head and with --full-head: the 24-id stream equals
-  the reference CPU engine's (tests/golden/e2e_small.npz, same model and prompt).
+  the reference CPU engine's (tests/golden/e2e_small.npz, same model and prompt);
+- `gen --top-k 64` and `--top-k 256` (head queries of top-k 64 / 256 with the history as must ids, greedy picks):
+  the stream equals the reference Session's on the CPU (oracle/_ref, the same flow through its library).
 """
 import os
 import re
@@ -88,3 +90,26 @@ def test_reference_gen_stream(small_model, full_head):
     assert r.returncode == 0, r.stderr
     got = [int(t) for t in r.stdout.strip().split(",")]
     assert got == g["out"].tolist()
+
+
+@pytest.mark.parametrize("top_k", [64, 256])
+def test_reference_gen_large_topk(small_model, top_k):
+    """`gen --top-k K` queries the shortlist head with top-k K and the history as must ids (session.cpp:63-79) and
+    picks greedily (tools/cli/main.cpp:233-246); the reference engine bound to the GPU path gives the CPU build's
+    stream."""
+    import oracle as orc
+    if orc.ref is None:
+        pytest.skip("oracle/_ref/libquanta_ref.so is not built")
+    g = np.load(os.path.join(GOLDEN, "e2e_small.npz"))
+    n_gen = 16
+    ids = ",".join(str(int(i)) for i in g["prompt"])
+    r = run_engine("gen", "-m", small_model, "--ids", ids, "-n", str(n_gen), "--top-k", str(top_k), "-t", "8")
+    assert r.returncode == 0, r.stderr
+    got = [int(t) for t in r.stdout.strip().split(",")]
+    m = orc.ref.load_model(small_model, 4096, 8)
+    try:
+        want, _ = orc.ref.gen_sampled(m, g["prompt"], n_gen, orc.sampler_params(top_k=top_k),
+                                      orc.sampler_params(temperature=0.0, repeat_penalty=1.0), 1)
+    finally:
+        orc.ref.free_model(m)
+    assert got == want.tolist()

@@ -99,7 +99,7 @@ def _check_head(qh, oracle, head_np, sl, xq, xd, V, D, top_k, n_valid=0, must=No
     return st, o
 
 
-@pytest.mark.parametrize("top_k", [1, 20])
+@pytest.mark.parametrize("top_k", [1, 20, 64, 256])
 def test_shortlist_small_vocab(qh, oracle, synth, gpu, top_k):
     V, D = 6007, 896
     head_np, (h8, h4, he) = _head(qh, synth, gpu, V, D, 41)
@@ -206,7 +206,7 @@ def test_shortlist_second_rescoring_pass(qh, oracle, synth, gpu, top_k):
     assert st["n_rows"] == o["n_rows"] > 500
 
 
-@pytest.mark.parametrize("top_k,r0,n", [(1, 70001, 300), (20, 5, 700), (55, 40000, 9600)])
+@pytest.mark.parametrize("top_k,r0,n", [(1, 70001, 300), (20, 5, 700), (55, 40000, 9600), (256, 90000, 9600)])
 def test_shortlist_crowded_shares(qh, oracle, synth, gpu, top_k, r0, n):
     """The best keys crowd a few screen shares: each share publishes only its best four keys, so shares holding more
     than four of them are read again (a few hundred keys), and past 1024 keys at or above the cut the selection falls
@@ -230,10 +230,35 @@ def test_shortlist_fewer_shares_than_seeds(qh, oracle, synth, gpu):
     head_np, (h8, h4, he) = _head(qh, synth, gpu, V, D, 223)
     x = synth.activations(227, 2, D, scale=0.5)
     xq, xd = qh.quantize_q8(_dev(x, gpu))
-    for top_k in (1, 20, 55):
+    for top_k in (1, 20, 55, 64, 256):
         sl = qh.ShortlistHead(h8, h4, he, top_k=top_k)
         _check_head(qh, oracle, head_np, sl, xq[0], xd[0], V, D, top_k)
         _check_head(qh, oracle, head_np, sl, xq[1], xd[1], V, D, top_k, n_valid=250, must=[3, 299, 3, 7])
+
+
+@pytest.mark.parametrize("top_k", [64, 128, 256])
+def test_shortlist_large_topk_full_vocab(qh, oracle, synth, gpu, top_k):
+    """The benchmark head's shape at the top-k values of sampling (more seeds than a wave's lanes: the cut from a radix
+    select over the published keys, tau over the workgroup, the seeds as band bits), with and without must ids:
+    everything equals the oracle bit for bit, and the reference build's own Model::shortlist_head returns the same
+    rows and logits."""
+    import oracle as orc
+    V, D = 151936, 896
+    head_np, (h8, h4, he) = _head(qh, synth, gpu, V, D, 47)
+    sl = qh.ShortlistHead(h8, h4, he, top_k=top_k)
+    x = synth.activations(59, 3, D, scale=0.5)
+    xq, xd = qh.quantize_q8(_dev(x, gpu))
+    must = np.random.default_rng(61).integers(0, V, 500).tolist()
+    for t, mu in ((0, None), (1, None), (2, must)):
+        print(f"large top-k {top_k}, vector {t}", flush=True)
+        st, o = _check_head(qh, oracle, head_np, sl, xq[t], xd[t], V, D, top_k, must=mu)
+        assert st["n_seeds"] == top_k + 8
+        if orc.ref is not None:
+            r = orc.ref.shortlist_head(*head_np, V, D, xq[t].cpu().numpy(), xd[t].cpu().numpy(), top_k=top_k, must=mu,
+                                       threads=8)
+            assert r["n_rows"] == st["n_rows"]
+            assert sorted(r["rows"].tolist()) == sorted(sl.rows.cpu().numpy()[: st["n_rows"]].tolist())
+            assert (bits(r["logits"]) == bits(sl.logits.cpu().numpy())).all()
 
 
 def test_shortlist_full_vocab(qh, oracle, synth, gpu):

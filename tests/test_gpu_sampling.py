@@ -77,7 +77,8 @@ def test_sample_full_vocab_pool_overflow(qh, oracle, gpu):
     _draws(qh, oracle, torch.from_numpy(logits).to(gpu), 151936, hist, (0.7, 20, 0.8, 0.0, 1.1, 0), 5, 4)
 
 
-@pytest.mark.parametrize("t", [(0.7, 20, 0.8, 0.0, 1.1, 0), (0.0, 20, 0.8, 0.0, 1.2, 0), (1.2, 55, 0.9, 0.0, 1.1, 9)])
+@pytest.mark.parametrize("t", [(0.7, 20, 0.8, 0.0, 1.1, 0), (0.0, 20, 0.8, 0.0, 1.2, 0), (1.2, 55, 0.9, 0.0, 1.1, 9),
+                               (1.0, 64, 0.95, 0.0, 1.1, 0), (1.3, 256, 0.99, 0.0, 1.05, 0)])
 def test_sample_over_shortlist_rows(qh, oracle, synth, gpu, t):
     """Candidates from the Exact Shortlist Head's row list (every other logit is -inf), with the history as must ids
     of the head query, as the decoder runs it."""
@@ -103,6 +104,9 @@ FLOWS = {
     "chat_window_minp": ((0.9, 40, 0.95, 0.02, 1.3, 12), (0.9, 40, 0.95, 0.02, 1.3, 12), 77),
     "gen_topk20_greedy": ((0.7, 20, 0.8, 0.0, 1.1, 0), None, 1),
     "greedy_penalty": ((0.0, 20, 0.8, 0.0, 1.5, 0), (0.0, 20, 0.8, 0.0, 1.5, 0), 3),
+    "chat_topk64": ((0.8, 64, 0.95, 0.0, 1.1, 0), (0.8, 64, 0.95, 0.0, 1.1, 0), 19),
+    "chat_topk256": ((1.1, 256, 0.98, 0.0, 1.1, 0), (1.1, 256, 0.98, 0.0, 1.1, 0), 23),
+    "gen_topk128_greedy": ((0.7, 128, 0.8, 0.0, 1.1, 0), None, 1),
 }
 
 
