@@ -172,7 +172,7 @@ int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_t
                       size_t workspace_bytes, void* stream);
 
 /* Bytes of the scratch array qh_shortlist_head_noalloc works in: one array in each GPU's memory, held by the library
- * until the process ends. Enough for the 151,936-row Qwen2.5 head (about 0.85 MB at top_k 1, 1.3 MB at top_k 55) and
+ * until the process ends. Enough for the 151,936-row Qwen2.5 head (0.78 MB, the same at every top_k) and
  * for heads up to about 800,000 rows of 896. */
 #define QH_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
 
@@ -224,10 +224,18 @@ int qh_sample(const float* logits, int32_t n_valid, const int32_t* rows, const q
 
 /* ------------------------------------------------------------------ GPU-resident decoder */
 
-/* Model shape (reference engine/src/model_file.h:40-45, HParams) and the context length of the KV cache. */
+/* FLAG_HADAMARD_DOWN (reference engine/src/model_file.h:19-21): the down projection's input is rotated by the
+ * block-diagonal 256 x 256 Walsh-Hadamard transform (model.cpp:216-220), the weights having been rotated offline. */
+#define QH_FLAG_HADAMARD_DOWN 1u
+
+/* Model shape (reference engine/src/model_file.h:40-45, HParams, with its flags) and the load options: the context
+ * length of the KV cache and kv_f32, an f32 cache in place of fp16 (Model::load's kv_f16 = false, the CLI's --kv-f32,
+ * model.cpp:96-104). */
 typedef struct qh_model_desc {
     int32_t vocab_size, dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, ctx_len, qkv_bias;
     float rope_theta, norm_eps;
+    uint32_t flags;  /* QH_FLAG_* */
+    int32_t kv_f32;  /* 0: fp16 cache (the reference's default); 1: f32 cache */
 } qh_model_desc;
 
 typedef struct qh_decoder qh_decoder;
@@ -255,15 +263,21 @@ typedef struct qh_decoder_state {
                                prompt ids of every prefill since position 0, then each chosen id */
     int32_t* history_len;   /* its length */
     uint64_t* rng_state;    /* the sampler's xorshift64* state */
+    float* kcache_f32;      /* with kv_f32 (kcache and vcache NULL then): [n_layers][ctx_len][n_kv_heads * head_dim],
+                               the reference's own layout (model.cpp:96-104); NULL otherwise */
+    float* vcache_f32;      /* the same for V */
 } qh_decoder_state;
 
 /* Creates a decoder over device tensors, in this order (reference model.cpp:14-33, 47-58):
- *   model.embed_tokens.weight (Q8_0 [vocab][dim], also the LM head), model.norm.weight (F32 [1][dim]);
+ *   model.embed_tokens.weight (Q8_0 [vocab][dim], also the LM head when tied), model.norm.weight (F32 [1][dim]);
  *   per layer: input_layernorm (F32), q_proj, k_proj, v_proj, o_proj (Q8_0 or Q4_0), q/k/v biases (F32, or data NULL
  *   without qkv_bias), post_attention_layernorm (F32), gate_proj, up_proj, down_proj (Q8_0 or Q4_0);
- *   then quanta.head_q4 (Q4_0 [vocab][dim]) and quanta.head_err (F16 [vocab][dim/32]), or both with data NULL.
- * Allocates an fp16 KV cache for ctx_len positions and the work buffers. dim, ctx_len <= 8192, head_dim 64 or
- * 128, n_heads * head_dim == dim. The tensors must stay alive while the decoder is used.
+ *   then quanta.head_q4 (Q4_0 [vocab][dim]) and quanta.head_err (F16 [vocab][dim/32]), or both with data NULL;
+ *   optionally (n_tensors 5 + 12 n_layers) lm_head.weight ([vocab][dim], Q8_0 or Q4_0; Q8_0 with the shortlist head
+ *   tensors), the LM head of an untied model; data NULL there, or n_tensors 4 + 12 n_layers, means tied.
+ * Allocates an fp16 KV cache (f32 with hp->kv_f32) for ctx_len positions and the work buffers. dim, ctx_len <= 8192,
+ * head_dim 64 or 128, n_heads * head_dim == dim, ffn_dim % 256 == 0 with QH_FLAG_HADAMARD_DOWN. The tensors must
+ * stay alive while the decoder is used.
  * Replaces: Model::load (reference model.cpp:10-106) after the .qnt file is read and uploaded. */
 int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tensors, qh_decoder** out);
 int qh_decoder_destroy(qh_decoder* d);

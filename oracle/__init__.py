@@ -102,21 +102,26 @@ class _Oracle:
         arrays / dtypes in the order of qo_decoder_create (None for absent tensors)."""
         return Decoder(self.lib, hp, arrays, dtypes)
 
-    def decoder_for(self, hp, tensors: dict, ctx_len: int | None = None) -> "Decoder":
+    def decoder_for(self, hp, tensors: dict, ctx_len: int | None = None, kv_f32: bool = False) -> "Decoder":
         """The decoder over a .qnt tensor set (name -> record with .data / .dtype, as quanta_cpp_amd.qnt writes and
-        reads them) with hyperparameters hp (an HParams record)."""
+        reads them) with hyperparameters hp (an HParams record: its flags and tied_embeddings too); kv_f32: an f32 KV
+        cache (Model::load with kv_f16 false)."""
         arrays, dtypes = [], []
         names = ["model.embed_tokens.weight", "model.norm.weight"]
         for l in range(hp.n_layers):
             names += [f"model.layers.{l}.{n}" for n in LAYER_ORDER]
         names += ["quanta.head_q4", "quanta.head_err"]
+        untied = not getattr(hp, "tied_embeddings", True)
+        if untied:
+            names.append("lm_head.weight")
         for name in names:
             t = tensors.get(name)
             arrays.append(None if t is None else np.asarray(t.data))
             dtypes.append(-1 if t is None else t.dtype)
         h = dict(vocab=hp.vocab_size, dim=hp.dim, n_layers=hp.n_layers, n_heads=hp.n_heads, n_kv_heads=hp.n_kv_heads,
                  head_dim=hp.head_dim, ffn_dim=hp.ffn_dim, ctx_len=ctx_len or hp.max_seq, qkv_bias=int(hp.qkv_bias),
-                 rope_theta=hp.rope_theta, norm_eps=hp.norm_eps)
+                 rope_theta=hp.rope_theta, norm_eps=hp.norm_eps, flags=int(getattr(hp, "flags", 0)),
+                 kv_f32=int(kv_f32), untied=int(untied))
         return Decoder(self.lib, h, arrays, dtypes)
 
     def quantize_q8(self, x: np.ndarray):
@@ -191,8 +196,13 @@ class Decoder:
         self.V, self.D = hp["vocab"], hp["dim"]
         self._keep = [None if a is None else np.ascontiguousarray(a) for a in arrays]
         self._ptrs = (C.c_void_p * len(arrays))(*[None if a is None else a.ctypes.data for a in self._keep])
+        hp = dict(hp)
+        hp.setdefault("flags", 0)
+        hp.setdefault("kv_f32", 0)
+        hp.setdefault("untied", 0)
+        self.kv_f32 = bool(hp["kv_f32"])
         ints = np.array([hp[k] for k in ("vocab", "dim", "n_layers", "n_heads", "n_kv_heads", "head_dim", "ffn_dim",
-                                         "ctx_len", "qkv_bias")], np.int32)
+                                         "ctx_len", "qkv_bias", "flags", "kv_f32", "untied")], np.int32)
         floats = np.array([hp["rope_theta"], hp["norm_eps"]], np.float32)
         self._dt = np.array(dtypes, np.int32)
         self.h = lib.qo_decoder_create(ints, floats, C.cast(self._ptrs, C.c_void_p), self._dt)
@@ -221,9 +231,11 @@ class Decoder:
         return dict(logits=lg, hidden=h, hq=q, hd=d, rows=rows)
 
     def kv(self, layer, n_pos, kv_dim):
-        """The f16 KV cache bits of one layer, positions [0, n_pos): (k, v) as uint16 [n_pos][kv_dim]."""
-        k = np.empty((n_pos, kv_dim), np.uint16)
-        v = np.empty((n_pos, kv_dim), np.uint16)
+        """The KV cache of one layer, positions [0, n_pos): (k, v) as [n_pos][kv_dim] f16 bits (uint16), or f32 values
+        with an f32 cache."""
+        dt = np.float32 if self.kv_f32 else np.uint16
+        k = np.empty((n_pos, kv_dim), dt)
+        v = np.empty((n_pos, kv_dim), dt)
         self.lib.qo_decoder_kv(self.h, layer, n_pos, k.ctypes.data, v.ctypes.data)
         return k, v
 
@@ -274,8 +286,10 @@ class _Ref:
         buf = C.create_string_buffer(512)
         return None if L.ref_model_load_error(path.encode(), buf, 512) else buf.value.decode()
 
-    def load_model(self, path: str, ctx_len: int, threads: int):
-        m = self.lib.ref_model_load(path.encode(), ctx_len, threads)
+    def load_model(self, path: str, ctx_len: int, threads: int, kv_f16: bool = True):
+        L = self.lib
+        L.ref_model_load_kv.argtypes, L.ref_model_load_kv.restype = [C.c_char_p, _int, _int, _int], C.c_void_p
+        m = L.ref_model_load_kv(path.encode(), ctx_len, threads, int(kv_f16))
         if not m:
             raise ValueError(f"the reference could not load {path}")
         return m

@@ -345,10 +345,14 @@ enum { L_ATTN_NORM, L_WQ, L_WK, L_WV, L_WO, L_BQ, L_BK, L_BV, L_FFN_NORM, L_WG, 
 
 struct qo_decoder {
     int V, D, nl, nh, nkv, hdim, F, ctx, bias;
+    int flags; /* model_file.h:21 FLAG_HADAMARD_DOWN */
+    int kv32;  /* f32 KV cache (Model::load kv_f16 = false, the CLI's --kv-f32) */
+    int lm;    /* index of the LM head tensor: 0 (tied embedding) or 4 + 12 n_layers (lm_head.weight) */
     float theta, eps;
     const void* const* t;
     const int* dt;
     uint16_t *kc, *vc; /* [layer][ctx][kv_dim] f16 bits */
+    float *kcf, *vcf;  /* [layer][ctx][kv_dim] f32, with kv32 */
     float *x, *xb, *xb2, *q, *k, *v, *att, *hb, *hb2, *logits, *coarse, *upper, *cs;
     int8_t *xq, *hq;
     float *xd, *hd;
@@ -363,14 +367,21 @@ static int ldt(const qo_decoder* d, int l, int which) { return d->dt[2 + l * L_C
 qo_decoder* qo_decoder_create(const int* hp, const float* hpf, const void* const* tensors, const int* dtypes) {
     qo_decoder* d = (qo_decoder*)calloc(1, sizeof(qo_decoder));
     d->V = hp[0]; d->D = hp[1]; d->nl = hp[2]; d->nh = hp[3]; d->nkv = hp[4]; d->hdim = hp[5]; d->F = hp[6];
-    d->ctx = hp[7]; d->bias = hp[8];
+    d->ctx = hp[7]; d->bias = hp[8]; d->flags = hp[9]; d->kv32 = hp[10];
+    d->lm = hp[11] ? 4 + 12 * d->nl : 0;
     d->theta = hpf[0]; d->eps = hpf[1];
     if (d->nh * d->hdim != d->D || d->nh % d->nkv != 0 || d->D % QO_QK || d->F % QO_QK) { free(d); return NULL; }
+    if ((d->flags & 1) && d->F % 256 != 0) { free(d); return NULL; } /* model.cpp:39-42 */
     d->t = tensors;
     d->dt = dtypes;
     const size_t kvd = (size_t)d->nkv * d->hdim;
-    d->kc = (uint16_t*)calloc((size_t)d->nl * d->ctx * kvd, 2);
-    d->vc = (uint16_t*)calloc((size_t)d->nl * d->ctx * kvd, 2);
+    if (d->kv32) {
+        d->kcf = (float*)calloc((size_t)d->nl * d->ctx * kvd, 4);
+        d->vcf = (float*)calloc((size_t)d->nl * d->ctx * kvd, 4);
+    } else {
+        d->kc = (uint16_t*)calloc((size_t)d->nl * d->ctx * kvd, 2);
+        d->vc = (uint16_t*)calloc((size_t)d->nl * d->ctx * kvd, 2);
+    }
     d->x = (float*)calloc(d->D, 4); d->xb = (float*)calloc(d->D, 4); d->xb2 = (float*)calloc(d->D, 4);
     d->q = (float*)calloc(d->D, 4); d->k = (float*)calloc(kvd, 4); d->v = (float*)calloc(kvd, 4);
     d->att = (float*)calloc((size_t)d->ctx, 4);
@@ -384,15 +395,21 @@ qo_decoder* qo_decoder_create(const int* hp, const float* hpf, const void* const
     return d;
 }
 
-void qo_decoder_kv(const qo_decoder* d, int l, int n_pos, uint16_t* k, uint16_t* v) {
+/* The KV cache rows of one layer, positions [0, n_pos): f16 bits (2 bytes each) or, with kv32, f32 (4 bytes). */
+void qo_decoder_kv(const qo_decoder* d, int l, int n_pos, void* k, void* v) {
     const size_t kvd = (size_t)d->nkv * d->hdim, off = (size_t)l * d->ctx * kvd;
-    memcpy(k, d->kc + off, 2 * kvd * (size_t)n_pos);
-    memcpy(v, d->vc + off, 2 * kvd * (size_t)n_pos);
+    if (d->kv32) {
+        memcpy(k, d->kcf + off, 4 * kvd * (size_t)n_pos);
+        memcpy(v, d->vcf + off, 4 * kvd * (size_t)n_pos);
+    } else {
+        memcpy(k, d->kc + off, 2 * kvd * (size_t)n_pos);
+        memcpy(v, d->vc + off, 2 * kvd * (size_t)n_pos);
+    }
 }
 
 void qo_decoder_free(qo_decoder* d) {
     if (!d) return;
-    free(d->kc); free(d->vc); free(d->x); free(d->xb); free(d->xb2); free(d->q); free(d->k); free(d->v);
+    free(d->kc); free(d->vc); free(d->kcf); free(d->vcf); free(d->x); free(d->xb); free(d->xb2); free(d->q); free(d->k); free(d->v);
     free(d->att); free(d->hb); free(d->hb2); free(d->logits); free(d->coarse); free(d->upper); free(d->rows);
     free(d->xq); free(d->hq); free(d->xd); free(d->hd); free(d->cs); free(d);
 }
@@ -416,6 +433,23 @@ static void rope(float* v, int n_heads, int hd, const float* cs) {
             p[i] = fmaf(a, c, -(b * s));
             p[i + half] = fmaf(b, c, a * s);
         }
+    }
+}
+
+/* ops_ref.cpp:228-241: in-place Walsh-Hadamard transform of each block of `block` values (butterflies v[j] = a + c,
+ * v[j + h] = a - c for h = 1, 2, 4, ...), then * 1 / sqrt(block) */
+static void fwht_blocks(float* x, int n, int block) {
+    const float norm = 1.0f / sqrtf((float)block);
+    for (int b0 = 0; b0 < n; b0 += block) {
+        float* v = x + b0;
+        for (int h = 1; h < block; h *= 2)
+            for (int i = 0; i < block; i += 2 * h)
+                for (int j = i; j < i + h; ++j) {
+                    const float a = v[j], c = v[j + h];
+                    v[j] = a + c;
+                    v[j + h] = a - c;
+                }
+        for (int i = 0; i < block; ++i) v[i] *= norm;
     }
 }
 
@@ -461,31 +495,36 @@ static void layers(qo_decoder* d, int token, int pos) {
         }
         rope(d->q, d->nh, hd, cs);
         rope(d->k, d->nkv, hd, cs);
-        uint16_t* kc = d->kc + (size_t)l * d->ctx * kvd;
-        uint16_t* vc = d->vc + (size_t)l * d->ctx * kvd;
+        const size_t loff = (size_t)l * d->ctx * kvd;
+        /* store (model.cpp:113-114, 197-204): the f16 rounding of k / v, or k / v themselves with kv32 */
         for (int i = 0; i < kvd; ++i) {
-            kc[(size_t)pos * kvd + i] = qo_f32_to_f16(d->k[i]);
-            vc[(size_t)pos * kvd + i] = qo_f32_to_f16(d->v[i]);
+            if (d->kv32) {
+                d->kcf[loff + (size_t)pos * kvd + i] = d->k[i];
+                d->vcf[loff + (size_t)pos * kvd + i] = d->v[i];
+            } else {
+                d->kc[loff + (size_t)pos * kvd + i] = qo_f32_to_f16(d->k[i]);
+                d->vc[loff + (size_t)pos * kvd + i] = qo_f32_to_f16(d->v[i]);
+            }
         }
+#define QO_KV(c, t, i) (d->kv32 ? d->c##f[loff + (size_t)(t) * kvd + (i)] : qo_fp16_to_f32(d->c[loff + (size_t)(t) * kvd + (i)]))
         /* attend (model.cpp:115-137), head by head */
         for (int h = 0; h < d->nh; ++h) {
             const float* qh = d->q + h * hd;
             const int kvh = h / group;
             for (int t = 0; t <= pos; ++t) {
-                const uint16_t* kt = kc + (size_t)t * kvd + kvh * hd;
                 float s = 0.f;
-                for (int i = 0; i < hd; ++i) s = fmaf(qh[i], qo_fp16_to_f32(kt[i]), s);
+                for (int i = 0; i < hd; ++i) s = fmaf(qh[i], QO_KV(kc, t, kvh * hd + i), s);
                 d->att[t] = s * scale;
             }
             softmax(d->att, pos + 1);
             float* out = d->xb + h * hd;
             for (int i = 0; i < hd; ++i) out[i] = 0.f;
             for (int t = 0; t <= pos; ++t) {
-                const uint16_t* vt = vc + (size_t)t * kvd + kvh * hd;
                 const float a = d->att[t];
-                for (int i = 0; i < hd; ++i) out[i] = fmaf(a, qo_fp16_to_f32(vt[i]), out[i]);
+                for (int i = 0; i < hd; ++i) out[i] = fmaf(a, QO_KV(vc, t, kvh * hd + i), out[i]);
             }
         }
+#undef QO_KV
         qo_quantize_q8(d->xb, D, d->xq, d->xd);
         linear(d, d->xb2, l, L_WO, D, D, d->xq, d->xd);
         for (int i = 0; i < D; ++i) d->x[i] += d->xb2[i];
@@ -497,6 +536,7 @@ static void layers(qo_decoder* d, int token, int pos) {
             const float g = d->hb[i];
             d->hb[i] = g / (1.0f + expf(-g)) * d->hb2[i];
         }
+        if (d->flags & 1) fwht_blocks(d->hb, F, 256); /* model.cpp:219 */
         qo_quantize_q8(d->hb, F, d->hq, d->hd);
         linear(d, d->xb2, l, L_WD, D, F, d->hq, d->hd);
         for (int i = 0; i < D; ++i) d->x[i] += d->xb2[i];
@@ -514,11 +554,12 @@ static int head(qo_decoder* d, int top_k, float* logits, float* hidden, int8_t* 
     if (top_k > 0 && h4 && he) {
         int ns, tie;
         float tau;
-        rows = qo_shortlist_head((const uint8_t*)d->t[0], (const uint8_t*)h4, (const uint16_t*)he, V, D, d->xq, d->xd,
+        rows = qo_shortlist_head((const uint8_t*)d->t[d->lm], (const uint8_t*)h4, (const uint16_t*)he, V, D, d->xq, d->xd,
                                  top_k, V, d->must, d->n_must, d->logits, d->coarse, d->upper, d->rows, &ns, &tau,
                                  &tie);
     } else {
-        qo_matvec_q(d->logits, QO_Q8_0, V, D, (const uint8_t*)d->t[0], d->xq, d->xd, 0, V);
+        /* the LM head (model.cpp:16): the embedding when tied, else lm_head.weight */
+        qo_matvec_q(d->logits, d->dt[d->lm], V, D, (const uint8_t*)d->t[d->lm], d->xq, d->xd, 0, V);
         rows = V;
     }
     if (logits) memcpy(logits, d->logits, sizeof(float) * (size_t)V);

@@ -84,11 +84,14 @@ uint16_t qo_f32_to_f16(float f);
 
 typedef struct qo_decoder qo_decoder;
 
-/* hp: vocab, dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, ctx_len, qkv_bias (9 ints);
- * hpf: rope_theta, norm_eps. tensors / dtypes: embed (Q8_0 [V][D], tied head), final norm (F32 [D]); per layer
- * attn_norm, wq, wk, wv, wo, bq, bk, bv, ffn_norm, w_gate, w_up, w_down (12 each; biases NULL without qkv_bias,
- * weights Q8_0 or Q4_0); then the shortlist copy head_q4 (Q4_0 [V][D]) and head_err (F16 [V][D/32]), or NULL.
- * The KV cache is f16, as the reference's default. Returns NULL on a bad argument. */
+/* hp: vocab, dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, ctx_len, qkv_bias, flags (model_file.h:21:
+ * bit 0 FLAG_HADAMARD_DOWN), kv_f32 (1: an f32 KV cache, Model::load with kv_f16 false), untied (1: an lm_head.weight
+ * tensor, model.cpp:16) (12 ints); hpf: rope_theta, norm_eps. tensors / dtypes: embed (Q8_0 [V][D]), final norm
+ * (F32 [D]); per layer attn_norm, wq, wk, wv, wo, bq, bk, bv, ffn_norm, w_gate, w_up, w_down (12 each; biases NULL
+ * without qkv_bias, weights Q8_0 or Q4_0); then the shortlist copy head_q4 (Q4_0 [V][D]) and head_err
+ * (F16 [V][D/32]), or NULL; then, when untied, lm_head (Q8_0 or Q4_0 [V][D]; Q8_0 with the shortlist copy), the LM
+ * head in place of the embedding. Returns NULL on a bad argument (also the Hadamard flag with ffn_dim % 256 != 0,
+ * model.cpp:39-42). */
 qo_decoder* qo_decoder_create(const int* hp, const float* hpf, const void* const* tensors, const int* dtypes);
 void qo_decoder_free(qo_decoder* d);
 
@@ -107,8 +110,9 @@ int qo_decoder_forward(qo_decoder* d, int token, int pos, int top_k, float* logi
 int qo_decoder_forward_batch(qo_decoder* d, const int* tokens, int n, int pos0, int top_k, float* logits,
                              float* hidden, int8_t* hq, float* hd);
 
-/* Copies the f16 KV cache of layer l, positions [0, n_pos): k and v as [n_pos][n_kv_heads * head_dim] bits. */
-void qo_decoder_kv(const qo_decoder* d, int l, int n_pos, uint16_t* k, uint16_t* v);
+/* Copies the KV cache of layer l, positions [0, n_pos): k and v as [n_pos][n_kv_heads * head_dim] f16 bits, or f32
+ * values with kv_f32. */
+void qo_decoder_kv(const qo_decoder* d, int l, int n_pos, void* k, void* v);
 
 /* RoPE table of the reference (ops_ref.cpp:201-214) for positions [0, n_pos): cs[pos][i] = (cosf, sinf) of
  * pos * powf(theta, -2 i / head_dim), i < head_dim / 2, as [n_pos][head_dim / 2][2] floats. */

@@ -152,6 +152,14 @@ void* ref_model_load(const char* path, int ctx_len, int n_threads) {
     return m.release();
 }
 
+// The same with the KV cache's type chosen: kv_f16 0 is the CLI's --kv-f32 (model.cpp:96-104).
+void* ref_model_load_kv(const char* path, int ctx_len, int n_threads, int kv_f16) {
+    auto m = std::make_unique<quanta::Model>();
+    std::string err;
+    if (!m->load(path, ctx_len, &err, n_threads, kv_f16 != 0)) return nullptr;
+    return m.release();
+}
+
 void ref_model_free(void* m) { delete static_cast<quanta::Model*>(m); }
 
 // Replaces a loaded model's thread pool with one of n_threads (n <= 0: ThreadPool::default_threads()), resizing the

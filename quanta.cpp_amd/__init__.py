@@ -48,13 +48,15 @@ class qh_head_out(C.Structure):
 class qh_model_desc(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("vocab_size", "dim", "n_layers", "n_heads", "n_kv_heads", "head_dim",
                                          "ffn_dim", "ctx_len", "qkv_bias")] + [("rope_theta", C.c_float),
-                                                                              ("norm_eps", C.c_float)]
+                                                                              ("norm_eps", C.c_float),
+                                                                              ("flags", C.c_uint32),
+                                                                              ("kv_f32", C.c_int32)]
 
 
 class qh_decoder_state(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("logits", "hidden", "xq", "xd", "stats", "top1_full", "pos", "n_out",
                                           "token", "kcache", "vcache", "status", "history", "history_len",
-                                          "rng_state")]
+                                          "rng_state", "kcache_f32", "vcache_f32")]
 
 
 class qh_sampler_params(C.Structure):
@@ -316,15 +318,20 @@ def _d2h(ptr, nbytes, dtype):
 
 
 class Decoder:
-    """The GPU-resident decoder (qh_decoder_*) over a .qnt tensor set (quanta_cpp_amd.qnt records), uploaded once."""
+    """The GPU-resident decoder (qh_decoder_*) over a .qnt tensor set (quanta_cpp_amd.qnt records), uploaded once.
+    hp.tied_embeddings false takes lm_head.weight as the LM head, hp.flags carries FLAG_HADAMARD_DOWN, and kv_f32
+    keeps an f32 KV cache (Model::load's kv_f16 = false, model.cpp:10, 96-104)."""
 
-    def __init__(self, hp, tensors: dict, ctx_len: int | None = None, device="cuda"):
+    def __init__(self, hp, tensors: dict, ctx_len: int | None = None, device="cuda", kv_f32: bool = False):
         torch = _torch()
         self.hp = hp
+        self.kv_f32 = bool(kv_f32)
         names = ["model.embed_tokens.weight", "model.norm.weight"]
         for l in range(hp.n_layers):
             names += [f"model.layers.{l}.{n}" for n in LAYER_ORDER]
         names += ["quanta.head_q4", "quanta.head_err"]
+        if not getattr(hp, "tied_embeddings", True):
+            names.append("lm_head.weight")
         offs, total = [], 0
         for n in names:
             offs.append(total)
@@ -344,7 +351,8 @@ class Decoder:
             arr[i] = qh_tensor(0, 0, 0, None) if t is None else qh_tensor(t.dtype, t.rows, t.cols, base + o)
         self._tensors = arr
         self.desc = qh_model_desc(hp.vocab_size, hp.dim, hp.n_layers, hp.n_heads, hp.n_kv_heads, hp.head_dim,
-                                  hp.ffn_dim, ctx_len or hp.max_seq, int(hp.qkv_bias), hp.rope_theta, hp.norm_eps)
+                                  hp.ffn_dim, ctx_len or hp.max_seq, int(hp.qkv_bias), hp.rope_theta, hp.norm_eps,
+                                  int(getattr(hp, "flags", 0)), int(self.kv_f32))
         h = C.c_void_p()
         _check(lib().qh_decoder_create(C.byref(self.desc), arr, len(names), C.byref(h)))
         self.h = h
@@ -421,9 +429,14 @@ class Decoder:
         return int(_d2h(self.views.status, 4, np.int32)[0])
 
     def kv(self, layer: int, n_pos: int):
-        """The f16 KV cache bits of one layer, positions [0, n_pos): (k, v) as uint16 [n_pos][n_kv_heads*head_dim]."""
+        """The KV cache of one layer, positions [0, n_pos): (k, v) [n_pos][n_kv_heads*head_dim], as uint16 f16 bits,
+        or float32 with kv_f32."""
         kvd = self.hp.n_kv_heads * self.hp.head_dim
         ctx = self.desc.ctx_len
+        if self.kv_f32:  # the reference's layout, [ctx][kv_dim] per layer
+            off = 4 * layer * ctx * kvd
+            return (_d2h(self.views.kcache_f32 + off, 4 * n_pos * kvd, np.float32).reshape(n_pos, kvd),
+                    _d2h(self.views.vcache_f32 + off, 4 * n_pos * kvd, np.float32).reshape(n_pos, kvd))
         # K is stored in chunks of 8 dimensions, [n_kv_heads][head_dim / 8][ctx][8]
         rawk = _d2h(self.views.kcache + 2 * layer * ctx * kvd, 2 * ctx * kvd, np.uint16)
         k = np.ascontiguousarray(rawk.reshape(kvd // 8, ctx, 8)[:, :n_pos].transpose(1, 0, 2).reshape(n_pos, kvd))

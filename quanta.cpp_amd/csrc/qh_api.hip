@@ -356,7 +356,12 @@ int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_t
         (hp->head_dim != 64 && hp->head_dim != 128) || hp->n_heads * hp->head_dim != D || hp->ctx_len <= 0 ||
         hp->ctx_len > 8192 || hp->vocab_size <= 0)
         return fail(QH_ERR_SHAPE, "qh_decoder_create: unsupported model shape");  // as model.cpp:39-46
-    if (n_tensors != 2 + 12 * L + 2) return fail(QH_ERR_ARG, "qh_decoder_create: %d tensors, needs %d", n_tensors, 4 + 12 * L);
+    if (n_tensors != 4 + 12 * L && n_tensors != 5 + 12 * L)
+        return fail(QH_ERR_ARG, "qh_decoder_create: %d tensors, needs %d or %d", n_tensors, 4 + 12 * L, 5 + 12 * L);
+    if (hp->flags & ~QH_FLAG_HADAMARD_DOWN) return fail(QH_ERR_ARG, "qh_decoder_create: unknown flags %#x", hp->flags);
+    if ((hp->flags & QH_FLAG_HADAMARD_DOWN) && hp->ffn_dim % 256 != 0)
+        return fail(QH_ERR_SHAPE, "qh_decoder_create: hadamard flag needs ffn_dim %% 256 == 0");  // as model.cpp:39-42
+    if (hp->kv_f32 != 0 && hp->kv_f32 != 1) return fail(QH_ERR_ARG, "qh_decoder_create: kv_f32 = %d", hp->kv_f32);
     const int kvd = hp->n_kv_heads * hp->head_dim, F = hp->ffn_dim;
     auto want = [&](int i, int rows, int cols, bool quant, const char* what) -> int {
         const qh_tensor& t = tensors[i];
@@ -383,11 +388,19 @@ int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_t
             if (int rc = want(b + j, rows[j], cols[j], quant[j], "layer tensor")) return rc;
         }
     }
+    // the LM head: lm_head.weight when untied (model.cpp:16), Q8_0 or Q4_0, else the embedding
+    const bool untied = n_tensors == 5 + 12 * L && tensors[4 + 12 * L].data;
+    if (untied && (tensors[4 + 12 * L].dtype != QH_Q8_0 && tensors[4 + 12 * L].dtype != QH_Q4_0))
+        return fail(QH_ERR_DTYPE, "qh_decoder_create: lm_head must be q8_0 or q4_0");
+    if (untied)
+        if (int rc = want(4 + 12 * L, hp->vocab_size, D, true, "lm_head")) return rc;
+    const int lm_dtype = untied ? tensors[4 + 12 * L].dtype : QH_Q8_0;
     const qh_tensor& h4 = tensors[2 + 12 * L];
     const qh_tensor& he = tensors[3 + 12 * L];
     if (h4.data || he.data) {
-        if (h4.dtype != QH_Q4_0 || he.dtype != QH_F16 || h4.rows != hp->vocab_size || h4.cols != D ||
-            he.rows != hp->vocab_size || he.cols != D / QH_QK || !h4.data || !he.data || !head_shape_supported(D))
+        if (h4.dtype != QH_Q4_0 || he.dtype != QH_F16 || lm_dtype != QH_Q8_0 || h4.rows != hp->vocab_size ||
+            h4.cols != D || he.rows != hp->vocab_size || he.cols != D / QH_QK || !h4.data || !he.data ||
+            !head_shape_supported(D))
             return fail(QH_ERR_SHAPE, "qh_decoder_create: bad shortlist head tensors");  // as model.cpp:49-58
     }
     if (int rc = qh_init_current()) return rc;

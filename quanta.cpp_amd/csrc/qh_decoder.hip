@@ -1127,6 +1127,177 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     }
 }
 
+// Attention over an f32 KV cache (the reference's --kv-f32, model.cpp:96-104, 197-204: the cache keeps k / v as
+// computed, no f16 rounding), laid out as the reference keeps it, [ctx][n_kv * head_dim] per layer. One 256-thread
+// workgroup per (query head, token of the chunk), prefill and decode alike: the chunk's K / V rows 0..t are rebuilt
+// from the projections (bias, RoPE) in LDS, so no workgroup reads a cache row another one writes; scores
+// s = fma(q_i, k_i, s) in dimension order, * 1 / sqrt(head_dim); max; glibc expf; the sum in position order (four
+// segments with candidate starts, as attention_kernel); normalise; out_i = fma(a_j, v_ji, out_i) in position order
+// over V rows staged in LDS; the output quantized per 32-block (model.cpp:115-137, ops_ref.cpp:201-226).
+template <int HD>
+__global__ __launch_bounds__(256) void attention_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv,
+    const float* __restrict__ cs, const int* __restrict__ pos_dev, int ctx, int n_heads, int n_kv,
+    float* __restrict__ kc, float* __restrict__ vc, int8_t* __restrict__ oq, float* __restrict__ od,
+    int* __restrict__ status) {
+    constexpr int HALF = HD / 2, C4 = HD / 4;
+    constexpr int kVR = 16384 / HD;  // V rows per LDS stage (64 KB)
+    __shared__ __align__(16) float att[kMaxCtx + kChainPad];
+    __shared__ __align__(16) float vst[kVR * HD];
+    __shared__ __align__(16) float kloc[kChunk * HD];
+    __shared__ __align__(16) float vloc[kChunk * HD];
+    __shared__ __align__(16) float qs[HD];
+    __shared__ float red[4];
+    __shared__ float sum_sh;
+    __shared__ uint64_t exptab[32];
+    __shared__ SegShared ssh;
+    ExpTab et;
+    et.load();
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos0 = *pos_dev, pos = pos0 + t, nrows = pos + 1;
+    if (pos >= ctx || pos0 < 0) {  // uniform: a step past the context touches no cache row
+        if (tid == 0 && h == 0) atomicOr(status, kStatusCtx);
+        return;
+    }
+    const int qd = n_heads * HD, kvd = n_kv * HD, group = n_heads / n_kv, kvh = h / group;
+    // add_bias, then rope: a * c - b * s and b * c + a * s with the reference build's contraction
+    for (int e = tid; e < (t + 1) * HALF; e += 256) {
+        const int r = e / HALF, i = e % HALF;
+        const float* row = k + (size_t)r * kvd + kvh * HD;
+        float a = row[i], b = row[i + HALF];
+        if (bk) {
+            a = a + bk[kvh * HD + i];
+            b = b + bk[kvh * HD + i + HALF];
+        }
+        const float* crow = cs + (size_t)(pos0 + r) * HD;
+        kloc[r * HD + i] = __builtin_fmaf(a, crow[2 * i], -(b * crow[2 * i + 1]));
+        kloc[r * HD + i + HALF] = __builtin_fmaf(b, crow[2 * i], a * crow[2 * i + 1]);
+    }
+    for (int e = tid; e < (t + 1) * HD; e += 256) {
+        const int r = e / HD, i = e % HD;
+        const float x = v[(size_t)r * kvd + kvh * HD + i];
+        vloc[e] = bv ? x + bv[kvh * HD + i] : x;
+    }
+    if (tid < HALF) {
+        const float* row = q + (size_t)t * qd + h * HD;
+        float a = row[tid], b = row[tid + HALF];
+        if (bq) {
+            a = a + bq[h * HD + tid];
+            b = b + bq[h * HD + tid + HALF];
+        }
+        const float* crow = cs + (size_t)pos * HD;
+        qs[tid] = __builtin_fmaf(a, crow[2 * tid], -(b * crow[2 * tid + 1]));
+        qs[tid + HALF] = __builtin_fmaf(b, crow[2 * tid], a * crow[2 * tid + 1]);
+    }
+    et.store(exptab);
+    __syncthreads();
+    if (h % group == 0)
+        for (int i = tid; i < HD; i += 256) {
+            kc[(size_t)pos * kvd + kvh * HD + i] = kloc[t * HD + i];
+            vc[(size_t)pos * kvd + kvh * HD + i] = vloc[t * HD + i];
+        }
+    // scores (model.cpp:122-125): cached rows below pos0 from the cache, the chunk's rows from LDS
+    const float scale = 1.0f / __builtin_sqrtf((float)HD);
+    const float4* q4 = reinterpret_cast<const float4*>(qs);
+    float mx = -__builtin_inff();
+    for (int j = tid; j < nrows; j += 256) {
+        const float* kr = j < pos0 ? kc + (size_t)j * kvd + kvh * HD : kloc + (j - pos0) * HD;
+        float sc = 0.0f;
+#pragma unroll 4
+        for (int c = 0; c < C4; ++c) {
+            const float4 kk = reinterpret_cast<const float4*>(kr)[c], qq = q4[c];
+            sc = __builtin_fmaf(qq.x, kk.x, sc);
+            sc = __builtin_fmaf(qq.y, kk.y, sc);
+            sc = __builtin_fmaf(qq.z, kk.z, sc);
+            sc = __builtin_fmaf(qq.w, kk.w, sc);
+        }
+        const float a = sc * scale;
+        att[j] = a;
+        mx = a > mx ? a : mx;
+    }
+    mx = wave_max_sel(mx);  // the maximum does not depend on the order of comparison
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = red[0];
+    for (int w = 1; w < 4; ++w) mx = red[w] > mx ? red[w] : mx;
+    // exp, with each lane's exact partial sums below the segment starts; the sum in position order (ops_ref.cpp:216-226)
+    const bool seg = nrows >= 128;  // uniform; shorter rows keep the single chain
+    const int Ls = (nrows / 4) & ~15;
+    const Segs4 sg{(nrows - 3 * Ls) & ~15, Ls, nrows};
+    double p1 = 0.0, p2 = 0.0, p3 = 0.0;
+    for (int j = tid; j < nrows; j += 256) {
+        const float e = dev_expf(att[j] - mx, exptab);
+        att[j] = e;
+        p1 += j < sg.start(1) ? (double)e : 0.0;
+        p2 += j < sg.start(2) ? (double)e : 0.0;
+        p3 += j < sg.start(3) ? (double)e : 0.0;
+    }
+    if (seg) seg_partials(ssh, p1, p2, p3);
+    __syncthreads();
+    auto add = [](float acc, float a) { return acc + a; };
+    float sum;
+    if (seg) {
+        sum = seg_chain_run(ssh, [&](int kk, float s0) { return lds_chain(att + sg.start(kk), sg.len(kk), add, s0); });
+    } else {
+        if (tid == 0) sum_sh = lds_chain(att, nrows, add);
+        __syncthreads();
+        sum = sum_sh;
+    }
+    const float inv = 1.0f / sum;
+    for (int j = tid; j < nrows; j += 256) att[j] = att[j] * inv;
+    // out_i = sum_j a_j * v_ji (model.cpp:131-135): thread i per dimension, V rows staged in LDS
+    float acc = 0.0f;
+    for (int s0 = 0; s0 < nrows; s0 += kVR) {
+        const int sn = min(nrows, s0 + kVR);
+        __syncthreads();  // the weights are final, the previous stage is consumed
+        for (int e = tid; e < (sn - s0) * C4; e += 256) {
+            const int r = s0 + e / C4, c = e % C4;
+            const float* src = r < pos0 ? vc + (size_t)r * kvd + kvh * HD : vloc + (r - pos0) * HD;
+            reinterpret_cast<float4*>(vst + (r - s0) * HD)[c] = reinterpret_cast<const float4*>(src)[c];
+        }
+        __syncthreads();
+        if (tid < HD)
+            for (int j = s0; j < sn; ++j) acc = __builtin_fmaf(att[j], vst[(j - s0) * HD + tid], acc);
+    }
+    if (tid < HD) {  // quantize_q8 of the attention output
+        const int col = h * HD + (tid & ~31);
+        quant_block32(acc, oq + (size_t)t * qd + col, od + (size_t)t * (qd / QK) + col / QK);
+    }
+}
+
+// h = g / (1 + expf(-g)) * u (ops_ref.cpp:243-248) over a 256-value block, then the block's Walsh-Hadamard transform
+// (FLAG_HADAMARD_DOWN, model.cpp:219, 424: fwht_blocks, ops_ref.cpp:228-241: butterflies v[j] = a + c, v[j + h] = a - c
+// for h = 1, 2, .., 128, then * 1 / sqrt(256)) and the quantization of its 8 32-blocks for the down projection. Each
+// butterfly adds or subtracts the same two values as the reference's loop, so the result does not depend on the
+// order the butterflies of a stage run in. Grid (ffn_dim / 256, tokens).
+__global__ __launch_bounds__(256) void swiglu_fwht_quant_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                                int F, int8_t* __restrict__ oq, float* __restrict__ od) {
+    __shared__ float vb[256];
+    const int tid = threadIdx.x;
+    const size_t b0 = (size_t)blockIdx.y * F + (size_t)blockIdx.x * 256;
+    const float gv = g[b0 + tid];
+    vb[tid] = gv / (1.0f + dev_expf(-gv)) * u[b0 + tid];
+    __syncthreads();
+    for (int hh = 1; hh < 256; hh *= 2) {
+        const int j = (tid / hh) * 2 * hh + tid % hh;  // butterfly tid (< 128): v[j], v[j + hh]
+        float a = 0.0f, c = 0.0f;
+        if (tid < 128) {
+            a = vb[j];
+            c = vb[j + hh];
+        }
+        __syncthreads();
+        if (tid < 128) {
+            vb[j] = a + c;
+            vb[j + hh] = a - c;
+        }
+        __syncthreads();
+    }
+    const float norm = 1.0f / __builtin_sqrtf(256.0f);
+    const size_t blk = b0 + (tid & ~31);
+    quant_block32(vb[tid] * norm, oq + blk, od + blk / QK);
+}
+
 // ------------------------------------------------------------------------------ decode attention, 16 waves per head
 // Timeline stamps for phase measurements: compiled in only with -DQH_TIMELINE (thread 0 of workgroup 0 records the
 // shader clock at each stamp; qh_timeline_read copies them out).
@@ -1911,8 +2082,12 @@ __global__ __launch_bounds__(256) void history_append_kernel(const int32_t* __re
 struct Decoder {
     qh_model_desc hp;
     std::vector<qh_tensor> t;  // the caller's device tensors, in the qh_decoder_create order
+    const qh_tensor* lmh = nullptr;  // the LM head: the embedding, or lm_head.weight when untied (model.cpp:16)
+    bool hadamard = false;           // FLAG_HADAMARD_DOWN (model_file.h:21)
+    bool kv32 = false;               // an f32 KV cache (Model::load kv_f16 false)
     // device state
-    uint16_t *kc = nullptr, *vc = nullptr;
+    uint16_t *kc = nullptr, *vc = nullptr;  // f16 cache (the default)
+    float *kcf = nullptr, *vcf = nullptr;   // f32 cache, [n_layers][ctx][kv_dim] each
     float* cs = nullptr;
     float *x = nullptr, *o = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *g = nullptr, *u = nullptr,
           *hidden = nullptr;
@@ -2106,6 +2281,20 @@ hipError_t residual(Decoder* d, const qh_tensor& W, const int8_t* xq, const floa
     return hipGetLastError();
 }
 
+// The down projection's input from gate / up rows g, u of n tokens (ffn values each): SwiGLU and quantization, with
+// the block-256 Walsh-Hadamard transform between them when the model has FLAG_HADAMARD_DOWN (model.cpp:216-220).
+hipError_t swiglu_down_input(Decoder* d, int F, int n, hipStream_t s) {
+    if (d->hadamard) {
+        qh_launch(swiglu_fwht_quant_kernel, dim3((unsigned)(F / 256), (unsigned)n), dim3(256), 0, s, d->g, d->u, F,
+                  d->qb, d->db);
+    } else {
+        const long nblk = (long)n * F / QK;
+        qh_launch(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g, d->u, nblk,
+                  d->qb, d->db);
+    }
+    return hipGetLastError();
+}
+
 hipError_t norm_quant(Decoder* d, const float* w, float* normed, hipStream_t s) {
     by_row_slots(d->hp.dim, [&](auto r) {
         qh_launch((norm_quant_kernel<decltype(r)::value>), dim3(1), dim3(256), 0, s, d->x, w, d->hp.dim,
@@ -2119,7 +2308,7 @@ hipError_t gate_up(Decoder* d, int l, hipStream_t s) {
     const qh_tensor &wg = lt(d, l, L_WG), &wu = lt(d, l, L_WU);
     const int nb = wg.cols / QK;
     const size_t lds = norm_tile_lds(wg.cols, 2 * QK, d->hp.dim);
-    if (d->fuse && wg.dtype == wu.dtype && lds <= kFuseLds) {
+    if (d->fuse && !d->hadamard && wg.dtype == wu.dtype && lds <= kFuseLds) {
         const unsigned grid = (unsigned)(wg.rows / QK);
         NormAct act = make_norm(d, false, lf(d, l, L_FFN_NORM));
         act.tlk = 3;
@@ -2137,10 +2326,7 @@ hipError_t gate_up(Decoder* d, int l, hipStream_t s) {
     QH_TRY(norm_quant(d, lf(d, l, L_FFN_NORM), nullptr, s));
     QH_TRY(launch_gemv(d->g, wg, d->qa, d->da, 0, wg.rows, gemv_plan(wg.dtype, wg.cols, wg.rows), s));
     QH_TRY(launch_gemv(d->u, wu, d->qa, d->da, 0, wu.rows, gemv_plan(wu.dtype, wu.cols, wu.rows), s));
-    const long nblk = wg.rows / QK;
-    qh_launch(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g, d->u,
-                       nblk, d->qb, d->db);
-    return hipGetLastError();
+    return swiglu_down_input(d, wg.rows, 1, s);
 }
 
 hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
@@ -2148,6 +2334,18 @@ hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
     const size_t layer_k = (size_t)hp.ctx_len * hp.n_kv_heads * hp.head_dim;
     const size_t layer_v = (size_t)v_ctx(hp.ctx_len) * hp.n_kv_heads * hp.head_dim;
     const dim3 grid(hp.n_heads, n);
+    if (d->kv32) {  // the f32 cache: prefill and decode alike
+        const size_t layer_kv = (size_t)hp.ctx_len * hp.n_kv_heads * hp.head_dim;
+        if (hp.head_dim == 64)
+            qh_launch((attention_f32_kernel<64>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
+                      bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
+                      d->kcf + l * layer_kv, d->vcf + l * layer_kv, d->qb, d->db, d->status);
+        else
+            qh_launch((attention_f32_kernel<128>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
+                      bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
+                      d->kcf + l * layer_kv, d->vcf + l * layer_kv, d->qb, d->db, d->status);
+        return hipGetLastError();
+    }
     if (n == 1 && hp.head_dim == 64 && d->fuse)  // decode: one 16-wave workgroup per head
         qh_launch((attention_decode_kernel<64>), dim3(hp.n_heads / hp.n_kv_heads, hp.n_kv_heads), dim3(1024), 0,
                            s, d->q, d->k, d->v, d->kc + l * layer_k, d->pos, hp.ctx_len, hp.n_heads / hp.n_kv_heads,
@@ -2205,7 +2403,7 @@ hipError_t decode_layers(Decoder* d, hipStream_t s) {
 // (the matmul launch and swiglu_quant_kernel instead: one launch per operation, different formats or widths, rows
 // not a multiple of 32, unaligned operands).
 bool swiglu_fused(Decoder* d, const qh_tensor& wg, const qh_tensor& wu, int n, hipStream_t s) {
-    if (!d->fuse || wg.dtype != wu.dtype || wg.rows != wu.rows || wg.cols != wu.cols || wg.rows % QK != 0 ||
+    if (!d->fuse || d->hadamard || wg.dtype != wu.dtype || wg.rows != wu.rows || wg.cols != wu.cols || wg.rows % QK != 0 ||
         (wg.dtype != kQ8 && wg.dtype != kQ4) || wg.cols % QK != 0 || wg.cols < 2 * QK)
         return false;
     const uint8_t *qg = quants(wg), *qu = quants(wu);
@@ -2272,9 +2470,7 @@ hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
         if (!swiglu_fused(d, wg, wu, n, s)) {
             const MmOut gu[2] = {{&wg, d->g, wg.rows, 0, wg.rows}, {&wu, d->u, wu.rows, 0, wu.rows}};
             QH_TRY(matmul_group(gu, 2, d->qa, d->da, n, s));
-            const long nblk = (long)n * F / QK;
-            qh_launch(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g,
-                               d->u, nblk, d->qb, d->db);
+            QH_TRY(swiglu_down_input(d, F, n, s));
         }
         QH_TRY(hipGetLastError());
         QH_TRY(launch_matmul(d->o, wd.rows, wd, d->qb, d->db, n, 0, wd.rows, s));
@@ -2317,7 +2513,7 @@ TokenFeedback token_feedback(Decoder* d) {
 
 // advance: a greedy decode step through the shortlist head, whose last kernel then also feeds the token back.
 hipError_t run_head(Decoder* d, int top_k, hipStream_t s, bool advance = false) {
-    const qh_tensor& h8 = d->t[T_EMBED];
+    const qh_tensor& h8 = *d->lmh;
     if (shortlist_on(d, top_k)) {
         qh_head_query q{query_top_k(d, top_k), d->hp.vocab_size, nullptr, 0};
         qh_head_out out{d->logits, d->coarse, d->upper, d->rows, d->stats};
@@ -2342,17 +2538,27 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
     const char* fuse = getenv("QH_DECODER_FUSE");
     d->fuse = !(fuse && strcmp(fuse, "0") == 0);
     d->t.assign(tensors, tensors + n_tensors);
+    const size_t n_lm = T_LAYER0 + (size_t)hp->n_layers * L_COUNT + 2;  // lm_head.weight's slot, when given
+    d->lmh = d->t.size() > n_lm && d->t[n_lm].data ? &d->t[n_lm] : &d->t[T_EMBED];
+    d->hadamard = (hp->flags & QH_FLAG_HADAMARD_DOWN) != 0;
+    d->kv32 = hp->kv_f32 != 0;
     const int D = hp->dim, F = hp->ffn_dim, V = hp->vocab_size, hd = hp->head_dim;
     const size_t kvd = (size_t)hp->n_kv_heads * hd;
     const size_t kv_bytes = (size_t)hp->n_layers * hp->ctx_len * kvd * 2;
     const size_t v_bytes = (size_t)hp->n_layers * v_ctx(hp->ctx_len) * kvd * 2;
+    const size_t kv32_bytes = (size_t)hp->n_layers * hp->ctx_len * kvd * 4;
     const int wide = D > F ? D : F;
     hipError_t e = hipSuccess;
     auto A = [&](void** p, size_t b) {
         if (e == hipSuccess) e = dalloc(d, p, b);
     };
-    A((void**)&d->kc, kv_bytes);
-    A((void**)&d->vc, v_bytes);
+    if (d->kv32) {
+        A((void**)&d->kcf, kv32_bytes);
+        A((void**)&d->vcf, kv32_bytes);
+    } else {
+        A((void**)&d->kc, kv_bytes);
+        A((void**)&d->vc, v_bytes);
+    }
     A((void**)&d->cs, sizeof(float) * (size_t)hp->ctx_len * hd);
     A((void**)&d->x, sizeof(float) * kChunk * D);
     A((void**)&d->o, sizeof(float) * kChunk * D);
@@ -2535,6 +2741,8 @@ void decoder_views(Decoder* d, qh_decoder_state* v) {
     v->token = d->tokens;
     v->kcache = d->kc;
     v->vcache = d->vc;
+    v->kcache_f32 = d->kcf;
+    v->vcache_f32 = d->vcf;
     v->status = d->status;
     v->history = d->hist;
     v->history_len = d->hist_len;

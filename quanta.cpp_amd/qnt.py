@@ -209,8 +209,7 @@ LAYER_TENSORS = ("input_layernorm.weight", "self_attn.q_proj.weight", "self_attn
 def check_model(hp: HParams, tensors: dict) -> None:
     """Model::load's checks after the file is read (model.cpp:13-58), in its order and with its messages: every tensor
     the forward reads is present (q/k/v biases only with qkv_bias; lm_head.weight only without tied embeddings), the
-    Hadamard flag's width rule, the head configuration, and the shortlist tensors' types and shapes. Two more refusals
-    mark what the GPU decoder does not run: an untied LM head and Hadamard-rotated down projections."""
+    Hadamard flag's width rule, the head configuration, and the shortlist tensors' types and shapes."""
     def get(name):
         if name not in tensors:
             raise QntError(f"missing tensor: {name}")
@@ -235,10 +234,6 @@ def check_model(hp: HParams, tensors: dict) -> None:
               he.cols == lm_head.cols // 32)
         if not ok:
             raise QntError("bad shortlist head tensors")
-    if not hp.tied_embeddings:
-        raise QntError("untied lm_head.weight: the GPU decoder runs tied embeddings only")
-    if hp.flags & FLAG_HADAMARD_DOWN:
-        raise QntError("Hadamard-rotated down projections: not supported by the GPU decoder")
 
 
 def load_model(path: str):
@@ -254,7 +249,9 @@ def _f32(a) -> np.ndarray:
 
 
 def synthetic_q4mix(seed: int, hp: HParams | None = None, shortlist: bool = True) -> dict[str, TensorRec]:
-    """The random-init q4mix model (tensor name -> record). Sub-seeds: seed * 1000 + a fixed index per tensor."""
+    """The random-init q4mix model (tensor name -> record). Sub-seeds: seed * 1000 + a fixed index per tensor. With
+    hp.tied_embeddings false an lm_head.weight (Q8_0 [vocab][dim], its own seed) is the LM head, and the shortlist copy
+    is made from it; hp.flags (FLAG_HADAMARD_DOWN) changes the forward, not the tensors."""
     hp = hp or HParams()
     D, F, V = hp.dim, hp.ffn_dim, hp.vocab_size
     qd, kvd = hp.n_heads * hp.head_dim, hp.n_kv_heads * hp.head_dim
@@ -280,8 +277,12 @@ def synthetic_q4mix(seed: int, hp: HParams | None = None, shortlist: bool = True
         t[p + "mlp.gate_proj.weight"] = TensorRec(Q4_0, F, D, synth.q4_tensor(s(b + 5), F, D))
         t[p + "mlp.up_proj.weight"] = TensorRec(Q4_0, F, D, synth.q4_tensor(s(b + 6), F, D))
         t[p + "mlp.down_proj.weight"] = TensorRec(Q4_0, D, F, synth.q4_tensor(s(b + 7), D, F))
+    head = embed
+    if not hp.tied_embeddings:
+        head = synth.q8_tensor(s(1), V, D)
+        t["lm_head.weight"] = TensorRec(Q8_0, V, D, head)
     if shortlist:
-        head4, err = synth.shortlist_copy(embed, V, D)
+        head4, err = synth.shortlist_copy(head, V, D)
         t["quanta.head_q4"] = TensorRec(Q4_0, V, D, head4)
         t["quanta.head_err"] = TensorRec(F16, V, D // 32, err.view(np.uint8).reshape(-1))
     return t

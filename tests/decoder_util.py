@@ -8,8 +8,22 @@ def qnt_module():
     return qnt
 
 
-def oracle_decoder(oracle, hp, tensors, ctx_len=None):
-    return oracle.decoder_for(hp, tensors, ctx_len)
+def oracle_decoder(oracle, hp, tensors, ctx_len=None, kv_f32=False):
+    return oracle.decoder_for(hp, tensors, ctx_len, kv_f32=kv_f32)
+
+
+def option_model(g, name):
+    """The model of one variant of tests/golden/e2e_options.npz: (HParams, tensors, kv_f32)."""
+    qnt = qnt_module()
+    hp = qnt.HParams(vocab_size=4096, n_layers=2, tied_embeddings=bool(g[f"{name}_tied"]),
+                     flags=int(g[f"{name}_flags"]))
+    return hp, qnt.synthetic_q4mix(int(g[f"{name}_seed"]), hp), not bool(g[f"{name}_kv_f16"])
+
+
+def logits_sha256(logits):
+    import hashlib
+    import numpy as np
+    return hashlib.sha256(np.ascontiguousarray(logits, np.float32).view(np.uint8).tobytes()).hexdigest()
 
 
 def must_window(hist, params):

@@ -22,7 +22,11 @@ build, so it runs only where the reference tree is mounted; the .npz files are d
                   and "gen" (`quanta gen --top-k 20 --repeat-penalty 1.1`: top-k 20 queries with the history as
                   must ids, greedy picks): 256 ids each and the 8-bit head rows of the forward before each pick.
 
-Usage: python tests/golden/make_e2e_golden.py [--small-only | --full-only | --sampled-only]
+  e2e_options.npz the reference's load-time options on 2-layer, vocab-4096 models of the same widths: an untied LM
+                  head, the Hadamard-rotated down projection, the f32 KV cache and all three together; per variant the
+                  gen flow's states after every forward (as e2e_small) and one full-head forward's logits digest.
+
+Usage: python tests/golden/make_e2e_golden.py [--small-only | --full-only | --sampled-only | --options-only]
 """
 import ctypes as C
 import hashlib
@@ -101,6 +105,54 @@ def make_small(qnt, L):
     np.savez_compressed(os.path.join(HERE, "e2e_small.npz"), seed=np.int32(7), vocab=np.int32(hp.vocab_size),
                         n_layers=np.int32(hp.n_layers), prompt=ids, out=out, head_rows=rows, hidden=hidden, hq=hq, hd=hd)
     os.remove(path)
+
+
+# The reference's load-time options on a 2-layer, vocabulary-4096 model of the Qwen2.5-0.5B widths (ffn 4864, a
+# multiple of 256): an untied LM head (lm_head.weight, model.cpp:16), the Hadamard-rotated down projection
+# (FLAG_HADAMARD_DOWN, model.cpp:219, 424; ops_ref.cpp:228-241), the f32 KV cache (--kv-f32, model.cpp:96-104,
+# 197-204), and all three together; (name, seed, tied, flags, kv_f16).
+OPTIONS = (("untied", 17, False, 0, True), ("hadamard", 19, True, 1, True), ("kv_f32", 23, True, 0, False),
+           ("all", 29, False, 1, False))
+
+
+def make_options(qnt, L):
+    """e2e_options.npz: per variant, the gen flow (batched prefill of a 40-id prompt, 16 greedy shortlist steps) with
+    the final normed hidden state, its quantization and the head rows after every forward, then one full-head
+    forward's logits (their sha256)."""
+    out = {}
+    for name, seed, tied, flags, kv_f16 in OPTIONS:
+        hp = qnt.HParams(vocab_size=4096, n_layers=2, tied_embeddings=tied, flags=flags)
+        path = f"/tmp/quanta_e2e_{name}.qnt"
+        qnt.write_qnt(path, hp, qnt.synthetic_q4mix(seed, hp))
+        m = oracle.ref.load_model(path, 4096, 8, kv_f16=kv_f16)
+        ids = np.random.default_rng(seed + 1).integers(0, hp.vocab_size, 40).astype(np.int32)
+        n_gen = 16
+        D = hp.dim
+        hidden = np.zeros((n_gen + 1, D), np.float32)
+        hq = np.zeros((n_gen + 1, D), np.int8)
+        hd = np.zeros((n_gen + 1, D // 32), np.float32)
+        logits = np.zeros(hp.vocab_size, np.float32)
+        toks = np.zeros(n_gen, np.int32)
+        rows = np.zeros(n_gen + 1, np.int32)
+        rows[0] = L.ref_model_forward_batch(m, ids.ctypes.data, len(ids), 0, 1, logits.ctypes.data,
+                                            hidden[0].ctypes.data, hq[0].ctypes.data, hd[0].ctypes.data)
+        pos = len(ids)
+        for s in range(n_gen):
+            tok = int(np.argmax(logits))
+            toks[s] = tok
+            rows[s + 1] = L.ref_model_forward(m, tok, pos, 1, logits.ctypes.data, hidden[s + 1].ctypes.data,
+                                              hq[s + 1].ctypes.data, hd[s + 1].ctypes.data)
+            pos += 1
+        tok = int(np.argmax(logits))
+        full_rows = L.ref_model_forward(m, tok, pos, 0, logits.ctypes.data, None, None, None)
+        assert full_rows == hp.vocab_size
+        oracle.ref.free_model(m)
+        os.remove(path)
+        out.update({f"{name}_seed": np.int32(seed), f"{name}_tied": np.int32(tied), f"{name}_flags": np.int32(flags),
+                    f"{name}_kv_f16": np.int32(kv_f16), f"{name}_prompt": ids, f"{name}_out": toks,
+                    f"{name}_head_rows": rows, f"{name}_hidden": hidden, f"{name}_hq": hq, f"{name}_hd": hd,
+                    f"{name}_full_token": np.int32(tok), f"{name}_full_logits_sha256": np.array(digest(logits))})
+    np.savez_compressed(os.path.join(HERE, "e2e_options.npz"), variants=np.array([o[0] for o in OPTIONS]), **out)
 
 
 def state_digest(hidden, hq, hd) -> np.ndarray:
@@ -185,9 +237,13 @@ def main():
         raise SystemExit("oracle/_ref/libquanta_ref.so is missing: run `make -C oracle ref`")
     qnt = load_pkg()
     L = bind(oracle.ref.lib)
+    if "--options-only" in sys.argv:
+        make_options(qnt, L)
+        return
     if "--sampled-only" not in sys.argv:
         if "--full-only" not in sys.argv:
             make_small(qnt, L)
+            make_options(qnt, L)
         if "--small-only" not in sys.argv:
             make_full(qnt, L)
     if "--small-only" not in sys.argv and "--full-only" not in sys.argv:

@@ -149,3 +149,44 @@ def test_forced_allocation_failure(qh):
         assert L.qh_malloc(C.byref(p), 0) == 0  # an empty allocation is no allocation: nothing to fail
     finally:
         L.qh_fault_alloc(-1)
+
+
+def _desc_and_tensors(qh, flags=0, kv_f32=0, ffn=512, lm=None, shortlist=True):
+    """A one-layer model descriptor and tensor list (descriptors at made-up, aligned addresses: only the host checks
+    of qh_decoder_create may run on them)."""
+    V, D, kvd, F = 1024, 256, 64, ffn
+    desc = qh.qh_model_desc(V, D, 1, 4, 1, 64, F, 128, 0, 1e6, 1e-6, flags, kv_f32)
+    addr = iter(range(1 << 20, 1 << 30, 1 << 16))
+    t = lambda dt, r, c: qh.qh_tensor(dt, r, c, next(addr))
+    none = qh.qh_tensor(0, 0, 0, None)
+    ts = [t(qh.Q8_0, V, D), t(qh.F32, 1, D), t(qh.F32, 1, D), t(qh.Q4_0, D, D), t(qh.Q4_0, kvd, D),
+          t(qh.Q4_0, kvd, D), t(qh.Q4_0, D, D), none, none, none, t(qh.F32, 1, D), t(qh.Q4_0, F, D),
+          t(qh.Q4_0, F, D), t(qh.Q4_0, D, F)]
+    ts += [t(qh.Q4_0, V, D), t(qh.F16, V, D // 32)] if shortlist else [none, none]
+    if lm is not None:
+        ts.append(t(*lm))
+    return desc, (qh.qh_tensor * len(ts))(*ts), len(ts)
+
+
+@pytest.mark.parametrize("case,code,msg", [
+    (dict(flags=2), "ERR_ARG", b"unknown flags"),
+    (dict(flags=1, ffn=480), "ERR_SHAPE", b"ffn_dim % 256"),  # as model.cpp:39-42
+    (dict(kv_f32=2), "ERR_ARG", b"kv_f32"),
+    (dict(lm=(1, 1024, 256)), "ERR_DTYPE", b"lm_head must be"),
+    (dict(lm=(2, 1000, 256)), "ERR_SHAPE", b"lm_head is 1000 x 256"),
+    (dict(lm=(3, 1024, 256)), "ERR_SHAPE", b"bad shortlist head tensors"),  # Q8_0 with the shortlist (model.cpp:51)
+])
+def test_decoder_create_option_checks(qh, case, code, msg):
+    """qh_decoder_create's checks of the load-time options (flags, kv_f32, an untied lm_head.weight), refused on the
+    host before any device work."""
+    desc, ts, n = _desc_and_tensors(qh, **case)
+    h = C.c_void_p()
+    rc = qh.lib().qh_decoder_create(C.byref(desc), ts, n, C.byref(h))
+    assert rc == getattr(qh, code) and msg in qh.lib().qh_last_error() and not h.value
+
+
+def test_decoder_create_tensor_count(qh):
+    desc, ts, n = _desc_and_tensors(qh, lm=(2, 1024, 256))
+    h = C.c_void_p()
+    assert qh.lib().qh_decoder_create(C.byref(desc), ts, n - 2, C.byref(h)) == qh.ERR_ARG
+    assert b"needs 16 or 17" in qh.lib().qh_last_error()

@@ -1,6 +1,8 @@
 """Pins the oracle's decoder restatement (oracle/quanta_oracle.c, qo_decoder_*) bit for bit: against the golden
-states the reference engine wrote for a small synthetic model (tests/golden/e2e_small.npz), against the reference
-build itself where it is present (oracle/_ref), and its float->half rounding against numpy's. No GPU."""
+states the reference engine wrote for a small synthetic model (tests/golden/e2e_small.npz) and for its load-time
+options (an untied LM head, the Hadamard-rotated down projection, the f32 KV cache: tests/golden/e2e_options.npz),
+against the reference build itself where it is present (oracle/_ref), and its float->half rounding against numpy's.
+No GPU."""
 import ctypes as C
 import os
 
@@ -8,7 +10,7 @@ import numpy as np
 import pytest
 
 from conftest import GOLDEN, bits
-from decoder_util import oracle_decoder, qnt_module
+from decoder_util import logits_sha256, option_model, oracle_decoder, qnt_module
 
 
 def test_f32_to_f16_rounding(oracle):
@@ -126,3 +128,27 @@ def test_oracle_second_turn_prefill_equals_reference_build(oracle, ref, tmp_path
         r = dec.forward_batch(second, pos, top_k=1)
         assert r["rows"] == rows and (bits(r["hidden"]) == bits(h)).all() and (bits(r["logits"]) == bits(lg)).all()
         ref.ref_model_free(m)
+
+
+@pytest.mark.parametrize("name", ["untied", "hadamard", "kv_f32", "all"])
+def test_oracle_decoder_options_match_golden(oracle, name):
+    """The gen flow of each load-time option: every forward's final normed state, quantization, head rows and token
+    as the reference wrote them, then one full-head forward's logits."""
+    g = np.load(os.path.join(GOLDEN, "e2e_options.npz"), allow_pickle=False)
+    hp, tens, kv_f32 = option_model(g, name)
+    dec = oracle_decoder(oracle, hp, tens, ctx_len=4096, kv_f32=kv_f32)
+    prompt = g[f"{name}_prompt"]
+    r = dec.forward_batch(prompt, 0, top_k=1)
+    pos = len(prompt)
+    for s in range(len(g[f"{name}_out"]) + 1):
+        assert (bits(r["hidden"]) == bits(g[f"{name}_hidden"][s])).all(), (name, s)
+        assert (r["hq"] == g[f"{name}_hq"][s]).all() and (bits(r["hd"]) == bits(g[f"{name}_hd"][s])).all(), (name, s)
+        assert r["rows"] == int(g[f"{name}_head_rows"][s]), (name, s)
+        tok = oracle.argmax(r["logits"])
+        if s < len(g[f"{name}_out"]):
+            assert tok == int(g[f"{name}_out"][s]), (name, s)
+            r = dec.forward(tok, pos, top_k=1)
+            pos += 1
+    assert tok == int(g[f"{name}_full_token"])
+    r = dec.forward(tok, pos, top_k=0)
+    assert logits_sha256(r["logits"]) == str(g[f"{name}_full_logits_sha256"])
