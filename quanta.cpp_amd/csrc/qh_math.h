@@ -10,6 +10,9 @@
 // the method's published ones (relative error 1.69 * 2^-34), pre-divided by 32, 32^2 and 32^3. Which products the
 // host build fuses into multiply-adds is selected by QH_EXPF_FUSED (see tests/cpp/expf_exhaustive.cpp, which
 // compares every one of the 2^32 inputs with the host's expf).
+// Source of the method: ARM optimized-routines (github.com/ARM-software/optimized-routines, math/expf.c and
+// math/exp2f_data.c), licensed MIT OR Apache-2.0 WITH LLVM-exception; the code here is written from that published
+// description, and the table holds the values 2^(i/32) themselves.
 #pragma once
 
 #include <stdint.h>
