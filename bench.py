@@ -586,8 +586,8 @@ def main():
     ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end prefill + decode measurement")
     ap.add_argument("--only", choices=["e2e", "roofline", "prefill", "sampling", "head", "stages"],
                     help="one measurement alone (for counter runs): e2e = --e2e-only; roofline = a 256 MiB copy "
-                         "(counter calibration) then the Q4_0 GEMV rotation; prefill = Q4_0 4864x896 at M = 512, then "
-                         "9728x896 (the decoder's gate + up rows) and 896x4864 (down) at M = 32")
+                         "(counter calibration) then the Q4_0 GEMV rotation; prefill = Q4_0 4864x896 and 896x4864 at M = 512, "
+                         "then 9728x896 (the decoder's gate + up rows) and 896x4864 (down) at M = 32")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this path runs on a single MI355X "
@@ -611,6 +611,7 @@ def main():
         return 0
     if args.only == "prefill":
         out = {"q4_prefill_4864x896_M512": rnd(prefill_rotation(qh, synth, torch, 3, 4864, 896, 512, 5, 1))}
+        out["q4_prefill_896x4864_M512"] = rnd(prefill_rotation(qh, synth, torch, 3, 896, 4864, 512, 5, 1))
         out["q4_prefill_9728x896_M32"] = rnd(prefill_rotation(qh, synth, torch, 3, 9728, 896, 32, 5, 1))
         out["q4_prefill_896x4864_M32"] = rnd(prefill_rotation(qh, synth, torch, 3, 896, 4864, 32, 5, 1))
         print(json.dumps(out), flush=True)

@@ -461,15 +461,18 @@ __global__ __launch_bounds__(NS == 0 ? kMmThreads : 2 * kMmThreads) void matmul_
     if (tok < n && r < r1) sg.out[(size_t)tok * sg.ldo + r] = acc;
 }
 
-// Tile variant for batches of 64 tokens and more: a workgroup of 4 waves owns 64 rows x 64 tokens over all of K, in
-// chunks of 8 blocks brought into LDS by coalesced 16-byte loads (a row's chunk is 128 (Q4_0) or 256 (Q8_0) contiguous
-// bytes, a token's 256; 16 rows x 2 lane groups of a half-wave operand read hit 64 distinct banks), double-buffered:
-// the loads of chunk c + 1 are in flight while chunk c is multiplied. Wave (wr, wt) multiplies rows 32 wr .. + 31 by
-// tokens 32 wt .. + 31: per block four MFMAs (2 row tiles x 2 token tiles), each weight operand read once for two
-// token tiles and each activation operand once for two row tiles, and the wave runs the 16 chains of its lanes'
-// outputs in registers (lane l: rows 4 (l / 16) + i of each row tile, token l % 16 of each token tile), so no block
-// sum goes through LDS. Operand loads in MFMA layout (8 bytes per lane from 16 rows) kept the texture-address units
-// busy for most of the register kernel's time at 512 tokens.
+// Tile variant for batches of 128 tokens and more: a workgroup of 4 waves owns 64 rows x TT tokens (TT = 32 or 64)
+// over all of K, in chunks of KC blocks brought into LDS by coalesced 16-byte loads (a row's chunk is KC x 16 (Q4_0) or
+// KC x 32 (Q8_0) contiguous bytes, a token's KC x 32; Q4_0 codes are unpacked to int8 as they are staged, so both
+// formats share the LDS layout and the compute loop), double-buffered with two register sets: the loads of chunk
+// c + 3 are issued as chunk c + 1 is staged. Wave (wr, wt) multiplies rows 32 wr .. + 31 by TT / 2 tokens: per block
+// two MFMAs per 16-token tile (2 row tiles), each weight operand read once for every token tile and each activation
+// operand once for two row tiles, and the wave runs the chains of its lanes' outputs in registers (lane l: rows
+// 4 (l / 16) + i of each row tile, token l % 16 of each token tile), so no block sum goes through LDS. A whole chunk
+// runs straight-line two blocks deep (block b's chains, block b + 1's MFMAs, block b + 2's operand reads). Operand
+// loads in MFMA layout (8 bytes per lane from 16 rows) kept the texture-address units busy for most of the register
+// kernel's time at 512 tokens; here they are busy about a third of the time, and the exact f32 chains (a convert, a
+// scale multiply and an FMA per output and block) and the per-chunk staging and barrier are what is left.
 // Timeline stamps of workgroup 0, wave 0 (compiled in only with -DQH_TIMELINE; qh_timeline_mm_read copies them out).
 #if defined(QH_TIMELINE)
 __device__ uint64_t qh_tl_mm[64];
@@ -482,11 +485,11 @@ __device__ uint64_t qh_tl_mm[64];
     do {              \
     } while (0)
 #endif
-template <int DT, int KC>
+template <int DT, int KC, int TT>
 struct TileRegs {
     static constexpr int kBw = DT == kQ8 ? QK : QK / 2;           // weight bytes per block
     static constexpr int kAu = 64 * KC * kBw / 16 / kMmThreads;  // 16-byte weight units per thread
-    static constexpr int kXu = 64 * KC * QK / 16 / kMmThreads;   // 16-byte activation units per thread
+    static constexpr int kXu = TT * KC * QK / 16 / kMmThreads;   // 16-byte activation units per thread
     static constexpr int kSp = KC / 4;                           // scales per thread and chunk
     uint4 a[kAu];
     uint4 x[kXu];
@@ -494,18 +497,24 @@ struct TileRegs {
     float dx[kSp];     // token tid / 4, blocks kSp (tid % 4) + j of the chunk
 };
 
-template <int DT, int KC>
+// TT: tokens per workgroup, 64 (waves of 32 rows x 32 tokens) or 32 (waves of 32 rows x 16 tokens: twice the
+// workgroups for matrices with few row tiles).
+template <int DT, int KC, int TT>
 __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, const int8_t* __restrict__ xq,
                                                                 const float* __restrict__ xd, int cols, int n,
                                                                 int n_tg) {
-    using R = TileRegs<DT, KC>;
+    static_assert(TT == 64 || TT == 32, "token tile");
+    constexpr int NTS = TT / 32;  // 16-token tiles per wave
+    using R = TileRegs<DT, KC, TT>;
     constexpr int kBw = R::kBw, kSp = R::kSp;
-    constexpr int kArow = KC * kBw + 16, kXrow = KC * QK + 16;  // LDS row strides (bytes)
+    // Weights are staged as int8 codes whatever the format (Q4_0 nibbles are unpacked once, as they are staged, not by
+    // both token waves at every block): LDS row strides in bytes
+    constexpr int kArow = KC * QK + 16, kXrow = KC * QK + 16;
     constexpr int kAupr = KC * kBw / 16, kXupr = KC * QK / 16;  // 16-byte units per row and chunk
     __shared__ __align__(16) uint8_t as[2][64 * kArow];
-    __shared__ __align__(16) int8_t xs[2][64 * kXrow];
+    __shared__ __align__(16) int8_t xs[2][TT * kXrow];
     __shared__ __align__(16) float dws[2][KC][64];  // [block][row], f32
-    __shared__ __align__(16) float dxs[2][KC][64];  // [block][token]
+    __shared__ __align__(16) float dxs[2][KC][TT];  // [block][token]
     const int nb = cols / QK;
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
@@ -519,8 +528,9 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
     const int tg = logical % n_tg;
     const MmSeg sg(segs, rt);
     const int r1 = sg.r1;
-    const int rbase = sg.r0 + rt * 64, tbase = tg * 64;
+    const int rbase = sg.r0 + rt * 64, tbase = tg * TT;
     const size_t wrow_bytes = (size_t)nb * kBw;
+    const bool dx_thread = TT == 64 || tid < 4 * TT;  // threads of a token's scales (wave-uniform)
 
     // Source rows of this thread's staged units; rows and tokens past the end are clamped (loaded, never stored), and
     // byte offsets past the end of a row onto its last unit (blocks no chain adds).
@@ -555,14 +565,27 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
         for (int j = 0; j < kSp; ++j) {
             const int b = min(c0 + sk + j, nb - 1);
             S.dw[j] = dwsrc[b];
-            S.dx[j] = dxsrc[b];
+            if (dx_thread) S.dx[j] = dxsrc[b];
         }
     };
     auto stage = [&](const R& S, int buf) {
 #pragma unroll
         for (int j = 0; j < R::kAu; ++j) {
             const int e = j * kMmThreads + tid;
-            *reinterpret_cast<uint4*>(&as[buf][(e / kAupr) * kArow + (e % kAupr) * 16]) = S.a[j];
+            if (DT == kQ8) {
+                *reinterpret_cast<uint4*>(&as[buf][(e / kAupr) * kArow + (e % kAupr) * 16]) = S.a[j];
+            } else {  // one block: element i < 16 in the low nibble of byte i, element 16 + i in its high nibble
+                const uint32_t w[4] = {S.a[j].x, S.a[j].y, S.a[j].z, S.a[j].w};
+                uint32_t lo[4], hi[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    lo[q] = nibbles_to_i8(w[q] & 0x0F0F0F0Fu);
+                    hi[q] = nibbles_to_i8((w[q] >> 4) & 0x0F0F0F0Fu);
+                }
+                uint8_t* dst = &as[buf][(e / kAupr) * kArow + (e % kAupr) * QK];
+                *reinterpret_cast<uint4*>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                *reinterpret_cast<uint4*>(dst + 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            }
         }
 #pragma unroll
         for (int j = 0; j < R::kXu; ++j) {
@@ -575,59 +598,49 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
             uint32_t h = S.dw[j];
             asm volatile("" : "+v"(h));  // keeps the conversion here (hoisted, it would wait for the next loads)
             dws[buf][sk + j][t] = f16_to_f32((uint16_t)h);
-            dxs[buf][sk + j][t] = S.dx[j];
+            if (dx_thread) dxs[buf][sk + j][t] = S.dx[j];
         }
     };
 
-    float acc[2][2][4];
+    float acc[2][NTS][4];
 #pragma unroll
     for (int rs = 0; rs < 2; ++rs)
 #pragma unroll
-        for (int ts = 0; ts < 2; ++ts)
+        for (int ts = 0; ts < NTS; ++ts)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[rs][ts][i] = 0.0f;
-    const int shift = DT == kQ8 ? 0 : (lq >> 1) * 4;
-    const int aoff_l = DT == kQ8 ? lq * 8 : (lq & 1) * 8;
     // One block's operands (two weight tiles, two token tiles) and its products.
     struct Ops {
-        long a[2], x[2];
+        long a[2], x[NTS];
         float4 dw[2];
-        float dx[2];
+        float dx[NTS];
     };
     auto ld_ops = [&](Ops& o, int buf, int b) {
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs) {
-            o.a[rs] = *reinterpret_cast<const long*>(&as[buf][(wr * 32 + rs * 16 + li) * kArow + b * kBw + aoff_l]);
+            o.a[rs] = *reinterpret_cast<const long*>(&as[buf][(wr * 32 + rs * 16 + li) * kArow + b * QK + lq * 8]);
             o.dw[rs] = *reinterpret_cast<const float4*>(&dws[buf][b][wr * 32 + rs * 16 + 4 * lq]);
         }
 #pragma unroll
-        for (int ts = 0; ts < 2; ++ts) {
-            o.x[ts] = *reinterpret_cast<const long*>(&xs[buf][(wt * 32 + ts * 16 + li) * kXrow + b * QK + lq * 8]);
-            o.dx[ts] = dxs[buf][b][wt * 32 + ts * 16 + li];
+        for (int ts = 0; ts < NTS; ++ts) {
+            o.x[ts] = *reinterpret_cast<const long*>(&xs[buf][(wt * (TT / 2) + ts * 16 + li) * kXrow + b * QK + lq * 8]);
+            o.dx[ts] = dxs[buf][b][wt * (TT / 2) + ts * 16 + li];
         }
     };
-    auto mma = [&](const Ops& o, v4i(&c)[2][2]) {
+    auto mma = [&](const Ops& o, v4i(&c)[2][NTS]) {
 #pragma unroll
-        for (int rs = 0; rs < 2; ++rs) {
-            long a = o.a[rs];
-            if (DT == kQ4) {
-                const uint64_t v = (uint64_t)a;
-                const uint32_t lo = nibbles_to_i8(((uint32_t)v >> shift) & 0x0F0F0F0Fu);
-                const uint32_t hi = nibbles_to_i8(((uint32_t)(v >> 32) >> shift) & 0x0F0F0F0Fu);
-                a = (long)(((uint64_t)hi << 32) | lo);
-            }
+        for (int rs = 0; rs < 2; ++rs)
 #pragma unroll
-            for (int ts = 0; ts < 2; ++ts)
-                c[rs][ts] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, o.x[ts], (v4i){0, 0, 0, 0}, 0, 0, 0);
-        }
+            for (int ts = 0; ts < NTS; ++ts)
+                c[rs][ts] = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[rs], o.x[ts], (v4i){0, 0, 0, 0}, 0, 0, 0);
     };
     // acc = fma(float(s) * dw, dx, acc) (ops_ref.cpp:97-98) for one block
-    auto chain = [&](const Ops& o, const v4i(&c)[2][2]) {
+    auto chain = [&](const Ops& o, const v4i(&c)[2][NTS]) {
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs) {
             const float dwv[4] = {o.dw[rs].x, o.dw[rs].y, o.dw[rs].z, o.dw[rs].w};
 #pragma unroll
-            for (int ts = 0; ts < 2; ++ts)
+            for (int ts = 0; ts < NTS; ++ts)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     acc[rs][ts][i] = __builtin_fmaf((float)c[rs][ts][i] * dwv[i], o.dx[ts], acc[rs][ts][i]);
@@ -637,7 +650,7 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
     // products issued while block b's chains run.
     auto compute = [&](int buf, int nblk) {
         Ops o0, o1;
-        v4i c0[2][2], c1[2][2];
+        v4i c0[2][NTS], c1[2][NTS];
         ld_ops(o0, buf, 0);
         mma(o0, c0);
         int b = 0;
@@ -652,6 +665,25 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
             if (b + 2 < nblk) mma(o0, c0);
         }
         if (b < nblk) chain(o0, c0);
+    };
+    // A whole chunk (KC blocks), straight-line and two blocks deep: while block b's chains run, block b + 1's MFMAs
+    // are in flight and block b + 2's operands are being read, so neither the LDS latency nor the MFMA latency waits
+    // in front of a chain.
+    auto compute_full = [&](int buf) {
+        Ops o[3];
+        v4i c[2][2][NTS];
+        ld_ops(o[0], buf, 0);
+        if (KC > 1) ld_ops(o[1], buf, 1);
+        mma(o[0], c[0]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < KC; ++b) {
+            if (b + 2 < KC) ld_ops(o[(b + 2) % 3], buf, b + 2);
+            if (b + 1 < KC) mma(o[(b + 1) % 3], c[(b + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(o[b % 3], c[b & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
     // Two register sets, chunk j in set j % 2: chunk c + 1 is staged after chunk c is multiplied (its buffer was last
@@ -668,7 +700,10 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
     __syncthreads();
     QH_MMSTAMP(1);
     auto step = [&](int c, R& Sn) {  // Sn holds chunk c + 1
-        compute(c & 1, min(KC, nb - c * KC));
+        if ((c + 1) * KC <= nb)
+            compute_full(c & 1);
+        else
+            compute(c & 1, nb - c * KC);
         QH_MMSTAMP(2 + 3 * c);
         if (c + 1 < n_chunks) {
             stage(Sn, (c + 1) & 1);
@@ -685,8 +720,8 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
     }
 
 #pragma unroll
-    for (int ts = 0; ts < 2; ++ts) {
-        const int tok = tbase + wt * 32 + ts * 16 + li;
+    for (int ts = 0; ts < NTS; ++ts) {
+        const int tok = tbase + wt * (TT / 2) + ts * 16 + li;
         if (tok < n) {
 #pragma unroll
             for (int rs = 0; rs < 2; ++rs)
@@ -875,8 +910,9 @@ struct MmPlan {
     int tt, nw;
     bool stage = false;  // the LDS-staged kernel (one token tile per workgroup)
     int ns = 0;          // its register sets in flight past two chunks (2, 3 or 4; 0: default)
-    bool tile = false;   // the 64 x 64 tile kernel
+    bool tile = false;   // the 64-row tile kernel
     int kc = 4;          // its blocks per chunk (4 or 8)
+    int ttile = 64;      // its tokens per workgroup (64 or 32)
 };
 
 MmPlan matmul_plan(int rows, int cols, int n) {
@@ -888,20 +924,23 @@ MmPlan matmul_plan(int rows, int cols, int n) {
         if (strcmp(env, "stage") == 0) return MmPlan{false, 1, 4, true};
         if (strcmp(env, "tile") == 0) return MmPlan{false, 1, 4, false, 0, true, 4};
         if (sscanf(env, "tile:%d", &a) == 1 && (a == 4 || a == 8)) return MmPlan{false, 1, 4, false, 0, true, a};
+        if (strcmp(env, "tile32") == 0) return MmPlan{false, 1, 4, false, 0, true, 4, 32};
+        if (sscanf(env, "tile32:%d", &a) == 1 && (a == 4 || a == 8)) return MmPlan{false, 1, 4, false, 0, true, a, 32};
         if (sscanf(env, "stage:%d", &a) == 1 && a >= 2 && a <= 4) return MmPlan{false, 1, 4, true, a};
         if (sscanf(env, "reg:%d:%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && (b == 1 || b == 2 || b == 4))
             return MmPlan{true, a, b};
     }
     (void)pl;
-    // From sweeps on MI355X (cold weights) at the Qwen2.5-0.5B shapes, M = 32 / 64 / 128 / 512: the 64 x 64 tile
-    // kernel wins from 128 tokens on rows of up to 64 blocks once there are about 96 tiles or more (Q4_0 4864x896 at
-    // M = 512: 22.1 us, against 45.0 staged and 54.2 register-chain; M = 128: 13.1 against 14.5; Q8_0 896x896 at
-    // M = 512: 11.9 against 13.3); everywhere else the LDS-staged kernel wins, also over the register-chain kernel
-    // (Q4_0 896x4864 at M = 512: 40.5 against 49.6 us; the tile kernel 45.7, its 112 tiles run 152-block chains on a
-    // quarter of the SIMDs). The LDS-staged kernel measured 4-12% under the LDS and register kernels at 32 tokens
-    // (q/k/v, o, gate/up, down).
-    const long tiles64 = (long)((rows + 63) / 64) * ((n + 63) / 64);
-    if (n >= 128 && cols <= 2048 && tiles64 >= 96) return MmPlan{false, 1, 4, false, 0, true, 4};
+    // From sweeps on MI355X (cold weights) at the Qwen2.5-0.5B shapes, M = 32 / 64 / 128 / 512: the tile kernel with
+    // 32-token workgroups wins from 128 tokens once there are about 192 tiles or more, with 4-block chunks on rows of
+    // up to 64 blocks and 8-block chunks past that (Q4_0 4864x896 at M = 512: 21.4 us, against 21.2-24.2 for 64-token
+    // workgroups, 45.0 staged and 54.2 register-chain; M = 128: 10.8 against 14.4 staged; Q8_0 896x896 at M = 512:
+    // 8.7 against 11.9 and 13.3; Q4_0 896x4864 at M = 512: 25.6 against 31.0 with 4-block chunks, 26.4 with 16, 40.5
+    // staged). Everywhere else (32 and 64 tokens, few row tiles) the LDS-staged kernel wins, also over the
+    // register-chain kernel; it measured 4-12% under the LDS and register kernels at 32 tokens (q/k/v, o, gate/up,
+    // down).
+    const long tiles32 = (long)((rows + 63) / 64) * ((n + 31) / 32);
+    if (n >= 128 && tiles32 >= 192) return MmPlan{false, 1, 4, false, 0, true, cols >= 2048 ? 8 : 4, 32};
     return MmPlan{false, 1, 4, true};
 }
 
@@ -952,12 +991,13 @@ hipError_t launch_matmul_segs(const MmOut* m, int n_mats, const int8_t* xq, cons
             sg64.tiles[i] = (m[i].r1 - m[i].r0 + 63) / 64;
             row_tiles64 += sg64.tiles[i];
         }
-        const int n_tg = (n + 63) / 64;
+        const int n_tg = (n + pl.ttile - 1) / pl.ttile;
         const dim3 grid((unsigned)(row_tiles64 * n_tg));
-#define QH_MM_TILE(DT, KC)                                                                                     \
-    if (W.dtype == DT && pl.kc == KC)                                                                             \
-        qh_launch((matmul_tile_kernel<DT, KC>), grid, dim3(kMmThreads), 0, s, sg64, xq, xd, W.cols, n, n_tg);
-        QH_MM_TILE(kQ8, 4) QH_MM_TILE(kQ8, 8) QH_MM_TILE(kQ4, 4) QH_MM_TILE(kQ4, 8)
+#define QH_MM_TILE(DT, KC, TT)                                                                                     \
+    if (W.dtype == DT && pl.kc == KC && pl.ttile == TT)                                                                  \
+        qh_launch((matmul_tile_kernel<DT, KC, TT>), grid, dim3(kMmThreads), 0, s, sg64, xq, xd, W.cols, n, n_tg);
+        QH_MM_TILE(kQ8, 4, 64) QH_MM_TILE(kQ8, 8, 64) QH_MM_TILE(kQ4, 4, 64) QH_MM_TILE(kQ4, 8, 64)
+        QH_MM_TILE(kQ8, 4, 32) QH_MM_TILE(kQ8, 8, 32) QH_MM_TILE(kQ4, 4, 32) QH_MM_TILE(kQ4, 8, 32)
 #undef QH_MM_TILE
         return hipGetLastError();
     }

@@ -279,7 +279,7 @@ def test_shortlist_full_vocab(qh, oracle, synth, gpu):
     assert np.float32(st["top1_logit"]).tobytes() == full[st["top1"]].cpu().numpy().tobytes()
 
 
-@pytest.mark.parametrize("tt", ["stage", "stage:2", "stage:3", "stage:4", "tile"])
+@pytest.mark.parametrize("tt", ["stage", "stage:2", "stage:3", "stage:4", "tile", "tile32", "tile32:8"])
 @pytest.mark.parametrize("K", [512, 1536, 2560, 3584, 5632, 8192])
 @pytest.mark.parametrize("dtype", [2, 3])
 def test_matmul_staged_chunk_counts(qh, oracle, synth, gpu, monkeypatch, tt, dtype, K):
@@ -297,8 +297,8 @@ def test_matmul_staged_chunk_counts(qh, oracle, synth, gpu, monkeypatch, tt, dty
         assert (bits(got) == bits(want)).all(), (tt, M)
 
 
-@pytest.mark.parametrize("tt", ["stage", "tile", "tile:8", "lds:1", "lds:2", "lds:4", "reg:1:1", "reg:1:4", "reg:2:2", "reg:4:1",
-                                "reg:4:4"])
+@pytest.mark.parametrize("tt", ["stage", "tile", "tile:8", "tile32", "tile32:8", "lds:1", "lds:2", "lds:4", "reg:1:1",
+                                "reg:1:4", "reg:2:2", "reg:4:1", "reg:4:4"])
 @pytest.mark.parametrize("dtype,N,K", [(2, 200, 896), (3, 200, 896), (2, 40, 4864), (3, 40, 4864)])
 def test_matmul_every_token_tiling(qh, oracle, synth, gpu, monkeypatch, tt, dtype, N, K):
     """Both prefill kernels at every token tiling (LDS-staged block sums, register chains) on ragged shapes: rows not a
