@@ -104,6 +104,14 @@ int qh_quantize_q8(const float* x, int n_tok, int n, int8_t* q, float* d, void* 
 int qh_matvec_q(float* out, const qh_tensor* W, const int8_t* xq, const float* xd, int r0, int r1,
                 void* stream);
 
+/* GEMV over unquantized weights: out[r] = W[r,:] . x for r in [r0, r1), W F32 or F16 ([rows][cols] row-major, cols
+ * a multiple of 32), x [cols] f32. Per row the serial chain acc = fma(w_i, x_i, acc) from +0 in column order (the
+ * reference build's contraction of acc += w * x; an F16 weight is converted exactly).
+ * Replaces: void matvec_ref(float* out, const Tensor& W, const float* x, int r0, int r1) for F32 / F16 W
+ *           (reference ops.h:43, implementation ops_ref.cpp:8-27: Model::linear's path for an unquantized W,
+ *           model.cpp:154-156). */
+int qh_matvec_ref(float* out, const qh_tensor* W, const float* x, int r0, int r1, void* stream);
+
 /* Prefill matmul for n tokens: out[t*ldo + r] for t in [0, n), r in [r0, r1); xq is [n][cols]
  * int8, xd is [n][cols/32] f32 (the n QuantVecs back to back). Every (row, token) value is
  * bit-identical to qh_matvec_q on that token (int8 MFMA, K = 32 per instruction = one block).
@@ -269,12 +277,15 @@ typedef struct qh_decoder_state {
 } qh_decoder_state;
 
 /* Creates a decoder over device tensors, in this order (reference model.cpp:14-33, 47-58):
- *   model.embed_tokens.weight (Q8_0 [vocab][dim], also the LM head when tied), model.norm.weight (F32 [1][dim]);
- *   per layer: input_layernorm (F32), q_proj, k_proj, v_proj, o_proj (Q8_0 or Q4_0), q/k/v biases (F32, or data NULL
- *   without qkv_bias), post_attention_layernorm (F32), gate_proj, up_proj, down_proj (Q8_0 or Q4_0);
+ *   model.embed_tokens.weight ([vocab][dim], also the LM head when tied), model.norm.weight (F32 [1][dim]);
+ *   per layer: input_layernorm (F32), q_proj, k_proj, v_proj, o_proj, q/k/v biases (F32, or data NULL without
+ *   qkv_bias), post_attention_layernorm (F32), gate_proj, up_proj, down_proj;
  *   then quanta.head_q4 (Q4_0 [vocab][dim]) and quanta.head_err (F16 [vocab][dim/32]), or both with data NULL;
- *   optionally (n_tensors 5 + 12 n_layers) lm_head.weight ([vocab][dim], Q8_0 or Q4_0; Q8_0 with the shortlist head
- *   tensors), the LM head of an untied model; data NULL there, or n_tensors 4 + 12 n_layers, means tied.
+ *   optionally (n_tensors 5 + 12 n_layers) lm_head.weight ([vocab][dim]), the LM head of an untied model; data NULL
+ *   there, or n_tensors 4 + 12 n_layers, means tied.
+ * Every matrix (the embedding and LM head included) may be Q8_0, Q4_0, F32 or F16, each on its own, as the exporter
+ * writes them (F32 / F16 ones run matvec_ref's float chain on the f32 activation, model.cpp:150-157); the LM head is
+ * Q8_0 when the shortlist head tensors are given (model.cpp:49-58).
  * Allocates an fp16 KV cache (f32 with hp->kv_f32) for ctx_len positions and the work buffers. dim, ctx_len <= 8192,
  * head_dim 64 or 128, n_heads * head_dim == dim, ffn_dim % 256 == 0 with QH_FLAG_HADAMARD_DOWN. The tensors must
  * stay alive while the decoder is used.

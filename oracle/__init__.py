@@ -156,6 +156,24 @@ class _Oracle:
             self.lib.qo_matmul_q(out, rows, dtype, rows, cols, buf, xq, xd, n, r0, rows if r1 is None else r1)
         return out
 
+    def matvec_f(self, dtype, rows, cols, buf, x, r0=0, r1=None):
+        """matvec_ref over F32 / F16 weights (qo_matvec_f)."""
+        L = self.lib
+        L.qo_matvec_f.argtypes = [_f32p, _int, _int, _int, C.c_void_p, _f32p, _int, _int]
+        out = np.zeros(rows, np.float32)
+        buf = np.ascontiguousarray(buf)
+        L.qo_matvec_f(out, dtype, rows, cols, buf.ctypes.data, np.ascontiguousarray(x, np.float32), r0,
+                      rows if r1 is None else r1)
+        return out
+
+    def get_row(self, dtype, rows, cols, buf, row):
+        L = self.lib
+        L.qo_get_row.argtypes = [_f32p, _int, _int, _int, C.c_void_p, _int]
+        out = np.zeros(cols, np.float32)
+        buf = np.ascontiguousarray(buf)
+        L.qo_get_row(out, dtype, rows, cols, buf.ctypes.data, row)
+        return out
+
     def argmax(self, logits: np.ndarray, n: int | None = None) -> int:
         logits = np.ascontiguousarray(logits, np.float32)
         return self.lib.qo_argmax(logits, logits.size if n is None else n)
@@ -332,6 +350,22 @@ class _Ref:
         out = np.zeros(rows, np.float32)
         return self.lib.ref_time_matvec_q(out, dtype, rows, cols, buf, np.ascontiguousarray(xq, np.int8),
                                           np.ascontiguousarray(xd, np.float32), threads, reps)
+
+    def matvec_f(self, dtype, rows, cols, buf, x, threads=1):
+        """Model::linear for an F32 / F16 W (matvec_ref)."""
+        L = self.lib
+        L.ref_matvec_f.argtypes = [_f32p, _int, _int, _int, _u8p, _f32p, _int]
+        out = np.zeros(rows, np.float32)
+        L.ref_matvec_f(out, dtype, rows, cols, np.ascontiguousarray(buf).view(np.uint8).reshape(-1),
+                       np.ascontiguousarray(x, np.float32), threads)
+        return out
+
+    def get_row(self, dtype, rows, cols, buf, row):
+        L = self.lib
+        L.ref_get_row.argtypes = [_f32p, _int, _int, _int, _u8p, _int]
+        out = np.zeros(cols, np.float32)
+        L.ref_get_row(out, dtype, rows, cols, np.ascontiguousarray(buf).view(np.uint8).reshape(-1), row)
+        return out
 
     def matmul_q(self, dtype, rows, cols, buf, xq, xd, threads=1):
         xq = np.ascontiguousarray(xq, np.int8)

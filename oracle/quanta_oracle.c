@@ -107,6 +107,48 @@ void qo_matvec_q(float* out, int dtype, int rows, int cols, const uint8_t* data,
     for (int r = r0; r < r1; ++r) out[r] = row_dot(dtype, cols, data, scales, r, xq, xd);
 }
 
+/* ops_ref.cpp:8-27: acc += w_i * x_i from +0 in column order; the reference build contracts each step into one
+ * multiply-add (-march with FMA, GCC's default contraction); an F16 weight is converted exactly first. */
+void qo_matvec_f(float* out, int dtype, int rows, int cols, const void* data, const float* x, int r0, int r1) {
+    (void)rows;
+    for (int r = r0; r < r1; ++r) {
+        float acc = 0.f;
+        if (dtype == QO_F32) {
+            const float* w = (const float*)data + (size_t)r * cols;
+            for (int i = 0; i < cols; ++i) acc = fmaf(w[i], x[i], acc);
+        } else {
+            const uint16_t* w = (const uint16_t*)data + (size_t)r * cols;
+            for (int i = 0; i < cols; ++i) acc = fmaf(qo_fp16_to_f32(w[i]), x[i], acc);
+        }
+        out[r] = acc;
+    }
+}
+
+/* ops_ref.cpp:162-192; the products q * d are exact in f32 (at most 8 + 11 significant bits) */
+void qo_get_row(float* out, int dtype, int rows, int cols, const void* data, int row) {
+    const int nb = cols / QO_QK;
+    if (dtype == QO_F32) {
+        memcpy(out, (const float*)data + (size_t)row * cols, sizeof(float) * (size_t)cols);
+    } else if (dtype == QO_F16) {
+        const uint16_t* w = (const uint16_t*)data + (size_t)row * cols;
+        for (int i = 0; i < cols; ++i) out[i] = qo_fp16_to_f32(w[i]);
+    } else if (dtype == QO_Q8_0) {
+        const int8_t* q = (const int8_t*)data + (size_t)row * cols;
+        const uint16_t* d = (const uint16_t*)((const uint8_t*)data + (size_t)rows * cols) + (size_t)row * nb;
+        for (int i = 0; i < cols; ++i) out[i] = (float)q[i] * qo_fp16_to_f32(d[i / QO_QK]);
+    } else {
+        const uint8_t* q = (const uint8_t*)data + (size_t)row * cols / 2;
+        const uint16_t* d = (const uint16_t*)((const uint8_t*)data + (size_t)rows * cols / 2) + (size_t)row * nb;
+        for (int b = 0; b < nb; ++b) {
+            const float s = qo_fp16_to_f32(d[b]);
+            for (int j = 0; j < QO_QK / 2; ++j) {
+                out[b * QO_QK + j] = (float)((int)(q[b * QO_QK / 2 + j] & 0xF) - 8) * s;
+                out[b * QO_QK + j + QO_QK / 2] = (float)((int)(q[b * QO_QK / 2 + j] >> 4) - 8) * s;
+            }
+        }
+    }
+}
+
 void qo_matmul_q(float* out, int ldo, int dtype, int rows, int cols, const uint8_t* data,
                  const int8_t* xq, const float* xd, int n, int r0, int r1) {
     const uint16_t* scales = (const uint16_t*)(data + qo_quant_bytes(dtype, rows, cols));
@@ -466,26 +508,29 @@ static void softmax(float* x, int n) {
     for (int i = 0; i < n; ++i) x[i] *= inv;
 }
 
-static void linear(const qo_decoder* d, float* out, int l, int which, int rows, int cols, const int8_t* xq,
-                   const float* xd) {
-    qo_matvec_q(out, ldt(d, l, which), rows, cols, (const uint8_t*)lt(d, l, which), xq, xd, 0, rows);
+/* Model::linear (model.cpp:150-157): the integer-dot matvec on the quantized activation for a Q8_0 / Q4_0 W,
+ * matvec_ref on the f32 activation x for an F32 / F16 W */
+static void linear(const qo_decoder* d, float* out, int l, int which, int rows, int cols, const float* x,
+                   const int8_t* xq, const float* xd) {
+    const int dt = ldt(d, l, which);
+    if (dt == QO_F32 || dt == QO_F16)
+        qo_matvec_f(out, dt, rows, cols, lt(d, l, which), x, 0, rows);
+    else
+        qo_matvec_q(out, dt, rows, cols, (const uint8_t*)lt(d, l, which), xq, xd, 0, rows);
 }
 
 /* One token through every layer (model.cpp:174-222); leaves the residual stream in d->x. */
 static void layers(qo_decoder* d, int token, int pos) {
     const int D = d->D, hd = d->hdim, kvd = d->nkv * hd, group = d->nh / d->nkv, F = d->F;
     const float scale = 1.0f / sqrtf((float)hd);
-    /* get_row on the Q8_0 embedding (ops_ref.cpp:176-181) */
-    const int8_t* eq = (const int8_t*)d->t[0] + (size_t)token * D;
-    const uint16_t* es = (const uint16_t*)((const uint8_t*)d->t[0] + (size_t)d->V * D) + (size_t)token * (D / QO_QK);
-    for (int i = 0; i < D; ++i) d->x[i] = (float)eq[i] * qo_fp16_to_f32(es[i / QO_QK]);
+    qo_get_row(d->x, d->dt[0], d->V, D, d->t[0], token); /* get_row on the embedding (model.cpp:173) */
     const float* cs = d->cs + (size_t)pos * hd;
     for (int l = 0; l < d->nl; ++l) {
         rmsnorm(d->xb, d->x, (const float*)lt(d, l, L_ATTN_NORM), D, d->eps);
         qo_quantize_q8(d->xb, D, d->xq, d->xd);
-        linear(d, d->q, l, L_WQ, D, D, d->xq, d->xd);
-        linear(d, d->k, l, L_WK, kvd, D, d->xq, d->xd);
-        linear(d, d->v, l, L_WV, kvd, D, d->xq, d->xd);
+        linear(d, d->q, l, L_WQ, D, D, d->xb, d->xq, d->xd);
+        linear(d, d->k, l, L_WK, kvd, D, d->xb, d->xq, d->xd);
+        linear(d, d->v, l, L_WV, kvd, D, d->xb, d->xq, d->xd);
         if (d->bias) {
             const float *bq = (const float*)lt(d, l, L_BQ), *bk = (const float*)lt(d, l, L_BK),
                         *bv = (const float*)lt(d, l, L_BV);
@@ -526,19 +571,19 @@ static void layers(qo_decoder* d, int token, int pos) {
         }
 #undef QO_KV
         qo_quantize_q8(d->xb, D, d->xq, d->xd);
-        linear(d, d->xb2, l, L_WO, D, D, d->xq, d->xd);
+        linear(d, d->xb2, l, L_WO, D, D, d->xb, d->xq, d->xd);
         for (int i = 0; i < D; ++i) d->x[i] += d->xb2[i];
         rmsnorm(d->xb, d->x, (const float*)lt(d, l, L_FFN_NORM), D, d->eps);
         qo_quantize_q8(d->xb, D, d->xq, d->xd);
-        linear(d, d->hb, l, L_WG, F, D, d->xq, d->xd);
-        linear(d, d->hb2, l, L_WU, F, D, d->xq, d->xd);
+        linear(d, d->hb, l, L_WG, F, D, d->xb, d->xq, d->xd);
+        linear(d, d->hb2, l, L_WU, F, D, d->xb, d->xq, d->xd);
         for (int i = 0; i < F; ++i) { /* swiglu, ops_ref.cpp:243-248 */
             const float g = d->hb[i];
             d->hb[i] = g / (1.0f + expf(-g)) * d->hb2[i];
         }
         if (d->flags & 1) fwht_blocks(d->hb, F, 256); /* model.cpp:219 */
         qo_quantize_q8(d->hb, F, d->hq, d->hd);
-        linear(d, d->xb2, l, L_WD, D, F, d->hq, d->hd);
+        linear(d, d->xb2, l, L_WD, D, F, d->hb, d->hq, d->hd);
         for (int i = 0; i < D; ++i) d->x[i] += d->xb2[i];
     }
 }
@@ -558,8 +603,11 @@ static int head(qo_decoder* d, int top_k, float* logits, float* hidden, int8_t* 
                                  top_k, V, d->must, d->n_must, d->logits, d->coarse, d->upper, d->rows, &ns, &tau,
                                  &tie);
     } else {
-        /* the LM head (model.cpp:16): the embedding when tied, else lm_head.weight */
-        qo_matvec_q(d->logits, d->dt[d->lm], V, D, (const uint8_t*)d->t[d->lm], d->xq, d->xd, 0, V);
+        /* the LM head (model.cpp:16): the embedding when tied, else lm_head.weight; Model::linear by its dtype */
+        if (d->dt[d->lm] == QO_F32 || d->dt[d->lm] == QO_F16)
+            qo_matvec_f(d->logits, d->dt[d->lm], V, D, d->t[d->lm], d->x, 0, V);
+        else
+            qo_matvec_q(d->logits, d->dt[d->lm], V, D, (const uint8_t*)d->t[d->lm], d->xq, d->xd, 0, V);
         rows = V;
     }
     if (logits) memcpy(logits, d->logits, sizeof(float) * (size_t)V);

@@ -42,6 +42,13 @@ void qo_quantize_q8(const float* x, int n, int8_t* q, float* d);
 void qo_matvec_q(float* out, int dtype, int rows, int cols, const uint8_t* data, const int8_t* xq,
                  const float* xd, int r0, int r1);
 
+/* Matvec over F32 / F16 weights with an f32 activation (matvec_ref, ops_ref.cpp:8-27; Model::linear's path for an
+ * unquantized W, model.cpp:154-156), rows [r0, r1). data points at the row-major weights. */
+void qo_matvec_f(float* out, int dtype, int rows, int cols, const void* data, const float* x, int r0, int r1);
+
+/* Row `row` of a [rows][cols] tensor of any dtype as f32 (get_row, ops_ref.cpp:162-192). */
+void qo_get_row(float* out, int dtype, int rows, int cols, const void* data, int row);
+
 /* Multi-token matmul (ops_ref.cpp:122-160, contract ops.h:65-70): out[t*ldo + r] for tokens
  * t in [0, n) and rows r in [r0, r1). xq is [n][cols] int8, xd is [n][cols/32]. Every
  * (row, token) value is bit-identical to qo_matvec_q on that token. */

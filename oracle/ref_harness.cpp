@@ -80,6 +80,18 @@ void ref_matvec_q(float* out, int dtype, int rows, int cols, const uint8_t* data
     pool.parallel_for(rows, 16, [&](int r0, int r1) { quanta::matvec_q(out, W, x, r0, r1); });
 }
 
+// Model::linear for an F32 / F16 W: ThreadPool::parallel_for(rows, 16) over matvec_ref (model.cpp:154-156).
+void ref_matvec_f(float* out, int dtype, int rows, int cols, const uint8_t* data, const float* x, int n_threads) {
+    const Tensor W = make_tensor(dtype, rows, cols, data);
+    quanta::ThreadPool pool(n_threads);
+    pool.parallel_for(rows, 16, [&](int r0, int r1) { quanta::matvec_ref(out, W, x, r0, r1); });
+}
+
+// get_row (ops_ref.cpp:162-192) of a tensor of any dtype.
+void ref_get_row(float* out, int dtype, int rows, int cols, const uint8_t* data, int row) {
+    quanta::get_row(out, make_tensor(dtype, rows, cols, data), row);
+}
+
 // Seconds for `reps` calls of Model::linear on one pool (the CPU baseline's timed loop).
 double ref_time_matvec_q(float* out, int dtype, int rows, int cols, const uint8_t* data, const int8_t* xq,
                          const float* xd, int n_threads, int reps) {

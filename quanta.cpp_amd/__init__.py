@@ -77,7 +77,7 @@ STAGE_FINAL_NORM, STAGE_HEAD, STAGE_PICK = 1 << 20, (1 << 20) + 1, (1 << 20) + 2
 EXPORTS = ("qh_last_error", "qh_version", "qh_init", "qh_quant_bytes", "qh_tensor_bytes", "qh_validate_tensor",
            "qh_malloc", "qh_fault_alloc", "qh_free", "qh_memcpy_h2d", "qh_memcpy_d2h", "qh_memset", "qh_stream_sync",
            "qh_stream_create", "qh_stream_destroy",
-           "qh_quantize_q8", "qh_matvec_q", "qh_matmul_q", "qh_argmax_workspace_bytes", "qh_argmax",
+           "qh_quantize_q8", "qh_matvec_q", "qh_matvec_ref", "qh_matmul_q", "qh_argmax_workspace_bytes", "qh_argmax",
            "qh_shortlist_workspace_bytes", "qh_shortlist_head", "qh_shortlist_head_noalloc",
            "qh_sampler_state", "qh_sample", "qh_decoder_create", "qh_decoder_destroy",
            "qh_decoder_prefill", "qh_decoder_begin", "qh_decoder_step", "qh_decoder_views", "qh_decoder_step_timed",
@@ -102,6 +102,7 @@ def _bind(lib):
         "qh_stream_create": ([C.POINTER(vp)], i32), "qh_stream_destroy": ([vp], i32),
         "qh_quantize_q8": ([vp, i32, i32, vp, vp, vp], i32),
         "qh_matvec_q": ([vp, C.POINTER(qh_tensor), vp, vp, i32, i32, vp], i32),
+        "qh_matvec_ref": ([vp, C.POINTER(qh_tensor), vp, i32, i32, vp], i32),
         "qh_matmul_q": ([vp, i32, C.POINTER(qh_tensor), vp, vp, i32, i32, i32, vp], i32),
         "qh_argmax_workspace_bytes": ([i32], sz),
         "qh_argmax": ([vp, i32, vp, vp, sz, vp], i32),
@@ -205,6 +206,16 @@ def matvec_q(W: DeviceTensor, xq, xd, out=None, r0: int = 0, r1: int | None = No
         out = torch.zeros(W.rows, dtype=torch.float32, device=xq.device)
     r1 = W.rows if r1 is None else r1
     _check(lib().qh_matvec_q(_ptr(out), C.byref(W.view), _ptr(xq), _ptr(xd), r0, r1, _stream()))
+    return out
+
+
+def matvec_ref(W: DeviceTensor, x, out=None, r0: int = 0, r1: int | None = None):
+    """W F32 / F16, x [cols] f32 (a device tensor) -> out [rows] with rows [r0, r1) written (matvec_ref)."""
+    torch = _torch()
+    if out is None:
+        out = torch.zeros(W.rows, dtype=torch.float32, device=x.device)
+    r1 = W.rows if r1 is None else r1
+    _check(lib().qh_matvec_ref(_ptr(out), C.byref(W.view), _ptr(x), r0, r1, _stream()))
     return out
 
 

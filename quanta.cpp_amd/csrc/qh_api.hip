@@ -58,6 +58,20 @@ int validate_quant(const qh_tensor* W, const char* what) {
     return QH_OK;
 }
 
+// A decoder matrix: Q8_0 / Q4_0 as validate_quant, or F32 / F16 (matvec_ref) with the same shape rules.
+int validate_matrix(const qh_tensor* W, const char* what) {
+    if (W && (W->dtype == QH_F32 || W->dtype == QH_F16)) {
+        if (W->rows <= 0 || W->cols <= 0 || W->cols % QH_QK != 0 || W->cols > kMaxCols)
+            return fail(QH_ERR_SHAPE, "%s: bad shape %d x %d", what, W->rows, W->cols);
+        if (!W->data) return fail(QH_ERR_ARG, "%s: null data", what);
+        if (!aligned16(W->data)) return fail(QH_ERR_ALIGN, "%s: data is not 16-byte aligned", what);
+        return QH_OK;
+    }
+    if (W && W->dtype != QH_Q8_0 && W->dtype != QH_Q4_0)
+        return fail(QH_ERR_DTYPE, "%s: dtype %d is not f32 (0), f16 (1), q8_0 (2) or q4_0 (3)", what, W->dtype);
+    return validate_quant(W, what);
+}
+
 int validate_range(int rows, int r0, int r1, const char* what) {
     if (r0 < 0 || r1 > rows || r0 > r1)
         return fail(QH_ERR_ARG, "%s: row range [%d, %d) outside [0, %d)", what, r0, r1, rows);
@@ -251,6 +265,18 @@ int qh_quantize_q8(const float* x, int n_tok, int n, int8_t* q, float* d, void* 
     return check_hip(launch_quantize_q8(x, n_tok, n, q, d, as_stream(stream)), "qh_quantize_q8 launch");
 }
 
+int qh_matvec_ref(float* out, const qh_tensor* W, const float* x, int r0, int r1, void* stream) {
+    if (!W || !out || !x || !W->data) return fail(QH_ERR_ARG, "qh_matvec_ref: null pointer");
+    if (W->dtype != QH_F32 && W->dtype != QH_F16)
+        return fail(QH_ERR_DTYPE, "qh_matvec_ref: dtype %d is not f32 (0) or f16 (1); use qh_matvec_q", W->dtype);
+    if (W->rows <= 0 || W->cols <= 0 || W->cols % QH_QK != 0)
+        return fail(QH_ERR_SHAPE, "qh_matvec_ref: shape %d x %d (cols must be a multiple of 32)", W->rows, W->cols);
+    if (int rc = validate_range(W->rows, r0, r1, "qh_matvec_ref")) return rc;
+    if (!aligned16(W->data) || !aligned16(x)) return fail(QH_ERR_ALIGN, "qh_matvec_ref: W or x is not 16-byte aligned");
+    if (r0 == r1) return QH_OK;
+    return check_hip(launch_gemv_dense(out, 0, *W, x, W->cols, 1, r0, r1, as_stream(stream)), "qh_matvec_ref launch");
+}
+
 int qh_matvec_q(float* out, const qh_tensor* W, const int8_t* xq, const float* xd, int r0, int r1, void* stream) {
     if (int rc = validate_quant(W, "qh_matvec_q")) return rc;
     if (int rc = validate_range(W->rows, r0, r1, "qh_matvec_q")) return rc;
@@ -366,7 +392,7 @@ int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_t
     auto want = [&](int i, int rows, int cols, bool quant, const char* what) -> int {
         const qh_tensor& t = tensors[i];
         if (quant) {
-            if (int rc = validate_quant(&t, what)) return rc;
+            if (int rc = validate_matrix(&t, what)) return rc;
         } else if (t.dtype != QH_F32 || !t.data) {
             return fail(QH_ERR_DTYPE, "qh_decoder_create: %s must be f32", what);
         }
@@ -375,7 +401,6 @@ int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_t
                         cols);
         return QH_OK;
     };
-    if (tensors[0].dtype != QH_Q8_0) return fail(QH_ERR_DTYPE, "qh_decoder_create: the embedding must be q8_0");
     if (int rc = want(0, hp->vocab_size, D, true, "embedding")) return rc;
     if (int rc = want(1, 1, D, false, "final norm")) return rc;
     for (int l = 0; l < L; ++l) {
@@ -390,8 +415,6 @@ int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_t
     }
     // the LM head: lm_head.weight when untied (model.cpp:16), Q8_0 or Q4_0, else the embedding
     const bool untied = n_tensors == 5 + 12 * L && tensors[4 + 12 * L].data;
-    if (untied && (tensors[4 + 12 * L].dtype != QH_Q8_0 && tensors[4 + 12 * L].dtype != QH_Q4_0))
-        return fail(QH_ERR_DTYPE, "qh_decoder_create: lm_head must be q8_0 or q4_0");
     if (untied)
         if (int rc = want(4 + 12 * L, hp->vocab_size, D, true, "lm_head")) return rc;
     const int lm_dtype = untied ? tensors[4 + 12 * L].dtype : QH_Q8_0;

@@ -686,15 +686,16 @@ struct NormActR {
 
 // ------------------------------------------------------------------------------------------------------ kernels
 
-// x[t] = embedding row of tokens[t] (Q8_0 get_row, ops_ref.cpp:176-181: code * f16 scale, exact in f32), then the
-// first layer's rmsnorm and quantization. One workgroup per token.
+// x[t] = embedding row of tokens[t] (get_row, ops_ref.cpp:162-192: F32 as stored, F16 converted, Q8_0 / Q4_0 code *
+// f16 scale, all exact in f32), then the first layer's rmsnorm and quantization; the normed row also to normed[t]
+// when given (the f32 input of unquantized matrices). One workgroup per token.
 template <int R>
 __global__ __launch_bounds__(256) void embed_norm_quant_kernel(const int32_t* __restrict__ tokens,
-                                                               const int8_t* __restrict__ eq,
-                                                               const uint16_t* __restrict__ es, int D, int V,
-                                                               float* __restrict__ x, const float* __restrict__ w,
-                                                               float eps, int8_t* __restrict__ oq,
-                                                               float* __restrict__ od, int* __restrict__ status) {
+                                                               const uint8_t* __restrict__ emb, int dtype, int D,
+                                                               int V, float* __restrict__ x,
+                                                               const float* __restrict__ w, float eps,
+                                                               int8_t* __restrict__ oq, float* __restrict__ od,
+                                                               float* __restrict__ normed, int* __restrict__ status) {
     __shared__ __align__(16) float xs[8192 + kChainPad];
     const int t = blockIdx.x, tid = threadIdx.x;
     RowF4<R> wr;
@@ -705,25 +706,39 @@ __global__ __launch_bounds__(256) void embed_norm_quant_kernel(const int32_t* __
         if (tid == 0) atomicOr(status, kStatusToken);
         tok = 0;
     }
-    const int8_t* er = eq + (size_t)tok * D;
-    const uint16_t* sr = es + (size_t)tok * (D / QK);
-    for (int i4 = tid; i4 < D / 4; i4 += 256) {  // 4 codes and their block's scale
-        const uint32_t c4 = *reinterpret_cast<const uint32_t*>(er + 4 * i4);
-        const float sc = h2f(sr[i4 / (QK / 4)]);
+    const size_t nq = dtype == kQ4 ? (size_t)V * D / 2 : (size_t)V * D;  // quant bytes before the scales
+    const uint16_t* sr = reinterpret_cast<const uint16_t*>(emb + nq) + (size_t)tok * (D / QK);
+    for (int i4 = tid; i4 < D / 4; i4 += 256) {  // elements 4 i4 .. 4 i4 + 3 (one block, one half of a Q4_0 block)
         float4 v;
-        v.x = bad ? 0.0f : (float)(int8_t)(c4 & 0xff) * sc;
-        v.y = bad ? 0.0f : (float)(int8_t)((c4 >> 8) & 0xff) * sc;
-        v.z = bad ? 0.0f : (float)(int8_t)((c4 >> 16) & 0xff) * sc;
-        v.w = bad ? 0.0f : (float)(int8_t)(c4 >> 24) * sc;
+        if (dtype == kF32) {
+            v = reinterpret_cast<const float4*>(emb + (size_t)tok * D * 4)[i4];
+        } else if (dtype == kF16) {
+            const uint2 h = reinterpret_cast<const uint2*>(emb + (size_t)tok * D * 2)[i4];
+            v = make_float4(h2f((uint16_t)(h.x & 0xffffu)), h2f((uint16_t)(h.x >> 16)), h2f((uint16_t)(h.y & 0xffffu)),
+                            h2f((uint16_t)(h.y >> 16)));
+        } else {
+            const float sc = h2f(sr[i4 / (QK / 4)]);
+            uint32_t c4;
+            if (dtype == kQ8) {
+                c4 = *reinterpret_cast<const uint32_t*>(emb + (size_t)tok * D + 4 * i4);
+            } else {  // element j of a block: low nibble of byte j (j < 16), high nibble of byte j - 16
+                const int e = 4 * i4, j = e % QK;
+                const uint32_t b4 = *reinterpret_cast<const uint32_t*>(emb + (size_t)tok * D / 2 + (e / QK) * 16 + j % 16);
+                c4 = nibbles_to_i8(j < 16 ? b4 & 0x0F0F0F0Fu : (b4 >> 4) & 0x0F0F0F0Fu);
+            }
+            v = make_float4((float)(int8_t)(c4 & 0xff) * sc, (float)(int8_t)((c4 >> 8) & 0xff) * sc,
+                            (float)(int8_t)((c4 >> 16) & 0xff) * sc, (float)(int8_t)(c4 >> 24) * sc);
+        }
+        if (bad) v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         reinterpret_cast<float4*>(x + (size_t)t * D)[i4] = v;
         reinterpret_cast<float4*>(xs)[i4] = v;
     }
     __syncthreads();
-    norm_quant_lds(xs, D, wr, eps, oq + (size_t)t * D, od + (size_t)t * (D / QK), nullptr);
+    norm_quant_lds(xs, D, wr, eps, oq + (size_t)t * D, od + (size_t)t * (D / QK), normed ? normed + (size_t)t * D : nullptr);
 }
 
 // One workgroup per token: residual add x += o, then rmsnorm with weight w and int8 quantization of the normed row;
-// the normed row is also written to `normed` when given. D <= 8192.
+// the normed row is also written to normed[t] when given. D <= 8192.
 template <int R>
 __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(float* __restrict__ x, const float* __restrict__ o,
                                                                 const float* __restrict__ w, int D, float eps,
@@ -751,7 +766,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(float* __restric
     }
     __syncthreads();
     const float ss = D >= 128 ? seg_sum_squares_lds(xs, D, xr) : lds_sum_squares(xs, D);  // uniform
-    normalize_quant_lds(xs, D, rms_scale(ss, D, eps), wr, xq + (size_t)t * D, xd + (size_t)t * (D / QK), normed);
+    normalize_quant_lds(xs, D, rms_scale(ss, D, eps), wr, xq + (size_t)t * D, xd + (size_t)t * (D / QK),
+                        normed ? normed + (size_t)t * D : nullptr);
 }
 
 // Attention of token t (position pos0 + t) and query head h over positions [0, pos0 + t], for a chunk of n <= 32
@@ -773,7 +789,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv,
     const float* __restrict__ cs, const int* __restrict__ pos_dev, int ctx, int n_heads, int n_kv,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int8_t* __restrict__ oq, float* __restrict__ od,
-    int* __restrict__ status) {
+    int* __restrict__ status, float* __restrict__ of) {
     constexpr int HALF = HD / 2, CPR = HD / 8;           // 16-byte chunks per f16 K row
     constexpr int kVRows = (WPE == 1 ? kVStageBytes : 32 * 1024) / (HD * 2);  // V rows one LDS stage holds (mult. of 8)
     constexpr int kVBlk = kVRows / 8;                    // 8-row blocks per stage
@@ -1123,6 +1139,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     }
     if (tid < HD) {  // quantize_q8 of the attention output, two 32-blocks per 64 dimensions
         const int col = h * HD + (tid & ~31);
+        if (of) of[(size_t)t * qd + h * HD + tid] = acc;  // the f32 input of an unquantized o projection
         quant_block32(acc, oq + (size_t)t * qd + col, od + (size_t)t * (qd / QK) + col / QK);
     }
 }
@@ -1140,7 +1157,7 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(
     const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv,
     const float* __restrict__ cs, const int* __restrict__ pos_dev, int ctx, int n_heads, int n_kv,
     float* __restrict__ kc, float* __restrict__ vc, int8_t* __restrict__ oq, float* __restrict__ od,
-    int* __restrict__ status) {
+    int* __restrict__ status, float* __restrict__ of) {
     constexpr int HALF = HD / 2, C4 = HD / 4;
     constexpr int kVR = 16384 / HD;  // V rows per LDS stage (64 KB)
     __shared__ __align__(16) float att[kMaxCtx + kChainPad];
@@ -1262,6 +1279,7 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(
     }
     if (tid < HD) {  // quantize_q8 of the attention output
         const int col = h * HD + (tid & ~31);
+        if (of) of[(size_t)t * qd + h * HD + tid] = acc;  // the f32 input of an unquantized o projection
         quant_block32(acc, oq + (size_t)t * qd + col, od + (size_t)t * (qd / QK) + col / QK);
     }
 }
@@ -1272,7 +1290,8 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(
 // butterfly adds or subtracts the same two values as the reference's loop, so the result does not depend on the
 // order the butterflies of a stage run in. Grid (ffn_dim / 256, tokens).
 __global__ __launch_bounds__(256) void swiglu_fwht_quant_kernel(const float* __restrict__ g, const float* __restrict__ u,
-                                                                int F, int8_t* __restrict__ oq, float* __restrict__ od) {
+                                                                int F, int8_t* __restrict__ oq, float* __restrict__ od,
+                                                                float* __restrict__ of) {
     __shared__ float vb[256];
     const int tid = threadIdx.x;
     const size_t b0 = (size_t)blockIdx.y * F + (size_t)blockIdx.x * 256;
@@ -1295,7 +1314,9 @@ __global__ __launch_bounds__(256) void swiglu_fwht_quant_kernel(const float* __r
     }
     const float norm = 1.0f / __builtin_sqrtf(256.0f);
     const size_t blk = b0 + (tid & ~31);
-    quant_block32(vb[tid] * norm, oq + blk, od + blk / QK);
+    const float hv = vb[tid] * norm;
+    if (of) of[b0 + tid] = hv;
+    quant_block32(hv, oq + blk, od + blk / QK);
 }
 
 // ------------------------------------------------------------------------------ decode attention, 16 waves per head
@@ -1396,7 +1417,7 @@ __global__ __launch_bounds__(1024) void attention_decode_kernel(
     uint16_t* __restrict__ kc, const int* __restrict__ pos_dev, int ctx, int group, const float* __restrict__ bq,
     const float* __restrict__ bk, int n_kv, const float* __restrict__ bv, const float* __restrict__ cs,
     uint16_t* __restrict__ vc, int8_t* __restrict__ oq, float* __restrict__ od, float* __restrict__ escr,
-    int escr_stride, int* __restrict__ status) {
+    int escr_stride, int* __restrict__ status, float* __restrict__ of) {
     static_assert(HD == 64, "one chain wave and one K row of 8 chunks per thread");
     constexpr int NT = 1024, NW = NT / 64;
     constexpr int HALF = HD / 2, CPR = HD / 8;
@@ -1695,6 +1716,7 @@ __global__ __launch_bounds__(1024) void attention_decode_kernel(
     QH_WSTAMP(1, 3);
     if (tid < HD) {  // quantize_q8 of the attention output, two 32-blocks per 64 dimensions
         const int col = h * HD + (tid & ~31);
+        if (of) of[h * HD + tid] = acc;  // the f32 input of an unquantized o projection
         quant_block32(acc, oq + col, od + col / QK);
     }
 }
@@ -1702,12 +1724,14 @@ __global__ __launch_bounds__(1024) void attention_decode_kernel(
 // h = g / (1 + expf(-g)) * u (ops_ref.cpp:243-248) over n_blocks 32-blocks, quantized per block.
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                            long n_blocks, int8_t* __restrict__ oq,
-                                                           float* __restrict__ od) {
+                                                           float* __restrict__ od, float* __restrict__ of) {
     const long blk = ((long)blockIdx.x * 256 + threadIdx.x) >> 5;
     if (blk >= n_blocks) return;  // whole half-waves leave together
     const long i = blk * QK + (threadIdx.x & 31);
     const float gv = g[i];
-    quant_block32(gv / (1.0f + dev_expf(-gv)) * u[i], oq + blk * QK, od + blk);
+    const float hv = gv / (1.0f + dev_expf(-gv)) * u[i];
+    if (of) of[i] = hv;  // the f32 input of an unquantized down projection
+    quant_block32(hv, oq + blk * QK, od + blk);
 }
 
 // Prefill gate / up, SwiGLU and quantization of the down projection's input in one launch (model.cpp:212-218 for a
@@ -2085,6 +2109,9 @@ struct Decoder {
     const qh_tensor* lmh = nullptr;  // the LM head: the embedding, or lm_head.weight when untied (model.cpp:16)
     bool hadamard = false;           // FLAG_HADAMARD_DOWN (model_file.h:21)
     bool kv32 = false;               // an f32 KV cache (Model::load kv_f16 false)
+    bool dense = false;              // some matrix is F32 / F16 (matvec_ref): f32 copies of the activations are kept
+    float *fa = nullptr, *fb = nullptr;  // f32 normed layer input [kChunk][dim]; attention / SwiGLU output
+                                         // [kChunk][max(dim, ffn_dim)] (the unquantized matrices' inputs)
     // device state
     uint16_t *kc = nullptr, *vc = nullptr;  // f16 cache (the default)
     float *kcf = nullptr, *vcf = nullptr;   // f32 cache, [n_layers][ctx][kv_dim] each
@@ -2137,6 +2164,7 @@ const float* bias(const Decoder* d, int l, int which) { return d->hp.qkv_bias ? 
 const qh_tensor& head4(const Decoder* d) { return d->t[T_LAYER0 + d->hp.n_layers * L_COUNT]; }
 const qh_tensor& head_err(const Decoder* d) { return d->t[T_LAYER0 + d->hp.n_layers * L_COUNT + 1]; }
 const float* final_norm(const Decoder* d) { return static_cast<const float*>(d->t[T_NORM].data); }
+bool dense_w(const qh_tensor& W) { return W.dtype == kF32 || W.dtype == kF16; }
 
 const uint8_t* quants(const qh_tensor& W) { return static_cast<const uint8_t*>(W.data); }
 const uint16_t* scales(const qh_tensor& W) {
@@ -2195,12 +2223,22 @@ hipError_t plan_dispatch(int dtype, const GemvPlan& p, F&& f) {
 hipError_t embed(Decoder* d, const int32_t* tokens, int n, hipStream_t s) {
     const qh_tensor& emb = d->t[T_EMBED];
     by_row_slots(d->hp.dim, [&](auto r) {
-        qh_launch((embed_norm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, tokens,
-                           reinterpret_cast<const int8_t*>(quants(emb)),
-                           reinterpret_cast<const uint16_t*>(quants(emb) + (size_t)emb.rows * emb.cols), d->hp.dim,
-                           d->hp.vocab_size, d->x, lf(d, 0, L_ATTN_NORM), d->hp.norm_eps, d->qa, d->da, d->status);
+        qh_launch((embed_norm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, tokens, quants(emb),
+                  emb.dtype, d->hp.dim, d->hp.vocab_size, d->x, lf(d, 0, L_ATTN_NORM), d->hp.norm_eps, d->qa, d->da,
+                  d->fa, d->status);
     });
     return hipGetLastError();
+}
+
+// Model::linear / linear_batch (model.cpp:150-157, 336-347) of n tokens into out [n][ldo] (n == 1: out[r]): the
+// integer-dot GEMV / matmul on the quantized activation for a Q8_0 / Q4_0 W, matvec_ref on its f32 copy for an
+// F32 / F16 W. inner: the attention / SwiGLU output (qb / db / fb), else the normed layer input (qa / da / fa).
+hipError_t linear(Decoder* d, float* out, int ldo, const qh_tensor& W, bool inner, int n, hipStream_t s) {
+    if (dense_w(W)) return launch_gemv_dense(out, ldo, W, inner ? d->fb : d->fa, W.cols, n, 0, W.rows, s);
+    const int8_t* xq = inner ? d->qb : d->qa;
+    const float* xd = inner ? d->db : d->da;
+    if (n == 1) return launch_gemv(out, W, xq, xd, 0, W.rows, gemv_plan(W.dtype, W.cols, W.rows), s);
+    return launch_matmul(out, ldo, W, xq, xd, n, 0, W.rows, s);
 }
 
 // The normed-input fill of a decode kernel: layer input from the residual stream x, or (first layer) from the
@@ -2234,7 +2272,7 @@ size_t norm_tile_lds(int cols, int tile_rows, int D) {
 // or the plain GEMV would stream or the tile does not fit.
 bool qkv_plan(const Decoder* d, int l, GemvPlan* p, size_t* lds) {
     const qh_tensor &wq = lt(d, l, L_WQ), &wk = lt(d, l, L_WK), &wv = lt(d, l, L_WV);
-    if (!d->fuse || wq.dtype != wk.dtype || wq.dtype != wv.dtype) return false;
+    if (!d->fuse || dense_w(wq) || wq.dtype != wk.dtype || wq.dtype != wv.dtype) return false;
     *p = gemv_plan(wq.dtype, wq.cols, wq.rows);
     *lds = norm_tile_lds(wq.cols, p->tile_rows, d->hp.dim);
     return !p->stream && *lds <= kFuseLds;
@@ -2263,7 +2301,14 @@ hipError_t launch_qkv_norm(Decoder* d, int l, const GemvPlan& p, size_t lds, con
 
 // x += W . (xq, xd) for one token: the GEMV tile kernel with the add in its epilogue, or (a streaming-size W, or
 // one launch per operation) GEMV into d->o and a separate add.
-hipError_t residual(Decoder* d, const qh_tensor& W, const int8_t* xq, const float* xd, hipStream_t s) {
+hipError_t residual(Decoder* d, const qh_tensor& W, hipStream_t s) {
+    const int8_t* xq = d->qb;
+    const float* xd = d->db;
+    if (dense_w(W)) {
+        QH_TRY(linear(d, d->o, 0, W, true, 1, s));
+        qh_launch(residual_add_kernel, dim3((unsigned)((W.rows + 255) / 256)), dim3(256), 0, s, d->x, d->o, W.rows);
+        return hipGetLastError();
+    }
     const GemvPlan p = gemv_plan(W.dtype, W.cols, W.rows);
     if (d->fuse && !p.stream) {
         const int T = p.tile_rows, nb = W.cols / QK;
@@ -2286,11 +2331,11 @@ hipError_t residual(Decoder* d, const qh_tensor& W, const int8_t* xq, const floa
 hipError_t swiglu_down_input(Decoder* d, int F, int n, hipStream_t s) {
     if (d->hadamard) {
         qh_launch(swiglu_fwht_quant_kernel, dim3((unsigned)(F / 256), (unsigned)n), dim3(256), 0, s, d->g, d->u, F,
-                  d->qb, d->db);
+                  d->qb, d->db, d->fb);
     } else {
         const long nblk = (long)n * F / QK;
         qh_launch(swiglu_quant_kernel, dim3((unsigned)((nblk * QK + 255) / 256)), dim3(256), 0, s, d->g, d->u, nblk,
-                  d->qb, d->db);
+                  d->qb, d->db, d->fb);
     }
     return hipGetLastError();
 }
@@ -2308,7 +2353,7 @@ hipError_t gate_up(Decoder* d, int l, hipStream_t s) {
     const qh_tensor &wg = lt(d, l, L_WG), &wu = lt(d, l, L_WU);
     const int nb = wg.cols / QK;
     const size_t lds = norm_tile_lds(wg.cols, 2 * QK, d->hp.dim);
-    if (d->fuse && !d->hadamard && wg.dtype == wu.dtype && lds <= kFuseLds) {
+    if (d->fuse && !d->hadamard && !d->dense && wg.dtype == wu.dtype && lds <= kFuseLds) {
         const unsigned grid = (unsigned)(wg.rows / QK);
         NormAct act = make_norm(d, false, lf(d, l, L_FFN_NORM));
         act.tlk = 3;
@@ -2323,9 +2368,9 @@ hipError_t gate_up(Decoder* d, int l, hipStream_t s) {
         });
         return hipGetLastError();
     }
-    QH_TRY(norm_quant(d, lf(d, l, L_FFN_NORM), nullptr, s));
-    QH_TRY(launch_gemv(d->g, wg, d->qa, d->da, 0, wg.rows, gemv_plan(wg.dtype, wg.cols, wg.rows), s));
-    QH_TRY(launch_gemv(d->u, wu, d->qa, d->da, 0, wu.rows, gemv_plan(wu.dtype, wu.cols, wu.rows), s));
+    QH_TRY(norm_quant(d, lf(d, l, L_FFN_NORM), d->fa, s));
+    QH_TRY(linear(d, d->g, 0, wg, false, 1, s));
+    QH_TRY(linear(d, d->u, 0, wu, false, 1, s));
     return swiglu_down_input(d, wg.rows, 1, s);
 }
 
@@ -2339,26 +2384,26 @@ hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
         if (hp.head_dim == 64)
             qh_launch((attention_f32_kernel<64>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                       bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
-                      d->kcf + l * layer_kv, d->vcf + l * layer_kv, d->qb, d->db, d->status);
+                      d->kcf + l * layer_kv, d->vcf + l * layer_kv, d->qb, d->db, d->status, d->fb);
         else
             qh_launch((attention_f32_kernel<128>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                       bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
-                      d->kcf + l * layer_kv, d->vcf + l * layer_kv, d->qb, d->db, d->status);
+                      d->kcf + l * layer_kv, d->vcf + l * layer_kv, d->qb, d->db, d->status, d->fb);
         return hipGetLastError();
     }
     if (n == 1 && hp.head_dim == 64 && d->fuse)  // decode: one 16-wave workgroup per head
         qh_launch((attention_decode_kernel<64>), dim3(hp.n_heads / hp.n_kv_heads, hp.n_kv_heads), dim3(1024), 0,
                            s, d->q, d->k, d->v, d->kc + l * layer_k, d->pos, hp.ctx_len, hp.n_heads / hp.n_kv_heads,
                            bias(d, l, L_BQ), bias(d, l, L_BK), hp.n_kv_heads, bias(d, l, L_BV), d->cs,
-                           d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status);
+                           d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status, d->fb);
     else if (hp.head_dim == 64)
         qh_launch((attention_kernel<64, 2>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                            bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
-                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status);
+                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status, d->fb);
     else
         qh_launch((attention_kernel<128>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                            bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
-                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status);
+                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status, d->fb);
     return hipGetLastError();
 }
 
@@ -2369,7 +2414,7 @@ hipError_t decode_layers(Decoder* d, hipStream_t s) {
     for (int l = 0; l < hp.n_layers; ++l) {
         GemvPlan p;
         size_t lds = 0;
-        if (qkv_plan(d, l, &p, &lds)) {
+        if (qkv_plan(d, l, &p, &lds) && (l > 0 || d->t[T_EMBED].dtype == kQ8)) {
             NormAct act = make_norm(d, l == 0, lf(d, l, L_ATTN_NORM));
             act.tlk = 0;
             QH_TRY(launch_qkv_norm(d, l, p, lds, act, s));
@@ -2377,20 +2422,19 @@ hipError_t decode_layers(Decoder* d, hipStream_t s) {
             if (l == 0)
                 QH_TRY(embed(d, d->tokens, 1, s));
             else
-                QH_TRY(norm_quant(d, lf(d, l, L_ATTN_NORM), nullptr, s));
-            const qh_tensor &wq = lt(d, l, L_WQ), &wk = lt(d, l, L_WK), &wv = lt(d, l, L_WV);
-            QH_TRY(launch_gemv(d->q, wq, d->qa, d->da, 0, wq.rows, gemv_plan(wq.dtype, wq.cols, wq.rows), s));
-            QH_TRY(launch_gemv(d->k, wk, d->qa, d->da, 0, wk.rows, gemv_plan(wk.dtype, wk.cols, wk.rows), s));
-            QH_TRY(launch_gemv(d->v, wv, d->qa, d->da, 0, wv.rows, gemv_plan(wv.dtype, wv.cols, wv.rows), s));
+                QH_TRY(norm_quant(d, lf(d, l, L_ATTN_NORM), d->fa, s));
+            QH_TRY(linear(d, d->q, 0, lt(d, l, L_WQ), false, 1, s));
+            QH_TRY(linear(d, d->k, 0, lt(d, l, L_WK), false, 1, s));
+            QH_TRY(linear(d, d->v, 0, lt(d, l, L_WV), false, 1, s));
         }
         d->mark(l * QH_STAGES_PER_LAYER + QH_STAGE_QKV);
         QH_TRY(attention(d, l, 1, s));
         d->mark(l * QH_STAGES_PER_LAYER + QH_STAGE_ATTENTION);
-        QH_TRY(residual(d, lt(d, l, L_WO), d->qb, d->db, s));
+        QH_TRY(residual(d, lt(d, l, L_WO), s));
         d->mark(l * QH_STAGES_PER_LAYER + QH_STAGE_O);
         QH_TRY(gate_up(d, l, s));
         d->mark(l * QH_STAGES_PER_LAYER + QH_STAGE_GATE_UP);
-        QH_TRY(residual(d, lt(d, l, L_WD), d->qb, d->db, s));
+        QH_TRY(residual(d, lt(d, l, L_WD), s));
         d->mark(l * QH_STAGES_PER_LAYER + QH_STAGE_DOWN);
     }
     QH_TRY(norm_quant(d, final_norm(d), d->hidden, s));
@@ -2403,7 +2447,7 @@ hipError_t decode_layers(Decoder* d, hipStream_t s) {
 // (the matmul launch and swiglu_quant_kernel instead: one launch per operation, different formats or widths, rows
 // not a multiple of 32, unaligned operands).
 bool swiglu_fused(Decoder* d, const qh_tensor& wg, const qh_tensor& wu, int n, hipStream_t s) {
-    if (!d->fuse || d->hadamard || wg.dtype != wu.dtype || wg.rows != wu.rows || wg.cols != wu.cols || wg.rows % QK != 0 ||
+    if (!d->fuse || d->hadamard || d->dense || wg.dtype != wu.dtype || wg.rows != wu.rows || wg.cols != wu.cols || wg.rows % QK != 0 ||
         (wg.dtype != kQ8 && wg.dtype != kQ4) || wg.cols % QK != 0 || wg.cols < 2 * QK)
         return false;
     const uint8_t *qg = quants(wg), *qu = quants(wu);
@@ -2450,30 +2494,38 @@ hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
         if (l > 0) {
             by_row_slots(D, [&](auto r) {
                 qh_launch((add_rmsnorm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, d->x,
-                                   d->o, lf(d, l, L_ATTN_NORM), D, hp.norm_eps, d->qa, d->da, nullptr);
+                                   d->o, lf(d, l, L_ATTN_NORM), D, hp.norm_eps, d->qa, d->da, d->fa);
             });
             QH_TRY(hipGetLastError());
         }
         const qh_tensor &wq = lt(d, l, L_WQ), &wk = lt(d, l, L_WK), &wv = lt(d, l, L_WV);
         const MmOut qkv[3] = {{&wq, d->q, wq.rows, 0, wq.rows}, {&wk, d->k, wk.rows, 0, wk.rows},
                               {&wv, d->v, wv.rows, 0, wv.rows}};
-        QH_TRY(matmul_group(qkv, 3, d->qa, d->da, n, s));
+        if (dense_w(wq) || dense_w(wk) || dense_w(wv)) {
+            for (const MmOut& m : qkv) QH_TRY(linear(d, m.out, m.ldo, *m.W, false, n, s));
+        } else {
+            QH_TRY(matmul_group(qkv, 3, d->qa, d->da, n, s));
+        }
         QH_TRY(attention(d, l, n, s));
         const qh_tensor& wo = lt(d, l, L_WO);
-        QH_TRY(launch_matmul(d->o, wo.rows, wo, d->qb, d->db, n, 0, wo.rows, s));
+        QH_TRY(linear(d, d->o, wo.rows, wo, true, n, s));
         by_row_slots(D, [&](auto r) {
             qh_launch((add_rmsnorm_quant_kernel<decltype(r)::value>), dim3(n), dim3(256), 0, s, d->x, d->o,
-                               lf(d, l, L_FFN_NORM), D, hp.norm_eps, d->qa, d->da, nullptr);
+                               lf(d, l, L_FFN_NORM), D, hp.norm_eps, d->qa, d->da, d->fa);
         });
         QH_TRY(hipGetLastError());
         const qh_tensor &wg = lt(d, l, L_WG), &wu = lt(d, l, L_WU), &wd = lt(d, l, L_WD);
         if (!swiglu_fused(d, wg, wu, n, s)) {
             const MmOut gu[2] = {{&wg, d->g, wg.rows, 0, wg.rows}, {&wu, d->u, wu.rows, 0, wu.rows}};
-            QH_TRY(matmul_group(gu, 2, d->qa, d->da, n, s));
+            if (dense_w(wg) || dense_w(wu)) {
+                for (const MmOut& m : gu) QH_TRY(linear(d, m.out, m.ldo, *m.W, false, n, s));
+            } else {
+                QH_TRY(matmul_group(gu, 2, d->qa, d->da, n, s));
+            }
             QH_TRY(swiglu_down_input(d, F, n, s));
         }
         QH_TRY(hipGetLastError());
-        QH_TRY(launch_matmul(d->o, wd.rows, wd, d->qb, d->db, n, 0, wd.rows, s));
+        QH_TRY(linear(d, d->o, wd.rows, wd, true, n, s));
     }
     return hipSuccess;
 }
@@ -2523,7 +2575,10 @@ hipError_t run_head(Decoder* d, int top_k, hipStream_t s, bool advance = false) 
         return launch_shortlist_head(h8, head4(d), head_err(d), d->qa, d->da, q, must, out, d->head_ws, s,
                                      advance ? &fb : nullptr);
     }
-    QH_TRY(launch_gemv(d->logits, h8, d->qa, d->da, 0, h8.rows, gemv_plan(h8.dtype, h8.cols, h8.rows), s));
+    if (dense_w(h8))  // Model::linear on the final normed state itself (matvec_ref)
+        QH_TRY(launch_gemv_dense(d->logits, 0, h8, d->hidden, h8.cols, 1, 0, h8.rows, s));
+    else
+        QH_TRY(launch_gemv(d->logits, h8, d->qa, d->da, 0, h8.rows, gemv_plan(h8.dtype, h8.cols, h8.rows), s));
     return launch_argmax(d->logits, d->hp.vocab_size, d->top1_full, d->am_ws, s);
 }
 
@@ -2542,6 +2597,9 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
     d->lmh = d->t.size() > n_lm && d->t[n_lm].data ? &d->t[n_lm] : &d->t[T_EMBED];
     d->hadamard = (hp->flags & QH_FLAG_HADAMARD_DOWN) != 0;
     d->kv32 = hp->kv_f32 != 0;
+    d->dense = dense_w(*d->lmh);
+    for (int l = 0; l < hp->n_layers; ++l)
+        for (int m : {L_WQ, L_WK, L_WV, L_WO, L_WG, L_WU, L_WD}) d->dense = d->dense || dense_w(lt(d, l, m));
     const int D = hp->dim, F = hp->ffn_dim, V = hp->vocab_size, hd = hp->head_dim;
     const size_t kvd = (size_t)hp->n_kv_heads * hd;
     const size_t kv_bytes = (size_t)hp->n_layers * hp->ctx_len * kvd * 2;
@@ -2572,6 +2630,10 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
     A((void**)&d->qb, (size_t)kChunk * wide);
     A((void**)&d->da, sizeof(float) * kChunk * (wide / QK));
     A((void**)&d->db, sizeof(float) * kChunk * (wide / QK));
+    if (d->dense) {
+        A((void**)&d->fa, sizeof(float) * kChunk * D);
+        A((void**)&d->fb, sizeof(float) * kChunk * wide);
+    }
     d->escr_stride = escr_stride(hp->ctx_len);
     A((void**)&d->escr, sizeof(float) * 2 * (size_t)hp->n_heads * d->escr_stride);  // exp rows, weight rows
     A((void**)&d->tokens, sizeof(int32_t) * kChunk);

@@ -14,7 +14,9 @@
 namespace qh {
 
 constexpr int QK = 32;
-constexpr int kQ8 = 2;  // dtype numbers as in the .qnt file
+constexpr int kF32 = 0;  // dtype numbers as in the .qnt file
+constexpr int kF16 = 1;
+constexpr int kQ8 = 2;
 constexpr int kQ4 = 3;
 
 // IEEE binary16 bits -> binary32 (exact for every input, subnormals included): v_cvt_f32_f16.

@@ -375,6 +375,112 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(const uint
     }
 }
 
+// ------------------------------------------------------------------------- unquantized weights (F32 / F16)
+// matvec_ref (ops_ref.cpp:8-27) for n tokens: out[t * ldo + r] = acc with acc = fma(w_ri, x_ti, acc) from +0 in column
+// order (the reference build contracts acc += w * x into one multiply-add; an F16 weight converts exactly). Every
+// (row, token) chain is serial, so a workgroup owns 64 rows x 4 tokens: each 64-column tile of the rows (coalesced
+// 16-byte loads, F16 widened to f32 as it is staged) and of the 4 tokens' activations is staged in LDS, the next
+// tile's loads in flight while this one is used, and wave w runs the 64 chains of token 4 blockIdx.y + w, lane r on
+// row r (LDS rows padded to 65 floats: the lanes' reads of one column fall in 64 different banks; the activation
+// value is a broadcast). An option off the benchmark's path (the quantized GEMVs are its hot path): written for the
+// exact order first; the serial chain of a row (cols FMAs) bounds it.
+constexpr int kDenseT = 64, kDenseStride = kDenseT + 1;
+template <int DT>
+__global__ __launch_bounds__(256) void gemv_dense_kernel(const uint8_t* __restrict__ W, int cols, int r0, int r1,
+                                                         const float* __restrict__ x, int ldx, int n,
+                                                         float* __restrict__ out, int ldo) {
+    __shared__ float ws[2][64 * kDenseStride];
+    __shared__ __align__(16) float xs[2][4 * kDenseT];
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rbase = r0 + (int)blockIdx.x * 64;
+    const int t = (int)blockIdx.y * 4 + wave;
+    const int ntiles = (cols + kDenseT - 1) / kDenseT;
+    // 16-byte units u = 256 j + tid of the 64 x 64 tile: F32 four per thread (row u / 16, columns 4 (u % 16) ..), F16
+    // two (row u / 8, columns 8 (u % 8) ..). Rows past r1 and columns past cols are clamped (loaded, never used).
+    constexpr int kUnits = DT == kF32 ? 4 : 2;
+    uint4 wr[kUnits];
+    float4 xr = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto load = [&](int tile) {
+        const int c0 = tile * kDenseT;
+#pragma unroll
+        for (int j = 0; j < kUnits; ++j) {
+            const int u = 256 * j + tid;
+            const int row = min(rbase + (DT == kF32 ? u / 16 : u / 8), r1 - 1);
+            if (DT == kF32) {
+                const int c = min(c0 + 4 * (u % 16), cols - 4);
+                wr[j] = *reinterpret_cast<const uint4*>(W + ((size_t)row * cols + c) * 4);
+            } else {
+                const int c = min(c0 + 8 * (u % 8), cols - 8);
+                wr[j] = *reinterpret_cast<const uint4*>(W + ((size_t)row * cols + c) * 2);
+            }
+        }
+        if (tid < 64) {
+            const int tt = min((int)blockIdx.y * 4 + tid / 16, n - 1);
+            const int c = min(c0 + 4 * (tid % 16), cols - 4);
+            xr = *reinterpret_cast<const float4*>(x + (size_t)tt * ldx + c);
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < kUnits; ++j) {
+            const int u = 256 * j + tid;
+            if (DT == kF32) {
+                float* d = &ws[buf][(u / 16) * kDenseStride + 4 * (u % 16)];
+                d[0] = __uint_as_float(wr[j].x);
+                d[1] = __uint_as_float(wr[j].y);
+                d[2] = __uint_as_float(wr[j].z);
+                d[3] = __uint_as_float(wr[j].w);
+            } else {
+                float* d = &ws[buf][(u / 8) * kDenseStride + 8 * (u % 8)];
+                const uint32_t h[4] = {wr[j].x, wr[j].y, wr[j].z, wr[j].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    d[2 * e] = f16_to_f32((uint16_t)(h[e] & 0xffffu));
+                    d[2 * e + 1] = f16_to_f32((uint16_t)(h[e] >> 16));
+                }
+            }
+        }
+        if (tid < 64) reinterpret_cast<float4*>(&xs[buf][(tid / 16) * kDenseT])[tid % 16] = xr;
+    };
+    float acc = 0.0f;
+    const bool run = t < n && rbase + lane < r1;
+    load(0);
+    stage(0);
+    __syncthreads();
+    for (int tile = 0; tile < ntiles; ++tile) {
+        const int buf = tile & 1;
+        if (tile + 1 < ntiles) load(tile + 1);
+        if (run) {
+            const float* wrow = &ws[buf][lane * kDenseStride];
+            const float* xt = &xs[buf][wave * kDenseT];
+            const int cnt = min(kDenseT, cols - tile * kDenseT);  // 64, or 32 for the last tile (cols % 32 == 0)
+            if (cnt == kDenseT) {
+#pragma unroll
+                for (int c = 0; c < kDenseT; ++c) acc = __builtin_fmaf(wrow[c], xt[c], acc);
+            } else {
+#pragma unroll
+                for (int c = 0; c < kDenseT / 2; ++c) acc = __builtin_fmaf(wrow[c], xt[c], acc);
+            }
+        }
+        if (tile + 1 < ntiles) stage(buf ^ 1);
+        __syncthreads();
+    }
+    if (run) out[(size_t)t * ldo + rbase + lane] = acc;
+}
+
+hipError_t launch_gemv_dense(float* out, int ldo, const qh_tensor& W, const float* x, int ldx, int n, int r0, int r1,
+                             hipStream_t s) {
+    const dim3 grid((unsigned)((r1 - r0 + 63) / 64), (unsigned)((n + 3) / 4));
+    const uint8_t* w = static_cast<const uint8_t*>(W.data);
+    if (W.dtype == kF32)
+        qh_launch(gemv_dense_kernel<kF32>, grid, dim3(256), 0, s, w, W.cols, r0, r1, x, ldx, n, out, ldo);
+    else if (W.dtype == kF16)
+        qh_launch(gemv_dense_kernel<kF16>, grid, dim3(256), 0, s, w, W.cols, r0, r1, x, ldx, n, out, ldo);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 hipError_t launch_argmax(const float* logits, int n, int32_t* index, void* ws, hipStream_t s) {
     const int parts = argmax_parts(n);
     uint64_t* part = static_cast<uint64_t*>(ws);

@@ -73,6 +73,9 @@ hipError_t launch_gemv(float* out, const qh_tensor& W, const int8_t* xq, const f
                        const GemvPlan& plan, hipStream_t s);
 hipError_t launch_matmul(float* out, int ldo, const qh_tensor& W, const int8_t* xq, const float* xd, int n,
                          int r0, int r1, hipStream_t s);
+// matvec_ref for F32 / F16 W over n tokens of f32 activations x [n][ldx]: out[t * ldo + r], rows [r0, r1).
+hipError_t launch_gemv_dense(float* out, int ldo, const qh_tensor& W, const float* x, int ldx, int n, int r0, int r1,
+                             hipStream_t s);
 // One matrix of a fused launch: rows [r0, r1) of W, output row r of token t at out[t * ldo + r].
 struct MmOut {
     const qh_tensor* W;

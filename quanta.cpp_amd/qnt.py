@@ -248,6 +248,46 @@ def _f32(a) -> np.ndarray:
     return np.ascontiguousarray(a, np.float32).view(np.uint8).reshape(-1)
 
 
+def synthetic_dense(seed: int, hp: HParams | None = None, dtype: int = F32) -> dict[str, TensorRec]:
+    """A random-init model stored unquantized, as the exporter writes it with --dtype f32 / f16 (scripts/export.py:211-218:
+    every matrix, the embedding included, in that dtype; norms and biases F32): weights N(0, 0.02), rounded to f16 for
+    F16; an lm_head.weight of its own with hp.tied_embeddings false; no shortlist tensors (the shortlist head needs a
+    Q8_0 LM head, model.cpp:49-58). Sub-seeds: seed * 1000 + a fixed index per tensor."""
+    hp = hp or HParams()
+    D, F, V = hp.dim, hp.ffn_dim, hp.vocab_size
+    qd, kvd = hp.n_heads * hp.head_dim, hp.n_kv_heads * hp.head_dim
+    s = lambda i: seed * 1000 + i  # noqa: E731
+
+    def mat(i, rows, cols):
+        w = np.random.default_rng(s(i)).standard_normal((rows, cols)).astype(np.float32) * np.float32(0.02)
+        if dtype == F16:
+            return TensorRec(F16, rows, cols, w.astype(np.float16).view(np.uint8).reshape(-1))
+        return TensorRec(F32, rows, cols, _f32(w))
+
+    t: dict[str, TensorRec] = {"model.embed_tokens.weight": mat(0, V, D),
+                               "model.norm.weight": TensorRec(F32, 1, D, _f32(np.ones(D)), ndim=1)}
+    for l in range(hp.n_layers):
+        p = f"model.layers.{l}."
+        b = 10 + 20 * l
+        t[p + "input_layernorm.weight"] = TensorRec(F32, 1, D, _f32(np.ones(D)), ndim=1)
+        t[p + "post_attention_layernorm.weight"] = TensorRec(F32, 1, D, _f32(np.ones(D)), ndim=1)
+        t[p + "self_attn.q_proj.weight"] = mat(b + 0, qd, D)
+        t[p + "self_attn.k_proj.weight"] = mat(b + 1, kvd, D)
+        t[p + "self_attn.v_proj.weight"] = mat(b + 2, kvd, D)
+        t[p + "self_attn.o_proj.weight"] = mat(b + 3, D, qd)
+        if hp.qkv_bias:
+            g = np.random.default_rng(s(b + 4))
+            t[p + "self_attn.q_proj.bias"] = TensorRec(F32, 1, qd, _f32(g.standard_normal(qd) * 0.02), ndim=1)
+            t[p + "self_attn.k_proj.bias"] = TensorRec(F32, 1, kvd, _f32(g.standard_normal(kvd) * 0.02), ndim=1)
+            t[p + "self_attn.v_proj.bias"] = TensorRec(F32, 1, kvd, _f32(g.standard_normal(kvd) * 0.02), ndim=1)
+        t[p + "mlp.gate_proj.weight"] = mat(b + 5, F, D)
+        t[p + "mlp.up_proj.weight"] = mat(b + 6, F, D)
+        t[p + "mlp.down_proj.weight"] = mat(b + 7, D, F)
+    if not hp.tied_embeddings:
+        t["lm_head.weight"] = mat(1, V, D)
+    return t
+
+
 def synthetic_q4mix(seed: int, hp: HParams | None = None, shortlist: bool = True) -> dict[str, TensorRec]:
     """The random-init q4mix model (tensor name -> record). Sub-seeds: seed * 1000 + a fixed index per tensor. With
     hp.tied_embeddings false an lm_head.weight (Q8_0 [vocab][dim], its own seed) is the LM head, and the shortlist copy

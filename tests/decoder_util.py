@@ -17,7 +17,9 @@ def option_model(g, name):
     qnt = qnt_module()
     hp = qnt.HParams(vocab_size=4096, n_layers=2, tied_embeddings=bool(g[f"{name}_tied"]),
                      flags=int(g[f"{name}_flags"]))
-    return hp, qnt.synthetic_q4mix(int(g[f"{name}_seed"]), hp), not bool(g[f"{name}_kv_f16"])
+    seed, dtype = int(g[f"{name}_seed"]), int(g[f"{name}_dtype"])
+    tens = qnt.synthetic_q4mix(seed, hp) if dtype < 0 else qnt.synthetic_dense(seed, hp, dtype)
+    return hp, tens, not bool(g[f"{name}_kv_f16"])
 
 
 def logits_sha256(logits):

@@ -110,20 +110,23 @@ def make_small(qnt, L):
 # The reference's load-time options on a 2-layer, vocabulary-4096 model of the Qwen2.5-0.5B widths (ffn 4864, a
 # multiple of 256): an untied LM head (lm_head.weight, model.cpp:16), the Hadamard-rotated down projection
 # (FLAG_HADAMARD_DOWN, model.cpp:219, 424; ops_ref.cpp:228-241), the f32 KV cache (--kv-f32, model.cpp:96-104,
-# 197-204), and all three together; (name, seed, tied, flags, kv_f16).
-OPTIONS = (("untied", 17, False, 0, True), ("hadamard", 19, True, 1, True), ("kv_f32", 23, True, 0, False),
-           ("all", 29, False, 1, False))
+# 197-204), and all three together on the q4mix tensors; then unquantized models as the exporter writes them with
+# --dtype f32 / f16 (every matrix and the embedding in that dtype: matvec_ref and get_row, ops_ref.cpp:8-27,
+# 162-192), tied and untied; (name, seed, tied, flags, kv_f16, dtype: -1 for q4mix, else F32 / F16).
+OPTIONS = (("untied", 17, False, 0, True, -1), ("hadamard", 19, True, 1, True, -1), ("kv_f32", 23, True, 0, False, -1),
+           ("all", 29, False, 1, False, -1), ("f32", 31, True, 0, True, 0), ("f16", 37, False, 1, True, 1))
 
 
 def make_options(qnt, L):
     """e2e_options.npz: per variant, the gen flow (batched prefill of a 40-id prompt, 16 greedy shortlist steps) with
     the final normed hidden state, its quantization and the head rows after every forward, then one full-head
-    forward's logits (their sha256)."""
+    forward's logits (their sha256). An unquantized model quantizes nothing (Model::prepare_input), so its hq / hd
+    stay zero."""
     out = {}
-    for name, seed, tied, flags, kv_f16 in OPTIONS:
+    for name, seed, tied, flags, kv_f16, dtype in OPTIONS:
         hp = qnt.HParams(vocab_size=4096, n_layers=2, tied_embeddings=tied, flags=flags)
         path = f"/tmp/quanta_e2e_{name}.qnt"
-        qnt.write_qnt(path, hp, qnt.synthetic_q4mix(seed, hp))
+        qnt.write_qnt(path, hp, qnt.synthetic_q4mix(seed, hp) if dtype < 0 else qnt.synthetic_dense(seed, hp, dtype))
         m = oracle.ref.load_model(path, 4096, 8, kv_f16=kv_f16)
         ids = np.random.default_rng(seed + 1).integers(0, hp.vocab_size, 40).astype(np.int32)
         n_gen = 16
@@ -134,14 +137,15 @@ def make_options(qnt, L):
         logits = np.zeros(hp.vocab_size, np.float32)
         toks = np.zeros(n_gen, np.int32)
         rows = np.zeros(n_gen + 1, np.int32)
+        qp = (lambda a: a.ctypes.data) if dtype < 0 else (lambda a: None)  # noqa: E731
         rows[0] = L.ref_model_forward_batch(m, ids.ctypes.data, len(ids), 0, 1, logits.ctypes.data,
-                                            hidden[0].ctypes.data, hq[0].ctypes.data, hd[0].ctypes.data)
+                                            hidden[0].ctypes.data, qp(hq[0]), qp(hd[0]))
         pos = len(ids)
         for s in range(n_gen):
             tok = int(np.argmax(logits))
             toks[s] = tok
             rows[s + 1] = L.ref_model_forward(m, tok, pos, 1, logits.ctypes.data, hidden[s + 1].ctypes.data,
-                                              hq[s + 1].ctypes.data, hd[s + 1].ctypes.data)
+                                              qp(hq[s + 1]), qp(hd[s + 1]))
             pos += 1
         tok = int(np.argmax(logits))
         full_rows = L.ref_model_forward(m, tok, pos, 0, logits.ctypes.data, None, None, None)
@@ -149,6 +153,7 @@ def make_options(qnt, L):
         oracle.ref.free_model(m)
         os.remove(path)
         out.update({f"{name}_seed": np.int32(seed), f"{name}_tied": np.int32(tied), f"{name}_flags": np.int32(flags),
+                    f"{name}_dtype": np.int32(dtype),
                     f"{name}_kv_f16": np.int32(kv_f16), f"{name}_prompt": ids, f"{name}_out": toks,
                     f"{name}_head_rows": rows, f"{name}_hidden": hidden, f"{name}_hq": hq, f"{name}_hd": hd,
                     f"{name}_full_token": np.int32(tok), f"{name}_full_logits_sha256": np.array(digest(logits))})

@@ -172,7 +172,8 @@ def _desc_and_tensors(qh, flags=0, kv_f32=0, ffn=512, lm=None, shortlist=True):
     (dict(flags=2), "ERR_ARG", b"unknown flags"),
     (dict(flags=1, ffn=480), "ERR_SHAPE", b"ffn_dim % 256"),  # as model.cpp:39-42
     (dict(kv_f32=2), "ERR_ARG", b"kv_f32"),
-    (dict(lm=(1, 1024, 256)), "ERR_DTYPE", b"lm_head must be"),
+    (dict(lm=(7, 1024, 256)), "ERR_DTYPE", b"lm_head: dtype 7 is not"),
+    (dict(lm=(1, 1024, 256)), "ERR_SHAPE", b"bad shortlist head tensors"),  # an F16 LM head with the shortlist
     (dict(lm=(2, 1000, 256)), "ERR_SHAPE", b"lm_head is 1000 x 256"),
     (dict(lm=(3, 1024, 256)), "ERR_SHAPE", b"bad shortlist head tensors"),  # Q8_0 with the shortlist (model.cpp:51)
 ])

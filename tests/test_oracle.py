@@ -303,3 +303,73 @@ def test_oracle_shortlist_equals_reference_build(oracle, ref, synth):
         ns = o["n_seeds"]
         assert sorted(o["rows"][:ns].tolist()) == sorted(r["rows"][:ns].tolist())
         assert o["rows"][ns:].tolist() == r["rows"][ns:].tolist()
+
+
+# ------------------------------------------------------------------ unquantized weights (matvec_ref, get_row)
+
+F32, F16 = 0, 1
+
+
+def _dense(seed, rows, cols, dtype):
+    w = (np.random.default_rng(seed).standard_normal((rows, cols)) * 0.05).astype(np.float32)
+    return w.astype(np.float16).view(np.uint8).reshape(-1) if dtype == F16 else w.view(np.uint8).reshape(-1)
+
+
+def _dense_values(buf, rows, cols, dtype):
+    return (buf.view(np.float16) if dtype == F16 else buf.view(np.float32)).astype(np.float32).reshape(rows, cols)
+
+
+@pytest.mark.parametrize("dtype", [F32, F16])
+def test_matvec_f_exact_arithmetic(oracle, dtype):
+    """matvec_ref (ops_ref.cpp:8-27): each output is the chain acc = rnd(w_i x_i + acc) from +0 in column order (the
+    build's multiply-add contraction), evaluated exactly; the unfused chain rnd(acc + rnd(w_i x_i)) differs."""
+    rows, cols = 12, 160
+    buf = _dense(5 + dtype, rows, cols, dtype)
+    x = (np.random.default_rng(7).standard_normal(cols) * np.exp(np.random.default_rng(8).uniform(-3, 3, cols)))
+    x = x.astype(np.float32)
+    got = oracle.matvec_f(dtype, rows, cols, buf, x)
+    w = _dense_values(buf, rows, cols, dtype)
+    fused, split = np.empty(rows, np.float32), np.empty(rows, np.float32)
+    for r in range(rows):
+        a = b = Fraction(0)
+        for i in range(cols):
+            p = Fraction(float(w[r, i])) * Fraction(float(x[i]))
+            a = f32_round(p + a)
+            b = f32_round(b + f32_round(p))
+        fused[r], split[r] = np.float32(float(a)), np.float32(float(b))
+    assert (bits(got) == bits(fused)).all()
+    assert (bits(got) != bits(split)).any()
+    band = oracle.matvec_f(dtype, rows, cols, buf, x, r0=3, r1=9)
+    assert (bits(band[3:9]) == bits(fused[3:9])).all() and (band[:3] == 0).all() and (band[9:] == 0).all()
+
+
+def test_get_row_every_dtype(oracle, synth):
+    """get_row (ops_ref.cpp:162-192) against an independent dequantization of the .qnt bytes."""
+    rows, cols = 9, 256
+    for dtype in (F32, F16):
+        buf = _dense(3, rows, cols, dtype)
+        want = _dense_values(buf, rows, cols, dtype)
+        for r in (0, 4, 8):
+            assert (bits(oracle.get_row(dtype, rows, cols, buf, r)) == bits(want[r])).all()
+    for dtype in (Q8_0, Q4_0):
+        buf = synth.q8_tensor(3, rows, cols) if dtype == Q8_0 else synth.q4_tensor(3, rows, cols)
+        codes, sc = decode(buf, dtype, rows, cols)
+        want = codes.astype(np.float32) * np.repeat(sc, 32, axis=1)
+        for r in (0, 4, 8):
+            assert (bits(oracle.get_row(dtype, rows, cols, buf, r)) == bits(want[r])).all()
+
+
+def test_oracle_dense_equals_reference_build(oracle, ref, synth):
+    """qo_matvec_f and qo_get_row against the reference's own matvec_ref (through Model::linear's row split) and
+    get_row, at the decoder's shapes."""
+    for dtype in (F32, F16):
+        for n, k in [(896, 896), (128, 896), (4864, 896), (896, 4864)]:
+            buf = _dense(n + k + dtype, n, k, dtype)
+            x = synth.activations(k + dtype, 1, k)[0]
+            assert (bits(oracle.matvec_f(dtype, n, k, buf, x)) == bits(ref.matvec_f(dtype, n, k, buf, x, threads=4))).all()
+    for dtype in (F32, F16, Q8_0, Q4_0):
+        rows, cols = 300, 896
+        buf = (_dense(17, rows, cols, dtype) if dtype in (F32, F16) else
+               synth.q8_tensor(17, rows, cols) if dtype == Q8_0 else synth.q4_tensor(17, rows, cols))
+        for r in (0, 151, 299):
+            assert (bits(oracle.get_row(dtype, rows, cols, buf, r)) == bits(ref.get_row(dtype, rows, cols, buf, r))).all()
