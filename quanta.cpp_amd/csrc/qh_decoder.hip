@@ -783,6 +783,19 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(float* __restric
 // per thread in registers). WPE = 2 (prefill chunks at head_dim 64): a 32 KB stage (256 rows) and two cached K rows
 // per thread, so two workgroups share a CU (LDS under 80 KB, registers under 256 each) and the 448 workgroups of a
 // 14-head chunk run in one round instead of two; their serial chains leave each SIMD mostly idle.
+// Timeline stamps of the chunk's last token, query head 0 (compiled in only with -DQH_TIMELINE; the last launch's
+// stamps stay in qh_tl_pa, qh_timeline_pa_read copies them out).
+#if defined(QH_TIMELINE)
+__device__ uint64_t qh_tl_pa[16];
+#define QH_PASTAMP(i)                                                                                        \
+    do {                                                                                                     \
+        if (blockIdx.x == 0 && blockIdx.y == gridDim.y - 1 && threadIdx.x == 0) qh_tl_pa[i] = __builtin_readcyclecounter(); \
+    } while (0)
+#else
+#define QH_PASTAMP(i) \
+    do {              \
+    } while (0)
+#endif
 template <int HD, int WPE = 1>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void attention_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
@@ -810,6 +823,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
         return;
     }
     const int qd = n_heads * HD, kvd = n_kv * HD, group = n_heads / n_kv, kvh = h / group;
+    QH_PASTAMP(0);
     // V block b of this head: HD uint4 at vbase + b * kvd (in uint4 units, kvd / 8 per position... see vblock())
     const uint4* vc4 = reinterpret_cast<const uint4*>(vc);
     auto vchunk = [&](int blk, int d) { return (size_t)blk * kvd + kvh * HD + d; };  // uint4 index of (block, dim)
@@ -903,6 +917,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     }
     et.store(exptab);
     __syncthreads();
+    QH_PASTAMP(1);
     if (h % group == 0)
         for (int i = tid; i < HD; i += 256) {
             kc[(kchunk(i >> 3, pos) << 3) + (i & 7)] = kloc[t * HD + i];
@@ -978,6 +993,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
         mx = a > mx ? a : mx;
     }
     // the maximum does not depend on the order of comparison
+    QH_PASTAMP(2);
     mx = wave_max_sel(mx);
     if (lane == 0) red[wave] = mx;
     dma_v(0, kVEarly / 2);
@@ -989,6 +1005,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     __syncthreads();
     mx = red[0];
     for (int w = 1; w < 4; ++w) mx = red[w] > mx ? red[w] : mx;
+    QH_PASTAMP(3);
     // exp, kept in LDS, with each lane's exact partial sums below the segment starts
     const bool seg = nrows >= 128;  // uniform; shorter rows keep the single chain
     const int Ls = (nrows / 4) & ~15;
@@ -1001,6 +1018,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
         p2 += j < sg.start(2) ? (double)e : 0.0;
         p3 += j < sg.start(3) ? (double)e : 0.0;
     }
+    QH_PASTAMP(4);
     __shared__ SegShared ssh;
     if (seg) seg_partials(ssh, p1, p2, p3);
     __builtin_amdgcn_s_waitcnt(0);  // the first half of the V DMA
@@ -1019,6 +1037,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
         __syncthreads();
         sum = sum_sh;
     }
+    QH_PASTAMP(5);
     const float inv = 1.0f / sum;
     for (int j = tid; j < nrows; j += 256) {
         att[j] = att[j] * inv;
@@ -1036,6 +1055,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
         }
         __syncthreads();
     }
+    QH_PASTAMP(6);
 
     // out_i = sum_j a_j * v_ji, one FMA per position in order (model.cpp:131-135): thread i per dimension, over
     // the rows of each LDS stage. The weights are broadcast LDS reads of att (every lane the same address), so a
@@ -1137,6 +1157,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
         }
         __syncthreads();
     }
+    QH_PASTAMP(7);
     if (tid < HD) {  // quantize_q8 of the attention output, two 32-blocks per 64 dimensions
         const int col = h * HD + (tid & ~31);
         if (of) of[(size_t)t * qd + h * HD + tid] = acc;  // the f32 input of an unquantized o projection
@@ -2783,6 +2804,10 @@ hipError_t decoder_begin(Decoder* d, int top_k, int32_t* out, int out_cap, hipSt
 int decoder_ctx(const Decoder* d) { return d->hp.ctx_len; }
 
 #if defined(QH_TIMELINE)
+extern "C" int qh_timeline_pa_read(uint64_t* host, int n) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(qh_tl_pa), sizeof(uint64_t) * (n < 16 ? n : 16)) == hipSuccess ? 0 : 1;
+}
+
 extern "C" int qh_timeline_read(uint64_t* host, int n) {
     return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(qh_tl), sizeof(uint64_t) * (size_t)n);
 }
