@@ -211,6 +211,17 @@ def head_bench(qh, synth, torch, oracle, steps, warmup):
     g = capture(torch, full_step)
     sec = time_graph(torch, g, steps, warmup)
     full_us = sec / calls * 1e6
+    del g
+
+    def gemv_step():  # the full head's Q8_0 GEMV alone: the one decode GEMV large enough to stream
+        for c in range(copies):
+            for t in range(n_vec):
+                qh.matvec_q(r8.tensors[c], xq[t], xd[t], out=logits)
+
+    g = capture(torch, gemv_step)
+    sec = time_graph(torch, g, steps, warmup)
+    gemv_us = sec / calls * 1e6
+    gemv_bytes = 1.0625 * V * D + 1.125 * D + 4 * V  # weights and scales, activation, output
     screen = V * (D // 2 + 2 * (D // 32) * 2)
     row8 = D + 2 * (D // 32)
     mean_rows = float(np.mean(rows))
@@ -221,12 +232,42 @@ def head_bench(qh, synth, torch, oracle, steps, warmup):
     return {"shortlist_us": sl_us, "full_head_us": full_us, "mean_rows": mean_rows, "rows": rows,
             "shortlist_bytes": sl_bytes, "full_head_bytes": full_bytes,
             "shortlist_GBps": sl_bytes / sl_us / 1e3, "full_head_GBps": full_bytes / full_us / 1e3,
+            "q8_gemv_151936x896": {"us_per_call": gemv_us, "bytes": gemv_bytes, "GBps": gemv_bytes / gemv_us / 1e3,
+                                   "frac_of_hbm_peak": gemv_bytes / gemv_us / 1e3 / HBM_PEAK_GBS},
             "sweep_1024": {"vectors": n_sweep, "x_seed": 502, "rows_mean": float(sweep_rows.mean()),
                            "rows_median": float(np.median(sweep_rows)),
                            "rows_p99": float(np.percentile(sweep_rows, 99)), "rows_max": float(sweep_rows.max()),
                            "rows_mean_frac_of_vocab": float(sweep_rows.mean() / V),
                            "bytes_mean": float(sweep_bytes.mean()),
                            "bytes_mean_frac_of_full_head": float(sweep_bytes.mean() / full_bytes)}}
+
+
+def sampler_bench(qh, torch, orc, reps=50):
+    """One Sampler::sample draw over 151936 device logits (N(0, 3), seed 503; a 64-id history), per parameter set:
+    top_k 20 (the one-workgroup kernel), 1000 and 0 (qh_sample_ws: radix sort, then the in-order sums). The first
+    draw is checked against the oracle; the time is the mean over `reps` draws captured in one graph."""
+    V = 151936
+    rng = np.random.default_rng(503)
+    host = rng.normal(0.0, 3.0, V).astype(np.float32)
+    hist = rng.integers(0, V, 64).astype(np.int32)
+    logits = torch.from_numpy(host).cuda()
+    hd = torch.from_numpy(hist).cuda()
+    ws = qh.sample_workspace(V)
+    out = {}
+    for name, t in [("topk20_chat", (0.7, 20, 0.8, 0.0, 1.1, 0)), ("topk1000", (1.0, 1000, 0.95, 0.0, 1.1, 0)),
+                    ("topk0_topp0.8", (0.7, 0, 0.8, 0.0, 1.1, 0)), ("topk0_topp1", (1.0, 0, 1.0, 0.0, 1.1, 0))]:
+        pq, po = qh.qh_sampler_params(*t), orc.SamplerParams(*t)
+        st0 = orc.oracle.sampler_seed(7)
+        sd = torch.tensor(np.array([st0], np.uint64).view(np.int64), device="cuda")
+        got = int(qh.sample(logits, pq, sd, hd, ws=ws).cpu().item())
+        want, _, _ = orc.oracle.sample(host, V, hist, po, st0)
+        if got != want:
+            raise SystemExit(f"bench: sampler draw differs from the oracle ({name})")
+        g = capture(torch, lambda: [qh.sample(logits, pq, sd, hd, ws=ws) for _ in range(reps)])
+        sec = time_graph(torch, g, 5, 1)
+        out[name] = {"us_per_draw": sec / (5 * reps) * 1e6, "params": list(t)}
+        del g
+    return out
 
 
 def stage_bytes(hp, pos):
@@ -584,7 +625,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end prefill + decode measurement")
-    ap.add_argument("--only", choices=["e2e", "roofline", "prefill", "sampling", "head", "stages"],
+    ap.add_argument("--only", choices=["e2e", "roofline", "prefill", "sampling", "head", "sampler", "stages"],
                     help="one measurement alone (for counter runs): e2e = --e2e-only; roofline = a 256 MiB copy "
                          "(counter calibration) then the Q4_0 GEMV rotation; prefill = Q4_0 4864x896 and 896x4864 at M = 512, "
                          "then 9728x896 (the decoder's gate + up rows) and 896x4864 (down) at M = 32")
@@ -619,6 +660,9 @@ def main():
     if args.only == "head":
         print(json.dumps({"shortlist_head_151936x896": rnd(head_bench(qh, synth, torch, orc.oracle, 5, 1))}),
               flush=True)
+        return 0
+    if args.only == "sampler":
+        print(json.dumps({"sampler_151936": rnd(sampler_bench(qh, torch, orc))}), flush=True)
         return 0
     if args.only == "sampling":
         hp, tens = e2e_model()
@@ -700,6 +744,8 @@ def main():
                 extra[f"{name}_prefill_{n}x{k}_M{m}"] = rnd(r)
         log("shortlist head")
         extra["shortlist_head_151936x896"] = rnd(head_bench(qh, synth, torch, orc.oracle, 5, 1))
+        log("sampler draws over the full vocabulary")
+        extra["sampler_151936"] = rnd(sampler_bench(qh, torch, orc))
         log("sampling mode: prefill 512 + decode steps of the chat flow")
         extra["sampling_chat"] = rnd(e2e_bench(qh, torch, hp, tens, steps=args.steps, warmup=args.warmup,
                                                mode="chat"))

@@ -210,7 +210,7 @@ typedef struct qh_sampler_params {
     int32_t repeat_window; /* how many recent history ids the penalty looks at; 0 = all */
 } qh_sampler_params;
 
-#define QH_SAMPLE_MAX_TOPK 256       /* survivors of the top-k cut the sampler handles (temperature > 0) */
+#define QH_SAMPLE_MAX_TOPK 256       /* survivors of the top-k cut qh_sample handles without a workspace */
 #define QH_SAMPLE_MAX_VOCAB 262144   /* n_valid limit (the history bitmap lives in LDS) */
 
 /* The generator state a reference Sampler constructed with a nonzero seed starts from (sampler.cpp:10-13). */
@@ -224,11 +224,22 @@ uint64_t qh_sampler_state(uint64_t seed);
  *                      ids whose logits are finite; NULL / NULL to consider every id below n_valid.
  *   history[0, n_hist): DEVICE token history (the session's prompt and generated ids), NULL when n_hist is 0.
  * Requires 1 <= n_valid <= QH_SAMPLE_MAX_VOCAB and, with temperature > 0, min(top_k or n_valid, n_valid) <=
- * QH_SAMPLE_MAX_TOPK. Ties between equal logits in the top-k go to the lower id (unspecified in the reference).
+ * QH_SAMPLE_MAX_TOPK (qh_sample_ws takes any number). Ties between equal logits in the top-k go to the lower id
+ * (unspecified in the reference).
  * Replaces: Sampler::sample (reference sampler.cpp:22-85) and Sampler's generator (sampler.cpp:10-21). */
 int qh_sample(const float* logits, int32_t n_valid, const int32_t* rows, const qh_head_stats* head_stats,
               const int32_t* history, int32_t n_hist, const qh_sampler_params* params, uint64_t* state,
               int32_t* out_id, void* stream);
+
+/* qh_sample with a DEVICE workspace of qh_sample_workspace_bytes(n_valid) bytes (16-byte aligned), which lifts the
+ * QH_SAMPLE_MAX_TOPK limit: any top_k, top_k 0 (every id a survivor) included. More survivors than that are sorted by
+ * a device-wide radix sort (4 passes over the logit half); the softmax sum, top-p, total and draw then run in the reference's order and
+ * stop where the remaining terms can no longer change a rounded result. Calls that share a workspace must not
+ * overlap. Replaces: Sampler::sample (reference sampler.cpp:22-85) with top_k 0 or large. */
+size_t qh_sample_workspace_bytes(int32_t n_valid);
+int qh_sample_ws(const float* logits, int32_t n_valid, const int32_t* rows, const qh_head_stats* head_stats,
+                 const int32_t* history, int32_t n_hist, const qh_sampler_params* params, uint64_t* state,
+                 int32_t* out_id, void* ws, size_t ws_bytes, void* stream);
 
 /* ------------------------------------------------------------------ GPU-resident decoder */
 
@@ -341,7 +352,8 @@ int qh_decoder_step_timed(qh_decoder* d, int top_k, void* stream, float* us_host
 /* The head queries of later prefill / begin / step calls, as Session::head_query builds them from the session's
  * sampler parameters (session.cpp:63-79): top_k = (temperature <= 0 ? 1 : p->top_k), the full head when that is 0,
  * and, when p->repeat_penalty != 1, the last p->repeat_window ids of the token history (all when 0) as must ids. The
- * calls' own top_k argument is then ignored. NULL restores plain queries (the calls' top_k, no must ids).
+ * calls' own top_k argument is then ignored. NULL restores plain queries (the calls' top_k, no must ids). With the
+ * shortlist head tensors, top_k is at most QH_HEAD_MAX_TOPK (QH_ERR_UNSUPPORTED above).
  * Replaces: Session::set_sampler and Session::head_query (reference session.h, session.cpp:63-79). */
 int qh_decoder_set_query(qh_decoder* d, const qh_sampler_params* p);
 

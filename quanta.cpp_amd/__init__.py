@@ -79,7 +79,8 @@ EXPORTS = ("qh_last_error", "qh_version", "qh_init", "qh_quant_bytes", "qh_tenso
            "qh_stream_create", "qh_stream_destroy",
            "qh_quantize_q8", "qh_matvec_q", "qh_matvec_ref", "qh_matmul_q", "qh_argmax_workspace_bytes", "qh_argmax",
            "qh_shortlist_workspace_bytes", "qh_shortlist_head", "qh_shortlist_head_noalloc",
-           "qh_sampler_state", "qh_sample", "qh_decoder_create", "qh_decoder_destroy",
+           "qh_sampler_state", "qh_sample", "qh_sample_workspace_bytes", "qh_sample_ws", "qh_decoder_create",
+           "qh_decoder_destroy",
            "qh_decoder_prefill", "qh_decoder_begin", "qh_decoder_step", "qh_decoder_views", "qh_decoder_step_timed",
            "qh_decoder_set_query",
            "qh_decoder_set_sampler")
@@ -120,6 +121,8 @@ def _bind(lib):
         "qh_decoder_step_timed": ([vp, i32, vp, vp, vp, i32, vp], i32),
         "qh_sampler_state": ([C.c_uint64], C.c_uint64),
         "qh_sample": ([vp, i32, vp, vp, vp, i32, C.POINTER(qh_sampler_params), vp, vp, vp], i32),
+        "qh_sample_workspace_bytes": ([i32], C.c_size_t),
+        "qh_sample_ws": ([vp, i32, vp, vp, vp, i32, C.POINTER(qh_sampler_params), vp, vp, vp, C.c_size_t, vp], i32),
         "qh_decoder_set_query": ([vp, C.POINTER(qh_sampler_params)], i32),
         "qh_decoder_set_sampler": ([vp, C.POINTER(qh_sampler_params), C.c_uint64], i32),
     }
@@ -257,18 +260,27 @@ def sampler_state(seed: int) -> int:
     return int(lib().qh_sampler_state(seed))
 
 
-def sample(logits, params: qh_sampler_params, state, history=None, n_valid: int | None = None, head=None):
+def sample(logits, params: qh_sampler_params, state, history=None, n_valid: int | None = None, head=None,
+           ws=None):
     """One Sampler::sample draw on the device: returns the chosen id as a device int32 tensor of one element.
     state: device uint64 tensor of one element (advanced in place); history: device int32 tensor or None;
-    head: a ShortlistHead whose last call's row list and stats restrict the candidates."""
+    head: a ShortlistHead whose last call's row list and stats restrict the candidates; ws: a device uint8 tensor of
+    sample_workspace_bytes(n_valid) bytes for more than SAMPLE_MAX_TOPK survivors (qh_sample_ws), or None."""
     torch = _torch()
     out = torch.empty(1, dtype=torch.int32, device=logits.device)
     nv = logits.numel() if n_valid is None else n_valid
     nh = 0 if history is None else int(history.numel())
-    _check(lib().qh_sample(_ptr(logits), nv, _ptr(head.rows) if head is not None else None,
-                           _ptr(head.stats_dev) if head is not None else None, _ptr(history) if nh else None, nh,
-                           C.byref(params), _ptr(state), _ptr(out), _stream()))
+    _check(lib().qh_sample_ws(_ptr(logits), nv, _ptr(head.rows) if head is not None else None,
+                              _ptr(head.stats_dev) if head is not None else None, _ptr(history) if nh else None, nh,
+                              C.byref(params), _ptr(state), _ptr(out), _ptr(ws) if ws is not None else None,
+                              0 if ws is None else ws.numel(), _stream()))
     return out
+
+
+def sample_workspace(n_valid: int, device="cuda"):
+    """A device workspace for sample(..., ws=) over n_valid candidates."""
+    torch = _torch()
+    return torch.empty(int(lib().qh_sample_workspace_bytes(n_valid)), dtype=torch.uint8, device=device)
 
 
 class ShortlistHead:

@@ -82,14 +82,14 @@ hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 // The sampler parameters the device sampler handles (a finite temperature; at most QH_SAMPLE_MAX_TOPK survivors of
 // the top-k cut when sampling).
-int check_sampler(const qh_sampler_params& p, int n_valid, const char* who) {
+int check_sampler(const qh_sampler_params& p, int n_valid, const char* who, bool have_ws) {
     if (!(p.temperature == p.temperature) || !(p.repeat_penalty > 0.0f) || p.top_k < 0 || p.repeat_window < 0)
         return fail(QH_ERR_ARG, "%s: bad sampler parameters", who);
-    if (p.temperature > 0.0f) {
+    if (p.temperature > 0.0f && !have_ws) {
         const int k = (p.top_k > 0 && p.top_k < n_valid) ? p.top_k : n_valid;
         if (k > QH_SAMPLE_MAX_TOPK)
-            return fail(QH_ERR_UNSUPPORTED, "%s: %d survivors of the top-k cut (at most %d)", who, k,
-                        QH_SAMPLE_MAX_TOPK);
+            return fail(QH_ERR_UNSUPPORTED, "%s: %d survivors of the top-k cut need a workspace (qh_sample_ws)", who,
+                        k);
     }
     return QH_OK;
 }
@@ -314,16 +314,31 @@ int qh_argmax(const float* logits, int n, int32_t* index, void* workspace, size_
 
 uint64_t qh_sampler_state(uint64_t seed) { return seed | 1u; }
 
+size_t qh_sample_workspace_bytes(int32_t n_valid) {
+    if (n_valid < 1 || n_valid > QH_SAMPLE_MAX_VOCAB) return 0;
+    return sample_workspace_bytes(n_valid);
+}
+
 int qh_sample(const float* logits, int32_t n_valid, const int32_t* rows, const qh_head_stats* head_stats,
               const int32_t* history, int32_t n_hist, const qh_sampler_params* params, uint64_t* state,
               int32_t* out_id, void* stream) {
+    return qh_sample_ws(logits, n_valid, rows, head_stats, history, n_hist, params, state, out_id, nullptr, 0,
+                        stream);
+}
+
+int qh_sample_ws(const float* logits, int32_t n_valid, const int32_t* rows, const qh_head_stats* head_stats,
+                 const int32_t* history, int32_t n_hist, const qh_sampler_params* params, uint64_t* state,
+                 int32_t* out_id, void* ws, size_t ws_bytes, void* stream) {
     if (!logits || !params || !state || !out_id) return fail(QH_ERR_ARG, "qh_sample: null argument");
     if (n_valid < 1 || n_valid > QH_SAMPLE_MAX_VOCAB)
         return fail(QH_ERR_UNSUPPORTED, "qh_sample: n_valid %d outside [1, %d]", n_valid, QH_SAMPLE_MAX_VOCAB);
     if ((rows == nullptr) != (head_stats == nullptr))
         return fail(QH_ERR_ARG, "qh_sample: rows and head_stats go together");
     if (n_hist < 0 || (n_hist > 0 && !history)) return fail(QH_ERR_ARG, "qh_sample: bad history");
-    if (int rc = check_sampler(*params, n_valid, "qh_sample")) return rc;
+    if (ws && (ws_bytes < sample_workspace_bytes(n_valid) || !aligned16(ws)))
+        return fail(QH_ERR_ARG, "qh_sample_ws: workspace of %zu bytes (needs %zu, 16-byte aligned)", ws_bytes,
+                    sample_workspace_bytes(n_valid));
+    if (int rc = check_sampler(*params, n_valid, "qh_sample", ws != nullptr)) return rc;
     HeadMust hist;
     hist.ids = history;
     hist.n = n_hist;
@@ -332,8 +347,9 @@ int qh_sample(const float* logits, int32_t n_valid, const int32_t* rows, const q
         hist.ids = history + (n_hist - params->repeat_window);
         hist.n = params->repeat_window;
     }
-    return check_hip(launch_sample(logits, n_valid, rows, head_stats, hist, *params, state, out_id, as_stream(stream)),
-                     "qh_sample launch");
+    return check_hip(
+        launch_sample(logits, n_valid, rows, head_stats, hist, *params, state, out_id, ws, as_stream(stream)),
+        "qh_sample launch");
 }
 
 size_t qh_shortlist_workspace_bytes(int V, int D, int top_k) {
@@ -483,8 +499,10 @@ int qh_decoder_set_query(qh_decoder* d, const qh_sampler_params* p) {
     if (p) {
         if (!(p->repeat_penalty > 0.0f) || p->repeat_window < 0 || p->top_k < 0 || !(p->temperature == p->temperature))
             return fail(QH_ERR_ARG, "qh_decoder_set_query: bad parameters");
-        if (p->temperature > 0.0f && p->top_k > QH_HEAD_MAX_TOPK)
-            return fail(QH_ERR_UNSUPPORTED, "qh_decoder_set_query: top_k %d above %d", p->top_k, QH_HEAD_MAX_TOPK);
+        // the shortlist head takes up to QH_HEAD_MAX_TOPK; a model without its tensors runs the full head anyway
+        if (p->temperature > 0.0f && p->top_k > QH_HEAD_MAX_TOPK && decoder_has_shortlist(reinterpret_cast<Decoder*>(d)))
+            return fail(QH_ERR_UNSUPPORTED, "qh_decoder_set_query: top_k %d above %d with the shortlist head",
+                        p->top_k, QH_HEAD_MAX_TOPK);
     }
     decoder_set_query(reinterpret_cast<Decoder*>(d), p);
     return QH_OK;
@@ -497,7 +515,7 @@ int qh_decoder_set_sampler(qh_decoder* d, const qh_sampler_params* p, uint64_t s
         const int V = decoder_vocab(reinterpret_cast<Decoder*>(d));
         if (V > QH_SAMPLE_MAX_VOCAB)
             return fail(QH_ERR_UNSUPPORTED, "qh_decoder_set_sampler: vocab %d above %d", V, QH_SAMPLE_MAX_VOCAB);
-        if (int rc = check_sampler(*p, V, "qh_decoder_set_sampler")) return rc;
+        if (int rc = check_sampler(*p, V, "qh_decoder_set_sampler", true)) return rc;
     }
     return check_hip(decoder_set_sampler(reinterpret_cast<Decoder*>(d), p, seed), "qh_decoder_set_sampler");
 }

@@ -2165,6 +2165,7 @@ struct Decoder {
     size_t head_ws_bytes = 0;
     void* am_ws = nullptr;
     size_t am_ws_bytes = 0;
+    void* sample_ws = nullptr;  // the sampler's sorted path (more than QH_SAMPLE_MAX_TOPK survivors)
     int32_t* top1_full = nullptr;
     bool fuse = true;  // fused decode kernels (QH_DECODER_FUSE=0 at creation selects one launch per operation)
     std::vector<void*> allocs;
@@ -2677,6 +2678,7 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
     }
     d->am_ws_bytes = argmax_workspace_bytes(V);
     A(&d->am_ws, d->am_ws_bytes);
+    if (V <= QH_SAMPLE_MAX_VOCAB) A(&d->sample_ws, sample_workspace_bytes(V));
     if (e != hipSuccess) {
         decoder_destroy(d);
         return check_hip(e, "qh_decoder_create allocation");
@@ -2745,7 +2747,7 @@ hipError_t pick_and_advance(Decoder* d, int top_k, bool advance, hipStream_t s) 
     if (d->has_sampler) {
         const HeadMust hist = d->sp.repeat_penalty != 1.f ? history_window(d, d->sp.repeat_window) : HeadMust{};
         QH_TRY(launch_sample(d->logits, d->hp.vocab_size, sl ? d->rows : nullptr, sl ? d->stats : nullptr, hist,
-                             d->sp, d->rng, d->sampled, s));
+                             d->sp, d->rng, d->sampled, d->sample_ws, s));
         pick.sampled = d->sampled;
     }
     qh_launch(advance_kernel, dim3(1), dim3(1), 0, s, pick, token_feedback(d), advance ? 1 : 0);
@@ -2837,6 +2839,8 @@ void decoder_views(Decoder* d, qh_decoder_state* v) {
 }
 
 int decoder_vocab(const Decoder* d) { return d->hp.vocab_size; }
+
+bool decoder_has_shortlist(const Decoder* d) { return head4(d).data != nullptr; }
 
 int decoder_set_query(Decoder* d, const qh_sampler_params* p) {
     d->has_query = p != nullptr;

@@ -153,10 +153,12 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
 
 // Sampler::sample on the device (qh_sample.hip). Candidates: rows[0, hs->n_rows) (the shortlist head's list; every
 // other id counts as -inf) or, with rows null, every id below n_valid; the penalty looks at the ids `hist` names.
-// Requires 1 <= n_valid <= QH_SAMPLE_MAX_VOCAB, and with temperature > 0 at most QH_SAMPLE_MAX_TOPK survivors.
+// Requires 1 <= n_valid <= QH_SAMPLE_MAX_VOCAB; with temperature > 0 and more than QH_SAMPLE_MAX_TOPK survivors, a
+// workspace of sample_workspace_bytes(n_valid) (the sorted path), else ws may be null.
+size_t sample_workspace_bytes(int n_valid);
 hipError_t launch_sample(const float* logits, int n_valid, const int32_t* rows, const qh_head_stats* hs,
                          const HeadMust& hist, const qh_sampler_params& p, uint64_t* state, int32_t* out_id,
-                         hipStream_t s);
+                         void* ws, hipStream_t s);
 
 // GPU-resident decoder (qh_decoder.hip). Tensors in qh_decoder_create order; all sizes validated by the caller.
 struct Decoder;
@@ -170,6 +172,7 @@ void decoder_views(Decoder* d, qh_decoder_state* v);
 int decoder_set_query(Decoder* d, const qh_sampler_params* p);
 hipError_t decoder_set_sampler(Decoder* d, const qh_sampler_params* p, uint64_t seed);
 int decoder_vocab(const Decoder* d);
+bool decoder_has_shortlist(const Decoder* d);
 int decoder_ctx(const Decoder* d);
 
 }  // namespace qh

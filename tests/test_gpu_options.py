@@ -169,3 +169,47 @@ def test_unquantized_models_equal_oracle(qh, oracle, synth, gpu, monkeypatch, ki
     dec.prefill(more, pos, top_k=1)
     assert (bits(dec.hidden()) == bits(r["hidden"])).all() and (bits(dec.logits()) == bits(r["logits"])).all()
     dec.close()
+
+
+@pytest.mark.parametrize("kind", ["options", "dense"])
+def test_option_decode_step_graph_replay_equals_eager(qh, oracle, synth, gpu, kind):
+    """A decode step of a model on the option paths (untied head, Hadamard down projection, f32 cache; or a model mixing
+    F32 / F16 / Q4_0 matrices and a Q4_0 embedding) captured once in a HIP graph and replayed, with eager work between
+    the replays: the same tokens as eager steps, and the final hidden state equal to the oracle's."""
+    import torch
+    qnt = qnt_module()
+    if kind == "options":
+        hp = _narrow(qnt, tied_embeddings=False, flags=1)
+        tens, kv_f32 = qnt.synthetic_q4mix(91, hp), True
+    else:
+        hp = _narrow(qnt, tied_embeddings=False)
+        tens, kv_f32 = _mixed(qnt, synth, hp, 93, 3), False
+    dec = qh.Decoder(hp, tens, ctx_len=256, kv_f32=kv_f32)
+    ids = np.random.default_rng(6).integers(0, hp.vocab_size, 40).astype(np.int32)
+    n = 12
+    dec.prefill(ids, 0, top_k=1)
+    dec.begin(n + 1)
+    for _ in range(n):
+        dec.step(top_k=1)
+    eager = dec.outputs(n + 1).copy()
+    dec.prefill(ids, 0, top_k=1)
+    dec.begin(n + 1)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            dec.step(top_k=1)
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(n):
+        graph.replay()
+        torch.cuda.synchronize()  # eager work of the program between replays
+    assert (dec.outputs(n + 1) == eager).all()
+    orc = oracle_decoder(oracle, hp, tens, ctx_len=256, kv_f32=kv_f32)
+    r = orc.forward_batch(ids, 0, top_k=1)
+    pos = len(ids)
+    for t in eager[:n]:
+        r = orc.forward(int(t), pos, top_k=1)
+        pos += 1
+    assert (bits(dec.hidden()) == bits(r["hidden"])).all()
+    dec.close()
