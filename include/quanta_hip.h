@@ -233,9 +233,9 @@ int qh_sample(const float* logits, int32_t n_valid, const int32_t* rows, const q
 
 /* qh_sample with a DEVICE workspace of qh_sample_workspace_bytes(n_valid) bytes (16-byte aligned), which lifts the
  * QH_SAMPLE_MAX_TOPK limit: any top_k, top_k 0 (every id a survivor) included. More survivors than that are sorted by
- * a device-wide radix sort (4 passes over the logit half); the softmax sum, top-p, total and draw then run in the reference's order and
- * stop where the remaining terms can no longer change a rounded result. Calls that share a workspace must not
- * overlap. Replaces: Sampler::sample (reference sampler.cpp:22-85) with top_k 0 or large. */
+ * a device-wide radix sort (4 passes over the logit half); the softmax sum, top-p, total and draw then run in the
+ * reference's order and stop where the remaining terms can no longer change a rounded result. Calls that share a
+ * workspace must not overlap. Replaces: Sampler::sample (reference sampler.cpp:22-85) with top_k 0 or large. */
 size_t qh_sample_workspace_bytes(int32_t n_valid);
 int qh_sample_ws(const float* logits, int32_t n_valid, const int32_t* rows, const qh_head_stats* head_stats,
                  const int32_t* history, int32_t n_hist, const qh_sampler_params* params, uint64_t* state,
