@@ -103,8 +103,11 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const float* __restric
     const int k = (p.top_k > 0 && p.top_k < n_valid) ? p.top_k : n_valid;  // <= QH_SAMPLE_MAX_TOPK (host check)
     if (tid < 32) exptab[tid] = tabv;  // read after the barriers below
     uint64_t thr;
-    if (n > kThreads) {  // lower bound on the k-th largest key: the k-th largest of the threads' own maxima (k
-                         // distinct candidates are at or above it)
+    // Lower bound on the k-th largest key. The head's row list starts with its seeds (the k + 8 best coarse scores),
+    // so for k <= 64 the first 64 entries already hold k candidates: each wave's k-th largest of its 64 bounds it.
+    // Past 1024 candidates otherwise: the k-th largest of the threads' own maxima (k distinct candidates are at or
+    // above it).
+    if (n > kThreads && (!rows || k > 64)) {
         uint64_t m = 0;
 #pragma unroll 8
         for (int i = tid; i < n; i += kThreads) {
@@ -117,7 +120,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const float* __restric
         bitonic_sort_desc_u64<kThreads>(pool, kThreads);
         thr = pool[k - 1];
         __syncthreads();  // pool is refilled below
-    } else {  // the k-th largest of the wave's 64 candidates (when k <= 64)
+    } else {  // the k-th largest of each wave's 64 candidates (when k <= 64)
         const int i = wave * 64 + lane;
         const uint64_t a = i < n ? key_of(i) : 0ull;
         int rank = 0;
