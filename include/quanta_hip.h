@@ -43,6 +43,13 @@ enum {
 /* Tensor dtypes, numbered as the .qnt file stores them (reference model_file.h:16, DType). */
 enum { QH_F32 = 0, QH_F16 = 1, QH_Q8_0 = 2, QH_Q4_0 = 3 };
 
+/* A device-only layout, never a .qnt dtype: a Q8_0 [rows][cols] head as nibble planes (qh_head_planes), the same
+ * int8 values q = 16 h + l with h = floor(q / 16) in [-8, 7] and l = q - 16 h in [0, 15], in as many bytes as the
+ * Q8_0 tensor: the high plane [rows][cols/2] (Q4_0 blocks of the codes h + 8), the low plane [rows][cols/2] (Q4_0
+ * blocks of l, no offset), then the Q8_0 fp16 scales [rows][cols/32] unchanged. The shortlist head screens with the
+ * high plane alone (reference research/head_deep.py:68-78, docs/PROGRESS.md:121-130). */
+enum { QH_Q8_0_PLANES = 16 };
+
 /* Quantization block size (reference model_file.h:17, QK). */
 #define QH_QK 32
 
@@ -197,6 +204,26 @@ int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_t
  * hipMalloc. */
 int qh_shortlist_head_noalloc(const qh_tensor* head8, const qh_tensor* head4, const qh_tensor* err, const int8_t* xq,
                               const float* xd, const qh_head_query* query, const qh_head_out* out, void* stream);
+
+/* The nibble-plane layout of a Q8_0 [V][D] head (D a multiple of 64): writes qh_tensor_bytes(QH_Q8_0_PLANES, V, D)
+ * bytes (the Q8_0 tensor's size) at `planes`, a 16-byte aligned DEVICE buffer that must not overlap head8's data.
+ * The caller may free the Q8_0 copy afterwards: the planes hold the same values, so the exact rows (and an embedding
+ * lookup) can be read from them.
+ * Replaces: the research layout "the Q8 ints stored as two nibble planes" (reference research/head_deep.py:8-10,
+ *           68-78; docs/PROGRESS.md:121-130); the reference engine keeps the Q8_0 head and a separate Q4_0 copy. */
+int qh_head_planes(const qh_tensor* head8, void* planes, void* stream);
+
+/* The Exact Shortlist Head over a nibble-plane head alone (planes: QH_Q8_0_PLANES [V][D]), with no extra copy:
+ * the screen reads the high plane and the scales (coarse = the chain acc = fma(float(sum_i (16 h_i + 8) x_i) * d_b,
+ * dx_b, acc), the values at the midpoints of their high-nibble buckets; bound = fma(sum_b fma(d_b, (8 dx_b) *
+ * sum_i |x_i|), 1.001, 1e-5), since |q - (16 h + 8)| = |l - 8| <= 8), then the same seeds, tau, candidates, must ids
+ * and greedy argmax as qh_shortlist_head; exact rows are rebuilt from both planes, so every rescored logit is
+ * bit-identical to the full Q8_0 head's. Outputs and workspace as qh_shortlist_head
+ * (qh_shortlist_workspace_bytes(V, D, top_k)).
+ * Replaces: the scope's nibble-plane shortlist variant (reference research/head_deep.py:68-78 "hi4, analytic
+ *           bound", docs/PROGRESS.md:121-130) run through Model::shortlist_head's procedure (model.cpp:240-334). */
+int qh_shortlist_planes(const qh_tensor* planes, const int8_t* xq, const float* xd, const qh_head_query* query,
+                        const qh_head_out* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ sampler */
 

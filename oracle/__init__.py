@@ -71,6 +71,10 @@ class _Oracle:
         L.qo_shortlist_head.argtypes = [_u8p, _u8p, _u16p, _int, _int, _i8p, _f32p, _int, _int, C.c_void_p, _int,
                                         _f32p, _f32p, _f32p, _i32p, C.POINTER(_int), C.POINTER(_f), C.POINTER(_int)]
         L.qo_shortlist_head.restype = _int
+        L.qo_head_planes.argtypes = [_u8p, _int, _int, _u8p]
+        L.qo_shortlist_planes.argtypes = [_u8p, _int, _int, _i8p, _f32p, _int, _int, C.c_void_p, _int, _f32p, _f32p,
+                                          _f32p, _i32p, C.POINTER(_int), C.POINTER(_f), C.POINTER(_int)]
+        L.qo_shortlist_planes.restype = _int
 
         L.qo_f32_to_f16.argtypes, L.qo_f32_to_f16.restype = [_f], C.c_uint16
         L.qo_decoder_create.argtypes = [_i32p, np.ctypeslib.ndpointer(np.float32), C.c_void_p, _i32p]
@@ -202,6 +206,29 @@ class _Oracle:
                                        top_k, n_valid, must_arr.ctypes.data if must_arr.size else None,
                                        must_arr.size, logits, coarse, upper, rows, C.byref(ns), C.byref(tau),
                                        C.byref(tie))
+        return dict(logits=logits, coarse=coarse, upper=upper, rows=rows[:n].copy(), n_rows=n,
+                    n_seeds=ns.value, tau=tau.value, seed_tie=bool(tie.value))
+
+    def head_planes(self, head8, V, D):
+        """The nibble-plane layout of a Q8_0 [V][D] head (qo_head_planes): uint8 of the Q8_0 tensor's size."""
+        head8 = np.ascontiguousarray(head8, np.uint8)
+        planes = np.empty(V * D + V * D // 16, np.uint8)
+        self.lib.qo_head_planes(head8, V, D, planes)
+        return planes
+
+    def shortlist_planes(self, planes, V, D, xq, xd, top_k=1, n_valid=0, must=None):
+        """The shortlist head over the nibble planes alone (qo_shortlist_planes); outputs as shortlist_head."""
+        must_arr = np.ascontiguousarray(must if must is not None else [], np.int32)
+        logits = np.empty(V, np.float32)
+        coarse = np.empty(V, np.float32)
+        upper = np.empty(V, np.float32)
+        rows = np.empty(V + must_arr.size, np.int32)
+        ns, tau, tie = _int(0), _f(0), _int(0)
+        n = self.lib.qo_shortlist_planes(np.ascontiguousarray(planes, np.uint8), V, D,
+                                         np.ascontiguousarray(xq, np.int8), np.ascontiguousarray(xd, np.float32),
+                                         top_k, n_valid, must_arr.ctypes.data if must_arr.size else None,
+                                         must_arr.size, logits, coarse, upper, rows, C.byref(ns), C.byref(tau),
+                                         C.byref(tie))
         return dict(logits=logits, coarse=coarse, upper=upper, rows=rows[:n].copy(), n_rows=n,
                     n_seeds=ns.value, tau=tau.value, seed_tie=bool(tie.value))
 

@@ -177,26 +177,97 @@ typedef struct {
 /* Higher score first; lower row first among equal scores. */
 static int better(float sa, int ra, float sb, int rb) { return sa > sb || (sa == sb && ra < rb); }
 
-int qo_shortlist_head(const uint8_t* head8, const uint8_t* head4, const uint16_t* err, int V, int D,
-                      const int8_t* xq, const float* xd, int top_k, int n_valid, const int* must, int n_must,
-                      float* logits, float* coarse, float* upper, int* rows, int* n_seeds_out, float* tau_out,
-                      int* seed_tie) {
+/* Where one head call reads its rows: the Q8_0 head with its Q4_0 copy and f16 block errors (the engine's layout,
+ * model.cpp:47-58), or the Q8_0 head alone as nibble planes (qo_head_planes). */
+typedef struct {
+    int planes;
+    const uint8_t* head8;
+    const uint16_t* s8;
+    const uint8_t* head4;
+    const uint16_t* s4;
+    const uint16_t* err;
+    const uint8_t* hi; /* planes: high nibbles [V][D/2], low nibbles [V][D/2], scales [V][D/32] */
+    const uint8_t* lo;
+    const uint16_t* ps;
+} head_src;
+
+/* One 32-block of the head rebuilt from the nibble planes: q = 16 * h + l, h = (high nibble) - 8, l = low nibble. */
+static void planes_block(const head_src* h, int D, int r, int b, int8_t* q) {
+    const size_t off = ((size_t)r * (D / QO_QK) + b) * (QO_QK / 2);
+    for (int j = 0; j < QO_QK / 2; ++j) {
+        const uint8_t hb = h->hi[off + j], lb = h->lo[off + j];
+        q[j] = (int8_t)(16 * ((int)(hb & 15u) - 8) + (int)(lb & 15u));
+        q[j + QO_QK / 2] = (int8_t)(16 * ((int)(hb >> 4) - 8) + (int)(lb >> 4));
+    }
+}
+
+/* Exact logit of row r: the Q8_0 chain of row_dot (from the planes, over the rebuilt int8 values). */
+static float head_exact(const head_src* h, int D, int r, const int8_t* xq, const float* xd) {
+    if (!h->planes) return row_dot(QO_Q8_0, D, h->head8, h->s8, r, xq, xd);
+    const int nb = D / QO_QK;
+    float acc = 0.f;
+    for (int b = 0; b < nb; ++b) {
+        int8_t q[QO_QK];
+        planes_block(h, D, r, b, q);
+        const int32_t s = block_dot_q8(q, xq + (size_t)b * QO_QK);
+        const float p = (float)s * qo_fp16_to_f32(h->ps[(size_t)r * nb + b]);
+        acc = fmaf(p, xd[b], acc);
+    }
+    return acc;
+}
+
+/* Screen of row r: the coarse score and its bound (before the slack).
+ *   engine layout (model.cpp:263-271): coarse = the Q4_0 copy's chain, bound = sum_b fma(err_b, xnorm_b);
+ *   planes (research/head_deep.py:68-78, restated over the int8 activation): coarse = the chain of
+ *     float(sum_i (16 h_i + 8) x_i) * d_b, i.e. every value at the midpoint of its 16-wide high-nibble bucket, and
+ *     bound = sum_b fma(d_b, bop_b) with bop_b = (8 * dx_b) * sum_i |x_i|: |q - (16 h + 8)| = |l - 8| <= 8. */
+static float head_screen(const head_src* h, int D, int r, const int8_t* xq, const float* xd, const float* bop,
+                         float* bound_out) {
+    const int nb = D / QO_QK;
+    float bound = 0.f, c = 0.f;
+    if (!h->planes) {
+        c = row_dot(QO_Q4_0, D, h->head4, h->s4, r, xq, xd);
+        const uint16_t* e = h->err + (size_t)r * nb;
+        for (int b = 0; b < nb; ++b) bound = fmaf(qo_fp16_to_f32(e[b]), bop[b], bound);
+    } else {
+        for (int b = 0; b < nb; ++b) {
+            /* the high plane only: h = nibble - 8 */
+            const uint8_t* hb = h->hi + ((size_t)r * nb + b) * (QO_QK / 2);
+            const int8_t* xb = xq + (size_t)b * QO_QK;
+            int32_t s = 0;
+            for (int j = 0; j < QO_QK / 2; ++j) {
+                s += (16 * ((int)(hb[j] & 15u) - 8) + 8) * (int32_t)xb[j];
+                s += (16 * ((int)(hb[j] >> 4) - 8) + 8) * (int32_t)xb[j + QO_QK / 2];
+            }
+            const float d = qo_fp16_to_f32(h->ps[(size_t)r * nb + b]);
+            c = fmaf((float)s * d, xd[b], c);
+            bound = fmaf(d, bop[b], bound);
+        }
+    }
+    *bound_out = bound;
+    return c;
+}
+
+static int shortlist_core(const head_src* h, int V, int D, const int8_t* xq, const float* xd, int top_k, int n_valid,
+                          const int* must, int n_must, float* logits, float* coarse, float* upper, int* rows,
+                          int* n_seeds_out, float* tau_out, int* seed_tie) {
     const int nb = D / QO_QK;
     const int nv = (n_valid > 0 && n_valid < V) ? n_valid : V; /* model.cpp:245 */
     const int k = top_k;
     const int n_seed = k + 8; /* model.cpp:256 */
-    const uint16_t* s8 = (const uint16_t*)(head8 + qo_quant_bytes(QO_Q8_0, V, D));
-    const uint16_t* s4 = (const uint16_t*)(head4 + qo_quant_bytes(QO_Q4_0, V, D));
 
-    /* model.cpp:247-251: xnorm_b = d_b * sqrt(sum q^2) (an exact integer sum below 2^24). */
-    float* xnorm = (float*)malloc(sizeof(float) * (size_t)nb);
+    /* The bound's per-block operands. Engine layout (model.cpp:247-251): xnorm_b = d_b * sqrt(sum q^2) (an exact
+     * integer sum below 2^24). Planes: (8 * d_b) * sum |q| (an exact integer below 2^24). */
+    float* bop = (float*)malloc(sizeof(float) * (size_t)nb);
     for (int b = 0; b < nb; ++b) {
         float ss = 0.f;
+        int l1 = 0;
         for (int i = 0; i < QO_QK; ++i) {
             const float v = (float)xq[b * QO_QK + i];
             ss = fmaf(v, v, ss);
+            l1 += abs((int)xq[b * QO_QK + i]);
         }
-        xnorm[b] = xd[b] * sqrtf(ss);
+        bop[b] = h->planes ? (8.f * xd[b]) * (float)l1 : xd[b] * sqrtf(ss);
     }
 
     /* mark: 1 = must id (kept out of seeds and candidates), 2 = seed (already exact). */
@@ -209,11 +280,9 @@ int qo_shortlist_head(const uint8_t* head8, const uint8_t* head4, const uint16_t
     scored_t* seeds = (scored_t*)malloc(sizeof(scored_t) * (size_t)(n_seed + 1));
     int ns = 0;
     for (int r = 0; r < V; ++r) {
-        const float c = row_dot(QO_Q4_0, D, head4, s4, r, xq, xd);
-        const uint16_t* e = err + (size_t)r * nb;
-        float bound = 0.f;
-        for (int b = 0; b < nb; ++b) bound = fmaf(qo_fp16_to_f32(e[b]), xnorm[b], bound);
-        bound = fmaf(bound, 1.001f, 1e-5f);
+        float bound;
+        const float c = head_screen(h, D, r, xq, xd, bop, &bound);
+        bound = fmaf(bound, 1.001f, 1e-5f); /* model.cpp:271 */
         coarse[r] = c;
         upper[r] = c + bound;
         logits[r] = -INFINITY;
@@ -249,7 +318,7 @@ int qo_shortlist_head(const uint8_t* head8, const uint8_t* head4, const uint16_t
         const int r = seeds[i].row;
         rows[n_rows++] = r;
         mark[r] = 2;
-        logits[r] = row_dot(QO_Q8_0, D, head8, s8, r, xq, xd);
+        logits[r] = head_exact(h, D, r, xq, xd);
     }
     float tau = -INFINITY;
     if (ns >= k) {
@@ -272,7 +341,7 @@ int qo_shortlist_head(const uint8_t* head8, const uint8_t* head4, const uint16_t
     for (int r = 0; r < nv; ++r)
         if (!mark[r] && upper[r] >= tau) {
             rows[n_rows++] = r;
-            logits[r] = row_dot(QO_Q8_0, D, head8, s8, r, xq, xd);
+            logits[r] = head_exact(h, D, r, xq, xd);
         }
     /* must ids, first occurrence only (model.cpp:324-330) */
     for (int i = 0; i < n_must; ++i) {
@@ -280,7 +349,7 @@ int qo_shortlist_head(const uint8_t* head8, const uint8_t* head4, const uint16_t
         if (id >= 0 && id < nv && mark[id] == 1) {
             rows[n_rows++] = id;
             mark[id] = 0;
-            logits[id] = row_dot(QO_Q8_0, D, head8, s8, id, xq, xd);
+            logits[id] = head_exact(h, D, id, xq, xd);
         }
     }
 
@@ -289,8 +358,57 @@ int qo_shortlist_head(const uint8_t* head8, const uint8_t* head4, const uint16_t
     if (seed_tie) *seed_tie = tie;
     free(seeds);
     free(mark);
-    free(xnorm);
+    free(bop);
     return n_rows;
+}
+
+int qo_shortlist_head(const uint8_t* head8, const uint8_t* head4, const uint16_t* err, int V, int D,
+                      const int8_t* xq, const float* xd, int top_k, int n_valid, const int* must, int n_must,
+                      float* logits, float* coarse, float* upper, int* rows, int* n_seeds_out, float* tau_out,
+                      int* seed_tie) {
+    head_src h;
+    memset(&h, 0, sizeof(h));
+    h.head8 = head8;
+    h.s8 = (const uint16_t*)(head8 + qo_quant_bytes(QO_Q8_0, V, D));
+    h.head4 = head4;
+    h.s4 = (const uint16_t*)(head4 + qo_quant_bytes(QO_Q4_0, V, D));
+    h.err = err;
+    return shortlist_core(&h, V, D, xq, xd, top_k, n_valid, must, n_must, logits, coarse, upper, rows, n_seeds_out,
+                          tau_out, seed_tie);
+}
+
+void qo_head_planes(const uint8_t* head8, int V, int D, uint8_t* planes) {
+    /* q = 16 * h + l with h = floor(q / 16) in [-8, 7] and l = q - 16 h in [0, 15] (research/head_deep.py:72-73:
+     * h4 = floor(q / 16)); each plane packed as Q4_0 blocks (byte j: element j low, element j + 16 high), the high
+     * plane's nibble h + 8 as a Q4_0 code. The scales follow unchanged. */
+    const size_t n = (size_t)V * (size_t)D;
+    const int8_t* q = (const int8_t*)head8;
+    uint8_t* hi = planes;
+    uint8_t* lo = planes + n / 2;
+    for (size_t blk = 0; blk < n / QO_QK; ++blk) {
+        const int8_t* qb = q + blk * QO_QK;
+        for (int j = 0; j < QO_QK / 2; ++j) {
+            const int a = qb[j], c = qb[j + QO_QK / 2];
+            const int ha = (int)floor(a / 16.0), hc = (int)floor(c / 16.0);
+            hi[blk * (QO_QK / 2) + j] = (uint8_t)((ha + 8) | ((hc + 8) << 4));
+            lo[blk * (QO_QK / 2) + j] = (uint8_t)((a - 16 * ha) | ((c - 16 * hc) << 4));
+        }
+    }
+    memcpy(planes + n, head8 + n, n / QO_QK * 2);
+}
+
+int qo_shortlist_planes(const uint8_t* planes, int V, int D, const int8_t* xq, const float* xd, int top_k,
+                        int n_valid, const int* must, int n_must, float* logits, float* coarse, float* upper,
+                        int* rows, int* n_seeds_out, float* tau_out, int* seed_tie) {
+    const size_t n = (size_t)V * (size_t)D;
+    head_src h;
+    memset(&h, 0, sizeof(h));
+    h.planes = 1;
+    h.hi = planes;
+    h.lo = planes + n / 2;
+    h.ps = (const uint16_t*)(planes + n);
+    return shortlist_core(&h, V, D, xq, xd, top_k, n_valid, must, n_must, logits, coarse, upper, rows, n_seeds_out,
+                          tau_out, seed_tie);
 }
 
 /* ---------------------------------------------------------------- threaded CPU baseline */

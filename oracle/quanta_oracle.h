@@ -71,6 +71,19 @@ int qo_shortlist_head(const uint8_t* head8, const uint8_t* head4, const uint16_t
                       float* logits, float* coarse, float* upper, int* rows, int* n_seeds, float* tau,
                       int* seed_tie);
 
+/* Nibble planes of a Q8_0 [V][D] head (the scope's nibble-plane shortlist variant, research/head_deep.py:68-78,
+ * docs/PROGRESS.md:121-130): each int8 q = 16 h + l with h = floor(q / 16) in [-8, 7], l in [0, 15]. planes receives
+ * V*D + V*D/16 bytes, the size of the Q8_0 tensor: the high plane [V][D/2] (Q4_0 packing of the codes h + 8), the low
+ * plane [V][D/2] (Q4_0 packing of l) and the Q8_0 scales [V][D/32] unchanged. */
+void qo_head_planes(const uint8_t* head8, int V, int D, uint8_t* planes);
+
+/* qo_shortlist_head over the nibble planes alone: the screen reads the high plane and the scales (coarse = the chain
+ * of float(sum_i (16 h_i + 8) x_i) * d_b, bound = sum_b fma(d_b, (8 dx_b) * sum_i |x_i|), then the same slack,
+ * seeds, tau, candidates and must ids), exact rows are the Q8_0 rows rebuilt from both planes. Same outputs. */
+int qo_shortlist_planes(const uint8_t* planes, int V, int D, const int8_t* xq, const float* xd, int top_k,
+                        int n_valid, const int* must, int n_must, float* logits, float* coarse, float* upper,
+                        int* rows, int* n_seeds, float* tau, int* seed_tie);
+
 /* Greedy token: first index of the maximum over logits[0, n) (sampler.cpp:35-37). */
 int qo_argmax(const float* logits, int n);
 

@@ -17,6 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libquanta_hip.so")
 QK = 32
 F32, F16, Q8_0, Q4_0 = 0, 1, 2, 3
+Q8_0_PLANES = 16  # device-only nibble-plane layout of a Q8_0 head (qh_head_planes)
 HEAD_MAX_TOPK = 256
 NOALLOC_SCRATCH_BYTES = 4 << 20  # QH_NOALLOC_SCRATCH_BYTES
 # status codes (quanta_hip.h)
@@ -79,6 +80,7 @@ EXPORTS = ("qh_last_error", "qh_version", "qh_init", "qh_quant_bytes", "qh_tenso
            "qh_stream_create", "qh_stream_destroy",
            "qh_quantize_q8", "qh_matvec_q", "qh_matvec_ref", "qh_matmul_q", "qh_argmax_workspace_bytes", "qh_argmax",
            "qh_shortlist_workspace_bytes", "qh_shortlist_head", "qh_shortlist_head_noalloc",
+           "qh_head_planes", "qh_shortlist_planes",
            "qh_sampler_state", "qh_sample", "qh_sample_workspace_bytes", "qh_sample_ws", "qh_decoder_create",
            "qh_decoder_destroy",
            "qh_decoder_prefill", "qh_decoder_begin", "qh_decoder_step", "qh_decoder_views", "qh_decoder_step_timed",
@@ -112,6 +114,9 @@ def _bind(lib):
                                vp, sz, vp], i32),
         "qh_shortlist_head_noalloc": ([C.POINTER(qh_tensor)] * 3 + [vp, vp, C.POINTER(qh_head_query),
                                        C.POINTER(qh_head_out), vp], i32),
+        "qh_head_planes": ([C.POINTER(qh_tensor), vp, vp], i32),
+        "qh_shortlist_planes": ([C.POINTER(qh_tensor), vp, vp, C.POINTER(qh_head_query), C.POINTER(qh_head_out), vp,
+                                 sz, vp], i32),
         "qh_decoder_create": ([C.POINTER(qh_model_desc), C.POINTER(qh_tensor), i32, C.POINTER(vp)], i32),
         "qh_decoder_destroy": ([vp], i32),
         "qh_decoder_prefill": ([vp, vp, i32, i32, i32, vp], i32),
@@ -283,10 +288,19 @@ def sample_workspace(n_valid: int, device="cuda"):
     return torch.empty(int(lib().qh_sample_workspace_bytes(n_valid)), dtype=torch.uint8, device=device)
 
 
-class ShortlistHead:
-    """Device-resident Exact Shortlist Head: Q8_0 head, its Q4_0 copy and f16 block error bounds."""
+def head_planes(head8: DeviceTensor) -> DeviceTensor:
+    """The nibble-plane layout of a Q8_0 head (qh_head_planes), a new device tensor of the same size."""
+    torch = _torch()
+    buf = torch.empty(tensor_bytes(Q8_0_PLANES, head8.rows, head8.cols), dtype=torch.uint8, device=head8.buf.device)
+    _check(lib().qh_head_planes(C.byref(head8.view), _ptr(buf), _stream()))
+    return DeviceTensor(buf, Q8_0_PLANES, head8.rows, head8.cols)
 
-    def __init__(self, head8: DeviceTensor, head4: DeviceTensor, err: DeviceTensor, top_k: int = 1):
+
+class ShortlistHead:
+    """Device-resident Exact Shortlist Head: Q8_0 head, its Q4_0 copy and f16 block error bounds; or a nibble-plane
+    head alone (head8 of dtype Q8_0_PLANES, head4 and err None: qh_shortlist_planes)."""
+
+    def __init__(self, head8: DeviceTensor, head4: DeviceTensor | None, err: DeviceTensor | None, top_k: int = 1):
         torch = _torch()
         self.head8, self.head4, self.err = head8, head4, err
         self.V, self.D = head8.rows, head8.cols
@@ -316,6 +330,10 @@ class ShortlistHead:
         q = qh_head_query(k, n_valid, must.data_ptr() if n_must else None, n_must)
         o = qh_head_out(self.logits.data_ptr(), self.coarse.data_ptr(), self.upper.data_ptr(), self.rows.data_ptr(),
                         self.stats_dev.data_ptr())
+        if self.head8.dtype == Q8_0_PLANES:
+            _check(lib().qh_shortlist_planes(C.byref(self.head8.view), _ptr(xq), _ptr(xd), C.byref(q), C.byref(o),
+                                             _ptr(self.ws), self.ws.numel(), _stream()))
+            return
         _check(lib().qh_shortlist_head(C.byref(self.head8.view), C.byref(self.head4.view), C.byref(self.err.view),
                                        _ptr(xq), _ptr(xd), C.byref(q), C.byref(o), _ptr(self.ws),
                                        self.ws.numel(), _stream()))

@@ -111,6 +111,33 @@ int scratch_current(void** ws) {
     return *ws ? QH_OK : fail(QH_ERR_HIP, "no scratch array on device %d", dev);
 }
 
+// A nibble-plane head: shape as a Q8_0 head of the shortlist (cols a multiple of 64, at most kMaxHeadCols).
+int validate_planes(const qh_tensor* W, const char* what) {
+    if (!W) return fail(QH_ERR_ARG, "%s: null tensor", what);
+    if (W->dtype != QH_Q8_0_PLANES) return fail(QH_ERR_DTYPE, "%s: dtype %d is not q8_0 planes (16)", what, W->dtype);
+    if (W->rows <= 0 || W->cols <= 0 || W->cols % 64 != 0 || W->cols > kMaxHeadCols)
+        return fail(QH_ERR_SHAPE, "%s: bad shape %d x %d (cols a multiple of 64, at most %d)", what, W->rows, W->cols,
+                    kMaxHeadCols);
+    if (!W->data) return fail(QH_ERR_ARG, "%s: null data", what);
+    if (!aligned16(W->data)) return fail(QH_ERR_ALIGN, "%s: data is not 16-byte aligned", what);
+    return QH_OK;
+}
+
+// The query, activation and outputs of a shortlist call over a V x D head.
+int validate_head_io(int V, int D, const int8_t* xq, const float* xd, const qh_head_query* query,
+                     const qh_head_out* out, const char* who) {
+    if (!query || !out) return fail(QH_ERR_ARG, "%s: null argument", who);
+    if (!xq || !xd || !aligned16(xq)) return fail(QH_ERR_ARG, "%s: bad activation pointers", who);
+    if (query->top_k < 1 || query->top_k > QH_HEAD_MAX_TOPK)
+        return fail(QH_ERR_UNSUPPORTED, "%s: top_k %d outside [1, %d]", who, query->top_k, QH_HEAD_MAX_TOPK);
+    if (query->n_must < 0 || (query->n_must > 0 && !query->must)) return fail(QH_ERR_ARG, "%s: bad must list", who);
+    if (!head_select_supported(V, D, query->top_k))
+        return fail(QH_ERR_UNSUPPORTED, "%s: %d rows with top_k %d exceed the seed selection", who, V, query->top_k);
+    if (!out->logits || !out->coarse || !out->upper || !out->rows || !out->stats)
+        return fail(QH_ERR_ARG, "%s: null output buffer", who);
+    return QH_OK;
+}
+
 // Arguments of the shortlist head entry points (everything but the workspace).
 int validate_head(const qh_tensor* head8, const qh_tensor* head4, const qh_tensor* err, const int8_t* xq,
                   const float* xd, const qh_head_query* query, const qh_head_out* out, const char* who) {
@@ -185,18 +212,20 @@ size_t qh_quant_bytes(int dtype, int rows, int cols) {
         case QH_F16: return n * 2;
         case QH_Q8_0: return n;
         case QH_Q4_0: return n / 2;
+        case QH_Q8_0_PLANES: return n;  // both planes
         default: return 0;
     }
 }
 
 size_t qh_tensor_bytes(int dtype, int rows, int cols) {
     size_t b = qh_quant_bytes(dtype, rows, cols);
-    if (dtype == QH_Q8_0 || dtype == QH_Q4_0) b += (size_t)rows * cols / QH_QK * 2;
+    if (dtype == QH_Q8_0 || dtype == QH_Q4_0 || dtype == QH_Q8_0_PLANES) b += (size_t)rows * cols / QH_QK * 2;
     return b;
 }
 
 int qh_validate_tensor(const qh_tensor* W) {
     if (!W) return fail(QH_ERR_ARG, "qh_validate_tensor: null tensor");
+    if (W->dtype == QH_Q8_0_PLANES) return validate_planes(W, "qh_validate_tensor");
     if (W->dtype == QH_F32 || W->dtype == QH_F16) {
         if (W->rows <= 0 || W->cols <= 0) return fail(QH_ERR_SHAPE, "bad shape %d x %d", W->rows, W->cols);
         if (!W->data) return fail(QH_ERR_ARG, "null data");
@@ -371,6 +400,37 @@ int qh_shortlist_head(const qh_tensor* head8, const qh_tensor* head4, const qh_t
     return check_hip(
         launch_shortlist_head(*head8, *head4, *err, xq, xd, *query, must, *out, workspace, as_stream(stream)),
         "qh_shortlist_head launch");
+}
+
+int qh_head_planes(const qh_tensor* head8, void* planes, void* stream) {
+    if (int rc = validate_quant(head8, "qh_head_planes")) return rc;
+    if (head8->dtype != QH_Q8_0) return fail(QH_ERR_DTYPE, "qh_head_planes: needs a q8_0 head");
+    if (head8->cols % 64 != 0 || head8->cols > kMaxHeadCols)
+        return fail(QH_ERR_SHAPE, "qh_head_planes: cols %d must be a multiple of 64 and at most %d", head8->cols,
+                    kMaxHeadCols);
+    if (!planes || !aligned16(planes)) return fail(QH_ERR_ALIGN, "qh_head_planes: planes not 16-byte aligned");
+    const size_t n = qh_tensor_bytes(QH_Q8_0, head8->rows, head8->cols);
+    const uintptr_t a = reinterpret_cast<uintptr_t>(head8->data), b = reinterpret_cast<uintptr_t>(planes);
+    if (a < b + n && b < a + n) return fail(QH_ERR_ARG, "qh_head_planes: planes overlap the q8_0 head");
+    return check_hip(launch_head_planes(head8->data, planes, head8->rows, head8->cols, as_stream(stream)),
+                     "qh_head_planes launch");
+}
+
+int qh_shortlist_planes(const qh_tensor* planes, const int8_t* xq, const float* xd, const qh_head_query* query,
+                        const qh_head_out* out, void* workspace, size_t workspace_bytes, void* stream) {
+    if (int rc = validate_planes(planes, "qh_shortlist_planes")) return rc;
+    if (int rc = validate_head_io(planes->rows, planes->cols, xq, xd, query, out, "qh_shortlist_planes")) return rc;
+    const size_t need = head_workspace_bytes(planes->rows, planes->cols, query->top_k);
+    if (!workspace || workspace_bytes < need)
+        return fail(QH_ERR_NOMEM, "qh_shortlist_planes: workspace %zu bytes, needs %zu", workspace_bytes, need);
+    if (!aligned16(workspace)) return fail(QH_ERR_ALIGN, "qh_shortlist_planes: workspace not 16-byte aligned");
+    HeadMust must;
+    must.ids = query->must;
+    must.n = query->n_must;
+    const qh_tensor none{QH_F16, 0, 0, nullptr};
+    return check_hip(
+        launch_shortlist_head(*planes, none, none, xq, xd, *query, must, *out, workspace, as_stream(stream)),
+        "qh_shortlist_planes launch");
 }
 
 int qh_shortlist_head_noalloc(const qh_tensor* head8, const qh_tensor* head4, const qh_tensor* err, const int8_t* xq,

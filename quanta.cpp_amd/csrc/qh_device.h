@@ -191,6 +191,20 @@ __device__ __forceinline__ int dot_q4_block(const uint4 w, const uint4 xlo, cons
     return dot4(kM8, (int)xhi.w, s);
 }
 
+// 32 unsigned nibbles (Q4_0 packing: low nibbles are elements 0-15, high nibbles 16-31, no offset) . 32 int8
+// activations: 8 four-byte dots, exact int32.
+__device__ __forceinline__ int dot_u4_block(const uint4 w, const uint4 xlo, const uint4 xhi) {
+    constexpr int kLo = 0x0F0F0F0F;
+    int s = dot4((int)w.x & kLo, (int)xlo.x, 0);
+    s = dot4((int)w.y & kLo, (int)xlo.y, s);
+    s = dot4((int)w.z & kLo, (int)xlo.z, s);
+    s = dot4((int)w.w & kLo, (int)xlo.w, s);
+    s = dot4((int)(w.x >> 4) & kLo, (int)xhi.x, s);
+    s = dot4((int)(w.y >> 4) & kLo, (int)xhi.y, s);
+    s = dot4((int)(w.z >> 4) & kLo, (int)xhi.z, s);
+    return dot4((int)(w.w >> 4) & kLo, (int)xhi.w, s);
+}
+
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
 // Accumulator of one 16x16x32 int8 MFMA.

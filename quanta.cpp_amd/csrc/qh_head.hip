@@ -154,11 +154,13 @@ WsLayout ws_layout(int V, int D) {
     return l;
 }
 
-// Register set of one screen tile: the Q4_0 chunks with their block scales, and the f16 error words.
+// Register set of one screen tile: the Q4_0 chunks with their block scales, and the f16 error words. PL (nibble
+// planes): the high plane's chunks (Q4_0 packing of h + 8) with the Q8_0 scales, and no error words.
+template <bool PL>
 struct ScreenRegs {
     uint4 w[kScreenU];
     uint16_t sc[kScreenU];
-    uint32_t e[kScreenErrU];
+    uint32_t e[PL ? 1 : kScreenErrU];
 
     __device__ __forceinline__ void load(const uint8_t* __restrict__ w4, const uint16_t* __restrict__ s4,
                                          const uint32_t* __restrict__ e32, int r, int nrows, int nb) {
@@ -172,16 +174,19 @@ struct ScreenRegs {
             w[j] = load16(base + (size_t)c * 16);
             sc[j] = load_f16_bits(sbase + c);
         }
+        if constexpr (PL) return;
         // nb is even, so a tile's errors are nrows * nb / 2 whole 4-byte words starting 4-byte aligned.
         const int n32 = nrows * nb / 2;
         const uint32_t* ebase = e32 + (size_t)r * nb / 2;
 #pragma unroll
-        for (int j = 0; j < kScreenErrU; ++j) e[j] = ebase[min(j * kScreenThreads + tid, n32 - 1)];
+        for (int j = 0; j < (PL ? 1 : kScreenErrU); ++j) e[j] = ebase[min(j * kScreenThreads + tid, n32 - 1)];
     }
 
-    // Block products and block errors (as f32) into LDS tiles [row][pstride].
+    // Block products and block errors (as f32) into LDS tiles [row][pstride]. PL: the block product of the
+    // high-nibble midpoints, sum_i (16 h_i + 8) x_i = 16 sum_i (h_i + 8) x_i - 120 sum_i x_i (sxs: the activation's
+    // block sums), and the bound's operand d_b itself.
     __device__ __forceinline__ void stage(float* prod, float* errf, int pstride, int nrows, int nb, uint32_t nb_magic,
-                                          const int8_t* xs) const {
+                                          const int8_t* xs, const int* sxs) const {
         const int tid = (int)threadIdx.x;
         const int nch = nrows * nb;
 #pragma unroll
@@ -192,12 +197,22 @@ struct ScreenRegs {
             const uint32_t b = g - rt * (uint32_t)nb;
             const uint4 xlo = *reinterpret_cast<const uint4*>(xs + b * QK);
             const uint4 xhi = *reinterpret_cast<const uint4*>(xs + b * QK + 16);
-            const int s = dot_q4_block(w[j], xlo, xhi);
-            if (c < nch) prod[rt * pstride + b] = (float)s * f16_to_f32(sc[j]);
+            if constexpr (PL) {
+                const int s = 16 * dot_u4_block(w[j], xlo, xhi) - 120 * sxs[b];
+                const float d = f16_to_f32(sc[j]);
+                if (c < nch) {
+                    prod[rt * pstride + b] = (float)s * d;
+                    errf[rt * pstride + b] = d;
+                }
+            } else {
+                const int s = dot_q4_block(w[j], xlo, xhi);
+                if (c < nch) prod[rt * pstride + b] = (float)s * f16_to_f32(sc[j]);
+            }
         }
+        if constexpr (PL) return;
         const int n32 = nrows * nb / 2;
 #pragma unroll
-        for (int j = 0; j < kScreenErrU; ++j) {
+        for (int j = 0; j < (PL ? 1 : kScreenErrU); ++j) {
             const int i = j * kScreenThreads + tid;
             const uint32_t g = 2u * (uint32_t)min(i, n32 - 1);  // first of the word's two blocks (same row)
             const uint32_t rt = div_magic(g, nb_magic);
@@ -378,15 +393,23 @@ struct ShareRows {
 // (barriers inside). mid() runs once, by every thread, while the first pass's loads are in flight (it may hold
 // barriers and must not touch prod). Returns, in each row's chain lane, the best key of the rows it scored (0
 // elsewhere).
+// The exact head's rows: Q8_0 (w: quants [V][D], s: scales), or with PL the nibble planes (w: high plane, lo: low
+// plane, both [V][nb][16 bytes], s: the Q8_0 scales; sxs: the activation's block sums in LDS). A row's chunk ch is
+// half ch % 2 of block ch / 2: the block's bytes 16 (ch % 2) .. + 15 (Q8_0), or its high (even) / low (odd) plane.
+struct ExactHead {
+    const uint8_t* w;
+    const uint8_t* lo;
+    const uint16_t* s;
+    const int* sxs;
+};
 constexpr int kRescoreLanes = 8, kRescoreRows = kSelThreads / kRescoreLanes;
 struct NoMid {
     __device__ void operator()() const {}
 };
-template <typename Mid = NoMid>
-__device__ uint64_t rescore_lists(const int* a, int na, const int* b, int nb_, const uint8_t* __restrict__ w8,
-                                  const uint16_t* __restrict__ s8, const int8_t* xs, const float* xds, int nb,
-                                  float* prod, float* out, bool to_out, float* __restrict__ logits,
-                                  const Mid& mid = Mid()) {
+template <bool PL, typename Mid = NoMid>
+__device__ uint64_t rescore_lists(const int* a, int na, const int* b, int nb_, const ExactHead& eh, const int8_t* xs,
+                                  const float* xds, int nb, float* prod, float* out, bool to_out,
+                                  float* __restrict__ logits, const Mid& mid = Mid()) {
     constexpr int kPer = 8;  // chunks per lane per batch: one batch for rows of up to 1024 columns
     const int tid = (int)threadIdx.x, g = tid / kRescoreLanes, j = tid % kRescoreLanes;
     const int nch = 2 * nb, cnt = na + nb_;
@@ -396,15 +419,18 @@ __device__ uint64_t rescore_lists(const int* a, int na, const int* b, int nb_, c
         const int i = p0 + g;
         const bool act = i < cnt;
         const int r = !act ? 0 : i < na ? a[i] : b[i - na];
-        const uint8_t* wr = w8 + (size_t)r * nb * QK;
-        const uint16_t* sr = s8 + (size_t)r * nb;
+        const uint8_t* wr = eh.w + (size_t)r * nb * QK;
+        const uint16_t* sr = eh.s + (size_t)r * nb;
         for (int c0 = 0; c0 < nch; c0 += kRescoreLanes * kPer) {  // uniform
             uint4 w[kPer];
             uint16_t sc[kPer];
 #pragma unroll
             for (int c = 0; c < kPer; ++c) {  // unconditional (clamped) loads: all in flight before the first wait
                 const int ch = min(c0 + j + kRescoreLanes * c, nch - 1);
-                w[c] = load16(wr + (size_t)ch * 16);
+                if constexpr (PL)
+                    w[c] = load16(((ch & 1) ? eh.lo : eh.w) + ((size_t)r * nb + (ch >> 1)) * 16);
+                else
+                    w[c] = load16(wr + (size_t)ch * 16);
                 sc[c] = load_f16_bits(sr + (ch >> 1));
             }
             if (p0 == 0 && c0 == 0) mid();  // with the first pass's loads in flight
@@ -420,8 +446,16 @@ __device__ uint64_t rescore_lists(const int* a, int na, const int* b, int nb_, c
             for (int c = 0; c < kPer; ++c) {
                 const int ch = c0 + j + kRescoreLanes * c;
                 const int blk = min(ch >> 1, nb - 1);
-                const uint4 xv = *reinterpret_cast<const uint4*>(xs + blk * QK + (ch & 1) * 16);
-                int sdot = dot16_i8(w[c], xv);
+                int sdot;
+                if constexpr (PL) {  // q = 16 h + l: 16 sum (h + 8) x - 128 sum x from the high plane, sum l x
+                    const uint4 xlo = *reinterpret_cast<const uint4*>(xs + blk * QK);
+                    const uint4 xhi = *reinterpret_cast<const uint4*>(xs + blk * QK + 16);
+                    const int u = dot_u4_block(w[c], xlo, xhi);
+                    sdot = (ch & 1) ? u : 16 * u - 128 * eh.sxs[blk];
+                } else {
+                    const uint4 xv = *reinterpret_cast<const uint4*>(xs + blk * QK + (ch & 1) * 16);
+                    sdot = dot16_i8(w[c], xv);
+                }
                 sdot += swap_pair(sdot);
                 if (act && ch < nch && !(ch & 1)) prod[g * nb + blk] = (float)sdot * scf[c];
             }
@@ -453,6 +487,9 @@ __device__ uint64_t rescore_lists(const int* a, int na, const int* b, int nb_, c
 
 }  // namespace
 
+// PL: the nibble-plane head (w4 the high plane, s4 the Q8_0 scales, e32 unused): coarse scores of the high-nibble
+// midpoints and the bound sum_b fma(d_b, (8 dx_b) * sum_i |x_i|), since |q - (16 h + 8)| = |l - 8| <= 8.
+template <bool PL>
 __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void head_screen_kernel(
     const uint8_t* __restrict__ w4, const uint16_t* __restrict__ s4, const uint32_t* __restrict__ e32,
     const int8_t* __restrict__ xq, const float* __restrict__ xd, int V, int nb, int nv, HeadMust mq, int tile, ShareMap sm,
@@ -471,6 +508,7 @@ __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(
     float* bsh = errf1 + (size_t)tile * ps + kChainPipePad;  // [2][64] bounds of a tile (wave 1 -> wave 0)
     uint8_t* mshare = reinterpret_cast<uint8_t*>(bsh + 128);                    // [kScreenMaxShare] must flags
     int8_t* xs = reinterpret_cast<int8_t*>(mshare + kScreenMaxShare);            // [nb * 32]
+    int* sxs = reinterpret_cast<int*>(xs + nb * QK);                             // PL: [nb] block sums of xs
     float* xds = xdsp + zp;
     float* xnorm = xnormp + zp;
 
@@ -499,7 +537,7 @@ __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(
     for (int j = 0; j < kMaxHeadCols / 16 / kScreenThreads; ++j)
         if (tid + j * kScreenThreads < nx) xv[j] = load16(xq + (tid + j * kScreenThreads) * 16);
     if (tid < nb) xdv = xd[tid];
-    ScreenRegs A, B;
+    ScreenRegs<PL> A, B;
     A.load(w4, s4, e32, ra, min(tile, rb - ra), nb);
     for (int i = 4 * tid; i < share; i += 4 * kScreenThreads) *reinterpret_cast<uint32_t*>(mshare + i) = 0u;
     zero_chain_prefix(xdsp, prod0, nb, 2 * tile);   // both product buffers
@@ -511,11 +549,24 @@ __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(
     __syncthreads();
     // xnorm_b = d_b * sqrt(sum q^2) (model.cpp:247-251): every partial sum is an integer below 2^24, so the reference's
     // float accumulation is exact and equals this integer dot.
+    // PL: the bound's operand (8 dx_b) * sum_i |x_i| (an exact integer below 2^24; 8 dx_b is exact) and the block sums.
     for (int b = tid; b < nb; b += kScreenThreads) {
         const uint4 lo = *reinterpret_cast<const uint4*>(xs + b * QK), hi = *reinterpret_cast<const uint4*>(xs + b * QK + 16);
-        const int ss = dot16_i8(lo, lo) + dot16_i8(hi, hi);
-        xnorm[b] = xds[b] * __builtin_sqrtf((float)ss);
+        if constexpr (PL) {
+            int l1 = 0, sum = 0;
+            for (int i = 0; i < QK; ++i) {
+                const int v = xs[b * QK + i];
+                l1 += v < 0 ? -v : v;
+                sum += v;
+            }
+            sxs[b] = sum;
+            xnorm[b] = (8.0f * xds[b]) * (float)l1;
+        } else {
+            const int ss = dot16_i8(lo, lo) + dot16_i8(hi, hi);
+            xnorm[b] = xds[b] * __builtin_sqrtf((float)ss);
+        }
     }
+    if constexpr (PL) __syncthreads();  // the block sums, read by the first tile's staging
     // The share's must ids as LDS flags (read once; loads batched so they are in flight together), and with must ids
     // the share's rows of the first-occurrence array reset for the select kernel.
     if (n_must > 0) {  // uniform
@@ -543,10 +594,10 @@ __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(
     // One tile whose chunks sit in `regs`: stage into LDS, then wave 0 (one row per lane) runs the coarse chains and
     // wave 1 the bound chains (model.cpp:263-271).
     int buf = 0;
-    auto tile_body = [&](const ScreenRegs& regs, int r, float* prod, float* errf) {
+    auto tile_body = [&](const ScreenRegs<PL>& regs, int r, float* prod, float* errf) {
         const int nrows = min(tile, rb - r);
         const uint8_t* mf = mshare + (r - ra);
-        regs.stage(prod + zp, errf + zp, ps, nrows, nb, nb_magic, xs);
+        regs.stage(prod + zp, errf + zp, ps, nrows, nb, nb_magic, xs, sxs);
         __syncthreads();
         if (tid < 64) {
             finish_prev();
@@ -621,17 +672,23 @@ __global__ __launch_bounds__(kScreenThreads) __attribute__((amdgpu_waves_per_eu(
     QH_HSTAMP(0, 3);
 }
 
-template <int SH>  // screen shares per thread: 2 for grids of up to 512 shares, else SH
+// SH: screen shares per thread (2 for grids of up to 512 shares, else kSelShares). PL: the exact rows are the nibble
+// planes (w8 the high plane, lo the low plane, s8 the Q8_0 scales); else the Q8_0 head (lo unused).
+template <int SH, bool PL>
 __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
-    const uint8_t* __restrict__ w8, const uint16_t* __restrict__ s8, const int8_t* __restrict__ xq,
+    const uint8_t* __restrict__ w8, const uint8_t* __restrict__ lo, const uint16_t* __restrict__ s8,
+    const int8_t* __restrict__ xq,
     const float* __restrict__ xd, int nb, int nv, int k, int n_parts, ShareMap sm, int band,
     const uint64_t* __restrict__ tops, const float* __restrict__ coarse, const float* __restrict__ upper,
     const uint8_t* __restrict__ mark, int32_t* __restrict__ firsts, HeadMust mq, int32_t* __restrict__ rows,
     float* __restrict__ logits, HeadCtrl* __restrict__ ctrl, qh_head_stats* __restrict__ stats, TokenFeedback fb) {
-    extern __shared__ __align__(16) float ssm[];  // products [32][nb], activation codes [nb * 32], scales [nb]
+    // products [32][nb], activation codes [nb * 32], scales [nb], block sums [nb] (PL)
+    extern __shared__ __align__(16) float ssm[];
     float* prod = ssm;
     int8_t* xs = reinterpret_cast<int8_t*>(ssm + kRescoreRows * nb);
     float* xds = reinterpret_cast<float*>(xs + nb * QK);
+    int* sxs = reinterpret_cast<int*>(xds + nb);
+    const ExactHead eh{w8, lo, s8, sxs};
     __shared__ uint64_t pool[kPoolCap];
     __shared__ int prow[kPoolCap];
     __shared__ uint64_t gmax[kSelThreads / 4];
@@ -686,6 +743,13 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     }
     for (int i = tid; i < nb * 2; i += kSelThreads) reinterpret_cast<uint4*>(xs)[i] = load16(xq + (size_t)i * 16);
     for (int i = tid; i < nb; i += kSelThreads) xds[i] = xd[i];
+    if constexpr (PL) {  // the activation's block sums (from global memory: xs is not complete before the barrier)
+        for (int b = tid; b < nb; b += kSelThreads) {
+            int sum = 0;
+            for (int i = 0; i < QK; ++i) sum += xq[b * QK + i];
+            sxs[b] = sum;
+        }
+    }
     for (int i = tid; i < kMaxKeep; i += kSelThreads) best[i] = 0ull;
     if (tid < kBandWords) seedmap[tid] = 0u;
     if (tid == 0) {
@@ -898,10 +962,10 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     const int nsp = n_c;  // candl: nm must rows, then nsp speculative candidates (at most band rows in all)
     const int na = early ? np : min(np, n_seed);
     // (early: the pool is ranked while the pass's loads are in flight)
-    rescore_lists(early ? prow : seedrow, na, candl, nm + nsp, w8, s8, xs, xds, nb, prod, rx, true, logits,
-                  [&]() {
-                      if (early) rank_pool();
-                  });
+    rescore_lists<PL>(early ? prow : seedrow, na, candl, nm + nsp, eh, xs, xds, nb, prod, rx, true, logits,
+                      [&]() {
+                          if (early) rank_pool();
+                      });
     for (int i = tid; i < min(np, n_seed); i += kSelThreads) exact[i] = rx[early ? seedidx[i] : i];
     __syncthreads();
     QH_HSTAMP(2, 3);
@@ -1025,7 +1089,7 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
         }
         __syncthreads();
         const int nx = n_x;
-        const uint64_t kb = rescore_lists(mustl, nx, candl, 0, w8, s8, xs, xds, nb, prod, rx, false, logits);
+        const uint64_t kb = rescore_lists<PL>(mustl, nx, candl, 0, eh, xs, xds, nb, prod, rx, false, logits);
         kbest = kb > kbest ? kb : kbest;
         for (int i0 = 0; i0 < nx; i0 += kSelThreads) {
             const int i = i0 + tid;
@@ -1132,6 +1196,33 @@ __global__ __launch_bounds__(kSelThreads) void head_select_kernel(
     }
 }
 
+// The nibble planes of a Q8_0 head, one 32-block per thread: q = 16 h + l with h = floor(q / 16) in [-8, 7] and
+// l = q mod 16. A byte's high nibble u (as unsigned) gives h + 8 = u ^ 8, its low nibble is l; each plane keeps the
+// Q4_0 packing (byte j: element j in the low nibble, element j + 16 in the high one).
+__global__ __launch_bounds__(256) void head_planes_kernel(const uint8_t* __restrict__ q8, uint8_t* __restrict__ hi,
+                                                          uint8_t* __restrict__ lo, long n_blocks) {
+    const long b = (long)blockIdx.x * 256 + threadIdx.x;
+    if (b >= n_blocks) return;
+    const uint4 a = load16(q8 + b * QK), c = load16(q8 + b * QK + 16);
+    auto hw = [](uint32_t x, uint32_t y) {
+        return ((((x >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u) | ((((y >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u) << 4));
+    };
+    auto lw = [](uint32_t x, uint32_t y) { return (x & 0x0F0F0F0Fu) | ((y & 0x0F0F0F0Fu) << 4); };
+    *reinterpret_cast<uint4*>(hi + b * 16) = make_uint4(hw(a.x, c.x), hw(a.y, c.y), hw(a.z, c.z), hw(a.w, c.w));
+    *reinterpret_cast<uint4*>(lo + b * 16) = make_uint4(lw(a.x, c.x), lw(a.y, c.y), lw(a.z, c.z), lw(a.w, c.w));
+}
+
+hipError_t launch_head_planes(const void* head8, void* planes, int V, int D, hipStream_t s) {
+    const size_t n = (size_t)V * D;
+    const long nblk = (long)(n / QK);
+    uint8_t* out = static_cast<uint8_t*>(planes);
+    qh_launch(head_planes_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s,
+              static_cast<const uint8_t*>(head8), out, out + n / 2, nblk);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return hipMemcpyAsync(out + n, static_cast<const uint8_t*>(head8) + n, n / QK * 2, hipMemcpyDeviceToDevice, s);
+}
+
 bool head_select_supported(int V, int D, int top_k) {
     return top_k >= 1 && top_k <= QH_HEAD_MAX_TOPK && screen_shape(V, D / QK).grid <= kSelShares * kSelThreads;
 }
@@ -1155,25 +1246,31 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
     int32_t* firsts = reinterpret_cast<int32_t*>(wsb + l.first);
     uint64_t* tops = reinterpret_cast<uint64_t*>(wsb + l.tops);
     HeadCtrl* ctrl = reinterpret_cast<HeadCtrl*>(wsb + l.ctrl);
+    // The nibble-plane head (QH_Q8_0_PLANES) screens with its high plane and rescores from both planes; head4 and err
+    // are not read then.
+    const bool pl = head8.dtype == QH_Q8_0_PLANES;
     const uint8_t* w8 = static_cast<const uint8_t*>(head8.data);
     const uint16_t* s8 = reinterpret_cast<const uint16_t*>(w8 + qh_quant_bytes(QH_Q8_0, V, D));
-    const uint8_t* w4 = static_cast<const uint8_t*>(head4.data);
-    const uint16_t* s4 = reinterpret_cast<const uint16_t*>(w4 + qh_quant_bytes(QH_Q4_0, V, D));
-    const uint32_t* e32 = static_cast<const uint32_t*>(err.data);
+    const uint8_t* lo = pl ? w8 + (size_t)V * D / 2 : nullptr;
+    const uint8_t* w4 = pl ? w8 : static_cast<const uint8_t*>(head4.data);
+    const uint16_t* s4 = pl ? s8 : reinterpret_cast<const uint16_t*>(w4 + qh_quant_bytes(QH_Q4_0, V, D));
+    const uint32_t* e32 = pl ? nullptr : static_cast<const uint32_t*>(err.data);
 
     const ScreenShape sh = screen_shape(V, nb);
     const int tile = sh.tile;
     const uint32_t magic = nb == 1 ? 0u : (uint32_t)((0x100000000ull + (uint64_t)nb - 1) / (uint64_t)nb);
     const size_t lds1 = ((size_t)2 * chain_len32(nb) + 4 * (size_t)tile * chain_stride32(nb) + kChainPipePad + 128) * 4 +
-                        kScreenMaxShare + (size_t)D;
-    qh_launch(head_screen_kernel, dim3(sh.grid), dim3(kScreenThreads), lds1, s, w4, s4, e32, xq, xd, V, nb, nv, must,
-              tile, sh.map, magic, out.coarse, out.upper, out.logits, mark, firsts, tops, ctrl);
+                        kScreenMaxShare + (size_t)D + (pl ? (size_t)nb * 4 : 0);
+    qh_launch(pl ? head_screen_kernel<true> : head_screen_kernel<false>, dim3(sh.grid), dim3(kScreenThreads), lds1, s,
+              w4, s4, e32, xq, xd, V, nb, nv, must, tile, sh.map, magic, out.coarse, out.upper, out.logits, mark, firsts,
+              tops, ctrl);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int band = select_band(nv);
-    const size_t lds2 = (size_t)kRescoreRows * nb * 4 + (size_t)nb * QK + (size_t)nb * 4;
-    auto* sel = sh.grid <= 2 * kSelThreads ? head_select_kernel<2> : head_select_kernel<kSelShares>;
-    qh_launch(sel, dim3((unsigned)((nv + band - 1) / band)), dim3(kSelThreads), lds2, s, w8, s8, xq, xd, nb, nv,
+    const size_t lds2 = (size_t)kRescoreRows * nb * 4 + (size_t)nb * QK + (size_t)nb * 4 + (pl ? (size_t)nb * 4 : 0);
+    auto* sel = sh.grid <= 2 * kSelThreads ? (pl ? head_select_kernel<2, true> : head_select_kernel<2, false>)
+                                           : (pl ? head_select_kernel<kSelShares, true> : head_select_kernel<kSelShares, false>);
+    qh_launch(sel, dim3((unsigned)((nv + band - 1) / band)), dim3(kSelThreads), lds2, s, w8, lo, s8, xq, xd, nb, nv,
               q.top_k, sh.grid, sh.map, band, tops, out.coarse, out.upper, mark, firsts, must, out.rows, out.logits,
               ctrl, out.stats, advance ? *advance : TokenFeedback{});
     return hipGetLastError();

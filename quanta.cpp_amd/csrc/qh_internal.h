@@ -151,6 +151,9 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
                                  const qh_head_out& out, void* ws, hipStream_t s,
                                  const TokenFeedback* advance = nullptr);
 
+// The nibble-plane layout (QH_Q8_0_PLANES) of a Q8_0 [V][D] head at planes (the same size, not overlapping it).
+hipError_t launch_head_planes(const void* head8, void* planes, int V, int D, hipStream_t s);
+
 // Sampler::sample on the device (qh_sample.hip). Candidates: rows[0, hs->n_rows) (the shortlist head's list; every
 // other id counts as -inf) or, with rows null, every id below n_valid; the penalty looks at the ids `hist` names.
 // Requires 1 <= n_valid <= QH_SAMPLE_MAX_VOCAB; with temperature > 0 and more than QH_SAMPLE_MAX_TOPK survivors, a

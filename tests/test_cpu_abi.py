@@ -191,3 +191,30 @@ def test_decoder_create_tensor_count(qh):
     h = C.c_void_p()
     assert qh.lib().qh_decoder_create(C.byref(desc), ts, n - 2, C.byref(h)) == qh.ERR_ARG
     assert b"needs 16 or 17" in qh.lib().qh_last_error()
+
+
+def test_planes_entry_points_host_checks(qh):
+    """The nibble-plane head: the layout's size equals the Q8_0 tensor's, and bad arguments are refused on the host
+    (descriptors at made-up aligned addresses: nothing may be launched)."""
+    L = qh.lib()
+    V, D = 151936, 896
+    assert L.qh_tensor_bytes(qh.Q8_0_PLANES, V, D) == L.qh_tensor_bytes(qh.Q8_0, V, D)
+    assert L.qh_quant_bytes(qh.Q8_0_PLANES, V, D) == V * D
+    h8 = qh.qh_tensor(qh.Q8_0, V, D, 1 << 30)
+    assert L.qh_head_planes(C.byref(h8), C.c_void_p((1 << 30) + 4096), None) == qh.ERR_ARG  # overlapping
+    assert b"overlap" in L.qh_last_error()
+    assert L.qh_head_planes(C.byref(h8), C.c_void_p((1 << 33) + 8), None) == qh.ERR_ALIGN
+    h4 = qh.qh_tensor(qh.Q4_0, V, D, 1 << 30)
+    assert L.qh_head_planes(C.byref(h4), C.c_void_p(1 << 33), None) == qh.ERR_DTYPE
+    odd = qh.qh_tensor(qh.Q8_0, V, 96, 1 << 30)
+    assert L.qh_head_planes(C.byref(odd), C.c_void_p(1 << 33), None) == qh.ERR_SHAPE
+    out = qh.qh_head_out(16, 16, 16, 16, 16)
+    q = qh.qh_head_query(1, 0, None, 0)
+    call = lambda t, ws_bytes: L.qh_shortlist_planes(C.byref(t), C.c_void_p(16), C.c_void_p(16), C.byref(q),
+                                                     C.byref(out), C.c_void_p(4096), ws_bytes, None)
+    assert call(h8, 1 << 30) == qh.ERR_DTYPE  # a plain Q8_0 descriptor is not the plane layout
+    pl = qh.qh_tensor(qh.Q8_0_PLANES, V, D, 1 << 30)
+    assert L.qh_validate_tensor(C.byref(pl)) == 0
+    assert call(pl, 16) == qh.ERR_NOMEM  # workspace too small
+    q.top_k = 0
+    assert call(pl, 1 << 30) == qh.ERR_UNSUPPORTED
