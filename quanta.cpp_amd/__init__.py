@@ -363,7 +363,11 @@ class Decoder:
     hp.tied_embeddings false takes lm_head.weight as the LM head, hp.flags carries FLAG_HADAMARD_DOWN, and kv_f32
     keeps an f32 KV cache (Model::load's kv_f16 = false, model.cpp:10, 96-104)."""
 
-    def __init__(self, hp, tensors: dict, ctx_len: int | None = None, device="cuda", kv_f32: bool = False):
+    def __init__(self, hp, tensors: dict, ctx_len: int | None = None, device="cuda", kv_f32: bool = False,
+                 head_planes: bool = False):
+        """head_planes: the Q8_0 LM head (the embedding when tied) is stored as nibble planes (qh_head_planes) in place
+        of its Q8_0 form, and the shortlist head screens with the high plane: no head_q4 / head_err are uploaded (the
+        scope's nibble-plane variant, zero extra memory)."""
         torch = _torch()
         self.hp = hp
         self.kv_f32 = bool(kv_f32)
@@ -371,25 +375,37 @@ class Decoder:
         for l in range(hp.n_layers):
             names += [f"model.layers.{l}.{n}" for n in LAYER_ORDER]
         names += ["quanta.head_q4", "quanta.head_err"]
-        if not getattr(hp, "tied_embeddings", True):
+        tied = getattr(hp, "tied_embeddings", True)
+        if not tied:
             names.append("lm_head.weight")
+        lm_name = "model.embed_tokens.weight" if tied else "lm_head.weight"
+        skip = {"quanta.head_q4", "quanta.head_err"} if head_planes else set()
+        if head_planes and tensors[lm_name].dtype != Q8_0:
+            raise QHError("head_planes needs a Q8_0 LM head")
         offs, total = [], 0
         for n in names:
             offs.append(total)
-            if n in tensors:
+            if n in tensors and n not in skip:
                 total += (tensors[n].data.size + 255) // 256 * 256
         self.buf = torch.empty(max(total, 256), dtype=torch.uint8, device=device)
         host = np.zeros(max(total, 256), np.uint8)
         for n, o in zip(names, offs):
-            if n in tensors:
+            if n in tensors and n not in skip and not (head_planes and n == lm_name):
                 host[o:o + tensors[n].data.size] = np.asarray(tensors[n].data)
         self.buf.copy_(torch.from_numpy(host))
         del host
         arr = (qh_tensor * len(names))()
         base = self.buf.data_ptr()
         for i, (n, o) in enumerate(zip(names, offs)):
-            t = tensors.get(n)
+            t = None if n in skip else tensors.get(n)
             arr[i] = qh_tensor(0, 0, 0, None) if t is None else qh_tensor(t.dtype, t.rows, t.cols, base + o)
+            if head_planes and n == lm_name:  # the Q8_0 copy goes through a scratch upload into its slot as planes
+                q8 = torch.from_numpy(np.ascontiguousarray(t.data).view(np.uint8).reshape(-1)).to(device)
+                src = qh_tensor(Q8_0, t.rows, t.cols, q8.data_ptr())
+                _check(lib().qh_head_planes(C.byref(src), C.c_void_p(base + o), _stream()))
+                torch.cuda.synchronize()
+                del q8
+                arr[i] = qh_tensor(Q8_0_PLANES, t.rows, t.cols, base + o)
         self._tensors = arr
         self.desc = qh_model_desc(hp.vocab_size, hp.dim, hp.n_layers, hp.n_heads, hp.n_kv_heads, hp.head_dim,
                                   hp.ffn_dim, ctx_len or hp.max_seq, int(hp.qkv_bias), hp.rope_theta, hp.norm_eps,

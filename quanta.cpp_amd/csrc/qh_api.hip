@@ -307,6 +307,13 @@ int qh_matvec_ref(float* out, const qh_tensor* W, const float* x, int r0, int r1
 }
 
 int qh_matvec_q(float* out, const qh_tensor* W, const int8_t* xq, const float* xd, int r0, int r1, void* stream) {
+    if (W && W->dtype == QH_Q8_0_PLANES) {  // a nibble-plane head: the same values as its Q8_0 form
+        if (int rc = validate_planes(W, "qh_matvec_q")) return rc;
+        if (int rc = validate_range(W->rows, r0, r1, "qh_matvec_q")) return rc;
+        if (!out || !xq || !xd) return fail(QH_ERR_ARG, "qh_matvec_q: null pointer");
+        if (!aligned16(xq)) return fail(QH_ERR_ALIGN, "qh_matvec_q: xq is not 16-byte aligned");
+        return check_hip(launch_gemv_planes(out, *W, xq, xd, r0, r1, as_stream(stream)), "qh_matvec_q launch");
+    }
     if (int rc = validate_quant(W, "qh_matvec_q")) return rc;
     if (int rc = validate_range(W->rows, r0, r1, "qh_matvec_q")) return rc;
     if (!out || !xq || !xd) return fail(QH_ERR_ARG, "qh_matvec_q: null pointer");
@@ -477,7 +484,16 @@ int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_t
                         cols);
         return QH_OK;
     };
-    if (int rc = want(0, hp->vocab_size, D, true, "embedding")) return rc;
+    // a nibble-plane embedding / LM head (QH_Q8_0_PLANES, qh_head_planes): the Q8_0 values in another layout
+    auto want_lm = [&](int i, const char* what) -> int {
+        if (tensors[i].dtype != QH_Q8_0_PLANES) return want(i, hp->vocab_size, D, true, what);
+        if (int rc = validate_planes(&tensors[i], what)) return rc;
+        if (tensors[i].rows != hp->vocab_size || tensors[i].cols != D)
+            return fail(QH_ERR_SHAPE, "qh_decoder_create: %s is %d x %d, expected %d x %d", what, tensors[i].rows,
+                        tensors[i].cols, hp->vocab_size, D);
+        return QH_OK;
+    };
+    if (int rc = want_lm(0, "embedding")) return rc;
     if (int rc = want(1, 1, D, false, "final norm")) return rc;
     for (int l = 0; l < L; ++l) {
         const int b = 2 + 12 * l;
@@ -492,10 +508,12 @@ int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_t
     // the LM head: lm_head.weight when untied (model.cpp:16), Q8_0 or Q4_0, else the embedding
     const bool untied = n_tensors == 5 + 12 * L && tensors[4 + 12 * L].data;
     if (untied)
-        if (int rc = want(4 + 12 * L, hp->vocab_size, D, true, "lm_head")) return rc;
-    const int lm_dtype = untied ? tensors[4 + 12 * L].dtype : QH_Q8_0;
+        if (int rc = want_lm(4 + 12 * L, "lm_head")) return rc;
+    const int lm_dtype = untied ? tensors[4 + 12 * L].dtype : tensors[0].dtype;
     const qh_tensor& h4 = tensors[2 + 12 * L];
     const qh_tensor& he = tensors[3 + 12 * L];
+    if (lm_dtype == QH_Q8_0_PLANES && (h4.data || he.data))
+        return fail(QH_ERR_ARG, "qh_decoder_create: a nibble-plane LM head is its own shortlist: no head_q4 / head_err");
     if (h4.data || he.data) {
         if (h4.dtype != QH_Q4_0 || he.dtype != QH_F16 || lm_dtype != QH_Q8_0 || h4.rows != hp->vocab_size ||
             h4.cols != D || he.rows != hp->vocab_size || he.cols != D / QH_QK || !h4.data || !he.data ||
@@ -503,7 +521,7 @@ int qh_decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_t
             return fail(QH_ERR_SHAPE, "qh_decoder_create: bad shortlist head tensors");  // as model.cpp:49-58
     }
     if (int rc = qh_init_current()) return rc;
-    if (h4.data && !head_select_supported(hp->vocab_size, D, 1))
+    if ((h4.data || lm_dtype == QH_Q8_0_PLANES) && !head_select_supported(hp->vocab_size, D, 1))
         return fail(QH_ERR_UNSUPPORTED, "qh_decoder_create: a %d x %d shortlist head is beyond the seed selection",
                     hp->vocab_size, D);
     Decoder* d = nullptr;

@@ -706,7 +706,7 @@ __global__ __launch_bounds__(256) void embed_norm_quant_kernel(const int32_t* __
         if (tid == 0) atomicOr(status, kStatusToken);
         tok = 0;
     }
-    const size_t nq = dtype == kQ4 ? (size_t)V * D / 2 : (size_t)V * D;  // quant bytes before the scales
+    const size_t nq = dtype == kQ4 ? (size_t)V * D / 2 : (size_t)V * D;  // quant bytes (both planes) before the scales
     const uint16_t* sr = reinterpret_cast<const uint16_t*>(emb + nq) + (size_t)tok * (D / QK);
     for (int i4 = tid; i4 < D / 4; i4 += 256) {  // elements 4 i4 .. 4 i4 + 3 (one block, one half of a Q4_0 block)
         float4 v;
@@ -721,6 +721,14 @@ __global__ __launch_bounds__(256) void embed_norm_quant_kernel(const int32_t* __
             uint32_t c4;
             if (dtype == kQ8) {
                 c4 = *reinterpret_cast<const uint32_t*>(emb + (size_t)tok * D + 4 * i4);
+            } else if (dtype == kQ8P) {  // q = 16 (h + 8) + l - 128: the byte (h + 8) << 4 | l, top bit flipped
+                const int e = 4 * i4, j = e % QK;
+                const size_t off = (size_t)tok * D / 2 + (e / QK) * 16 + j % 16;
+                const uint32_t hb = *reinterpret_cast<const uint32_t*>(emb + off);
+                const uint32_t lb = *reinterpret_cast<const uint32_t*>(emb + (size_t)V * D / 2 + off);
+                const uint32_t hn = j < 16 ? hb & 0x0F0F0F0Fu : (hb >> 4) & 0x0F0F0F0Fu;
+                const uint32_t ln = j < 16 ? lb & 0x0F0F0F0Fu : (lb >> 4) & 0x0F0F0F0Fu;
+                c4 = ((hn << 4) | ln) ^ 0x80808080u;
             } else {  // element j of a block: low nibble of byte j (j < 16), high nibble of byte j - 16
                 const int e = 4 * i4, j = e % QK;
                 const uint32_t b4 = *reinterpret_cast<const uint32_t*>(emb + (size_t)tok * D / 2 + (e / QK) * 16 + j % 16);
@@ -2569,7 +2577,9 @@ HeadMust history_window(const Decoder* d, int window) {
     return m;
 }
 
-bool shortlist_on(const Decoder* d, int top_k) { return query_top_k(d, top_k) > 0 && head4(d).data; }
+// The shortlist head runs for top_k > 0 queries on a model with head_q4 / head_err or with a nibble-plane LM head.
+bool has_shortlist(const Decoder* d) { return head4(d).data != nullptr || d->lmh->dtype == kQ8P; }
+bool shortlist_on(const Decoder* d, int top_k) { return query_top_k(d, top_k) > 0 && has_shortlist(d); }
 
 // The feedback of a chosen token into the decoder's state.
 TokenFeedback token_feedback(Decoder* d) {
@@ -2599,6 +2609,8 @@ hipError_t run_head(Decoder* d, int top_k, hipStream_t s, bool advance = false) 
     }
     if (dense_w(h8))  // Model::linear on the final normed state itself (matvec_ref)
         QH_TRY(launch_gemv_dense(d->logits, 0, h8, d->hidden, h8.cols, 1, 0, h8.rows, s));
+    else if (h8.dtype == kQ8P)
+        QH_TRY(launch_gemv_planes(d->logits, h8, d->qa, d->da, 0, h8.rows, s));
     else
         QH_TRY(launch_gemv(d->logits, h8, d->qa, d->da, 0, h8.rows, gemv_plan(h8.dtype, h8.cols, h8.rows), s));
     return launch_argmax(d->logits, d->hp.vocab_size, d->top1_full, d->am_ws, s);
@@ -2672,7 +2684,7 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
     A((void**)&d->rows, sizeof(int32_t) * (size_t)(V + 64));
     A((void**)&d->stats, sizeof(qh_head_stats));
     A((void**)&d->top1_full, 256);
-    if (head4(d).data) {
+    if (has_shortlist(d)) {
         d->head_ws_bytes = head_workspace_bytes(V, D, 1);  // the same for every top_k the selection holds
         A(&d->head_ws, d->head_ws_bytes);
     }
@@ -2840,7 +2852,7 @@ void decoder_views(Decoder* d, qh_decoder_state* v) {
 
 int decoder_vocab(const Decoder* d) { return d->hp.vocab_size; }
 
-bool decoder_has_shortlist(const Decoder* d) { return head4(d).data != nullptr; }
+bool decoder_has_shortlist(const Decoder* d) { return has_shortlist(d); }
 
 int decoder_set_query(Decoder* d, const qh_sampler_params* p) {
     d->has_query = p != nullptr;

@@ -18,6 +18,7 @@ constexpr int kF32 = 0;  // dtype numbers as in the .qnt file
 constexpr int kF16 = 1;
 constexpr int kQ8 = 2;
 constexpr int kQ4 = 3;
+constexpr int kQ8P = 16;  // the device-only nibble-plane layout of a Q8_0 head (QH_Q8_0_PLANES)
 
 // IEEE binary16 bits -> binary32 (exact for every input, subnormals included): v_cvt_f32_f16.
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }

@@ -1212,6 +1212,48 @@ __global__ __launch_bounds__(256) void head_planes_kernel(const uint8_t* __restr
     *reinterpret_cast<uint4*>(lo + b * 16) = make_uint4(lw(a.x, c.x), lw(a.y, c.y), lw(a.z, c.z), lw(a.w, c.w));
 }
 
+// matvec_q over a nibble-plane head: rows [r0, r1), 256 per workgroup in passes of 32 through rescore_lists (8 lanes
+// a row, every load of a pass in flight, then the row's serial chain acc = fma(float(s_b) * d_b, dx_b, acc)), so each
+// value equals the Q8_0 GEMV's bit for bit. out is indexed by absolute row.
+__global__ __launch_bounds__(kSelThreads) void gemv_planes_kernel(const uint8_t* __restrict__ hi,
+                                                                  const uint8_t* __restrict__ lo,
+                                                                  const uint16_t* __restrict__ sc,
+                                                                  const int8_t* __restrict__ xq,
+                                                                  const float* __restrict__ xd, int nb, int r0, int r1,
+                                                                  float* __restrict__ out) {
+    extern __shared__ __align__(16) float ssm[];  // products [32][nb], activation codes, scales, block sums
+    float* prod = ssm;
+    int8_t* xs = reinterpret_cast<int8_t*>(ssm + kRescoreRows * nb);
+    float* xds = reinterpret_cast<float*>(xs + nb * QK);
+    int* sxs = reinterpret_cast<int*>(xds + nb);
+    __shared__ int list[kSelThreads];
+    const int tid = (int)threadIdx.x, ra = r0 + (int)blockIdx.x * kSelThreads;
+    for (int i = tid; i < nb * 2; i += kSelThreads) reinterpret_cast<uint4*>(xs)[i] = load16(xq + (size_t)i * 16);
+    for (int b = tid; b < nb; b += kSelThreads) {
+        xds[b] = xd[b];
+        int sum = 0;
+        for (int i = 0; i < QK; ++i) sum += xq[b * QK + i];
+        sxs[b] = sum;
+    }
+    list[tid] = ra + tid;
+    __syncthreads();
+    const ExactHead eh{hi, lo, sc, sxs};
+    rescore_lists<true>(list, min(kSelThreads, r1 - ra), list, 0, eh, xs, xds, nb, prod, nullptr, false, out);
+}
+
+hipError_t launch_gemv_planes(float* out, const qh_tensor& planes, const int8_t* xq, const float* xd, int r0, int r1,
+                              hipStream_t s) {
+    if (r1 <= r0) return hipSuccess;
+    const int V = planes.rows, D = planes.cols, nb = D / QK;
+    const uint8_t* hi = static_cast<const uint8_t*>(planes.data);
+    const uint8_t* lo = hi + (size_t)V * D / 2;
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(hi + (size_t)V * D);
+    const size_t lds = (size_t)kRescoreRows * nb * 4 + (size_t)nb * QK + (size_t)nb * 8;
+    qh_launch(gemv_planes_kernel, dim3((unsigned)((r1 - r0 + kSelThreads - 1) / kSelThreads)), dim3(kSelThreads), lds,
+              s, hi, lo, sc, xq, xd, nb, r0, r1, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_head_planes(const void* head8, void* planes, int V, int D, hipStream_t s) {
     const size_t n = (size_t)V * D;
     const long nblk = (long)(n / QK);

@@ -153,6 +153,9 @@ hipError_t launch_shortlist_head(const qh_tensor& head8, const qh_tensor& head4,
 
 // The nibble-plane layout (QH_Q8_0_PLANES) of a Q8_0 [V][D] head at planes (the same size, not overlapping it).
 hipError_t launch_head_planes(const void* head8, void* planes, int V, int D, hipStream_t s);
+// matvec_q over a nibble-plane head (rows [r0, r1) of out), bit-identical to the Q8_0 GEMV of the same values.
+hipError_t launch_gemv_planes(float* out, const qh_tensor& planes, const int8_t* xq, const float* xd, int r0, int r1,
+                              hipStream_t s);
 
 // Sampler::sample on the device (qh_sample.hip). Candidates: rows[0, hs->n_rows) (the shortlist head's list; every
 // other id counts as -inf) or, with rows null, every id below n_valid; the penalty looks at the ids `hist` names.

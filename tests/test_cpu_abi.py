@@ -151,7 +151,7 @@ def test_forced_allocation_failure(qh):
         L.qh_fault_alloc(-1)
 
 
-def _desc_and_tensors(qh, flags=0, kv_f32=0, ffn=512, lm=None, shortlist=True):
+def _desc_and_tensors(qh, flags=0, kv_f32=0, ffn=512, lm=None, shortlist=True, emb=2):
     """A one-layer model descriptor and tensor list (descriptors at made-up, aligned addresses: only the host checks
     of qh_decoder_create may run on them)."""
     V, D, kvd, F = 1024, 256, 64, ffn
@@ -159,7 +159,7 @@ def _desc_and_tensors(qh, flags=0, kv_f32=0, ffn=512, lm=None, shortlist=True):
     addr = iter(range(1 << 20, 1 << 30, 1 << 16))
     t = lambda dt, r, c: qh.qh_tensor(dt, r, c, next(addr))
     none = qh.qh_tensor(0, 0, 0, None)
-    ts = [t(qh.Q8_0, V, D), t(qh.F32, 1, D), t(qh.F32, 1, D), t(qh.Q4_0, D, D), t(qh.Q4_0, kvd, D),
+    ts = [t(emb, V, D), t(qh.F32, 1, D), t(qh.F32, 1, D), t(qh.Q4_0, D, D), t(qh.Q4_0, kvd, D),
           t(qh.Q4_0, kvd, D), t(qh.Q4_0, D, D), none, none, none, t(qh.F32, 1, D), t(qh.Q4_0, F, D),
           t(qh.Q4_0, F, D), t(qh.Q4_0, D, F)]
     ts += [t(qh.Q4_0, V, D), t(qh.F16, V, D // 32)] if shortlist else [none, none]
@@ -176,6 +176,10 @@ def _desc_and_tensors(qh, flags=0, kv_f32=0, ffn=512, lm=None, shortlist=True):
     (dict(lm=(1, 1024, 256)), "ERR_SHAPE", b"bad shortlist head tensors"),  # an F16 LM head with the shortlist
     (dict(lm=(2, 1000, 256)), "ERR_SHAPE", b"lm_head is 1000 x 256"),
     (dict(lm=(3, 1024, 256)), "ERR_SHAPE", b"bad shortlist head tensors"),  # Q8_0 with the shortlist (model.cpp:51)
+    (dict(emb=3), "ERR_SHAPE", b"bad shortlist head tensors"),  # a tied Q4_0 LM head with the shortlist tensors
+    (dict(emb=16), "ERR_ARG", b"nibble-plane LM head is its own shortlist"),
+    (dict(lm=(16, 1024, 256)), "ERR_ARG", b"nibble-plane LM head is its own shortlist"),
+    (dict(lm=(16, 1024, 96), shortlist=False), "ERR_SHAPE", b"lm_head: bad shape 1024 x 96"),
 ])
 def test_decoder_create_option_checks(qh, case, code, msg):
     """qh_decoder_create's checks of the load-time options (flags, kv_f32, an untied lm_head.weight), refused on the

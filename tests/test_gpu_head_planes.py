@@ -121,3 +121,101 @@ def test_planes_sweep_equals_full_head(qh, synth, gpu):
     rows = torch.stack(n_rows).cpu().numpy()
     print(f"planes sweep: rescored rows mean {rows.mean():.1f}, max {rows.max()}", flush=True)
     assert rows.max() < V // 20
+
+
+def test_matvec_planes_equals_q8(qh, synth, gpu):
+    """qh_matvec_q over the plane layout equals the Q8_0 GEMV of the same values bit for bit, row ranges included."""
+    import torch
+    V, D = 5003, 896
+    head8 = synth.q8_tensor(57, V, D)
+    h8 = qh.DeviceTensor.upload(head8, qh.Q8_0, V, D)
+    pl = qh.head_planes(h8)
+    x = synth.activations(58, 2, D, scale=0.5)
+    xq, xd = qh.quantize_q8(_dev(x, gpu))
+    for t in range(2):
+        want = qh.matvec_q(h8, xq[t], xd[t]).cpu().numpy()
+        got = qh.matvec_q(pl, xq[t], xd[t]).cpu().numpy()
+        assert (bits(got) == bits(want)).all()
+        part = torch.full((V,), 7.0, device=gpu)
+        qh.matvec_q(pl, xq[t], xd[t], out=part, r0=300, r1=4100)
+        p = part.cpu().numpy()
+        assert (bits(p[300:4100]) == bits(want[300:4100])).all() and (p[:300] == 7).all() and (p[4100:] == 7).all()
+
+
+def test_decoder_planes_equals_oracle(qh, oracle, gpu):
+    """A decoder whose tied embedding / LM head is stored as nibble planes (no head_q4 / head_err uploaded): the
+    embedding rows come from the planes, shortlist steps equal the oracle's nibble-plane head on the same hidden
+    state, full-head steps (the plane GEMV) equal the oracle's full 8-bit head, every hidden state bit for bit."""
+    from decoder_util import oracle_decoder, qnt_module
+    qnt = qnt_module()
+    hp = qnt.HParams(vocab_size=3072, n_layers=3)
+    tens = qnt.synthetic_q4mix(23, hp)
+    V, D = hp.vocab_size, hp.dim
+    planes_np = oracle.head_planes(np.asarray(tens["model.embed_tokens.weight"].data), V, D)
+    ctx = 512
+    orc = oracle_decoder(oracle, hp, tens, ctx_len=ctx)
+    dec = qh.Decoder(hp, tens, ctx_len=ctx, head_planes=True)
+
+    def check_shortlist(tag):
+        hq, hd = dec.hq()
+        o = oracle.shortlist_planes(planes_np, V, D, hq, hd, top_k=1)
+        assert dec.stats()["n_rows"] == o["n_rows"], tag
+        assert (bits(dec.logits()) == bits(o["logits"])).all(), tag
+        return oracle.argmax(o["logits"], V)
+
+    ids = np.random.default_rng(5).integers(0, V, 77).astype(np.int32)
+    r = orc.forward_batch(ids, 0, top_k=0)
+    dec.prefill(ids, 0, top_k=1)
+    assert (bits(dec.hidden()) == bits(r["hidden"])).all()
+    tok = check_shortlist("prefill")
+    assert tok == oracle.argmax(r["logits"])
+    dec.begin(16, top_k=1)
+    pos = len(ids)
+    for step in range(8):
+        top_k = 0 if step % 3 == 2 else 1
+        r = orc.forward(tok, pos, top_k=0)
+        dec.step(top_k=top_k)
+        assert (bits(dec.hidden()) == bits(r["hidden"])).all(), step
+        if top_k:
+            assert check_shortlist(step) == oracle.argmax(r["logits"]), step
+        else:
+            assert (bits(dec.logits()) == bits(r["logits"])).all(), step
+            assert dec.top1_full() == oracle.argmax(r["logits"]), step
+        tok = oracle.argmax(r["logits"])
+        pos += 1
+
+
+def test_decoder_planes_q4mix_stream_equals_reference(qh, oracle, gpu):
+    """The benchmark model with its tied head as nibble planes: the 256 greedy tokens after the 512-token prompt equal
+    the reference's gen stream, with each forward's chosen logit and final-state digest (tests/golden/e2e_q4mix.npz);
+    the rescored rows equal the oracle's nibble-plane head at every 64th forward."""
+    import os
+    from conftest import GOLDEN
+    from decoder_util import qnt_module
+    from test_gpu_decoder import state_digest
+    qnt = qnt_module()
+    g = np.load(os.path.join(GOLDEN, "e2e_q4mix.npz"), allow_pickle=False)
+    hp = qnt.HParams()
+    tens = qnt.synthetic_q4mix(int(g["seed"]), hp)
+    V, D = hp.vocab_size, hp.dim
+    planes_np = oracle.head_planes(np.asarray(tens["model.embed_tokens.weight"].data), V, D)
+    dec = qh.Decoder(hp, tens, ctx_len=4096, head_planes=True)
+    del tens
+    n_gen = len(g["out"])
+    dec.prefill(g["prompt"], 0, top_k=1)
+    dec.begin(n_gen + 1)
+    tops, digs = [], []
+    for s in range(n_gen + 1):
+        st = dec.stats()
+        tops.append(st["top1_logit"])
+        digs.append(state_digest(dec.hidden(), *dec.hq()))
+        if s % 64 == 0:
+            hq, hd = dec.hq()
+            o = oracle.shortlist_planes(planes_np, V, D, hq, hd, top_k=1)
+            assert st["n_rows"] == o["n_rows"], s
+        if s < n_gen:
+            dec.step(top_k=1)
+    out = dec.outputs(n_gen)
+    assert (out == g["out"]).all()
+    assert (np.array(digs) == g["state_digests"]).all()
+    assert (bits(np.array(tops[:n_gen], np.float32)) == bits(g["top_logit"])).all()
