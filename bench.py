@@ -227,9 +227,55 @@ def head_bench(qh, synth, torch, oracle, steps, warmup):
     mean_rows = float(np.mean(rows))
     sl_bytes = screen + mean_rows * row8
     full_bytes = V * row8
-    del g, heads, r8, r4, re
+    del g, heads, r4, re
+
+    # The nibble-plane head (no Q4_0 copy, no error stream): planes built on the device from the Q8_0 copies, as many
+    # as make the screened bytes (high plane + scales) a >= 1 GiB rotation.
+    screen_pl = V * (D // 2 + 2 * (D // 32))
+    copies_pl = max(1, math.ceil(GIB / screen_pl))
+    pls = [qh.head_planes(r8.tensors[c % copies]) for c in range(copies_pl)]
+    del r8
+    pheads = [qh.ShortlistHead(p, None, None, top_k=1) for p in pls]
+    pheads[0](xq[0], xd[0])
+    pst = pheads[0].stats()
+    po = oracle.shortlist_planes(oracle.head_planes(head8, V, D), V, D, xq[0].cpu().numpy(), xd[0].cpu().numpy(),
+                                 top_k=1)
+    if pst["top1"] != st["top1"] or pst["n_rows"] != po["n_rows"] or pst["top1"] != oracle.argmax(po["logits"]):
+        raise SystemExit("bench: GPU nibble-plane head differs from the oracle")
+    p_rows = []
+    for t in range(n_vec):
+        pheads[0](xq[t], xd[t])
+        p_rows.append(pheads[0].stats()["n_rows"])
+    xs = torch.from_numpy(synth.activations(502, n_sweep, D, scale=0.5)).cuda()
+    sq, sd = qh.quantize_q8(xs)
+    p_sweep = []
+    for t in range(n_sweep):
+        pheads[0](sq[t], sd[t])
+        p_sweep.append(pheads[0].stats()["n_rows"])
+    p_sweep = np.array(p_sweep, np.float64)
+    del xs, sq, sd
+
+    def pl_step():
+        for c in range(copies_pl):
+            for t in range(n_vec):
+                pheads[c](xq[t], xd[t])
+
+    g = capture(torch, pl_step)
+    sec = time_graph(torch, g, steps, warmup)
+    pl_us = sec / (steps * copies_pl * n_vec) * 1e6
+    del g, pheads, pls
+    pl_mean = float(np.mean(p_rows))
+    pl_bytes = screen_pl + pl_mean * row8
+    planes = {"us": pl_us, "mean_rows": pl_mean, "rows": p_rows, "bytes": pl_bytes, "GBps": pl_bytes / pl_us / 1e3,
+              "copies": copies_pl, "extra_memory_bytes": 0,
+              "sweep_1024": {"vectors": n_sweep, "x_seed": 502, "rows_mean": float(p_sweep.mean()),
+                             "rows_median": float(np.median(p_sweep)), "rows_p99": float(np.percentile(p_sweep, 99)),
+                             "rows_max": float(p_sweep.max()),
+                             "bytes_mean": float((screen_pl + p_sweep * row8).mean()),
+                             "bytes_mean_frac_of_full_head": float((screen_pl + p_sweep * row8).mean() / full_bytes)}}
     sweep_bytes = screen + sweep_rows * row8
     return {"shortlist_us": sl_us, "full_head_us": full_us, "mean_rows": mean_rows, "rows": rows,
+            "nibble_planes": planes,
             "shortlist_bytes": sl_bytes, "full_head_bytes": full_bytes,
             "shortlist_GBps": sl_bytes / sl_us / 1e3, "full_head_GBps": full_bytes / full_us / 1e3,
             "q8_gemv_151936x896": {"us_per_call": gemv_us, "bytes": gemv_bytes, "GBps": gemv_bytes / gemv_us / 1e3,
@@ -353,15 +399,16 @@ def state_digest(hidden, hq, hd):
     return np.frombuffer(h1 + h2, np.uint64)
 
 
-def e2e_bench(qh, torch, hp, tens, steps=256, warmup=3, n_prompt=512, check=True, mode="greedy"):
+def e2e_bench(qh, torch, hp, tens, steps=256, warmup=3, n_prompt=512, check=True, mode="greedy", head_planes=False):
     """End-to-end generation on the q4mix Qwen2.5-0.5B-shaped model (configuration 5): a 512-token prompt in
     32-token prefill chunks, then `steps` decode steps, each one replay of a HIP graph holding one captured decode step
     (the chosen token is fed back on the device). A warm-up run of `warmup` steps precedes the timed run; the timed
     stream (positions 512 ..) is checked against the reference engine's. mode "greedy": top-1 shortlist queries and
     greedy picks (`quanta gen --greedy`, tests/golden/e2e_q4mix.npz); "chat": the reference's default sampler
     parameters for both the head queries (top-k 20, the whole history as must ids) and the draws (temperature 0.7,
-    top-p 0.8, penalty 1.1), seed 0x51A7C0DE (tests/golden/e2e_sampled.npz)."""
-    dec = qh.Decoder(hp, tens, ctx_len=4096)
+    top-p 0.8, penalty 1.1), seed 0x51A7C0DE (tests/golden/e2e_sampled.npz). head_planes: the tied head as nibble
+    planes (no Q4_0 copy or error bounds on the device; the same stream)."""
+    dec = qh.Decoder(hp, tens, ctx_len=4096, head_planes=head_planes)
     chat = mode == "chat"
     if chat:
         dec.set_query(qh.sampler_params())
@@ -660,6 +707,9 @@ def main():
     if args.only == "head":
         print(json.dumps({"shortlist_head_151936x896": rnd(head_bench(qh, synth, torch, orc.oracle, 5, 1))}),
               flush=True)
+        hp, tens = e2e_model()
+        ep = e2e_bench(qh, torch, hp, tens, steps=args.steps, warmup=args.warmup, head_planes=True)
+        print(json.dumps({"decode_nibble_planes": rnd(ep)}), flush=True)
         return 0
     if args.only == "sampler":
         print(json.dumps({"sampler_151936": rnd(sampler_bench(qh, torch, orc))}), flush=True)
@@ -744,6 +794,10 @@ def main():
                 extra[f"{name}_prefill_{n}x{k}_M{m}"] = rnd(r)
         log("shortlist head")
         extra["shortlist_head_151936x896"] = rnd(head_bench(qh, synth, torch, orc.oracle, 5, 1))
+        log("greedy decode with the nibble-plane head")
+        ep = e2e_bench(qh, torch, hp, tens, steps=args.steps, warmup=args.warmup, head_planes=True)
+        extra["decode_nibble_planes"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in ep.items()
+                                         if k != "prefill_ms"}
         log("sampler draws over the full vocabulary")
         extra["sampler_151936"] = rnd(sampler_bench(qh, torch, orc))
         log("sampling mode: prefill 512 + decode steps of the chat flow")
