@@ -349,6 +349,16 @@ int qh_decoder_step(qh_decoder* d, int top_k, void* stream);
 
 int qh_decoder_views(qh_decoder* d, qh_decoder_state* v);
 
+/* The prefill stack: how many prompt tokens later qh_decoder_prefill calls take through each layer's norms and
+ * matmuls at once. 32 (the default) is the reference's chunk (Model::kBatch, model.h:52; forward_batch,
+ * model.cpp:349-361); a multiple of 32 up to 1024 runs the same arithmetic on larger batches (the matmul tile kernels
+ * at M up to `stack`), attention still in 32-token sub-chunks in order, so every hidden state, cache row and logit is
+ * bit-identical to the 32-token chunks. Reallocates the decoder's work buffers: it synchronises the device, the
+ * pointers qh_decoder_views gave (xq / xd) change and their contents are lost, and a step captured in a HIP graph
+ * before the call must be captured again. On failure the previous stack stays.
+ * Replaces: nothing (the reference's chunk is a compile-time constant); a scheduling choice of the GPU path. */
+int qh_decoder_set_prefill_stack(qh_decoder* d, int stack);
+
 /* Stages of a decode step, as qh_decoder_step_timed names them: per layer l, id l * QH_STAGES_PER_LAYER + one of
  * QH_STAGE_QKV (rmsnorm + q/k/v projections), QH_STAGE_ATTENTION, QH_STAGE_O (o projection + residual),
  * QH_STAGE_GATE_UP (rmsnorm + gate/up projections + SwiGLU), QH_STAGE_DOWN (down projection + residual); then

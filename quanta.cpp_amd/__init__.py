@@ -83,7 +83,8 @@ EXPORTS = ("qh_last_error", "qh_version", "qh_init", "qh_quant_bytes", "qh_tenso
            "qh_head_planes", "qh_shortlist_planes",
            "qh_sampler_state", "qh_sample", "qh_sample_workspace_bytes", "qh_sample_ws", "qh_decoder_create",
            "qh_decoder_destroy",
-           "qh_decoder_prefill", "qh_decoder_begin", "qh_decoder_step", "qh_decoder_views", "qh_decoder_step_timed",
+           "qh_decoder_prefill", "qh_decoder_begin", "qh_decoder_step", "qh_decoder_views",
+           "qh_decoder_set_prefill_stack", "qh_decoder_step_timed",
            "qh_decoder_set_query",
            "qh_decoder_set_sampler")
 
@@ -123,6 +124,7 @@ def _bind(lib):
         "qh_decoder_begin": ([vp, i32, vp, i32, vp], i32),
         "qh_decoder_step": ([vp, i32, vp], i32),
         "qh_decoder_views": ([vp, C.POINTER(qh_decoder_state)], i32),
+        "qh_decoder_set_prefill_stack": ([vp, i32], i32),
         "qh_decoder_step_timed": ([vp, i32, vp, vp, vp, i32, vp], i32),
         "qh_sampler_state": ([C.c_uint64], C.c_uint64),
         "qh_sample": ([vp, i32, vp, vp, vp, i32, C.POINTER(qh_sampler_params), vp, vp, vp], i32),
@@ -429,6 +431,14 @@ class Decoder:
             self.close()
         except Exception:
             pass
+
+    def set_prefill_stack(self, stack: int):
+        """Prompt tokens per launch of each layer's norms and matmuls (32 = the reference's chunk; up to 1024), with
+        bit-identical results; the device views are re-read (the work buffers move)."""
+        _check(lib().qh_decoder_set_prefill_stack(self.h, stack))
+        st = qh_decoder_state()
+        _check(lib().qh_decoder_views(self.h, C.byref(st)))
+        self.views = st
 
     def prefill(self, tokens, pos0: int = 0, top_k: int = 1):
         torch = _torch()

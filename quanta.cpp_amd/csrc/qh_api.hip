@@ -572,6 +572,13 @@ int qh_decoder_views(qh_decoder* d, qh_decoder_state* v) {
     return QH_OK;
 }
 
+int qh_decoder_set_prefill_stack(qh_decoder* d, int stack) {
+    if (!d) return fail(QH_ERR_ARG, "qh_decoder_set_prefill_stack: null decoder");
+    if (stack < 32 || stack > 1024 || stack % 32 != 0)
+        return fail(QH_ERR_ARG, "qh_decoder_set_prefill_stack: stack %d is not a multiple of 32 in [32, 1024]", stack);
+    return check_hip(decoder_set_prefill_stack(reinterpret_cast<Decoder*>(d), stack), "qh_decoder_set_prefill_stack");
+}
+
 int qh_decoder_set_query(qh_decoder* d, const qh_sampler_params* p) {
     if (!d) return fail(QH_ERR_ARG, "qh_decoder_set_query: null decoder");
     if (p) {

@@ -43,6 +43,7 @@ namespace qh {
 namespace {
 
 constexpr int kChunk = 32;            // prefill chunk (reference Model::kBatch, model.h:52)
+constexpr int kMaxStack = 1024;       // prefill stack limit (tokens whose matmuls share a launch)
 constexpr int kMaxCtx = 8192;         // positions the attention kernel's score array holds
 constexpr int kVStageBytes = 96 * 1024;  // LDS for staged V rows (768 rows at head_dim 64)
 constexpr int kFuseLds = 65536;       // dynamic LDS limit of the fused GEMV kernels
@@ -2102,6 +2103,12 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(const float* __restrict
 // Prefill / decode bookkeeping on the device.
 __global__ void set_int_kernel(int* p, int value) { *p = value; }
 
+// The first positions of a prefill stack's 32-token attention sub-chunks: p[i] = base + 32 i, i < n.
+__global__ void set_subpos_kernel(int* p, int base, int n) {
+    const int i = (int)threadIdx.x;
+    if (i < n) p[i] = base + kChunk * i;
+}
+
 // The token a step chose: the sampler's pick when there is one, else the head's greedy top-1.
 struct Pick {
     const int32_t* sampled;
@@ -2153,6 +2160,11 @@ struct Decoder {
     float* escr = nullptr;      // decode attention: a row of exp values, then one of weights, per head
     int escr_stride = 0;
     int32_t* tokens = nullptr;  // [kChunk] prefill input / [0] decode input
+    // Prefill stack: the tokens whose norms and matmuls share one launch (kChunk, the reference's Model::kBatch, by
+    // default; larger stacks run the matmul tile kernels at M up to kMaxStack). Attention runs each stack as 32-token
+    // sub-chunks in order, the sub-chunk i starting at subpos[i].
+    int stack = kChunk;
+    int* subpos = nullptr;
     // token history (prompt ids since position 0, then each chosen id) and the optional query / sampler settings
     int32_t* hist = nullptr;  // [ctx_len + 1]
     int* hist_len = nullptr;
@@ -2206,6 +2218,45 @@ hipError_t dalloc(Decoder* d, void** p, size_t bytes) {
     if (fault_alloc_fires()) return hipErrorOutOfMemory;  // qh_fault_alloc's forced failure
     hipError_t e = hipMalloc(p, bytes < 256 ? 256 : bytes);
     if (e == hipSuccess) d->allocs.push_back(*p);
+    return e;
+}
+
+void dfree(Decoder* d, void* p) {
+    if (!p) return;
+    for (size_t i = 0; i < d->allocs.size(); ++i)
+        if (d->allocs[i] == p) {
+            d->allocs.erase(d->allocs.begin() + (long)i);
+            break;
+        }
+    (void)hipFree(p);
+}
+
+// The work buffers of a prefill stack of c tokens: the residual stream, projections, MLP rows, int8 activations and
+// their scales, the f32 copies for unquantized matrices and the attention sub-chunks' positions. On failure the ones
+// allocated stay listed (the caller frees them).
+hipError_t alloc_stack(Decoder* d, int c) {
+    const qh_model_desc& hp = d->hp;
+    const size_t D = hp.dim, F = hp.ffn_dim, wide = D > F ? D : F, kvd = (size_t)hp.n_kv_heads * hp.head_dim;
+    hipError_t e = hipSuccess;
+    auto A = [&](void** p, size_t b) {
+        if (e == hipSuccess) e = dalloc(d, p, b);
+    };
+    A((void**)&d->x, sizeof(float) * c * D);
+    A((void**)&d->o, sizeof(float) * c * D);
+    A((void**)&d->q, sizeof(float) * c * D);
+    A((void**)&d->k, sizeof(float) * c * kvd);
+    A((void**)&d->v, sizeof(float) * c * kvd);
+    A((void**)&d->g, sizeof(float) * c * F);
+    A((void**)&d->u, sizeof(float) * c * F);
+    A((void**)&d->qa, c * wide);
+    A((void**)&d->qb, c * wide);
+    A((void**)&d->da, sizeof(float) * c * (wide / QK));
+    A((void**)&d->db, sizeof(float) * c * (wide / QK));
+    if (d->dense) {
+        A((void**)&d->fa, sizeof(float) * c * D);
+        A((void**)&d->fb, sizeof(float) * c * wide);
+    }
+    A((void**)&d->subpos, sizeof(int) * (kMaxStack / kChunk));
     return e;
 }
 
@@ -2404,37 +2455,57 @@ hipError_t gate_up(Decoder* d, int l, hipStream_t s) {
     return swiglu_down_input(d, wg.rows, 1, s);
 }
 
-hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
+// Attention of a chunk of n <= kChunk tokens at positions *pos_dev .. + n - 1 whose projections start at row r0 of
+// q / k / v; outputs to rows r0 .. of qb / db (and fb).
+hipError_t attention_chunk(Decoder* d, int l, int n, int r0, const int* pos_dev, hipStream_t s) {
     const qh_model_desc& hp = d->hp;
     const size_t layer_k = (size_t)hp.ctx_len * hp.n_kv_heads * hp.head_dim;
     const size_t layer_v = (size_t)v_ctx(hp.ctx_len) * hp.n_kv_heads * hp.head_dim;
+    const size_t qd = (size_t)hp.n_heads * hp.head_dim, kvd = (size_t)hp.n_kv_heads * hp.head_dim;
+    const float *q = d->q + r0 * qd, *k = d->k + r0 * kvd, *v = d->v + r0 * kvd;
+    int8_t* oq = d->qb + r0 * qd;
+    float* od = d->db + r0 * (qd / QK);
+    float* of = d->fb ? d->fb + r0 * qd : nullptr;
     const dim3 grid(hp.n_heads, n);
     if (d->kv32) {  // the f32 cache: prefill and decode alike
         const size_t layer_kv = (size_t)hp.ctx_len * hp.n_kv_heads * hp.head_dim;
         if (hp.head_dim == 64)
-            qh_launch((attention_f32_kernel<64>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
-                      bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
-                      d->kcf + l * layer_kv, d->vcf + l * layer_kv, d->qb, d->db, d->status, d->fb);
+            qh_launch((attention_f32_kernel<64>), grid, dim3(256), 0, s, q, k, v, bias(d, l, L_BQ),
+                      bias(d, l, L_BK), bias(d, l, L_BV), d->cs, pos_dev, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
+                      d->kcf + l * layer_kv, d->vcf + l * layer_kv, oq, od, d->status, of);
         else
-            qh_launch((attention_f32_kernel<128>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
-                      bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
-                      d->kcf + l * layer_kv, d->vcf + l * layer_kv, d->qb, d->db, d->status, d->fb);
+            qh_launch((attention_f32_kernel<128>), grid, dim3(256), 0, s, q, k, v, bias(d, l, L_BQ),
+                      bias(d, l, L_BK), bias(d, l, L_BV), d->cs, pos_dev, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
+                      d->kcf + l * layer_kv, d->vcf + l * layer_kv, oq, od, d->status, of);
+    } else if (hp.head_dim == 64) {
+        qh_launch((attention_kernel<64, 2>), grid, dim3(256), 0, s, q, k, v, bias(d, l, L_BQ), bias(d, l, L_BK),
+                  bias(d, l, L_BV), d->cs, pos_dev, hp.ctx_len, hp.n_heads, hp.n_kv_heads, d->kc + l * layer_k,
+                  d->vc + l * layer_v, oq, od, d->status, of);
+    } else {
+        qh_launch((attention_kernel<128>), grid, dim3(256), 0, s, q, k, v, bias(d, l, L_BQ), bias(d, l, L_BK),
+                  bias(d, l, L_BV), d->cs, pos_dev, hp.ctx_len, hp.n_heads, hp.n_kv_heads, d->kc + l * layer_k,
+                  d->vc + l * layer_v, oq, od, d->status, of);
+    }
+    return hipGetLastError();
+}
+
+hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
+    const qh_model_desc& hp = d->hp;
+    if (n > kChunk) {  // a prefill stack: its 32-token sub-chunks in order (each reads the rows the ones before wrote)
+        for (int i = 0; i * kChunk < n; ++i)
+            QH_TRY(attention_chunk(d, l, min(kChunk, n - i * kChunk), i * kChunk, d->subpos + i, s));
+        return hipSuccess;
+    }
+    if (n == 1 && hp.head_dim == 64 && d->fuse && !d->kv32) {  // decode: one 16-wave workgroup per head
+        const size_t layer_k = (size_t)hp.ctx_len * hp.n_kv_heads * hp.head_dim;
+        const size_t layer_v = (size_t)v_ctx(hp.ctx_len) * hp.n_kv_heads * hp.head_dim;
+        qh_launch((attention_decode_kernel<64>), dim3(hp.n_heads / hp.n_kv_heads, hp.n_kv_heads), dim3(1024), 0, s,
+                  d->q, d->k, d->v, d->kc + l * layer_k, d->pos, hp.ctx_len, hp.n_heads / hp.n_kv_heads,
+                  bias(d, l, L_BQ), bias(d, l, L_BK), hp.n_kv_heads, bias(d, l, L_BV), d->cs, d->vc + l * layer_v,
+                  d->qb, d->db, d->escr, d->escr_stride, d->status, d->fb);
         return hipGetLastError();
     }
-    if (n == 1 && hp.head_dim == 64 && d->fuse)  // decode: one 16-wave workgroup per head
-        qh_launch((attention_decode_kernel<64>), dim3(hp.n_heads / hp.n_kv_heads, hp.n_kv_heads), dim3(1024), 0,
-                           s, d->q, d->k, d->v, d->kc + l * layer_k, d->pos, hp.ctx_len, hp.n_heads / hp.n_kv_heads,
-                           bias(d, l, L_BQ), bias(d, l, L_BK), hp.n_kv_heads, bias(d, l, L_BV), d->cs,
-                           d->vc + l * layer_v, d->qb, d->db, d->escr, d->escr_stride, d->status, d->fb);
-    else if (hp.head_dim == 64)
-        qh_launch((attention_kernel<64, 2>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
-                           bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
-                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status, d->fb);
-    else
-        qh_launch((attention_kernel<128>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
-                           bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads,
-                           d->kc + l * layer_k, d->vc + l * layer_v, d->qb, d->db, d->status, d->fb);
-    return hipGetLastError();
+    return attention_chunk(d, l, n, 0, d->pos, s);  // a chunk of the prefill (either cache), or the f32 cache
 }
 
 // One decode step's layers for the token in d->tokens[0], from its embedding. Leaves the final normed hidden state
@@ -2477,7 +2548,7 @@ hipError_t decode_layers(Decoder* d, hipStream_t s) {
 // (the matmul launch and swiglu_quant_kernel instead: one launch per operation, different formats or widths, rows
 // not a multiple of 32, unaligned operands).
 bool swiglu_fused(Decoder* d, const qh_tensor& wg, const qh_tensor& wu, int n, hipStream_t s) {
-    if (!d->fuse || d->hadamard || d->dense || wg.dtype != wu.dtype || wg.rows != wu.rows || wg.cols != wu.cols || wg.rows % QK != 0 ||
+    if (n > kChunk || !d->fuse || d->hadamard || d->dense || wg.dtype != wu.dtype || wg.rows != wu.rows || wg.cols != wu.cols || wg.rows % QK != 0 ||
         (wg.dtype != kQ8 && wg.dtype != kQ4) || wg.cols % QK != 0 || wg.cols < 2 * QK)
         return false;
     const uint8_t *qg = quants(wg), *qu = quants(wu);
@@ -2634,12 +2705,11 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
     d->dense = dense_w(*d->lmh);
     for (int l = 0; l < hp->n_layers; ++l)
         for (int m : {L_WQ, L_WK, L_WV, L_WO, L_WG, L_WU, L_WD}) d->dense = d->dense || dense_w(lt(d, l, m));
-    const int D = hp->dim, F = hp->ffn_dim, V = hp->vocab_size, hd = hp->head_dim;
+    const int D = hp->dim, V = hp->vocab_size, hd = hp->head_dim;
     const size_t kvd = (size_t)hp->n_kv_heads * hd;
     const size_t kv_bytes = (size_t)hp->n_layers * hp->ctx_len * kvd * 2;
     const size_t v_bytes = (size_t)hp->n_layers * v_ctx(hp->ctx_len) * kvd * 2;
     const size_t kv32_bytes = (size_t)hp->n_layers * hp->ctx_len * kvd * 4;
-    const int wide = D > F ? D : F;
     hipError_t e = hipSuccess;
     auto A = [&](void** p, size_t b) {
         if (e == hipSuccess) e = dalloc(d, p, b);
@@ -2652,22 +2722,8 @@ int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tens
         A((void**)&d->vc, v_bytes);
     }
     A((void**)&d->cs, sizeof(float) * (size_t)hp->ctx_len * hd);
-    A((void**)&d->x, sizeof(float) * kChunk * D);
-    A((void**)&d->o, sizeof(float) * kChunk * D);
-    A((void**)&d->q, sizeof(float) * kChunk * D);
-    A((void**)&d->k, sizeof(float) * kChunk * kvd);
-    A((void**)&d->v, sizeof(float) * kChunk * kvd);
-    A((void**)&d->g, sizeof(float) * kChunk * F);
-    A((void**)&d->u, sizeof(float) * kChunk * F);
+    if (e == hipSuccess) e = alloc_stack(d, kChunk);
     A((void**)&d->hidden, sizeof(float) * D);
-    A((void**)&d->qa, (size_t)kChunk * wide);
-    A((void**)&d->qb, (size_t)kChunk * wide);
-    A((void**)&d->da, sizeof(float) * kChunk * (wide / QK));
-    A((void**)&d->db, sizeof(float) * kChunk * (wide / QK));
-    if (d->dense) {
-        A((void**)&d->fa, sizeof(float) * kChunk * D);
-        A((void**)&d->fb, sizeof(float) * kChunk * wide);
-    }
     d->escr_stride = escr_stride(hp->ctx_len);
     A((void**)&d->escr, sizeof(float) * 2 * (size_t)hp->n_heads * d->escr_stride);  // exp rows, weight rows
     A((void**)&d->tokens, sizeof(int32_t) * kChunk);
@@ -2723,6 +2779,28 @@ void decoder_destroy(Decoder* d) {
     delete d;
 }
 
+hipError_t decoder_set_prefill_stack(Decoder* d, int c) {
+    if (c == d->stack) return hipSuccess;
+    QH_TRY(hipDeviceSynchronize());  // nothing in flight uses the buffers that are replaced
+    void** slots[] = {(void**)&d->x,  (void**)&d->o,  (void**)&d->q,  (void**)&d->k,  (void**)&d->v,
+                      (void**)&d->g,  (void**)&d->u,  (void**)&d->qa, (void**)&d->qb, (void**)&d->da,
+                      (void**)&d->db, (void**)&d->fa, (void**)&d->fb, (void**)&d->subpos};
+    constexpr int kSlots = (int)(sizeof(slots) / sizeof(slots[0]));
+    void* old[kSlots];
+    for (int i = 0; i < kSlots; ++i) {
+        old[i] = *slots[i];
+        *slots[i] = nullptr;
+    }
+    const hipError_t e = alloc_stack(d, c);
+    for (int i = 0; i < kSlots; ++i) {
+        void* drop = e == hipSuccess ? old[i] : *slots[i];
+        if (e != hipSuccess) *slots[i] = old[i];  // keep the previous stack on failure
+        dfree(d, drop);
+    }
+    if (e == hipSuccess) d->stack = c;
+    return e;
+}
+
 hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, int top_k, hipStream_t s) {
     const qh_model_desc& hp = d->hp;
     const int D = hp.dim;
@@ -2732,9 +2810,13 @@ hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, i
                        d->hist_len, hp.ctx_len + 1);
     QH_TRY(hipGetLastError());
     int last = 0;
-    for (int c0 = 0; c0 < n; c0 += kChunk) {
-        const int m = n - c0 < kChunk ? n - c0 : kChunk;
-        qh_launch(set_int_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + c0);
+    for (int c0 = 0; c0 < n; c0 += d->stack) {
+        const int m = n - c0 < d->stack ? n - c0 : d->stack;
+        if (m > kChunk)
+            qh_launch(set_subpos_kernel, dim3(1), dim3(kMaxStack / kChunk), 0, s, d->subpos, pos0 + c0,
+                      (m + kChunk - 1) / kChunk);
+        else
+            qh_launch(set_int_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + c0);
         QH_TRY(hipGetLastError());
         QH_TRY(embed(d, tokens + c0, m, s));
         QH_TRY(prefill_layers(d, m, s));

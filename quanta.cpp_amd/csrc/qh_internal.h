@@ -170,6 +170,8 @@ hipError_t launch_sample(const float* logits, int n_valid, const int32_t* rows, 
 struct Decoder;
 int decoder_create(const qh_model_desc* hp, const qh_tensor* tensors, int n_tensors, Decoder** out);
 void decoder_destroy(Decoder* d);
+// The prefill stack (tokens whose matmuls share a launch, kChunk..1024): reallocates the work buffers (synchronises).
+hipError_t decoder_set_prefill_stack(Decoder* d, int c);
 hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, int top_k, hipStream_t s);
 hipError_t decoder_begin(Decoder* d, int top_k, int32_t* out, int out_cap, hipStream_t s);
 hipError_t decoder_step(Decoder* d, int top_k, hipStream_t s);

@@ -222,3 +222,13 @@ def test_planes_entry_points_host_checks(qh):
     assert call(pl, 16) == qh.ERR_NOMEM  # workspace too small
     q.top_k = 0
     assert call(pl, 1 << 30) == qh.ERR_UNSUPPORTED
+
+
+def test_prefill_stack_argument_checks(qh):
+    """qh_decoder_set_prefill_stack refuses a null decoder and stacks that are no multiple of 32 in [32, 1024] before
+    it touches the decoder (a made-up handle here)."""
+    L = qh.lib()
+    assert L.qh_decoder_set_prefill_stack(None, 64) == qh.ERR_ARG
+    for bad in (0, 16, 48, 1056, -32):
+        assert L.qh_decoder_set_prefill_stack(C.c_void_p(4096), bad) == qh.ERR_ARG
+        assert b"multiple of 32" in L.qh_last_error()
