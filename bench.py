@@ -483,6 +483,35 @@ def e2e_bench(qh, torch, hp, tens, steps=256, warmup=3, n_prompt=512, check=True
             "stream_equals_reference": parity, "tokens": int(steps), "prompt": int(n_prompt), **r}
 
 
+def prefill_stack_bench(qh, torch, hp, tens, stacks=(32, 128, 512), reps=5, n_prompt=512):
+    """Prefill of the 512-token prompt alone with each prefill stack (qh_decoder_set_prefill_stack: 32 is the
+    reference's chunk), best of `reps` runs between HIP events; after each, the final normed state's digest is
+    checked against the reference's (tests/golden/e2e_q4mix.npz, forward 0)."""
+    ids = np.random.default_rng(9).integers(0, hp.vocab_size, n_prompt).astype(np.int32)
+    g = np.load(os.path.join(ROOT, "tests", "golden", "e2e_q4mix.npz"), allow_pickle=False)
+    dec = qh.Decoder(hp, tens, ctx_len=4096)
+    out = {}
+    for st in stacks:
+        dec.set_prefill_stack(st)
+        best = None
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            dec.prefill(ids, 0, top_k=1)
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1)
+            best = ms if best is None else min(best, ms)
+        ok = bool((state_digest(dec.hidden(), *dec.hq()) == g["state_digests"][0]).all())
+        if not ok:
+            raise SystemExit(f"bench: prefill with stack {st} differs from the reference's state")
+        out[f"stack_{st}"] = {"prefill_ms": round(best, 3), "prefill_tok_per_s": round(n_prompt / best * 1e3, 1),
+                              "state_equals_reference": ok}
+    dec.close()
+    return out
+
+
 def e2e_cpu_sampled(hp, tens, n_prompt=512, n_gen=16):
     """The reference's Session in the chat flow on the host cores (oracle/_ref): the batched prefill then n_gen
     sampled tokens (default SamplerParams for the head queries and the draws), timed as two runs that differ by
@@ -672,7 +701,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end prefill + decode measurement")
-    ap.add_argument("--only", choices=["e2e", "roofline", "prefill", "sampling", "head", "sampler", "stages"],
+    ap.add_argument("--only", choices=["e2e", "roofline", "prefill", "sampling", "head", "sampler", "stages",
+                                       "prefill_stack"],
                     help="one measurement alone (for counter runs): e2e = --e2e-only; roofline = a 256 MiB copy "
                          "(counter calibration) then the Q4_0 GEMV rotation; prefill = Q4_0 4864x896 and 896x4864 at M = 512, "
                          "then 9728x896 (the decoder's gate + up rows) and 896x4864 (down) at M = 32")
@@ -718,6 +748,10 @@ def main():
         hp, tens = e2e_model()
         r = e2e_bench(qh, torch, hp, tens, steps=args.steps, warmup=args.warmup, mode="chat")
         print(json.dumps({"sampling_chat": rnd(r)}), flush=True)
+        return 0
+    if args.only == "prefill_stack":
+        hp, tens = e2e_model()
+        print(json.dumps({"prefill_stack": prefill_stack_bench(qh, torch, hp, tens)}), flush=True)
         return 0
     if args.only == "stages":
         hp, tens = e2e_model()
@@ -792,6 +826,8 @@ def main():
             for m in (32, 128, 512):
                 r = prefill_rotation(qh, synth, torch, dtype, n, k, m, 5, 1)
                 extra[f"{name}_prefill_{n}x{k}_M{m}"] = rnd(r)
+        log("prefill of the 512-token prompt by prefill stack")
+        extra["prefill_stack"] = prefill_stack_bench(qh, torch, hp, tens)
         log("shortlist head")
         extra["shortlist_head_151936x896"] = rnd(head_bench(qh, synth, torch, orc.oracle, 5, 1))
         log("greedy decode with the nibble-plane head")
