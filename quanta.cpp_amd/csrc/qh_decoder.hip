@@ -811,7 +811,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv,
     const float* __restrict__ cs, const int* __restrict__ pos_dev, int ctx, int n_heads, int n_kv,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int8_t* __restrict__ oq, float* __restrict__ od,
-    int* __restrict__ status, float* __restrict__ of) {
+    int* __restrict__ status, float* __restrict__ of, int single) {
     constexpr int HALF = HD / 2, CPR = HD / 8;           // 16-byte chunks per f16 K row
     constexpr int kVRows = (WPE == 1 ? kVStageBytes : 32 * 1024) / (HD * 2);  // V rows one LDS stage holds (mult. of 8)
     constexpr int kVBlk = kVRows / 8;                    // 8-row blocks per stage
@@ -825,13 +825,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     __shared__ uint64_t exptab[32];
     ExpTab et;
     et.load();
-    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int pos0 = *pos_dev, pos = pos0 + t, nrows = pos + 1;
+    // single: every token of a prefill stack is its own chunk (token y = blockIdx.y at position *pos_dev + y), its
+    // earlier rows all in the cache already (kv_store_kernel), so the workgroup rebuilds only its own row and stores
+    // none.
+    const int h = blockIdx.x, y = blockIdx.y, t = single ? 0 : y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos0 = *pos_dev + (single ? y : 0), pos = pos0 + t, nrows = pos + 1;
     if (pos >= ctx || pos0 < 0) {  // uniform: a step past the context touches no cache row
         if (tid == 0 && h == 0) atomicOr(status, kStatusCtx);
         return;
     }
     const int qd = n_heads * HD, kvd = n_kv * HD, group = n_heads / n_kv, kvh = h / group;
+    if (single) {  // uniform: this token's rows of the projections and of the output
+        q += (size_t)y * qd;
+        k += (size_t)y * kvd;
+        v += (size_t)y * kvd;
+        oq += (size_t)y * qd;
+        od += (size_t)y * (qd / QK);
+        if (of) of += (size_t)y * qd;
+    }
     QH_PASTAMP(0);
     // V block b of this head: HD uint4 at vbase + b * kvd (in uint4 units, kvd / 8 per position... see vblock())
     const uint4* vc4 = reinterpret_cast<const uint4*>(vc);
@@ -927,7 +938,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     et.store(exptab);
     __syncthreads();
     QH_PASTAMP(1);
-    if (h % group == 0)
+    if (!single && h % group == 0)
         for (int i = tid; i < HD; i += 256) {
             kc[(kchunk(i >> 3, pos) << 3) + (i & 7)] = kloc[t * HD + i];
             vc[vchunk(pos / 8, i) * 8 + (pos & 7)] = vloc[t * HD + i];
@@ -1171,6 +1182,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
         const int col = h * HD + (tid & ~31);
         if (of) of[(size_t)t * qd + h * HD + tid] = acc;  // the f32 input of an unquantized o projection
         quant_block32(acc, oq + (size_t)t * qd + col, od + (size_t)t * (qd / QK) + col / QK);
+    }
+}
+
+// The f16 cache rows of n tokens at positions *pos_dev .. + n - 1 (a prefill stack) from their projections k / v
+// ([n][n_kv * HD]): bias, RoPE as a*c - b*s and b*c + a*s with the reference build's contraction
+// (fma(a, c, -(b*s)), fma(b, c, a*s)), rounded to f16, exactly what attention_kernel rebuilds and stores
+// (model.cpp:183-206, ops_ref.cpp:201-214), in the K chunk and V block layouts. One workgroup per token; positions
+// past the context store nothing (attention_kernel raises the status).
+template <int HD>
+__global__ __launch_bounds__(256) void kv_store_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                       const float* __restrict__ bk, const float* __restrict__ bv,
+                                                       const float* __restrict__ cs, const int* __restrict__ pos_dev,
+                                                       int ctx, int n_kv, uint16_t* __restrict__ kc,
+                                                       uint16_t* __restrict__ vc) {
+    constexpr int HALF = HD / 2, CPR = HD / 8;
+    const int t = blockIdx.x, tid = threadIdx.x, pos = *pos_dev + t;
+    if (pos >= ctx || pos < 0) return;
+    const int kvd = n_kv * HD;
+    const float* krow = k + (size_t)t * kvd;
+    const float* crow = cs + (size_t)pos * HD;
+    for (int e = tid; e < n_kv * HALF; e += 256) {
+        const int kvh = e / HALF, i = e % HALF;
+        float a = krow[kvh * HD + i], b = krow[kvh * HD + i + HALF];
+        if (bk) {
+            a = a + bk[kvh * HD + i];
+            b = b + bk[kvh * HD + i + HALF];
+        }
+        const float c = crow[2 * i], sn = crow[2 * i + 1];
+        const float lo = __builtin_fmaf(a, c, -(b * sn)), hi = __builtin_fmaf(b, c, a * sn);
+        const size_t base = (size_t)kvh * CPR * ctx;
+        kc[((base + (size_t)(i >> 3) * ctx + pos) << 3) + (i & 7)] = f2h(lo);
+        kc[((base + (size_t)((i + HALF) >> 3) * ctx + pos) << 3) + ((i + HALF) & 7)] = f2h(hi);
+    }
+    for (int e = tid; e < kvd; e += 256) {
+        const float x = v[(size_t)t * kvd + e];
+        vc[((size_t)(pos / 8) * kvd + e) * 8 + (pos & 7)] = f2h(bv ? x + bv[e] : x);
     }
 }
 
@@ -2480,17 +2527,45 @@ hipError_t attention_chunk(Decoder* d, int l, int n, int r0, const int* pos_dev,
     } else if (hp.head_dim == 64) {
         qh_launch((attention_kernel<64, 2>), grid, dim3(256), 0, s, q, k, v, bias(d, l, L_BQ), bias(d, l, L_BK),
                   bias(d, l, L_BV), d->cs, pos_dev, hp.ctx_len, hp.n_heads, hp.n_kv_heads, d->kc + l * layer_k,
-                  d->vc + l * layer_v, oq, od, d->status, of);
+                  d->vc + l * layer_v, oq, od, d->status, of, 0);
     } else {
         qh_launch((attention_kernel<128>), grid, dim3(256), 0, s, q, k, v, bias(d, l, L_BQ), bias(d, l, L_BK),
                   bias(d, l, L_BV), d->cs, pos_dev, hp.ctx_len, hp.n_heads, hp.n_kv_heads, d->kc + l * layer_k,
-                  d->vc + l * layer_v, oq, od, d->status, of);
+                  d->vc + l * layer_v, oq, od, d->status, of, 0);
+    }
+    return hipGetLastError();
+}
+
+// Attention of a prefill stack of n > kChunk tokens at positions *d->pos ..: the f16 cache rows of every token of the
+// stack first (kv_store_kernel), then one attention launch in which each token is its own chunk (every earlier row
+// read from the cache), so the stack's (head, token) workgroups fill the GPU together.
+hipError_t attention_stack(Decoder* d, int l, int n, hipStream_t s) {
+    const qh_model_desc& hp = d->hp;
+    const size_t layer_k = (size_t)hp.ctx_len * hp.n_kv_heads * hp.head_dim;
+    const size_t layer_v = (size_t)v_ctx(hp.ctx_len) * hp.n_kv_heads * hp.head_dim;
+    uint16_t *kc = d->kc + l * layer_k, *vc = d->vc + l * layer_v;
+    const dim3 grid(hp.n_heads, n);
+    if (hp.head_dim == 64) {
+        qh_launch((kv_store_kernel<64>), dim3(n), dim3(256), 0, s, d->k, d->v, bias(d, l, L_BK), bias(d, l, L_BV),
+                  d->cs, d->pos, hp.ctx_len, hp.n_kv_heads, kc, vc);
+        QH_TRY(hipGetLastError());
+        qh_launch((attention_kernel<64, 2>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
+                  bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads, kc, vc,
+                  d->qb, d->db, d->status, d->fb, 1);
+    } else {
+        qh_launch((kv_store_kernel<128>), dim3(n), dim3(256), 0, s, d->k, d->v, bias(d, l, L_BK), bias(d, l, L_BV),
+                  d->cs, d->pos, hp.ctx_len, hp.n_kv_heads, kc, vc);
+        QH_TRY(hipGetLastError());
+        qh_launch((attention_kernel<128>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
+                  bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads, kc, vc,
+                  d->qb, d->db, d->status, d->fb, 1);
     }
     return hipGetLastError();
 }
 
 hipError_t attention(Decoder* d, int l, int n, hipStream_t s) {
     const qh_model_desc& hp = d->hp;
+    if (n > kChunk && !d->kv32 && d->fuse) return attention_stack(d, l, n, s);
     if (n > kChunk) {  // a prefill stack: its 32-token sub-chunks in order (each reads the rows the ones before wrote)
         for (int i = 0; i * kChunk < n; ++i)
             QH_TRY(attention_chunk(d, l, min(kChunk, n - i * kChunk), i * kChunk, d->subpos + i, s));
@@ -2812,11 +2887,12 @@ hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, i
     int last = 0;
     for (int c0 = 0; c0 < n; c0 += d->stack) {
         const int m = n - c0 < d->stack ? n - c0 : d->stack;
-        if (m > kChunk)
+        if (m > kChunk) {
             qh_launch(set_subpos_kernel, dim3(1), dim3(kMaxStack / kChunk), 0, s, d->subpos, pos0 + c0,
                       (m + kChunk - 1) / kChunk);
-        else
-            qh_launch(set_int_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + c0);
+            QH_TRY(hipGetLastError());
+        }
+        qh_launch(set_int_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + c0);
         QH_TRY(hipGetLastError());
         QH_TRY(embed(d, tokens + c0, m, s));
         QH_TRY(prefill_layers(d, m, s));

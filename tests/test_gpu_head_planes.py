@@ -219,3 +219,31 @@ def test_decoder_planes_q4mix_stream_equals_reference(qh, oracle, gpu):
     assert (out == g["out"]).all()
     assert (np.array(digs) == g["state_digests"]).all()
     assert (bits(np.array(tops[:n_gen], np.float32)) == bits(g["top_logit"])).all()
+
+
+@pytest.mark.parametrize("flow", ["chat", "gen"])
+def test_decoder_planes_sampled_stream_equals_reference(qh, gpu, flow):
+    """The benchmark model's sampling flows with the nibble-plane head: top-k 20 queries with the token history as
+    must ids and the reference Sampler's draws (chat: temperature 0.7, top-p 0.8, penalty 1.1; gen: greedy with
+    penalty). The head rescores other rows than the Q4_0 copy's, but every row the sampler can keep (the top-k and
+    the must ids) is exact in both, so the stream equals the reference Session's (tests/golden/e2e_sampled.npz)."""
+    import os
+    from conftest import GOLDEN
+    from decoder_util import qnt_module
+    qnt = qnt_module()
+    g = np.load(os.path.join(GOLDEN, "e2e_sampled.npz"), allow_pickle=False)
+    hp = qnt.HParams()
+    dec = qh.Decoder(hp, qnt.synthetic_q4mix(int(g["seed"]), hp), ctx_len=4096, head_planes=True)
+    chat = qh.sampler_params()
+    q = chat if flow == "chat" else qh.sampler_params(top_k=20, repeat_penalty=1.1)
+    dec.set_query(q)
+    dec.set_sampler(chat if flow == "chat" else None, int(g["sampler_seed"]))
+    want = g[flow + "_out"]
+    n = len(want)
+    dec.prefill(g["prompt"], 0)
+    dec.begin(n)
+    for _ in range(1, n):
+        dec.step()
+    out = dec.outputs(n)
+    dec.close()
+    assert (out == want).all(), np.nonzero(out != want)[0][:5]
