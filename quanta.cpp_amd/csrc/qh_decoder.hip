@@ -1221,6 +1221,181 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const float* __restrict__
     }
 }
 
+// Attention of a prefill stack at head_dim 64 with kStackTok consecutive tokens of one query head per workgroup, once
+// kv_store_kernel has stored every row of the stack, so the workgroup rebuilds nothing and its tokens share the K and
+// V rows it reads: positions *pos_dev + y0 .. + kStackTok - 1 (y0 = kStackTok * blockIdx.y, tokens below n), all
+// below kStackCtx. The same arithmetic and order as attention_kernel for each token (model.cpp:115-137,
+// ops_ref.cpp:216-226): q with bias and RoPE in f32; one thread per cached row scores it for every token whose row
+// count reaches it (s = fma(q_i, k_i, s) in dimension order, then * 1/sqrt(64)); the maxima; glibc expf; then wave i
+// runs token i's softmax sum in position order, its normalisation and its weighted V chain over V rows staged in LDS
+// (lane d for dimension d, the weights as LDS broadcast reads), the four tokens' chains on four SIMDs at once; the
+// output quantized per 32-block.
+constexpr int kStackTok = 4;
+constexpr int kStackCtx = 1024;
+__global__ __launch_bounds__(256) void attention_stack_kernel(
+    const float* __restrict__ q, const float* __restrict__ bq, const float* __restrict__ cs,
+    const int* __restrict__ pos_dev, int n, int ctx, int n_heads, int n_kv, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, int8_t* __restrict__ oq, float* __restrict__ od, int* __restrict__ status,
+    float* __restrict__ of) {
+    constexpr int HD = 64, HALF = HD / 2, CPR = HD / 8, NTK = kStackTok;
+    constexpr int kVRows = 256, kVBlk = kVRows / 8;  // V rows per LDS stage (32 KB)
+    __shared__ __align__(16) float att[NTK][kStackCtx + kChainPad];
+    __shared__ __align__(16) uint4 vst[(kVBlk + 4) * HD];  // [block][dim] -> 8 rows; 4 blocks of read padding
+    __shared__ __align__(16) float qs[NTK][HD];
+    __shared__ float red[4][NTK];
+    __shared__ uint64_t exptab[32];
+    ExpTab et;
+    et.load();
+    const int h = blockIdx.x, y0 = (int)blockIdx.y * NTK, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nt = min(NTK, n - y0);  // tokens of this workgroup (uniform)
+    const int base = *pos_dev + y0;   // position of token 0
+    const int nmax = base + nt;       // rows of the last token
+    if (base < 0 || nmax > ctx || nmax > kStackCtx) {  // uniform; the host launches this only within both limits
+        if (tid == 0) atomicOr(status, kStatusCtx);
+        return;
+    }
+    const int qd = n_heads * HD, kvd = n_kv * HD, group = n_heads / n_kv, kvh = h / group;
+    auto kchunk = [&](int c, int p) { return ((size_t)kvh * CPR + c) * ctx + p; };
+    auto vchunk = [&](int blk, int d) { return (size_t)blk * kvd + kvh * HD + d; };
+    const uint4* vc4 = reinterpret_cast<const uint4*>(vc);
+    // q of token `wave` (lanes 0-31: one rotated pair each), with bias (model.cpp:183-195, ops_ref.cpp:201-214)
+    if (wave < nt && lane < HALF) {
+        const float* src = q + (size_t)(y0 + wave) * qd + h * HD;
+        const float* crow = cs + (size_t)(base + wave) * HD;
+        float a = src[lane], b = src[lane + HALF];
+        if (bq) {
+            a = a + bq[h * HD + lane];
+            b = b + bq[h * HD + lane + HALF];
+        }
+        const float c = crow[2 * lane], sn = crow[2 * lane + 1];
+        qs[wave][lane] = __builtin_fmaf(a, c, -(b * sn));
+        qs[wave][lane + HALF] = __builtin_fmaf(b, c, a * sn);
+    }
+    et.store(exptab);
+    __syncthreads();
+
+    // scores of every cached row j < nmax, thread per row; token i scores rows j <= base + i
+    const float scale = 1.0f / __builtin_sqrtf((float)HD);
+    float mx[NTK];
+#pragma unroll
+    for (int i = 0; i < NTK; ++i) mx[i] = -__builtin_inff();
+    for (int j = tid; j < nmax; j += 256) {
+        v4u kk[CPR];
+        const uint16_t* kg = kc + (kchunk(0, j) << 3);
+#pragma unroll
+        for (int c = 0; c < CPR; ++c) kk[c] = ld4(kg + (size_t)c * ctx * 8);
+#pragma unroll
+        for (int i = 0; i < NTK; ++i) {
+            if (i < nt && j <= base + i) {
+                const float4* q4 = reinterpret_cast<const float4*>(lane_ptr(qs[i]));
+                float sc = 0.0f;
+#pragma unroll
+                for (int c = 0; c < CPR; ++c) {
+                    const float4 qa = q4[2 * c], qb = q4[2 * c + 1];
+                    const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        sc = __builtin_fmaf(qq[2 * e], h2f((uint16_t)(kk[c][e] & 0xffffu)), sc);
+                        sc = __builtin_fmaf(qq[2 * e + 1], h2f((uint16_t)(kk[c][e] >> 16)), sc);
+                    }
+                }
+                const float a = sc * scale;
+                att[i][j] = a;
+                mx[i] = a > mx[i] ? a : mx[i];
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NTK; ++i) {  // the maximum does not depend on the order of comparison
+        const float m = wave_max_sel(mx[i]);
+        if (lane == 0) red[wave][i] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NTK; ++i) {
+        float m = red[0][i];
+        for (int w = 1; w < 4; ++w) m = red[w][i] > m ? red[w][i] : m;
+        mx[i] = m;
+    }
+    for (int j = tid; j < nmax; j += 256) {
+#pragma unroll
+        for (int i = 0; i < NTK; ++i)
+            if (i < nt && j <= base + i) att[i][j] = dev_expf(att[i][j] - mx[i], exptab);
+    }
+    __syncthreads();
+
+    // wave i: token i's softmax sum in position order (ops_ref.cpp:220-224) and its normalisation
+    const int tk = wave, nrows = base + tk + 1;
+    if (tk < nt) {
+        const float sum = lds_chain(att[tk], nrows, [](float acc, float a) { return acc + a; });
+        const float inv = 1.0f / sum;
+        for (int j = lane; j < nrows; j += 64) att[tk][j] = att[tk][j] * inv;
+    }
+    // out_i = sum_j a_j * v_ji, one FMA per position in order (model.cpp:131-135): wave i, lane d, over the rows of
+    // each V stage (whole cache blocks of 8 positions; rows past a token's count are never used)
+    float acc = 0.0f;
+    for (int s0 = 0; s0 < nmax; s0 += kVRows) {
+        const int sn = min(nmax, s0 + kVRows);
+        const int nb8 = (sn - s0 + 7) / 8;
+        __syncthreads();  // the previous stage is consumed (and, for the first, the normalised rows are written)
+        for (int c = tid; c < nb8 * HD; c += 256) vst[c] = vc4[vchunk(s0 / 8 + c / HD, c % HD)];
+        __syncthreads();
+        if (tk < nt && s0 < nrows) {
+            const int n_ = min(nrows, sn) - s0;
+            const float4* ap = reinterpret_cast<const float4*>(lane_ptr(att[tk] + s0));  // s0 % 32 == 0
+            auto ldv = [&](uint4(&vv)[4], float4(&w)[8], int jr) {  // rows s0 + jr .. + 31 (jr % 32 == 0)
+                const uint4* vp = vst + (jr >> 3) * HD + lane;
+#pragma unroll
+                for (int q4i = 0; q4i < 4; ++q4i) vv[q4i] = vp[q4i * HD];
+#pragma unroll
+                for (int qi = 0; qi < 8; ++qi) w[qi] = ap[jr / 4 + qi];
+            };
+            auto use = [&](const uint4(&vv)[4], const float4(&w)[8], int cnt) {
+#pragma unroll
+                for (int q4i = 0; q4i < 4; ++q4i) {
+                    const uint32_t vw[4] = {vv[q4i].x, vv[q4i].y, vv[q4i].z, vv[q4i].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int kx = 8 * q4i + e;
+                        const float4 wq = w[kx >> 2];
+                        const float wk = (kx & 3) == 0 ? wq.x : (kx & 3) == 1 ? wq.y : (kx & 3) == 2 ? wq.z : wq.w;
+                        if (kx < cnt)
+                            acc = __builtin_fmaf(wk, h2f((uint16_t)(e & 1 ? vw[e >> 1] >> 16 : vw[e >> 1] & 0xffffu)),
+                                                 acc);
+                    }
+                }
+            };
+            uint4 vA[4], vB[4];
+            float4 wA[8], wB[8];
+            ldv(vA, wA, 0);
+            int jr = 0;
+#pragma unroll 1
+            for (; jr + 64 <= n_; jr += 64) {
+                ldv(vB, wB, jr + 32);
+                __builtin_amdgcn_sched_barrier(0);
+                use(vA, wA, 32);
+                ldv(vA, wA, jr + 64);
+                __builtin_amdgcn_sched_barrier(0);
+                use(vB, wB, 32);
+            }
+            if (jr + 32 <= n_) {
+                ldv(vB, wB, jr + 32);
+                __builtin_amdgcn_sched_barrier(0);
+                use(vA, wA, 32);
+                use(vB, wB, n_ - jr - 32);
+            } else {
+                use(vA, wA, n_ - jr);
+            }
+        }
+    }
+    if (tk < nt) {  // quantize_q8 of the output, two 32-blocks per 64 dimensions
+        const size_t row = (size_t)(y0 + tk) * qd;
+        const int col = h * HD + (lane & ~31);
+        if (of) of[row + h * HD + lane] = acc;
+        quant_block32(acc, oq + row + col, od + row / QK + col / QK);
+    }
+}
+
 // Attention over an f32 KV cache (the reference's --kv-f32, model.cpp:96-104, 197-204: the cache keeps k / v as
 // computed, no f16 rounding), laid out as the reference keeps it, [ctx][n_kv * head_dim] per layer. One 256-thread
 // workgroup per (query head, token of the chunk), prefill and decode alike: the chunk's K / V rows 0..t are rebuilt
@@ -2212,6 +2387,7 @@ struct Decoder {
     // sub-chunks in order, the sub-chunk i starting at subpos[i].
     int stack = kChunk;
     int* subpos = nullptr;
+    int stack_end = 0;  // the current prefill stack's end position (host-side, for the attention plan)
     // token history (prompt ids since position 0, then each chosen id) and the optional query / sampler settings
     int32_t* hist = nullptr;  // [ctx_len + 1]
     int* hist_len = nullptr;
@@ -2549,6 +2725,12 @@ hipError_t attention_stack(Decoder* d, int l, int n, hipStream_t s) {
         qh_launch((kv_store_kernel<64>), dim3(n), dim3(256), 0, s, d->k, d->v, bias(d, l, L_BK), bias(d, l, L_BV),
                   d->cs, d->pos, hp.ctx_len, hp.n_kv_heads, kc, vc);
         QH_TRY(hipGetLastError());
+        if (d->stack_end <= kStackCtx) {  // the stack's last row within the four-token kernel's score rows
+            qh_launch(attention_stack_kernel, dim3(hp.n_heads, (n + kStackTok - 1) / kStackTok), dim3(256), 0, s,
+                      d->q, bias(d, l, L_BQ), d->cs, d->pos, n, hp.ctx_len, hp.n_heads, hp.n_kv_heads, kc, vc, d->qb,
+                      d->db, d->status, d->fb);
+            return hipGetLastError();
+        }
         qh_launch((attention_kernel<64, 2>), grid, dim3(256), 0, s, d->q, d->k, d->v, bias(d, l, L_BQ),
                   bias(d, l, L_BK), bias(d, l, L_BV), d->cs, d->pos, hp.ctx_len, hp.n_heads, hp.n_kv_heads, kc, vc,
                   d->qb, d->db, d->status, d->fb, 1);
@@ -2894,6 +3076,7 @@ hipError_t decoder_prefill(Decoder* d, const int32_t* tokens, int n, int pos0, i
         }
         qh_launch(set_int_kernel, dim3(1), dim3(1), 0, s, d->pos, pos0 + c0);
         QH_TRY(hipGetLastError());
+        d->stack_end = pos0 + c0 + m;
         QH_TRY(embed(d, tokens + c0, m, s));
         QH_TRY(prefill_layers(d, m, s));
         last = m - 1;
