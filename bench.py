@@ -701,8 +701,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end prefill + decode measurement")
+    ap.add_argument("--stacks", default="32,128,512", help="prefill stacks of --only prefill_stack")
     ap.add_argument("--only", choices=["e2e", "roofline", "prefill", "sampling", "head", "sampler", "stages",
-                                       "prefill_stack"],
+                                       "prefill_stack", "planes"],
                     help="one measurement alone (for counter runs): e2e = --e2e-only; roofline = a 256 MiB copy "
                          "(counter calibration) then the Q4_0 GEMV rotation; prefill = Q4_0 4864x896 and 896x4864 at M = 512, "
                          "then 9728x896 (the decoder's gate + up rows) and 896x4864 (down) at M = 32")
@@ -737,6 +738,8 @@ def main():
     if args.only == "head":
         print(json.dumps({"shortlist_head_151936x896": rnd(head_bench(qh, synth, torch, orc.oracle, 5, 1))}),
               flush=True)
+        return 0
+    if args.only == "planes":
         hp, tens = e2e_model()
         ep = e2e_bench(qh, torch, hp, tens, steps=args.steps, warmup=args.warmup, head_planes=True)
         print(json.dumps({"decode_nibble_planes": rnd(ep)}), flush=True)
@@ -751,7 +754,8 @@ def main():
         return 0
     if args.only == "prefill_stack":
         hp, tens = e2e_model()
-        print(json.dumps({"prefill_stack": prefill_stack_bench(qh, torch, hp, tens)}), flush=True)
+        stacks = tuple(int(x) for x in args.stacks.split(","))
+        print(json.dumps({"prefill_stack": prefill_stack_bench(qh, torch, hp, tens, stacks=stacks)}), flush=True)
         return 0
     if args.only == "stages":
         hp, tens = e2e_model()
