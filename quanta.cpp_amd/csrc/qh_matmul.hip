@@ -513,12 +513,15 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
     constexpr int kAupr = KC * kBw / 16, kXupr = KC * QK / 16;  // 16-byte units per row and chunk
     __shared__ __align__(16) uint8_t as[2][64 * kArow];
     __shared__ __align__(16) int8_t xs[2][TT * kXrow];
-    __shared__ __align__(16) float dws[2][KC][64];  // [block][row], f32
+    // Row scales as f16 bits in the order the waves read them: [block][row half wr][lane group lq][row tile rs][i]
+    // holds row 32 wr + 16 rs + 4 lq + i, so a lane's eight scales of a block are one 16-byte read
+    __shared__ __align__(16) uint16_t dws[2][KC][2][4][8];
     __shared__ __align__(16) float dxs[2][KC][TT];  // [block][token]
     const int nb = cols / QK;
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
     const int wr = wave >> 1, wt = wave & 1;
+    const int lqs = lq ^ ((li >> 3) & 1);  // the 8-byte half this lane reads in its row (rows 8-15 swapped)
 
     // XCD-aware numbering as in the other variants; segment tiles count 64-row tiles here
     const int G = (int)gridDim.x, p = (int)blockIdx.x;
@@ -568,14 +571,21 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
             if (dx_thread) S.dx[j] = dxsrc[b];
         }
     };
+    // Rows 8-15 of each 16 hold every 16-byte unit with its 8-byte halves swapped (an operand read's lane group lq
+    // takes half lq ^ 1 there), so the rows li and li + 8 of one read fall in different banks
+    auto swz = [](const uint4& v, int row) {
+        const bool h = (row >> 3) & 1;
+        return make_uint4(h ? v.z : v.x, h ? v.w : v.y, h ? v.x : v.z, h ? v.y : v.w);
+    };
     auto stage = [&](const R& S, int buf) {
 #pragma unroll
         for (int j = 0; j < R::kAu; ++j) {
             const int e = j * kMmThreads + tid;
             if (DT == kQ8) {
-                *reinterpret_cast<uint4*>(&as[buf][(e / kAupr) * kArow + (e % kAupr) * 16]) = S.a[j];
+                *reinterpret_cast<uint4*>(&as[buf][(e / kAupr) * kArow + (e % kAupr) * 16]) = swz(S.a[j], e / kAupr);
             } else {  // one block: element i < 16 in the low nibble of byte i, element 16 + i in its high nibble
-                const uint32_t w[4] = {S.a[j].x, S.a[j].y, S.a[j].z, S.a[j].w};
+                const uint4 v = swz(S.a[j], e / kAupr);  // both unpacked units come out with their halves swapped
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
                 uint32_t lo[4], hi[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -590,14 +600,12 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
 #pragma unroll
         for (int j = 0; j < R::kXu; ++j) {
             const int e = j * kMmThreads + tid;
-            *reinterpret_cast<uint4*>(&xs[buf][(e / kXupr) * kXrow + (e % kXupr) * 16]) = S.x[j];
+            *reinterpret_cast<uint4*>(&xs[buf][(e / kXupr) * kXrow + (e % kXupr) * 16]) = swz(S.x[j], e / kXupr);
         }
         const int t = tid / 4;
 #pragma unroll
         for (int j = 0; j < kSp; ++j) {
-            uint32_t h = S.dw[j];
-            asm volatile("" : "+v"(h));  // keeps the conversion here (hoisted, it would wait for the next loads)
-            dws[buf][sk + j][t] = f16_to_f32((uint16_t)h);
+            dws[buf][sk + j][t >> 5][(t >> 2) & 3][((t >> 4) & 1) * 4 + (t & 3)] = S.dw[j];
             if (dx_thread) dxs[buf][sk + j][t] = S.dx[j];
         }
     };
@@ -612,18 +620,18 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
     // One block's operands (two weight tiles, two token tiles) and its products.
     struct Ops {
         long a[2], x[NTS];
-        float4 dw[2];
+        uint4 dw;  // f16 scales of rows 16 rs + 4 lq + i (rs = 0, 1; i = 0..3) of the wave's 32
         float dx[NTS];
     };
     auto ld_ops = [&](Ops& o, int buf, int b) {
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs) {
-            o.a[rs] = *reinterpret_cast<const long*>(&as[buf][(wr * 32 + rs * 16 + li) * kArow + b * QK + lq * 8]);
-            o.dw[rs] = *reinterpret_cast<const float4*>(&dws[buf][b][wr * 32 + rs * 16 + 4 * lq]);
+            o.a[rs] = *reinterpret_cast<const long*>(&as[buf][(wr * 32 + rs * 16 + li) * kArow + b * QK + lqs * 8]);
         }
+        o.dw = *reinterpret_cast<const uint4*>(&dws[buf][b][wr][lq][0]);
 #pragma unroll
         for (int ts = 0; ts < NTS; ++ts) {
-            o.x[ts] = *reinterpret_cast<const long*>(&xs[buf][(wt * (TT / 2) + ts * 16 + li) * kXrow + b * QK + lq * 8]);
+            o.x[ts] = *reinterpret_cast<const long*>(&xs[buf][(wt * (TT / 2) + ts * 16 + li) * kXrow + b * QK + lqs * 8]);
             o.dx[ts] = dxs[buf][b][wt * (TT / 2) + ts * 16 + li];
         }
     };
@@ -634,16 +642,23 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
             for (int ts = 0; ts < NTS; ++ts)
                 c[rs][ts] = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[rs], o.x[ts], (v4i){0, 0, 0, 0}, 0, 0, 0);
     };
-    // acc = fma(float(s) * dw, dx, acc) (ops_ref.cpp:97-98) for one block
+    // acc = fma(float(s) * dw, dx, acc) (ops_ref.cpp:97-98) for one block. float(s) * dw is taken as
+    // fma(float(s), dw, 0) with the f16 scale as a mixed-precision operand (v_fma_mix_f32: the scale widens exactly,
+    // one rounding, as the product; a zero product comes out +0 where the product could be -0, which a chain from +0
+    // never shows, since +0 + -0 = +0)
     auto chain = [&](const Ops& o, const v4i(&c)[2][NTS]) {
+        const uint32_t dww[4] = {o.dw.x, o.dw.y, o.dw.z, o.dw.w};
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs) {
-            const float dwv[4] = {o.dw[rs].x, o.dw[rs].y, o.dw[rs].z, o.dw[rs].w};
 #pragma unroll
             for (int ts = 0; ts < NTS; ++ts)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[rs][ts][i] = __builtin_fmaf((float)c[rs][ts][i] * dwv[i], o.dx[ts], acc[rs][ts][i]);
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t w = dww[2 * rs + (i >> 1)];
+                    const float dw = (float)__builtin_bit_cast(_Float16, (uint16_t)(i & 1 ? w >> 16 : w & 0xffffu));
+                    const float pr = __builtin_fmaf((float)c[rs][ts][i], dw, 0.0f);
+                    acc[rs][ts][i] = __builtin_fmaf(pr, o.dx[ts], acc[rs][ts][i]);
+                }
         }
     };
     // Blocks 0 .. nblk - 1 of buffer buf in order, software-pipelined: block b + 1's operands are read and its

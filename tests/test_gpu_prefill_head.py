@@ -50,6 +50,51 @@ def test_matmul_rows_equal_gemv(qh, oracle, synth, gpu, dtype, N, K, M):
     assert torch.equal(got.view(torch.int32), per_tok.view(torch.int32))
 
 
+def _bits_or_nan_equal(got, want):
+    nan = np.isnan(want)
+    assert (np.isnan(got) == nan).all(), f"{int((np.isnan(got) != nan).sum())} NaN positions differ"
+    bad = np.nonzero(bits(got[~nan]) != bits(want[~nan]))[0]
+    assert bad.size == 0, f"{bad.size} outputs differ, first flat indices {bad[:8]}"
+
+
+@pytest.mark.parametrize("tt", ["tile", "tile32"])
+@pytest.mark.parametrize("dtype", [2, 3])
+def test_matmul_tile_every_f16_scale(qh, oracle, synth, gpu, monkeypatch, tt, dtype):
+    """The tile kernel's block products float(s) * d over every binary16 pattern as a row's scale (subnormals, -0,
+    the largest finite values, inf and NaN), 128 tokens: NaN where the oracle has NaN, every other output bit-equal."""
+    monkeypatch.setenv("QH_MM", tt)
+    N, K, M = 65536, 64, 128
+    buf = synth.q8_tensor(5, N, K) if dtype == 2 else synth.q4_tensor(7, N, K, group=32)
+    synth.scales_of(buf, dtype, N, K).view(np.uint16)[:] = np.repeat(np.arange(65536, dtype=np.uint32)
+                                                                     .astype(np.uint16), K // 32)
+    W = qh.DeviceTensor.upload(buf, dtype, N, K)
+    xq, xd = qh.quantize_q8(_dev(synth.activations(3, M, K), gpu))
+    got = qh.matmul_q(W, xq, xd).cpu().numpy()
+    want = oracle.matmul_q(dtype, N, K, buf, xq.cpu().numpy(), xd.cpu().numpy(), threads=8)
+    _bits_or_nan_equal(got, want)
+
+
+@pytest.mark.parametrize("tt", ["tile", "tile:8", "tile32", "tile32:8"])
+@pytest.mark.parametrize("dtype", [2, 3])
+def test_matmul_tile_nonfinite_scales_by_chunk(qh, oracle, synth, gpu, monkeypatch, tt, dtype):
+    """Inf and NaN row scales planted in some K chunks of some row tiles, with extreme finite scales (the largest f16,
+    subnormals, negative, -0) elsewhere, at every tile variant and chunk size: every output equals the oracle's."""
+    monkeypatch.setenv("QH_MM", tt)
+    N, K = 200, 4864
+    buf = synth.q8_tensor(41, N, K) if dtype == 2 else synth.q4_tensor(43, N, K, group=32)
+    sc = synth.scales_of(buf, dtype, N, K).view(np.uint16).reshape(N, K // 32)
+    for r, b, h in [(5, 9, 0x7C00), (70, 20, 0xFC00), (130, 3, 0x7E00), (131, 150, 0x7C00), (199, 151, 0xFE01),
+                    (6, 10, 0x7BFF), (7, 0, 0x0001), (8, 33, 0x8000), (9, 34, 0xFBFF), (64, 70, 0x83FF),
+                    (65, 71, 0x0400)]:
+        sc[r, b] = h
+    W = qh.DeviceTensor.upload(buf, dtype, N, K)
+    for M in (130, 512):
+        xq, xd = qh.quantize_q8(_dev(synth.activations(47 + M, M, K), gpu))
+        got = qh.matmul_q(W, xq, xd).cpu().numpy()
+        want = oracle.matmul_q(dtype, N, K, buf, xq.cpu().numpy(), xd.cpu().numpy(), threads=8)
+        _bits_or_nan_equal(got, want)
+
+
 def test_matmul_row_range_and_ldo(qh, oracle, synth, gpu):
     import torch
     N, K, M = 200, 896, 19
