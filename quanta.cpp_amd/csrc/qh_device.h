@@ -23,6 +23,18 @@ constexpr int kQ8P = 16;  // the device-only nibble-plane layout of a Q8_0 head 
 // IEEE binary16 bits -> binary32 (exact for every input, subnormals included): v_cvt_f32_f16.
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
+// A block product float(s) * d in one FMA. An integer sum that starts from kSumBias (the bits of B = 1.5 * 2^23) ends
+// at the bits of the float B + s, exactly, for |s| < 2^22 (a block's |s| <= 32 * 128 * 128 = 2^19); then
+// fma(B + s, d, -(B * d)) is the exact value s * d rounded once, the same f32 as float(s) * d, because B * d needs at
+// most 13 significant bits for an f16 scale d, so -(B * d) is exact (checked on the CPU for every finite f16 d and
+// |s| <= 2^19, apart from the sign of a zero product, which a chain acc = fma(p, dx, acc) from +0 never shows). Not
+// for d = inf or NaN (the terms cancel into NaN, or the NaN's sign flips): callers take (B + s - B) * d there, which
+// is float(s) * d again.
+constexpr int kSumBias = 0x4B400000;
+constexpr float kSumBiasF = 12582912.0f;
+// True for the f16 bits of inf and NaN (the scales the one-FMA product cannot take).
+__device__ __forceinline__ bool f16_nonfinite(uint32_t h) { return (h & 0x7C00u) == 0x7C00u; }
+
 // The f16 bits at p (2-byte aligned) through a 4-byte load of the aligned word holding them: 16-bit global loads cost
 // gfx950 far more than 32-bit ones (measured: eight per lane add about 1.8 us to a scattered row fetch against 0.2 us
 // as words). The word starts inside the array, so it stays inside the allocation's granule even where it reaches

@@ -461,18 +461,20 @@ __global__ __launch_bounds__(NS == 0 ? kMmThreads : 2 * kMmThreads) void matmul_
     if (tok < n && r < r1) sg.out[(size_t)tok * sg.ldo + r] = acc;
 }
 
-// Tile variant for batches of 128 tokens and more: a workgroup of 4 waves owns 64 rows x TT tokens (TT = 32 or 64)
-// over all of K, in chunks of KC blocks brought into LDS by coalesced 16-byte loads (a row's chunk is KC x 16 (Q4_0) or
-// KC x 32 (Q8_0) contiguous bytes, a token's KC x 32; Q4_0 codes are unpacked to int8 as they are staged, so both
-// formats share the LDS layout and the compute loop), double-buffered with two register sets: the loads of chunk
-// c + 3 are issued as chunk c + 1 is staged. Wave (wr, wt) multiplies rows 32 wr .. + 31 by TT / 2 tokens: per block
-// two MFMAs per 16-token tile (2 row tiles), each weight operand read once for every token tile and each activation
-// operand once for two row tiles, and the wave runs the chains of its lanes' outputs in registers (lane l: rows
-// 4 (l / 16) + i of each row tile, token l % 16 of each token tile), so no block sum goes through LDS. A whole chunk
-// runs straight-line two blocks deep (block b's chains, block b + 1's MFMAs, block b + 2's operand reads). Operand
-// loads in MFMA layout (8 bytes per lane from 16 rows) kept the texture-address units busy for most of the register
-// kernel's time at 512 tokens; here they are busy about a third of the time, and the exact f32 chains (a convert, a
-// scale multiply and an FMA per output and block) and the per-chunk staging and barrier are what is left.
+// Tile variant for batches of 128 tokens and more: a workgroup of NW = 4 or 8 waves owns 64 rows x TT tokens
+// (TT = 16, 32 or 64) over all of K, in chunks of KC blocks brought into LDS by coalesced 16-byte loads (a row's chunk
+// is KC x 16 (Q4_0) or KC x 32 (Q8_0) contiguous bytes, a token's KC x 32; Q4_0 codes are unpacked to int8 as they
+// are staged, so both formats share the LDS layout and the compute loop), double-buffered with two register sets:
+// the loads of chunk c + 3 are issued as chunk c + 1 is staged. Wave (wr, wt) multiplies 16 NRS rows by 16 NTS tokens
+// (four waves at TT >= 32: 32 rows x TT / 2 tokens; at TT = 16: 16 rows x 16 tokens; eight waves: 16 rows x TT / 2
+// tokens, two waves per SIMD): per block one MFMA per (16-row, 16-token) tile, each weight operand read once for
+// every token tile and each activation operand once for every row tile, and the wave runs the chains of its lanes'
+// outputs in registers (lane l: rows 4 (l / 16) + i of each row tile, token l % 16 of each token tile), so no block
+// sum goes through LDS. A whole chunk runs straight-line two blocks deep (block b's chains, block b + 1's MFMAs,
+// block b + 2's operand reads). Operand loads in MFMA layout (8 bytes per lane from 16 rows) kept the texture-address
+// units busy for most of the register kernel's time at 512 tokens; here they are busy about a third of the time, and
+// the exact f32 chains (a convert, a scale multiply and an FMA per output and block; two FMAs with eight waves) and
+// the per-chunk staging and barrier are what is left.
 // Timeline stamps of workgroup 0, wave 0 (compiled in only with -DQH_TIMELINE; qh_timeline_mm_read copies them out).
 #if defined(QH_TIMELINE)
 __device__ uint64_t qh_tl_mm[64];
@@ -485,42 +487,57 @@ __device__ uint64_t qh_tl_mm[64];
     do {              \
     } while (0)
 #endif
-template <int DT, int KC, int TT>
+template <int DT, int KC, int TT, int NT>
 struct TileRegs {
-    static constexpr int kBw = DT == kQ8 ? QK : QK / 2;           // weight bytes per block
-    static constexpr int kAu = 64 * KC * kBw / 16 / kMmThreads;  // 16-byte weight units per thread
-    static constexpr int kXu = TT * KC * QK / 16 / kMmThreads;   // 16-byte activation units per thread
-    static constexpr int kSp = KC / 4;                           // scales per thread and chunk
+    static constexpr int kBw = DT == kQ8 ? QK : QK / 2;   // weight bytes per block
+    static constexpr int kAu = 64 * KC * kBw / 16 / NT;  // 16-byte weight units per thread
+    static constexpr int kXu = TT * KC * QK / 16 / NT;   // 16-byte activation units per thread
+    static constexpr int kTpr = NT / 64;                 // threads per row (and per token) of the scales
+    static constexpr int kSp = KC / kTpr;                // scales per thread and chunk
     uint4 a[kAu];
     uint4 x[kXu];
-    uint16_t dw[kSp];  // row tid / 4, blocks kSp (tid % 4) + j of the chunk
-    float dx[kSp];     // token tid / 4, blocks kSp (tid % 4) + j of the chunk
+    uint16_t dw[kSp];  // row tid / kTpr, blocks kSp (tid % kTpr) + j of the chunk
+    float dx[kSp];     // token tid / kTpr, blocks kSp (tid % kTpr) + j of the chunk
 };
 
-// TT: tokens per workgroup, 64 (waves of 32 rows x 32 tokens) or 32 (waves of 32 rows x 16 tokens: twice the
-// workgroups for matrices with few row tiles).
-template <int DT, int KC, int TT>
-__global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, const int8_t* __restrict__ xq,
-                                                                const float* __restrict__ xd, int cols, int n,
-                                                                int n_tg) {
-    static_assert(TT == 64 || TT == 32, "token tile");
-    constexpr int NTS = TT / 32;  // 16-token tiles per wave
-    using R = TileRegs<DT, KC, TT>;
-    constexpr int kBw = R::kBw, kSp = R::kSp;
+// TT: tokens per workgroup, 64 (waves of 32 rows x 32 tokens), 32 (waves of 32 rows x 16 tokens: twice the
+// workgroups for matrices with few row tiles) or 16 (four waves of 16 rows x 16 tokens: four times, for long rows,
+// KC = 8).
+template <int DT, int KC, int TT, int NW>
+__global__ __launch_bounds__(64 * NW) void matmul_tile_kernel(MmSegs segs, const int8_t* __restrict__ xq,
+                                                             const float* __restrict__ xd, int cols, int n, int n_tg) {
+    constexpr int NT = 64 * NW;  // threads
+    static_assert(TT == 64 || TT == 32 || TT == 16, "token tile");
+    static_assert(NW == 4 || (NW == 8 && TT >= 32), "waves");
+    // With eight waves (two per SIMD) the chains' VALU issue is what bounds the kernel: the integer sums start from
+    // kSumBias and each block product is one FMA with a staged -(B * dw) (two-step products in a chunk with an inf or
+    // NaN row scale)
+    constexpr bool BIAS = NW == 8;
+    static_assert(64 * KC * (DT == kQ8 ? QK : QK / 2) / 16 % NT == 0 && TT * KC * QK / 16 % NT == 0 &&
+                      KC % (NT / 64) == 0,
+                  "whole units and scales per thread");
+    constexpr int WT = TT == 16 ? 1 : 2;  // waves across the tokens
+    constexpr int WR = NW / WT;           // waves across the 64 rows
+    constexpr int NRS = 4 / WR;           // 16-row tiles per wave
+    constexpr int NTS = TT / (16 * WT);   // 16-token tiles per wave
+    using R = TileRegs<DT, KC, TT, NT>;
+    constexpr int kBw = R::kBw, kSp = R::kSp, kTpr = R::kTpr;
     // Weights are staged as int8 codes whatever the format (Q4_0 nibbles are unpacked once, as they are staged, not by
     // both token waves at every block): LDS row strides in bytes
     constexpr int kArow = KC * QK + 16, kXrow = KC * QK + 16;
     constexpr int kAupr = KC * kBw / 16, kXupr = KC * QK / 16;  // 16-byte units per row and chunk
     __shared__ __align__(16) uint8_t as[2][64 * kArow];
     __shared__ __align__(16) int8_t xs[2][TT * kXrow];
-    // Row scales as f16 bits in the order the waves read them: [block][row half wr][lane group lq][row tile rs][i]
-    // holds row 32 wr + 16 rs + 4 lq + i, so a lane's eight scales of a block are one 16-byte read
-    __shared__ __align__(16) uint16_t dws[2][KC][2][4][8];
+    // Row scales as f16 bits in the order the waves read them: [block][row wave wr][lane group lq][row tile rs][i]
+    // holds row 16 NRS wr + 16 rs + 4 lq + i, so a lane's scales of a block are one 16-byte (8-byte) read
+    __shared__ __align__(16) uint16_t dws[2][KC][WR][4][4 * NRS];
+    __shared__ __align__(16) float cws[BIAS ? 2 : 1][BIAS ? KC : 1][WR][4][4 * NRS];  // -(kSumBiasF * dw), same order
     __shared__ __align__(16) float dxs[2][KC][TT];  // [block][token]
+    __shared__ int first_nonfinite;  // lowest chunk with an inf or NaN row scale (INT_MAX if none)
     const int nb = cols / QK;
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
-    const int wr = wave >> 1, wt = wave & 1;
+    const int wr = wave / WT, wt = wave % WT;
     const int lqs = lq ^ ((li >> 3) & 1);  // the 8-byte half this lane reads in its row (rows 8-15 swapped)
 
     // XCD-aware numbering as in the other variants; segment tiles count 64-row tiles here
@@ -533,7 +550,7 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
     const int r1 = sg.r1;
     const int rbase = sg.r0 + rt * 64, tbase = tg * TT;
     const size_t wrow_bytes = (size_t)nb * kBw;
-    const bool dx_thread = TT == 64 || tid < 4 * TT;  // threads of a token's scales (wave-uniform)
+    const bool dx_thread = tid < kTpr * TT;  // threads of a token's scales (wave-uniform)
 
     // Source rows of this thread's staged units; rows and tokens past the end are clamped (loaded, never stored), and
     // byte offsets past the end of a row onto its last unit (blocks no chain adds).
@@ -541,7 +558,7 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
     int aoff[R::kAu];
 #pragma unroll
     for (int j = 0; j < R::kAu; ++j) {
-        const int e = j * kMmThreads + tid;
+        const int e = j * NT + tid;
         asrc[j] = sg.wq + (size_t)min(rbase + e / kAupr, r1 - 1) * wrow_bytes;
         aoff[j] = (e % kAupr) * 16;
     }
@@ -549,13 +566,13 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
     int xoff[R::kXu];
 #pragma unroll
     for (int j = 0; j < R::kXu; ++j) {
-        const int e = j * kMmThreads + tid;
+        const int e = j * NT + tid;
         xsrc[j] = xq + (size_t)min(tbase + e / kXupr, n - 1) * cols;
         xoff[j] = (e % kXupr) * 16;
     }
-    const uint16_t* dwsrc = sg.ws + (size_t)min(rbase + tid / 4, r1 - 1) * nb;
-    const float* dxsrc = xd + (size_t)min(tbase + tid / 4, n - 1) * nb;
-    const int sk = kSp * (tid % 4);
+    const uint16_t* dwsrc = sg.ws + (size_t)min(rbase + tid / kTpr, r1 - 1) * nb;
+    const float* dxsrc = xd + (size_t)min(tbase + tid / kTpr, n - 1) * nb;
+    const int sk = kSp * (tid % kTpr);
 
     auto load = [&](R& S, int c0) {
 #pragma unroll
@@ -577,10 +594,10 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
         const bool h = (row >> 3) & 1;
         return make_uint4(h ? v.z : v.x, h ? v.w : v.y, h ? v.x : v.z, h ? v.y : v.w);
     };
-    auto stage = [&](const R& S, int buf) {
+    auto stage = [&](const R& S, int buf, int c) {
 #pragma unroll
         for (int j = 0; j < R::kAu; ++j) {
-            const int e = j * kMmThreads + tid;
+            const int e = j * NT + tid;
             if (DT == kQ8) {
                 *reinterpret_cast<uint4*>(&as[buf][(e / kAupr) * kArow + (e % kAupr) * 16]) = swz(S.a[j], e / kAupr);
             } else {  // one block: element i < 16 in the low nibble of byte i, element 16 + i in its high nibble
@@ -599,94 +616,127 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
         }
 #pragma unroll
         for (int j = 0; j < R::kXu; ++j) {
-            const int e = j * kMmThreads + tid;
+            const int e = j * NT + tid;
             *reinterpret_cast<uint4*>(&xs[buf][(e / kXupr) * kXrow + (e % kXupr) * 16]) = swz(S.x[j], e / kXupr);
         }
-        const int t = tid / 4;
+        const int t = tid / kTpr;
+        bool nonfinite = false;
 #pragma unroll
         for (int j = 0; j < kSp; ++j) {
-            dws[buf][sk + j][t >> 5][(t >> 2) & 3][((t >> 4) & 1) * 4 + (t & 3)] = S.dw[j];
+            dws[buf][sk + j][t / (16 * NRS)][(t >> 2) & 3][((t >> 4) % NRS) * 4 + (t & 3)] = S.dw[j];
+            if constexpr (BIAS) {
+                cws[buf][sk + j][t / (16 * NRS)][(t >> 2) & 3][((t >> 4) % NRS) * 4 + (t & 3)] =
+                    -(kSumBiasF * f16_to_f32(S.dw[j]));
+                nonfinite = nonfinite || f16_nonfinite(S.dw[j]);
+            }
             if (dx_thread) dxs[buf][sk + j][t] = S.dx[j];
         }
+        if (BIAS && nonfinite) atomicMin(&first_nonfinite, c);  // rare: that chunk takes the two-step products
     };
 
-    float acc[2][NTS][4];
+    float acc[NRS][NTS][4];
 #pragma unroll
-    for (int rs = 0; rs < 2; ++rs)
+    for (int rs = 0; rs < NRS; ++rs)
 #pragma unroll
         for (int ts = 0; ts < NTS; ++ts)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[rs][ts][i] = 0.0f;
-    // One block's operands (two weight tiles, two token tiles) and its products.
+    // One block's operands (NRS weight tiles, NTS token tiles) and its products.
     struct Ops {
-        long a[2], x[NTS];
-        uint4 dw;  // f16 scales of rows 16 rs + 4 lq + i (rs = 0, 1; i = 0..3) of the wave's 32
+        long a[NRS], x[NTS];
+        uint32_t dw[2 * NRS];  // f16 scales of rows 16 rs + 4 lq + i (i = 0..3) of the wave's rows
         float dx[NTS];
+        float cw[BIAS ? 4 * NRS : 1];
     };
     auto ld_ops = [&](Ops& o, int buf, int b) {
 #pragma unroll
-        for (int rs = 0; rs < 2; ++rs) {
-            o.a[rs] = *reinterpret_cast<const long*>(&as[buf][(wr * 32 + rs * 16 + li) * kArow + b * QK + lqs * 8]);
+        for (int rs = 0; rs < NRS; ++rs) {
+            o.a[rs] = *reinterpret_cast<const long*>(
+                &as[buf][(wr * 16 * NRS + rs * 16 + li) * kArow + b * QK + lqs * 8]);
         }
-        o.dw = *reinterpret_cast<const uint4*>(&dws[buf][b][wr][lq][0]);
+        if constexpr (NRS == 2) {
+            const uint4 w = *reinterpret_cast<const uint4*>(&dws[buf][b][wr][lq][0]);
+            o.dw[0] = w.x, o.dw[1] = w.y, o.dw[2] = w.z, o.dw[3] = w.w;
+        } else {
+            const uint2 w = *reinterpret_cast<const uint2*>(&dws[buf][b][wr][lq][0]);
+            o.dw[0] = w.x, o.dw[1] = w.y;
+        }
+        if constexpr (BIAS) {
+#pragma unroll
+            for (int rs = 0; rs < NRS; ++rs) {
+                const float4 w = *reinterpret_cast<const float4*>(&cws[buf][b][wr][lq][4 * rs]);
+                o.cw[4 * rs] = w.x, o.cw[4 * rs + 1] = w.y, o.cw[4 * rs + 2] = w.z, o.cw[4 * rs + 3] = w.w;
+            }
+        }
 #pragma unroll
         for (int ts = 0; ts < NTS; ++ts) {
-            o.x[ts] = *reinterpret_cast<const long*>(&xs[buf][(wt * (TT / 2) + ts * 16 + li) * kXrow + b * QK + lqs * 8]);
-            o.dx[ts] = dxs[buf][b][wt * (TT / 2) + ts * 16 + li];
+            o.x[ts] = *reinterpret_cast<const long*>(
+                &xs[buf][(wt * (TT / WT) + ts * 16 + li) * kXrow + b * QK + lqs * 8]);
+            o.dx[ts] = dxs[buf][b][wt * (TT / WT) + ts * 16 + li];
         }
     };
-    auto mma = [&](const Ops& o, v4i(&c)[2][NTS]) {
+    auto mma = [&](const Ops& o, v4i(&c)[NRS][NTS]) {
 #pragma unroll
-        for (int rs = 0; rs < 2; ++rs)
+        for (int rs = 0; rs < NRS; ++rs)
 #pragma unroll
             for (int ts = 0; ts < NTS; ++ts)
-                c[rs][ts] = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[rs], o.x[ts], (v4i){0, 0, 0, 0}, 0, 0, 0);
+                c[rs][ts] = BIAS ? __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[rs], o.x[ts],
+                                                                         (v4i){kSumBias, kSumBias, kSumBias, kSumBias},
+                                                                         0, 0, 0)
+                                 : __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[rs], o.x[ts], (v4i){0, 0, 0, 0}, 0, 0, 0);
     };
     // acc = fma(float(s) * dw, dx, acc) (ops_ref.cpp:97-98) for one block. float(s) * dw is taken as
     // fma(float(s), dw, 0) with the f16 scale as a mixed-precision operand (v_fma_mix_f32: the scale widens exactly,
     // one rounding, as the product; a zero product comes out +0 where the product could be -0, which a chain from +0
-    // never shows, since +0 + -0 = +0)
-    auto chain = [&](const Ops& o, const v4i(&c)[2][NTS]) {
-        const uint32_t dww[4] = {o.dw.x, o.dw.y, o.dw.z, o.dw.w};
+    // never shows, since +0 + -0 = +0). With BIAS the sums are B + s: fma(B + s, dw, -(B * dw)) (FAST), else
+    // fma(B + s - B, dw, 0).
+    auto chain = [&](auto fast, const Ops& o, const v4i(&c)[NRS][NTS]) {
+        const uint32_t* dww = o.dw;
 #pragma unroll
-        for (int rs = 0; rs < 2; ++rs) {
+        for (int rs = 0; rs < NRS; ++rs) {
 #pragma unroll
             for (int ts = 0; ts < NTS; ++ts)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const uint32_t w = dww[2 * rs + (i >> 1)];
                     const float dw = (float)__builtin_bit_cast(_Float16, (uint16_t)(i & 1 ? w >> 16 : w & 0xffffu));
-                    const float pr = __builtin_fmaf((float)c[rs][ts][i], dw, 0.0f);
+                    float pr;
+                    if constexpr (!BIAS)
+                        pr = __builtin_fmaf((float)c[rs][ts][i], dw, 0.0f);
+                    else if constexpr (decltype(fast)::value)
+                        pr = __builtin_fmaf(__int_as_float(c[rs][ts][i]), dw, o.cw[4 * rs + i]);
+                    else
+                        pr = __builtin_fmaf(__int_as_float(c[rs][ts][i]) - kSumBiasF, dw, 0.0f);
                     acc[rs][ts][i] = __builtin_fmaf(pr, o.dx[ts], acc[rs][ts][i]);
                 }
         }
     };
     // Blocks 0 .. nblk - 1 of buffer buf in order, software-pipelined: block b + 1's operands are read and its
     // products issued while block b's chains run.
-    auto compute = [&](int buf, int nblk) {
+    auto compute = [&](auto fast, int buf, int nblk) {
         Ops o0, o1;
-        v4i c0[2][NTS], c1[2][NTS];
+        v4i c0[NRS][NTS], c1[NRS][NTS];
         ld_ops(o0, buf, 0);
         mma(o0, c0);
         int b = 0;
         for (; b + 2 <= nblk; b += 2) {
             ld_ops(o1, buf, b + 1);
             __builtin_amdgcn_sched_barrier(0);
-            chain(o0, c0);
+            chain(fast, o0, c0);
             mma(o1, c1);
             if (b + 2 < nblk) ld_ops(o0, buf, b + 2);
             __builtin_amdgcn_sched_barrier(0);
-            chain(o1, c1);
+            chain(fast, o1, c1);
             if (b + 2 < nblk) mma(o0, c0);
         }
-        if (b < nblk) chain(o0, c0);
+        if (b < nblk) chain(fast, o0, c0);
     };
     // A whole chunk (KC blocks), straight-line and two blocks deep: while block b's chains run, block b + 1's MFMAs
     // are in flight and block b + 2's operands are being read, so neither the LDS latency nor the MFMA latency waits
     // in front of a chain.
-    auto compute_full = [&](int buf) {
+    auto compute_full = [&](auto fast, int buf) {
         Ops o[3];
-        v4i c[2][2][NTS];
+        v4i c[2][NRS][NTS];
         ld_ops(o[0], buf, 0);
         if (KC > 1) ld_ops(o[1], buf, 1);
         mma(o[0], c[0]);
@@ -696,7 +746,7 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
             if (b + 2 < KC) ld_ops(o[(b + 2) % 3], buf, b + 2);
             if (b + 1 < KC) mma(o[(b + 1) % 3], c[(b + 1) & 1]);
             __builtin_amdgcn_sched_barrier(0);
-            chain(o[b % 3], c[b & 1]);
+            chain(fast, o[b % 3], c[b & 1]);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -709,19 +759,31 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
     R S0, S1;
     load(S0, 0);
     if (n_chunks > 1) load(S1, KC);
-    stage(S0, 0);
+    if constexpr (BIAS) {
+        if (tid == 0) first_nonfinite = 0x7fffffff;
+        __syncthreads();  // the loads above are in flight
+    }
+    stage(S0, 0, 0);
     if (n_chunks > 2) load(S0, 2 * KC);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     QH_MMSTAMP(1);
     auto step = [&](int c, R& Sn) {  // Sn holds chunk c + 1
-        if ((c + 1) * KC <= nb)
-            compute_full(c & 1);
-        else
-            compute(c & 1, nb - c * KC);
+        // Chunk c's scales were staged before the last barrier; a later chunk's flag only lowers the bound to c + 1
+        const bool fast = !BIAS || __builtin_amdgcn_readfirstlane(first_nonfinite) > c;
+        if ((c + 1) * KC <= nb) {
+            if (fast)
+                compute_full(std::true_type{}, c & 1);
+            else
+                compute_full(std::false_type{}, c & 1);
+        } else if (fast) {
+            compute(std::true_type{}, c & 1, nb - c * KC);
+        } else {
+            compute(std::false_type{}, c & 1, nb - c * KC);
+        }
         QH_MMSTAMP(2 + 3 * c);
         if (c + 1 < n_chunks) {
-            stage(Sn, (c + 1) & 1);
+            stage(Sn, (c + 1) & 1, c + 1);
             QH_MMSTAMP(3 + 3 * c);
             if (c + 3 < n_chunks) load(Sn, (c + 3) * KC);
             __builtin_amdgcn_sched_barrier(0);
@@ -736,13 +798,13 @@ __global__ __launch_bounds__(kMmThreads) void matmul_tile_kernel(MmSegs segs, co
 
 #pragma unroll
     for (int ts = 0; ts < NTS; ++ts) {
-        const int tok = tbase + wt * (TT / 2) + ts * 16 + li;
+        const int tok = tbase + wt * (TT / WT) + ts * 16 + li;
         if (tok < n) {
 #pragma unroll
-            for (int rs = 0; rs < 2; ++rs)
+            for (int rs = 0; rs < NRS; ++rs)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int r = rbase + wr * 32 + rs * 16 + 4 * lq + i;
+                    const int r = rbase + wr * 16 * NRS + rs * 16 + 4 * lq + i;
                     if (r < r1) sg.out[(size_t)tok * sg.ldo + r] = acc[rs][ts][i];
                 }
         }
@@ -927,7 +989,7 @@ struct MmPlan {
     int ns = 0;          // its register sets in flight past two chunks (2, 3 or 4; 0: default)
     bool tile = false;   // the 64-row tile kernel
     int kc = 4;          // its blocks per chunk (4 or 8)
-    int ttile = 64;      // its tokens per workgroup (64 or 32)
+    int ttile = 64;      // its tokens per workgroup (64, 32 or 16)
 };
 
 MmPlan matmul_plan(int rows, int cols, int n) {
@@ -941,21 +1003,29 @@ MmPlan matmul_plan(int rows, int cols, int n) {
         if (sscanf(env, "tile:%d", &a) == 1 && (a == 4 || a == 8)) return MmPlan{false, 1, 4, false, 0, true, a};
         if (strcmp(env, "tile32") == 0) return MmPlan{false, 1, 4, false, 0, true, 4, 32};
         if (sscanf(env, "tile32:%d", &a) == 1 && (a == 4 || a == 8)) return MmPlan{false, 1, 4, false, 0, true, a, 32};
+        if (strcmp(env, "tile16") == 0) return MmPlan{false, 1, 4, false, 0, true, 8, 16};
+        if (strcmp(env, "tile32w8") == 0) return MmPlan{false, 1, 8, false, 0, true, 8, 32};
+        if (strcmp(env, "tile32w8:16") == 0) return MmPlan{false, 1, 8, false, 0, true, 16, 32};
         if (sscanf(env, "stage:%d", &a) == 1 && a >= 2 && a <= 4) return MmPlan{false, 1, 4, true, a};
         if (sscanf(env, "reg:%d:%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && (b == 1 || b == 2 || b == 4))
             return MmPlan{true, a, b};
     }
     (void)pl;
-    // From sweeps on MI355X (cold weights) at the Qwen2.5-0.5B shapes, M = 32 / 64 / 128 / 512: the tile kernel with
-    // 32-token workgroups wins from 128 tokens once there are about 192 tiles or more, with 4-block chunks on rows of
-    // up to 64 blocks and 8-block chunks past that (Q4_0 4864x896 at M = 512: 21.4 us, against 21.2-24.2 for 64-token
+    // From sweeps on MI355X (cold weights) at the Qwen2.5-0.5B shapes, M = 32 / 64 / 128 / 256 / 512: the tile kernel
+    // with 32-token workgroups wins from 128 tokens once there are about 192 tiles or more, with 4-block chunks on rows
+    // of up to 64 blocks (Q4_0 4864x896 at M = 512: 20.2 us, against 24.4 with 8-block chunks, 21.2-24.2 for 64-token
     // workgroups, 45.0 staged and 54.2 register-chain; M = 128: 10.8 against 14.4 staged; Q8_0 896x896 at M = 512:
-    // 8.7 against 11.9 and 13.3; Q4_0 896x4864 at M = 512: 25.6 against 31.0 with 4-block chunks, 26.4 with 16, 40.5
+    // 8.4 against 11.9 and 13.3) and eight waves with 16-block chunks on longer rows (Q4_0 896x4864 at M = 512: 22.4,
+    // against 23.0 with 8-block chunks, 24.4 with four waves, 25.4 with 16-token workgroups). Long rows with too few
+    // 32-token tiles take 16-token workgroups when they make about 192 (896x4864 at M = 256: 19.4 against 24.7
     // staged). Everywhere else (32 and 64 tokens, few row tiles) the LDS-staged kernel wins, also over the
     // register-chain kernel; it measured 4-12% under the LDS and register kernels at 32 tokens (q/k/v, o, gate/up,
     // down).
-    const long tiles32 = (long)((rows + 63) / 64) * ((n + 31) / 32);
-    if (n >= 128 && tiles32 >= 192) return MmPlan{false, 1, 4, false, 0, true, cols >= 2048 ? 8 : 4, 32};
+    const long row_tiles = (rows + 63) / 64;
+    const long tiles32 = row_tiles * ((n + 31) / 32), tiles16 = row_tiles * ((n + 15) / 16);
+    if (n >= 128 && tiles32 >= 192)
+        return cols >= 2048 ? MmPlan{false, 1, 8, false, 0, true, 16, 32} : MmPlan{false, 1, 4, false, 0, true, 4, 32};
+    if (n >= 128 && cols >= 2048 && tiles16 >= 192) return MmPlan{false, 1, 4, false, 0, true, 8, 16};
     return MmPlan{false, 1, 4, true};
 }
 
@@ -1008,11 +1078,13 @@ hipError_t launch_matmul_segs(const MmOut* m, int n_mats, const int8_t* xq, cons
         }
         const int n_tg = (n + pl.ttile - 1) / pl.ttile;
         const dim3 grid((unsigned)(row_tiles64 * n_tg));
-#define QH_MM_TILE(DT, KC, TT)                                                                                     \
-    if (W.dtype == DT && pl.kc == KC && pl.ttile == TT)                                                                  \
-        qh_launch((matmul_tile_kernel<DT, KC, TT>), grid, dim3(kMmThreads), 0, s, sg64, xq, xd, W.cols, n, n_tg);
-        QH_MM_TILE(kQ8, 4, 64) QH_MM_TILE(kQ8, 8, 64) QH_MM_TILE(kQ4, 4, 64) QH_MM_TILE(kQ4, 8, 64)
-        QH_MM_TILE(kQ8, 4, 32) QH_MM_TILE(kQ8, 8, 32) QH_MM_TILE(kQ4, 4, 32) QH_MM_TILE(kQ4, 8, 32)
+#define QH_MM_TILE(DT, KC, TT, NW)                                                                       \
+    if (W.dtype == DT && pl.kc == KC && pl.ttile == TT && pl.nw == NW)                                          \
+        qh_launch((matmul_tile_kernel<DT, KC, TT, NW>), grid, dim3(64 * NW), 0, s, sg64, xq, xd, W.cols, n, n_tg);
+        QH_MM_TILE(kQ8, 4, 64, 4) QH_MM_TILE(kQ8, 8, 64, 4) QH_MM_TILE(kQ4, 4, 64, 4) QH_MM_TILE(kQ4, 8, 64, 4)
+        QH_MM_TILE(kQ8, 4, 32, 4) QH_MM_TILE(kQ8, 8, 32, 4) QH_MM_TILE(kQ4, 4, 32, 4) QH_MM_TILE(kQ4, 8, 32, 4)
+        QH_MM_TILE(kQ8, 8, 16, 4) QH_MM_TILE(kQ4, 8, 16, 4) QH_MM_TILE(kQ8, 8, 32, 8) QH_MM_TILE(kQ4, 8, 32, 8)
+        QH_MM_TILE(kQ8, 16, 32, 8) QH_MM_TILE(kQ4, 16, 32, 8)
 #undef QH_MM_TILE
         return hipGetLastError();
     }

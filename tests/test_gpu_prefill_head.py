@@ -57,7 +57,7 @@ def _bits_or_nan_equal(got, want):
     assert bad.size == 0, f"{bad.size} outputs differ, first flat indices {bad[:8]}"
 
 
-@pytest.mark.parametrize("tt", ["tile", "tile32"])
+@pytest.mark.parametrize("tt", ["tile", "tile32", "tile16", "tile32w8", "tile32w8:16"])
 @pytest.mark.parametrize("dtype", [2, 3])
 def test_matmul_tile_every_f16_scale(qh, oracle, synth, gpu, monkeypatch, tt, dtype):
     """The tile kernel's block products float(s) * d over every binary16 pattern as a row's scale (subnormals, -0,
@@ -74,7 +74,7 @@ def test_matmul_tile_every_f16_scale(qh, oracle, synth, gpu, monkeypatch, tt, dt
     _bits_or_nan_equal(got, want)
 
 
-@pytest.mark.parametrize("tt", ["tile", "tile:8", "tile32", "tile32:8"])
+@pytest.mark.parametrize("tt", ["tile", "tile:8", "tile32", "tile32:8", "tile16", "tile32w8", "tile32w8:16"])
 @pytest.mark.parametrize("dtype", [2, 3])
 def test_matmul_tile_nonfinite_scales_by_chunk(qh, oracle, synth, gpu, monkeypatch, tt, dtype):
     """Inf and NaN row scales planted in some K chunks of some row tiles, with extreme finite scales (the largest f16,
@@ -342,7 +342,7 @@ def test_matmul_staged_chunk_counts(qh, oracle, synth, gpu, monkeypatch, tt, dty
         assert (bits(got) == bits(want)).all(), (tt, M)
 
 
-@pytest.mark.parametrize("tt", ["stage", "tile", "tile:8", "tile32", "tile32:8", "lds:1", "lds:2", "lds:4", "reg:1:1",
+@pytest.mark.parametrize("tt", ["stage", "tile", "tile:8", "tile32", "tile32:8", "tile16", "tile32w8", "tile32w8:16", "lds:1", "lds:2", "lds:4", "reg:1:1",
                                 "reg:1:4", "reg:2:2", "reg:4:1", "reg:4:4"])
 @pytest.mark.parametrize("dtype,N,K", [(2, 200, 896), (3, 200, 896), (2, 40, 4864), (3, 40, 4864)])
 def test_matmul_every_token_tiling(qh, oracle, synth, gpu, monkeypatch, tt, dtype, N, K):
