@@ -258,6 +258,15 @@ struct StageRegs {
     float dx;     // token tid / 16, block tid % 16
 };
 
+// LDS operand rows of the tile kernel: rows 8-15 of each 16 hold every 16-byte unit with its 8-byte halves swapped
+// (an operand read's lane takes half h ^ 1 there), so the rows li and li + 8 of one 8-byte operand read fall in
+// different banks (measured: bank-conflict cycles 27-31% -> 9-10% of the LDS's active cycles; the same layout made the
+// 32-token staged kernel slower, 9.9 -> 11.4 us on 896x4864, so it keeps plain rows).
+__device__ __forceinline__ uint4 swz16(const uint4& v, int row) {
+    const bool h = (row >> 3) & 1;
+    return make_uint4(h ? v.z : v.x, h ? v.w : v.y, h ? v.x : v.z, h ? v.y : v.w);
+}
+
 template <int DT, int NS>
 __global__ __launch_bounds__(NS == 0 ? kMmThreads : 2 * kMmThreads) void matmul_stage_kernel(MmSegs segs, const int8_t* __restrict__ xq,
                                                               const float* __restrict__ xd, int cols, int n,
@@ -538,7 +547,7 @@ __global__ __launch_bounds__(64 * NW) void matmul_tile_kernel(MmSegs segs, const
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
     const int wr = wave / WT, wt = wave % WT;
-    const int lqs = lq ^ ((li >> 3) & 1);  // the 8-byte half this lane reads in its row (rows 8-15 swapped)
+    const int lqs = lq ^ ((li >> 3) & 1);  // the 8-byte half this lane reads in its row (rows 8-15 swapped, swz16)
 
     // XCD-aware numbering as in the other variants; segment tiles count 64-row tiles here
     const int G = (int)gridDim.x, p = (int)blockIdx.x;
@@ -588,20 +597,14 @@ __global__ __launch_bounds__(64 * NW) void matmul_tile_kernel(MmSegs segs, const
             if (dx_thread) S.dx[j] = dxsrc[b];
         }
     };
-    // Rows 8-15 of each 16 hold every 16-byte unit with its 8-byte halves swapped (an operand read's lane group lq
-    // takes half lq ^ 1 there), so the rows li and li + 8 of one read fall in different banks
-    auto swz = [](const uint4& v, int row) {
-        const bool h = (row >> 3) & 1;
-        return make_uint4(h ? v.z : v.x, h ? v.w : v.y, h ? v.x : v.z, h ? v.y : v.w);
-    };
     auto stage = [&](const R& S, int buf, int c) {
 #pragma unroll
         for (int j = 0; j < R::kAu; ++j) {
             const int e = j * NT + tid;
             if (DT == kQ8) {
-                *reinterpret_cast<uint4*>(&as[buf][(e / kAupr) * kArow + (e % kAupr) * 16]) = swz(S.a[j], e / kAupr);
+                *reinterpret_cast<uint4*>(&as[buf][(e / kAupr) * kArow + (e % kAupr) * 16]) = swz16(S.a[j], e / kAupr);
             } else {  // one block: element i < 16 in the low nibble of byte i, element 16 + i in its high nibble
-                const uint4 v = swz(S.a[j], e / kAupr);  // both unpacked units come out with their halves swapped
+                const uint4 v = swz16(S.a[j], e / kAupr);  // both unpacked units come out with their halves swapped
                 const uint32_t w[4] = {v.x, v.y, v.z, v.w};
                 uint32_t lo[4], hi[4];
 #pragma unroll
@@ -617,7 +620,7 @@ __global__ __launch_bounds__(64 * NW) void matmul_tile_kernel(MmSegs segs, const
 #pragma unroll
         for (int j = 0; j < R::kXu; ++j) {
             const int e = j * NT + tid;
-            *reinterpret_cast<uint4*>(&xs[buf][(e / kXupr) * kXrow + (e % kXupr) * 16]) = swz(S.x[j], e / kXupr);
+            *reinterpret_cast<uint4*>(&xs[buf][(e / kXupr) * kXrow + (e % kXupr) * 16]) = swz16(S.x[j], e / kXupr);
         }
         const int t = tid / kTpr;
         bool nonfinite = false;
