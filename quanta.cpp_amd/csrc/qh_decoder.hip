@@ -1225,24 +1225,27 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const float* __restrict__
 // kv_store_kernel has stored every row of the stack, so the workgroup rebuilds nothing and its tokens share the K and
 // V rows it reads: positions *pos_dev + y0 .. + kStackTok - 1 (y0 = kStackTok * blockIdx.y, tokens below n), all
 // below kStackCtx. The same arithmetic and order as attention_kernel for each token (model.cpp:115-137,
-// ops_ref.cpp:216-226): q with bias and RoPE in f32; one thread per cached row scores it for every token whose row
-// count reaches it (s = fma(q_i, k_i, s) in dimension order, then * 1/sqrt(64)); the maxima; glibc expf; then wave i
-// runs token i's softmax sum in position order, its normalisation and its weighted V chain over V rows staged in LDS
-// (lane d for dimension d, the weights as LDS broadcast reads), the four tokens' chains on four SIMDs at once; the
-// output quantized per 32-block.
+// ops_ref.cpp:216-226): q with bias and RoPE in f32; wave i takes token i: its q as 64 scalar operands, lane l
+// scores cached rows l, l + 64, ... up to the token's row count (s = fma(q_i, k_i, s) in dimension order, the f16 key
+// as a mixed-precision operand, then * 1/sqrt(64)), the next row's key loaded while a row is scored; the maximum over
+// the wave; glibc expf; the softmax sum in position order, its normalisation, and the weighted V chain over V rows
+// staged in LDS (lane d for dimension d, the weights as LDS broadcast reads), the four tokens' chains on four SIMDs
+// at once. The V stages' loads are issued a stage ahead (the first at the start), so their latency hides under the
+// scores and the previous stage's chains. The output is quantized per 32-block. Its LDS holds two workgroups per CU,
+// so the register budget is that of two waves per SIMD.
 constexpr int kStackTok = 4;
 constexpr int kStackCtx = 1024;
-__global__ __launch_bounds__(256) void attention_stack_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_stack_kernel(
     const float* __restrict__ q, const float* __restrict__ bq, const float* __restrict__ cs,
     const int* __restrict__ pos_dev, int n, int ctx, int n_heads, int n_kv, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int8_t* __restrict__ oq, float* __restrict__ od, int* __restrict__ status,
     float* __restrict__ of) {
     constexpr int HD = 64, HALF = HD / 2, CPR = HD / 8, NTK = kStackTok;
     constexpr int kVRows = 256, kVBlk = kVRows / 8;  // V rows per LDS stage (32 KB)
+    constexpr int kVPer = kVBlk * HD / 256;          // 16-byte V units per thread and stage
     __shared__ __align__(16) float att[NTK][kStackCtx + kChainPad];
     __shared__ __align__(16) uint4 vst[(kVBlk + 4) * HD];  // [block][dim] -> 8 rows; 4 blocks of read padding
     __shared__ __align__(16) float qs[NTK][HD];
-    __shared__ float red[4][NTK];
     __shared__ uint64_t exptab[32];
     ExpTab et;
     et.load();
@@ -1258,6 +1261,21 @@ __global__ __launch_bounds__(256) void attention_stack_kernel(
     auto kchunk = [&](int c, int p) { return ((size_t)kvh * CPR + c) * ctx + p; };
     auto vchunk = [&](int blk, int d) { return (size_t)blk * kvd + kvh * HD + d; };
     const uint4* vc4 = reinterpret_cast<const uint4*>(vc);
+    // V units of the stage at s0 (whole cache blocks of 8 positions below nmax) into registers, then into vst
+    v4u vreg[kVPer];
+    auto vload = [&](int s0) {  // units past the stage's blocks: re-reads, never stored
+        const int nb8 = (min(nmax, s0 + kVRows) - s0 + 7) / 8;
+#pragma unroll
+        for (int k = 0; k < kVPer; ++k) {
+            const int c = min(tid + 256 * k, nb8 * HD - 1);
+            vreg[k] = ld4(vc4 + vchunk(s0 / 8 + c / HD, c % HD));
+        }
+    };
+    auto vput = [&]() {  // the whole stage area (rows past the stage: never read)
+#pragma unroll
+        for (int k = 0; k < kVPer; ++k) *reinterpret_cast<v4u*>(&vst[tid + 256 * k]) = vreg[k];
+    };
+    vload(0);
     // q of token `wave` (lanes 0-31: one rotated pair each), with bias (model.cpp:183-195, ops_ref.cpp:201-214)
     if (wave < nt && lane < HALF) {
         const float* src = q + (size_t)(y0 + wave) * qd + h * HD;
@@ -1274,59 +1292,50 @@ __global__ __launch_bounds__(256) void attention_stack_kernel(
     et.store(exptab);
     __syncthreads();
 
-    // scores of every cached row j < nmax, thread per row; token i scores rows j <= base + i
-    const float scale = 1.0f / __builtin_sqrtf((float)HD);
-    float mx[NTK];
-#pragma unroll
-    for (int i = 0; i < NTK; ++i) mx[i] = -__builtin_inff();
-    for (int j = tid; j < nmax; j += 256) {
-        v4u kk[CPR];
-        const uint16_t* kg = kc + (kchunk(0, j) << 3);
-#pragma unroll
-        for (int c = 0; c < CPR; ++c) kk[c] = ld4(kg + (size_t)c * ctx * 8);
-#pragma unroll
-        for (int i = 0; i < NTK; ++i) {
-            if (i < nt && j <= base + i) {
-                const float4* q4 = reinterpret_cast<const float4*>(lane_ptr(qs[i]));
-                float sc = 0.0f;
-#pragma unroll
-                for (int c = 0; c < CPR; ++c) {
-                    const float4 qa = q4[2 * c], qb = q4[2 * c + 1];
-                    const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        sc = __builtin_fmaf(qq[2 * e], h2f((uint16_t)(kk[c][e] & 0xffffu)), sc);
-                        sc = __builtin_fmaf(qq[2 * e + 1], h2f((uint16_t)(kk[c][e] >> 16)), sc);
-                    }
-                }
-                const float a = sc * scale;
-                att[i][j] = a;
-                mx[i] = a > mx[i] ? a : mx[i];
-            }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < NTK; ++i) {  // the maximum does not depend on the order of comparison
-        const float m = wave_max_sel(mx[i]);
-        if (lane == 0) red[wave][i] = m;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < NTK; ++i) {
-        float m = red[0][i];
-        for (int w = 1; w < 4; ++w) m = red[w][i] > m ? red[w][i] : m;
-        mx[i] = m;
-    }
-    for (int j = tid; j < nmax; j += 256) {
-#pragma unroll
-        for (int i = 0; i < NTK; ++i)
-            if (i < nt && j <= base + i) att[i][j] = dev_expf(att[i][j] - mx[i], exptab);
-    }
-    __syncthreads();
-
-    // wave i: token i's softmax sum in position order (ops_ref.cpp:220-224) and its normalisation
+    // wave tk: token tk's scores, maximum, exponentials, softmax sum in position order (ops_ref.cpp:220-224) and
+    // normalisation, all within the wave (its rows of att are its own)
     const int tk = wave, nrows = base + tk + 1;
     if (tk < nt) {
+        const float scale = 1.0f / __builtin_sqrtf((float)HD);
+        const float qv = qs[tk][lane];
+        float qsg[HD];  // q_i, wave-uniform
+#pragma unroll
+        for (int d = 0; d < HD; ++d) qsg[d] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, qv), d));
+        float mx = -__builtin_inff();
+        v4u kA[CPR], kB[CPR];
+        auto kload = [&](v4u(&kk)[CPR], int j) {  // row j's key, clamped to the token's last row
+            const uint16_t* kg = kc + (kchunk(0, min(j, nrows - 1)) << 3);
+#pragma unroll
+            for (int c = 0; c < CPR; ++c) kk[c] = ld4(kg + (size_t)c * ctx * 8);
+        };
+        auto score = [&](const v4u(&kk)[CPR], int j) {
+            float sc = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CPR; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    sc = __builtin_fmaf(qsg[8 * c + 2 * e], h2f((uint16_t)(kk[c][e] & 0xffffu)), sc);
+                    sc = __builtin_fmaf(qsg[8 * c + 2 * e + 1], h2f((uint16_t)(kk[c][e] >> 16)), sc);
+                }
+            if (j < nrows) {
+                const float a = sc * scale;
+                att[tk][j] = a;
+                mx = a > mx ? a : mx;
+            }
+        };
+        kload(kA, lane);
+        int j0 = 0;
+        for (; j0 + 64 < nrows; j0 += 128) {
+            kload(kB, j0 + 64 + lane);
+            score(kA, j0 + lane);
+            kload(kA, j0 + 128 + lane);
+            score(kB, j0 + 64 + lane);
+        }
+        if (j0 < nrows) score(kA, j0 + lane);
+        mx = wave_max_sel(mx);  // the maximum does not depend on the order of comparison
+        __builtin_amdgcn_wave_barrier();
+        for (int j = lane; j < nrows; j += 64) att[tk][j] = dev_expf(att[tk][j] - mx, exptab);
+        __builtin_amdgcn_wave_barrier();
         const float sum = lds_chain(att[tk], nrows, [](float acc, float a) { return acc + a; });
         const float inv = 1.0f / sum;
         for (int j = lane; j < nrows; j += 64) att[tk][j] = att[tk][j] * inv;
@@ -1336,9 +1345,9 @@ __global__ __launch_bounds__(256) void attention_stack_kernel(
     float acc = 0.0f;
     for (int s0 = 0; s0 < nmax; s0 += kVRows) {
         const int sn = min(nmax, s0 + kVRows);
-        const int nb8 = (sn - s0 + 7) / 8;
         __syncthreads();  // the previous stage is consumed (and, for the first, the normalised rows are written)
-        for (int c = tid; c < nb8 * HD; c += 256) vst[c] = vc4[vchunk(s0 / 8 + c / HD, c % HD)];
+        vput();
+        if (s0 + kVRows < nmax) vload(s0 + kVRows);  // the next stage's loads run under this stage's chains
         __syncthreads();
         if (tk < nt && s0 < nrows) {
             const int n_ = min(nrows, sn) - s0;
