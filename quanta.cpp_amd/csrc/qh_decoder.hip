@@ -57,17 +57,6 @@ inline int escr_stride(int ctx) { return ((ctx + 15) & ~15) + 64; }
 
 enum { kStatusCtx = 1, kStatusToken = 2 };
 
-// glibc-identical expf on the device (all 2^32 inputs checked against the host's expf in tests).
-__device__ __forceinline__ float dev_expf(float x) { return expf_variant<2>(x); }
-// The same with its table in LDS (ExpTab): a table read from global memory costs a cache round trip per call.
-struct ExpTab {
-    uint64_t v;  // thread t < 32: entry t, loaded first thing
-    __device__ __forceinline__ void load() { v = expf_detail::kTab[min((int)threadIdx.x, 31)]; }
-    __device__ __forceinline__ void store(uint64_t* lds) const {
-        if (threadIdx.x < 32) lds[threadIdx.x] = v;
-    }
-};
-__device__ __forceinline__ float dev_expf(float x, const uint64_t* lds_tab) { return expf_variant<2>(x, lds_tab); }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return f16_to_f32(h); }
 
@@ -118,18 +107,6 @@ __device__ __forceinline__ float wave_max_sel(float a) {
     u = __builtin_bit_cast(uint32_t, a);
     const auto s32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
     return step(__builtin_bit_cast(float, (uint32_t)s32[0]), __builtin_bit_cast(float, (uint32_t)s32[1]));
-}
-
-// quantize_q8 of one 32-block (ops_ref.cpp:69-83) held one value per lane by an aligned group of 32 lanes: amax
-// (the maximum does not depend on the order of comparison), d = amax / 127, inv = d > 0 ? 1 / d : 0, and
-// q = lround(v * inv).
-__device__ __forceinline__ void quant_block32(float v, int8_t* __restrict__ q, float* __restrict__ d) {
-    const float a = max32_lanes(__builtin_fabsf(v));
-    const float sc = a / 127.0f;
-    const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
-    const int i = (int)threadIdx.x & 31;
-    q[i] = (int8_t)(int)round_half_away(v * inv);
-    if (i == 0) *d = sc;
 }
 
 // The same for a block held four consecutive values per lane by an aligned group of 8 lanes (lane j of the group
@@ -2882,7 +2859,13 @@ hipError_t prefill_layers(Decoder* d, int n, hipStream_t s) {
         });
         QH_TRY(hipGetLastError());
         const qh_tensor &wg = lt(d, l, L_WG), &wu = lt(d, l, L_WU), &wd = lt(d, l, L_WD);
-        if (!swiglu_fused(d, wg, wu, n, s)) {
+        // a prefill stack: gate / up with the SwiGLU epilogue in one tile launch where the plan allows it
+        const hipError_t sw = n > kChunk && d->fuse && !d->hadamard && !d->dense
+                                  ? launch_matmul_swiglu(wg, wu, d->qa, d->da, n, d->qb, d->db, s)
+                                  : hipErrorNotSupported;
+        if (sw != hipErrorNotSupported) {
+            QH_TRY(sw);
+        } else if (!swiglu_fused(d, wg, wu, n, s)) {
             const MmOut gu[2] = {{&wg, d->g, wg.rows, 0, wg.rows}, {&wu, d->u, wu.rows, 0, wu.rows}};
             if (dense_w(wg) || dense_w(wu)) {
                 for (const MmOut& m : gu) QH_TRY(linear(d, m.out, m.ldo, *m.W, false, n, s));

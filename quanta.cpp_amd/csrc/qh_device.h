@@ -11,6 +11,8 @@
 #include <type_traits>
 #include <utility>
 
+#include "qh_math.h"
+
 namespace qh {
 
 constexpr int QK = 32;
@@ -302,6 +304,30 @@ __device__ __forceinline__ float chain_lds_pipe(const float* p, const float* dx,
         }
     }
     return acc;
+}
+
+// glibc-identical expf on the device (all 2^32 inputs checked against the host's expf in tests).
+__device__ __forceinline__ float dev_expf(float x) { return expf_variant<2>(x); }
+// The same with its table in LDS (ExpTab): a table read from global memory costs a cache round trip per call.
+struct ExpTab {
+    uint64_t v;  // thread t < 32: entry t, loaded first thing
+    __device__ __forceinline__ void load() { v = expf_detail::kTab[min((int)threadIdx.x, 31)]; }
+    __device__ __forceinline__ void store(uint64_t* lds) const {
+        if (threadIdx.x < 32) lds[threadIdx.x] = v;
+    }
+};
+__device__ __forceinline__ float dev_expf(float x, const uint64_t* lds_tab) { return expf_variant<2>(x, lds_tab); }
+
+// quantize_q8 of one 32-block (ops_ref.cpp:69-83) held one value per lane by an aligned group of 32 lanes: amax
+// (the maximum does not depend on the order of comparison), d = amax / 127, inv = d > 0 ? 1 / d : 0, and
+// q = lround(v * inv).
+__device__ __forceinline__ void quant_block32(float v, int8_t* __restrict__ q, float* __restrict__ d) {
+    const float a = max32_lanes(__builtin_fabsf(v));
+    const float sc = a / 127.0f;
+    const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
+    const int i = (int)threadIdx.x & 31;
+    q[i] = (int8_t)(int)round_half_away(v * inv);
+    if (i == 0) *d = sc;
 }
 
 }  // namespace qh

@@ -84,6 +84,11 @@ struct MmOut {
 };
 // Up to three matrices of one dtype and width over the same activation in one launch (prefill q / k / v, gate / up).
 hipError_t launch_matmul_segs(const MmOut* m, int n_mats, const int8_t* xq, const float* xd, int n, hipStream_t s);
+// Gate / up of n >= 128 tokens (a prefill stack) with h = g / (1 + expf(-g)) * u quantized per 32 rows into hq / hd
+// ([n][rows], [n][rows / 32]) in one tile launch; hipErrorNotSupported (nothing launched) where the tile plan or the
+// shapes do not allow it.
+hipError_t launch_matmul_swiglu(const qh_tensor& wg, const qh_tensor& wu, const int8_t* xq, const float* xd, int n,
+                                int8_t* hq, float* hd, hipStream_t s);
 size_t argmax_workspace_bytes(int n);
 hipError_t launch_argmax(const float* logits, int n, int32_t* index, void* ws, hipStream_t s);
 

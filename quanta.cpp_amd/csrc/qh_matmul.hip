@@ -512,12 +512,19 @@ struct TileRegs {
 // TT: tokens per workgroup, 64 (waves of 32 rows x 32 tokens), 32 (waves of 32 rows x 16 tokens: twice the
 // workgroups for matrices with few row tiles) or 16 (four waves of 16 rows x 16 tokens: four times, for long rows,
 // KC = 8).
-template <int DT, int KC, int TT, int NW>
+// SW: the prefill stack's gate / up launch with SwiGLU and the down projection's input quantization in the epilogue
+// (model.cpp:212-218; ops_ref.cpp:243-248, 69-83): workgroup row tile rt stages gate rows [32 rt, 32 rt + 32) of segment
+// 0 as its rows 0-31 and the same up rows of segment 1 as rows 32-63, so the row-0 waves hold g and the row-1 waves u
+// of the same (row, token) outputs; h = g / (1 + expf(-g)) * u of each token's 32 rows is one 32-block of hq / hd
+// (rows = segs.r1[0] values per token).
+template <int DT, int KC, int TT, int NW, bool SW>
 __global__ __launch_bounds__(64 * NW) void matmul_tile_kernel(MmSegs segs, const int8_t* __restrict__ xq,
-                                                             const float* __restrict__ xd, int cols, int n, int n_tg) {
+                                                             const float* __restrict__ xd, int cols, int n, int n_tg,
+                                                             int8_t* __restrict__ hq, float* __restrict__ hd) {
     constexpr int NT = 64 * NW;  // threads
     static_assert(TT == 64 || TT == 32 || TT == 16, "token tile");
     static_assert(NW == 4 || (NW == 8 && TT >= 32), "waves");
+    static_assert(!SW || (NW == 4 && TT == 32), "SwiGLU epilogue: four waves, 32 tokens");
     // With eight waves (two per SIMD) the chains' VALU issue is what bounds the kernel: the integer sums start from
     // kSumBias and each block product is one FMA with a staged -(B * dw) (two-step products in a chunk with an inf or
     // NaN row scale)
@@ -547,6 +554,8 @@ __global__ __launch_bounds__(64 * NW) void matmul_tile_kernel(MmSegs segs, const
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
     const int wr = wave / WT, wt = wave % WT;
+    ExpTab et;  // SW: the expf table, loaded first thing
+    if constexpr (SW) et.load();
     const int lqs = lq ^ ((li >> 3) & 1);  // the 8-byte half this lane reads in its row (rows 8-15 swapped, swz16)
 
     // XCD-aware numbering as in the other variants; segment tiles count 64-row tiles here
@@ -563,12 +572,17 @@ __global__ __launch_bounds__(64 * NW) void matmul_tile_kernel(MmSegs segs, const
 
     // Source rows of this thread's staged units; rows and tokens past the end are clamped (loaded, never stored), and
     // byte offsets past the end of a row onto its last unit (blocks no chain adds).
+    // SW: staged row t is row 32 rt + (t & 31) of segment t / 32 (gate, up)
+    auto wrow = [&](int t) {
+        return SW ? (t < 32 ? segs.wq[0] : segs.wq[1]) + (size_t)(32 * rt + (t & 31)) * wrow_bytes
+                  : sg.wq + (size_t)min(rbase + t, r1 - 1) * wrow_bytes;
+    };
     const uint8_t* asrc[R::kAu];
     int aoff[R::kAu];
 #pragma unroll
     for (int j = 0; j < R::kAu; ++j) {
         const int e = j * NT + tid;
-        asrc[j] = sg.wq + (size_t)min(rbase + e / kAupr, r1 - 1) * wrow_bytes;
+        asrc[j] = wrow(e / kAupr);
         aoff[j] = (e % kAupr) * 16;
     }
     const int8_t* xsrc[R::kXu];
@@ -579,7 +593,8 @@ __global__ __launch_bounds__(64 * NW) void matmul_tile_kernel(MmSegs segs, const
         xsrc[j] = xq + (size_t)min(tbase + e / kXupr, n - 1) * cols;
         xoff[j] = (e % kXupr) * 16;
     }
-    const uint16_t* dwsrc = sg.ws + (size_t)min(rbase + tid / kTpr, r1 - 1) * nb;
+    const uint16_t* dwsrc = SW ? (tid / kTpr < 32 ? segs.ws[0] : segs.ws[1]) + (size_t)(32 * rt + (tid / kTpr & 31)) * nb
+                               : sg.ws + (size_t)min(rbase + tid / kTpr, r1 - 1) * nb;
     const float* dxsrc = xd + (size_t)min(tbase + tid / kTpr, n - 1) * nb;
     const int sk = kSp * (tid % kTpr);
 
@@ -799,6 +814,29 @@ __global__ __launch_bounds__(64 * NW) void matmul_tile_kernel(MmSegs segs, const
         if (c + 1 < n_chunks) step(c + 1, S0);
     }
 
+    if constexpr (SW) {
+        __shared__ float hsw[2][32][TT + 1];  // [gate, up][row][token]
+        __shared__ uint64_t exptab[32];
+#pragma unroll
+        for (int rs = 0; rs < NRS; ++rs)
+#pragma unroll
+            for (int ts = 0; ts < NTS; ++ts)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) hsw[wr][16 * rs + 4 * lq + i][wt * (TT / WT) + ts * 16 + li] = acc[rs][ts][i];
+        et.store(exptab);
+        __syncthreads();
+        const int F = segs.r1[0];
+#pragma unroll
+        for (int pass = 0; pass < TT / 8; ++pass) {  // 32 lanes per token's block
+            const int tk = pass * 8 + tid / 32, rr = tid % 32, tok = tbase + tk;
+            if (tok < n) {  // uniform per 32-lane group
+                const float gv = hsw[0][rr][tk], uv = hsw[1][rr][tk];
+                quant_block32(gv / (1.0f + dev_expf(-gv, exptab)) * uv, hq + (size_t)tok * F + 32 * rt,
+                              hd + (size_t)tok * (F / QK) + rt);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int ts = 0; ts < NTS; ++ts) {
         const int tok = tbase + wt * (TT / WT) + ts * 16 + li;
@@ -1081,9 +1119,10 @@ hipError_t launch_matmul_segs(const MmOut* m, int n_mats, const int8_t* xq, cons
         }
         const int n_tg = (n + pl.ttile - 1) / pl.ttile;
         const dim3 grid((unsigned)(row_tiles64 * n_tg));
-#define QH_MM_TILE(DT, KC, TT, NW)                                                                       \
-    if (W.dtype == DT && pl.kc == KC && pl.ttile == TT && pl.nw == NW)                                          \
-        qh_launch((matmul_tile_kernel<DT, KC, TT, NW>), grid, dim3(64 * NW), 0, s, sg64, xq, xd, W.cols, n, n_tg);
+#define QH_MM_TILE(DT, KC, TT, NW)                                                                             \
+    if (W.dtype == DT && pl.kc == KC && pl.ttile == TT && pl.nw == NW)                                                \
+        qh_launch((matmul_tile_kernel<DT, KC, TT, NW, false>), grid, dim3(64 * NW), 0, s, sg64, xq, xd, W.cols, n, n_tg, \
+                  (int8_t*)nullptr, (float*)nullptr);
         QH_MM_TILE(kQ8, 4, 64, 4) QH_MM_TILE(kQ8, 8, 64, 4) QH_MM_TILE(kQ4, 4, 64, 4) QH_MM_TILE(kQ4, 8, 64, 4)
         QH_MM_TILE(kQ8, 4, 32, 4) QH_MM_TILE(kQ8, 8, 32, 4) QH_MM_TILE(kQ4, 4, 32, 4) QH_MM_TILE(kQ4, 8, 32, 4)
         QH_MM_TILE(kQ8, 8, 16, 4) QH_MM_TILE(kQ4, 8, 16, 4) QH_MM_TILE(kQ8, 8, 32, 8) QH_MM_TILE(kQ4, 8, 32, 8)
@@ -1142,6 +1181,34 @@ hipError_t launch_matmul(float* out, int ldo, const qh_tensor& W, const int8_t* 
                          int r1, hipStream_t s) {
     const MmOut m{&W, out, ldo, r0, r1};
     return launch_matmul_segs(&m, 1, xq, xd, n, s);
+}
+
+hipError_t launch_matmul_swiglu(const qh_tensor& wg, const qh_tensor& wu, const int8_t* xq, const float* xd, int n,
+                                int8_t* hq, float* hd, hipStream_t s) {
+    const int F = wg.rows;
+    if (wg.dtype != wu.dtype || (wg.dtype != kQ8 && wg.dtype != kQ4) || wu.rows != F || wu.cols != wg.cols ||
+        F % QK != 0 || wg.cols % QK != 0 || wg.cols < 16 || n < 128)
+        return hipErrorNotSupported;
+    const MmPlan pl = matmul_plan(2 * F, wg.cols, n);
+    if (!pl.tile || pl.nw != 4 || pl.kc != 4 || pl.ttile != 32) return hipErrorNotSupported;
+    const uint8_t *qg = static_cast<const uint8_t*>(wg.data), *qu = static_cast<const uint8_t*>(wu.data);
+    if (((reinterpret_cast<uintptr_t>(qg) | reinterpret_cast<uintptr_t>(qu) | reinterpret_cast<uintptr_t>(xq)) & 15u) != 0)
+        return hipErrorNotSupported;
+    MmSegs sg{};
+    sg.wq[0] = qg;
+    sg.wq[1] = qu;
+    sg.ws[0] = reinterpret_cast<const uint16_t*>(qg + qh_quant_bytes(wg.dtype, F, wg.cols));
+    sg.ws[1] = reinterpret_cast<const uint16_t*>(qu + qh_quant_bytes(wu.dtype, F, wu.cols));
+    sg.r0[0] = 0;
+    sg.r1[0] = F;
+    sg.tiles[0] = F / QK;  // 32-row pairs: every tile in segment 0
+    const int n_tg = (n + 31) / 32;
+    const dim3 grid((unsigned)(F / QK * n_tg));
+    if (wg.dtype == kQ8)
+        qh_launch((matmul_tile_kernel<kQ8, 4, 32, 4, true>), grid, dim3(256), 0, s, sg, xq, xd, wg.cols, n, n_tg, hq, hd);
+    else
+        qh_launch((matmul_tile_kernel<kQ4, 4, 32, 4, true>), grid, dim3(256), 0, s, sg, xq, xd, wg.cols, n, n_tg, hq, hd);
+    return hipGetLastError();
 }
 
 }  // namespace qh

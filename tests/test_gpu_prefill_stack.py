@@ -105,3 +105,27 @@ def test_prefill_stack_q4mix_stream_equals_reference(qh, gpu):
     assert (np.array(digs) == g["state_digests"]).all()
     assert rows == g["head_rows"].tolist()
     assert (bits(np.array(tops, np.float32)) == bits(g["top_logit"])).all()
+
+
+def test_prefill_stack_fused_swiglu_q8_mlp_equals_oracle(qh, oracle, gpu):
+    """The stack's gate / up launch with the SwiGLU epilogue over Q8_0 MLP weights (the q4mix model with its gate, up
+    and down matrices re-drawn as Q8_0), stacks of 128 and 256 over a 300-token prompt (full and partial 32-token
+    tiles): states, logits, rows and every cache row equal the oracle's."""
+    from quanta_cpp_amd import synth
+    qnt = qnt_module()
+    hp = qnt.HParams(vocab_size=3072, n_layers=2)
+    tens = qnt.synthetic_q4mix(31, hp)
+    D, F = hp.dim, hp.ffn_dim
+    for l in range(hp.n_layers):
+        p = f"model.layers.{l}."
+        tens[p + "mlp.gate_proj.weight"] = qnt.TensorRec(2, F, D, synth.q8_tensor(700 + l, F, D))
+        tens[p + "mlp.up_proj.weight"] = qnt.TensorRec(2, F, D, synth.q8_tensor(710 + l, F, D))
+        tens[p + "mlp.down_proj.weight"] = qnt.TensorRec(2, D, F, synth.q8_tensor(720 + l, D, F))
+    ids = np.random.default_rng(8).integers(0, hp.vocab_size, 300).astype(np.int32)
+    for stack in (128, 256):
+        orc = oracle_decoder(oracle, hp, tens, ctx_len=512)
+        dec = qh.Decoder(hp, tens, ctx_len=512)
+        dec.set_prefill_stack(stack)
+        _steps_vs_oracle(oracle, orc, dec, ids, 3, full_every=3)
+        _kv_equal(dec, orc, hp, 303)
+        dec.close()
