@@ -1226,7 +1226,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     __shared__ uint64_t exptab[32];
     ExpTab et;
     et.load();
-    const int h = blockIdx.x, y0 = (int)blockIdx.y * NTK, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // groups in reverse order: the longest (the stack's last tokens) are dispatched first, the short ones fill in
+    const int h = blockIdx.x, y0 = ((int)gridDim.y - 1 - (int)blockIdx.y) * NTK, tid = threadIdx.x, lane = tid & 63,
+              wave = tid >> 6;
     const int nt = min(NTK, n - y0);  // tokens of this workgroup (uniform)
     const int base = *pos_dev + y0;   // position of token 0
     const int nmax = base + nt;       // rows of the last token
